@@ -1,0 +1,98 @@
+/*
+ * ns_sampling.h -- C ABI of the MI355X (gfx950) token sampler.
+ *
+ * Drop-in boundary for NanoServe's sampling hot path.  It replaces the body of
+ *   Sampler.sample(logits, sampling_params_list, history_token_ids, generators)
+ *   (nanoserve/scheduler/sampler.py:21-89)
+ * whose only caller is the engine loop (nanoserve/engine/engine.py:247-249).
+ * The Python host mirror (Sampler.sample in the package) packs the per-request
+ * SamplingParams (nanoserve/config.py:68-79) and histories
+ * (nanoserve/engine/engine.py:242-246) into the device arrays below and calls
+ * ns_sample on the current HIP stream.
+ *
+ * Conventions: plain pointers and sizes only; every pointer in
+ * ns_sample_args is a DEVICE pointer; the caller owns all memory and the
+ * library allocates nothing and never synchronises.  Calls are asynchronous on
+ * `stream`.  Functions return NS_OK (0) or an NS_ERR_* code; ns_last_error()
+ * returns the calling thread's last message.
+ */
+#ifndef NS_SAMPLING_H
+#define NS_SAMPLING_H
+
+#include <stdint.h>
+#include <hip/hip_runtime_api.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define NS_ABI_VERSION 1
+
+#define NS_OK 0
+#define NS_ERR_INVALID 1   /* bad argument (message says which) */
+#define NS_ERR_ALIGN 2     /* logits rows not 16-byte aligned */
+#define NS_ERR_HIP 3       /* a HIP runtime call failed */
+
+#define NS_DTYPE_F32 0
+#define NS_DTYPE_BF16 1
+
+#define NS_MAX_VOCAB 262144     /* vocab limit (LDS presence bitmap of vocab/8 bytes) */
+#define NS_MAX_HISTORY 8192     /* per-row history limit (the reference's max_model_len, config.py:52) */
+#define NS_INFO_WORDS 8         /* int32 words per row in out_info */
+
+/* Per-row diagnostics written to out_info[row * NS_INFO_WORDS + w]:
+ *   w=0 path (1 greedy, 2 uniform/NaN guard, 3 top-k set, 4 generic set, 5 large draw, 9 error)
+ *   w=1 tokens kept after top-k and top-p
+ *   w=2 float32 bits of the top-k threshold in scaled logits (-inf when top-k is off)
+ *   w=3 tokens kept after top-k
+ *   w=4 top-k candidates examined in LDS (-1 when not applicable)
+ *   w=5 flags: 1 history id out of range (ignored), 2 history too long, 4 sample row out of range,
+ *       8 candidate overflow (generic path taken), 16 histogram refinement limit reached,
+ *       32 inverse-CDF locate fell back to the last kept token
+ *   w=6 float32 bits of the scaled logit at the top-p cut
+ *   w=7 token id at the top-p cut
+ */
+
+typedef struct ns_sample_args {
+  const void*    logits;        /* [n_rows_total, row_stride] float32 or bfloat16; the model's logits
+                                   (engine.py:235-236; bf16 is taken directly, no .float() copy) */
+  int32_t        dtype;         /* NS_DTYPE_F32 or NS_DTYPE_BF16 */
+  int32_t        n_sample;      /* B, rows to sample (len(sampling_params_list), sampler.py:28) */
+  int64_t        n_rows_total;  /* rows of `logits` (bounds for sample_idx) */
+  int64_t        vocab;         /* V (sampler.py:28) */
+  int64_t        row_stride;    /* elements between consecutive logits rows (>= vocab) */
+  const int64_t* sample_idx;    /* [B] rows of `logits` to sample, ascending as built at
+                                   scheduler.py:240-246; NULL = rows 0..B-1 (engine.py:235 gather fused) */
+  const float*   temperature;   /* [B] SamplingParams.temperature; 0 = greedy (sampler.py:41-50) */
+  const int32_t* top_k;         /* [B] SamplingParams.top_k; <= 0 or >= V disables (sampler.py:55) */
+  const float*   top_p;         /* [B] SamplingParams.top_p; >= 1 disables (sampler.py:63) */
+  const float*   rep_penalty;   /* [B] SamplingParams.repetition_penalty; 1 disables (sampler.py:33) */
+  const int32_t* hist_offsets;  /* [B+1] CSR offsets into hist_ids, or NULL for no histories */
+  const int32_t* hist_ids;      /* token ids of each row's history (history_token_ids, sampler.py:25) */
+  int32_t        max_hist;      /* upper bound on any row's history length (sizes LDS), <= NS_MAX_HISTORY */
+  const float*   uniforms;      /* [B] uniforms in [0, 1) replacing torch.multinomial's RNG (sampler.py:87) */
+  int64_t*       out_ids;       /* [B] sampled token ids (the LongTensor returned at sampler.py:89) */
+  float*         out_probs;     /* [B, vocab] final probabilities (sampler.py:76-80), or NULL; greedy rows
+                                   are not written.  Debug/parity output, not part of the timed path. */
+  int32_t*       out_info;      /* [B, NS_INFO_WORDS] per-row diagnostics, or NULL */
+} ns_sample_args;
+
+/* Version of this ABI (NS_ABI_VERSION). */
+int ns_abi_version(void);
+
+/* Sample one token per row: the whole of sampler.py:28-89 (repetition penalty, temperature,
+ * top-k, top-p, softmax with the NaN guard, greedy argmax, inverse-CDF draw) in one launch.
+ * Replaces Sampler.sample (nanoserve/scheduler/sampler.py:21-89). */
+int ns_sample(const ns_sample_args* args, hipStream_t stream);
+
+/* LDS bytes one workgroup of ns_sample needs for this vocab and history bound. */
+int ns_sample_lds_bytes(int64_t vocab, int32_t max_hist, int32_t* lds_bytes);
+
+/* Last error message of the calling thread ("" if none). */
+const char* ns_last_error(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* NS_SAMPLING_H */

@@ -1,0 +1,145 @@
+"""ctypes binding of the sampler's C ABI (include/ns_sampling.h).
+
+Loads the in-tree ``libns_sampling.so`` built by ``build.py``.  There is no
+fallback: if the library is missing or fails to load, every call raises.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+from typing import Optional
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libns_sampling.so")
+
+NS_OK = 0
+NS_DTYPE_F32 = 0
+NS_DTYPE_BF16 = 1
+NS_MAX_VOCAB = 262144
+NS_MAX_HISTORY = 8192
+NS_INFO_WORDS = 8
+ABI_VERSION = 1
+
+# exported symbols, as declared in include/ns_sampling.h
+EXPORTS = ("ns_abi_version", "ns_sample", "ns_sample_lds_bytes", "ns_last_error")
+
+
+class NsSampleArgs(ctypes.Structure):
+    """Mirror of ``ns_sample_args`` (field order and types must match the header)."""
+
+    _fields_ = [
+        ("logits", ctypes.c_void_p),
+        ("dtype", ctypes.c_int32),
+        ("n_sample", ctypes.c_int32),
+        ("n_rows_total", ctypes.c_int64),
+        ("vocab", ctypes.c_int64),
+        ("row_stride", ctypes.c_int64),
+        ("sample_idx", ctypes.c_void_p),
+        ("temperature", ctypes.c_void_p),
+        ("top_k", ctypes.c_void_p),
+        ("top_p", ctypes.c_void_p),
+        ("rep_penalty", ctypes.c_void_p),
+        ("hist_offsets", ctypes.c_void_p),
+        ("hist_ids", ctypes.c_void_p),
+        ("max_hist", ctypes.c_int32),
+        ("uniforms", ctypes.c_void_p),
+        ("out_ids", ctypes.c_void_p),
+        ("out_probs", ctypes.c_void_p),
+        ("out_info", ctypes.c_void_p),
+    ]
+
+
+class SamplerLibraryError(RuntimeError):
+    pass
+
+
+_LIB: Optional[ctypes.CDLL] = None
+
+
+def load(path: str = LIB_PATH) -> ctypes.CDLL:
+    """Load the native library once; raise if it is missing or incompatible."""
+    global _LIB
+    if _LIB is not None:
+        return _LIB
+    if not os.path.exists(path):
+        raise SamplerLibraryError(
+            f"native sampler library not found at {path}; build it with build.py (hipcc, gfx950)")
+    lib = ctypes.CDLL(path)
+    lib.ns_abi_version.restype = ctypes.c_int
+    lib.ns_abi_version.argtypes = []
+    lib.ns_sample.restype = ctypes.c_int
+    lib.ns_sample.argtypes = [ctypes.POINTER(NsSampleArgs), ctypes.c_void_p]
+    lib.ns_sample_lds_bytes.restype = ctypes.c_int
+    lib.ns_sample_lds_bytes.argtypes = [ctypes.c_int64, ctypes.c_int32, ctypes.POINTER(ctypes.c_int32)]
+    lib.ns_last_error.restype = ctypes.c_char_p
+    lib.ns_last_error.argtypes = []
+    v = lib.ns_abi_version()
+    if v != ABI_VERSION:
+        raise SamplerLibraryError(f"ABI version mismatch: library {v}, binding {ABI_VERSION}")
+    _LIB = lib
+    return lib
+
+
+def last_error() -> str:
+    return load().ns_last_error().decode(errors="replace")
+
+
+def check(rc: int) -> None:
+    if rc != NS_OK:
+        raise SamplerLibraryError(f"ns_sample failed ({rc}): {last_error()}")
+
+
+def lds_bytes(vocab: int, max_hist: int) -> int:
+    out = ctypes.c_int32(0)
+    check(load().ns_sample_lds_bytes(int(vocab), int(max_hist), ctypes.byref(out)))
+    return int(out.value)
+
+
+def _ptr(t) -> int:
+    return 0 if t is None else int(t.data_ptr())
+
+
+def sample_raw(logits, temperature, top_k, top_p, rep_penalty, uniforms, out_ids, *, sample_idx=None,
+               hist_offsets=None, hist_ids=None, max_hist: int = 0, out_probs=None, out_info=None,
+               stream=None) -> None:
+    """Launch ``ns_sample`` on device tensors (no copies, no synchronisation).
+
+    logits: (N, V) float32 or bfloat16 CUDA tensor with unit stride in the last dim.
+    temperature/top_p/rep_penalty/uniforms: (B,) float32; top_k: (B,) int32;
+    sample_idx: (B,) int64 or None; hist_offsets: (B+1,) int32; hist_ids: int32;
+    out_ids: (B,) int64; out_probs: (B, V) float32 or None; out_info: (B, 8) int32 or None.
+    """
+    import torch
+
+    lib = load()
+    if logits.dim() != 2 or logits.stride(1) != 1:
+        raise ValueError("logits must be a 2-D tensor with unit stride along the vocabulary")
+    if logits.dtype == torch.float32:
+        dt = NS_DTYPE_F32
+    elif logits.dtype == torch.bfloat16:
+        dt = NS_DTYPE_BF16
+    else:
+        raise TypeError(f"logits dtype {logits.dtype} not supported (float32 or bfloat16)")
+    B = int(out_ids.shape[0])
+    a = NsSampleArgs()
+    a.logits = _ptr(logits)
+    a.dtype = dt
+    a.n_sample = B
+    a.n_rows_total = int(logits.shape[0])
+    a.vocab = int(logits.shape[1])
+    a.row_stride = int(logits.stride(0))
+    a.sample_idx = _ptr(sample_idx)
+    a.temperature = _ptr(temperature)
+    a.top_k = _ptr(top_k)
+    a.top_p = _ptr(top_p)
+    a.rep_penalty = _ptr(rep_penalty)
+    a.hist_offsets = _ptr(hist_offsets)
+    a.hist_ids = _ptr(hist_ids)
+    a.max_hist = int(max_hist)
+    a.uniforms = _ptr(uniforms)
+    a.out_ids = _ptr(out_ids)
+    a.out_probs = _ptr(out_probs)
+    a.out_info = _ptr(out_info)
+    if stream is None:
+        stream = torch.cuda.current_stream(logits.device)
+    check(lib.ns_sample(ctypes.byref(a), ctypes.c_void_p(int(stream.cuda_stream))))

@@ -1,0 +1,206 @@
+// Device helpers for the gfx950 token sampler: float keys, wave64 and
+// workgroup reductions/scans, exact division by a row-uniform divisor.
+//
+// Workgroups are 1024 threads = 16 wave64s.  Reductions go through DPP/
+// shuffles inside a wave and a small LDS slot array across waves; they never
+// use same-address LDS atomics (which serialise across all 1024 lanes).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace ns {
+
+constexpr int NT = 1024;          // threads per workgroup
+constexpr int NWAVE = NT / 64;    // 16 wave64s
+
+__device__ __forceinline__ int lane_id() { return threadIdx.x & 63; }
+__device__ __forceinline__ int wave_id() { return threadIdx.x >> 6; }
+
+// IEEE-754-2019 maximum/minimum: NaN-propagating (v_maximum3_f32 on gfx950).
+__device__ __forceinline__ float fmax_nan(float a, float b) { return __builtin_elementwise_maximum(a, b); }
+__device__ __forceinline__ float fmin_nan(float a, float b) { return __builtin_elementwise_minimum(a, b); }
+
+// Order-preserving uint32 key of a float; -0 and +0 map to the same key (the
+// reference compares logits with IEEE ==, where -0 == +0).  NaN is never keyed.
+__device__ __forceinline__ uint32_t fkey(float f) {
+  uint32_t u = __float_as_uint(f);
+  if (u == 0x80000000u) u = 0u;
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+__device__ __forceinline__ float fkey_inv(uint32_t k) {
+  uint32_t u = (k & 0x80000000u) ? (k & 0x7fffffffu) : ~k;
+  return __uint_as_float(u);
+}
+
+// Sort key ordering (value descending, token id ascending) as an ascending u64.
+__device__ __forceinline__ uint64_t desc_key(float y, uint32_t id) {
+  return ((uint64_t)(~fkey(y)) << 32) | (uint64_t)id;
+}
+__device__ __forceinline__ float desc_key_val(uint64_t k) { return fkey_inv(~(uint32_t)(k >> 32)); }
+__device__ __forceinline__ uint32_t desc_key_id(uint64_t k) { return (uint32_t)k; }
+
+// ---------------------------------------------------------------- wave ops
+template <typename T> __device__ __forceinline__ T wave_sum(T v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+  return v;
+}
+__device__ __forceinline__ float wave_max_nan(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = fmax_nan(v, __shfl_xor(v, o));
+  return v;
+}
+__device__ __forceinline__ float wave_min_nan(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = fmin_nan(v, __shfl_xor(v, o));
+  return v;
+}
+template <typename T> __device__ __forceinline__ T wave_max(T v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) { T w = __shfl_xor(v, o); v = w > v ? w : v; }
+  return v;
+}
+template <typename T> __device__ __forceinline__ T wave_min(T v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) { T w = __shfl_xor(v, o); v = w < v ? w : v; }
+  return v;
+}
+// inclusive prefix sum over the 64 lanes
+template <typename T> __device__ __forceinline__ T wave_incl_scan(T v) {
+  const int l = lane_id();
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    T w = __shfl_up(v, o);
+    if (l >= o) v += w;
+  }
+  return v;
+}
+__device__ __forceinline__ uint64_t ballot(bool p) { return __ballot(p); }
+__device__ __forceinline__ int lanes_below(uint64_t mask) {
+  return __builtin_amdgcn_mbcnt_hi((uint32_t)(mask >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)mask, 0u));
+}
+
+// ---------------------------------------------------------- block helpers
+// Scratch for cross-wave exchange: 16 waves x 4 doubles.
+struct BlockScratch {
+  double d[NWAVE][4];
+};
+
+__device__ __forceinline__ float block_max_nan(float v, BlockScratch* s) {
+  v = wave_max_nan(v);
+  if (lane_id() == 0) s->d[wave_id()][0] = (double)v;
+  __syncthreads();
+  float r = (float)s->d[0][0];
+#pragma unroll
+  for (int w = 1; w < NWAVE; ++w) r = fmax_nan(r, (float)s->d[w][0]);
+  __syncthreads();
+  return r;
+}
+__device__ __forceinline__ float block_min_nan(float v, BlockScratch* s) {
+  v = wave_min_nan(v);
+  if (lane_id() == 0) s->d[wave_id()][0] = (double)v;
+  __syncthreads();
+  float r = (float)s->d[0][0];
+#pragma unroll
+  for (int w = 1; w < NWAVE; ++w) r = fmin_nan(r, (float)s->d[w][0]);
+  __syncthreads();
+  return r;
+}
+// Deterministic fixed-order sum (double).
+__device__ __forceinline__ double block_sum(double v, BlockScratch* s) {
+  v = wave_sum(v);
+  if (lane_id() == 0) s->d[wave_id()][0] = v;
+  __syncthreads();
+  double r = 0.0;
+#pragma unroll
+  for (int w = 0; w < NWAVE; ++w) r += s->d[w][0];
+  __syncthreads();
+  return r;
+}
+__device__ __forceinline__ int64_t block_sum_i64(int64_t v, BlockScratch* s) {
+  v = wave_sum(v);
+  if (lane_id() == 0) s->d[wave_id()][0] = __longlong_as_double(v);
+  __syncthreads();
+  int64_t r = 0;
+#pragma unroll
+  for (int w = 0; w < NWAVE; ++w) r += __double_as_longlong(s->d[w][0]);
+  __syncthreads();
+  return r;
+}
+__device__ __forceinline__ int64_t block_min_i64(int64_t v, BlockScratch* s) {
+  v = wave_min(v);
+  if (lane_id() == 0) s->d[wave_id()][0] = __longlong_as_double(v);
+  __syncthreads();
+  int64_t r = __double_as_longlong(s->d[0][0]);
+#pragma unroll
+  for (int w = 1; w < NWAVE; ++w) { int64_t x = __double_as_longlong(s->d[w][0]); r = x < r ? x : r; }
+  __syncthreads();
+  return r;
+}
+__device__ __forceinline__ int64_t block_max_i64(int64_t v, BlockScratch* s) {
+  v = wave_max(v);
+  if (lane_id() == 0) s->d[wave_id()][0] = __longlong_as_double(v);
+  __syncthreads();
+  int64_t r = __double_as_longlong(s->d[0][0]);
+#pragma unroll
+  for (int w = 1; w < NWAVE; ++w) { int64_t x = __double_as_longlong(s->d[w][0]); r = x > r ? x : r; }
+  __syncthreads();
+  return r;
+}
+// Exclusive prefix over threads in thread order (double); *total receives the block sum.
+__device__ __forceinline__ double block_excl_scan(double v, double* total, BlockScratch* s) {
+  double inc = wave_incl_scan(v);
+  if (lane_id() == 63) s->d[wave_id()][1] = inc;
+  __syncthreads();
+  double off = 0.0, tot = 0.0;
+#pragma unroll
+  for (int w = 0; w < NWAVE; ++w) {
+    double t = s->d[w][1];
+    if (w < wave_id()) off += t;
+    tot += t;
+  }
+  __syncthreads();
+  *total = tot;
+  return off + inc - v;
+}
+__device__ __forceinline__ int block_excl_scan_int(int v, int* total, BlockScratch* s) {
+  int inc = wave_incl_scan(v);
+  if (lane_id() == 63) s->d[wave_id()][1] = (double)inc;
+  __syncthreads();
+  int off = 0, tot = 0;
+#pragma unroll
+  for (int w = 0; w < NWAVE; ++w) {
+    int t = (int)s->d[w][1];
+    if (w < wave_id()) off += t;
+    tot += t;
+  }
+  __syncthreads();
+  *total = tot;
+  return off + inc - v;
+}
+
+// exp from the ROCm device library (ocml expf, faithfully rounded); not the
+// reduced-precision __expf.
+__device__ __forceinline__ float ns_expf(float x) { return expf(x); }
+
+// ------------------------------------------------- exact division x / t
+// Correctly rounded quotient by a row-uniform divisor t > 0 with precomputed
+// r = RN(1/t): q0 = RN(x*r); rem = fma(-q0, t, x) is exact; q = RN(q0 + rem*r)
+// (Markstein's correction theorem for a correctly rounded reciprocal).  Outside
+// the range where the theorem's no-underflow/no-overflow conditions hold the
+// IEEE division is used.  Bit-exactness against IEEE x/t is tested on the CPU
+// over every float32 mantissa for a set of divisors.
+__device__ __forceinline__ float div_rn(float x, float t, float r) {
+  float q0 = x * r;
+  float rem = __builtin_fmaf(-q0, t, x);
+  float q = __builtin_fmaf(rem, r, q0);
+  float aq = __builtin_fabsf(q0);
+  bool slow = !(aq >= 0x1.0p-100f && aq <= 0x1.0p+100f);
+  if (__ballot(slow) != 0ull) {  // wave-uniform branch: the IEEE division is never speculated
+    if (slow) q = x / t;
+  }
+  return q;
+}
+
+}  // namespace ns

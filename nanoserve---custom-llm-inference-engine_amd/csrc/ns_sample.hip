@@ -1,0 +1,1175 @@
+// gfx950 token sampler: kernel body and the C-ABI entry points.
+// Design notes are in ns_sample_kernel.h; the ABI is declared in
+// include/ns_sampling.h.
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+#include <string>
+
+#include "ns_sample_kernel.h"
+#include "ns_sampling.h"
+
+namespace ns {
+
+constexpr float NEG_INF = -__builtin_inff();
+constexpr float POS_INF = __builtin_inff();
+constexpr float FLT_MAXV = 3.40282347e38f;
+
+template <typename T>
+__device__ __forceinline__ uint4 ninf_chunk() {
+  const uint32_t w = T::EPC == 8 ? 0xff80ff80u : 0xff800000u;
+  return make_uint4(w, w, w, w);
+}
+
+// Wave-aggregated append of (x, id) into the LDS candidate array.  Must be
+// reached by all lanes of the wave (convergent control flow); `take` selects.
+__device__ __forceinline__ void cand_append(bool take, float x, int64_t id, uint64_t* cand, Misc* misc) {
+  take = take && x > -__builtin_inff();   // -inf entries (history positions of the chunk layout) never enter
+  uint64_t m = ballot(take);
+  if (m == 0ull) return;
+  int leader = __builtin_ctzll(m);
+  int base = 0;
+  if (lane_id() == leader) base = atomicAdd(&misc->cand_n, __popcll(m));
+  base = __shfl(base, leader);
+  int pos = base + lanes_below(m);
+  if (take && pos < CAP) cand[pos] = ((uint64_t)__float_as_uint(x) << 32) | (uint32_t)id;
+}
+
+// Streaming visit of this row thread's chunks (history positions read as -inf).
+// f(x, id, j) with j the chunk row.
+template <typename T, typename F>
+__device__ __forceinline__ void visit_rows(const uint4* rowv, const uint32_t* bm, bool pen_on, int64_t nch,
+                                           int64_t nrows_j, F&& f) {
+  const int tid = threadIdx.x;
+  for (int64_t j = 0; j < nrows_j; j += 4) {
+    uint4 v[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      int64_t c = (j + q) * RT + tid;
+      v[q] = (j + q < nrows_j && c < nch) ? rowv[c] : ninf_chunk<T>();
+    }
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      int64_t c = (j + q) * RT + tid;
+      if (j + q < nrows_j && c < nch) {
+        uint4 w = v[q];
+        if (pen_on) w = T::mask(w, T::bits(bm, c));
+#pragma unroll
+        for (int e = 0; e < T::EPC; ++e) f(T::elem(w, e), c * T::EPC + e, j + q);
+      }
+    }
+  }
+}
+
+// Linear-bin histogram levels used by the generic paths.  Level r maps a value
+// v with hi_r >= v to bin (hi_r - v) * s_r clamped to [0, NB-1]; membership in
+// level r+1 is "bin at every earlier level equals the chosen bin".
+struct Levels {
+  double hi[MAX_LEVELS];
+  double s[MAX_LEVELS];
+  int b[MAX_LEVELS];
+  int n;
+  __device__ __forceinline__ static int bin(double hi, double s, float v) {
+    double t = (hi - (double)v) * s;
+    int b = t <= 0.0 ? 0 : (t >= (double)(NB - 1) ? NB - 1 : (int)t);
+    return b;
+  }
+  __device__ __forceinline__ void set(int r, double h, double sc, int bb) {
+#pragma unroll
+    for (int i = 0; i < MAX_LEVELS; ++i)
+      if (i == r) { hi[i] = h; s[i] = sc; b[i] = bb; }
+    n = r + 1;
+  }
+  __device__ __forceinline__ bool member(float v) const {
+    bool ok = true;
+#pragma unroll
+    for (int r = 0; r < MAX_LEVELS; ++r)
+      if (r < n) ok = ok && bin(hi[r], s[r], v) == b[r];
+    return ok;
+  }
+};
+
+// Find the first bin whose inclusive cumulative (count or fixed-point mass)
+// exceeds `target` (strictly greater if `strict`, else >=).  Thread t owns bins
+// 2t and 2t+1.  Returns the bin (or -1) and the cumulative before it.
+__device__ __forceinline__ int find_bin(const uint64_t* vals64, const uint32_t* vals32, bool use64, double target,
+                                        bool strict, double* before, Misc* misc) {
+  const int t = threadIdx.x;
+  double a = use64 ? (double)vals64[2 * t] : (double)vals32[2 * t];
+  double b = use64 ? (double)vals64[2 * t + 1] : (double)vals32[2 * t + 1];
+  double tot;
+  if (t == 0) { misc->ib[10] = -1; }
+  double pre = block_excl_scan(a + b, &tot, &misc->red);  // contains barriers
+  auto over = [&](double c) { return strict ? (c > target) : (c >= target); };
+  if (!over(pre) && over(pre + a)) { misc->ib[10] = 2 * t; misc->db[6] = pre; }
+  else if (!over(pre + a) && over(pre + a + b)) { misc->ib[10] = 2 * t + 1; misc->db[6] = pre + a; }
+  __syncthreads();
+  int r = misc->ib[10];
+  *before = misc->db[6];
+  __syncthreads();
+  return r;
+}
+
+// Threshold tau with count(values >= tau) >= k from per-thread value arrays
+// (chunk or group maxima): histogram over [lo, hi], first bin reaching k, tau =
+// the smallest value in bins up to it.  Returns -inf when fewer than k values.
+template <int NV>
+__device__ float select_tau(const float (&v)[NV], bool active, int k, uint32_t* hcnt, Misc* misc) {
+  float hi = NEG_INF, lo = POS_INF;
+  int cnt = 0;
+  if (active) {
+#pragma unroll
+    for (int i = 0; i < NV; ++i)
+      if (v[i] > NEG_INF) { hi = __builtin_fmaxf(hi, v[i]); lo = __builtin_fminf(lo, v[i]); ++cnt; }
+  }
+  hi = block_max_nan(hi, &misc->red);
+  lo = block_min_nan(lo, &misc->red);
+  int64_t total = block_sum_i64(cnt, &misc->red);
+  if (total < k) return NEG_INF;
+  if (!(hi > lo)) return lo;
+  const double dh = hi, ds = (double)NB / ((double)hi - (double)lo);
+  for (int i = threadIdx.x; i < NB; i += NT) hcnt[i] = 0u;
+  __syncthreads();
+  if (active) {
+#pragma unroll
+    for (int i = 0; i < NV; ++i)
+      if (v[i] > NEG_INF) atomicAdd(&hcnt[Levels::bin(dh, ds, v[i])], 1u);
+  }
+  __syncthreads();
+  double before;
+  int bstar = find_bin(nullptr, hcnt, false, (double)k, false, &before, misc);
+  float m = POS_INF;
+  if (active) {
+#pragma unroll
+    for (int i = 0; i < NV; ++i)
+      if (v[i] > NEG_INF && Levels::bin(dh, ds, v[i]) <= bstar) m = __builtin_fminf(m, v[i]);
+  }
+  return block_min_nan(m, &misc->red);
+}
+
+struct RowOut {
+  int64_t* out_ids;
+  float* out_probs;
+  int32_t* out_info;
+  int row;
+  int64_t V;
+};
+
+__device__ __forceinline__ void write_info(const RowOut& o, int32_t path, int32_t n_kept, float thr, int32_t n_topk,
+                                           int32_t n_cand, int32_t flags, float vstar, int32_t istar) {
+  if (o.out_info == nullptr || threadIdx.x != 0) return;
+  int32_t* w = o.out_info + (int64_t)o.row * INFO_WORDS;
+  w[0] = path; w[1] = n_kept; w[2] = (int32_t)__float_as_uint(thr); w[3] = n_topk;
+  w[4] = n_cand; w[5] = flags; w[6] = (int32_t)__float_as_uint(vstar); w[7] = istar;
+}
+
+__device__ __forceinline__ void zero_probs(const RowOut& o) {
+  if (o.out_probs == nullptr) return;
+  float* pr = o.out_probs + (int64_t)o.row * o.V;
+  for (int64_t i = threadIdx.x; i < o.V; i += NT) pr[i] = 0.0f;
+  __syncthreads();
+}
+
+// Exact selection, top-p and draw over the n entries (x, id) in `cand`.
+// need_topk: keep the entries >= the k-th largest scaled value; need_topp: apply
+// the nucleus cut.  Without either, the entries are the whole kept set.
+__device__ __attribute__((noinline)) void lds_set(int n, bool need_topk, int k, bool need_topp, float p32, float My, float tdiv, float rdiv,
+                        float u, uint64_t* cand, Misc* misc, const RowOut& o, int32_t path, int32_t flags,
+                        float thr_in, int32_t n_topk_in) {
+  const int tid = threadIdx.x;
+  uint64_t kv[CAP / NT];
+#pragma unroll
+  for (int q = 0; q < CAP / NT; ++q) {
+    int i = tid + q * NT;
+    kv[q] = ~0ull;
+    if (i < n) {
+      uint64_t e = cand[i];
+      float x = __uint_as_float((uint32_t)(e >> 32));
+      float y = div_rn(x, tdiv, rdiv);
+      kv[q] = desc_key(y, (uint32_t)e);
+    }
+  }
+  const int P = next_pow2(n < 2 ? 2 : n);
+  if (tid == 0) { misc->ib[1] = n; misc->ib[2] = -1; misc->ib[3] = -1; }
+  __syncthreads();
+#pragma unroll
+  for (int q = 0; q < CAP / NT; ++q) {
+    int i = tid + q * NT;
+    if (i < P) cand[i] = kv[q];
+  }
+  __syncthreads();
+  lds_bitonic_sort(cand, P);
+
+  // top-k: keep every entry >= the k-th largest (ties kept, sampler.py:56-58)
+  int nk = n;
+  float thr = thr_in;
+  if (need_topk) {
+    if (n < k) {
+      // fewer than k finite candidates: the k-th largest is -inf and nothing is removed
+      thr = NEG_INF;
+    } else {
+      thr = desc_key_val(cand[k - 1]);
+      for (int i = tid; i < n; i += NT) {
+        float yi = desc_key_val(cand[i]);
+        if (yi >= thr && (i + 1 == n || desc_key_val(cand[i + 1]) < thr)) misc->ib[1] = i + 1;
+      }
+      __syncthreads();
+      nk = misc->ib[1];
+    }
+  }
+  const int n_topk = need_topk ? nk : n_topk_in;
+
+  // masses over sorted positions; thread t owns positions 4t .. 4t+3
+  const int p0 = tid * (CAP / NT);
+  float e[CAP / NT];
+  double es = 0.0;
+#pragma unroll
+  for (int q = 0; q < CAP / NT; ++q) {
+    int pos = p0 + q;
+    e[q] = pos < nk ? ns_expf(desc_key_val(cand[pos]) - My) : 0.0f;
+    es += (double)e[q];
+  }
+  int nf = nk;
+  float vstar = NEG_INF;
+  int32_t istar = -1;
+  if (need_topp) {
+    // sampler.py:64-73: sorted softmax, float32 prefix sums, keep through the crossing
+    double Z = block_sum(es, &misc->red);
+    float qv[CAP / NT];
+    double qs = 0.0;
+#pragma unroll
+    for (int q = 0; q < CAP / NT; ++q) {
+      qv[q] = (p0 + q) < nk ? (float)((double)e[q] / Z) : 0.0f;
+      qs += (double)qv[q];
+    }
+    double tot;
+    double run = block_excl_scan(qs, &tot, &misc->red);
+#pragma unroll
+    for (int q = 0; q < CAP / NT; ++q) {
+      int pos = p0 + q;
+      if (pos < nk) {
+        float cprev = (float)run;
+        run += (double)qv[q];
+        float c = (float)run;
+        if (c > p32 && (pos == 0 || !(cprev > p32))) misc->ib[2] = pos;
+      }
+    }
+    __syncthreads();
+    int J = misc->ib[2];
+    nf = J >= 0 ? J + 1 : nk;
+    uint64_t kc = cand[nf - 1];
+    vstar = desc_key_val(kc);
+    istar = (int32_t)desc_key_id(kc);
+  }
+  // final probabilities over positions [0, nf) (sampler.py:76)
+  double es2 = 0.0;
+#pragma unroll
+  for (int q = 0; q < CAP / NT; ++q)
+    if (p0 + q < nf) es2 += (double)e[q];
+  const double Z2 = block_sum(es2, &misc->red);
+  uint64_t k2[CAP / NT];
+#pragma unroll
+  for (int q = 0; q < CAP / NT; ++q) {
+    int pos = p0 + q;
+    k2[q] = ~0ull;
+    if (pos < nf) {
+      float pv = (float)((double)e[q] / Z2);
+      k2[q] = ((uint64_t)desc_key_id(cand[pos]) << 32) | __float_as_uint(pv);
+    }
+  }
+  const int P2 = next_pow2(nf < 2 ? 2 : nf);
+  __syncthreads();
+#pragma unroll
+  for (int q = 0; q < CAP / NT; ++q) {
+    int pos = p0 + q;
+    if (pos < P2) cand[pos] = k2[q];
+  }
+  __syncthreads();
+  lds_bitonic_sort(cand, P2);
+
+  // inverse CDF in token-id order
+  const double ud = (double)u;
+  float pp[CAP / NT];
+  double ps = 0.0;
+  int64_t lastpos = -1;
+#pragma unroll
+  for (int q = 0; q < CAP / NT; ++q) {
+    int pos = p0 + q;
+    pp[q] = pos < nf ? __uint_as_float((uint32_t)cand[pos]) : 0.0f;
+    ps += (double)pp[q];
+    if (pos < nf && pp[q] > 0.0f) lastpos = pos;
+  }
+  double tot2;
+  double run2 = block_excl_scan(ps, &tot2, &misc->red);
+#pragma unroll
+  for (int q = 0; q < CAP / NT; ++q) {
+    int pos = p0 + q;
+    if (pos < nf) {
+      double before = run2;
+      run2 += (double)pp[q];
+      if (run2 > ud && !(before > ud)) misc->ib[3] = pos;
+    }
+  }
+  lastpos = block_max_i64(lastpos, &misc->red);  // barriers order the ib[3] writes
+  int pick = misc->ib[3];
+  if (pick < 0) pick = lastpos >= 0 ? (int)lastpos : 0;
+  const int64_t token = (int64_t)(cand[pick] >> 32);
+  if (tid == 0) o.out_ids[o.row] = token;
+  write_info(o, path, nf, thr, n_topk, n, flags, vstar, istar);
+  if (o.out_probs != nullptr) {
+    zero_probs(o);
+    float* pr = o.out_probs + (int64_t)o.row * o.V;
+    for (int i = tid; i < nf; i += NT) pr[cand[i] >> 32] = __uint_as_float((uint32_t)cand[i]);
+  }
+}
+
+// State handed from the kernel to the generic (histogram) path.
+struct GCtx {
+  const uint4* rowv;
+  uint32_t* bm;
+  float* xl_val;
+  int32_t* xl_id;
+  uint64_t* cand;
+  uint32_t* hcnt;
+  uint64_t* hmass;
+  Misc* misc;
+  int64_t* out_ids;
+  float* out_probs;
+  int32_t* out_info;
+  int64_t V, nch, nrows_j;
+  int row, U, k, flags;
+  float pen, tdiv, rdiv, p32, Mx, My, u;
+  bool pen_on, topk_on, topp_on;
+};
+
+// Rows not resolved by the greedy, NaN-guard or small-k paths: top-k for
+// large k (count histogram), top-p over large sets (fixed-point mass
+// histogram), and the inverse-CDF draw over a large kept set.  Every pass
+// re-reads the row (served from L2 / Infinity Cache after P1).
+template <typename T>
+__device__ __attribute__((noinline)) void generic_path(const GCtx g) {
+  const int tid = threadIdx.x;
+  const int lane = lane_id();
+  const int wid = wave_id();
+  const bool rowthr = tid < RT;
+  const bool hwave = wid == NWAVE - 1;
+  constexpr int EPC = T::EPC;
+  const uint4* rowv = g.rowv;
+  const uint32_t* bm = g.bm;
+  const float* xl_val = g.xl_val;
+  const int32_t* xl_id = g.xl_id;
+  uint64_t* cand = g.cand;
+  uint32_t* hcnt = g.hcnt;
+  uint64_t* hmass = g.hmass;
+  Misc* misc = g.misc;
+  BlockScratch* red = &misc->red;
+  const int64_t V = g.V, nch = g.nch, nrows_j = g.nrows_j;
+  const int row = g.row, U = g.U, k = g.k;
+  int32_t flags = g.flags;
+  const float pen = g.pen, tdiv = g.tdiv, rdiv = g.rdiv, p32 = g.p32, Mx = g.Mx, My = g.My, u = g.u;
+  const bool pen_on = g.pen_on, topk_on = g.topk_on, topp_on = g.topp_on;
+  const RowOut o{g.out_ids, g.out_probs, g.out_info, row, V};
+  struct { int64_t* out_ids; float* out_probs; } P{g.out_ids, g.out_probs};
+
+  // ================= generic path: histogram passes over re-read data =================
+  // Extras (history wave) contribute through `xl_each`.
+  auto xl_each = [&](auto&& f) {
+    if (hwave)
+      for (int i = lane; i < U; i += 64) f(xl_val[i], (int64_t)xl_id[i]);
+  };
+  auto row_each = [&](auto&& f) {
+    if (rowthr) visit_rows<T>(rowv, bm, pen_on, nch, nrows_j, [&](float x, int64_t id, int64_t) { f(x, id); });
+  };
+  auto compact = [&](auto&& pred) -> int {
+    if (tid == 0) misc->cand_n = 0;
+    __syncthreads();
+    if (rowthr) {
+      for (int64_t j = 0; j < nrows_j; ++j) {
+        const int64_t c = j * RT + tid;
+        const bool ok = c < nch;
+        uint4 w = ok ? rowv[c] : ninf_chunk<T>();
+        if (ok && pen_on) w = T::mask(w, T::bits(bm, c));
+#pragma unroll
+        for (int e = 0; e < EPC; ++e) {
+          const float x = T::elem(w, e);
+          cand_append(ok && pred(x, c * EPC + e), x, c * EPC + e, cand, misc);
+        }
+      }
+    } else {
+      for (int base = 0; base < U; base += 64) {
+        const int i = base + lane;
+        const float x = i < U ? xl_val[i] : NEG_INF;
+        const int64_t id = i < U ? xl_id[i] : 0;
+        cand_append(i < U && pred(x, id), x, id, cand, misc);
+      }
+    }
+    __syncthreads();
+    return misc->cand_n;
+  };
+
+  // ---- top-k for large k (or candidate overflow): count histogram in x
+  float Lx = NEG_INF;
+  float thr_y = NEG_INF;
+  int32_t n_topk = (int32_t)V;
+  if (topk_on) {
+    float lmin = POS_INF;
+    int cntf = 0;
+    auto f_min = [&](float x, int64_t) { if (x > NEG_INF) { lmin = __builtin_fminf(lmin, x); ++cntf; } };
+    row_each(f_min);
+    xl_each(f_min);
+    const float lo0 = block_min_nan(lmin, red);
+    const int64_t nfinite = block_sum_i64(cntf, red);
+    float thr_x = NEG_INF;
+    if (nfinite >= k) {
+      Levels L;
+      L.n = 0;
+      double hi = Mx, lo = lo0;
+      int kk = k;
+      bool done = false;
+      for (int r = 0; r < MAX_LEVELS && !done; ++r) {
+        if (!(hi > lo)) { thr_x = (float)hi; done = true; break; }
+        const double s = (double)NB / (hi - lo);
+        for (int i = tid; i < NB; i += NT) hcnt[i] = 0u;
+        __syncthreads();
+        auto f_h = [&](float x, int64_t) {
+          if (x > NEG_INF && L.member(x)) atomicAdd(&hcnt[Levels::bin(hi, s, x)], 1u);
+        };
+        row_each(f_h);
+        xl_each(f_h);
+        __syncthreads();
+        double before;
+        const int b = find_bin(nullptr, hcnt, false, (double)kk, false, &before, misc);
+        const int cntb = (int)hcnt[b < 0 ? 0 : b];
+        __syncthreads();
+        if (b < 0) { flags |= FLAG_REFINE_LIMIT; thr_x = (float)lo; done = true; break; }
+        kk -= (int)before;
+        L.set(r, hi, s, b);
+        if (cntb <= CAP || r == MAX_LEVELS - 1) {
+          if (cntb > CAP) flags |= FLAG_REFINE_LIMIT;
+          const int n = compact([&](float x, int64_t) { return x > NEG_INF && L.member(x); });
+          const int nn = n < CAP ? n : CAP;
+          // sort the bin's members descending and take the kk-th
+          uint64_t kv[CAP / NT];
+#pragma unroll
+          for (int q = 0; q < CAP / NT; ++q) {
+            const int i = tid + q * NT;
+            kv[q] = i < nn ? desc_key(__uint_as_float((uint32_t)(cand[i] >> 32)), (uint32_t)cand[i]) : ~0ull;
+          }
+          const int P2 = next_pow2(nn < 2 ? 2 : nn);
+          __syncthreads();
+#pragma unroll
+          for (int q = 0; q < CAP / NT; ++q) {
+            const int i = tid + q * NT;
+            if (i < P2) cand[i] = kv[q];
+          }
+          __syncthreads();
+          lds_bitonic_sort(cand, P2);
+          const int pos = kk - 1 < nn - 1 ? kk - 1 : nn - 1;
+          thr_x = desc_key_val(cand[pos < 0 ? 0 : pos]);
+          __syncthreads();
+          done = true;
+          break;
+        }
+        const double h0v = hi;
+        hi = h0v - (double)b / s;
+        lo = h0v - (double)(b + 1) / s;
+      }
+    }
+    Lx = lower_preimage(thr_x, tdiv, rdiv);
+    thr_y = div_rn(thr_x, tdiv, rdiv);
+    int cnt = 0;
+    auto f_c = [&](float x, int64_t) { if (x >= Lx && x > NEG_INF) ++cnt; };
+    row_each(f_c);
+    xl_each(f_c);
+    n_topk = (int32_t)block_sum_i64(cnt, red);
+    if (n_topk <= CAP) {
+      const int n = compact([&](float x, int64_t) { return x >= Lx; });
+      lds_set(n, true, k, topp_on, p32, My, tdiv, rdiv, u, cand, misc, o, PATH_GENERIC_SET, flags, NEG_INF, 0);
+      return;
+    }
+  }
+
+  // ---- top-p on a large set: fixed-point mass histogram in y = x / t
+  bool cut = false;
+  float vstar = NEG_INF;
+  int64_t istar = -1;
+  int64_t n_kept = -1;
+  if (topp_on) {
+    Levels L;
+    L.n = 0;
+    double hi = My, lo = (double)My - 64.0;
+    double above_fx = 0.0;     // fixed-point mass of elements ranked above the current level's bins
+    int64_t above_cnt = 0;
+    double Zfx = 0.0;
+    bool done = false;
+    for (int r = 0; r < MAX_LEVELS && !done; ++r) {
+      const double s = (double)NB / (hi - lo);
+      for (int i = tid; i < NB; i += NT) { hcnt[i] = 0u; hmass[i] = 0ull; }
+      __syncthreads();
+      auto f_h = [&](float x, int64_t) {
+        if (x >= Lx) {
+          const float y = div_rn(x, tdiv, rdiv);
+          if (y >= (float)((double)My - 64.0) && L.member(y)) {
+            const int b = Levels::bin(hi, s, y);
+            atomicAdd(&hcnt[b], 1u);
+            atomicAdd((unsigned long long*)&hmass[b], (unsigned long long)mass_fx(ns_expf(y - My)));
+          }
+        }
+      };
+      row_each(f_h);
+      xl_each(f_h);
+      __syncthreads();
+      if (r == 0) {
+        int64_t zz = (int64_t)(hmass[2 * tid] + hmass[2 * tid + 1]);
+        Zfx = (double)block_sum_i64(zz, red);
+      }
+      const double target = (double)p32 * Zfx - above_fx;
+      double before;
+      const int b = find_bin(hmass, nullptr, true, target, true, &before, misc);
+      if (b < 0) { done = true; cut = false; break; }  // the nucleus holds everything
+      // count of elements in bins before b
+      int c0 = (2 * tid < b ? (int)hcnt[2 * tid] : 0) + (2 * tid + 1 < b ? (int)hcnt[2 * tid + 1] : 0);
+      const int64_t cnt_before = block_sum_i64(c0, red);
+      const int cntb = (int)hcnt[b];
+      __syncthreads();
+      L.set(r, hi, s, b);
+      above_fx += before;
+      above_cnt += cnt_before;
+      if (cntb <= CAP || r == MAX_LEVELS - 1) {
+        if (cntb > CAP) flags |= FLAG_REFINE_LIMIT;
+        const int n = compact([&](float x, int64_t) {
+          if (!(x >= Lx)) return false;
+          const float y = div_rn(x, tdiv, rdiv);
+          return y >= (float)((double)My - 64.0) && L.member(y);
+        });
+        const int nn = n < CAP ? n : CAP;
+        uint64_t kv[CAP / NT];
+#pragma unroll
+        for (int q = 0; q < CAP / NT; ++q) {
+          const int i = tid + q * NT;
+          kv[q] = ~0ull;
+          if (i < nn) {
+            const float y = div_rn(__uint_as_float((uint32_t)(cand[i] >> 32)), tdiv, rdiv);
+            kv[q] = desc_key(y, (uint32_t)cand[i]);
+          }
+        }
+        const int P2 = next_pow2(nn < 2 ? 2 : nn);
+        __syncthreads();
+#pragma unroll
+        for (int q = 0; q < CAP / NT; ++q) {
+          const int i = tid + q * NT;
+          if (i < P2) cand[i] = kv[q];
+        }
+        if (tid == 0) misc->ib[2] = -1;
+        __syncthreads();
+        lds_bitonic_sort(cand, P2);
+        // exact crossing inside the bin: c_j = fl32(base + sum of fl32(e/Z))
+        const double Z = Zfx * FX_INV;
+        const double base_q = above_fx / Zfx;
+        const int p0 = tid * (CAP / NT);
+        float qv[CAP / NT];
+        double qs = 0.0;
+#pragma unroll
+        for (int q = 0; q < CAP / NT; ++q) {
+          const int pos = p0 + q;
+          qv[q] = pos < nn ? (float)((double)ns_expf(desc_key_val(cand[pos]) - My) / Z) : 0.0f;
+          qs += (double)qv[q];
+        }
+        double tot;
+        double run = base_q + block_excl_scan(qs, &tot, red);
+#pragma unroll
+        for (int q = 0; q < CAP / NT; ++q) {
+          const int pos = p0 + q;
+          if (pos < nn) {
+            const float cprev = (float)run;
+            run += (double)qv[q];
+            if ((float)run > p32 && (pos == 0 ? !((float)base_q > p32) : !(cprev > p32))) misc->ib[2] = pos;
+          }
+        }
+        __syncthreads();
+        int J = misc->ib[2];
+        if (J < 0) J = nn - 1;
+        const uint64_t kc = cand[J];
+        vstar = desc_key_val(kc);
+        istar = (int64_t)desc_key_id(kc);
+        cut = true;
+        n_kept = above_cnt + J + 1;
+        __syncthreads();
+        done = true;
+        break;
+      }
+      const double h0v = hi;
+      hi = h0v - (double)b / s;
+      lo = h0v - (double)(b + 1) / s;
+    }
+  }
+  auto keep = [&](float x, int64_t id) -> bool {
+    if (!(x >= Lx) || !(x > NEG_INF)) return false;
+    if (!cut) return true;
+    const float y = div_rn(x, tdiv, rdiv);
+    return y > vstar || (y == vstar && id <= istar);
+  };
+  if (n_kept < 0) {
+    int cnt = 0;
+    auto f_c = [&](float x, int64_t id) { if (keep(x, id)) ++cnt; };
+    row_each(f_c);
+    xl_each(f_c);
+    n_kept = block_sum_i64(cnt, red);
+  }
+  if (n_kept <= CAP) {
+    const int n = compact(keep);
+    lds_set(n, false, k, false, p32, My, tdiv, rdiv, u, cand, misc, o, PATH_GENERIC_SET, flags, thr_y, n_topk);
+    return;
+  }
+
+  // ---- large kept set: inverse CDF over per-chunk-row mass sums
+  {
+    // LDS: rowsum[(nrows_j + 1) * NWAVE] doubles and xrow[nrows_j + 1] fixed-point, in the histogram area
+    double* rowsum = reinterpret_cast<double*>(hmass);
+    uint64_t* xrow = reinterpret_cast<uint64_t*>(cand);
+    const int64_t nrow_tot = nrows_j + 1;   // last row = tail elements
+    for (int64_t i = tid; i < nrow_tot * NWAVE; i += NT) rowsum[i] = 0.0;
+    for (int64_t i = tid; i < nrow_tot; i += NT) xrow[i] = 0ull;
+    __syncthreads();
+    int64_t lastid = -1;
+    double zsum = 0.0;
+    if (rowthr) {
+      for (int64_t j = 0; j < nrows_j; ++j) {
+        const int64_t c = j * RT + tid;
+        const bool ok = c < nch;
+        uint4 w = ok ? rowv[c] : ninf_chunk<T>();
+        if (ok && pen_on) w = T::mask(w, T::bits(bm, c));
+        double s = 0.0;
+#pragma unroll
+        for (int e = 0; e < EPC; ++e) {
+          const float x = T::elem(w, e);
+          if (ok && keep(x, c * EPC + e)) {
+            const float ev = ns_expf(div_rn(x, tdiv, rdiv) - My);
+            s += (double)ev;
+            if (ev > 0.0f) lastid = c * EPC + e;
+          }
+        }
+        zsum += s;
+        s = wave_sum(s);
+        if (lane == 0) rowsum[j * NWAVE + wid] = s;
+      }
+    } else {
+      for (int i = lane; i < U; i += 64) {
+        const float x = xl_val[i];
+        const int64_t id = xl_id[i];
+        if (keep(x, id)) {
+          const float ev = ns_expf(div_rn(x, tdiv, rdiv) - My);
+          const int64_t rj = id < nch * EPC ? (id / EPC) / RT : nrows_j;
+          atomicAdd((unsigned long long*)&xrow[rj], (unsigned long long)mass_fx(ev));
+          if (ev > 0.0f && id > lastid) lastid = id;
+        }
+      }
+    }
+    lastid = block_max_i64(lastid, red);
+    // row totals and the row holding the crossing (wave 0, two rows per lane)
+    if (wid == 0) {
+      double tsum[2] = {0.0, 0.0};
+#pragma unroll
+      for (int q = 0; q < 2; ++q) {
+        const int64_t rj = lane * 2 + q;
+        if (rj < nrow_tot) {
+          double t = (double)xrow[rj] * FX_INV;
+          for (int w = 0; w < NWAVE; ++w) t += rowsum[rj * NWAVE + w];
+          tsum[q] = t;
+        }
+      }
+      const double pair = tsum[0] + tsum[1];
+      const double incl = wave_incl_scan(pair);
+      const double Z = __shfl(incl, 63);
+      const double Tu = (double)u * Z;
+      const double excl = incl - pair;
+      int found = -1;
+      double bef = 0.0;
+      if (excl <= Tu && excl + tsum[0] > Tu) { found = lane * 2; bef = excl; }
+      else if (excl + tsum[0] <= Tu && excl + pair > Tu) { found = lane * 2 + 1; bef = excl + tsum[0]; }
+      const uint64_t fm = ballot(found >= 0 && found < nrow_tot);
+      if (lane == 0) { misc->ib[5] = -1; misc->db[0] = Tu; misc->db[1] = Z; }
+      if (fm != 0ull) {
+        const int fl = __builtin_ctzll(fm);
+        if (lane == fl) { misc->ib[5] = found; misc->db[2] = bef; }
+      }
+    }
+    __syncthreads();
+    const int jstar = misc->ib[5];
+    const double Tt = misc->db[0] - misc->db[2];
+    int64_t token = -1;
+    if (jstar < 0) {
+      token = lastid;
+    } else if (jstar == nrows_j) {
+      // tail row: extras with ids beyond the chunk layout, in id order (at most EPC-1 of them)
+      if (tid == 0) {
+        double run = 0.0;
+        int64_t last = -1;
+        for (int64_t id = nch * EPC; id < V && token < 0; ++id) {
+          for (int i = 0; i < U; ++i) {
+            if (xl_id[i] == id && keep(xl_val[i], id)) {
+              const float ev = ns_expf(div_rn(xl_val[i], tdiv, rdiv) - My);
+              run += (double)ev;
+              if (ev > 0.0f) last = id;
+              if (run > Tt) token = id;
+            }
+          }
+        }
+        misc->ib[6] = (int)(token >= 0 ? token : (last >= 0 ? last : lastid));
+      }
+      __syncthreads();
+      token = misc->ib[6];
+    } else {
+      // chunk row jstar: per-thread chunk masses (history positions recomputed), scan, walk
+      const int64_t c = (int64_t)jstar * RT + tid;
+      const bool ok = rowthr && c < nch;
+      float xe[EPC];
+      double mt = 0.0;
+      uint4 w = ok ? rowv[c] : ninf_chunk<T>();
+      const uint32_t hb = (ok && pen_on) ? T::bits(bm, c) : 0u;
+#pragma unroll
+      for (int e = 0; e < EPC; ++e) {
+        float x = T::elem(w, e);
+        if ((hb >> e) & 1u) x = penalize(x, pen);
+        float ev = 0.0f;
+        if (ok && keep(x, c * EPC + e)) ev = ns_expf(div_rn(x, tdiv, rdiv) - My);
+        xe[e] = ev;
+        mt += (double)ev;
+      }
+      double tot;
+      const double pre = block_excl_scan(mt, &tot, red);
+      if (tid == 0) { misc->ib[6] = -1; misc->ib[7] = -1; }
+      __syncthreads();
+      if (ok && mt > 0.0) {
+        double run = pre;
+        int64_t lastk = -1;
+        for (int e = 0; e < EPC; ++e) {
+          if (xe[e] > 0.0f) {
+            const double b4 = run;
+            run += (double)xe[e];
+            lastk = c * EPC + e;
+            if (run > Tt && !(b4 > Tt)) misc->ib[6] = (int)(c * EPC + e);
+          }
+        }
+        atomicMax(&misc->ib[7], (int)lastk);
+      }
+      __syncthreads();
+      token = misc->ib[6];
+      if (token < 0) {
+        flags |= FLAG_LOCATE_FALLBACK;
+        token = misc->ib[7] >= 0 ? misc->ib[7] : lastid;
+      }
+    }
+    if (tid == 0) P.out_ids[row] = token < 0 ? 0 : token;
+    write_info(o, PATH_LARGE_DRAW, (int32_t)n_kept, thr_y, n_topk, -1, flags, vstar, (int32_t)istar);
+    if (P.out_probs != nullptr) {
+      const double Z = misc->db[1];
+      __syncthreads();
+      float* pr = P.out_probs + (int64_t)row * V;
+      if (rowthr) {
+        for (int64_t cc = tid; cc < nch; cc += RT) {
+          uint4 w2 = rowv[cc];
+          if (pen_on) w2 = T::mask(w2, T::bits(bm, cc));
+#pragma unroll
+          for (int e = 0; e < EPC; ++e) {
+            const float x = T::elem(w2, e);
+            const int64_t id = cc * EPC + e;
+            pr[id] = keep(x, id) ? (float)((double)ns_expf(div_rn(x, tdiv, rdiv) - My) / Z) : 0.0f;
+          }
+        }
+      } else {
+        for (int64_t id = nch * EPC + lane; id < V; id += 64) pr[id] = 0.0f;
+      }
+      __syncthreads();
+      if (hwave)
+        for (int i = lane; i < U; i += 64) {
+          const float x = xl_val[i];
+          const int64_t id = xl_id[i];
+          pr[id] = keep(x, id) ? (float)((double)ns_expf(div_rn(x, tdiv, rdiv) - My) / Z) : 0.0f;
+        }
+    }
+  }
+}
+
+template <typename T>
+__global__ __launch_bounds__(NT) void sample_kernel(const KParams P) {
+  extern __shared__ __align__(16) unsigned char smem[];
+  Misc* misc = reinterpret_cast<Misc*>(smem);
+  uint32_t* bm = reinterpret_cast<uint32_t*>(smem + P.off_bm);
+  float* xl_val = reinterpret_cast<float*>(smem + P.off_xl);
+  int32_t* xl_id = reinterpret_cast<int32_t*>(smem + P.off_xl + 4u * (uint32_t)P.xcap);
+  uint64_t* cand = reinterpret_cast<uint64_t*>(smem + P.off_cand);
+  uint32_t* hcnt = reinterpret_cast<uint32_t*>(smem + P.off_hist);
+  uint64_t* hmass = reinterpret_cast<uint64_t*>(smem + P.off_hist + 4u * NB);
+  BlockScratch* red = &misc->red;
+
+  const int tid = threadIdx.x;
+  const int lane = lane_id();
+  const int wid = wave_id();
+  const bool rowthr = tid < RT;
+  const bool hwave = wid == NWAVE - 1;
+  const int row = blockIdx.x;
+  const int64_t V = P.vocab;
+  constexpr int EPC = T::EPC;
+  const int64_t nch = V / EPC;
+  const int ntail = (int)(V - nch * EPC);
+  const int64_t nrows_j = (nch + RT - 1) / RT;
+  const RowOut o{P.out_ids, P.out_probs, P.out_info, row, V};
+
+  // ---- row parameters (uniform across the workgroup)
+  const int64_t src = P.sample_idx ? P.sample_idx[row] : (int64_t)row;
+  const float temp = P.temperature[row];
+  const float topp = P.top_p[row];
+  const float pen = P.penalty[row];
+  float u = P.uniforms[row];
+  u = (u >= 0.0f) ? (u < 1.0f ? u : 0x1.fffffep-1f) : 0.0f;
+  const int32_t k = P.top_k[row];
+  int32_t h0 = 0, h1 = 0;
+  if (P.hist_off != nullptr) { h0 = P.hist_off[row]; h1 = P.hist_off[row + 1]; }
+  int32_t flags = 0;
+  if (src < 0 || src >= P.n_rows_total) flags |= FLAG_BAD_ROW;
+  if (h1 < h0 || h1 - h0 > MAX_HIST || h1 - h0 > P.xcap - 8) flags |= FLAG_HIST_TOO_LONG;
+  if (flags != 0) {
+    if (tid == 0) P.out_ids[row] = -1;
+    write_info(o, PATH_ERROR, 0, 0.0f, 0, 0, flags, 0.0f, -1);
+    return;
+  }
+  const unsigned char* rowp = (const unsigned char*)P.logits + src * P.row_stride * T::SZ;
+  const uint4* rowv = reinterpret_cast<const uint4*>(rowp);
+  const bool greedy = temp == 0.0f;
+  const float tdiv = temp > 0.0f ? __builtin_fmaxf(temp, 1e-6f) : 1.0f;  // sampler.py:42
+  const float rdiv = 1.0f / tdiv;
+  const int32_t H = h1 - h0;
+  const bool pen_on = (pen != 1.0f) && H > 0;                            // sampler.py:33
+  const bool topk_on = k > 0 && (int64_t)k < V;                          // sampler.py:55
+  const bool topp_on = topp < 1.0f;                                      // sampler.py:63
+  const float p32 = topp;
+
+  // ---- phase 0: history ids (all threads), then the row loads, zero LDS state
+  int32_t hid[HPT];
+  {
+    const int32_t* hp = P.hist_ids + h0;
+#pragma unroll
+    for (int s = 0; s < HPT; ++s) {
+      const int32_t i = s * NT + tid;
+      hid[s] = -1;
+      if (pen_on && i < H) hid[s] = hp[i];
+    }
+  }
+  if (pen_on) {
+    const int nbw = (int)((V + 31) / 32);
+    for (int i = tid; i < nbw; i += NT) bm[i] = 0u;
+  }
+  if (tid == 0) { misc->xl_n = 0; misc->cand_n = 0; misc->flags = 0; }
+  __syncthreads();
+
+  // ---- phase 1: presence bitmap and unique history ids (set semantics, sampler.py:34-38)
+  if (pen_on) {
+#pragma unroll
+    for (int s = 0; s < HPT; ++s) {
+      if (s * NT < H) {
+        const int32_t id = hid[s];
+        const bool act = s * NT + tid < H;
+        const bool valid = act && id >= 0 && (int64_t)id < V;
+        if (act && !valid) atomicOr(&misc->flags, FLAG_BAD_HIST_ID);
+        bool uniq = false;
+        if (valid) {
+          const uint32_t bit = 1u << (id & 31);
+          const uint32_t old = atomicOr(&bm[id >> 5], bit);
+          uniq = (old & bit) == 0u;
+        }
+        const uint64_t m = ballot(uniq);
+        if (m != 0ull) {
+          int base = 0;
+          if (lane == 0) base = atomicAdd(&misc->xl_n, __popcll(m));
+          base = __shfl(base, 0);
+          if (uniq) xl_id[base + lanes_below(m)] = id;
+        }
+      }
+    }
+  }
+  __syncthreads();
+
+  // ---- phase 2: history wave gathers and penalizes; row threads run P1
+  float tmax = NEG_INF;
+  int targ = -1;
+  float gm[NGROUP];
+#pragma unroll
+  for (int g = 0; g < NGROUP; ++g) gm[g] = NEG_INF;
+  if (hwave) {
+    int U = misc->xl_n;
+    if (pen_on) {
+      for (int base = 0; base < U; base += 64 * GATHER) {
+        float xv[GATHER];
+#pragma unroll
+        for (int s = 0; s < GATHER; ++s) {
+          int i = base + s * 64 + lane;
+          xv[s] = i < U ? T::load1(rowp, xl_id[i]) : 0.0f;
+        }
+#pragma unroll
+        for (int s = 0; s < GATHER; ++s) {
+          int i = base + s * 64 + lane;
+          if (i < U) xl_val[i] = penalize(xv[s], pen);
+        }
+      }
+    }
+    if (ntail > 0) {
+      const bool act = lane < ntail;
+      const int64_t id = nch * EPC + lane;
+      const bool inhist = act && pen_on && ((bm[id >> 5] >> (id & 31)) & 1u);
+      const bool take = act && !inhist;
+      const float x = take ? T::load1(rowp, id) : 0.0f;
+      const uint64_t m = ballot(take);
+      const int pos = U + lanes_below(m);
+      if (take) { xl_id[pos] = (int32_t)id; xl_val[pos] = x; }
+      U += __popcll(m);
+    }
+    if (lane == 0) misc->xl_n = U;
+  } else {
+    const int64_t jg = (nrows_j + NGROUP - 1) / NGROUP;
+#pragma unroll
+    for (int g = 0; g < NGROUP; ++g) {
+      const int64_t j0 = g * jg;
+      const int64_t j1 = j0 + jg < nrows_j ? j0 + jg : nrows_j;
+      float gmax = NEG_INF;
+      for (int64_t j = j0; j < j1; j += 4) {
+        uint4 v[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const int64_t c = (j + q) * RT + tid;
+          v[q] = (j + q < j1 && c < nch) ? rowv[c] : ninf_chunk<T>();
+        }
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const int64_t c = (j + q) * RT + tid;
+          if (j + q < j1 && c < nch) {
+            if (pen_on) v[q] = T::mask(v[q], T::bits(bm, c));
+            const float m = chunk_max<T>(v[q]);
+            if (m > tmax || (m != m && tmax == tmax)) { tmax = m; targ = (int)(j + q); }
+            gmax = fmax_nan(gmax, m);
+          }
+        }
+      }
+      gm[g] = gmax;
+    }
+  }
+  __syncthreads();
+  const int U = misc->xl_n;
+  flags |= misc->flags;
+
+  // ---- row max over chunks and extras
+  float my = rowthr ? tmax : NEG_INF;
+  if (hwave)
+    for (int i = lane; i < U; i += 64) my = fmax_nan(my, xl_val[i]);
+  const float Mx = block_max_nan(my, red);
+  const float My = div_rn(Mx, tdiv, rdiv);
+
+  // ---- greedy rows: first index of the maximum (sampler.py:82-83, 88)
+  if (greedy) {
+    const bool nanrow = Mx != Mx;
+    int64_t best = INT64_MAX;
+    if (rowthr) {
+      {
+        if (nanrow) {
+          visit_rows<T>(rowv, bm, pen_on, nch, nrows_j, [&](float x, int64_t id, int64_t) {
+            if (x != x && id < best) best = id;
+          });
+        } else if (targ >= 0 && tmax == Mx) {
+          const int64_t c = (int64_t)targ * RT + tid;
+          uint4 w = rowv[c];
+          if (pen_on) w = T::mask(w, T::bits(bm, c));
+#pragma unroll
+          for (int e = 0; e < EPC; ++e)
+            if (T::elem(w, e) == Mx && c * EPC + e < best) best = c * EPC + e;
+        }
+      }
+    }
+    if (hwave)
+      for (int i = lane; i < U; i += 64) {
+        const float x = xl_val[i];
+        if ((nanrow ? (x != x) : (x == Mx)) && xl_id[i] < best) best = xl_id[i];
+      }
+    best = block_min_i64(best, red);
+    if (tid == 0) P.out_ids[row] = best == INT64_MAX ? 0 : best;
+    write_info(o, PATH_GREEDY, 1, NEG_INF, 0, 0, flags, Mx, (int32_t)best);
+    return;
+  }
+
+  // ---- rows whose softmax is NaN: uniform 1/V over the vocabulary (sampler.py:77-80)
+  if (!(__builtin_fabsf(My) <= FLT_MAXV)) {
+    const float q = (float)(1.0 / (double)V);
+    const double qd = q, ud = u;
+    if (tid == 0) {
+      int64_t i = (int64_t)(ud / qd);
+      while (i > 0 && (double)i * qd > ud) --i;
+      while ((double)(i + 1) * qd <= ud && i < V) ++i;
+      if (i >= V) i = V - 1;
+      P.out_ids[row] = i;
+    }
+    write_info(o, PATH_UNIFORM, (int32_t)V, NEG_INF, (int32_t)V, 0, flags, My, -1);
+    if (P.out_probs != nullptr) {
+      float* pr = P.out_probs + (int64_t)row * V;
+      for (int64_t i = tid; i < V; i += NT) pr[i] = q;
+    }
+    return;
+  }
+
+  // ---- top-k with k <= KSMALL: threshold from chunk maxima, candidates to LDS
+  if (topk_on && k <= KSMALL) {
+    const float tau = select_tau<NGROUP>(gm, rowthr, k, hcnt, misc);
+    const float tc = lower_preimage(tau, tdiv, rdiv);
+    if (tid == 0) misc->cand_n = 0;
+    __syncthreads();
+    if (hwave) {
+      for (int base = 0; base < U; base += 64) {
+        const int i = base + lane;
+        const float x = i < U ? xl_val[i] : NEG_INF;
+        cand_append(i < U && x >= tc, x, i < U ? xl_id[i] : 0, cand, misc);
+      }
+    } else {
+      const int64_t jg = (nrows_j + NGROUP - 1) / NGROUP;
+#pragma unroll
+      for (int g = 0; g < NGROUP; ++g) {
+        if (ballot(gm[g] >= tc) != 0ull) {
+          const bool hitg = gm[g] >= tc;
+          const int64_t j0 = g * jg;
+          const int64_t j1 = j0 + jg < nrows_j ? j0 + jg : nrows_j;
+          for (int64_t j = j0; j < j1; ++j) {
+            const int64_t c = j * RT + tid;
+            const bool ok = hitg && c < nch;
+            uint4 w = ok ? rowv[c] : ninf_chunk<T>();
+            if (ok && pen_on) w = T::mask(w, T::bits(bm, c));
+#pragma unroll
+            for (int e = 0; e < EPC; ++e) {
+              const float x = T::elem(w, e);
+              cand_append(ok && x >= tc, x, c * EPC + e, cand, misc);
+            }
+          }
+        }
+      }
+    }
+    __syncthreads();
+    const int n = misc->cand_n;
+    if (n <= CAP) {
+      lds_set(n, true, k, topp_on, p32, My, tdiv, rdiv, u, cand, misc, o, PATH_TOPK_SET, flags, NEG_INF, 0);
+      return;
+    }
+    flags |= FLAG_CAND_OVERFLOW;
+  }
+
+  generic_path<T>(GCtx{rowv, bm, xl_val, xl_id, cand, hcnt, hmass, misc, P.out_ids, P.out_probs, P.out_info,
+                      V, nch, nrows_j, row, U, k, flags, pen, tdiv, rdiv, p32, Mx, My, u, pen_on, topk_on, topp_on});
+}
+
+}  // namespace ns
+
+// =====================================================================================
+// C ABI
+// =====================================================================================
+namespace {
+thread_local std::string g_err;
+int fail(int code, const std::string& msg) {
+  g_err = msg;
+  return code;
+}
+}  // namespace
+
+extern "C" {
+
+int ns_abi_version(void) { return NS_ABI_VERSION; }
+
+const char* ns_last_error(void) { return g_err.c_str(); }
+
+int ns_sample_lds_bytes(int64_t vocab, int32_t max_hist, int32_t* lds_bytes) {
+  if (lds_bytes == nullptr) return fail(NS_ERR_INVALID, "lds_bytes is NULL");
+  if (vocab <= 0 || vocab > NS_MAX_VOCAB) return fail(NS_ERR_INVALID, "vocab out of range");
+  if (max_hist < 0 || max_hist > NS_MAX_HISTORY) return fail(NS_ERR_INVALID, "max_hist out of range");
+  const int64_t nbw = (vocab + 31) / 32;
+  const int64_t uniq = max_hist < vocab ? max_hist : vocab;
+  const int64_t xcap = ((uniq + 8 + 3) / 4) * 4;
+  int64_t off = ((int64_t)sizeof(ns::Misc) + 15) / 16 * 16;
+  off += (nbw * 4 + 15) / 16 * 16;
+  off += (xcap * 8 + 15) / 16 * 16;
+  off += (int64_t)ns::CAP * 8;
+  off += (int64_t)ns::NB * 12;
+  *lds_bytes = (int32_t)off;
+  return NS_OK;
+}
+
+int ns_sample(const ns_sample_args* a, hipStream_t stream) {
+  if (a == nullptr) return fail(NS_ERR_INVALID, "args is NULL");
+  if (a->n_sample < 0) return fail(NS_ERR_INVALID, "n_sample < 0");
+  if (a->n_sample == 0) return NS_OK;
+  if (a->logits == nullptr || a->temperature == nullptr || a->top_k == nullptr || a->top_p == nullptr ||
+      a->rep_penalty == nullptr || a->uniforms == nullptr || a->out_ids == nullptr)
+    return fail(NS_ERR_INVALID, "a required pointer is NULL");
+  if (a->dtype != NS_DTYPE_F32 && a->dtype != NS_DTYPE_BF16) return fail(NS_ERR_INVALID, "dtype must be f32 or bf16");
+  if (a->vocab <= 0 || a->vocab > NS_MAX_VOCAB)
+    return fail(NS_ERR_INVALID, "vocab must be in [1, " + std::to_string(NS_MAX_VOCAB) + "]");
+  if (a->row_stride < a->vocab) return fail(NS_ERR_INVALID, "row_stride < vocab");
+  if (a->n_rows_total <= 0) return fail(NS_ERR_INVALID, "n_rows_total <= 0");
+  if (a->sample_idx == nullptr && a->n_rows_total < a->n_sample)
+    return fail(NS_ERR_INVALID, "n_rows_total < n_sample without sample_idx");
+  if (a->hist_offsets != nullptr && a->hist_ids == nullptr) return fail(NS_ERR_INVALID, "hist_ids is NULL");
+  if (a->max_hist < 0 || a->max_hist > NS_MAX_HISTORY)
+    return fail(NS_ERR_INVALID, "max_hist must be in [0, " + std::to_string(NS_MAX_HISTORY) + "]");
+  const int esz = a->dtype == NS_DTYPE_F32 ? 4 : 2;
+  if (((uintptr_t)a->logits % 16) != 0 || ((a->row_stride * esz) % 16) != 0)
+    return fail(NS_ERR_ALIGN, "logits rows must start on 16-byte boundaries (base and row stride)");
+
+  int32_t lds = 0;
+  int rc = ns_sample_lds_bytes(a->vocab, a->hist_offsets ? a->max_hist : 0, &lds);
+  if (rc != NS_OK) return rc;
+  ns::KParams p{};
+  p.logits = a->logits;
+  p.row_stride = a->row_stride;
+  p.vocab = a->vocab;
+  p.n_rows_total = a->n_rows_total;
+  p.sample_idx = a->sample_idx;
+  p.temperature = a->temperature;
+  p.top_k = a->top_k;
+  p.top_p = a->top_p;
+  p.penalty = a->rep_penalty;
+  p.hist_off = a->hist_offsets;
+  p.hist_ids = a->hist_ids;
+  p.uniforms = a->uniforms;
+  p.out_ids = a->out_ids;
+  p.out_probs = a->out_probs;
+  p.out_info = a->out_info;
+  p.n_sample = a->n_sample;
+  {
+    const int64_t mh = a->hist_offsets ? a->max_hist : 0;
+    const int64_t nbw = (a->vocab + 31) / 32;
+    const int64_t uniq = mh < a->vocab ? mh : a->vocab;
+    const int64_t xcap = ((uniq + 8 + 3) / 4) * 4;
+    uint32_t off = (uint32_t)(((int64_t)sizeof(ns::Misc) + 15) / 16 * 16);
+    p.off_bm = off;
+    off += (uint32_t)((nbw * 4 + 15) / 16 * 16);
+    p.off_xl = off;
+    p.xcap = (int32_t)xcap;
+    off += (uint32_t)((xcap * 8 + 15) / 16 * 16);
+    p.off_cand = off;
+    off += (uint32_t)ns::CAP * 8u;
+    p.off_hist = off;
+  }
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return fail(NS_ERR_HIP, std::string("hipGetDevice: ") + hipGetErrorString(e));
+  int max_lds = 0;
+  e = hipDeviceGetAttribute(&max_lds, hipDeviceAttributeMaxSharedMemoryPerBlock, dev);
+  if (e != hipSuccess) return fail(NS_ERR_HIP, std::string("hipDeviceGetAttribute: ") + hipGetErrorString(e));
+  if (lds > max_lds)
+    return fail(NS_ERR_INVALID, "LDS requirement " + std::to_string(lds) + " exceeds device limit " +
+                                    std::to_string(max_lds));
+
+  const dim3 grid((unsigned)a->n_sample), block(ns::NT);
+  if (a->dtype == NS_DTYPE_BF16) hipLaunchKernelGGL((ns::sample_kernel<ns::BF16>), grid, block, lds, stream, p);
+  else hipLaunchKernelGGL((ns::sample_kernel<ns::F32>), grid, block, lds, stream, p);
+  e = hipGetLastError();
+  if (e != hipSuccess) return fail(NS_ERR_HIP, std::string("kernel launch: ") + hipGetErrorString(e));
+  return NS_OK;
+}
+
+}  // extern "C"

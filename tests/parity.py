@@ -1,0 +1,101 @@
+"""Parity harness: run the HIP sampler through its C ABI and compare with the oracle.
+
+The comparison bar (per sampled row):
+  * token ids bit-exact, except rows the oracle marks exempt: the uniform lies
+    within ``1e-6 + zone_mass`` of a cumulative-mass boundary next to the pick,
+    or more than 1e-5 of probability sits in the ambiguous top-p zone;
+  * greedy rows: ids bit-exact with no exemption;
+  * the top-k threshold (scaled logit of the k-th largest) bit-exact;
+  * final probabilities within 1e-5 relative (plus a 1e-12 absolute floor),
+    tokens of the ambiguous top-p zone excepted;
+  * kept-token count equal up to the size of the zone.
+"""
+from __future__ import annotations
+
+import numpy as np
+import torch
+
+from conftest import pkg
+
+W = pkg("workloads")
+L = pkg("_lib")
+S = pkg("sampler")
+C = pkg("config")
+
+PROB_RTOL = 1e-5
+PROB_ATOL = 1e-12
+
+
+def params_of(w):
+    return [C.SamplingParams(temperature=float(w.temperature[i]), top_k=int(w.top_k[i]), top_p=float(w.top_p[i]),
+                             repetition_penalty=float(w.repetition_penalty[i])) for i in range(w.batch)]
+
+
+def run_gpu(w, device, logits=None, want_probs=True, uniforms=None):
+    """One ns_sample call over workload ``w``; returns ids, probs (CPU) and info words."""
+    packed = S.PackedRows(params_of(w), w.histories, w.vocab)
+    d = packed.to_device(device)
+    if logits is None:
+        logits = w.device_logits(device)
+    B, V = w.batch, w.vocab
+    u = torch.from_numpy(np.asarray(w.uniforms if uniforms is None else uniforms, dtype=np.float32)).to(device)
+    sidx = torch.from_numpy(w.sample_indices).to(device) if w.sample_indices is not None else None
+    out = torch.full((B,), -7, dtype=torch.int64, device=device)
+    probs = torch.zeros((B, V), dtype=torch.float32, device=device) if want_probs else None
+    info = torch.zeros((B, L.NS_INFO_WORDS), dtype=torch.int32, device=device)
+    L.sample_raw(logits, d["temperature"], d["top_k"], d["top_p"], d["rep_penalty"], u, out,
+                 sample_idx=sidx, hist_offsets=d["hist_offsets"], hist_ids=d["hist_ids"],
+                 max_hist=packed.max_hist, out_probs=probs, out_info=info)
+    torch.cuda.synchronize()
+    return {"ids": out.cpu().numpy(), "probs": None if probs is None else probs.cpu(),
+            "info": info.cpu().numpy()}
+
+
+def f32_bits(x) -> int:
+    return int(np.asarray(x, dtype=np.float32).view(np.int32))
+
+
+def compare(g, r, check_probs: bool = True, max_report: int = 8):
+    """Return (failures, stats) comparing GPU output ``g`` with OracleResult ``r``."""
+    B = len(r.ids)
+    fails = []
+    stats = {"rows": B, "exempt": 0, "greedy": int(r.greedy.sum()), "id_equal": 0, "zone_rows": 0,
+             "max_prob_rel": 0.0}
+    for i in range(B):
+        gi, ri = int(g["ids"][i]), int(r.ids[i])
+        info = g["info"][i]
+        exempt = bool(r.exempt[i])
+        stats["exempt"] += int(exempt)
+        if gi == ri:
+            stats["id_equal"] += 1
+        elif r.greedy[i] or not exempt:
+            fails.append(f"row {i}: id {gi} != oracle {ri} (path {info[0]}, flags {info[5]}, greedy {r.greedy[i]})")
+        if r.greedy[i] or r.nan_row[i]:
+            continue
+        if not np.isnan(r.topk_thr[i]):
+            if int(info[2]) != f32_bits(r.topk_thr[i]):
+                g_thr = np.int32(info[2]).view(np.float32)
+                fails.append(f"row {i}: top-k threshold {g_thr!r} != oracle {r.topk_thr[i]!r} (path {info[0]})")
+        zone = r.zone_ids[i]
+        nz = len(zone)
+        stats["zone_rows"] += int(nz > 0)
+        if abs(int(info[1]) - int(r.n_kept[i])) > nz:
+            fails.append(f"row {i}: kept {info[1]} vs oracle {r.n_kept[i]} (zone {nz}, path {info[0]})")
+        if check_probs and g["probs"] is not None and not r.topp_boundary[i]:
+            pg = g["probs"][i].double()
+            po = r.probs[i].double()
+            diff = (pg - po).abs()
+            tol = PROB_RTOL * torch.maximum(pg.abs(), po.abs()) + PROB_ATOL + po.abs() * r.zone_mass[i]
+            if nz:
+                diff[torch.as_tensor(zone)] = 0.0
+            bad = diff > tol
+            rel = (diff / torch.clamp(po.abs(), min=1e-30))[po > 1e-9]
+            if rel.numel():
+                stats["max_prob_rel"] = max(stats["max_prob_rel"], float(rel.max()))
+            if bool(bad.any()):
+                j = int(torch.nonzero(bad)[0, 0])
+                fails.append(f"row {i}: prob[{j}] {float(pg[j])!r} vs oracle {float(po[j])!r} "
+                             f"({int(bad.sum())} tokens off, path {info[0]})")
+    if len(fails) > max_report:
+        fails = fails[:max_report] + [f"... {len(fails) - max_report} more"]
+    return fails, stats

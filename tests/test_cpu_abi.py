@@ -1,0 +1,86 @@
+"""CPU-only checks of the boundary: the C-ABI library loads, exports every symbol
+declared in include/ns_sampling.h, reports its ABI version and validates
+arguments without touching a GPU; the host packing mirrors the reference."""
+import ctypes
+import os
+import re
+
+import numpy as np
+import pytest
+
+from conftest import ROOT, pkg
+
+L = pkg("_lib")
+S = pkg("sampler")
+C = pkg("config")
+
+HEADER = os.path.join(ROOT, "include", "ns_sampling.h")
+
+
+def header_functions():
+    txt = open(HEADER).read()
+    return sorted(set(re.findall(r"^\s*(?:int|const char\*)\s+(ns_\w+)\s*\(", txt, flags=re.M)))
+
+
+def test_header_declares_the_binding_exports():
+    assert header_functions() == sorted(L.EXPORTS)
+
+
+def test_library_exports_every_header_symbol():
+    if not os.path.exists(L.LIB_PATH):
+        pytest.skip("library not built (run __graft_entry__.build())")
+    lib = ctypes.CDLL(L.LIB_PATH)
+    for name in header_functions():
+        assert hasattr(lib, name), name
+    assert L.load().ns_abi_version() == L.ABI_VERSION
+
+
+def test_struct_layout_matches_header():
+    # ns_sample_args field order/types must match the C declaration
+    txt = open(HEADER).read()
+    body = txt[txt.index("typedef struct ns_sample_args"):txt.index("} ns_sample_args;")]
+    names = re.findall(r"^\s*[\w\s\*]+?\b(\w+);", body, flags=re.M)
+    assert names == [f[0] for f in L.NsSampleArgs._fields_]
+    assert ctypes.sizeof(L.NsSampleArgs) == 136
+
+
+def test_lds_bytes_and_argument_errors():
+    if not os.path.exists(L.LIB_PATH):
+        pytest.skip("library not built")
+    assert L.lds_bytes(128256, 2048) <= 160 * 1024
+    assert L.lds_bytes(262144, 8192) <= 160 * 1024
+    with pytest.raises(L.SamplerLibraryError, match="vocab"):
+        L.lds_bytes(0, 0)
+    with pytest.raises(L.SamplerLibraryError, match="max_hist"):
+        L.lds_bytes(1000, 9000)
+    lib = L.load()
+    a = L.NsSampleArgs()
+    a.n_sample = 1
+    assert lib.ns_sample(ctypes.byref(a), None) == 1
+    assert "NULL" in L.last_error()
+    a.n_sample = 0
+    assert lib.ns_sample(ctypes.byref(a), None) == 0
+
+
+def test_packing_follows_reference_rules():
+    P = C.SamplingParams
+    params = [P(temperature=0.0), P(temperature=1e-9), P(temperature=-2.0), P(temperature=0.7, top_k=2**40),
+              P(top_k=-5, top_p=0.95, repetition_penalty=1.2), P(repetition_penalty=1.0)]
+    hist = [[1, 2], [3], [], [4, 4, 4], [9, 0, 9], [7]]
+    pk = S.PackedRows(params, hist, vocab=10)
+    # sampler.py:42: t' = max(t, 1e-6) if t > 0 else 1.0; greedy encoded as 0
+    assert pk.temperature.tolist() == [0.0, np.float32(1e-6), 1.0, np.float32(0.7), 1.0, 1.0]
+    assert pk.top_k.tolist() == [-1, -1, -1, 2**31 - 1, -1, -1]
+    # only penalised rows carry their history (sampler.py:33)
+    assert pk.hist_offsets.tolist() == [0, 0, 0, 0, 0, 3, 3]
+    assert pk.hist_ids.tolist() == [9, 0, 9]
+    assert pk.max_hist == 3
+    with pytest.raises(IndexError):
+        S.PackedRows([P(repetition_penalty=1.1)], [[10]], vocab=10)
+
+
+def test_sampling_params_match_reference_defaults():
+    p = C.SamplingParams()
+    assert (p.max_tokens, p.temperature, p.top_p, p.top_k, p.repetition_penalty, p.ignore_eos, p.seed) == \
+        (128, 1.0, 1.0, -1, 1.0, False, None)
+    assert p.stop_token_ids == [] and p.stop == []
