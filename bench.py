@@ -1,0 +1,230 @@
+"""Benchmark of the MI355X token sampler (one ns_sample launch per step).
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--cpu-rows R]
+
+Workload: the decode-heavy batch -- 256 sampled rows x vocab 128256, logits
+stored as bfloat16 (N(0, 3^2)) and upcast in the kernel, temperature 1.0,
+top_k 50, top_p 0.95, repetition penalty 1.1 over 2048 Zipf-distributed
+history ids per row, one uniform per row.  A step is one ``ns_sample`` call
+over the whole batch with every input already resident in device memory.
+
+The timed loop rotates ROTATE independent input sets (logits, histories and
+uniforms) so that the working set (> 512 MB) exceeds the 256 MB Infinity
+Cache and the rate measured is the HBM rate.  Kernel time is taken with HIP
+events on the stream the kernel is launched on.
+
+Prints one JSON line: rows/s (whole job), the roofline of the sampling
+kernel against MI355X's 8 TB/s HBM peak, and the CPU baseline (the reference
+sampler's op sequence restated on torch CPU, timed on this host).
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes
+import importlib
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+PKG = "nanoserve---custom-llm-inference-engine_amd"
+
+HBM_PEAK_GBS = 8000.0
+ROTATE = 8
+WORKLOAD_CFG = 2
+METRIC = "sampled rows/sec at B=256, V=128256 fp32; achieved HBM GB/s vs peak"
+
+
+def _pkg(sub=""):
+    return importlib.import_module(PKG + ("." + sub if sub else ""))
+
+
+def build_sets(w, dev, n_sets):
+    """Device inputs for ``n_sets`` independent calls over workload ``w``."""
+    import torch
+
+    S = _pkg("sampler")
+    C = _pkg("config")
+    params = [C.SamplingParams(temperature=float(w.temperature[i]), top_k=int(w.top_k[i]), top_p=float(w.top_p[i]),
+                               repetition_penalty=float(w.repetition_penalty[i])) for i in range(w.batch)]
+    sets = []
+    for s in range(n_sets):
+        if s == 0:
+            logits = w.device_logits(dev)
+        else:
+            g = torch.Generator(device=dev)
+            g.manual_seed(5150 + s)
+            x = torch.randn((w.batch, w.vocab), generator=g, device=dev, dtype=torch.float32).mul_(3.0)
+            logits = x.to(torch.bfloat16) if w.bf16_bits is not None else x
+            del x
+        hist = w.histories if s == 0 else [np.roll(h, s) for h in w.histories]
+        packed = S.PackedRows(params, hist, w.vocab)
+        d = packed.to_device(dev)
+        rng = np.random.default_rng(900 + s)
+        u = w.uniforms if s == 0 else rng.random(w.batch, dtype=np.float32)
+        ut = torch.from_numpy(np.asarray(u, dtype=np.float32)).to(dev)
+        out = torch.empty(w.batch, dtype=torch.int64, device=dev)
+        sets.append(dict(logits=logits, d=d, max_hist=packed.max_hist, u=ut, out=out))
+    torch.cuda.synchronize()
+    return sets
+
+
+def make_args(L, st):
+    import torch
+
+    logits = st["logits"]
+    d = st["d"]
+    a = L.NsSampleArgs()
+    a.logits = logits.data_ptr()
+    a.dtype = L.NS_DTYPE_BF16 if logits.dtype == torch.bfloat16 else L.NS_DTYPE_F32
+    a.n_sample = int(st["out"].shape[0])
+    a.n_rows_total = int(logits.shape[0])
+    a.vocab = int(logits.shape[1])
+    a.row_stride = int(logits.stride(0))
+    a.sample_idx = 0
+    a.temperature = d["temperature"].data_ptr()
+    a.top_k = d["top_k"].data_ptr()
+    a.top_p = d["top_p"].data_ptr()
+    a.rep_penalty = d["rep_penalty"].data_ptr()
+    a.hist_offsets = 0 if d["hist_offsets"] is None else d["hist_offsets"].data_ptr()
+    a.hist_ids = 0 if d["hist_ids"] is None else d["hist_ids"].data_ptr()
+    a.max_hist = int(st["max_hist"])
+    a.uniforms = st["u"].data_ptr()
+    a.out_ids = st["out"].data_ptr()
+    a.out_probs = 0
+    a.out_info = 0
+    return a
+
+
+def cpu_baseline(w, rows: int, reps: int):
+    """The reference sampler's op sequence on torch CPU over ``rows`` rows of the workload."""
+    import torch
+
+    from oracle import sampler_oracle as O  # the CPU restatement of sampler.py:28-89
+
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    rows = min(rows, w.batch)
+    x = torch.from_numpy(np.ascontiguousarray(w.rows[:rows]))
+    args = (w.temperature[:rows], w.top_k[:rows], w.top_p[:rows], w.repetition_penalty[:rows],
+            [list(map(int, h)) for h in w.histories[:rows]])
+    gen = torch.Generator()
+    gen.manual_seed(0)
+    O.reference_restatement_multinomial(x[:1], *(a[:1] for a in args), generator=gen)  # warm
+    times = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        O.reference_restatement_multinomial(x, *args, generator=gen)
+        times.append(time.perf_counter() - t0)
+    med = float(np.median(times))
+    return {"value": rows / med, "unit": "rows/s", "cores": cores, "kind": "port",
+            "sample": f"{rows} rows of the same workload (fp32 logits, the reference's .float() input), "
+                      f"median of {reps} runs of {med:.2f} s; torch {torch.__version__} CPU"}
+
+
+def main(argv=None):
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=400)
+    ap.add_argument("--warmup", type=int, default=40)
+    ap.add_argument("--cpu-rows", type=int, default=256, help="rows in the CPU-baseline sample (0 = skip)")
+    ap.add_argument("--cpu-reps", type=int, default=3)
+    args = ap.parse_args(argv)
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU: the sampler's rows are independent and this build runs on a single "
+              "MI355X; --gpus above 1 is not supported", file=sys.stderr)
+        return 2
+
+    import torch
+
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        return 2
+    W = _pkg("workloads")
+    L = _pkg("_lib")
+    lib = L.load()
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+
+    w = W.make_workload(WORKLOAD_CFG)
+    sets = build_sets(w, dev, ROTATE)
+    cargs = [make_args(L, st) for st in sets]
+    stream = torch.cuda.current_stream(dev)
+    sh = ctypes.c_void_p(int(stream.cuda_stream))
+    bytes_per_call = W.algorithmic_bytes(w)
+
+    def step(i):
+        rc = lib.ns_sample(ctypes.byref(cargs[i % ROTATE]), sh)
+        if rc != 0:
+            raise RuntimeError(f"ns_sample failed ({rc}): {L.last_error()}")
+
+    for i in range(args.warmup):
+        step(i)
+    torch.cuda.synchronize()
+    ev0 = torch.cuda.Event(enable_timing=True)
+    ev1 = torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    ev0.record(stream)
+    for i in range(args.steps):
+        step(i)
+    ev1.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    gpu_ms = ev0.elapsed_time(ev1)
+    ms_per_step = gpu_ms / args.steps
+    rows_per_s = w.batch / (ms_per_step * 1e-3)
+    achieved = bytes_per_call / (ms_per_step * 1e-3) / 1e9
+
+    # wrapper-inclusive rate (Sampler.sample: host packing and the host-to-device copy of params/histories)
+    S = _pkg()
+    C = _pkg("config")
+    params = [C.SamplingParams(temperature=float(w.temperature[i]), top_k=int(w.top_k[i]), top_p=float(w.top_p[i]),
+                               repetition_penalty=float(w.repetition_penalty[i])) for i in range(w.batch)]
+    hist_lists = [list(map(int, h)) for h in w.histories]
+    sampler = S.Sampler(dev)
+    for _ in range(3):
+        sampler.sample(sets[0]["logits"], params, hist_lists, uniforms=sets[0]["u"])
+    torch.cuda.synchronize()
+    nwrap = 10
+    t1 = time.perf_counter()
+    for _ in range(nwrap):
+        ids = sampler.sample(sets[0]["logits"], params, hist_lists, uniforms=sets[0]["u"])
+    ids.tolist()
+    wrap_ms = (time.perf_counter() - t1) / nwrap * 1e3
+
+    cpu = cpu_baseline(w, args.cpu_rows, args.cpu_reps) if args.cpu_rows > 0 else None
+    line = {
+        "metric": METRIC,
+        "value": rows_per_s,
+        "unit": "rows/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms_per_step,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (seeded N(0,3^2) logits rounded to bf16, Zipf histories)",
+        "config": {"workload": "decode batch B=256 x V=128256, bf16 logits upcast to f32 in-kernel, "
+                               "t=1.0 top_k=50 top_p=0.95 penalty=1.1, 2048 history ids/row",
+                   "batch": w.batch, "vocab": w.vocab, "history": 2048, "rotating_input_sets": ROTATE,
+                   "parallelism": "single GPU"},
+        "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": achieved / HBM_PEAK_GBS, "traffic": None},
+        "cpu_baseline": cpu,
+        "extra": {"algorithmic_bytes_per_call": bytes_per_call, "kernel_us": ms_per_step * 1e3,
+                  "wall_s": wall, "wrapper_inclusive_ms": wrap_ms,
+                  "wrapper_inclusive_rows_per_s": w.batch / (wrap_ms * 1e-3)},
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

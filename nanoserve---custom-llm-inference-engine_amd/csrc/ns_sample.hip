@@ -1165,6 +1165,10 @@ int ns_sample(const ns_sample_args* a, hipStream_t stream) {
                                     std::to_string(max_lds));
 
   const dim3 grid((unsigned)a->n_sample), block(ns::NT);
+  const void* fn = a->dtype == NS_DTYPE_BF16 ? reinterpret_cast<const void*>(&ns::sample_kernel<ns::BF16>)
+                                             : reinterpret_cast<const void*>(&ns::sample_kernel<ns::F32>);
+  e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, lds);
+  if (e != hipSuccess) return fail(NS_ERR_HIP, std::string("hipFuncSetAttribute: ") + hipGetErrorString(e));
   if (a->dtype == NS_DTYPE_BF16) hipLaunchKernelGGL((ns::sample_kernel<ns::BF16>), grid, block, lds, stream, p);
   else hipLaunchKernelGGL((ns::sample_kernel<ns::F32>), grid, block, lds, stream, p);
   e = hipGetLastError();
