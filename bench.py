@@ -74,7 +74,7 @@ def build_sets(w, dev, n_sets):
     return sets
 
 
-def make_args(L, st):
+def make_args(L, st, ws):
     import torch
 
     logits = st["logits"]
@@ -98,6 +98,8 @@ def make_args(L, st):
     a.out_ids = st["out"].data_ptr()
     a.out_probs = 0
     a.out_info = 0
+    a.workspace = ws.data_ptr()
+    a.workspace_bytes = ws.numel()
     return a
 
 
@@ -134,6 +136,9 @@ def main(argv=None):
     ap.add_argument("--warmup", type=int, default=40)
     ap.add_argument("--cpu-rows", type=int, default=256, help="rows in the CPU-baseline sample (0 = skip)")
     ap.add_argument("--cpu-reps", type=int, default=3)
+    ap.add_argument("--copy-mb", type=int, default=0,
+                    help="after the timed loop, run 4 plain device copies of this many MiB (a known-size "
+                         "reference for HBM byte counters under rocprofv3 --pmc)")
     args = ap.parse_args(argv)
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: the sampler's rows are independent and this build runs on a single "
@@ -153,7 +158,8 @@ def main(argv=None):
 
     w = W.make_workload(WORKLOAD_CFG)
     sets = build_sets(w, dev, ROTATE)
-    cargs = [make_args(L, st) for st in sets]
+    ws = L.workspace_for(dev, w.batch, w.vocab, L.NS_DTYPE_BF16 if w.bf16_bits is not None else L.NS_DTYPE_F32)
+    cargs = [make_args(L, st, ws) for st in sets]
     stream = torch.cuda.current_stream(dev)
     sh = ctypes.c_void_p(int(stream.cuda_stream))
     bytes_per_call = W.algorithmic_bytes(w)
@@ -196,6 +202,15 @@ def main(argv=None):
         ids = sampler.sample(sets[0]["logits"], params, hist_lists, uniforms=sets[0]["u"])
     ids.tolist()
     wrap_ms = (time.perf_counter() - t1) / nwrap * 1e3
+
+    if args.copy_mb > 0:
+        n = args.copy_mb * (1 << 20) // 4
+        src = torch.ones(n, dtype=torch.float32, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(4):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
 
     cpu = cpu_baseline(w, args.cpu_rows, args.cpu_reps) if args.cpu_rows > 0 else None
     line = {

@@ -26,7 +26,7 @@
 extern "C" {
 #endif
 
-#define NS_ABI_VERSION 1
+#define NS_ABI_VERSION 3
 
 #define NS_OK 0
 #define NS_ERR_INVALID 1   /* bad argument (message says which) */
@@ -36,16 +36,21 @@ extern "C" {
 #define NS_DTYPE_F32 0
 #define NS_DTYPE_BF16 1
 
+#define NS_MODE_AUTO 0        /* per-row once the batch fills the GPU, else segmented (needs a workspace) */
+#define NS_MODE_SEGMENTED 1   /* greedy and small-k rows split over several workgroups (needs a workspace) */
+#define NS_MODE_PER_ROW 2     /* one workgroup per row for every row */
+
 #define NS_MAX_VOCAB 262144     /* vocab limit (LDS presence bitmap of vocab/8 bytes) */
 #define NS_MAX_HISTORY 8192     /* per-row history limit (the reference's max_model_len, config.py:52) */
 #define NS_INFO_WORDS 8         /* int32 words per row in out_info */
 
 /* Per-row diagnostics written to out_info[row * NS_INFO_WORDS + w]:
- *   w=0 path (1 greedy, 2 uniform/NaN guard, 3 top-k set, 4 generic set, 5 large draw, 9 error)
+ *   w=0 path (1 greedy, 2 uniform/NaN guard, 3 top-k set, 4 generic set, 5 large draw,
+ *       6 segmented top-k, 9 error)
  *   w=1 tokens kept after top-k and top-p
  *   w=2 float32 bits of the top-k threshold in scaled logits (-inf when top-k is off)
  *   w=3 tokens kept after top-k
- *   w=4 top-k candidates examined in LDS (-1 when not applicable)
+ *   w=4 top-k candidates examined (-1 when not applicable)
  *   w=5 flags: 1 history id out of range (ignored), 2 history too long, 4 sample row out of range,
  *       8 candidate overflow (generic path taken), 16 histogram refinement limit reached,
  *       32 inverse-CDF locate fell back to the last kept token
@@ -75,15 +80,27 @@ typedef struct ns_sample_args {
   float*         out_probs;     /* [B, vocab] final probabilities (sampler.py:76-80), or NULL; greedy rows
                                    are not written.  Debug/parity output, not part of the timed path. */
   int32_t*       out_info;      /* [B, NS_INFO_WORDS] per-row diagnostics, or NULL */
+  void*          workspace;     /* device scratch of ns_sample_workspace_bytes() bytes, 256-byte aligned,
+                                   zero-filled before its first use (the library leaves its counters at
+                                   zero after every call); one workspace per stream.  NULL: every row
+                                   takes the one-workgroup-per-row kernel. */
+  uint64_t       workspace_bytes;
+  int32_t        mode;          /* NS_MODE_*: which kernels resolve which rows (results are identical) */
 } ns_sample_args;
 
 /* Version of this ABI (NS_ABI_VERSION). */
 int ns_abi_version(void);
 
 /* Sample one token per row: the whole of sampler.py:28-89 (repetition penalty, temperature,
- * top-k, top-p, softmax with the NaN guard, greedy argmax, inverse-CDF draw) in one launch.
+ * top-k, top-p, softmax with the NaN guard, greedy argmax, inverse-CDF draw).  One
+ * workgroup per row (greedy and 1 <= top_k <= 64 rows that fit in registers stream in one
+ * pass), optionally preceded by a segmented kernel for greedy and small-k rows of small
+ * batches (see NS_MODE_*); every launch is enqueued on `stream`.
  * Replaces Sampler.sample (nanoserve/scheduler/sampler.py:21-89). */
 int ns_sample(const ns_sample_args* args, hipStream_t stream);
+
+/* Workspace bytes ns_sample needs for n_sample rows of this vocab and logits dtype. */
+int ns_sample_workspace_bytes(int32_t n_sample, int64_t vocab, int32_t dtype, uint64_t* bytes);
 
 /* LDS bytes one workgroup of ns_sample needs for this vocab and history bound. */
 int ns_sample_lds_bytes(int64_t vocab, int32_t max_hist, int32_t* lds_bytes);

@@ -18,10 +18,13 @@ NS_DTYPE_BF16 = 1
 NS_MAX_VOCAB = 262144
 NS_MAX_HISTORY = 8192
 NS_INFO_WORDS = 8
-ABI_VERSION = 1
+NS_MODE_AUTO = 0
+NS_MODE_SEGMENTED = 1
+NS_MODE_PER_ROW = 2
+ABI_VERSION = 3
 
 # exported symbols, as declared in include/ns_sampling.h
-EXPORTS = ("ns_abi_version", "ns_sample", "ns_sample_lds_bytes", "ns_last_error")
+EXPORTS = ("ns_abi_version", "ns_sample", "ns_sample_lds_bytes", "ns_sample_workspace_bytes", "ns_last_error")
 
 
 class NsSampleArgs(ctypes.Structure):
@@ -46,6 +49,9 @@ class NsSampleArgs(ctypes.Structure):
         ("out_ids", ctypes.c_void_p),
         ("out_probs", ctypes.c_void_p),
         ("out_info", ctypes.c_void_p),
+        ("workspace", ctypes.c_void_p),
+        ("workspace_bytes", ctypes.c_uint64),
+        ("mode", ctypes.c_int32),
     ]
 
 
@@ -71,6 +77,9 @@ def load(path: str = LIB_PATH) -> ctypes.CDLL:
     lib.ns_sample.argtypes = [ctypes.POINTER(NsSampleArgs), ctypes.c_void_p]
     lib.ns_sample_lds_bytes.restype = ctypes.c_int
     lib.ns_sample_lds_bytes.argtypes = [ctypes.c_int64, ctypes.c_int32, ctypes.POINTER(ctypes.c_int32)]
+    lib.ns_sample_workspace_bytes.restype = ctypes.c_int
+    lib.ns_sample_workspace_bytes.argtypes = [ctypes.c_int32, ctypes.c_int64, ctypes.c_int32,
+                                              ctypes.POINTER(ctypes.c_uint64)]
     lib.ns_last_error.restype = ctypes.c_char_p
     lib.ns_last_error.argtypes = []
     v = lib.ns_abi_version()
@@ -95,19 +104,47 @@ def lds_bytes(vocab: int, max_hist: int) -> int:
     return int(out.value)
 
 
+def workspace_bytes(n_sample: int, vocab: int, dtype: int) -> int:
+    out = ctypes.c_uint64(0)
+    check(load().ns_sample_workspace_bytes(int(n_sample), int(vocab), int(dtype), ctypes.byref(out)))
+    return int(out.value)
+
+
+_WS = {}
+
+
+def workspace_for(device, n_sample: int, vocab: int, dtype: int):
+    """A cached zero-filled workspace tensor on ``device`` large enough for this call.
+
+    One workspace per device, used on the current stream; it is regrown (and
+    zero-filled again) when a call needs more.
+    """
+    import torch
+
+    need = workspace_bytes(n_sample, vocab, dtype)
+    key = str(device)
+    ws = _WS.get(key)
+    if ws is None or ws.numel() < need:
+        ws = torch.zeros(max(need, 1 << 20), dtype=torch.uint8, device=device)
+        _WS[key] = ws
+    return ws
+
+
 def _ptr(t) -> int:
     return 0 if t is None else int(t.data_ptr())
 
 
 def sample_raw(logits, temperature, top_k, top_p, rep_penalty, uniforms, out_ids, *, sample_idx=None,
                hist_offsets=None, hist_ids=None, max_hist: int = 0, out_probs=None, out_info=None,
-               stream=None) -> None:
+               stream=None, workspace="auto", mode: int = NS_MODE_AUTO) -> None:
     """Launch ``ns_sample`` on device tensors (no copies, no synchronisation).
 
     logits: (N, V) float32 or bfloat16 CUDA tensor with unit stride in the last dim.
     temperature/top_p/rep_penalty/uniforms: (B,) float32; top_k: (B,) int32;
     sample_idx: (B,) int64 or None; hist_offsets: (B+1,) int32; hist_ids: int32;
     out_ids: (B,) int64; out_probs: (B, V) float32 or None; out_info: (B, 8) int32 or None.
+    workspace: "auto" (a cached per-device workspace), a uint8 CUDA tensor, or None (every row
+    takes the one-workgroup-per-row kernel).
     """
     import torch
 
@@ -140,6 +177,12 @@ def sample_raw(logits, temperature, top_k, top_p, rep_penalty, uniforms, out_ids
     a.out_ids = _ptr(out_ids)
     a.out_probs = _ptr(out_probs)
     a.out_info = _ptr(out_info)
+    if isinstance(workspace, str) and workspace == "auto":
+        workspace = workspace_for(logits.device, B, a.vocab, dt)
+    if workspace is not None:
+        a.workspace = _ptr(workspace)
+        a.workspace_bytes = int(workspace.numel() * workspace.element_size())
+    a.mode = int(mode)
     if stream is None:
         stream = torch.cuda.current_stream(logits.device)
     check(lib.ns_sample(ctypes.byref(a), ctypes.c_void_p(int(stream.cuda_stream))))

@@ -180,6 +180,20 @@ __device__ __forceinline__ int block_excl_scan_int(int v, int* total, BlockScrat
   return off + inc - v;
 }
 
+// ------------------------------------------------------- buffer loads
+// Raw buffer loads through a resource descriptor: the base address lives in
+// scalar registers and one 32-bit offset register serves every load of a thread;
+// loads at or past `nbytes` return zeros (hardware range check).  Word 3 of the
+// descriptor is the gfx9-family value for untyped dword access.
+typedef unsigned int ns_v4u __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t nbytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)nbytes, 0x00020000);
+}
+__device__ __forceinline__ uint4 buf_load16(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+  const ns_v4u x = __builtin_amdgcn_raw_buffer_load_b128(r, (int)voff, (int)soff, 0);
+  return make_uint4(x.x, x.y, x.z, x.w);
+}
+
 // exp from the ROCm device library (ocml expf, faithfully rounded); not the
 // reduced-precision __expf.
 __device__ __forceinline__ float ns_expf(float x) { return expf(x); }

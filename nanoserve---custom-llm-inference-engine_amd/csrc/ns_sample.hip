@@ -9,6 +9,7 @@
 #include <string>
 
 #include "ns_sample_kernel.h"
+#include "ns_segment.h"
 #include "ns_sampling.h"
 
 namespace ns {
@@ -793,8 +794,21 @@ __device__ __attribute__((noinline)) void generic_path(const GCtx g) {
   }
 }
 
+}  // namespace ns
+
+#include "ns_rowfast.h"
+
+namespace ns {
+
+// Every row kind: P1 streaming with group maxima, the small-k LDS set path and the
+// histogram paths.  Called for rows the streaming path does not take.
+// The kernel's argument block, read in place: passing the struct by value to a
+// non-inlined function would copy it to scratch memory.
+typedef const KParams* KArgs;
+
 template <typename T>
-__global__ __launch_bounds__(NT) void sample_kernel(const KParams P) {
+__device__ __attribute__((noinline)) void row_general(KArgs PA) {
+  const KParams P = *PA;
   extern __shared__ __align__(16) unsigned char smem[];
   Misc* misc = reinterpret_cast<Misc*>(smem);
   uint32_t* bm = reinterpret_cast<uint32_t*>(smem + P.off_bm);
@@ -846,6 +860,7 @@ __global__ __launch_bounds__(NT) void sample_kernel(const KParams P) {
   const bool topk_on = k > 0 && (int64_t)k < V;                          // sampler.py:55
   const bool topp_on = topp < 1.0f;                                      // sampler.py:63
   const float p32 = topp;
+
 
   // ---- phase 0: history ids (all threads), then the row loads, zero LDS state
   int32_t hid[HPT];
@@ -1063,6 +1078,39 @@ __global__ __launch_bounds__(NT) void sample_kernel(const KParams P) {
                       V, nch, nrows_j, row, U, k, flags, pen, tdiv, rdiv, p32, Mx, My, u, pen_on, topk_on, topp_on});
 }
 
+template <typename T>
+__global__ __launch_bounds__(NT) void sample_kernel(const KParams P) {
+  const int row = blockIdx.x;
+  // rows the segment kernel resolved carry status 0; every other row carries 1
+  if (P.status != nullptr && P.status[row] == 0) return;
+  if (P.fast) {
+    // greedy and small-k rows that fit in registers: one streaming pass
+    const float temp = P.temperature[row];
+    const int32_t k = P.top_k[row];
+    if (seg_row(temp, k, P.vocab) && row_fits<T>(P.vocab)) {
+      const int64_t src = P.sample_idx ? P.sample_idx[row] : (int64_t)row;
+      int32_t h0 = 0, h1 = 0;
+      if (P.hist_off != nullptr) { h0 = P.hist_off[row]; h1 = P.hist_off[row + 1]; }
+      if (src >= 0 && src < P.n_rows_total && h0 >= 0 && h1 >= h0 && h1 - h0 <= MAX_HIST && h1 - h0 <= P.xcap - 8) {
+        extern __shared__ __align__(16) unsigned char smem[];
+        Misc* misc = reinterpret_cast<Misc*>(smem);
+        uint32_t* bm = reinterpret_cast<uint32_t*>(smem + P.off_bm);
+        float* xl_val = reinterpret_cast<float*>(smem + P.off_xl);
+        int32_t* xl_id = reinterpret_cast<int32_t*>(smem + P.off_xl + 4u * (uint32_t)P.xcap);
+        uint64_t* cand = reinterpret_cast<uint64_t*>(smem + P.off_cand);
+        float u = P.uniforms[row];
+        u = (u >= 0.0f) ? (u < 1.0f ? u : 0x1.fffffep-1f) : 0.0f;
+        const int st = row_fast<T>(RowArgs{P.logits, P.row_stride, P.vocab, P.hist_ids, P.out_ids, P.out_probs,
+                                           P.out_info},
+                                   row, src, temp, k, P.top_p[row], P.penalty[row], u, h0, h1 - h0, 0, misc, bm,
+                                   xl_id, xl_val, cand);
+        if (st == 0) return;
+      }
+    }
+  }
+  row_general<T>((KArgs)__builtin_amdgcn_kernarg_segment_ptr());
+}
+
 }  // namespace ns
 
 // =====================================================================================
@@ -1073,6 +1121,26 @@ thread_local std::string g_err;
 int fail(int code, const std::string& msg) {
   g_err = msg;
   return code;
+}
+
+// Segment geometry: elements per segment and segments per row.
+int64_t seg_elems(int32_t dtype) { return (int64_t)ns::SEG_CH * (dtype == NS_DTYPE_BF16 ? 8 : 4); }
+int64_t seg_count(int64_t vocab, int32_t dtype) { return (vocab + seg_elems(dtype) - 1) / seg_elems(dtype); }
+int64_t align256(int64_t x) { return (x + 255) / 256 * 256; }
+
+struct WsLayout {
+  int64_t counters, status, stats, cand, total;
+};
+WsLayout ws_layout(int32_t n_sample, int64_t vocab, int32_t dtype) {
+  const int64_t rows = ((int64_t)n_sample + 7) / 8 * 8;
+  const int64_t S = seg_count(vocab, dtype);
+  WsLayout L;
+  L.counters = 0;
+  L.status = align256(rows * 4);
+  L.stats = L.status + align256(rows * 4);
+  L.cand = L.stats + align256(rows * S * (int64_t)sizeof(ns::SegStat));
+  L.total = L.cand + align256(rows * S * ns::SEG_CAP * 8);
+  return L;
 }
 }  // namespace
 
@@ -1098,6 +1166,15 @@ int ns_sample_lds_bytes(int64_t vocab, int32_t max_hist, int32_t* lds_bytes) {
   return NS_OK;
 }
 
+int ns_sample_workspace_bytes(int32_t n_sample, int64_t vocab, int32_t dtype, uint64_t* bytes) {
+  if (bytes == nullptr) return fail(NS_ERR_INVALID, "bytes is NULL");
+  if (n_sample < 0) return fail(NS_ERR_INVALID, "n_sample < 0");
+  if (vocab <= 0 || vocab > NS_MAX_VOCAB) return fail(NS_ERR_INVALID, "vocab out of range");
+  if (dtype != NS_DTYPE_F32 && dtype != NS_DTYPE_BF16) return fail(NS_ERR_INVALID, "dtype must be f32 or bf16");
+  *bytes = (uint64_t)ws_layout(n_sample, vocab, dtype).total;
+  return NS_OK;
+}
+
 int ns_sample(const ns_sample_args* a, hipStream_t stream) {
   if (a == nullptr) return fail(NS_ERR_INVALID, "args is NULL");
   if (a->n_sample < 0) return fail(NS_ERR_INVALID, "n_sample < 0");
@@ -1118,6 +1195,13 @@ int ns_sample(const ns_sample_args* a, hipStream_t stream) {
   const int esz = a->dtype == NS_DTYPE_F32 ? 4 : 2;
   if (((uintptr_t)a->logits % 16) != 0 || ((a->row_stride * esz) % 16) != 0)
     return fail(NS_ERR_ALIGN, "logits rows must start on 16-byte boundaries (base and row stride)");
+  const WsLayout L = ws_layout(a->n_sample, a->vocab, a->dtype);
+  if (a->workspace != nullptr) {
+    if (a->workspace_bytes < (uint64_t)L.total)
+      return fail(NS_ERR_INVALID, "workspace of " + std::to_string(a->workspace_bytes) + " bytes, " +
+                                      std::to_string(L.total) + " needed (ns_sample_workspace_bytes)");
+    if (((uintptr_t)a->workspace % 256) != 0) return fail(NS_ERR_ALIGN, "workspace must be 256-byte aligned");
+  }
 
   int32_t lds = 0;
   int rc = ns_sample_lds_bytes(a->vocab, a->hist_offsets ? a->max_hist : 0, &lds);
@@ -1164,6 +1248,60 @@ int ns_sample(const ns_sample_args* a, hipStream_t stream) {
     return fail(NS_ERR_INVALID, "LDS requirement " + std::to_string(lds) + " exceeds device limit " +
                                     std::to_string(max_lds));
 
+  // Path choice.  Per-row mode: one workgroup per row for every row (greedy and small-k
+  // rows that fit in registers stream in one pass); a single launch, best once the batch
+  // fills the GPU.  Segmented mode: greedy and small-k rows split over 16-byte-chunk
+  // segments (a few workgroups per row), the per-row kernel after it for the rest.
+  if (a->mode < NS_MODE_AUTO || a->mode > NS_MODE_PER_ROW) return fail(NS_ERR_INVALID, "unknown mode");
+  if (a->mode == NS_MODE_SEGMENTED && a->workspace == nullptr)
+    return fail(NS_ERR_INVALID, "segmented mode needs a workspace");
+  int n_cu = 0;
+  e = hipDeviceGetAttribute(&n_cu, hipDeviceAttributeMultiprocessorCount, dev);
+  if (e != hipSuccess) return fail(NS_ERR_HIP, std::string("hipDeviceGetAttribute: ") + hipGetErrorString(e));
+  bool segmented = a->workspace != nullptr && a->mode != NS_MODE_PER_ROW;
+  if (a->mode == NS_MODE_AUTO && (int64_t)a->n_sample * 8 >= (int64_t)n_cu * 7) segmented = false;
+  p.fast = 1;
+  p.status = nullptr;
+
+  // 1) segment kernel: greedy and small-k rows
+  if (segmented) {
+    const int64_t S = seg_count(a->vocab, a->dtype);
+    if (S > ns::MAX_SEGS) return fail(NS_ERR_INVALID, "vocab too large for the segment kernel");
+    const int64_t groups = ((int64_t)a->n_sample + 7) / 8;
+    const int64_t nblk = groups * 8 * S;
+    if (nblk > 0x7fffffffLL) return fail(NS_ERR_INVALID, "too many rows for one launch");
+    unsigned char* ws = static_cast<unsigned char*>(a->workspace);
+    ns::SegParams s{};
+    s.logits = a->logits;
+    s.row_stride = a->row_stride;
+    s.vocab = a->vocab;
+    s.n_rows_total = a->n_rows_total;
+    s.sample_idx = a->sample_idx;
+    s.temperature = a->temperature;
+    s.top_k = a->top_k;
+    s.top_p = a->top_p;
+    s.penalty = a->rep_penalty;
+    s.hist_off = a->hist_offsets;
+    s.hist_ids = a->hist_ids;
+    s.uniforms = a->uniforms;
+    s.out_ids = a->out_ids;
+    s.out_probs = a->out_probs;
+    s.out_info = a->out_info;
+    s.n_sample = a->n_sample;
+    s.S = (int32_t)S;
+    s.counters = reinterpret_cast<int32_t*>(ws + L.counters);
+    s.status = reinterpret_cast<int32_t*>(ws + L.status);
+    s.stats = reinterpret_cast<ns::SegStat*>(ws + L.stats);
+    s.cand = reinterpret_cast<uint64_t*>(ws + L.cand);
+    p.status = s.status;
+    const dim3 g((unsigned)nblk), bs(ns::SNT);
+    if (a->dtype == NS_DTYPE_BF16) hipLaunchKernelGGL((ns::segment_kernel<ns::BF16>), g, bs, 0, stream, s);
+    else hipLaunchKernelGGL((ns::segment_kernel<ns::F32>), g, bs, 0, stream, s);
+    e = hipGetLastError();
+    if (e != hipSuccess) return fail(NS_ERR_HIP, std::string("segment kernel launch: ") + hipGetErrorString(e));
+  }
+
+  // 2) one workgroup per row: every other row, and rows the segment kernel deferred
   const dim3 grid((unsigned)a->n_sample), block(ns::NT);
   const void* fn = a->dtype == NS_DTYPE_BF16 ? reinterpret_cast<const void*>(&ns::sample_kernel<ns::BF16>)
                                              : reinterpret_cast<const void*>(&ns::sample_kernel<ns::F32>);

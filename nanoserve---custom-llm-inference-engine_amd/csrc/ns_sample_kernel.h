@@ -68,7 +68,9 @@ struct KParams {
   int64_t* out_ids;
   float* out_probs;
   int32_t* out_info;
+  const int32_t* status;   // [n_sample] from the segment kernel (0 = resolved there), or NULL: every row
   int32_t n_sample;
+  int32_t fast;            // 1: greedy and small-k rows that fit in registers take the streaming path
   int32_t xcap;            // extras capacity (unique history + tail)
   uint32_t off_bm, off_xl, off_cand, off_hist;   // LDS byte offsets
 };

@@ -1,0 +1,935 @@
+// gfx950 segment kernel: the sampler's fast path for greedy rows and top-k rows
+// with k <= KFAST (sampler.py:31-89 for those rows).
+//
+// Each sampled row is cut into S segments of SEG_CH 16-byte chunks; one
+// 256-thread workgroup per (row, segment), SCPT chunks per thread, all loads of
+// a thread issued together (one HBM round trip per workgroup; at the decode
+// batch every workgroup is resident at once).  Workgroups of one row are mapped
+// to the same XCD (the dispatcher deals workgroup ids to the 8 XCDs
+// round-robin), so a row's history ids and candidates stay in one L2.
+//
+// Per segment, per element only a NaN-propagating chunk maximum is computed:
+//   * repetition penalty (sampler.py:34-38): the row's history ids falling in
+//     the segment set bits of an LDS bitmap; each id that sets its bit first
+//     (set semantics) is gathered, penalized and kept as an "extra" element.
+//     History positions are skipped in the chunk data wherever exact values
+//     matter (candidates, greedy), and chunks holding one are not used as
+//     threshold sources.
+//   * greedy rows: masked segment max and first index of the max (sampler.py:82-83).
+//   * top-k rows: a lower bound tau of the row's k-th largest scaled logit from
+//     the thread maxima (the ceil(k/4)-th largest of each wave's 64 thread
+//     maxima, minimum over the 4 waves: at least k distinct elements reach it);
+//     chunks whose maximum reaches tau are re-read (L2) and their elements >= tau
+//     written as candidates (scaled value, token id).
+// The last workgroup of a row to finish (atomic arrival counter) finalises the
+// row: NaN/inf guard, the candidates above the largest segment bound, a
+// histogram refinement, then exact top-k (ties kept), top-p, softmax and the
+// inverse-CDF draw inside one wave over at most 256 survivors.  Rows it cannot
+// resolve there (candidate overflow, huge tie groups) are flagged in `status`
+// and resolved by the one-workgroup-per-row kernel launched after this one.
+#pragma once
+
+#include "ns_sample_kernel.h"
+
+namespace ns {
+
+constexpr int SNT = 256;               // threads per segment workgroup
+constexpr int SNW = SNT / 64;          // waves per segment workgroup
+constexpr int SCPT = 16;               // 16-byte chunks per thread
+constexpr int SEG_CH = SNT * SCPT;     // chunks per segment
+constexpr int SEG_CAP = 1024;          // candidate slots per segment (workspace)
+constexpr int KFAST = 64;              // largest top_k resolved by the segment path
+constexpr int XCAP = 2048;             // unique history ids per segment kept as extras
+constexpr int FIN_SLOTS = 8;           // candidates per finaliser thread (FIN_SLOTS * SNT gathered)
+constexpr int WAVE_CAP = 256;          // survivors finalised inside one wave
+constexpr int SHIST = 256;             // refinement histogram bins
+constexpr int HBATCH = 8;              // history ids per thread per batch
+constexpr int MAX_SEGS = 16;           // segments per row (vocab <= 262144 at 16384 fp32 per segment)
+
+constexpr int PATH_WAVE_SET = 6;       // out_info path code: top-k set finalised inside one wave
+constexpr int SFLAG_NAN = 1 << 16;     // segment statistics: a NaN among the penalized values
+constexpr int SFLAG_PINF = 1 << 17;    // segment statistics: a +inf among the penalized values
+constexpr int SFLAG_XOVER = 1 << 18;   // segment statistics: more than XCAP unique history ids
+
+struct SegStat {
+  float ymax;       // segment max of the scaled logits (NaN-propagating)
+  int32_t amax;     // greedy rows: first token id of the max
+  float tau;        // top-k rows: lower bound of the row's k-th largest scaled logit
+  int32_t ncand;    // candidates >= tau found (may exceed SEG_CAP: overflow)
+  int32_t flags;    // FLAG_* row flags | SFLAG_* segment flags
+  int32_t pad[3];
+};
+
+struct SegParams {
+  const void* logits;
+  int64_t row_stride;
+  int64_t vocab;
+  int64_t n_rows_total;
+  const int64_t* sample_idx;
+  const float* temperature;
+  const int32_t* top_k;
+  const float* top_p;
+  const float* penalty;
+  const int32_t* hist_off;
+  const int32_t* hist_ids;
+  const float* uniforms;
+  int64_t* out_ids;
+  float* out_probs;
+  int32_t* out_info;
+  int32_t n_sample;
+  int32_t S;             // segments per row
+  int32_t* counters;     // [rows] arrival counters, zero between calls
+  int32_t* status;       // [rows] written for every row: 1 = resolve in the per-row kernel
+  SegStat* stats;        // [rows * S]
+  uint64_t* cand;        // [rows * S * SEG_CAP]  (float bits << 32) | token id
+};
+
+// Rows this path resolves: greedy, or top-k with 1 <= k <= KFAST (and k < V, sampler.py:55).
+__host__ __device__ __forceinline__ bool seg_row(float t, int32_t k, int64_t V) {
+  return t == 0.0f || (k >= 1 && k <= KFAST && (int64_t)k < V);
+}
+
+// ------------------------------------------------------------ register access
+// Raw float of element j (0 <= j < SCPT * EPC) of the thread's chunks, by selects
+// (no dynamically indexed register arrays).
+template <typename T>
+__device__ __forceinline__ float elem_dyn(const uint4 (&v)[SCPT], int j) {
+  const int dw = (j * T::SZ) >> 2;   // dword 0 .. 4*SCPT-1
+  const int q = dw >> 2, c = dw & 3;
+  uint32_t x = v[0].x, y = v[0].y, z = v[0].z, w = v[0].w;
+#pragma unroll
+  for (int i = 1; i < SCPT; ++i) {
+    const bool s = q == i;
+    x = s ? v[i].x : x;
+    y = s ? v[i].y : y;
+    z = s ? v[i].z : z;
+    w = s ? v[i].w : w;
+  }
+  uint32_t d = x;
+  d = c == 1 ? y : d;
+  d = c == 2 ? z : d;
+  d = c == 3 ? w : d;
+  if (T::EPC == 8) return __uint_as_float((j & 1) ? (d & 0xffff0000u) : (d << 16));
+  return __uint_as_float(d);
+}
+
+template <typename T>
+__device__ __forceinline__ uint4 seg_ninf() {
+  const uint32_t w = T::EPC == 8 ? 0xff80ff80u : 0xff800000u;
+  return make_uint4(w, w, w, w);
+}
+
+// Chunk c of a row that ends past V: elements at or beyond V read as -inf
+// (never loaded); the others are loaded one by one.
+template <typename T>
+__device__ __forceinline__ uint4 load_tail_chunk(const unsigned char* rowp, int64_t c, int64_t V) {
+  const int64_t e0 = c * T::EPC;
+  uint4 r = seg_ninf<T>();
+  if (e0 < V) {
+    uint32_t d[4] = {r.x, r.y, r.z, r.w};
+#pragma unroll
+    for (int e = 0; e < T::EPC; ++e) {
+      if (e0 + e < V) {
+        const uint32_t bits = __float_as_uint(T::load1(rowp, e0 + e));
+        if (T::EPC == 8) {
+          const int di = e >> 1;
+          d[di] = (e & 1) ? ((d[di] & 0x0000ffffu) | (bits & 0xffff0000u)) : ((d[di] & 0xffff0000u) | (bits >> 16));
+        } else {
+          d[e] = bits;
+        }
+      }
+    }
+    r = make_uint4(d[0], d[1], d[2], d[3]);
+  }
+  return r;
+}
+
+// ------------------------------------------------- cross-workgroup exchange
+// Candidates and segment statistics pass between workgroups of one launch
+// through device-coherent accesses (relaxed agent-scope atomic loads/stores:
+// they bypass the per-XCD L2's non-coherent state), so the arrival protocol
+// needs no cache-wide write-back or invalidation.
+__device__ __forceinline__ void dc_store(uint64_t* p, uint64_t v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint64_t dc_load(const uint64_t* p) {
+  return __hip_atomic_load(const_cast<uint64_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void dc_store_stat(SegStat* p, const SegStat& s) {
+  const uint64_t* w = reinterpret_cast<const uint64_t*>(&s);
+  uint64_t* d = reinterpret_cast<uint64_t*>(p);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) dc_store(d + i, w[i]);
+}
+__device__ __forceinline__ SegStat dc_load_stat(const SegStat* p) {
+  SegStat s;
+  uint64_t* w = reinterpret_cast<uint64_t*>(&s);
+  const uint64_t* d = reinterpret_cast<const uint64_t*>(p);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) w[i] = dc_load(d + i);
+  return s;
+}
+
+// ------------------------------------------------------------ wave sorting
+__device__ __forceinline__ uint64_t shfl_xor_u64(uint64_t v, int m) {
+  const uint32_t lo = __shfl_xor((uint32_t)v, m);
+  const uint32_t hi = __shfl_xor((uint32_t)(v >> 32), m);
+  return ((uint64_t)hi << 32) | lo;
+}
+__device__ __forceinline__ uint64_t shfl_u64(uint64_t v, int src) {
+  const uint32_t lo = __shfl((uint32_t)v, src);
+  const uint32_t hi = __shfl((uint32_t)(v >> 32), src);
+  return ((uint64_t)hi << 32) | lo;
+}
+
+// Ascending bitonic sort of 64*R keys held by one wave: element i = r*64 + lane.
+template <int R>
+__device__ __forceinline__ void wave_sort_u64(uint64_t (&a)[R]) {
+  const int lane = lane_id();
+#pragma unroll
+  for (int size = 2; size <= 64 * R; size <<= 1) {
+#pragma unroll
+    for (int stride = size >> 1; stride > 0; stride >>= 1) {
+      if (stride >= 64) {
+        const int rs = stride >> 6;
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+          if ((r & rs) == 0) {
+            const int i = r * 64 + lane;
+            const bool up = (i & size) == 0;
+            const uint64_t x = a[r], y = a[r | rs];
+            const uint64_t mn = x < y ? x : y, mx = x < y ? y : x;
+            a[r] = up ? mn : mx;
+            a[r | rs] = up ? mx : mn;
+          }
+        }
+      } else {
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+          const uint64_t p = shfl_xor_u64(a[r], stride);
+          const int i = r * 64 + lane;
+          const bool up = (i & size) == 0;
+          const bool lower = (lane & stride) == 0;
+          const bool keep_min = lower == up;
+          const uint64_t mn = a[r] < p ? a[r] : p, mx = a[r] < p ? p : a[r];
+          a[r] = keep_min ? mn : mx;
+        }
+      }
+    }
+  }
+}
+
+// Ascending bitonic sort of 64 u32 keys (one per lane).
+__device__ __forceinline__ uint32_t wave_sort_u32(uint32_t a) {
+  const int lane = lane_id();
+#pragma unroll
+  for (int size = 2; size <= 64; size <<= 1) {
+#pragma unroll
+    for (int stride = size >> 1; stride > 0; stride >>= 1) {
+      const uint32_t p = __shfl_xor(a, stride);
+      const bool up = (lane & size) == 0;
+      const bool lower = (lane & stride) == 0;
+      a = (lower == up) ? (a < p ? a : p) : (a < p ? p : a);
+    }
+  }
+  return a;
+}
+
+// Inclusive prefix sums of 64*R doubles in element order i = r*64 + lane.
+template <int R>
+__device__ __forceinline__ void wave_scan_rows(const double (&v)[R], double (&out)[R]) {
+  double carry = 0.0;
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const double s = wave_incl_scan(v[r]);
+    out[r] = carry + s;
+    carry += __shfl(s, 63);
+  }
+}
+
+// Shared memory of the segment workgroup.
+struct SegSmem {
+  uint32_t bm[SEG_CH * 8 / 32];     // history bitmap of the segment (8 elements per chunk max)
+  int32_t xl_id[XCAP];              // unique history ids of the segment
+  float xl_val[XCAP];               // their penalized values
+  uint64_t list[WAVE_CAP];          // finaliser survivors
+  uint32_t hist[SHIST];             // finaliser refinement histogram
+  int32_t off[MAX_SEGS + 1];        // finaliser candidate offsets per segment
+  float fred[SNW];
+  int32_t ired[SNW];
+  int32_t wbase[SNW];
+  int32_t xl_n;
+  int32_t cnt;
+  int32_t last;
+  int32_t flags;
+  float fb[4];
+  int32_t ib[8];
+};
+
+// Block reductions over the 4 waves (two barriers each).
+__device__ __forceinline__ float seg_max_nan(float v, SegSmem* sm) {
+  v = wave_max_nan(v);
+  if (lane_id() == 0) sm->fred[wave_id()] = v;
+  __syncthreads();
+  float r = sm->fred[0];
+#pragma unroll
+  for (int w = 1; w < SNW; ++w) r = fmax_nan(r, sm->fred[w]);
+  __syncthreads();
+  return r;
+}
+__device__ __forceinline__ float seg_min_f(float v, SegSmem* sm) {
+  v = wave_min(v);
+  if (lane_id() == 0) sm->fred[wave_id()] = v;
+  __syncthreads();
+  float r = sm->fred[0];
+#pragma unroll
+  for (int w = 1; w < SNW; ++w) r = sm->fred[w] < r ? sm->fred[w] : r;
+  __syncthreads();
+  return r;
+}
+__device__ __forceinline__ int32_t seg_min_i(int32_t v, SegSmem* sm) {
+  v = wave_min(v);
+  if (lane_id() == 0) sm->ired[wave_id()] = v;
+  __syncthreads();
+  int32_t r = sm->ired[0];
+#pragma unroll
+  for (int w = 1; w < SNW; ++w) r = sm->ired[w] < r ? sm->ired[w] : r;
+  __syncthreads();
+  return r;
+}
+__device__ __forceinline__ int32_t seg_sum_i(int32_t v, SegSmem* sm) {
+  v = wave_sum(v);
+  if (lane_id() == 0) sm->ired[wave_id()] = v;
+  __syncthreads();
+  int32_t r = 0;
+#pragma unroll
+  for (int w = 0; w < SNW; ++w) r += sm->ired[w];
+  __syncthreads();
+  return r;
+}
+
+__device__ __forceinline__ void seg_write_info(int32_t* out_info, int row, int32_t path, int32_t n_kept, float thr,
+                                               int32_t n_topk, int32_t n_cand, int32_t flags, float vstar,
+                                               int32_t istar) {
+  if (out_info == nullptr) return;
+  int32_t* w = out_info + (int64_t)row * INFO_WORDS;
+  w[0] = path; w[1] = n_kept; w[2] = (int32_t)__float_as_uint(thr); w[3] = n_topk;
+  w[4] = n_cand; w[5] = flags; w[6] = (int32_t)__float_as_uint(vstar); w[7] = istar;
+}
+
+// Exact top-k (ties kept), top-p, softmax and inverse-CDF draw over n <= 64*R
+// survivors, run by one wave.  list[i] = (float bits << 32) | token id where the
+// float is a logit after the penalty; it is scaled here by the row's temperature
+// (tdiv, rdiv = RN(1/tdiv)); pass tdiv = rdiv = 1 for values already scaled.
+// Every survivor is >= the row's k-th largest scaled value and the row maximum
+// is among them.
+template <int R>
+__device__ void wave_finalize(const uint64_t* list, int n, int k, bool topp_on, float p32, float tdiv, float rdiv,
+                              float u, int row, int64_t* out_ids, float* out_probs, int64_t V, int32_t* out_info,
+                              int32_t flags, int32_t n_cand, int32_t path) {
+  const int lane = lane_id();
+  uint64_t a[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const int i = r * 64 + lane;
+    a[r] = ~0ull;
+    if (i < n) {
+      const uint64_t e = list[i];
+      a[r] = desc_key(div_rn(__uint_as_float((uint32_t)(e >> 32)), tdiv, rdiv), (uint32_t)e);
+    }
+  }
+  wave_sort_u64<R>(a);   // value descending, token id ascending
+  const float M = desc_key_val(shfl_u64(a[0], 0));   // the row maximum
+
+  // top-k threshold: the k-th largest (sampler.py:56-58); every value >= it is kept
+  float thr = -__builtin_inff();
+  if (n >= k) {
+    const int rk = (k - 1) >> 6, lk = (k - 1) & 63;
+    uint64_t sel = a[0];
+#pragma unroll
+    for (int r = 1; r < R; ++r) sel = (r == rk) ? a[r] : sel;
+    thr = desc_key_val(shfl_u64(sel, lk));
+  }
+  float y[R];
+  int nk = 0;
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const int i = r * 64 + lane;
+    y[r] = i < n ? desc_key_val(a[r]) : -__builtin_inff();
+    nk += __popcll(ballot(i < n && y[r] >= thr));
+  }
+  // softmax numerators over the kept prefix (sampler.py:65 / :76)
+  float ev[R];
+  double es[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const int i = r * 64 + lane;
+    ev[r] = i < nk ? ns_expf(y[r] - M) : 0.0f;
+    es[r] = (double)ev[r];
+  }
+  int nf = nk;
+  float vstar = -__builtin_inff();
+  int32_t istar = -1;
+  if (topp_on) {
+    double z = 0.0;
+#pragma unroll
+    for (int r = 0; r < R; ++r) z += wave_sum(es[r]);
+    double qv[R], cs[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) qv[r] = (double)(float)(es[r] / z);
+    wave_scan_rows<R>(qv, cs);
+    // first sorted position whose float32 prefix exceeds top_p; it is kept (sampler.py:66-72)
+    int J = -1;
+#pragma unroll
+    for (int r = R - 1; r >= 0; --r) {
+      const int i = r * 64 + lane;
+      const uint64_t m = ballot(i < nk && (float)cs[r] > p32);
+      if (m != 0ull) J = r * 64 + __builtin_ctzll(m);
+    }
+    if (J >= 0) nf = J + 1;
+    const int rj = (nf - 1) >> 6, lj = (nf - 1) & 63;
+    uint64_t sel = a[0];
+#pragma unroll
+    for (int r = 1; r < R; ++r) sel = (r == rj) ? a[r] : sel;
+    const uint64_t kc = shfl_u64(sel, lj);
+    vstar = desc_key_val(kc);
+    istar = (int32_t)desc_key_id(kc);
+  }
+  // final probabilities over the nf kept tokens, then the draw in token-id order
+  double z2 = 0.0;
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const int i = r * 64 + lane;
+    z2 += wave_sum(i < nf ? es[r] : 0.0);
+  }
+  uint64_t b[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const int i = r * 64 + lane;
+    b[r] = ~0ull;
+    if (i < nf) {
+      const float pv = (float)(es[r] / z2);
+      b[r] = ((uint64_t)desc_key_id(a[r]) << 32) | __float_as_uint(pv);
+    }
+  }
+  wave_sort_u64<R>(b);
+  double pd[R], cd[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const int i = r * 64 + lane;
+    pd[r] = i < nf ? (double)__uint_as_float((uint32_t)b[r]) : 0.0;
+  }
+  wave_scan_rows<R>(pd, cd);
+  const double ud = (double)u;
+  int pick = -1, lastpos = -1;
+#pragma unroll
+  for (int r = R - 1; r >= 0; --r) {
+    const int i = r * 64 + lane;
+    const uint64_t m = ballot(i < nf && cd[r] > ud);
+    if (m != 0ull) pick = r * 64 + __builtin_ctzll(m);
+  }
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const int i = r * 64 + lane;
+    const uint64_t m = ballot(i < nf && pd[r] > 0.0);
+    if (m != 0ull) lastpos = r * 64 + 63 - __builtin_clzll(m);
+  }
+  int32_t fl = flags;
+  if (pick < 0) { pick = lastpos >= 0 ? lastpos : 0; fl |= FLAG_LOCATE_FALLBACK; }
+  {
+    const int rp = pick >> 6, lp = pick & 63;
+    uint64_t sel = b[0];
+#pragma unroll
+    for (int r = 1; r < R; ++r) sel = (r == rp) ? b[r] : sel;
+    const uint64_t kb = shfl_u64(sel, lp);
+    if (lane == 0) {
+      out_ids[row] = (int64_t)(kb >> 32);
+      seg_write_info(out_info, row, path, nf, thr, nk, n_cand, fl, vstar, istar);
+    }
+  }
+  if (out_probs != nullptr) {
+    float* pr = out_probs + (int64_t)row * V;
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const int i = r * 64 + lane;
+      if (i < nf) pr[b[r] >> 32] = __uint_as_float((uint32_t)b[r]);
+    }
+  }
+}
+
+// Wave-aggregated append of one candidate (scaled value y, token id) to the
+// segment's workspace slots; callable from divergent code (active lanes only).
+__device__ __forceinline__ void seg_append(float y, int64_t id, uint64_t* cbase, SegSmem* sm) {
+  const uint64_t m = ballot(true);
+  const int leader = __builtin_ctzll(m);
+  int base = 0;
+  if (lane_id() == leader) base = atomicAdd(&sm->cnt, __popcll(m));
+  base = __shfl(base, leader);
+  const int pos = base + lanes_below(m);
+  if (pos < SEG_CAP) dc_store(cbase + pos, ((uint64_t)__float_as_uint(y) << 32) | (uint32_t)id);
+}
+
+template <typename T>
+__global__ __launch_bounds__(SNT) __attribute__((amdgpu_waves_per_eu(4))) void segment_kernel(const SegParams P) {
+  __shared__ SegSmem sm;
+  constexpr int EPC = T::EPC;
+  constexpr int SEG_EL = SEG_CH * EPC;         // elements per segment
+  const int tid = threadIdx.x;
+  const int lane = lane_id();
+  const int wid = wave_id();
+  const int S = P.S;
+  // XCD-aware mapping: all segments of a row share blockIdx % 8
+  const int b = blockIdx.x;
+  const int xcd = b & 7;
+  const int i8 = b >> 3;
+  const int rg = i8 / S;
+  const int seg = i8 - rg * S;
+  const int row = rg * 8 + xcd;
+  if (row >= P.n_sample) return;
+  const int64_t V = P.vocab;
+  const float temp = P.temperature[row];
+  const int32_t k = P.top_k[row];
+  if (!seg_row(temp, k, V)) {                  // resolved by the per-row kernel
+    if (seg == 0 && tid == 0) P.status[row] = 1;
+    return;
+  }
+  const int64_t src = P.sample_idx ? P.sample_idx[row] : (int64_t)row;
+  int32_t h0 = 0, h1 = 0;
+  if (P.hist_off != nullptr) { h0 = P.hist_off[row]; h1 = P.hist_off[row + 1]; }
+  if (src < 0 || src >= P.n_rows_total || h0 < 0 || h1 < h0 || h1 - h0 > MAX_HIST) {
+    // invalid row: the per-row kernel reports it
+    if (seg == 0 && tid == 0) P.status[row] = 1;
+    return;
+  }
+  const unsigned char* rowp = (const unsigned char*)P.logits + src * P.row_stride * T::SZ;
+  const uint4* rowv = reinterpret_cast<const uint4*>(rowp);
+  const int64_t c0 = (int64_t)seg * SEG_CH;    // first chunk of the segment
+  const int64_t e0 = c0 * EPC;                 // first element
+
+  // ---- all row loads of this thread in flight at once
+  uint4 v[SCPT];
+  {
+    // buffer loads over the row's full chunks: chunks past them read zero and are
+    // replaced when first used
+    const __amdgpu_buffer_rsrc_t rs = make_rsrc(rowp, (uint32_t)((V / EPC) * 16));
+#pragma unroll
+    for (int q = 0; q < SCPT; ++q)
+      v[q] = buf_load16(rs, (uint32_t)tid * 16u, (uint32_t)((c0 + q * SNT) * 16));
+  }
+  // chunks past the row's full chunks: -inf, and the chunk holding the last tokens
+  // when V is not a multiple of EPC (its own register); replaced when first used
+  const int64_t nfull_r = V / EPC;
+  const bool has_tail = (nfull_r * EPC < V) && (nfull_r - c0) % SNT == tid && nfull_r >= c0 &&
+                        nfull_r < c0 + SEG_CH;
+  const uint4 vtail = has_tail ? load_tail_chunk<T>(rowp, nfull_r, V) : seg_ninf<T>();
+
+  const float pen = P.penalty[row];
+  const int32_t H = h1 - h0;
+  const bool pen_on = pen != 1.0f && H > 0;    // sampler.py:33
+  const bool greedy = temp == 0.0f;
+  const float tdiv = temp > 0.0f ? __builtin_fmaxf(temp, 1e-6f) : 1.0f;   // sampler.py:42
+  const float rdiv = 1.0f / tdiv;
+  const float rpen = 1.0f / pen;
+  auto pen_val = [&](float x) -> float {
+    // sampler.py:37: score * p if score < 0 else score / p (float32, correctly rounded)
+    return x < 0.0f ? x * pen : div_rn(x, pen, rpen);
+  };
+  int32_t flags = 0;
+
+  // ---- history: bitmap of the segment and the unique ids in it (set semantics)
+  int U = 0;
+  if (pen_on) {
+    for (int i = tid; i < SEG_EL / 32; i += SNT) sm.bm[i] = 0u;
+    if (tid == 0) { sm.flags = 0; sm.xl_n = 0; }
+    __syncthreads();
+    const int32_t* hp = P.hist_ids + h0;
+    bool bad = false;
+    for (int base = 0; base < H; base += SNT * HBATCH) {
+      int32_t hv[HBATCH];
+#pragma unroll
+      for (int s = 0; s < HBATCH; ++s) {
+        const int j = base + s * SNT + tid;
+        hv[s] = j < H ? hp[j] : 0;
+      }
+#pragma unroll
+      for (int s = 0; s < HBATCH; ++s) {
+        const int j = base + s * SNT + tid;
+        bool uniq = false;
+        if (j < H) {
+          const int32_t id = hv[s];
+          if (id < 0 || (int64_t)id >= V) {
+            bad = true;
+          } else if ((int64_t)id >= e0 && (int64_t)id < e0 + SEG_EL) {
+            const int32_t l = id - (int32_t)e0;
+            const uint32_t bit = 1u << (l & 31);
+            uniq = (atomicOr(&sm.bm[l >> 5], bit) & bit) == 0u;
+          }
+        }
+        const uint64_t m = ballot(uniq);
+        if (m != 0ull) {
+          int wb = 0;
+          if (lane == 0) wb = atomicAdd(&sm.xl_n, __popcll(m));
+          wb = __shfl(wb, 0);
+          const int pos = wb + lanes_below(m);
+          if (uniq && pos < XCAP) sm.xl_id[pos] = hv[s];
+        }
+      }
+    }
+    if (bad) atomicOr(&sm.flags, FLAG_BAD_HIST_ID);
+    __syncthreads();
+    flags |= sm.flags;
+    U = sm.xl_n;
+    if (U > XCAP) { flags |= SFLAG_XOVER; U = XCAP; }
+  }
+
+  // ---- extras: thread t gathers and penalizes entries t, t+SNT, ... (issued before the chunk work)
+  constexpr int XPT = XCAP / SNT;
+  float xr[XPT];
+#pragma unroll
+  for (int r = 0; r < XPT; ++r) {
+    const int i = tid + r * SNT;
+    xr[r] = i < U ? T::load1(rowp, sm.xl_id[i]) : 0.0f;
+  }
+
+  // ---- chunk maxima over the raw data; threshold sources skip chunks holding history positions
+  float cm[SCPT];
+  float tval = -__builtin_inff();             // max over distinct elements with exact (penalized) values
+  bool nanf = false, pinf = false;            // NaN / +inf among the penalized values
+  uint32_t hq = 0u;                           // bit q: chunk q holds a history position
+#pragma unroll
+  for (int q = 0; q < SCPT; ++q) {
+    {
+      const int64_t c = c0 + q * SNT + tid;
+      if (c >= nfull_r) v[q] = c == nfull_r ? vtail : seg_ninf<T>();
+    }
+    cm[q] = chunk_max<T>(v[q]);
+    const uint32_t hb = pen_on ? T::bits(sm.bm, q * SNT + tid) : 0u;
+    hq |= (hb != 0u) ? (1u << q) : 0u;
+    if (hb == 0u) tval = __builtin_fmaxf(tval, cm[q]);
+    else if (greedy) cm[q] = chunk_max<T>(T::mask(v[q], hb));   // greedy rows: exact masked chunk max
+    if (!(cm[q] <= 3.40282347e38f) && cm[q] != -__builtin_inff()) {   // NaN or +inf in the chunk (rare)
+#pragma unroll
+      for (int e = 0; e < EPC; ++e) {
+        const float x = T::elem(v[q], e);
+        if (!((hb >> e) & 1u)) { nanf |= x != x; pinf |= x == __builtin_inff(); }
+      }
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < XPT; ++r) {
+    const int i = tid + r * SNT;
+    if (i < U) {
+      const float pv = pen_val(xr[r]);
+      sm.xl_val[i] = pv;
+      xr[r] = pv;
+      tval = __builtin_fmaxf(tval, pv);
+      nanf |= pv != pv;
+      pinf |= pv == __builtin_inff();
+    }
+  }
+  if (ballot(nanf) != 0ull) flags |= SFLAG_NAN;
+  if (ballot(pinf) != 0ull) flags |= SFLAG_PINF;
+  if (lane == 0) sm.ired[wid] = flags;
+  if (tid == 0) sm.cnt = 0;
+
+  SegStat st;
+  st.ncand = 0;
+  st.tau = -__builtin_inff();
+  st.amax = -1;
+  st.ymax = -__builtin_inff();
+  st.pad[0] = st.pad[1] = st.pad[2] = 0;
+  uint64_t* cbase = P.cand + ((int64_t)row * S + seg) * SEG_CAP;
+
+  if (greedy) {
+    __syncthreads();
+    // masked maximum and its first index (NaN counts as the max, sampler.py:82-83):
+    // the masked chunk maxima, then an element scan (re-read from L2) of the first
+    // chunk of each thread that reaches the segment maximum.
+    float gm = -__builtin_inff();
+#pragma unroll
+    for (int q = 0; q < SCPT; ++q) gm = fmax_nan(gm, cm[q]);
+#pragma unroll
+    for (int r = 0; r < XPT; ++r)
+      if (tid + r * SNT < U) gm = fmax_nan(gm, xr[r]);
+    const float Mx = seg_max_nan(gm, &sm);
+    const bool nanm = Mx != Mx;
+    int32_t gi = 0x7fffffff;
+#pragma unroll
+    for (int q = 0; q < SCPT; ++q) {
+      // chunks of a thread are in ascending token order: the first matching chunk decides
+      if (gi == 0x7fffffff && (nanm ? (cm[q] != cm[q]) : (cm[q] == Mx))) {
+        const uint32_t hb = pen_on ? T::bits(sm.bm, q * SNT + tid) : 0u;
+        const int64_t c = c0 + q * SNT + tid;
+        const uint4 raw = (c + 1) * EPC <= V ? rowv[c] : load_tail_chunk<T>(rowp, c, V);   // re-read (L2)
+        const uint4 w = pen_on ? T::mask(raw, hb) : raw;
+#pragma unroll
+        for (int e = EPC - 1; e >= 0; --e) {
+          const float x = T::elem(w, e);
+          if ((nanm ? (x != x) : (x == Mx)) && c * EPC + e < V) gi = (int32_t)(c * EPC + e);
+        }
+      }
+    }
+#pragma unroll
+    for (int r = 0; r < XPT; ++r) {
+      const int i = tid + r * SNT;
+      if (i < U && (nanm ? (xr[r] != xr[r]) : (xr[r] == Mx)) && sm.xl_id[i] < gi) gi = sm.xl_id[i];
+    }
+    const int32_t best = seg_min_i(gi, &sm);
+    st.ymax = Mx;
+    st.amax = best;
+    st.flags = flags | sm.ired[0] | sm.ired[1] | sm.ired[2] | sm.ired[3];
+  } else {
+    // ---- lower bound of the k-th largest: ceil(k/4)-th largest thread value per wave, min over waves
+    const int kw = (k + SNW - 1) / SNW;
+    const uint32_t key = wave_sort_u32(~fkey(tval));   // descending
+    const float tw = fkey_inv(~__shfl(key, kw - 1));
+    if (lane == 0) sm.fred[wid] = tw;
+    __syncthreads();
+    float taux = sm.fred[0];
+#pragma unroll
+    for (int i = 1; i < SNW; ++i) taux = sm.fred[i] < taux ? sm.fred[i] : taux;
+    st.flags = flags | sm.ired[0] | sm.ired[1] | sm.ired[2] | sm.ired[3];
+    const float tauy = div_rn(taux, tdiv, rdiv);
+    const float tc = lower_preimage(taux, tdiv, rdiv);   // x >= tc  <=>  x / t >= tauy = RN(taux / t)
+    // ---- candidates: extras >= tc
+#pragma unroll
+    for (int r = 0; r < XPT; ++r) {
+      const int i = tid + r * SNT;
+      if (i < U && xr[r] >= tc && xr[r] > -__builtin_inff())
+        seg_append(div_rn(xr[r], tdiv, rdiv), sm.xl_id[i], cbase, &sm);
+    }
+    // ---- candidates: elements >= tc of chunks whose maximum reaches tc, re-read (L2);
+    // history positions are skipped (their values are the extras)
+    uint32_t fm = 0u;
+#pragma unroll
+    for (int q = 0; q < SCPT; ++q) fm |= (cm[q] >= tc) ? (1u << q) : 0u;
+    while (fm != 0u) {
+      const int qa = __builtin_ctz(fm);
+      fm &= fm - 1u;
+      const int qb = fm != 0u ? __builtin_ctz(fm) : -1;
+      if (qb >= 0) fm &= fm - 1u;
+      const int64_t ca = c0 + qa * SNT + tid;
+      const int64_t cb = c0 + (qb >= 0 ? qb : qa) * SNT + tid;
+      const uint4 wa = (ca + 1) * EPC <= V ? rowv[ca] : load_tail_chunk<T>(rowp, ca, V);
+      const uint4 wb = qb < 0 ? wa : ((cb + 1) * EPC <= V ? rowv[cb] : load_tail_chunk<T>(rowp, cb, V));
+      const uint32_t ha = pen_on ? T::bits(sm.bm, qa * SNT + tid) : 0u;
+      const uint32_t hb2 = pen_on ? T::bits(sm.bm, (qb >= 0 ? qb : qa) * SNT + tid) : 0u;
+#pragma unroll
+      for (int e = 0; e < EPC; ++e) {
+        const float x = T::elem(wa, e);
+        if (!((ha >> e) & 1u) && x >= tc && x > -__builtin_inff())
+          seg_append(div_rn(x, tdiv, rdiv), ca * EPC + e, cbase, &sm);
+      }
+      if (qb >= 0) {
+#pragma unroll
+        for (int e = 0; e < EPC; ++e) {
+          const float x = T::elem(wb, e);
+          if (!((hb2 >> e) & 1u) && x >= tc && x > -__builtin_inff())
+            seg_append(div_rn(x, tdiv, rdiv), cb * EPC + e, cbase, &sm);
+        }
+      }
+    }
+    __syncthreads();
+    st.tau = tauy;
+    st.ncand = sm.cnt;
+  }
+  if (tid == 0) dc_store_stat(P.stats + (int64_t)row * S + seg, st);
+
+  // ---- arrival: the last workgroup of the row finalises it.  Every wave waits
+  // for its device-coherent stores to complete before the barrier; the counter
+  // increment follows them.
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  if (tid == 0) sm.last = atomicAdd(&P.counters[row], 1) == S - 1;
+  __syncthreads();
+  if (!sm.last) return;
+  if (tid == 0) __hip_atomic_store(&P.counters[row], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+
+  // ================================ finaliser ================================
+  const SegStat* rs = P.stats + (int64_t)row * S;
+  // wave 0 combines the per-segment statistics (S <= 64: one lane per segment)
+  if (wid == 0) {
+    const bool act = lane < S;
+    SegStat s;
+    if (act) s = dc_load_stat(rs + lane);
+    int32_t fl = act ? s.flags : 0;
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) fl |= __shfl_xor(fl, o);
+    if (greedy) {
+      const float ym = act ? s.ymax : -__builtin_inff();
+      const float M = wave_max_nan(ym);
+      const bool nanm = M != M;
+      const bool hit = act && (nanm ? (ym != ym) : (ym == M));
+      const int32_t am = wave_min(hit ? s.amax : 0x7fffffff);
+      if (lane == 0) {
+        P.out_ids[row] = am == 0x7fffffff ? 0 : am;
+        P.status[row] = 0;
+        seg_write_info(P.out_info, row, PATH_GREEDY, 1, -__builtin_inff(), 0, 0, fl & 0xffff, M, am);
+      }
+    } else {
+      const float tau = wave_max(act ? s.tau : -__builtin_inff());
+      const int nc = act ? s.ncand : 0;
+      const bool over = ballot(act && nc > SEG_CAP) != 0ull;
+      const int ncl = nc < SEG_CAP ? nc : SEG_CAP;
+      const int inc = wave_incl_scan(ncl);
+      if (act) sm.off[lane + 1] = inc;
+      if (lane == 0) {
+        sm.off[0] = 0;
+        sm.fb[1] = tau;
+        sm.ib[0] = fl;
+        sm.ib[1] = (over || (fl & SFLAG_XOVER)) ? 1 : 0;
+      }
+    }
+  }
+  if (greedy) return;
+  __syncthreads();
+  const float tau = sm.fb[1];
+  const int32_t sfl = sm.ib[0];
+  const int32_t fl = sfl & 0xffff;
+  const int total = sm.off[S];
+  const float u0 = P.uniforms[row];
+  const float u = (u0 >= 0.0f) ? (u0 < 1.0f ? u0 : 0x1.fffffep-1f) : 0.0f;
+
+  auto uniform_row = [&](float Mrep) {
+    // rows whose softmax is NaN: uniform 1/V over the vocabulary (sampler.py:77-80)
+    const float qv = (float)(1.0 / (double)V);
+    if (tid == 0) {
+      const double qd = qv, ud = u;
+      int64_t i = (int64_t)(ud / qd);
+      while (i > 0 && (double)i * qd > ud) --i;
+      while ((double)(i + 1) * qd <= ud && i < V) ++i;
+      if (i >= V) i = V - 1;
+      P.out_ids[row] = i;
+      P.status[row] = 0;
+      seg_write_info(P.out_info, row, PATH_UNIFORM, (int32_t)V, -__builtin_inff(), (int32_t)V, 0, fl, Mrep, -1);
+    }
+    if (P.out_probs != nullptr) {
+      float* pr = P.out_probs + (int64_t)row * V;
+      for (int64_t i = tid; i < V; i += SNT) pr[i] = qv;
+    }
+  };
+  if (sfl & SFLAG_NAN) { uniform_row(__builtin_nanf("")); return; }
+  if (sfl & SFLAG_PINF) { uniform_row(__builtin_inff()); return; }
+  if (sm.ib[1] != 0 || total > FIN_SLOTS * SNT) {
+    if (tid == 0) P.status[row] = 1;   // candidate overflow: per-row kernel
+    return;
+  }
+
+  // ---- gather the candidates (each thread up to FIN_SLOTS, all loads in flight)
+  float cy[FIN_SLOTS];
+  int32_t cid[FIN_SLOTS];
+#pragma unroll
+  for (int r = 0; r < FIN_SLOTS; ++r) {
+    const int f = tid + r * SNT;
+    cy[r] = -__builtin_inff();
+    cid[r] = 0;
+    if (f < total) {
+      int lo = 0, hi = S;   // segment s with off[s] <= f < off[s+1]
+      while (hi - lo > 1) {
+        const int mid = (lo + hi) >> 1;
+        if (sm.off[mid] <= f) lo = mid; else hi = mid;
+      }
+      const uint64_t e = dc_load(P.cand + ((int64_t)row * S + lo) * SEG_CAP + (f - sm.off[lo]));
+      cy[r] = __uint_as_float((uint32_t)(e >> 32));
+      cid[r] = (int32_t)(uint32_t)e;
+    }
+  }
+  int nin = 0;
+  float lmin = 3.40282347e38f, lmax = -__builtin_inff();
+#pragma unroll
+  for (int r = 0; r < FIN_SLOTS; ++r) {
+    lmax = __builtin_fmaxf(lmax, cy[r]);
+    if (cy[r] >= tau && cy[r] > -__builtin_inff()) { ++nin; lmin = __builtin_fminf(lmin, cy[r]); }
+  }
+  // row max (the maximum is always a candidate) and the count above the largest segment bound
+  lmax = wave_max(lmax);
+  nin = wave_sum(nin);
+  lmin = wave_min(lmin);
+  if (lane == 0) { sm.fred[wid] = lmax; sm.ired[wid] = nin; sm.wbase[wid] = __float_as_int(lmin); }
+  __syncthreads();
+  float M = sm.fred[0], lo = __int_as_float(sm.wbase[0]);
+  int n1 = sm.ired[0];
+#pragma unroll
+  for (int w2 = 1; w2 < SNW; ++w2) {
+    M = __builtin_fmaxf(M, sm.fred[w2]);
+    lo = __builtin_fminf(lo, __int_as_float(sm.wbase[w2]));
+    n1 += sm.ired[w2];
+  }
+  if (n1 == 0) { uniform_row(-__builtin_inff()); return; }   // every logit -inf
+  // refine: linear histogram of [lo, M]; keep the bins up to the one holding the k-th largest
+  double hist_hi = 0.0, hist_s = 0.0;
+  int bstar = SHIST;   // keep everything >= tau
+  if (n1 > 64 && (double)M > (double)lo) {
+    hist_hi = (double)M;
+    hist_s = (double)SHIST / ((double)M - (double)lo);
+    for (int i = tid; i < SHIST; i += SNT) sm.hist[i] = 0u;
+    if (tid == 0) sm.ib[2] = SHIST - 1;
+    __syncthreads();
+#pragma unroll
+    for (int r = 0; r < FIN_SLOTS; ++r)
+      if (cy[r] >= tau && cy[r] > -__builtin_inff()) {
+        const double t = (hist_hi - (double)cy[r]) * hist_s;
+        const int bb = t <= 0.0 ? 0 : (t >= (double)(SHIST - 1) ? SHIST - 1 : (int)t);
+        atomicAdd(&sm.hist[bb], 1u);
+      }
+    __syncthreads();
+    // first bin whose inclusive count reaches k (thread t owns bin t)
+    const int c = (int)sm.hist[tid];
+    const int incl = wave_incl_scan(c);
+    if (lane == 63) sm.ired[wid] = incl;
+    __syncthreads();
+    int before = 0;
+#pragma unroll
+    for (int w2 = 0; w2 < SNW; ++w2) before += w2 < wid ? sm.ired[w2] : 0;
+    const int ci = before + incl;
+    if (ci >= k && ci - c < k) sm.ib[2] = tid;
+    __syncthreads();
+    bstar = sm.ib[2];
+  }
+  // ---- compact the survivors into LDS
+  if (tid == 0) sm.cnt = 0;
+  __syncthreads();
+#pragma unroll
+  for (int r = 0; r < FIN_SLOTS; ++r) {
+    bool take = cy[r] >= tau && cy[r] > -__builtin_inff();
+    if (take && bstar < SHIST) {
+      const double t = (hist_hi - (double)cy[r]) * hist_s;
+      const int bb = t <= 0.0 ? 0 : (t >= (double)(SHIST - 1) ? SHIST - 1 : (int)t);
+      take = bb <= bstar;
+    }
+    const uint64_t m = ballot(take);
+    if (m != 0ull) {
+      int base = 0;
+      const int leader = __builtin_ctzll(m);
+      if (lane == leader) base = atomicAdd(&sm.cnt, __popcll(m));
+      base = __shfl(base, leader);
+      const int p = base + lanes_below(m);
+      if (take && p < WAVE_CAP) sm.list[p] = ((uint64_t)__float_as_uint(cy[r]) << 32) | (uint32_t)cid[r];
+    }
+  }
+  if (P.out_probs != nullptr) {
+    float* pr = P.out_probs + (int64_t)row * V;
+    for (int64_t i = tid; i < V; i += SNT) pr[i] = 0.0f;
+  }
+  __syncthreads();
+  const int n2 = sm.cnt;
+  if (n2 > WAVE_CAP) {
+    if (tid == 0) P.status[row] = 1;   // huge tie group at the threshold: per-row kernel
+    return;
+  }
+  if (wid != 0) return;
+  if (lane == 0) P.status[row] = 0;
+  const float topp = P.top_p[row];
+  const bool topp_on = topp < 1.0f;
+  if (n2 <= 64)
+    wave_finalize<1>(sm.list, n2, k, topp_on, topp, 1.0f, 1.0f, u, row, P.out_ids, P.out_probs, V, P.out_info, fl, n1,
+                     PATH_WAVE_SET);
+  else if (n2 <= 128)
+    wave_finalize<2>(sm.list, n2, k, topp_on, topp, 1.0f, 1.0f, u, row, P.out_ids, P.out_probs, V, P.out_info, fl, n1,
+                     PATH_WAVE_SET);
+  else
+    wave_finalize<4>(sm.list, n2, k, topp_on, topp, 1.0f, 1.0f, u, row, P.out_ids, P.out_probs, V, P.out_info, fl, n1,
+                     PATH_WAVE_SET);
+}
+
+}  // namespace ns

@@ -31,8 +31,13 @@ def params_of(w):
                              repetition_penalty=float(w.repetition_penalty[i])) for i in range(w.batch)]
 
 
-def run_gpu(w, device, logits=None, want_probs=True, uniforms=None):
-    """One ns_sample call over workload ``w``; returns ids, probs (CPU) and info words."""
+def run_gpu(w, device, logits=None, want_probs=True, uniforms=None, workspace="auto", mode=None):
+    """One ns_sample call over workload ``w``; returns ids, probs (CPU) and info words.
+
+    ``mode``: NS_MODE_SEGMENTED (greedy and small-k rows split over several
+    workgroups, the per-row kernel for the rest), NS_MODE_PER_ROW (one workgroup
+    per row), or NS_MODE_AUTO (the default: chosen from the batch size).
+    """
     packed = S.PackedRows(params_of(w), w.histories, w.vocab)
     d = packed.to_device(device)
     if logits is None:
@@ -45,7 +50,8 @@ def run_gpu(w, device, logits=None, want_probs=True, uniforms=None):
     info = torch.zeros((B, L.NS_INFO_WORDS), dtype=torch.int32, device=device)
     L.sample_raw(logits, d["temperature"], d["top_k"], d["top_p"], d["rep_penalty"], u, out,
                  sample_idx=sidx, hist_offsets=d["hist_offsets"], hist_ids=d["hist_ids"],
-                 max_hist=packed.max_hist, out_probs=probs, out_info=info)
+                 max_hist=packed.max_hist, out_probs=probs, out_info=info, workspace=workspace,
+                 mode=L.NS_MODE_AUTO if mode is None else mode)
     torch.cuda.synchronize()
     return {"ids": out.cpu().numpy(), "probs": None if probs is None else probs.cpu(),
             "info": info.cpu().numpy()}

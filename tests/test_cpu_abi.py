@@ -41,7 +41,7 @@ def test_struct_layout_matches_header():
     body = txt[txt.index("typedef struct ns_sample_args"):txt.index("} ns_sample_args;")]
     names = re.findall(r"^\s*[\w\s\*]+?\b(\w+);", body, flags=re.M)
     assert names == [f[0] for f in L.NsSampleArgs._fields_]
-    assert ctypes.sizeof(L.NsSampleArgs) == 136
+    assert ctypes.sizeof(L.NsSampleArgs) == 160
 
 
 def test_lds_bytes_and_argument_errors():

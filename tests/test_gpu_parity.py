@@ -17,34 +17,56 @@ O = pytest.importorskip("oracle.sampler_oracle")
 pytestmark = pytest.mark.gpu
 
 
-def _check(w, device, **kw):
-    print(f"[parity] {w.name} B={w.batch} V={w.vocab} dtype={w.dtype}", flush=True)
-    g = run_gpu(w, device, **kw)
+L = pkg("_lib")
+# path name -> (workspace, mode)
+PATHS = {"segmented": ("auto", L.NS_MODE_SEGMENTED), "per-row": (None, L.NS_MODE_PER_ROW)}
+
+
+def _check(w, device, path="segmented", **kw):
+    print(f"[parity] {w.name} B={w.batch} V={w.vocab} dtype={w.dtype} path={path}", flush=True)
+    ws, mode = PATHS[path]
+    g = run_gpu(w, device, workspace=ws, mode=mode, **kw)
     r = O.sample_workload(w)
     fails, stats = compare(g, r)
+    stats["paths"] = {int(c): int((g["info"][:, 0] == c).sum()) for c in np.unique(g["info"][:, 0])}
     print(f"[parity] {w.name}: {stats}", flush=True)
     assert not fails, "\n".join(fails)
     return g, r, stats
 
 
+@pytest.mark.parametrize("path", list(PATHS))
 @pytest.mark.parametrize("cfg", [0, 2])
-def test_config_topk_rows(device, cfg):
-    _check(W.make_workload(cfg), device)
+def test_config_topk_rows(device, cfg, path):
+    g, r, stats = _check(W.make_workload(cfg), device, path)
+    if cfg == 2 or path == "segmented":
+        assert stats["paths"].get(6, 0) == len(r.ids)   # every row finalised inside one wave
 
 
+@pytest.mark.parametrize("path", list(PATHS))
 @pytest.mark.parametrize("cfg", [1, 4])
-def test_config_mixed_rows(device, cfg):
-    _check(W.make_workload(cfg), device)
+def test_config_mixed_rows(device, cfg, path):
+    _check(W.make_workload(cfg), device, path)
 
 
-def test_config_long_nucleus(device):
-    _check(W.make_workload(3, batch=32), device)
+@pytest.mark.parametrize("path", list(PATHS))
+def test_config_long_nucleus(device, path):
+    _check(W.make_workload(3, batch=32), device, path)
 
 
-def test_run_twice_identical(device):
+@pytest.mark.parametrize("path", list(PATHS))
+def test_run_twice_identical(device, path):
     w = W.make_workload(1, batch=16)
-    a = run_gpu(w, device)
-    b = run_gpu(w, device)
+    ws, mode = PATHS[path]
+    a = run_gpu(w, device, workspace=ws, mode=mode)
+    b = run_gpu(w, device, workspace=ws, mode=mode)
     assert np.array_equal(a["ids"], b["ids"])
     assert torch.equal(a["probs"], b["probs"])
     assert np.array_equal(a["info"], b["info"])
+
+
+def test_auto_mode_decode_batch(device):
+    """The default mode on the decode batch (one workgroup per row once the batch fills the GPU)."""
+    g, r, stats = _check(W.make_workload(2), device, "per-row")
+    w = W.make_workload(2)
+    a = run_gpu(w, device)
+    assert np.array_equal(a["ids"], g["ids"])
