@@ -35,6 +35,29 @@ __device__ __forceinline__ uint4 fresh(uint4 w) {
   return w;
 }
 
+// bfloat16 bits of an upper bound of x (x itself when x is a bfloat16 value, NaN or inf):
+// chunk maxima are kept this way, two per register, to flag chunks that may reach a bound.
+__device__ __forceinline__ uint32_t bf16_up(float x) {
+  const uint32_t b = __float_as_uint(x);
+  uint32_t h = b >> 16;
+  if (x > 0.0f && x <= 3.40282347e38f && (b & 0xffffu) != 0u) h += 1u;
+  return h;
+}
+__device__ __forceinline__ float bf16_float(uint32_t h) { return __uint_as_float(h << 16); }
+
+// Wave-aggregated append of (x, id) to the LDS candidate list (32-bit ids); every lane
+// of the wave calls it, `take` selects.
+__device__ __forceinline__ void cand_push(bool take, float x, uint32_t id, uint64_t* cand, Misc* misc) {
+  const uint64_t m = ballot(take);
+  if (m == 0ull) return;
+  const int leader = __builtin_ctzll(m);
+  int base = 0;
+  if (lane_id() == leader) base = atomicAdd(&misc->cand_n, __popcll(m));
+  base = __shfl(base, leader);
+  const int pos = base + lanes_below(m);
+  if (take && pos < CAP) cand[pos] = ((uint64_t)__float_as_uint(x) << 32) | id;
+}
+
 template <typename T>
 __host__ __device__ __forceinline__ bool row_fits(int64_t V) {
   return (V + T::EPC - 1) / T::EPC <= (int64_t)NT * RCPT;
@@ -81,43 +104,23 @@ __device__ __forceinline__ int row_fast(const RowArgs P, const int row, const in
   int32_t* is = reinterpret_cast<int32_t*>(&misc->red);
   BlockScratch* red = &misc->red;
 
-  // ---- bitmap cleared, then the history ids and the whole row: every load in flight at once
+  // ---- history first, before the row is requested (a load issued while the row
+  // streams waits behind it): presence bitmap, unique ids (set semantics), and the
+  // gather of the history positions' values
+  int U = 0;
   if (pen_on) {
     const int nbw = (int)((V + 31) / 32);
     for (int i = tid; i < nbw; i += NT) bm[i] = 0u;
     if (tid == 0) { misc->xl_n = 0; misc->flags = 0; }
     __syncthreads();
-  }
-  // the first RHB history ids of every thread go out before the row (histories up to
-  // RHB * NT ids); longer histories load the rest after it
-  const int32_t* hp = P.hist_ids + h0;
-  int32_t hid[RHB];
-#pragma unroll
-  for (int s = 0; s < RHB; ++s) {
-    const int j = s * NT + tid;
-    hid[s] = (pen_on && j < H) ? hp[j] : 0;
-  }
-  // buffer loads over the row's full chunks (chunk q*NT + t to thread t); chunks at or
-  // past the last full one read zeros and are never used: loaded registers are only read
-  const int nf = (int)nfull;
-  uint4 v[RCPT];
-  {
-    const __amdgpu_buffer_rsrc_t rs = make_rsrc(rowp, (uint32_t)nf * 16u);
-#pragma unroll
-    for (int q = 0; q < RCPT; ++q) v[q] = buf_load16(rs, (uint32_t)tid * 16u, (uint32_t)(q * NT * 16));
-  }
-
-  // ---- presence bitmap and the unique history ids (set semantics); waits only for the ids
-  int U = 0;
-  if (pen_on) {
+    const int32_t* hp = P.hist_ids + h0;
     bool bad = false;
     for (int base = 0; base < H; base += RHB * NT) {
-      if (base > 0) {
+      int32_t hid[RHB];
 #pragma unroll
-        for (int s = 0; s < RHB; ++s) {
-          const int j = base + s * NT + tid;
-          hid[s] = j < H ? hp[j] : 0;
-        }
+      for (int s = 0; s < RHB; ++s) {
+        const int j = base + s * NT + tid;
+        hid[s] = j < H ? hp[j] : 0;
       }
 #pragma unroll
       for (int s = 0; s < RHB; ++s) {
@@ -145,11 +148,21 @@ __device__ __forceinline__ int row_fast(const RowArgs P, const int row, const in
     flags |= misc->flags;
     U = misc->xl_n;
   }
-  // gather the first NT history positions' values (in flight during the chunk work)
-  const float x0 = tid < U ? T::load1(rowp, xl_id[tid]) : 0.0f;
+  const float x0 = tid < U ? T::load1(rowp, xl_id[tid]) : 0.0f;   // first NT history values
 
-  // ---- chunk maxima as the loads land; threshold sources skip chunks holding history positions
-  // (chunk maxima are recomputed where needed rather than kept: registers hold the row)
+  // ---- the whole row in flight: buffer loads over the row's full chunks (chunk q*NT + t to
+  // thread t); chunks at or past the last full one read zeros and are never used
+  const int nf = (int)nfull;
+  uint4 v[RCPT];
+  {
+    const __amdgpu_buffer_rsrc_t rs = make_rsrc(rowp, (uint32_t)nf * 16u);
+#pragma unroll
+    for (int q = 0; q < RCPT; ++q) v[q] = buf_load16(rs, (uint32_t)tid * 16u, (uint32_t)(q * NT * 16));
+  }
+
+  // ---- chunk maxima as the loads land (kept: the candidate pass compares them with the
+  // bound); threshold sources skip chunks holding history positions
+  uint32_t cmp[RCPT / 2];            // chunk maxima (greedy rows: masked), bfloat16 upper bounds
   float tval = -__builtin_inff();
   float gm = -__builtin_inff();      // greedy rows: NaN-propagating masked maximum
   bool nanf = false, pinf = false;
@@ -160,7 +173,10 @@ __device__ __forceinline__ int row_fast(const RowArgs P, const int row, const in
     if ((q + 1) * NT > nf && c >= nf) cmq = -__builtin_inff();   // past the last full chunk
     const uint32_t hb = (pen_on && c < nf) ? T::bits(bm, c) : 0u;
     if (hb == 0u) tval = __builtin_fmaxf(tval, cmq);
-    if (greedy) gm = fmax_nan(gm, hb == 0u ? cmq : chunk_max<T>(T::mask(v[q], hb)));
+    else if (greedy) cmq = chunk_max<T>(T::mask(v[q], hb));      // greedy rows: exact masked chunk max
+    if (greedy) gm = fmax_nan(gm, cmq);
+    if (q & 1) cmp[q >> 1] |= bf16_up(cmq) << 16;
+    else cmp[q >> 1] = bf16_up(cmq);
     if (!(cmq <= 3.40282347e38f) && cmq != -__builtin_inff()) {   // NaN or +inf in the chunk (rare)
 #pragma unroll
       for (int e = 0; e < EPC; ++e) {
@@ -215,11 +231,11 @@ __device__ __forceinline__ int row_fast(const RowArgs P, const int row, const in
     for (int q = 0; q < RCPT; ++q) {
       // chunks of a thread are in ascending token order: the first matching chunk decides
       const int c = q * NT + tid;
-      const uint32_t hb = (pen_on && c < nf) ? T::bits(bm, c) : 0u;
-      const uint4 vq = fresh(v[q]);
-      const uint4 w = pen_on ? T::mask(vq, hb) : vq;
-      const float cmq = chunk_max<T>(w);
-      if (c < nf && gi == INT64_MAX && (nanm ? (cmq != cmq) : (cmq == Mx))) {
+      const float cu = bf16_float((cmp[q >> 1] >> (16 * (q & 1))) & 0xffffu);
+      if (c < nf && gi == INT64_MAX && (nanm ? (cu != cu) : (cu >= Mx))) {
+        const uint32_t hb = pen_on ? T::bits(bm, c) : 0u;
+        const uint4 vq = rowv[c];   // re-read (L2)
+        const uint4 w = pen_on ? T::mask(vq, hb) : vq;
 #pragma unroll
         for (int e = EPC - 1; e >= 0; --e) {
           const float x = T::elem(w, e);
@@ -280,19 +296,37 @@ __device__ __forceinline__ int row_fast(const RowArgs P, const int row, const in
   const float taux = fs[64];
   const float tc = lower_preimage(taux, tdiv, rdiv);   // x >= tc  <=>  x / t >= RN(taux / t)
 
-  // ---- candidates x >= tc from the chunks reaching tc (registers) and the history positions
+  // ---- candidates x >= tc: chunks whose maximum reaches tc are re-read (L2) two at a time
+  // (the row's registers are free after the chunk pass), then the history positions
+  uint32_t fm = 0u;
 #pragma unroll
   for (int q = 0; q < RCPT; ++q) {
     const int c = q * NT + tid;
-    const uint4 vq = fresh(v[q]);
-    const bool fq = c < nf && chunk_max<T>(vq) >= tc;
-    if (ballot(fq) != 0ull) {
-      const uint32_t hb = (pen_on && c < nf) ? T::bits(bm, c) : 0u;
+    fm |= (c < nf && bf16_float((cmp[q >> 1] >> (16 * (q & 1))) & 0xffffu) >= tc) ? (1u << q) : 0u;
+  }
+  {
+    const __amdgpu_buffer_rsrc_t rs = make_rsrc(rowp, (uint32_t)nf * 16u);
+    while (ballot(fm != 0u) != 0ull) {
+      const int qa = fm != 0u ? __builtin_ctz(fm) : -1;
+      fm &= fm - 1u;
+      const int qb = fm != 0u ? __builtin_ctz(fm) : -1;
+      fm &= fm - 1u;
+      const int ca = qa * NT + tid, cb = qb * NT + tid;
+      const uint4 wa = buf_load16(rs, (uint32_t)(qa >= 0 ? ca : 0) * 16u, 0u);
+      const uint4 wb = buf_load16(rs, (uint32_t)(qb >= 0 ? cb : 0) * 16u, 0u);
+      const uint32_t ha = (pen_on && qa >= 0) ? T::bits(bm, ca) : 0u;
+      const uint32_t hb2 = (pen_on && qb >= 0) ? T::bits(bm, cb) : 0u;
 #pragma unroll
       for (int e = 0; e < EPC; ++e) {
-        const float x = T::elem(vq, e);
-        const int64_t id = c * EPC + e;
-        cand_append(fq && !((hb >> e) & 1u) && x >= tc && id < V, x, id, cand, misc);
+        const float x = T::elem(wa, e);
+        cand_push(qa >= 0 && !((ha >> e) & 1u) && x >= tc && x > -__builtin_inff(), x, (uint32_t)ca * EPC + e,
+                  cand, misc);
+      }
+#pragma unroll
+      for (int e = 0; e < EPC; ++e) {
+        const float x = T::elem(wb, e);
+        cand_push(qb >= 0 && !((hb2 >> e) & 1u) && x >= tc && x > -__builtin_inff(), x, (uint32_t)cb * EPC + e,
+                  cand, misc);
       }
     }
   }
@@ -300,7 +334,7 @@ __device__ __forceinline__ int row_fast(const RowArgs P, const int row, const in
     const int i = base + tid;
     const float x = i < U ? xl_val[i] : -__builtin_inff();
     const bool t = x >= tc;
-    if (ballot(t) != 0ull) cand_append(t, x, t ? xl_id[i] : 0, cand, misc);
+    if (ballot(t) != 0ull) cand_push(t && x > -__builtin_inff(), x, t ? (uint32_t)xl_id[i] : 0u, cand, misc);
   }
   __syncthreads();
   const int n = misc->cand_n;
