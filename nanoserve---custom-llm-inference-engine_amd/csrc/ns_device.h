@@ -41,39 +41,116 @@ __device__ __forceinline__ float desc_key_val(uint64_t k) { return fkey_inv(~(ui
 __device__ __forceinline__ uint32_t desc_key_id(uint64_t k) { return (uint32_t)k; }
 
 // ---------------------------------------------------------------- wave ops
+// Lane exchange by a constant xor distance s, on the VALU instead of the LDS
+// crossbar (ds_bpermute): DPP quad_perm for s = 1, 2; DPP row shifts plus a
+// select for s = 4, 8; v_permlane16_swap / v_permlane32_swap for s = 16, 32.
+// s must fold to a constant (it does inside fully unrolled loops).
+__device__ __forceinline__ uint32_t lane_xor_u32(uint32_t v, int s) {
+  const int lane = lane_id();
+  switch (s) {
+    case 1: return __builtin_amdgcn_update_dpp(0u, v, 0xB1, 0xF, 0xF, false);   // quad_perm [1,0,3,2]
+    case 2: return __builtin_amdgcn_update_dpp(0u, v, 0x4E, 0xF, 0xF, false);   // quad_perm [2,3,0,1]
+    case 4: {
+      const uint32_t up = __builtin_amdgcn_update_dpp(0u, v, 0x104, 0xF, 0xF, false);   // row_shl:4
+      const uint32_t dn = __builtin_amdgcn_update_dpp(0u, v, 0x114, 0xF, 0xF, false);   // row_shr:4
+      return (lane & 4) ? dn : up;
+    }
+    case 8: {
+      const uint32_t up = __builtin_amdgcn_update_dpp(0u, v, 0x108, 0xF, 0xF, false);   // row_shl:8
+      const uint32_t dn = __builtin_amdgcn_update_dpp(0u, v, 0x118, 0xF, 0xF, false);   // row_shr:8
+      return (lane & 8) ? dn : up;
+    }
+    case 16: {
+      const auto r = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+      return (lane & 16) ? r[0] : r[1];
+    }
+    case 32: {
+      const auto r = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+      return (lane & 32) ? r[0] : r[1];
+    }
+    default: return __shfl_xor(v, s);
+  }
+}
+template <typename T> __device__ __forceinline__ T lane_xor(T v, int s) {
+  static_assert(sizeof(T) == 4 || sizeof(T) == 8, "lane_xor: 32- or 64-bit values");
+  if constexpr (sizeof(T) == 4) {
+    return __builtin_bit_cast(T, lane_xor_u32(__builtin_bit_cast(uint32_t, v), s));
+  } else {
+    const uint64_t u = __builtin_bit_cast(uint64_t, v);
+    const uint64_t lo = lane_xor_u32((uint32_t)u, s), hi = lane_xor_u32((uint32_t)(u >> 32), s);
+    return __builtin_bit_cast(T, (hi << 32) | lo);
+  }
+}
+// Value of lane `src` (wave-uniform) broadcast to every lane.
+template <typename T> __device__ __forceinline__ T read_lane(T v, int src) {
+  static_assert(sizeof(T) == 4 || sizeof(T) == 8, "read_lane: 32- or 64-bit values");
+  if constexpr (sizeof(T) == 4) {
+    return __builtin_bit_cast(T, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), src));
+  } else {
+    const uint64_t u = __builtin_bit_cast(uint64_t, v);
+    const uint64_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)u, src);
+    const uint64_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(u >> 32), src);
+    return __builtin_bit_cast(T, (hi << 32) | lo);
+  }
+}
+// Lane l receives lane l - s of its 16-lane row, or 0 where l - s leaves the row.
+template <typename T> __device__ __forceinline__ T row_shr_zero(T v, int s) {
+  static_assert(sizeof(T) == 4 || sizeof(T) == 8, "row_shr_zero: 32- or 64-bit values");
+  if constexpr (sizeof(T) == 4) {
+    uint32_t u = __builtin_bit_cast(uint32_t, v);
+    switch (s) {
+      case 1: u = __builtin_amdgcn_update_dpp(0u, u, 0x111, 0xF, 0xF, true); break;
+      case 2: u = __builtin_amdgcn_update_dpp(0u, u, 0x112, 0xF, 0xF, true); break;
+      case 4: u = __builtin_amdgcn_update_dpp(0u, u, 0x114, 0xF, 0xF, true); break;
+      default: u = __builtin_amdgcn_update_dpp(0u, u, 0x118, 0xF, 0xF, true); break;
+    }
+    return __builtin_bit_cast(T, u);
+  } else {
+    const uint64_t u = __builtin_bit_cast(uint64_t, v);
+    const uint64_t lo = __builtin_bit_cast(uint32_t, row_shr_zero((uint32_t)u, s));
+    const uint64_t hi = __builtin_bit_cast(uint32_t, row_shr_zero((uint32_t)(u >> 32), s));
+    return __builtin_bit_cast(T, (hi << 32) | lo);
+  }
+}
+
 template <typename T> __device__ __forceinline__ T wave_sum(T v) {
 #pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+  for (int o = 32; o > 0; o >>= 1) v += lane_xor(v, o);
   return v;
 }
 __device__ __forceinline__ float wave_max_nan(float v) {
 #pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v = fmax_nan(v, __shfl_xor(v, o));
+  for (int o = 32; o > 0; o >>= 1) v = fmax_nan(v, lane_xor(v, o));
   return v;
 }
 __device__ __forceinline__ float wave_min_nan(float v) {
 #pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v = fmin_nan(v, __shfl_xor(v, o));
+  for (int o = 32; o > 0; o >>= 1) v = fmin_nan(v, lane_xor(v, o));
   return v;
 }
 template <typename T> __device__ __forceinline__ T wave_max(T v) {
 #pragma unroll
-  for (int o = 32; o > 0; o >>= 1) { T w = __shfl_xor(v, o); v = w > v ? w : v; }
+  for (int o = 32; o > 0; o >>= 1) { T w = lane_xor(v, o); v = w > v ? w : v; }
   return v;
 }
 template <typename T> __device__ __forceinline__ T wave_min(T v) {
 #pragma unroll
-  for (int o = 32; o > 0; o >>= 1) { T w = __shfl_xor(v, o); v = w < v ? w : v; }
+  for (int o = 32; o > 0; o >>= 1) { T w = lane_xor(v, o); v = w < v ? w : v; }
   return v;
 }
-// inclusive prefix sum over the 64 lanes
+// Inclusive prefix sum over the 64 lanes: Hillis-Steele inside each 16-lane
+// row (DPP row_shr), then the three lower row totals added by readlane.
 template <typename T> __device__ __forceinline__ T wave_incl_scan(T v) {
   const int l = lane_id();
 #pragma unroll
-  for (int o = 1; o < 64; o <<= 1) {
-    T w = __shfl_up(v, o);
-    if (l >= o) v += w;
+  for (int o = 1; o < 16; o <<= 1) {
+    const T w = row_shr_zero(v, o);
+    if ((l & 15) >= o) v += w;
   }
+  const T t0 = read_lane(v, 15), t1 = read_lane(v, 31), t2 = read_lane(v, 47);
+  if (l >= 16) v += t0;
+  if (l >= 32) v += t1;
+  if (l >= 48) v += t2;
   return v;
 }
 __device__ __forceinline__ uint64_t ballot(bool p) { return __ballot(p); }

@@ -53,7 +53,7 @@ __device__ __forceinline__ void cand_push(bool take, float x, uint32_t id, uint6
   const int leader = __builtin_ctzll(m);
   int base = 0;
   if (lane_id() == leader) base = atomicAdd(&misc->cand_n, __popcll(m));
-  base = __shfl(base, leader);
+  base = read_lane(base, leader);
   const int pos = base + lanes_below(m);
   if (take && pos < CAP) cand[pos] = ((uint64_t)__float_as_uint(x) << 32) | id;
 }
@@ -138,7 +138,7 @@ __device__ __forceinline__ int row_fast(const RowArgs P, const int row, const in
         if (m != 0ull) {
           int wb = 0;
           if (lane == 0) wb = atomicAdd(&misc->xl_n, __popcll(m));
-          wb = __shfl(wb, 0);
+          wb = read_lane(wb, 0);
           if (uniq) xl_id[wb + lanes_below(m)] = id;
         }
       }
@@ -288,7 +288,7 @@ __device__ __forceinline__ int row_fast(const RowArgs P, const int row, const in
     __syncthreads();
     if (wid == 0) {
       const uint32_t k2 = wave_sort_u32(~fkey(fs[lane]));
-      const float taux = fkey_inv(~__shfl(k2, k - 1));
+      const float taux = fkey_inv(~read_lane(k2, k - 1));
       if (lane == 0) { fs[64] = taux; misc->cand_n = 0; }
     }
     __syncthreads();

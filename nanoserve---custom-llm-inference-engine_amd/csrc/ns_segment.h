@@ -171,16 +171,6 @@ __device__ __forceinline__ SegStat dc_load_stat(const SegStat* p) {
 }
 
 // ------------------------------------------------------------ wave sorting
-__device__ __forceinline__ uint64_t shfl_xor_u64(uint64_t v, int m) {
-  const uint32_t lo = __shfl_xor((uint32_t)v, m);
-  const uint32_t hi = __shfl_xor((uint32_t)(v >> 32), m);
-  return ((uint64_t)hi << 32) | lo;
-}
-__device__ __forceinline__ uint64_t shfl_u64(uint64_t v, int src) {
-  const uint32_t lo = __shfl((uint32_t)v, src);
-  const uint32_t hi = __shfl((uint32_t)(v >> 32), src);
-  return ((uint64_t)hi << 32) | lo;
-}
 
 // Ascending bitonic sort of 64*R keys held by one wave: element i = r*64 + lane.
 template <int R>
@@ -206,7 +196,7 @@ __device__ __forceinline__ void wave_sort_u64(uint64_t (&a)[R]) {
       } else {
 #pragma unroll
         for (int r = 0; r < R; ++r) {
-          const uint64_t p = shfl_xor_u64(a[r], stride);
+          const uint64_t p = lane_xor(a[r], stride);
           const int i = r * 64 + lane;
           const bool up = (i & size) == 0;
           const bool lower = (lane & stride) == 0;
@@ -226,7 +216,7 @@ __device__ __forceinline__ uint32_t wave_sort_u32(uint32_t a) {
   for (int size = 2; size <= 64; size <<= 1) {
 #pragma unroll
     for (int stride = size >> 1; stride > 0; stride >>= 1) {
-      const uint32_t p = __shfl_xor(a, stride);
+      const uint32_t p = lane_xor(a, stride);
       const bool up = (lane & size) == 0;
       const bool lower = (lane & stride) == 0;
       a = (lower == up) ? (a < p ? a : p) : (a < p ? p : a);
@@ -243,7 +233,7 @@ __device__ __forceinline__ void wave_scan_rows(const double (&v)[R], double (&ou
   for (int r = 0; r < R; ++r) {
     const double s = wave_incl_scan(v[r]);
     out[r] = carry + s;
-    carry += __shfl(s, 63);
+    carry += read_lane(s, 63);
   }
 }
 
@@ -339,7 +329,7 @@ __device__ void wave_finalize(const uint64_t* list, int n, int k, bool topp_on, 
     }
   }
   wave_sort_u64<R>(a);   // value descending, token id ascending
-  const float M = desc_key_val(shfl_u64(a[0], 0));   // the row maximum
+  const float M = desc_key_val(read_lane(a[0], 0));   // the row maximum
 
   // top-k threshold: the k-th largest (sampler.py:56-58); every value >= it is kept
   float thr = -__builtin_inff();
@@ -348,7 +338,7 @@ __device__ void wave_finalize(const uint64_t* list, int n, int k, bool topp_on, 
     uint64_t sel = a[0];
 #pragma unroll
     for (int r = 1; r < R; ++r) sel = (r == rk) ? a[r] : sel;
-    thr = desc_key_val(shfl_u64(sel, lk));
+    thr = desc_key_val(read_lane(sel, lk));
   }
   float y[R];
   int nk = 0;
@@ -391,7 +381,7 @@ __device__ void wave_finalize(const uint64_t* list, int n, int k, bool topp_on, 
     uint64_t sel = a[0];
 #pragma unroll
     for (int r = 1; r < R; ++r) sel = (r == rj) ? a[r] : sel;
-    const uint64_t kc = shfl_u64(sel, lj);
+    const uint64_t kc = read_lane(sel, lj);
     vstar = desc_key_val(kc);
     istar = (int32_t)desc_key_id(kc);
   }
@@ -441,7 +431,7 @@ __device__ void wave_finalize(const uint64_t* list, int n, int k, bool topp_on, 
     uint64_t sel = b[0];
 #pragma unroll
     for (int r = 1; r < R; ++r) sel = (r == rp) ? b[r] : sel;
-    const uint64_t kb = shfl_u64(sel, lp);
+    const uint64_t kb = read_lane(sel, lp);
     if (lane == 0) {
       out_ids[row] = (int64_t)(kb >> 32);
       seg_write_info(out_info, row, path, nf, thr, nk, n_cand, fl, vstar, istar);
@@ -464,7 +454,7 @@ __device__ __forceinline__ void seg_append(float y, int64_t id, uint64_t* cbase,
   const int leader = __builtin_ctzll(m);
   int base = 0;
   if (lane_id() == leader) base = atomicAdd(&sm->cnt, __popcll(m));
-  base = __shfl(base, leader);
+  base = read_lane(base, leader);
   const int pos = base + lanes_below(m);
   if (pos < SEG_CAP) dc_store(cbase + pos, ((uint64_t)__float_as_uint(y) << 32) | (uint32_t)id);
 }
@@ -569,7 +559,7 @@ __global__ __launch_bounds__(SNT) __attribute__((amdgpu_waves_per_eu(4))) void s
         if (m != 0ull) {
           int wb = 0;
           if (lane == 0) wb = atomicAdd(&sm.xl_n, __popcll(m));
-          wb = __shfl(wb, 0);
+          wb = read_lane(wb, 0);
           const int pos = wb + lanes_below(m);
           if (uniq && pos < XCAP) sm.xl_id[pos] = hv[s];
         }
@@ -682,7 +672,7 @@ __global__ __launch_bounds__(SNT) __attribute__((amdgpu_waves_per_eu(4))) void s
     // ---- lower bound of the k-th largest: ceil(k/4)-th largest thread value per wave, min over waves
     const int kw = (k + SNW - 1) / SNW;
     const uint32_t key = wave_sort_u32(~fkey(tval));   // descending
-    const float tw = fkey_inv(~__shfl(key, kw - 1));
+    const float tw = fkey_inv(~read_lane(key, kw - 1));
     if (lane == 0) sm.fred[wid] = tw;
     __syncthreads();
     float taux = sm.fred[0];
@@ -754,7 +744,7 @@ __global__ __launch_bounds__(SNT) __attribute__((amdgpu_waves_per_eu(4))) void s
     if (act) s = dc_load_stat(rs + lane);
     int32_t fl = act ? s.flags : 0;
 #pragma unroll
-    for (int o = 32; o > 0; o >>= 1) fl |= __shfl_xor(fl, o);
+    for (int o = 32; o > 0; o >>= 1) fl |= lane_xor(fl, o);
     if (greedy) {
       const float ym = act ? s.ymax : -__builtin_inff();
       const float M = wave_max_nan(ym);
@@ -902,7 +892,7 @@ __global__ __launch_bounds__(SNT) __attribute__((amdgpu_waves_per_eu(4))) void s
       int base = 0;
       const int leader = __builtin_ctzll(m);
       if (lane == leader) base = atomicAdd(&sm.cnt, __popcll(m));
-      base = __shfl(base, leader);
+      base = read_lane(base, leader);
       const int p = base + lanes_below(m);
       if (take && p < WAVE_CAP) sm.list[p] = ((uint64_t)__float_as_uint(cy[r]) << 32) | (uint32_t)cid[r];
     }
