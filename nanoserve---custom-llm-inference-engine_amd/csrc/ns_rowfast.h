@@ -13,7 +13,8 @@
 //   * top-k rows: a lower bound of the k-th largest from the 4 largest thread
 //     values of every wave (64 values of distinct elements, k-th largest of
 //     them), the elements of the chunks reaching it taken from registers into
-//     an LDS list, then the one-wave exact top-k / top-p / softmax / draw.
+//     an LDS list, ordered by the whole workgroup (rank counting), then the
+//     one-wave top-p / softmax / draw over the top-k prefix.
 // Rows whose candidate list outgrows the one-wave capacity (huge tie groups) are
 // redone by the general per-row code.
 #pragma once
@@ -341,17 +342,8 @@ __device__ __forceinline__ int row_fast(const RowArgs P, const int row, const in
   if (n == 0) { uniform_row(-__builtin_inff()); return 0; }   // every logit -inf
   if (n <= WAVE_CAP) {
     zero_probs(o);
-    if (wid != 0) return 0;
-    const bool topp_on = topp < 1.0f;
-    if (n <= 64)
-      wave_finalize<1>(cand, n, k, topp_on, topp, tdiv, rdiv, u, row, P.out_ids, P.out_probs, V, P.out_info, flags, n,
-                       PATH_WAVE_SET);
-    else if (n <= 128)
-      wave_finalize<2>(cand, n, k, topp_on, topp, tdiv, rdiv, u, row, P.out_ids, P.out_probs, V, P.out_info, flags, n,
-                       PATH_WAVE_SET);
-    else
-      wave_finalize<4>(cand, n, k, topp_on, topp, tdiv, rdiv, u, row, P.out_ids, P.out_probs, V, P.out_info, flags, n,
-                       PATH_WAVE_SET);
+    block_finalize<NT>(cand, n, k, topp < 1.0f, topp, tdiv, rdiv, u, row, P.out_ids, P.out_probs, V, P.out_info,
+                       flags, n, PATH_WAVE_SET);
     return 0;
   }
   __syncthreads();   // every thread has read the candidate count before the caller reuses LDS

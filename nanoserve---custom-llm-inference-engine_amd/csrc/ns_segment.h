@@ -307,54 +307,37 @@ __device__ __forceinline__ void seg_write_info(int32_t* out_info, int row, int32
   w[4] = n_cand; w[5] = flags; w[6] = (int32_t)__float_as_uint(vstar); w[7] = istar;
 }
 
-// Exact top-k (ties kept), top-p, softmax and inverse-CDF draw over n <= 64*R
-// survivors, run by one wave.  list[i] = (float bits << 32) | token id where the
-// float is a logit after the penalty; it is scaled here by the row's temperature
-// (tdiv, rdiv = RN(1/tdiv)); pass tdiv = rdiv = 1 for values already scaled.
-// Every survivor is >= the row's k-th largest scaled value and the row maximum
-// is among them.
+// Element i = r*64 + l of a wave's register rows, r and l wave-uniform, read through
+// scalar registers (a select over a[r] would become a dynamically indexed array).
 template <int R>
-__device__ void wave_finalize(const uint64_t* list, int n, int k, bool topp_on, float p32, float tdiv, float rdiv,
-                              float u, int row, int64_t* out_ids, float* out_probs, int64_t V, int32_t* out_info,
-                              int32_t flags, int32_t n_cand, int32_t path) {
-  const int lane = lane_id();
-  uint64_t a[R];
+__device__ __forceinline__ uint64_t wave_elem(const uint64_t (&a)[R], int i) {
+  const int rr = i >> 6, l = i & 63;
+  uint64_t x = read_lane(a[0], l);
 #pragma unroll
-  for (int r = 0; r < R; ++r) {
-    const int i = r * 64 + lane;
-    a[r] = ~0ull;
-    if (i < n) {
-      const uint64_t e = list[i];
-      a[r] = desc_key(div_rn(__uint_as_float((uint32_t)(e >> 32)), tdiv, rdiv), (uint32_t)e);
-    }
+  for (int r = 1; r < R; ++r) {
+    const uint64_t t = read_lane(a[r], l);
+    x = r == rr ? t : x;
   }
-  wave_sort_u64<R>(a);   // value descending, token id ascending
-  const float M = desc_key_val(read_lane(a[0], 0));   // the row maximum
+  return x;
+}
 
-  // top-k threshold: the k-th largest (sampler.py:56-58); every value >= it is kept
-  float thr = -__builtin_inff();
-  if (n >= k) {
-    const int rk = (k - 1) >> 6, lk = (k - 1) & 63;
-    uint64_t sel = a[0];
-#pragma unroll
-    for (int r = 1; r < R; ++r) sel = (r == rk) ? a[r] : sel;
-    thr = desc_key_val(read_lane(sel, lk));
-  }
-  float y[R];
-  int nk = 0;
-#pragma unroll
-  for (int r = 0; r < R; ++r) {
-    const int i = r * 64 + lane;
-    y[r] = i < n ? desc_key_val(a[r]) : -__builtin_inff();
-    nk += __popcll(ballot(i < n && y[r] >= thr));
-  }
+// Top-p, softmax and inverse-CDF draw by one wave over the nk survivors of the
+// top-k cut, given in a[] (element i = r*64 + lane) in sorted order: scaled value
+// descending, token id ascending.  M is the row maximum and thr the k-th largest
+// value (-inf when fewer than k candidates); entries at i >= nk are ignored.
+template <int R>
+__device__ __forceinline__ void wave_select_draw(const uint64_t (&a)[R], int nk, float M, float thr, bool topp_on,
+                                                 float p32, float u, int row, int64_t* out_ids, float* out_probs,
+                                                 int64_t V, int32_t* out_info, int32_t flags, int32_t n_cand,
+                                                 int32_t path) {
+  const int lane = lane_id();
   // softmax numerators over the kept prefix (sampler.py:65 / :76)
   float ev[R];
   double es[R];
 #pragma unroll
   for (int r = 0; r < R; ++r) {
     const int i = r * 64 + lane;
-    ev[r] = i < nk ? ns_expf(y[r] - M) : 0.0f;
+    ev[r] = i < nk ? ns_expf(desc_key_val(a[r]) - M) : 0.0f;
     es[r] = (double)ev[r];
   }
   int nf = nk;
@@ -377,11 +360,7 @@ __device__ void wave_finalize(const uint64_t* list, int n, int k, bool topp_on, 
       if (m != 0ull) J = r * 64 + __builtin_ctzll(m);
     }
     if (J >= 0) nf = J + 1;
-    const int rj = (nf - 1) >> 6, lj = (nf - 1) & 63;
-    uint64_t sel = a[0];
-#pragma unroll
-    for (int r = 1; r < R; ++r) sel = (r == rj) ? a[r] : sel;
-    const uint64_t kc = read_lane(sel, lj);
+    const uint64_t kc = wave_elem<R>(a, nf - 1);
     vstar = desc_key_val(kc);
     istar = (int32_t)desc_key_id(kc);
   }
@@ -427,11 +406,7 @@ __device__ void wave_finalize(const uint64_t* list, int n, int k, bool topp_on, 
   int32_t fl = flags;
   if (pick < 0) { pick = lastpos >= 0 ? lastpos : 0; fl |= FLAG_LOCATE_FALLBACK; }
   {
-    const int rp = pick >> 6, lp = pick & 63;
-    uint64_t sel = b[0];
-#pragma unroll
-    for (int r = 1; r < R; ++r) sel = (r == rp) ? b[r] : sel;
-    const uint64_t kb = read_lane(sel, lp);
+    const uint64_t kb = wave_elem<R>(b, pick);
     if (lane == 0) {
       out_ids[row] = (int64_t)(kb >> 32);
       seg_write_info(out_info, row, path, nf, thr, nk, n_cand, fl, vstar, istar);
@@ -445,6 +420,121 @@ __device__ void wave_finalize(const uint64_t* list, int n, int k, bool topp_on, 
       if (i < nf) pr[b[r] >> 32] = __uint_as_float((uint32_t)b[r]);
     }
   }
+}
+
+// Exact top-k (ties kept), top-p, softmax and inverse-CDF draw over n <= 64*R
+// survivors, run by one wave.  list[i] = (float bits << 32) | token id where the
+// float is a logit after the penalty; it is scaled here by the row's temperature
+// (tdiv, rdiv = RN(1/tdiv)); pass tdiv = rdiv = 1 for values already scaled.
+// Every survivor is >= the row's k-th largest scaled value and the row maximum
+// is among them.
+template <int R>
+__device__ void wave_finalize(const uint64_t* list, int n, int k, bool topp_on, float p32, float tdiv, float rdiv,
+                              float u, int row, int64_t* out_ids, float* out_probs, int64_t V, int32_t* out_info,
+                              int32_t flags, int32_t n_cand, int32_t path) {
+  const int lane = lane_id();
+  uint64_t a[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const int i = r * 64 + lane;
+    a[r] = ~0ull;
+    if (i < n) {
+      const uint64_t e = list[i];
+      a[r] = desc_key(div_rn(__uint_as_float((uint32_t)(e >> 32)), tdiv, rdiv), (uint32_t)e);
+    }
+  }
+  wave_sort_u64<R>(a);   // value descending, token id ascending
+  const float M = desc_key_val(read_lane(a[0], 0));   // the row maximum
+
+  // top-k threshold: the k-th largest (sampler.py:56-58); every value >= it is kept
+  float thr = -__builtin_inff();
+  if (n >= k) {
+    thr = desc_key_val(wave_elem<R>(a, k - 1));
+  }
+  int nk = 0;
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const int i = r * 64 + lane;
+    nk += __popcll(ballot(i < n && desc_key_val(a[r]) >= thr));
+  }
+  wave_select_draw<R>(a, nk, M, thr, topp_on, p32, u, row, out_ids, out_probs, V, out_info, flags, n_cand, path);
+}
+
+// Tail of the workgroup finaliser: wave 0 loads the first nk sorted keys from LDS.
+template <int R>
+__device__ void wave_select_draw_lds(const uint64_t* sorted, int nk, float M, float thr, bool topp_on, float p32,
+                                     float u, int row, int64_t* out_ids, float* out_probs, int64_t V,
+                                     int32_t* out_info, int32_t flags, int32_t n_cand, int32_t path) {
+  const int lane = lane_id();
+  uint64_t a[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const int i = r * 64 + lane;
+    a[r] = i < nk ? sorted[i] : ~0ull;
+  }
+  wave_select_draw<R>(a, nk, M, thr, topp_on, p32, u, row, out_ids, out_probs, V, out_info, flags, n_cand, path);
+}
+
+// The same selection and draw as wave_finalize over n <= WAVE_CAP survivors, with the
+// ordering done by the whole workgroup (nthreads threads, all of which must call it):
+// each survivor's position is the number of keys that precede it, counted in
+// parallel slices and summed with LDS atomics, then the keys are scattered in
+// place.  list (>= WAVE_CAP + WAVE_CAP / 2 entries of LDS) is overwritten: its
+// first n entries end up sorted and rank counters live behind them.  Wave 0 then
+// runs the top-p / softmax / draw over the top-k prefix only.
+template <int NTH>
+__device__ __forceinline__ void block_finalize(uint64_t* list, int n, int k, bool topp_on, float p32, float tdiv,
+                                               float rdiv, float u, int row, int64_t* out_ids, float* out_probs,
+                                               int64_t V, int32_t* out_info, int32_t flags, int32_t n_cand,
+                                               int32_t path) {
+  static_assert(NTH % 256 == 0, "rank slices assume whole groups of 256 threads");
+  const int tid = threadIdx.x;
+  int32_t* rank = reinterpret_cast<int32_t*>(list + WAVE_CAP);
+  uint64_t key = ~0ull;
+  if (tid < n) {
+    const uint64_t e = list[tid];
+    key = desc_key(div_rn(__uint_as_float((uint32_t)(e >> 32)), tdiv, rdiv), (uint32_t)e);
+  }
+  __syncthreads();   // every entry read before it is overwritten
+  if (tid < n) list[tid] = key;
+  if (tid < WAVE_CAP) rank[tid] = 0;
+  __syncthreads();
+  {
+    // element i = tid % NI against the keys of slice tid / NI (slices are wave-uniform)
+    const int NI = n <= 64 ? 64 : (n <= 128 ? 128 : 256);
+    const int parts = NTH / NI;
+    const int i = tid & (NI - 1), part = tid / NI;
+    const int per = (n + parts - 1) / parts;
+    const int j0 = part * per;
+    const int j1 = j0 + per < n ? j0 + per : n;
+    if (i < n) {
+      const uint64_t ki = list[i];
+      int c = 0;
+      for (int j = j0; j < j1; ++j) c += list[j] < ki ? 1 : 0;
+      if (c != 0) atomicAdd(&rank[i], c);
+    }
+  }
+  __syncthreads();   // all counts in, all reads of the unsorted keys done
+  if (tid < n) list[rank[tid]] = key;
+  __syncthreads();
+  if (tid >= 64) return;
+  const float M = desc_key_val(list[0]);   // the row maximum
+  // top-k threshold: the k-th largest (sampler.py:56-58); every value >= it is kept
+  const float thr = n >= k ? desc_key_val(list[k - 1]) : -__builtin_inff();
+  int nk = 0;
+  for (int base = 0; base < n; base += 64) {
+    const int i = base + tid;
+    nk += __popcll(ballot(i < n && desc_key_val(list[i < n ? i : 0]) >= thr));
+  }
+  if (nk <= 64)
+    wave_select_draw_lds<1>(list, nk, M, thr, topp_on, p32, u, row, out_ids, out_probs, V, out_info, flags, n_cand,
+                            path);
+  else if (nk <= 128)
+    wave_select_draw_lds<2>(list, nk, M, thr, topp_on, p32, u, row, out_ids, out_probs, V, out_info, flags, n_cand,
+                            path);
+  else
+    wave_select_draw_lds<4>(list, nk, M, thr, topp_on, p32, u, row, out_ids, out_probs, V, out_info, flags, n_cand,
+                            path);
 }
 
 // Wave-aggregated append of one candidate (scaled value y, token id) to the
