@@ -1,22 +1,23 @@
 // gfx950 row streaming path of the one-workgroup-per-row kernel: greedy rows
 // and top-k rows with k <= KFAST whose whole row fits in the workgroup's
 // registers (RCPT 16-byte chunks per thread: bf16 rows up to 131072 tokens,
-// fp32 rows up to 65536).  sampler.py:31-89 for those rows, with one HBM round
-// trip per row and no exchange between workgroups:
-//   * the history ids are loaded first, then every chunk of the row (chunk
-//     q*NT + t to thread t), so the history bitmap (set semantics,
-//     sampler.py:34-38) is built while the row is still arriving;
-//   * per element only a NaN-propagating chunk maximum is computed, chunk by
-//     chunk as the loads land; the unique history positions are gathered and
-//     penalized as extra elements, and chunks holding one are no threshold source;
-//   * greedy rows: masked maximum and its first index (sampler.py:82-83);
-//   * top-k rows: a lower bound of the k-th largest from the 4 largest thread
-//     values of every wave (64 values of distinct elements, k-th largest of
-//     them), the elements of the chunks reaching it taken from registers into
-//     an LDS list, ordered by the whole workgroup (rank counting), then the
-//     one-wave top-p / softmax / draw over the top-k prefix.
-// Rows whose candidate list outgrows the one-wave capacity (huge tie groups) are
-// redone by the general per-row code.
+// fp32 rows up to 65536).  sampler.py:31-89 for those rows, with one HBM pass
+// over the row and no exchange between workgroups.
+//   * Greedy rows: the history (bitmap, unique ids) first, then the row; masked
+//     maximum and its first index (sampler.py:82-83).
+//   * Top-k rows with a penalty >= 1 (or none): every chunk of the row is
+//     requested at once (chunk q*NT + t to thread t), the history ids behind it.
+//     Such a penalty never raises a value and keeps NaN / +inf, so the row is
+//     processed raw: a lower bound of the k-th largest comes from the first half
+//     of the chunks (the k-th largest of the RF_J largest thread values of every
+//     wave), then the chunks reaching it are staged in LDS as the second half
+//     lands and expanded into a candidate list.  After the stream the history
+//     bitmap is built, the candidates at history positions are penalized, and a
+//     count check confirms the list still covers the top-k.  The list is ordered
+//     by the whole workgroup (rank counting) and one wave runs top-p, softmax
+//     and the draw over the top-k prefix.
+// Rows outside these cases (penalty < 1, huge tie groups, too many staged chunks,
+// a failed coverage check) are left to the general per-row code.
 #pragma once
 
 #include "ns_segment.h"
@@ -26,8 +27,15 @@ namespace ns {
 constexpr int RCPT = 16;               // chunks per thread: the whole row in flight
 constexpr int RF_J = 4;                // largest thread values per wave feeding the bound (RF_J * NWAVE >= KFAST)
 constexpr int RHB = 2;                 // history ids per thread per batch
+// LDS staging of the chunks that reach the bound, inside the candidate region (u64
+// units): the list and its rank counters use the first WAVE_CAP * 3 / 2 entries
+constexpr int HIT_PER_WAVE = 48;                               // chunk slots per wave
+constexpr int HIT_OFF64 = 512;                                 // 16-byte chunks
+constexpr int HIT_IDX_OFF64 = HIT_OFF64 + HIT_PER_WAVE * NWAVE * 2;   // chunk indices
+constexpr int HIT_CNT_OFF64 = HIT_IDX_OFF64 + HIT_PER_WAVE * NWAVE / 2;   // per-wave counts
 static_assert(RF_J * NWAVE == 64, "the bound is selected from one value per lane of wave 0");
 static_assert(KFAST <= RF_J * NWAVE, "k-th largest of the per-wave values");
+static_assert(WAVE_CAP * 3 / 2 <= HIT_OFF64 && HIT_CNT_OFF64 + NWAVE / 2 <= CAP, "candidate region layout");
 
 // An opaque copy of a chunk: values derived from it are recomputed rather than
 // kept alive from an earlier pass (the row's registers leave no room for them).
@@ -59,6 +67,51 @@ __device__ __forceinline__ void cand_push(bool take, float x, uint32_t id, uint6
   if (take && pos < CAP) cand[pos] = ((uint64_t)__float_as_uint(x) << 32) | id;
 }
 
+// Raw bits of token id's value (one element) through a buffer descriptor over the row;
+// ids outside the descriptor read 0.
+template <typename T>
+__device__ __forceinline__ uint32_t gather_raw(__amdgpu_buffer_rsrc_t r, int32_t id) {
+  if constexpr (T::SZ == 2) return (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(r, (int)((uint32_t)id * 2u), 0, 0);
+  else return __builtin_amdgcn_raw_buffer_load_b32(r, (int)((uint32_t)id * 4u), 0, 0);
+}
+template <typename T>
+__device__ __forceinline__ float raw_float(uint32_t b) {
+  if constexpr (T::SZ == 2) return __uint_as_float(b << 16);
+  else return __uint_as_float(b);
+}
+
+// One batch of history ids (NB per thread, id j = base + s*NT + thread): presence bits
+// in the LDS bitmap, first occurrences appended to the unique list.  Returns whether
+// this thread saw an id outside [0, V).
+template <int NB>
+__device__ __forceinline__ bool hist_batch(const int32_t (&ids)[NB], int base, int H, int64_t V, uint32_t* bm,
+                                           int32_t* xl_id, Misc* misc) {
+  const int tid = threadIdx.x;
+  const int lane = lane_id();
+  bool bad = false;
+#pragma unroll
+  for (int s = 0; s < NB; ++s) {
+    const int32_t id = ids[s];
+    bool uniq = false;
+    if (base + s * NT + tid < H) {
+      if (id < 0 || (int64_t)id >= V) {
+        bad = true;
+      } else {
+        const uint32_t bit = 1u << (id & 31);
+        uniq = (atomicOr(&bm[id >> 5], bit) & bit) == 0u;
+      }
+    }
+    const uint64_t m = ballot(uniq);
+    if (m != 0ull) {
+      int wb = 0;
+      if (lane == 0) wb = atomicAdd(&misc->xl_n, __popcll(m));
+      wb = read_lane(wb, 0);
+      if (uniq) xl_id[wb + lanes_below(m)] = id;
+    }
+  }
+  return bad;
+}
+
 template <typename T>
 __host__ __device__ __forceinline__ bool row_fits(int64_t V) {
   return (V + T::EPC - 1) / T::EPC <= (int64_t)NT * RCPT;
@@ -76,8 +129,9 @@ struct RowArgs {
   int32_t* out_info;
 };
 
-// Returns 0 when the row is resolved, 1 when its candidate set outgrows the one-wave
-// capacity (huge tie groups); the caller then runs the general per-row code.
+// Returns 0 when the row is resolved, 1 when it is left to the general per-row code:
+// top-k rows with a penalty below 1, candidate sets beyond WAVE_CAP (huge tie groups),
+// or penalized candidate sets that no longer cover the top-k.
 template <typename T>
 __device__ __forceinline__ int row_fast(const RowArgs P, const int row, const int64_t src, const float temp,
                                         const int32_t k, const float topp, const float pen, const float u,
@@ -105,126 +159,99 @@ __device__ __forceinline__ int row_fast(const RowArgs P, const int row, const in
   int32_t* is = reinterpret_cast<int32_t*>(&misc->red);
   BlockScratch* red = &misc->red;
 
-  // ---- history first, before the row is requested (a load issued while the row
-  // streams waits behind it): presence bitmap, unique ids (set semantics), and the
-  // gather of the history positions' values
-  int U = 0;
-  if (pen_on) {
-    const int nbw = (int)((V + 31) / 32);
-    for (int i = tid; i < nbw; i += NT) bm[i] = 0u;
-    if (tid == 0) { misc->xl_n = 0; misc->flags = 0; }
-    __syncthreads();
-    const int32_t* hp = P.hist_ids + h0;
-    bool bad = false;
-    for (int base = 0; base < H; base += RHB * NT) {
-      int32_t hid[RHB];
-#pragma unroll
-      for (int s = 0; s < RHB; ++s) {
-        const int j = base + s * NT + tid;
-        hid[s] = j < H ? hp[j] : 0;
-      }
-#pragma unroll
-      for (int s = 0; s < RHB; ++s) {
-        const int32_t id = hid[s];
-        bool uniq = false;
-        if (base + s * NT + tid < H) {
-          if (id < 0 || (int64_t)id >= V) {
-            bad = true;
-          } else {
-            const uint32_t bit = 1u << (id & 31);
-            uniq = (atomicOr(&bm[id >> 5], bit) & bit) == 0u;
-          }
-        }
-        const uint64_t m = ballot(uniq);
-        if (m != 0ull) {
-          int wb = 0;
-          if (lane == 0) wb = atomicAdd(&misc->xl_n, __popcll(m));
-          wb = read_lane(wb, 0);
-          if (uniq) xl_id[wb + lanes_below(m)] = id;
-        }
-      }
+  const int32_t* hp = P.hist_ids + h0;
+  const int nbw = (int)((V + 31) / 32);
+  const int nf = (int)nfull;
+  const RowOut o{P.out_ids, P.out_probs, P.out_info, row, V};
+  auto uniform_row = [&](float Mrep) {
+    const float qv = (float)(1.0 / (double)V);
+    if (tid == 0) {
+      const double qd = qv, ud = u;
+      int64_t i = (int64_t)(ud / qd);
+      while (i > 0 && (double)i * qd > ud) --i;
+      while ((double)(i + 1) * qd <= ud && i < V) ++i;
+      if (i >= V) i = V - 1;
+      P.out_ids[row] = i;
     }
-    if (bad) atomicOr(&misc->flags, FLAG_BAD_HIST_ID);
+    write_info(o, PATH_UNIFORM, (int32_t)V, -__builtin_inff(), (int32_t)V, 0, flags, Mrep, -1);
+    if (P.out_probs != nullptr) {
+      float* pr = P.out_probs + (int64_t)row * V;
+      for (int64_t i = tid; i < V; i += NT) pr[i] = qv;
+    }
+  };
+  // top-k rows with a penalty below 1 (or not finite) are left to the general code,
+  // before anything touches LDS
+  if (!greedy && pen_on && !(pen > 1.0f && pen <= 3.40282347e38f)) return 1;
+  if (tid == 0) { misc->xl_n = 0; misc->flags = 0; misc->cand_n = 0; }
+
+  if (greedy) {
+    // ---- greedy rows: masked maximum and its first index (NaN counts as the max,
+    // sampler.py:82-83, 88).  The history comes first (bitmap and unique ids, set
+    // semantics, sampler.py:34-38): requests issued behind the row would be served
+    // after it.
+    int U = 0;
+    if (pen_on) {
+      for (int i = tid; i < nbw; i += NT) bm[i] = 0u;
+      __syncthreads();
+      bool bad = false;
+      for (int base = 0; base < H; base += RHB * NT) {
+        int32_t ids[RHB];
+#pragma unroll
+        for (int s = 0; s < RHB; ++s) {
+          const int j = base + s * NT + tid;
+          ids[s] = j < H ? hp[j] : 0;
+        }
+        bad |= hist_batch<RHB>(ids, base, H, V, bm, xl_id, misc);
+      }
+      if (bad) atomicOr(&misc->flags, FLAG_BAD_HIST_ID);
+    }
     __syncthreads();
     flags |= misc->flags;
     U = misc->xl_n;
-  }
-  const float x0 = tid < U ? T::load1(rowp, xl_id[tid]) : 0.0f;   // first NT history values
-
-  // ---- the whole row in flight: buffer loads over the row's full chunks (chunk q*NT + t to
-  // thread t); chunks at or past the last full one read zeros and are never used
-  const int nf = (int)nfull;
-  uint4 v[RCPT];
-  {
-    const __amdgpu_buffer_rsrc_t rs = make_rsrc(rowp, (uint32_t)nf * 16u);
+    uint4 v[RCPT];
+    {
 #pragma unroll
-    for (int q = 0; q < RCPT; ++q) v[q] = buf_load16(rs, (uint32_t)tid * 16u, (uint32_t)(q * NT * 16));
-  }
-
-  // ---- chunk maxima as the loads land (kept: the candidate pass compares them with the
-  // bound); threshold sources skip chunks holding history positions
-  uint32_t cmp[RCPT / 2];            // chunk maxima (greedy rows: masked), bfloat16 upper bounds
-  float tval = -__builtin_inff();
-  float gm = -__builtin_inff();      // greedy rows: NaN-propagating masked maximum
-  bool nanf = false, pinf = false;
-#pragma unroll
-  for (int q = 0; q < RCPT; ++q) {
-    const int c = q * NT + tid;
-    float cmq = chunk_max<T>(v[q]);
-    if ((q + 1) * NT > nf && c >= nf) cmq = -__builtin_inff();   // past the last full chunk
-    const uint32_t hb = (pen_on && c < nf) ? T::bits(bm, c) : 0u;
-    if (hb == 0u) tval = __builtin_fmaxf(tval, cmq);
-    else if (greedy) cmq = chunk_max<T>(T::mask(v[q], hb));      // greedy rows: exact masked chunk max
-    if (greedy) gm = fmax_nan(gm, cmq);
-    if (q & 1) cmp[q >> 1] |= bf16_up(cmq) << 16;
-    else cmp[q >> 1] = bf16_up(cmq);
-    if (!(cmq <= 3.40282347e38f) && cmq != -__builtin_inff()) {   // NaN or +inf in the chunk (rare)
-#pragma unroll
-      for (int e = 0; e < EPC; ++e) {
-        const float x = T::elem(v[q], e);
-        if (!((hb >> e) & 1u)) { nanf |= x != x; pinf |= x == __builtin_inff(); }
-      }
+      for (int q = 0; q < RCPT; ++q)
+        v[q] = buf_load16_at(rowp, (uint32_t)nf * 16u, (uint32_t)(q * NT * 16), (uint32_t)tid * 16u);
     }
-  }
-  // penalized history values: kept in LDS (xl_val), folded into the thread's value
-  float xmax = -__builtin_inff();   // NaN-propagating max of this thread's extra values
-  for (int i = tid; i < U; i += NT) {
-    const float pv = pen_val(i == tid ? x0 : T::load1(rowp, xl_id[i]));
-    xl_val[i] = pv;
-    xmax = fmax_nan(xmax, pv);
-    tval = __builtin_fmaxf(tval, pv);
-    nanf |= pv != pv;
-    pinf |= pv == __builtin_inff();
-  }
-  // tokens past the last full chunk (V not a multiple of EPC) join the extras, raw
-  if (nfull < nchunks) {
-    if (tid == 0) misc->xl_n = U;
-    __syncthreads();
-    if (wid == 0) {
-      const int ntail = (int)(V - nfull * EPC);
-      const int64_t id = nfull * EPC + lane;
-      const bool act = lane < ntail;
-      const bool inhist = act && pen_on && ((bm[id >> 5] >> (id & 31)) & 1u);
-      const bool take = act && !inhist;
-      const float x = take ? T::load1(rowp, id) : -__builtin_inff();
-      const uint64_t m = ballot(take);
-      if (take) { xl_id[U + lanes_below(m)] = (int32_t)id; xl_val[U + lanes_below(m)] = x; }
-      if (lane == 0) misc->xl_n = U + __popcll(m);
-      if (take) {
-        xmax = fmax_nan(xmax, x);
-        tval = __builtin_fmaxf(tval, x);
-        nanf |= x != x;
-        pinf |= x == __builtin_inff();
-      }
+    // the first NT history positions' values: raw bits, converted after the row
+    const __amdgpu_buffer_rsrc_t rrow = make_rsrc(rowp, (uint32_t)(V * T::SZ));
+    const uint32_t x0raw = gather_raw<T>(rrow, U > 0 ? xl_id[tid < U ? tid : 0] : 0);
+    uint32_t cmp[RCPT / 2];   // bfloat16 upper bounds of the masked chunk maxima
+    float gm = -__builtin_inff();
+#pragma unroll
+    for (int q = 0; q < RCPT; ++q) {
+      const int c = q * NT + tid;
+      const uint32_t hb = (pen_on && c < nf) ? T::bits(bm, c) : 0u;
+      float cmq = chunk_max<T>(hb != 0u ? T::mask(v[q], hb) : v[q]);
+      if ((q + 1) * NT > nf && c >= nf) cmq = -__builtin_inff();   // past the last full chunk
+      gm = fmax_nan(gm, cmq);
+      if (q & 1) cmp[q >> 1] |= bf16_up(cmq) << 16;
+      else cmp[q >> 1] = bf16_up(cmq);
     }
-    __syncthreads();
-    U = misc->xl_n;
-  }
-  const RowOut o{P.out_ids, P.out_probs, P.out_info, row, V};
-
-  if (greedy) {
-    // masked maximum and its first index (NaN counts as the max, sampler.py:82-83, 88)
-    gm = fmax_nan(gm, xmax);
+    for (int i = tid; i < U; i += NT) {
+      const float pv = pen_val(i == tid ? raw_float<T>(x0raw) : T::load1(rowp, xl_id[i]));
+      xl_val[i] = pv;
+      gm = fmax_nan(gm, pv);
+    }
+    // tokens past the last full chunk (V not a multiple of EPC) join the extras, raw
+    if (nfull < nchunks) {
+      __syncthreads();
+      if (wid == 0) {
+        const int ntail = (int)(V - nfull * EPC);
+        const int64_t id = nfull * EPC + lane;
+        const bool act = lane < ntail;
+        const bool inhist = act && pen_on && ((bm[id >> 5] >> (id & 31)) & 1u);
+        const bool take = act && !inhist;
+        const float x = take ? T::load1(rowp, id) : -__builtin_inff();
+        const uint64_t m = ballot(take);
+        if (take) { xl_id[U + lanes_below(m)] = (int32_t)id; xl_val[U + lanes_below(m)] = x; }
+        if (lane == 0) misc->xl_n = U + __popcll(m);
+        if (take) gm = fmax_nan(gm, x);
+      }
+      __syncthreads();
+      U = misc->xl_n;
+    }
     const float Mx = block_max_nan(gm, red);
     const bool nanm = Mx != Mx;
     int64_t gi = INT64_MAX;
@@ -251,103 +278,175 @@ __device__ __forceinline__ int row_fast(const RowArgs P, const int row, const in
     const int64_t best = block_min_i64(gi, red);
     if (tid == 0) P.out_ids[row] = best == INT64_MAX ? 0 : best;
     write_info(o, PATH_GREEDY, 1, -__builtin_inff(), 0, 0, flags, Mx, (int32_t)best);
+    // nothing of this path is left in flight where the top-k path starts (the compiler
+    // merges their exits and would otherwise wait for the row there)
+    __builtin_amdgcn_s_waitcnt(0);
     return 0;
   }
 
-  // ---- NaN / +inf among the penalized logits: the softmax is NaN, uniform 1/V (sampler.py:77-80)
-  {
-    const int wf = (ballot(nanf) != 0ull ? 1 : 0) | (ballot(pinf) != 0ull ? 2 : 0);
-    if (lane == 0) is[wid] = wf;
-  }
-  __syncthreads();
-  int nanfl = 0;
+  // ---- top-k rows with a penalty >= 1 (or none).  Such a penalty never raises a value
+  // and keeps NaN and +inf, so the row is processed raw and the candidates are penalized
+  // at the end.  The history ids are requested behind the row: loads complete in issue
+  // order, and scattered requests are served after the row's streaming ones anyway.
+  uint4 v[RCPT];
 #pragma unroll
-  for (int w = 0; w < NWAVE; ++w) nanfl |= is[w];
-  __syncthreads();
-  auto uniform_row = [&](float Mrep) {
-    const float qv = (float)(1.0 / (double)V);
-    if (tid == 0) {
-      const double qd = qv, ud = u;
-      int64_t i = (int64_t)(ud / qd);
-      while (i > 0 && (double)i * qd > ud) --i;
-      while ((double)(i + 1) * qd <= ud && i < V) ++i;
-      if (i >= V) i = V - 1;
-      P.out_ids[row] = i;
-    }
-    write_info(o, PATH_UNIFORM, (int32_t)V, -__builtin_inff(), (int32_t)V, 0, flags, Mrep, -1);
-    if (P.out_probs != nullptr) {
-      float* pr = P.out_probs + (int64_t)row * V;
-      for (int64_t i = tid; i < V; i += NT) pr[i] = qv;
-    }
-  };
-  if (nanfl != 0) { uniform_row((nanfl & 1) ? __builtin_nanf("") : __builtin_inff()); return 0; }
-
-  // ---- lower bound of the k-th largest: the k-th largest of the RF_J largest thread values of each wave
+  for (int q = 0; q < RCPT; ++q) {
+    // issued in chunk order (loads complete in issue order; the passes below take the
+    // chunks in this order)
+    v[q] = buf_load16_at(rowp, (uint32_t)nf * 16u, (uint32_t)(q * NT * 16), (uint32_t)tid * 16u);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  int32_t hid[RHB];   // unconditional loads (bounds-checked by the descriptor) keep the counts exact
   {
+    const __amdgpu_buffer_rsrc_t rh = make_rsrc(hp, pen_on ? (uint32_t)H * 4u : 0u);
+#pragma unroll
+    for (int s = 0; s < RHB; ++s)
+      hid[s] = (int32_t)__builtin_amdgcn_raw_buffer_load_b32(rh, (int)((uint32_t)(s * NT + tid) * 4u), 0, 0);
+  }
+  if (pen_on)
+    for (int i = tid; i < nbw; i += NT) bm[i] = 0u;
+
+  // lower bound of the k-th largest raw value from the first half of the chunks (values
+  // of distinct elements: the k-th largest of any subset is a lower bound): the k-th
+  // largest of the RF_J largest thread values of each wave.  The barriers wait for LDS
+  // only; the rest of the row stays in flight.
+  constexpr int RH = RCPT / 2;
+  float cm[RH];   // NaN-propagating chunk maxima of the first half (-inf past the full chunks)
+  {
+    float tval = -__builtin_inff();
+#pragma unroll
+    for (int q = 0; q < RH; ++q) {
+      const int c = q * NT + tid;
+      cm[q] = c < nf ? chunk_max<T>(v[q]) : -__builtin_inff();
+      tval = __builtin_fmaxf(tval, cm[q]);
+    }
     const uint32_t key = wave_sort_u32(~fkey(tval));   // descending
     if (lane < RF_J) fs[wid * RF_J + lane] = fkey_inv(~key);
     __syncthreads();
     if (wid == 0) {
       const uint32_t k2 = wave_sort_u32(~fkey(fs[lane]));
       const float taux = fkey_inv(~read_lane(k2, k - 1));
-      if (lane == 0) { fs[64] = taux; misc->cand_n = 0; }
+      if (lane == 0) fs[64] = taux;
     }
     __syncthreads();
   }
   const float taux = fs[64];
   const float tc = lower_preimage(taux, tdiv, rdiv);   // x >= tc  <=>  x / t >= RN(taux / t)
 
-  // ---- candidates x >= tc: chunks whose maximum reaches tc are re-read (L2) two at a time
-  // (the row's registers are free after the chunk pass), then the history positions
-  uint32_t fm = 0u;
+  // chunks whose maximum reaches tc, as the rest of the row lands: the chunk and its index
+  // go to the wave's own LDS slots (no atomics); NaN / +inf only flagged here
+  uint4* hdat = reinterpret_cast<uint4*>(cand + HIT_OFF64) + wid * HIT_PER_WAVE;
+  int32_t* hidx = reinterpret_cast<int32_t*>(cand + HIT_IDX_OFF64) + wid * HIT_PER_WAVE;
+  int32_t* hcnt = reinterpret_cast<int32_t*>(cand + HIT_CNT_OFF64);
+  bool special = false;   // NaN or +inf in a chunk
+  int nh = 0;             // this wave's hit chunks (wave-uniform)
 #pragma unroll
   for (int q = 0; q < RCPT; ++q) {
     const int c = q * NT + tid;
-    fm |= (c < nf && bf16_float((cmp[q >> 1] >> (16 * (q & 1))) & 0xffffu) >= tc) ? (1u << q) : 0u;
-  }
-  {
-    const __amdgpu_buffer_rsrc_t rs = make_rsrc(rowp, (uint32_t)nf * 16u);
-    while (ballot(fm != 0u) != 0ull) {
-      const int qa = fm != 0u ? __builtin_ctz(fm) : -1;
-      fm &= fm - 1u;
-      const int qb = fm != 0u ? __builtin_ctz(fm) : -1;
-      fm &= fm - 1u;
-      const int ca = qa * NT + tid, cb = qb * NT + tid;
-      const uint4 wa = buf_load16(rs, (uint32_t)(qa >= 0 ? ca : 0) * 16u, 0u);
-      const uint4 wb = buf_load16(rs, (uint32_t)(qb >= 0 ? cb : 0) * 16u, 0u);
-      const uint32_t ha = (pen_on && qa >= 0) ? T::bits(bm, ca) : 0u;
-      const uint32_t hb2 = (pen_on && qb >= 0) ? T::bits(bm, cb) : 0u;
-#pragma unroll
-      for (int e = 0; e < EPC; ++e) {
-        const float x = T::elem(wa, e);
-        cand_push(qa >= 0 && !((ha >> e) & 1u) && x >= tc && x > -__builtin_inff(), x, (uint32_t)ca * EPC + e,
-                  cand, misc);
-      }
-#pragma unroll
-      for (int e = 0; e < EPC; ++e) {
-        const float x = T::elem(wb, e);
-        cand_push(qb >= 0 && !((hb2 >> e) & 1u) && x >= tc && x > -__builtin_inff(), x, (uint32_t)cb * EPC + e,
-                  cand, misc);
-      }
+    const float cmq = q < RH ? cm[q] : (c < nf ? chunk_max<T>(v[q]) : -__builtin_inff());
+    special |= !(cmq < __builtin_inff());
+    const bool hit = cmq >= tc;
+    const uint64_t m = ballot(hit);
+    if (m != 0ull) {
+      const int pos = nh + lanes_below(m);
+      if (hit && pos < HIT_PER_WAVE) { hdat[pos] = v[q]; hidx[pos] = c; }
+      nh += __popcll(m);
     }
   }
-  for (int base = 0; base < U; base += NT) {
-    const int i = base + tid;
-    const float x = i < U ? xl_val[i] : -__builtin_inff();
-    const bool t = x >= tc;
-    if (ballot(t) != 0ull) cand_push(t && x > -__builtin_inff(), x, t ? (uint32_t)xl_id[i] : 0u, cand, misc);
+  // the wave's own hit chunks: their elements >= tc into the candidate list, one element
+  // per lane (a wave's LDS accesses complete in order)
+  __builtin_amdgcn_wave_barrier();
+  {
+    const int nhc = nh < HIT_PER_WAVE ? nh : HIT_PER_WAVE;
+    for (int j = lane; j < nhc * EPC; j += 64) {
+      const int slot = j / EPC, e = j % EPC;
+      const float x = T::elem(hdat[slot], e);
+      const bool t = x >= tc && x > -__builtin_inff();
+      if (ballot(t) != 0ull) cand_push(t, x, (uint32_t)(hidx[slot] * EPC + e), cand, misc);
+    }
   }
+  if (lane == 0) hcnt[wid] = nh;
+  // tokens past the last full chunk (V not a multiple of EPC), raw
+  if (nfull < nchunks && wid == 0) {
+    const int ntail = (int)(V - nfull * EPC);
+    const int64_t id = nfull * EPC + lane;
+    const float x = lane < ntail ? T::load1(rowp, id) : -__builtin_inff();
+    special |= !(x < __builtin_inff()) && lane < ntail;
+    const bool t = x >= tc && x > -__builtin_inff();
+    if (ballot(t) != 0ull) cand_push(t, x, (uint32_t)id, cand, misc);
+  }
+  // the history bitmap (set semantics, sampler.py:34-38), from the ids that arrived
+  // while the row streamed
+  if (pen_on) {
+    bool bad = false;
+    for (int base = 0; base < H; base += RHB * NT) {
+#pragma unroll
+      for (int s = 0; s < RHB; ++s) {
+        const int j = base + s * NT + tid;
+        const int32_t id = base == 0 ? hid[s] : (j < H ? hp[j] : 0);
+        if (j < H) {
+          if (id < 0 || (int64_t)id >= V) bad = true;
+          else atomicOr(&bm[id >> 5], 1u << (id & 31));
+        }
+      }
+    }
+    if (bad) atomicOr(&misc->flags, FLAG_BAD_HIST_ID);
+  }
+  if (lane == 0) is[wid] = ballot(special) != 0ull ? 1 : 0;
   __syncthreads();
-  const int n = misc->cand_n;
-  if (n == 0) { uniform_row(-__builtin_inff()); return 0; }   // every logit -inf
-  if (n <= WAVE_CAP) {
-    zero_probs(o);
-    block_finalize<NT>(cand, n, k, topp < 1.0f, topp, tdiv, rdiv, u, row, P.out_ids, P.out_probs, V, P.out_info,
-                       flags, n, PATH_WAVE_SET);
+  int spec = 0, over = 0;
+#pragma unroll
+  for (int w = 0; w < NWAVE; ++w) {
+    spec |= is[w];
+    over |= hcnt[w] > HIT_PER_WAVE ? 1 : 0;
+  }
+  flags |= misc->flags;
+  if (spec != 0) {
+    // NaN / +inf among the logits (the penalty keeps both): the softmax is NaN, uniform
+    // 1/V (sampler.py:77-80).  Rare: the row is read again to tell NaN from +inf.
+    bool nanf = false;
+    for (int c = tid; c < nf; c += NT) {
+      const uint4 w = rowv[c];
+#pragma unroll
+      for (int e = 0; e < EPC; ++e) nanf |= T::elem(w, e) != T::elem(w, e);
+    }
+    if (wid == 0 && nfull < nchunks) {
+      const int ntail = (int)(V - nfull * EPC);
+      const float x = lane < ntail ? T::load1(rowp, nfull * EPC + lane) : 0.0f;
+      nanf |= x != x;
+    }
+    const int anynan = block_max_i64(nanf ? 1 : 0, red) != 0;
+    uniform_row(anynan ? __builtin_nanf("") : __builtin_inff());
     return 0;
   }
-  __syncthreads();   // every thread has read the candidate count before the caller reuses LDS
-  return 1;
+  if (over != 0) { __syncthreads(); return 1; }
+  const int n = misc->cand_n;
+  if (n == 0) { uniform_row(-__builtin_inff()); return 0; }   // every logit -inf
+  if (n > WAVE_CAP) { __syncthreads(); return 1; }
+  if (pen_on) {
+    // penalize the candidates at history positions (sampler.py:37); the list still holds
+    // the whole top-k if at least k of them stay >= tc: every element outside it is < tc
+    bool ok = false;
+    if (tid < n) {
+      const uint64_t e = cand[tid];
+      const uint32_t id = (uint32_t)e;
+      float x = __uint_as_float((uint32_t)(e >> 32));
+      if ((bm[id >> 5] >> (id & 31)) & 1u) {
+        x = pen_val(x);
+        cand[tid] = ((uint64_t)__float_as_uint(x) << 32) | id;
+      }
+      ok = x >= tc;
+    }
+    const int nok = __popcll(ballot(ok));
+    if (lane == 0 && nok != 0) atomicAdd(&misc->xl_n, nok);
+    __syncthreads();
+    if (misc->xl_n < k && tc > -__builtin_inff()) { __syncthreads(); return 1; }
+  }
+  zero_probs(o);
+  block_finalize<NT>(cand, n, k, topp < 1.0f, topp, tdiv, rdiv, u, row, P.out_ids, P.out_probs, V, P.out_info,
+                     flags, n, PATH_WAVE_SET);
+  return 0;
 }
+
 
 }  // namespace ns

@@ -591,10 +591,10 @@ __global__ __launch_bounds__(SNT) __attribute__((amdgpu_waves_per_eu(4))) void s
   {
     // buffer loads over the row's full chunks: chunks past them read zero and are
     // replaced when first used
-    const __amdgpu_buffer_rsrc_t rs = make_rsrc(rowp, (uint32_t)((V / EPC) * 16));
+    const uint32_t nbytes = (uint32_t)((V / EPC) * 16);
 #pragma unroll
     for (int q = 0; q < SCPT; ++q)
-      v[q] = buf_load16(rs, (uint32_t)tid * 16u, (uint32_t)((c0 + q * SNT) * 16));
+      v[q] = buf_load16_at(rowp, nbytes, (uint32_t)((c0 + q * SNT) * 16), (uint32_t)tid * 16u);
   }
   // chunks past the row's full chunks: -inf, and the chunk holding the last tokens
   // when V is not a multiple of EPC (its own register); replaced when first used
