@@ -36,6 +36,8 @@ PKG = "nanoserve---custom-llm-inference-engine_amd"
 
 HBM_PEAK_GBS = 8000.0
 ROTATE = 8
+# rocprofv3 FETCH_SIZE + WRITE_SIZE summary of this workload (copy-calibrated HBM bytes per launch)
+PMC_SUMMARY = os.path.join(ROOT, "profiles", "sample_kernel_decode_b256_v128256_bf16_pmc.md")
 WORKLOAD_CFG = 2
 METRIC = "sampled rows/sec at B=256, V=128256 fp32; achieved HBM GB/s vs peak"
 
@@ -101,6 +103,18 @@ def make_args(L, st, ws):
     a.workspace = ws.data_ptr()
     a.workspace_bytes = ws.numel()
     return a
+
+
+def measured_traffic():
+    """HBM bytes per launch from the committed rocprofv3 counter summary, or None."""
+    try:
+        with open(PMC_SUMMARY) as f:
+            for line in f:
+                if line.startswith("traffic_bytes_per_launch:"):
+                    return int(line.split(":", 1)[1])
+    except OSError:
+        pass
+    return None
 
 
 def cpu_baseline(w, rows: int, reps: int):
@@ -231,7 +245,7 @@ def main(argv=None):
                    "batch": w.batch, "vocab": w.vocab, "history": 2048, "rotating_input_sets": ROTATE,
                    "parallelism": "single GPU"},
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": achieved / HBM_PEAK_GBS, "traffic": None},
+                     "frac": achieved / HBM_PEAK_GBS, "traffic": measured_traffic()},
         "cpu_baseline": cpu,
         "extra": {"algorithmic_bytes_per_call": bytes_per_call, "kernel_us": ms_per_step * 1e3,
                   "wall_s": wall, "wrapper_inclusive_ms": wrap_ms,

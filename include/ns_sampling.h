@@ -43,10 +43,11 @@ extern "C" {
 #define NS_MAX_VOCAB 262144     /* vocab limit (LDS presence bitmap of vocab/8 bytes) */
 #define NS_MAX_HISTORY 8192     /* per-row history limit (the reference's max_model_len, config.py:52) */
 #define NS_INFO_WORDS 8         /* int32 words per row in out_info */
+#define NS_SEG_MAX_ROWS 16384   /* most rows a segmented call takes (AUTO switches to per-row above) */
 
 /* Per-row diagnostics written to out_info[row * NS_INFO_WORDS + w]:
  *   w=0 path (1 greedy, 2 uniform/NaN guard, 3 top-k set, 4 generic set, 5 large draw,
- *       6 segmented top-k, 9 error)
+ *       6 top-k set ordered and drawn by the streaming or segmented kernels, 9 error)
  *   w=1 tokens kept after top-k and top-p
  *   w=2 float32 bits of the top-k threshold in scaled logits (-inf when top-k is off)
  *   w=3 tokens kept after top-k
@@ -81,9 +82,10 @@ typedef struct ns_sample_args {
                                    are not written.  Debug/parity output, not part of the timed path. */
   int32_t*       out_info;      /* [B, NS_INFO_WORDS] per-row diagnostics, or NULL */
   void*          workspace;     /* device scratch of ns_sample_workspace_bytes() bytes, 256-byte aligned,
-                                   zero-filled before its first use (the library leaves its counters at
-                                   zero after every call); one workspace per stream.  NULL: every row
-                                   takes the one-workgroup-per-row kernel. */
+                                   zero-filled before its first use; calls of any shape may share it (the
+                                   library leaves its persistent counters at zero after every call), one
+                                   call at a time (one stream).  NULL: every row takes the
+                                   one-workgroup-per-row kernel.  Only read in segmented mode. */
   uint64_t       workspace_bytes;
   int32_t        mode;          /* NS_MODE_*: which kernels resolve which rows (results are identical) */
 } ns_sample_args;

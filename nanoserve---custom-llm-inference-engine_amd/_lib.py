@@ -134,6 +134,29 @@ def _ptr(t) -> int:
     return 0 if t is None else int(t.data_ptr())
 
 
+def aligned_rows(logits, sample_idx):
+    """``(logits, sample_idx)`` with every row starting on a 16-byte boundary.
+
+    The kernels read rows in 16-byte chunks, so the C ABI rejects misaligned
+    rows (NS_ERR_ALIGN).  Vocabularies whose row size is not a multiple of 16
+    bytes (an odd fp32 vocab such as 50257) and misaligned views are copied
+    here into rows padded to a multiple of 16 bytes: only the sampled rows
+    when ``sample_idx`` is given (which then becomes the identity).  Aligned
+    inputs, every vocab used by the benchmarks among them, are passed through.
+    """
+    import torch
+
+    esz = logits.element_size()
+    if logits.data_ptr() % 16 == 0 and (logits.stride(0) * esz) % 16 == 0:
+        return logits, sample_idx
+    rows = logits if sample_idx is None else logits.index_select(0, sample_idx.to(torch.int64))
+    V = int(rows.shape[1])
+    per = 16 // esz
+    padded = torch.empty((int(rows.shape[0]), (V + per - 1) // per * per), dtype=rows.dtype, device=rows.device)
+    padded[:, :V].copy_(rows)
+    return padded[:, :V], None
+
+
 def sample_raw(logits, temperature, top_k, top_p, rep_penalty, uniforms, out_ids, *, sample_idx=None,
                hist_offsets=None, hist_ids=None, max_hist: int = 0, out_probs=None, out_info=None,
                stream=None, workspace="auto", mode: int = NS_MODE_AUTO) -> None:
@@ -158,6 +181,7 @@ def sample_raw(logits, temperature, top_k, top_p, rep_penalty, uniforms, out_ids
     else:
         raise TypeError(f"logits dtype {logits.dtype} not supported (float32 or bfloat16)")
     B = int(out_ids.shape[0])
+    logits, sample_idx = aligned_rows(logits, sample_idx)
     a = NsSampleArgs()
     a.logits = _ptr(logits)
     a.dtype = dt

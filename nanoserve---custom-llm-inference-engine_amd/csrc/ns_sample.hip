@@ -1131,12 +1131,17 @@ int64_t align256(int64_t x) { return (x + 255) / 256 * 256; }
 struct WsLayout {
   int64_t counters, status, stats, cand, total;
 };
+// Workspace layout.  The per-row arrival counters are the only state that outlives a
+// call (each call leaves them at zero): they sit at fixed positions at the start, sized
+// for NS_SEG_MAX_ROWS rows, so calls of any shape sharing one workspace always find
+// zeroed counters.  Everything behind them is rewritten by every call before it is read.
 WsLayout ws_layout(int32_t n_sample, int64_t vocab, int32_t dtype) {
-  const int64_t rows = ((int64_t)n_sample + 7) / 8 * 8;
+  const int64_t n = n_sample < NS_SEG_MAX_ROWS ? n_sample : NS_SEG_MAX_ROWS;
+  const int64_t rows = (n + 7) / 8 * 8;
   const int64_t S = seg_count(vocab, dtype);
   WsLayout L;
   L.counters = 0;
-  L.status = align256(rows * 4);
+  L.status = align256((int64_t)NS_SEG_MAX_ROWS * 4);
   L.stats = L.status + align256(rows * 4);
   L.cand = L.stats + align256(rows * S * (int64_t)sizeof(ns::SegStat));
   L.total = L.cand + align256(rows * S * ns::SEG_CAP * 8);
@@ -1196,12 +1201,6 @@ int ns_sample(const ns_sample_args* a, hipStream_t stream) {
   if (((uintptr_t)a->logits % 16) != 0 || ((a->row_stride * esz) % 16) != 0)
     return fail(NS_ERR_ALIGN, "logits rows must start on 16-byte boundaries (base and row stride)");
   const WsLayout L = ws_layout(a->n_sample, a->vocab, a->dtype);
-  if (a->workspace != nullptr) {
-    if (a->workspace_bytes < (uint64_t)L.total)
-      return fail(NS_ERR_INVALID, "workspace of " + std::to_string(a->workspace_bytes) + " bytes, " +
-                                      std::to_string(L.total) + " needed (ns_sample_workspace_bytes)");
-    if (((uintptr_t)a->workspace % 256) != 0) return fail(NS_ERR_ALIGN, "workspace must be 256-byte aligned");
-  }
 
   int32_t lds = 0;
   int rc = ns_sample_lds_bytes(a->vocab, a->hist_offsets ? a->max_hist : 0, &lds);
@@ -1259,7 +1258,16 @@ int ns_sample(const ns_sample_args* a, hipStream_t stream) {
   e = hipDeviceGetAttribute(&n_cu, hipDeviceAttributeMultiprocessorCount, dev);
   if (e != hipSuccess) return fail(NS_ERR_HIP, std::string("hipDeviceGetAttribute: ") + hipGetErrorString(e));
   bool segmented = a->workspace != nullptr && a->mode != NS_MODE_PER_ROW;
-  if (a->mode == NS_MODE_AUTO && (int64_t)a->n_sample * 8 >= (int64_t)n_cu * 7) segmented = false;
+  if (a->mode == NS_MODE_AUTO && ((int64_t)a->n_sample * 8 >= (int64_t)n_cu * 7 || a->n_sample > NS_SEG_MAX_ROWS))
+    segmented = false;
+  if (segmented) {
+    if (a->n_sample > NS_SEG_MAX_ROWS)
+      return fail(NS_ERR_INVALID, "segmented mode takes at most " + std::to_string(NS_SEG_MAX_ROWS) + " rows");
+    if (a->workspace_bytes < (uint64_t)L.total)
+      return fail(NS_ERR_INVALID, "workspace of " + std::to_string(a->workspace_bytes) + " bytes, " +
+                                      std::to_string(L.total) + " needed (ns_sample_workspace_bytes)");
+    if (((uintptr_t)a->workspace % 256) != 0) return fail(NS_ERR_ALIGN, "workspace must be 256-byte aligned");
+  }
   p.fast = 1;
   p.status = nullptr;
 

@@ -1,0 +1,142 @@
+"""Write the golden fixtures under tests/golden/ from the CPU oracle.
+
+    python tests/golden/make_golden.py
+
+configs.json -- for each workload (c0, c1, c2, c3 at 32 rows, c4): the SHA-256
+digest of the generated inputs (so a run can confirm it regenerated identical
+logits, parameters, histories and uniforms) and, per sampled row, the oracle's
+token id, top-k threshold bits, kept counts and exemption flags.
+
+tiny_cases.json -- small hand-built rows with their full inputs and expected
+outputs (token id, threshold, kept counts, final probabilities): ties at the
+top-k threshold and across the top-p cut, penalties below and above 1 with
+duplicate history ids, NaN / +inf / -inf logits, greedy rows, temperatures
+below 1e-6 and negative, top_p <= 0, top_k >= V.
+
+The reference ships no tests, golden vectors or fixtures of its own; these
+fixtures pin the kernels and the oracle to one another across changes, and the
+oracle itself is pinned by tests/test_oracle_pins.py.
+"""
+from __future__ import annotations
+
+import importlib
+import json
+import os
+import sys
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+ROOT = os.path.dirname(os.path.dirname(HERE))
+sys.path.insert(0, ROOT)
+W = importlib.import_module("nanoserve---custom-llm-inference-engine_amd.workloads")
+from oracle import sampler_oracle as O  # noqa: E402
+
+CONFIGS = ((0, None), (1, None), (2, None), (3, 32), (4, None))
+
+
+def f32_bits(x) -> int:
+    return int(np.float32(x).view(np.uint32))
+
+
+def row_records(r) -> list:
+    out = []
+    for i in range(len(r.ids)):
+        out.append({
+            "id": int(r.ids[i]),
+            "thr_bits": None if np.isnan(r.topk_thr[i]) else f32_bits(r.topk_thr[i]),
+            "n_kept_topk": int(r.n_kept_topk[i]),
+            "n_kept": int(r.n_kept[i]),
+            "zone": int(len(r.zone_ids[i])),
+            "greedy": bool(r.greedy[i]),
+            "nan_row": bool(r.nan_row[i]),
+            "exempt": bool(r.exempt[i]),
+        })
+    return out
+
+
+def make_configs() -> dict:
+    res = {}
+    for cfg, batch in CONFIGS:
+        w = W.make_workload(cfg, batch=batch)
+        r = O.sample_workload(w)
+        res[w.name] = {"cfg": cfg, "batch_arg": batch, "batch": w.batch, "vocab": w.vocab, "dtype": w.dtype,
+                       "digest": w.digest(), "rows": row_records(r)}
+        print(f"{w.name}: {w.batch} rows, {int(r.exempt.sum())} exempt", flush=True)
+    return res
+
+
+def tiny_cases() -> list:
+    """Groups of rows sharing one vocabulary size; each group is one batch."""
+    rng = np.random.default_rng(20261201)
+    groups = []
+
+    def group(name, rows, temp, k, p, pen, hist, u):
+        rows = np.asarray(rows, dtype=np.float32)
+        B = rows.shape[0]
+        bc = lambda v, dt: np.broadcast_to(np.asarray(v, dtype=dt), (B,)).copy()
+        g = {"name": name, "rows": rows, "temperature": bc(temp, np.float64), "top_k": bc(k, np.int64),
+             "top_p": bc(p, np.float64), "repetition_penalty": bc(pen, np.float64),
+             "histories": [np.asarray(h, dtype=np.int32) for h in hist], "uniforms": bc(u, np.float32)}
+        groups.append(g)
+
+    # ties at the top-k threshold (kept, count exceeds k) and across the top-p cut
+    V = 17
+    base = np.array([3, 1, 3, 2, 3, 0, -1, 2, 3, 1, 0, 0, -2, 2, 1, 3, -1], dtype=np.float32)
+    group("ties", np.stack([base] * 6), [1.0, 0.5, 1.0, 1.0, 2.0, 1.0], [2, 5, 1, 17, 3, 0],
+          [1.0, 1.0, 0.5, 0.3, 0.6, 0.35], 1.0, [[]] * 6, [0.0, 0.3, 0.5, 0.7, 0.99, 0.42])
+    # penalties < 1 and > 1 with duplicated history ids (set semantics), negative and positive logits
+    V = 64
+    x = np.round(rng.normal(0, 2, size=(6, V)), 2).astype(np.float32)
+    hist = [[0, 1, 1, 2, 63, 63], [5, 5, 5], [10, 20, 30, 40], [], [7, 8, 9, 7, 8, 9], list(range(0, 64, 3))]
+    group("penalty", x, [1.0, 0.7, 1.3, 1.0, 0.0, 1.0], [0, 10, 5, 64, 0, 3], [0.9, 1.0, 0.95, 0.5, 1.0, 1.0],
+          [1.2, 0.8, 1.1, 1.5, 0.9, 2.0], hist, [0.1, 0.5, 0.9, 0.25, 0.6, 0.75])
+    # special values: NaN (uniform row), +inf (NaN softmax -> uniform), -inf masked tokens, all but one -inf
+    V = 33
+    x = np.round(rng.normal(0, 1, size=(5, V)), 3).astype(np.float32)
+    x[0, 4] = np.nan
+    x[1, 7] = np.inf
+    x[2, ::2] = -np.inf
+    x[3, :] = -np.inf
+    x[3, 12] = 1.0
+    x[4, 20] = np.nan
+    group("special", x, [1.0, 1.0, 0.8, 1.0, 0.0], [0, 5, 0, 4, 0], [0.9, 1.0, 0.7, 1.0, 1.0], 1.0,
+          [[]] * 5, [0.3, 0.6, 0.45, 0.2, 0.8])
+    # temperature edge cases and top_p <= 0 (keeps exactly one token), top_k >= V (off)
+    V = 257
+    x = np.round(rng.normal(0, 3, size=(6, V)), 1).astype(np.float32)
+    group("edges", x, [1e-9, -1.0, 0.0, 1.0, 3.0, 1.0], [0, 0, 300, 257, 256, 1], [1.0, 0.8, 1.0, 0.0, -0.5, 0.9],
+          [1.0, 1.1, 1.1, 1.0, 1.0, 1.0], [[], [1, 2, 3], [0, 256], [], [], []], [0.5, 0.123, 0.9, 0.77, 0.01, 0.6])
+    # a bf16-valued row set (coarse values: many ties) with k up to 64
+    V = 1000
+    x = np.round(rng.normal(0, 3, size=(4, V)) * 4) / 4
+    group("coarse", x.astype(np.float32), 1.0, [50, 64, 20, 1], [0.95, 0.9, 1.0, 1.0], 1.1,
+          [rng.integers(0, V, 40), rng.integers(0, V, 5), [], rng.integers(0, V, 100)], [0.2, 0.4, 0.6, 0.8])
+    out = []
+    for g in groups:
+        r = O.sample(g["rows"], g["temperature"], g["top_k"], g["top_p"], g["repetition_penalty"], g["histories"],
+                     g["uniforms"])
+        rec = row_records(r)
+        for i, d in enumerate(rec):
+            d["probs_bits"] = [f32_bits(v) for v in r.probs[i].numpy()]
+        out.append({
+            "name": g["name"], "vocab": int(g["rows"].shape[1]),
+            "rows_bits": [[f32_bits(v) for v in row] for row in g["rows"]],
+            "temperature": [float(v) for v in g["temperature"]], "top_k": [int(v) for v in g["top_k"]],
+            "top_p": [float(v) for v in g["top_p"]], "repetition_penalty": [float(v) for v in g["repetition_penalty"]],
+            "histories": [[int(v) for v in h] for h in g["histories"]],
+            "uniforms": [float(v) for v in g["uniforms"]], "expected": rec,
+        })
+        print(f"tiny {g['name']}: V={g['rows'].shape[1]} rows={len(rec)} ids={[d['id'] for d in rec]}", flush=True)
+    return out
+
+
+def main():
+    with open(os.path.join(HERE, "tiny_cases.json"), "w") as f:
+        json.dump(tiny_cases(), f, separators=(",", ":"))
+    with open(os.path.join(HERE, "configs.json"), "w") as f:
+        json.dump(make_configs(), f, separators=(",", ":"))
+
+
+if __name__ == "__main__":
+    main()

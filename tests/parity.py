@@ -22,6 +22,9 @@ L = pkg("_lib")
 S = pkg("sampler")
 C = pkg("config")
 
+# kernel modes under test: path name -> (workspace, mode)
+PATHS = {"segmented": ("auto", L.NS_MODE_SEGMENTED), "per-row": (None, L.NS_MODE_PER_ROW)}
+
 PROB_RTOL = 1e-5
 PROB_ATOL = 1e-12
 

@@ -84,3 +84,21 @@ def test_sampling_params_match_reference_defaults():
     assert (p.max_tokens, p.temperature, p.top_p, p.top_k, p.repetition_penalty, p.ignore_eos, p.seed) == \
         (128, 1.0, 1.0, -1, 1.0, False, None)
     assert p.stop_token_ids == [] and p.stop == []
+
+
+def test_aligned_rows_pads_misaligned_vocab():
+    import torch
+    L = pkg("_lib")
+    x = torch.arange(3 * 17, dtype=torch.float32).reshape(3, 17)
+    y, idx = L.aligned_rows(x, None)
+    assert y.shape == (3, 17) and y.stride(0) == 20 and idx is None
+    assert torch.equal(y, x)
+    sel = torch.tensor([2, 0], dtype=torch.int64)
+    y2, idx2 = L.aligned_rows(x, sel)
+    assert idx2 is None and torch.equal(y2, x[[2, 0]]) and (y2.stride(0) * 4) % 16 == 0
+    b = torch.zeros(4, 24, dtype=torch.bfloat16)            # 48-byte rows: already aligned
+    yb, ib = L.aligned_rows(b, sel)
+    assert yb.data_ptr() == b.data_ptr() and ib is sel
+    b9 = torch.ones(2, 9, dtype=torch.bfloat16)             # 18-byte rows: padded to 16 elements
+    yb9, _ = L.aligned_rows(b9, None)
+    assert yb9.stride(0) == 16 and torch.equal(yb9, b9)

@@ -9,7 +9,7 @@ import pytest
 import torch
 
 from conftest import pkg
-from parity import compare, run_gpu
+from parity import PATHS, compare, run_gpu
 
 W = pkg("workloads")
 O = pytest.importorskip("oracle.sampler_oracle")
@@ -18,8 +18,6 @@ pytestmark = pytest.mark.gpu
 
 
 L = pkg("_lib")
-# path name -> (workspace, mode)
-PATHS = {"segmented": ("auto", L.NS_MODE_SEGMENTED), "per-row": (None, L.NS_MODE_PER_ROW)}
 
 
 def _check(w, device, path="segmented", **kw):
