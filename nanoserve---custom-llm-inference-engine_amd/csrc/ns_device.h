@@ -270,14 +270,13 @@ __device__ __forceinline__ uint4 buf_load16(__amdgpu_buffer_rsrc_t r, uint32_t v
   const ns_v4u x = __builtin_amdgcn_raw_buffer_load_b128(r, (int)voff, (int)soff, 0);
   return make_uint4(x.x, x.y, x.z, x.w);
 }
-// 16 bytes at byte off + voff of a region of nbytes bytes (off wave-uniform, both
-// multiples of 16).  The descriptor starts at the uniform offset, so the range check,
-// which covers the VGPR offset, rejects everything past the region: such loads read
-// zero and touch no memory.
+// 16 bytes at byte off + voff of a region of nbytes bytes (both multiples of 16).  One
+// descriptor over the region, the whole offset in the VGPR operand, which the range
+// check covers: loads past the region read zero and touch no memory.  (A descriptor
+// per offset would be computed in VGPRs and turn every load into a waterfall loop.)
 __device__ __forceinline__ uint4 buf_load16_at(const unsigned char* base, uint32_t nbytes, uint32_t off,
                                                uint32_t voff) {
-  const uint32_t rem = nbytes > off ? nbytes - off : 0u;
-  return buf_load16(make_rsrc(base + off, rem), voff, 0u);
+  return buf_load16(make_rsrc(base, nbytes), voff + off, 0u);
 }
 
 // exp from the ROCm device library (ocml expf, faithfully rounded); not the

@@ -9,8 +9,8 @@
 //     requested at once (chunk q*NT + t to thread t), the history ids behind it.
 //     Such a penalty never raises a value and keeps NaN / +inf, so the row is
 //     processed raw: a lower bound of the k-th largest comes from the first half
-//     of the chunks (the k-th largest of the RF_J largest thread values of every
-//     wave), then the chunks reaching it are staged in LDS as the second half
+//     of the chunks (the k-th largest of the maxima of every 8-lane group), then
+//     the chunks reaching it are staged in LDS as the second half
 //     lands and expanded into a candidate list.  After the stream the history
 //     bitmap is built, the candidates at history positions are penalized, and a
 //     count check confirms the list still covers the top-k.  The list is ordered
@@ -25,7 +25,6 @@
 namespace ns {
 
 constexpr int RCPT = 16;               // chunks per thread: the whole row in flight
-constexpr int RF_J = 4;                // largest thread values per wave feeding the bound (RF_J * NWAVE >= KFAST)
 constexpr int RHB = 2;                 // history ids per thread per batch
 // LDS staging of the chunks that reach the bound, inside the candidate region (u64
 // units): the list and its rank counters use the first WAVE_CAP * 3 / 2 entries
@@ -33,8 +32,7 @@ constexpr int HIT_PER_WAVE = 48;                               // chunk slots pe
 constexpr int HIT_OFF64 = 512;                                 // 16-byte chunks
 constexpr int HIT_IDX_OFF64 = HIT_OFF64 + HIT_PER_WAVE * NWAVE * 2;   // chunk indices
 constexpr int HIT_CNT_OFF64 = HIT_IDX_OFF64 + HIT_PER_WAVE * NWAVE / 2;   // per-wave counts
-static_assert(RF_J * NWAVE == 64, "the bound is selected from one value per lane of wave 0");
-static_assert(KFAST <= RF_J * NWAVE, "k-th largest of the per-wave values");
+static_assert(KFAST <= 64 && NWAVE * 8 == 128, "the bound: k-th largest of 128 group maxima, k <= 64");
 static_assert(WAVE_CAP * 3 / 2 <= HIT_OFF64 && HIT_CNT_OFF64 + NWAVE / 2 <= CAP, "candidate region layout");
 
 // An opaque copy of a chunk: values derived from it are recomputed rather than
@@ -110,6 +108,14 @@ __device__ __forceinline__ bool hist_batch(const int32_t (&ids)[NB], int base, i
     }
   }
   return bad;
+}
+
+// Chunks at or past the row's last full one are read as zeros: their maxima become -inf.
+// Called behind a wave-uniform test that only the last chunk rows of a row pass; the empty
+// asm keeps that test a branch instead of a select evaluated for every chunk.
+__device__ __forceinline__ void past_row(float& m, int c, int nf) {
+  asm volatile("");
+  if (c >= nf) m = -__builtin_inff();
 }
 
 template <typename T>
@@ -291,8 +297,8 @@ __device__ __forceinline__ int row_fast(const RowArgs P, const int row, const in
   uint4 v[RCPT];
 #pragma unroll
   for (int q = 0; q < RCPT; ++q) {
-    // issued in chunk order (loads complete in issue order; the passes below take the
-    // chunks in this order)
+    // issued in chunk order (a wave's loads complete in issue order, and the pass below
+    // takes the chunks in that order)
     v[q] = buf_load16_at(rowp, (uint32_t)nf * 16u, (uint32_t)(q * NT * 16), (uint32_t)tid * 16u);
     __builtin_amdgcn_sched_barrier(0);
   }
@@ -306,50 +312,50 @@ __device__ __forceinline__ int row_fast(const RowArgs P, const int row, const in
   if (pen_on)
     for (int i = tid; i < nbw; i += NT) bm[i] = 0u;
 
-  // lower bound of the k-th largest raw value from the first half of the chunks (values
-  // of distinct elements: the k-th largest of any subset is a lower bound): the k-th
-  // largest of the RF_J largest thread values of each wave.  The barriers wait for LDS
-  // only; the rest of the row stays in flight.
-  constexpr int RH = RCPT / 2;
-  float cm[RH];   // NaN-propagating chunk maxima of the first half (-inf past the full chunks)
-  {
-    float tval = -__builtin_inff();
+  // every chunk's NaN-propagating maximum as the row lands (-inf past the full chunks;
+  // NaN / +inf only flagged here)
+  float cm[RCPT];
+  float tval = -__builtin_inff();
+  bool special = false;   // NaN or +inf in a chunk
 #pragma unroll
-    for (int q = 0; q < RH; ++q) {
-      const int c = q * NT + tid;
-      cm[q] = c < nf ? chunk_max<T>(v[q]) : -__builtin_inff();
-      tval = __builtin_fmaxf(tval, cm[q]);
-    }
-    const uint32_t key = wave_sort_u32(~fkey(tval));   // descending
-    if (lane < RF_J) fs[wid * RF_J + lane] = fkey_inv(~key);
+  for (int q = 0; q < RCPT; ++q) {
+    cm[q] = chunk_max<T>(v[q]);
+    if ((q + 1) * NT > nf) past_row(cm[q], q * NT + tid, nf);
+    tval = __builtin_fmaxf(tval, cm[q]);
+    special |= !(cm[q] < __builtin_inff());
+  }
+  // lower bound of the k-th largest raw value: the k-th largest of the maxima of every
+  // 8-lane group (128 values of distinct elements)
+  {
+    tval = __builtin_fmaxf(tval, lane_xor(tval, 1));
+    tval = __builtin_fmaxf(tval, lane_xor(tval, 2));
+    tval = __builtin_fmaxf(tval, lane_xor(tval, 4));
+    if ((lane & 7) == 0) fs[wid * 8 + (lane >> 3)] = tval;
     __syncthreads();
     if (wid == 0) {
-      const uint32_t k2 = wave_sort_u32(~fkey(fs[lane]));
-      const float taux = fkey_inv(~read_lane(k2, k - 1));
-      if (lane == 0) fs[64] = taux;
+      uint32_t kk[2] = {~fkey(fs[lane]), ~fkey(fs[64 + lane])};
+      wave_sort_u32r<2>(kk);   // descending values
+      const float taux = fkey_inv(~read_lane(kk[0], k - 1));
+      if (lane == 0) misc->fb[0] = taux;
     }
     __syncthreads();
   }
-  const float taux = fs[64];
+  const float taux = misc->fb[0];
   const float tc = lower_preimage(taux, tdiv, rdiv);   // x >= tc  <=>  x / t >= RN(taux / t)
 
-  // chunks whose maximum reaches tc, as the rest of the row lands: the chunk and its index
-  // go to the wave's own LDS slots (no atomics); NaN / +inf only flagged here
+  // chunks whose maximum reaches tc: the chunk and its index go to the wave's own LDS
+  // slots (no atomics)
   uint4* hdat = reinterpret_cast<uint4*>(cand + HIT_OFF64) + wid * HIT_PER_WAVE;
   int32_t* hidx = reinterpret_cast<int32_t*>(cand + HIT_IDX_OFF64) + wid * HIT_PER_WAVE;
   int32_t* hcnt = reinterpret_cast<int32_t*>(cand + HIT_CNT_OFF64);
-  bool special = false;   // NaN or +inf in a chunk
   int nh = 0;             // this wave's hit chunks (wave-uniform)
 #pragma unroll
   for (int q = 0; q < RCPT; ++q) {
-    const int c = q * NT + tid;
-    const float cmq = q < RH ? cm[q] : (c < nf ? chunk_max<T>(v[q]) : -__builtin_inff());
-    special |= !(cmq < __builtin_inff());
-    const bool hit = cmq >= tc;
+    const bool hit = cm[q] >= tc;
     const uint64_t m = ballot(hit);
     if (m != 0ull) {
       const int pos = nh + lanes_below(m);
-      if (hit && pos < HIT_PER_WAVE) { hdat[pos] = v[q]; hidx[pos] = c; }
+      if (hit && pos < HIT_PER_WAVE) { hdat[pos] = v[q]; hidx[pos] = q * NT + tid; }
       nh += __popcll(m);
     }
   }
@@ -423,28 +429,30 @@ __device__ __forceinline__ int row_fast(const RowArgs P, const int row, const in
   const int n = misc->cand_n;
   if (n == 0) { uniform_row(-__builtin_inff()); return 0; }   // every logit -inf
   if (n > WAVE_CAP) { __syncthreads(); return 1; }
-  if (pen_on) {
-    // penalize the candidates at history positions (sampler.py:37); the list still holds
-    // the whole top-k if at least k of them stay >= tc: every element outside it is < tc
+  // penalize the candidates at history positions (sampler.py:37) and turn them into sort
+  // keys of the scaled value, in place.  With a penalty, the list still holds the whole
+  // top-k if at least k of them stay >= tc: every element outside it is < tc.
+  {
     bool ok = false;
     if (tid < n) {
       const uint64_t e = cand[tid];
       const uint32_t id = (uint32_t)e;
       float x = __uint_as_float((uint32_t)(e >> 32));
-      if ((bm[id >> 5] >> (id & 31)) & 1u) {
-        x = pen_val(x);
-        cand[tid] = ((uint64_t)__float_as_uint(x) << 32) | id;
-      }
+      if (pen_on && ((bm[id >> 5] >> (id & 31)) & 1u)) x = pen_val(x);
       ok = x >= tc;
+      cand[tid] = desc_key(div_rn(x, tdiv, rdiv), id);
     }
-    const int nok = __popcll(ballot(ok));
-    if (lane == 0 && nok != 0) atomicAdd(&misc->xl_n, nok);
+    if (tid < WAVE_CAP) reinterpret_cast<int32_t*>(cand + WAVE_CAP)[tid] = 0;   // rank counters
+    if (pen_on) {
+      const int nok = __popcll(ballot(ok));
+      if (lane == 0 && nok != 0) atomicAdd(&misc->xl_n, nok);
+    }
     __syncthreads();
-    if (misc->xl_n < k && tc > -__builtin_inff()) { __syncthreads(); return 1; }
+    if (pen_on && misc->xl_n < k && tc > -__builtin_inff()) { __syncthreads(); return 1; }
   }
   zero_probs(o);
-  block_finalize<NT>(cand, n, k, topp < 1.0f, topp, tdiv, rdiv, u, row, P.out_ids, P.out_probs, V, P.out_info,
-                     flags, n, PATH_WAVE_SET);
+  block_finalize_keys<NT>(cand, n, k, topp < 1.0f, topp, u, row, P.out_ids, P.out_probs, V, P.out_info, flags, n,
+                          PATH_WAVE_SET);
   return 0;
 }
 

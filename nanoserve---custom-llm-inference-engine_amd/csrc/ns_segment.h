@@ -225,6 +225,39 @@ __device__ __forceinline__ uint32_t wave_sort_u32(uint32_t a) {
   return a;
 }
 
+// Ascending bitonic sort of 64*R u32 keys held by one wave: element i = r*64 + lane.
+template <int R>
+__device__ __forceinline__ void wave_sort_u32r(uint32_t (&a)[R]) {
+  const int lane = lane_id();
+#pragma unroll
+  for (int size = 2; size <= 64 * R; size <<= 1) {
+#pragma unroll
+    for (int stride = size >> 1; stride > 0; stride >>= 1) {
+      if (stride >= 64) {
+        const int rs = stride >> 6;
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+          if ((r & rs) == 0) {
+            const bool up = ((r * 64 + lane) & size) == 0;
+            const uint32_t x = a[r], y = a[r | rs];
+            const uint32_t mn = x < y ? x : y, mx = x < y ? y : x;
+            a[r] = up ? mn : mx;
+            a[r | rs] = up ? mx : mn;
+          }
+        }
+      } else {
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+          const uint32_t p = lane_xor(a[r], stride);
+          const bool up = ((r * 64 + lane) & size) == 0;
+          const bool lower = (lane & stride) == 0;
+          a[r] = (lower == up) ? (a[r] < p ? a[r] : p) : (a[r] < p ? p : a[r]);
+        }
+      }
+    }
+  }
+}
+
 // Inclusive prefix sums of 64*R doubles in element order i = r*64 + lane.
 template <int R>
 __device__ __forceinline__ void wave_scan_rows(const double (&v)[R], double (&out)[R]) {
@@ -371,22 +404,40 @@ __device__ __forceinline__ void wave_select_draw(const uint64_t (&a)[R], int nk,
     const int i = r * 64 + lane;
     z2 += wave_sum(i < nf ? es[r] : 0.0);
   }
-  uint64_t b[R];
+  // ids[r] / ps[r]: the kept tokens and their probabilities in ascending id order
+  uint32_t ids[R];
+  float ps[R];
+  if constexpr (R == 1) {
+    // one register row: sort (id << 6 | lane) as 32-bit keys (ids < 2^18), then fetch
+    // each probability from the lane it came from
+    const float pv = lane < nf ? (float)(es[0] / z2) : 0.0f;
+    uint32_t key = lane < nf ? ((desc_key_id(a[0]) << 6) | (uint32_t)lane) : 0xffffffffu;
+    key = wave_sort_u32(key);
+    ps[0] = __int_as_float(__builtin_amdgcn_ds_bpermute((int)((key & 63u) << 2), __float_as_int(pv)));
+    ids[0] = key >> 6;
+  } else {
+    uint64_t b[R];
 #pragma unroll
-  for (int r = 0; r < R; ++r) {
-    const int i = r * 64 + lane;
-    b[r] = ~0ull;
-    if (i < nf) {
-      const float pv = (float)(es[r] / z2);
-      b[r] = ((uint64_t)desc_key_id(a[r]) << 32) | __float_as_uint(pv);
+    for (int r = 0; r < R; ++r) {
+      const int i = r * 64 + lane;
+      b[r] = ~0ull;
+      if (i < nf) {
+        const float pv = (float)(es[r] / z2);
+        b[r] = ((uint64_t)desc_key_id(a[r]) << 32) | __float_as_uint(pv);
+      }
+    }
+    wave_sort_u64<R>(b);
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      ids[r] = (uint32_t)(b[r] >> 32);
+      ps[r] = __uint_as_float((uint32_t)b[r]);
     }
   }
-  wave_sort_u64<R>(b);
   double pd[R], cd[R];
 #pragma unroll
   for (int r = 0; r < R; ++r) {
     const int i = r * 64 + lane;
-    pd[r] = i < nf ? (double)__uint_as_float((uint32_t)b[r]) : 0.0;
+    pd[r] = i < nf ? (double)ps[r] : 0.0;
   }
   wave_scan_rows<R>(pd, cd);
   const double ud = (double)u;
@@ -406,9 +457,14 @@ __device__ __forceinline__ void wave_select_draw(const uint64_t (&a)[R], int nk,
   int32_t fl = flags;
   if (pick < 0) { pick = lastpos >= 0 ? lastpos : 0; fl |= FLAG_LOCATE_FALLBACK; }
   {
-    const uint64_t kb = wave_elem<R>(b, pick);
+    uint32_t idp = read_lane(ids[0], pick & 63);
+#pragma unroll
+    for (int r = 1; r < R; ++r) {
+      const uint32_t t = read_lane(ids[r], pick & 63);
+      idp = (pick >> 6) == r ? t : idp;
+    }
     if (lane == 0) {
-      out_ids[row] = (int64_t)(kb >> 32);
+      out_ids[row] = (int64_t)idp;
       seg_write_info(out_info, row, path, nf, thr, nk, n_cand, fl, vstar, istar);
     }
   }
@@ -417,7 +473,7 @@ __device__ __forceinline__ void wave_select_draw(const uint64_t (&a)[R], int nk,
 #pragma unroll
     for (int r = 0; r < R; ++r) {
       const int i = r * 64 + lane;
-      if (i < nf) pr[b[r] >> 32] = __uint_as_float((uint32_t)b[r]);
+      if (i < nf) pr[ids[r]] = ps[r];
     }
   }
 }
@@ -476,31 +532,25 @@ __device__ void wave_select_draw_lds(const uint64_t* sorted, int nk, float M, fl
 }
 
 // The same selection and draw as wave_finalize over n <= WAVE_CAP survivors, with the
-// ordering done by the whole workgroup (nthreads threads, all of which must call it):
-// each survivor's position is the number of keys that precede it, counted in
-// parallel slices and summed with LDS atomics, then the keys are scattered in
-// place.  list (>= WAVE_CAP + WAVE_CAP / 2 entries of LDS) is overwritten: its
-// first n entries end up sorted and rank counters live behind them.  Wave 0 then
-// runs the top-p / softmax / draw over the top-k prefix only.
+// ordering done by the whole workgroup (NTH threads, all of which must call it).
+// Entry: list[0..n) holds the sort keys (desc_key of the scaled value and token id),
+// the rank counters behind them (list + WAVE_CAP, WAVE_CAP int32) are zero, and a
+// workgroup barrier has passed since both were written; k <= 64.  Each key's position
+// is the number of keys that precede it, counted in parallel slices and summed with
+// LDS atomics; the keys are scattered in place, and wave 0 then runs top-p, softmax
+// and the draw over the top-k prefix.
 template <int NTH>
-__device__ __forceinline__ void block_finalize(uint64_t* list, int n, int k, bool topp_on, float p32, float tdiv,
-                                               float rdiv, float u, int row, int64_t* out_ids, float* out_probs,
-                                               int64_t V, int32_t* out_info, int32_t flags, int32_t n_cand,
-                                               int32_t path) {
+__device__ __forceinline__ void block_finalize_keys(uint64_t* list, int n, int k, bool topp_on, float p32, float u,
+                                                    int row, int64_t* out_ids, float* out_probs, int64_t V,
+                                                    int32_t* out_info, int32_t flags, int32_t n_cand,
+                                                    int32_t path) {
   static_assert(NTH % 256 == 0, "rank slices assume whole groups of 256 threads");
   const int tid = threadIdx.x;
   int32_t* rank = reinterpret_cast<int32_t*>(list + WAVE_CAP);
-  uint64_t key = ~0ull;
-  if (tid < n) {
-    const uint64_t e = list[tid];
-    key = desc_key(div_rn(__uint_as_float((uint32_t)(e >> 32)), tdiv, rdiv), (uint32_t)e);
-  }
-  __syncthreads();   // every entry read before it is overwritten
-  if (tid < n) list[tid] = key;
-  if (tid < WAVE_CAP) rank[tid] = 0;
-  __syncthreads();
+  const uint64_t key = tid < n ? list[tid] : ~0ull;
   {
-    // element i = tid % NI against the keys of slice tid / NI (slices are wave-uniform)
+    // element i = tid % NI against the keys of slice tid / NI (slices are wave-uniform);
+    // four keys per step keep several LDS reads in flight
     const int NI = n <= 64 ? 64 : (n <= 128 ? 128 : 256);
     const int parts = NTH / NI;
     const int i = tid & (NI - 1), part = tid / NI;
@@ -510,7 +560,12 @@ __device__ __forceinline__ void block_finalize(uint64_t* list, int n, int k, boo
     if (i < n) {
       const uint64_t ki = list[i];
       int c = 0;
-      for (int j = j0; j < j1; ++j) c += list[j] < ki ? 1 : 0;
+      int j = j0;
+      for (; j + 4 <= j1; j += 4) {
+        const uint64_t a0 = list[j], a1 = list[j + 1], a2 = list[j + 2], a3 = list[j + 3];
+        c += (a0 < ki ? 1 : 0) + (a1 < ki ? 1 : 0) + (a2 < ki ? 1 : 0) + (a3 < ki ? 1 : 0);
+      }
+      for (; j < j1; ++j) c += list[j] < ki ? 1 : 0;
       if (c != 0) atomicAdd(&rank[i], c);
     }
   }
@@ -518,23 +573,48 @@ __device__ __forceinline__ void block_finalize(uint64_t* list, int n, int k, boo
   if (tid < n) list[rank[tid]] = key;
   __syncthreads();
   if (tid >= 64) return;
-  const float M = desc_key_val(list[0]);   // the row maximum
+  // the first 128 sorted keys in registers: row maximum, k-th largest, kept count
+  uint64_t a2[2];
+  a2[0] = tid < n ? list[tid] : ~0ull;
+  a2[1] = 64 + tid < n ? list[64 + tid] : ~0ull;
+  const float M = desc_key_val(read_lane(a2[0], 0));   // the row maximum
   // top-k threshold: the k-th largest (sampler.py:56-58); every value >= it is kept
-  const float thr = n >= k ? desc_key_val(list[k - 1]) : -__builtin_inff();
-  int nk = 0;
-  for (int base = 0; base < n; base += 64) {
+  const float thr = n >= k ? desc_key_val(read_lane(a2[0], k - 1)) : -__builtin_inff();
+  int nk = __popcll(ballot(tid < n && desc_key_val(a2[0]) >= thr)) +
+           __popcll(ballot(64 + tid < n && desc_key_val(a2[1]) >= thr));
+  for (int base = 128; base < n && nk == base; base += 64) {   // tie group beyond 128 (rare)
     const int i = base + tid;
     nk += __popcll(ballot(i < n && desc_key_val(list[i < n ? i : 0]) >= thr));
   }
-  if (nk <= 64)
-    wave_select_draw_lds<1>(list, nk, M, thr, topp_on, p32, u, row, out_ids, out_probs, V, out_info, flags, n_cand,
-                            path);
-  else if (nk <= 128)
-    wave_select_draw_lds<2>(list, nk, M, thr, topp_on, p32, u, row, out_ids, out_probs, V, out_info, flags, n_cand,
-                            path);
-  else
+  if (nk <= 64) {
+    const uint64_t a1[1] = {a2[0]};
+    wave_select_draw<1>(a1, nk, M, thr, topp_on, p32, u, row, out_ids, out_probs, V, out_info, flags, n_cand, path);
+  } else if (nk <= 128) {
+    wave_select_draw<2>(a2, nk, M, thr, topp_on, p32, u, row, out_ids, out_probs, V, out_info, flags, n_cand, path);
+  } else {
     wave_select_draw_lds<4>(list, nk, M, thr, topp_on, p32, u, row, out_ids, out_probs, V, out_info, flags, n_cand,
                             path);
+  }
+}
+
+// block_finalize_keys over list[0..n) = (value bits << 32) | token id, values not yet
+// scaled by the temperature (tdiv, rdiv = RN(1/tdiv)).
+template <int NTH>
+__device__ __forceinline__ void block_finalize(uint64_t* list, int n, int k, bool topp_on, float p32, float tdiv,
+                                               float rdiv, float u, int row, int64_t* out_ids, float* out_probs,
+                                               int64_t V, int32_t* out_info, int32_t flags, int32_t n_cand,
+                                               int32_t path) {
+  const int tid = threadIdx.x;
+  uint64_t key = ~0ull;
+  if (tid < n) {
+    const uint64_t e = list[tid];
+    key = desc_key(div_rn(__uint_as_float((uint32_t)(e >> 32)), tdiv, rdiv), (uint32_t)e);
+  }
+  __syncthreads();   // every entry read before it is overwritten
+  if (tid < n) list[tid] = key;
+  if (tid < WAVE_CAP) reinterpret_cast<int32_t*>(list + WAVE_CAP)[tid] = 0;
+  __syncthreads();
+  block_finalize_keys<NTH>(list, n, k, topp_on, p32, u, row, out_ids, out_probs, V, out_info, flags, n_cand, path);
 }
 
 // Wave-aggregated append of one candidate (scaled value y, token id) to the
