@@ -52,19 +52,6 @@ __device__ __forceinline__ uint32_t bf16_up(float x) {
 }
 __device__ __forceinline__ float bf16_float(uint32_t h) { return __uint_as_float(h << 16); }
 
-// Wave-aggregated append of (x, id) to the LDS candidate list (32-bit ids); every lane
-// of the wave calls it, `take` selects.
-__device__ __forceinline__ void cand_push(bool take, float x, uint32_t id, uint64_t* cand, Misc* misc) {
-  const uint64_t m = ballot(take);
-  if (m == 0ull) return;
-  const int leader = __builtin_ctzll(m);
-  int base = 0;
-  if (lane_id() == leader) base = atomicAdd(&misc->cand_n, __popcll(m));
-  base = read_lane(base, leader);
-  const int pos = base + lanes_below(m);
-  if (take && pos < CAP) cand[pos] = ((uint64_t)__float_as_uint(x) << 32) | id;
-}
-
 // Raw bits of token id's value (one element) through a buffer descriptor over the row;
 // ids outside the descriptor read 0.
 template <typename T>
@@ -336,13 +323,30 @@ __device__ __forceinline__ int row_fast(const RowArgs P, const int row, const in
       uint32_t kk[2] = {~fkey(fs[lane]), ~fkey(fs[64 + lane])};
       wave_sort_u32r<2>(kk);   // descending values
       const float taux = fkey_inv(~read_lane(kk[0], k - 1));
-      if (lane == 0) misc->fb[0] = taux;
+      // x >= tc  <=>  x / t >= RN(taux / t)
+      if (lane == 0) misc->fb[0] = lower_preimage(taux, tdiv, rdiv);
     }
     __syncthreads();
   }
-  const float taux = misc->fb[0];
-  const float tc = lower_preimage(taux, tdiv, rdiv);   // x >= tc  <=>  x / t >= RN(taux / t)
+  const float tc = misc->fb[0];
 
+  // the history bitmap (set semantics, sampler.py:34-38), from the ids that arrived while
+  // the row streamed
+  if (pen_on) {
+    bool bad = false;
+    for (int base = 0; base < H; base += RHB * NT) {
+#pragma unroll
+      for (int s = 0; s < RHB; ++s) {
+        const int j = base + s * NT + tid;
+        const int32_t id = base == 0 ? hid[s] : (j < H ? hp[j] : 0);
+        if (j < H) {
+          if (id < 0 || (int64_t)id >= V) bad = true;
+          else atomicOr(&bm[id >> 5], 1u << (id & 31));
+        }
+      }
+    }
+    if (bad) atomicOr(&misc->flags, FLAG_BAD_HIST_ID);
+  }
   // chunks whose maximum reaches tc: the chunk and its index go to the wave's own LDS
   // slots (no atomics)
   uint4* hdat = reinterpret_cast<uint4*>(cand + HIT_OFF64) + wid * HIT_PER_WAVE;
@@ -359,47 +363,17 @@ __device__ __forceinline__ int row_fast(const RowArgs P, const int row, const in
       nh += __popcll(m);
     }
   }
-  // the wave's own hit chunks: their elements >= tc into the candidate list, one element
-  // per lane (a wave's LDS accesses complete in order)
-  __builtin_amdgcn_wave_barrier();
-  {
-    const int nhc = nh < HIT_PER_WAVE ? nh : HIT_PER_WAVE;
-    for (int j = lane; j < nhc * EPC; j += 64) {
-      const int slot = j / EPC, e = j % EPC;
-      const float x = T::elem(hdat[slot], e);
-      const bool t = x >= tc && x > -__builtin_inff();
-      if (ballot(t) != 0ull) cand_push(t, x, (uint32_t)(hidx[slot] * EPC + e), cand, misc);
-    }
-  }
   if (lane == 0) hcnt[wid] = nh;
   // tokens past the last full chunk (V not a multiple of EPC), raw
-  if (nfull < nchunks && wid == 0) {
-    const int ntail = (int)(V - nfull * EPC);
-    const int64_t id = nfull * EPC + lane;
-    const float x = lane < ntail ? T::load1(rowp, id) : -__builtin_inff();
-    special |= !(x < __builtin_inff()) && lane < ntail;
-    const bool t = x >= tc && x > -__builtin_inff();
-    if (ballot(t) != 0ull) cand_push(t, x, (uint32_t)id, cand, misc);
-  }
-  // the history bitmap (set semantics, sampler.py:34-38), from the ids that arrived
-  // while the row streamed
-  if (pen_on) {
-    bool bad = false;
-    for (int base = 0; base < H; base += RHB * NT) {
-#pragma unroll
-      for (int s = 0; s < RHB; ++s) {
-        const int j = base + s * NT + tid;
-        const int32_t id = base == 0 ? hid[s] : (j < H ? hp[j] : 0);
-        if (j < H) {
-          if (id < 0 || (int64_t)id >= V) bad = true;
-          else atomicOr(&bm[id >> 5], 1u << (id & 31));
-        }
-      }
-    }
-    if (bad) atomicOr(&misc->flags, FLAG_BAD_HIST_ID);
+  const int ntail = (int)(V - nfull * EPC);
+  float xt = -__builtin_inff();
+  if (ntail > 0 && wid == 0 && lane < ntail) {
+    xt = T::load1(rowp, nfull * EPC + lane);
+    special |= !(xt < __builtin_inff());
   }
   if (lane == 0) is[wid] = ballot(special) != 0ull ? 1 : 0;
-  __syncthreads();
+  if (tid < WAVE_CAP) reinterpret_cast<int32_t*>(cand + WAVE_CAP)[tid] = 0;   // rank counters
+  __syncthreads();   // bitmap, staged chunks, flags
   int spec = 0, over = 0;
 #pragma unroll
   for (int w = 0; w < NWAVE; ++w) {
@@ -416,40 +390,45 @@ __device__ __forceinline__ int row_fast(const RowArgs P, const int row, const in
 #pragma unroll
       for (int e = 0; e < EPC; ++e) nanf |= T::elem(w, e) != T::elem(w, e);
     }
-    if (wid == 0 && nfull < nchunks) {
-      const int ntail = (int)(V - nfull * EPC);
-      const float x = lane < ntail ? T::load1(rowp, nfull * EPC + lane) : 0.0f;
-      nanf |= x != x;
-    }
+    if (wid == 0) nanf |= xt != xt;
     const int anynan = block_max_i64(nanf ? 1 : 0, red) != 0;
     uniform_row(anynan ? __builtin_nanf("") : __builtin_inff());
     return 0;
   }
   if (over != 0) { __syncthreads(); return 1; }
-  const int n = misc->cand_n;
-  if (n == 0) { uniform_row(-__builtin_inff()); return 0; }   // every logit -inf
-  if (n > WAVE_CAP) { __syncthreads(); return 1; }
-  // penalize the candidates at history positions (sampler.py:37) and turn them into sort
-  // keys of the scaled value, in place.  With a penalty, the list still holds the whole
-  // top-k if at least k of them stay >= tc: every element outside it is < tc.
+  // The candidates, straight as sort keys (scaled value, token id): the elements of the
+  // wave's own staged chunks, and in wave 0 the tail tokens, penalized at history
+  // positions (sampler.py:37) and kept when they still reach tc.  A penalty >= 1 never
+  // raises a value, so every element of the top-k reaches tc after the penalty too;
+  // when k of them do, the list holds the whole top-k and its ties.
   {
-    bool ok = false;
-    if (tid < n) {
-      const uint64_t e = cand[tid];
-      const uint32_t id = (uint32_t)e;
-      float x = __uint_as_float((uint32_t)(e >> 32));
-      if (pen_on && ((bm[id >> 5] >> (id & 31)) & 1u)) x = pen_val(x);
-      ok = x >= tc;
-      cand[tid] = desc_key(div_rn(x, tdiv, rdiv), id);
+    auto take_key = [&](float x, uint32_t id, bool live) {
+      if (live && pen_on && ((bm[id >> 5] >> (id & 31)) & 1u)) x = pen_val(x);
+      const bool t = live && x >= tc && x > -__builtin_inff();
+      const uint64_t m = ballot(t);
+      if (m == 0ull) return;
+      const int leader = __builtin_ctzll(m);
+      int base = 0;
+      if (lane == leader) base = atomicAdd(&misc->cand_n, __popcll(m));
+      base = read_lane(base, leader);
+      const int pos = base + lanes_below(m);
+      if (t && pos < WAVE_CAP) cand[pos] = desc_key(div_rn(x, tdiv, rdiv), id);   // past it: counted only
+    };
+    const int nhc = nh < HIT_PER_WAVE ? nh : HIT_PER_WAVE;
+    for (int j = lane; j < ((nhc * EPC + 63) & ~63); j += 64) {
+      const bool live = j < nhc * EPC;
+      const int slot = live ? j / EPC : 0, e = j % EPC;
+      // the whole chunk into registers first: the element is then chosen by selects
+      // (a data-dependent LDS address for it was mis-selected for e >= 2)
+      const uint4 ch = fresh(hdat[slot]);
+      take_key(T::elem(ch, e), (uint32_t)(hidx[slot] * EPC + e), live);
     }
-    if (tid < WAVE_CAP) reinterpret_cast<int32_t*>(cand + WAVE_CAP)[tid] = 0;   // rank counters
-    if (pen_on) {
-      const int nok = __popcll(ballot(ok));
-      if (lane == 0 && nok != 0) atomicAdd(&misc->xl_n, nok);
-    }
-    __syncthreads();
-    if (pen_on && misc->xl_n < k && tc > -__builtin_inff()) { __syncthreads(); return 1; }
+    if (ntail > 0 && wid == 0) take_key(xt, (uint32_t)(nfull * EPC + lane), lane < ntail);
   }
+  __syncthreads();   // the list complete
+  const int n = misc->cand_n;
+  if (n == 0 && !(tc > -__builtin_inff())) { uniform_row(-__builtin_inff()); return 0; }   // every logit -inf
+  if (n > WAVE_CAP || (tc > -__builtin_inff() && n < k)) { __syncthreads(); return 1; }
   zero_probs(o);
   block_finalize_keys<NT>(cand, n, k, topp < 1.0f, topp, u, row, P.out_ids, P.out_probs, V, P.out_info, flags, n,
                           PATH_WAVE_SET);
