@@ -297,6 +297,7 @@ __device__ __forceinline__ float div_rn(float x, float t, float r) {
   float aq = __builtin_fabsf(q0);
   bool slow = !(aq >= 0x1.0p-100f && aq <= 0x1.0p+100f);
   if (__ballot(slow) != 0ull) {  // wave-uniform branch: the IEEE division is never speculated
+    asm volatile("");             // (the empty asm keeps the compiler from if-converting it)
     if (slow) q = x / t;
   }
   return q;

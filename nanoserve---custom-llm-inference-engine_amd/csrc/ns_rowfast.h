@@ -8,14 +8,14 @@
 //   * Top-k rows with a penalty >= 1 (or none): every chunk of the row is
 //     requested at once (chunk q*NT + t to thread t), the history ids behind it.
 //     Such a penalty never raises a value and keeps NaN / +inf, so the row is
-//     processed raw: a lower bound of the k-th largest comes from the first half
-//     of the chunks (the k-th largest of the maxima of every 8-lane group), then
-//     the chunks reaching it are staged in LDS as the second half
-//     lands and expanded into a candidate list.  After the stream the history
-//     bitmap is built, the candidates at history positions are penalized, and a
-//     count check confirms the list still covers the top-k.  The list is ordered
-//     by the whole workgroup (rank counting) and one wave runs top-p, softmax
-//     and the draw over the top-k prefix.
+//     processed raw: chunk maxima as the row lands, the history bitmap from the
+//     ids behind it, then a lower bound of the k-th largest (the k-th largest of
+//     the maxima of every 8-lane group, by a ballot radix select).  Each wave
+//     stages its chunks that reach the bound in LDS and expands them into a
+//     candidate list, penalized at history positions; a count check confirms the
+//     list still covers the top-k.  The list is ordered by the whole workgroup
+//     (rank counting) and one wave runs top-p, softmax and the draw over the
+//     top-k prefix.
 // Rows outside these cases (penalty < 1, huge tie groups, too many staged chunks,
 // a failed coverage check) are left to the general per-row code.
 #pragma once
@@ -27,13 +27,12 @@ namespace ns {
 constexpr int RCPT = 16;               // chunks per thread: the whole row in flight
 constexpr int RHB = 2;                 // history ids per thread per batch
 // LDS staging of the chunks that reach the bound, inside the candidate region (u64
-// units): the list and its rank counters use the first WAVE_CAP * 3 / 2 entries
+// units): the list and its ordered copy use the first 2 * WAVE_CAP entries
 constexpr int HIT_PER_WAVE = 48;                               // chunk slots per wave
-constexpr int HIT_OFF64 = 512;                                 // 16-byte chunks
+constexpr int HIT_OFF64 = 2 * WAVE_CAP;                        // 16-byte chunks
 constexpr int HIT_IDX_OFF64 = HIT_OFF64 + HIT_PER_WAVE * NWAVE * 2;   // chunk indices
-constexpr int HIT_CNT_OFF64 = HIT_IDX_OFF64 + HIT_PER_WAVE * NWAVE / 2;   // per-wave counts
 static_assert(KFAST <= 64 && NWAVE * 8 == 128, "the bound: k-th largest of 128 group maxima, k <= 64");
-static_assert(WAVE_CAP * 3 / 2 <= HIT_OFF64 && HIT_CNT_OFF64 + NWAVE / 2 <= CAP, "candidate region layout");
+static_assert(HIT_IDX_OFF64 + HIT_PER_WAVE * NWAVE / 2 <= CAP, "candidate region layout");
 
 // An opaque copy of a chunk: values derived from it are recomputed rather than
 // kept alive from an earlier pass (the row's registers leave no room for them).
@@ -105,6 +104,34 @@ __device__ __forceinline__ void past_row(float& m, int c, int nf) {
   if (c >= nf) m = -__builtin_inff();
 }
 
+// The k-th largest of the wave's 128 keys (a0, a1 in every lane), truncated to its top NB
+// bits: the largest such prefix p with at least k keys >= p, one bit per step from the
+// top, counted with ballots.  A lower bound of the k-th largest key.
+template <int NB>
+__device__ __forceinline__ uint32_t wave_kth_key(uint32_t a0, uint32_t a1, int k) {
+  uint32_t p = 0u;
+#pragma unroll
+  for (int b = 31; b >= 32 - NB; --b) {
+    const uint32_t c = p | (1u << b);
+    const int cnt = __popcll(ballot(a0 >= c)) + __popcll(ballot(a1 >= c));
+    p = cnt >= k ? c : p;
+  }
+  return p;
+}
+
+// Element e (lane-varying) of a chunk held in registers, by selects on the bits of e.
+template <typename T>
+__device__ __forceinline__ float elem_sel(const uint4& c, int e) {
+  if constexpr (T::EPC == 8) {
+    const uint32_t lo = (e & 4) ? c.z : c.x, hi = (e & 4) ? c.w : c.y;
+    const uint32_t w = (e & 2) ? hi : lo;
+    return __uint_as_float((e & 1) ? (w & 0xffff0000u) : (w << 16));
+  } else {
+    const uint32_t lo = (e & 2) ? c.z : c.x, hi = (e & 2) ? c.w : c.y;
+    return __uint_as_float((e & 1) ? hi : lo);
+  }
+}
+
 template <typename T>
 __host__ __device__ __forceinline__ bool row_fits(int64_t V) {
   return (V + T::EPC - 1) / T::EPC <= (int64_t)NT * RCPT;
@@ -149,7 +176,6 @@ __device__ __forceinline__ int row_fast(const RowArgs P, const int row, const in
     return x < 0.0f ? x * pen : div_rn(x, pen, rpen);
   };
   float* fs = reinterpret_cast<float*>(&misc->red);      // 128 floats of scratch
-  int32_t* is = reinterpret_cast<int32_t*>(&misc->red);
   BlockScratch* red = &misc->red;
 
   const int32_t* hp = P.hist_ids + h0;
@@ -279,8 +305,9 @@ __device__ __forceinline__ int row_fast(const RowArgs P, const int row, const in
 
   // ---- top-k rows with a penalty >= 1 (or none).  Such a penalty never raises a value
   // and keeps NaN and +inf, so the row is processed raw and the candidates are penalized
-  // at the end.  The history ids are requested behind the row: loads complete in issue
-  // order, and scattered requests are served after the row's streaming ones anyway.
+  // at the end.  The history ids and the tail tokens are requested behind the row: loads
+  // complete in issue order, and scattered requests are served after the row's streaming
+  // ones anyway.
   uint4 v[RCPT];
 #pragma unroll
   for (int q = 0; q < RCPT; ++q) {
@@ -296,6 +323,16 @@ __device__ __forceinline__ int row_fast(const RowArgs P, const int row, const in
     for (int s = 0; s < RHB; ++s)
       hid[s] = (int32_t)__builtin_amdgcn_raw_buffer_load_b32(rh, (int)((uint32_t)(s * NT + tid) * 4u), 0, 0);
   }
+  // tokens past the last full chunk (V not a multiple of EPC): lane l of every wave reads
+  // token nfull * EPC + l, zero past the row; wave 0 keeps them
+  const int ntail = (int)(V - nfull * EPC);
+  const uint32_t xtraw = gather_raw<T>(make_rsrc(rowp, (uint32_t)(V * T::SZ)), (int32_t)(nfull * EPC) + lane);
+  // LDS set-up while the row streams, with no barrier: a wave finishes issuing its loads
+  // only as the row drains, so a barrier here would hold every wave until then.  The list
+  // is padded with keys that sort last and the bitmap cleared; the first barrier below
+  // orders both before their use.
+  int32_t* is = reinterpret_cast<int32_t*>(misc->db);    // 16 per-wave flags
+  if (tid < WAVE_CAP) cand[tid] = ~0ull;
   if (pen_on)
     for (int i = tid; i < nbw; i += NT) bm[i] = 0u;
 
@@ -311,27 +348,37 @@ __device__ __forceinline__ int row_fast(const RowArgs P, const int row, const in
     tval = __builtin_fmaxf(tval, cm[q]);
     special |= !(cm[q] < __builtin_inff());
   }
-  // lower bound of the k-th largest raw value: the k-th largest of the maxima of every
-  // 8-lane group (128 values of distinct elements)
-  {
-    tval = __builtin_fmaxf(tval, lane_xor(tval, 1));
-    tval = __builtin_fmaxf(tval, lane_xor(tval, 2));
-    tval = __builtin_fmaxf(tval, lane_xor(tval, 4));
-    if ((lane & 7) == 0) fs[wid * 8 + (lane >> 3)] = tval;
-    __syncthreads();
-    if (wid == 0) {
-      uint32_t kk[2] = {~fkey(fs[lane]), ~fkey(fs[64 + lane])};
-      wave_sort_u32r<2>(kk);   // descending values
-      const float taux = fkey_inv(~read_lane(kk[0], k - 1));
-      // x >= tc  <=>  x / t >= RN(taux / t)
-      if (lane == 0) misc->fb[0] = lower_preimage(taux, tdiv, rdiv);
-    }
-    __syncthreads();
+  // the maxima of every 8-lane group (128 values of distinct elements) for the bound
+  tval = __builtin_fmaxf(tval, lane_xor(tval, 1));
+  tval = __builtin_fmaxf(tval, lane_xor(tval, 2));
+  tval = __builtin_fmaxf(tval, lane_xor(tval, 4));
+  if ((lane & 7) == 0) fs[wid * 8 + (lane >> 3)] = tval;
+  float xt = -__builtin_inff();
+  if (wid == 0 && lane < ntail) {
+    xt = raw_float<T>(xtraw);
+    special |= !(xt < __builtin_inff());
   }
-  const float tc = misc->fb[0];
-
-  // the history bitmap (set semantics, sampler.py:34-38), from the ids that arrived while
-  // the row streamed
+  const bool wspecial = ballot(special) != 0ull;
+  if (lane == 0) is[wid] = wspecial ? 1 : 0;
+  __syncthreads();   // group maxima, flags, cleared bitmap, padded list
+  int spec = 0;
+#pragma unroll
+  for (int w = 0; w < NWAVE; ++w) spec |= is[w];
+  if (spec != 0) {
+    // NaN / +inf among the logits (the penalty keeps both): the softmax is NaN, uniform
+    // 1/V (sampler.py:77-80).  Rare: the row is read again to tell NaN from +inf.
+    bool nanf = false;
+    for (int c = tid; c < nf; c += NT) {
+      const uint4 w = rowv[c];
+#pragma unroll
+      for (int e = 0; e < EPC; ++e) nanf |= T::elem(w, e) != T::elem(w, e);
+    }
+    if (wid == 0) nanf |= xt != xt;
+    const int anynan = block_max_i64(nanf ? 1 : 0, red) != 0;
+    uniform_row(anynan ? __builtin_nanf("") : __builtin_inff());
+    return 0;
+  }
+  // the history bitmap (set semantics, sampler.py:34-38), while wave 0 finds the bound
   if (pen_on) {
     bool bad = false;
     for (int base = 0; base < H; base += RHB * NT) {
@@ -347,11 +394,25 @@ __device__ __forceinline__ int row_fast(const RowArgs P, const int row, const in
     }
     if (bad) atomicOr(&misc->flags, FLAG_BAD_HIST_ID);
   }
-  // chunks whose maximum reaches tc: the chunk and its index go to the wave's own LDS
-  // slots (no atomics)
+  // lower bound of the k-th largest raw value: the k-th largest of the group maxima, its
+  // key truncated to the bits a bfloat16 value carries (24 for float32)
+  if (wid == 0) {
+    const uint32_t kp = wave_kth_key<T::SZ == 2 ? 16 : 24>(fkey(fs[lane]), fkey(fs[64 + lane]), k);
+    const float taux = kp <= fkey(-__builtin_inff()) ? -__builtin_inff() : fkey_inv(kp);
+    // x >= tc  <=>  x / t >= RN(taux / t)
+    if (lane == 0) misc->fb[0] = lower_preimage(taux, tdiv, rdiv);
+  }
+  __syncthreads();   // the bound, the bitmap
+  const float tc = misc->fb[0];
+  flags |= misc->flags;
+
+  // Chunks whose maximum reaches tc go to the wave's own LDS slots, then the wave expands
+  // them into candidates, straight as sort keys (scaled value, token id): elements
+  // penalized at history positions (sampler.py:37) and kept when they still reach tc.  A
+  // penalty >= 1 never raises a value, so every element of the top-k reaches tc after the
+  // penalty too; when k of them do, the list holds the whole top-k and its ties.
   uint4* hdat = reinterpret_cast<uint4*>(cand + HIT_OFF64) + wid * HIT_PER_WAVE;
   int32_t* hidx = reinterpret_cast<int32_t*>(cand + HIT_IDX_OFF64) + wid * HIT_PER_WAVE;
-  int32_t* hcnt = reinterpret_cast<int32_t*>(cand + HIT_CNT_OFF64);
   int nh = 0;             // this wave's hit chunks (wave-uniform)
 #pragma unroll
   for (int q = 0; q < RCPT; ++q) {
@@ -363,75 +424,41 @@ __device__ __forceinline__ int row_fast(const RowArgs P, const int row, const in
       nh += __popcll(m);
     }
   }
-  if (lane == 0) hcnt[wid] = nh;
-  // tokens past the last full chunk (V not a multiple of EPC), raw
-  const int ntail = (int)(V - nfull * EPC);
-  float xt = -__builtin_inff();
-  if (ntail > 0 && wid == 0 && lane < ntail) {
-    xt = T::load1(rowp, nfull * EPC + lane);
-    special |= !(xt < __builtin_inff());
-  }
-  if (lane == 0) is[wid] = ballot(special) != 0ull ? 1 : 0;
-  if (tid < WAVE_CAP) reinterpret_cast<int32_t*>(cand + WAVE_CAP)[tid] = 0;   // rank counters
-  __syncthreads();   // bitmap, staged chunks, flags
-  int spec = 0, over = 0;
-#pragma unroll
-  for (int w = 0; w < NWAVE; ++w) {
-    spec |= is[w];
-    over |= hcnt[w] > HIT_PER_WAVE ? 1 : 0;
-  }
-  flags |= misc->flags;
-  if (spec != 0) {
-    // NaN / +inf among the logits (the penalty keeps both): the softmax is NaN, uniform
-    // 1/V (sampler.py:77-80).  Rare: the row is read again to tell NaN from +inf.
-    bool nanf = false;
-    for (int c = tid; c < nf; c += NT) {
-      const uint4 w = rowv[c];
-#pragma unroll
-      for (int e = 0; e < EPC; ++e) nanf |= T::elem(w, e) != T::elem(w, e);
-    }
-    if (wid == 0) nanf |= xt != xt;
-    const int anynan = block_max_i64(nanf ? 1 : 0, red) != 0;
-    uniform_row(anynan ? __builtin_nanf("") : __builtin_inff());
-    return 0;
-  }
-  if (over != 0) { __syncthreads(); return 1; }
-  // The candidates, straight as sort keys (scaled value, token id): the elements of the
-  // wave's own staged chunks, and in wave 0 the tail tokens, penalized at history
-  // positions (sampler.py:37) and kept when they still reach tc.  A penalty >= 1 never
-  // raises a value, so every element of the top-k reaches tc after the penalty too;
-  // when k of them do, the list holds the whole top-k and its ties.
-  {
-    auto take_key = [&](float x, uint32_t id, bool live) {
-      if (live && pen_on && ((bm[id >> 5] >> (id & 31)) & 1u)) x = pen_val(x);
-      const bool t = live && x >= tc && x > -__builtin_inff();
-      const uint64_t m = ballot(t);
-      if (m == 0ull) return;
-      const int leader = __builtin_ctzll(m);
-      int base = 0;
-      if (lane == leader) base = atomicAdd(&misc->cand_n, __popcll(m));
-      base = read_lane(base, leader);
-      const int pos = base + lanes_below(m);
-      if (t && pos < WAVE_CAP) cand[pos] = desc_key(div_rn(x, tdiv, rdiv), id);   // past it: counted only
-    };
-    const int nhc = nh < HIT_PER_WAVE ? nh : HIT_PER_WAVE;
-    for (int j = lane; j < ((nhc * EPC + 63) & ~63); j += 64) {
-      const bool live = j < nhc * EPC;
+  auto take_key = [&](float x, uint32_t id, bool live) {
+    if (live && pen_on && ((bm[id >> 5] >> (id & 31)) & 1u)) x = pen_val(x);
+    const bool t = live && x >= tc && x > -__builtin_inff();
+    // the key before the position, so that its arithmetic overlaps the atomic
+    const uint64_t key = desc_key(div_rn(t ? x : 1.0f, tdiv, rdiv), id);
+    const uint64_t m = ballot(t);
+    if (m == 0ull) return;
+    const int leader = __builtin_ctzll(m);
+    int base = 0;
+    if (lane == leader) base = atomicAdd(&misc->cand_n, __popcll(m));
+    base = read_lane(base, leader);
+    const int pos = base + lanes_below(m);
+    if (t && pos < WAVE_CAP) cand[pos] = key;   // past it: counted only
+  };
+  if (nh > HIT_PER_WAVE) {
+    // more hit chunks than slots: the count goes past WAVE_CAP and the general code
+    // takes the row
+    if (lane == 0) atomicAdd(&misc->cand_n, WAVE_CAP + 1);
+  } else {
+    for (int j = lane; j < ((nh * EPC + 63) & ~63); j += 64) {
+      const bool live = j < nh * EPC;
       const int slot = live ? j / EPC : 0, e = j % EPC;
-      // the whole chunk into registers first: the element is then chosen by selects
-      // (a data-dependent LDS address for it was mis-selected for e >= 2)
-      const uint4 ch = fresh(hdat[slot]);
-      take_key(T::elem(ch, e), (uint32_t)(hidx[slot] * EPC + e), live);
+      const int32_t ci = hidx[slot];
+      const uint4 ch = hdat[slot];
+      take_key(elem_sel<T>(ch, e), (uint32_t)(ci * EPC + e), live);
     }
-    if (ntail > 0 && wid == 0) take_key(xt, (uint32_t)(nfull * EPC + lane), lane < ntail);
   }
+  if (ntail > 0 && wid == 0) take_key(xt, (uint32_t)(nfull * EPC + lane), lane < ntail);
   __syncthreads();   // the list complete
   const int n = misc->cand_n;
   if (n == 0 && !(tc > -__builtin_inff())) { uniform_row(-__builtin_inff()); return 0; }   // every logit -inf
   if (n > WAVE_CAP || (tc > -__builtin_inff() && n < k)) { __syncthreads(); return 1; }
   zero_probs(o);
-  block_finalize_keys<NT>(cand, n, k, topp < 1.0f, topp, u, row, P.out_ids, P.out_probs, V, P.out_info, flags, n,
-                          PATH_WAVE_SET);
+  block_finalize_keys<NT>(cand, cand + WAVE_CAP, n, k, topp < 1.0f, topp, u, row, P.out_ids, P.out_probs, V,
+                          P.out_info, flags, n, PATH_WAVE_SET);
   return 0;
 }
 

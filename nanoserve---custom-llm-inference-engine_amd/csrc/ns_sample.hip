@@ -1081,16 +1081,21 @@ __device__ __attribute__((noinline)) void row_general(KArgs PA) {
 template <typename T>
 __global__ __launch_bounds__(NT) void sample_kernel(const KParams P) {
   const int row = blockIdx.x;
+  // every per-row parameter is requested before any is used: one round trip to memory
+  // ahead of the row's stream instead of a chain of dependent ones
+  const float temp = P.temperature[row];
+  const int32_t k = P.top_k[row];
+  const float topp = P.top_p[row];
+  const float pen = P.penalty[row];
+  float u = P.uniforms[row];
+  const int64_t src = P.sample_idx ? P.sample_idx[row] : (int64_t)row;
+  int32_t h0 = 0, h1 = 0;
+  if (P.hist_off != nullptr) { h0 = P.hist_off[row]; h1 = P.hist_off[row + 1]; }
   // rows the segment kernel resolved carry status 0; every other row carries 1
   if (P.status != nullptr && P.status[row] == 0) return;
   if (P.fast) {
     // greedy and small-k rows that fit in registers: one streaming pass
-    const float temp = P.temperature[row];
-    const int32_t k = P.top_k[row];
     if (seg_row(temp, k, P.vocab) && row_fits<T>(P.vocab)) {
-      const int64_t src = P.sample_idx ? P.sample_idx[row] : (int64_t)row;
-      int32_t h0 = 0, h1 = 0;
-      if (P.hist_off != nullptr) { h0 = P.hist_off[row]; h1 = P.hist_off[row + 1]; }
       if (src >= 0 && src < P.n_rows_total && h0 >= 0 && h1 >= h0 && h1 - h0 <= MAX_HIST && h1 - h0 <= P.xcap - 8) {
         extern __shared__ __align__(16) unsigned char smem[];
         Misc* misc = reinterpret_cast<Misc*>(smem);
@@ -1098,12 +1103,10 @@ __global__ __launch_bounds__(NT) void sample_kernel(const KParams P) {
         float* xl_val = reinterpret_cast<float*>(smem + P.off_xl);
         int32_t* xl_id = reinterpret_cast<int32_t*>(smem + P.off_xl + 4u * (uint32_t)P.xcap);
         uint64_t* cand = reinterpret_cast<uint64_t*>(smem + P.off_cand);
-        float u = P.uniforms[row];
         u = (u >= 0.0f) ? (u < 1.0f ? u : 0x1.fffffep-1f) : 0.0f;
         const int st = row_fast<T>(RowArgs{P.logits, P.row_stride, P.vocab, P.hist_ids, P.out_ids, P.out_probs,
                                            P.out_info},
-                                   row, src, temp, k, P.top_p[row], P.penalty[row], u, h0, h1 - h0, 0, misc, bm,
-                                   xl_id, xl_val, cand);
+                                   row, src, temp, k, topp, pen, u, h0, h1 - h0, 0, misc, bm, xl_id, xl_val, cand);
         if (st == 0) return;
       }
     }

@@ -534,49 +534,47 @@ __device__ void wave_select_draw_lds(const uint64_t* sorted, int nk, float M, fl
 // The same selection and draw as wave_finalize over n <= WAVE_CAP survivors, with the
 // ordering done by the whole workgroup (NTH threads, all of which must call it).
 // Entry: list[0..n) holds the sort keys (desc_key of the scaled value and token id),
-// the rank counters behind them (list + WAVE_CAP, WAVE_CAP int32) are zero, and a
-// workgroup barrier has passed since both were written; k <= 64.  Each key's position
-// is the number of keys that precede it, counted in parallel slices and summed with
-// LDS atomics; the keys are scattered in place, and wave 0 then runs top-p, softmax
-// and the draw over the top-k prefix.
+// list[n..WAVE_CAP) holds ~0 (it sorts after every key), and a workgroup barrier has
+// passed since both were written; k <= 64.  The keys land in order in
+// sorted[0..n), a region apart from the list.  A key's position is the number of keys
+// below it: G consecutive lanes take one key, each counts one slice of the list, and
+// the group's counts are summed by lane exchanges (no atomics, no second barrier).
+// Wave 0 then runs top-p, softmax and the draw over the top-k prefix.
 template <int NTH>
-__device__ __forceinline__ void block_finalize_keys(uint64_t* list, int n, int k, bool topp_on, float p32, float u,
-                                                    int row, int64_t* out_ids, float* out_probs, int64_t V,
-                                                    int32_t* out_info, int32_t flags, int32_t n_cand,
+__device__ __forceinline__ void block_finalize_keys(const uint64_t* list, uint64_t* sorted, int n, int k, bool topp_on,
+                                                    float p32, float u, int row, int64_t* out_ids, float* out_probs,
+                                                    int64_t V, int32_t* out_info, int32_t flags, int32_t n_cand,
                                                     int32_t path) {
-  static_assert(NTH % 256 == 0, "rank slices assume whole groups of 256 threads");
+  static_assert(NTH == 4 * WAVE_CAP, "8 lanes per key up to WAVE_CAP / 2 keys, 4 lanes per key beyond");
   const int tid = threadIdx.x;
-  int32_t* rank = reinterpret_cast<int32_t*>(list + WAVE_CAP);
-  const uint64_t key = tid < n ? list[tid] : ~0ull;
   {
-    // element i = tid % NI against the keys of slice tid / NI (slices are wave-uniform);
-    // four keys per step keep several LDS reads in flight
-    const int NI = n <= 64 ? 64 : (n <= 128 ? 128 : 256);
-    const int parts = NTH / NI;
-    const int i = tid & (NI - 1), part = tid / NI;
-    const int per = (n + parts - 1) / parts;
-    const int j0 = part * per;
-    const int j1 = j0 + per < n ? j0 + per : n;
-    if (i < n) {
-      const uint64_t ki = list[i];
-      int c = 0;
-      int j = j0;
-      for (; j + 4 <= j1; j += 4) {
-        const uint64_t a0 = list[j], a1 = list[j + 1], a2 = list[j + 2], a3 = list[j + 3];
-        c += (a0 < ki ? 1 : 0) + (a1 < ki ? 1 : 0) + (a2 < ki ? 1 : 0) + (a3 < ki ? 1 : 0);
-      }
-      for (; j < j1; ++j) c += list[j] < ki ? 1 : 0;
-      if (c != 0) atomicAdd(&rank[i], c);
+    const bool g8 = n <= WAVE_CAP / 2;
+    const int G = g8 ? 8 : 4;
+    const int i = g8 ? tid >> 3 : tid >> 2;
+    const int s = tid & (G - 1);
+    // slices of an even length: G * per <= WAVE_CAP, so every read stays in the list
+    const int per = ((n + G - 1) / G + 1) & ~1;
+    const uint64_t ki = list[i];
+    const uint64_t* sl = list + s * per;
+    int c = 0;
+    if (g8) {
+      // per <= 16: every read issued at once (those at j >= per stay inside the list)
+#pragma unroll
+      for (int j = 0; j < 16; ++j) c += (j < per && sl[j] < ki) ? 1 : 0;
+    } else {
+      for (int j = 0; j < per; j += 2) c += (sl[j] < ki ? 1 : 0) + (sl[j + 1] < ki ? 1 : 0);
     }
+    c += lane_xor(c, 1);
+    c += lane_xor(c, 2);
+    if (g8) c += lane_xor(c, 4);
+    if (s == 0 && i < n) sorted[c] = ki;
   }
-  __syncthreads();   // all counts in, all reads of the unsorted keys done
-  if (tid < n) list[rank[tid]] = key;
   __syncthreads();
   if (tid >= 64) return;
   // the first 128 sorted keys in registers: row maximum, k-th largest, kept count
   uint64_t a2[2];
-  a2[0] = tid < n ? list[tid] : ~0ull;
-  a2[1] = 64 + tid < n ? list[64 + tid] : ~0ull;
+  a2[0] = tid < n ? sorted[tid] : ~0ull;
+  a2[1] = 64 + tid < n ? sorted[64 + tid] : ~0ull;
   const float M = desc_key_val(read_lane(a2[0], 0));   // the row maximum
   // top-k threshold: the k-th largest (sampler.py:56-58); every value >= it is kept
   const float thr = n >= k ? desc_key_val(read_lane(a2[0], k - 1)) : -__builtin_inff();
@@ -584,7 +582,7 @@ __device__ __forceinline__ void block_finalize_keys(uint64_t* list, int n, int k
            __popcll(ballot(64 + tid < n && desc_key_val(a2[1]) >= thr));
   for (int base = 128; base < n && nk == base; base += 64) {   // tie group beyond 128 (rare)
     const int i = base + tid;
-    nk += __popcll(ballot(i < n && desc_key_val(list[i < n ? i : 0]) >= thr));
+    nk += __popcll(ballot(i < n && desc_key_val(sorted[i < n ? i : 0]) >= thr));
   }
   if (nk <= 64) {
     const uint64_t a1[1] = {a2[0]};
@@ -592,29 +590,9 @@ __device__ __forceinline__ void block_finalize_keys(uint64_t* list, int n, int k
   } else if (nk <= 128) {
     wave_select_draw<2>(a2, nk, M, thr, topp_on, p32, u, row, out_ids, out_probs, V, out_info, flags, n_cand, path);
   } else {
-    wave_select_draw_lds<4>(list, nk, M, thr, topp_on, p32, u, row, out_ids, out_probs, V, out_info, flags, n_cand,
+    wave_select_draw_lds<4>(sorted, nk, M, thr, topp_on, p32, u, row, out_ids, out_probs, V, out_info, flags, n_cand,
                             path);
   }
-}
-
-// block_finalize_keys over list[0..n) = (value bits << 32) | token id, values not yet
-// scaled by the temperature (tdiv, rdiv = RN(1/tdiv)).
-template <int NTH>
-__device__ __forceinline__ void block_finalize(uint64_t* list, int n, int k, bool topp_on, float p32, float tdiv,
-                                               float rdiv, float u, int row, int64_t* out_ids, float* out_probs,
-                                               int64_t V, int32_t* out_info, int32_t flags, int32_t n_cand,
-                                               int32_t path) {
-  const int tid = threadIdx.x;
-  uint64_t key = ~0ull;
-  if (tid < n) {
-    const uint64_t e = list[tid];
-    key = desc_key(div_rn(__uint_as_float((uint32_t)(e >> 32)), tdiv, rdiv), (uint32_t)e);
-  }
-  __syncthreads();   // every entry read before it is overwritten
-  if (tid < n) list[tid] = key;
-  if (tid < WAVE_CAP) reinterpret_cast<int32_t*>(list + WAVE_CAP)[tid] = 0;
-  __syncthreads();
-  block_finalize_keys<NTH>(list, n, k, topp_on, p32, u, row, out_ids, out_probs, V, out_info, flags, n_cand, path);
 }
 
 // Wave-aggregated append of one candidate (scaled value y, token id) to the
