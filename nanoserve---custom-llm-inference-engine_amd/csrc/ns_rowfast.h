@@ -27,12 +27,13 @@ namespace ns {
 constexpr int RCPT = 16;               // chunks per thread: the whole row in flight
 constexpr int RHB = 2;                 // history ids per thread per batch
 // LDS staging of the chunks that reach the bound, inside the candidate region (u64
-// units): the list and its ordered copy use the first 2 * WAVE_CAP entries
+// units): the list uses the first WAVE_CAP entries, its ordered copies the next
+// 2 * WAVE_CAP (the id-ordered one over the staging slots, which are dead by then)
 constexpr int HIT_PER_WAVE = 48;                               // chunk slots per wave
 constexpr int HIT_OFF64 = 2 * WAVE_CAP;                        // 16-byte chunks
 constexpr int HIT_IDX_OFF64 = HIT_OFF64 + HIT_PER_WAVE * NWAVE * 2;   // chunk indices
 static_assert(KFAST <= 64 && NWAVE * 8 == 128, "the bound: k-th largest of 128 group maxima, k <= 64");
-static_assert(HIT_IDX_OFF64 + HIT_PER_WAVE * NWAVE / 2 <= CAP, "candidate region layout");
+static_assert(HIT_IDX_OFF64 + HIT_PER_WAVE * NWAVE / 2 <= CAP && 3 * WAVE_CAP <= CAP, "candidate region layout");
 
 // An opaque copy of a chunk: values derived from it are recomputed rather than
 // kept alive from an earlier pass (the row's registers leave no room for them).
@@ -137,6 +138,19 @@ __host__ __device__ __forceinline__ bool row_fits(int64_t V) {
   return (V + T::EPC - 1) / T::EPC <= (int64_t)NT * RCPT;
 }
 
+// The row's full chunks into registers, chunk q * NT + t to thread t (chunks past the
+// last full one, nf, read zeros), issued in chunk order: a wave's loads complete in issue
+// order and the passes over the row take the chunks in that order.
+template <typename T>
+__device__ __forceinline__ void issue_row(uint4 (&v)[RCPT], const unsigned char* rowp, int nf) {
+  const int tid = threadIdx.x;
+#pragma unroll
+  for (int q = 0; q < RCPT; ++q) {
+    v[q] = buf_load16_at(rowp, (uint32_t)nf * 16u, (uint32_t)(q * NT * 16), (uint32_t)tid * 16u);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+}
+
 // The kernel arguments row_fast reads, passed by value (a reference to the kernel's
 // argument block would make the compiler copy it to scratch memory).
 struct RowArgs {
@@ -228,11 +242,7 @@ __device__ __forceinline__ int row_fast(const RowArgs P, const int row, const in
     flags |= misc->flags;
     U = misc->xl_n;
     uint4 v[RCPT];
-    {
-#pragma unroll
-      for (int q = 0; q < RCPT; ++q)
-        v[q] = buf_load16_at(rowp, (uint32_t)nf * 16u, (uint32_t)(q * NT * 16), (uint32_t)tid * 16u);
-    }
+    issue_row<T>(v, rowp, nf);
     // the first NT history positions' values: raw bits, converted after the row
     const __amdgpu_buffer_rsrc_t rrow = make_rsrc(rowp, (uint32_t)(V * T::SZ));
     const uint32_t x0raw = gather_raw<T>(rrow, U > 0 ? xl_id[tid < U ? tid : 0] : 0);
@@ -305,17 +315,9 @@ __device__ __forceinline__ int row_fast(const RowArgs P, const int row, const in
 
   // ---- top-k rows with a penalty >= 1 (or none).  Such a penalty never raises a value
   // and keeps NaN and +inf, so the row is processed raw and the candidates are penalized
-  // at the end.  The history ids and the tail tokens are requested behind the row: loads
-  // complete in issue order, and scattered requests are served after the row's streaming
-  // ones anyway.
-  uint4 v[RCPT];
-#pragma unroll
-  for (int q = 0; q < RCPT; ++q) {
-    // issued in chunk order (a wave's loads complete in issue order, and the pass below
-    // takes the chunks in that order)
-    v[q] = buf_load16_at(rowp, (uint32_t)nf * 16u, (uint32_t)(q * NT * 16), (uint32_t)tid * 16u);
-    __builtin_amdgcn_sched_barrier(0);
-  }
+  // at the end.  The history ids and the tail tokens are requested ahead of the row, so
+  // they are in registers when the bitmap is built after the stream (a wave's loads
+  // complete in issue order; the few ids hold up the first chunk only).
   int32_t hid[RHB];   // unconditional loads (bounds-checked by the descriptor) keep the counts exact
   {
     const __amdgpu_buffer_rsrc_t rh = make_rsrc(hp, pen_on ? (uint32_t)H * 4u : 0u);
@@ -327,6 +329,9 @@ __device__ __forceinline__ int row_fast(const RowArgs P, const int row, const in
   // token nfull * EPC + l, zero past the row; wave 0 keeps them
   const int ntail = (int)(V - nfull * EPC);
   const uint32_t xtraw = gather_raw<T>(make_rsrc(rowp, (uint32_t)(V * T::SZ)), (int32_t)(nfull * EPC) + lane);
+  __builtin_amdgcn_sched_barrier(0);
+  uint4 v[RCPT];
+  issue_row<T>(v, rowp, nf);
   // LDS set-up while the row streams, with no barrier: a wave finishes issuing its loads
   // only as the row drains, so a barrier here would hold every wave until then.  The list
   // is padded with keys that sort last and the bitmap cleared; the first barrier below
@@ -378,7 +383,8 @@ __device__ __forceinline__ int row_fast(const RowArgs P, const int row, const in
     uniform_row(anynan ? __builtin_nanf("") : __builtin_inff());
     return 0;
   }
-  // the history bitmap (set semantics, sampler.py:34-38), while wave 0 finds the bound
+  // the history bitmap (set semantics, sampler.py:34-38), built by every wave (no wave waits
+  // for its atomics before the barrier)
   if (pen_on) {
     bool bad = false;
     for (int base = 0; base < H; base += RHB * NT) {

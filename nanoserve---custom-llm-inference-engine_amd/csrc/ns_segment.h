@@ -531,43 +531,145 @@ __device__ void wave_select_draw_lds(const uint64_t* sorted, int nk, float M, fl
   wave_select_draw<R>(a, nk, M, thr, topp_on, p32, u, row, out_ids, out_probs, V, out_info, flags, n_cand, path);
 }
 
+// Top-p, softmax and inverse-CDF draw by one wave over the nk <= 64 survivors of the
+// top-k cut, the ordering already done by the workgroup: a holds the sorted keys
+// (element i = lane; scaled value descending, token id ascending), byid[0..n) the same
+// n <= 128 candidates in ascending token-id order and vr[0..n) the sorted position of
+// each.  One float64 prefix sum of the softmax numerators gives both normalisers (the
+// top-k set's and the kept set's, sampler.py:65 and :76), and the draw runs over the
+// id-ordered candidates with probability 0 for those not kept, so nothing is sorted
+// here.  Probabilities are the float32 roundings of the numerators times the float64
+// reciprocal of the normaliser.
+__device__ __forceinline__ void wave_draw_sorted(uint64_t a, int nk, int n, const uint64_t* byid, const int32_t* vr,
+                                                 float M, float thr, bool topp_on, float p32, float u, int row,
+                                                 int64_t* out_ids, float* out_probs, int64_t V, int32_t* out_info,
+                                                 int32_t flags, int32_t n_cand, int32_t path) {
+  const int lane = lane_id();
+  const uint64_t b0 = lane < n ? byid[lane] : ~0ull;
+  const uint64_t b1 = 64 + lane < n ? byid[64 + lane] : ~0ull;
+  const int r0 = lane < n ? vr[lane] : 64;
+  const int r1 = 64 + lane < n ? vr[64 + lane] : 64;
+  const float ev = lane < nk ? ns_expf(desc_key_val(a) - M) : 0.0f;
+  const double cs = wave_incl_scan((double)ev);
+  int nf = nk;
+  float vstar = -__builtin_inff();
+  int32_t istar = -1;
+  if (topp_on) {
+    const double rz = 1.0 / read_lane(cs, nk - 1);
+    const double cq = wave_incl_scan((double)(float)((double)ev * rz));
+    // first sorted position whose float32 prefix exceeds top_p; it is kept (sampler.py:66-72)
+    const uint64_t m = ballot(lane < nk && (float)cq > p32);
+    if (m != 0ull) nf = __builtin_ctzll(m) + 1;
+    const uint64_t kc = read_lane(a, nf - 1);
+    vstar = desc_key_val(kc);
+    istar = (int32_t)desc_key_id(kc);
+  }
+  const double rz2 = 1.0 / read_lane(cs, nf - 1);
+  // final probabilities of the kept candidates (sorted position < nf), in id order
+  const bool k0 = r0 < nf, k1 = r1 < nf;
+  const float p0 = k0 ? (float)((double)ns_expf(desc_key_val(b0) - M) * rz2) : 0.0f;
+  const float p1 = k1 ? (float)((double)ns_expf(desc_key_val(b1) - M) * rz2) : 0.0f;
+  const double c0 = wave_incl_scan((double)p0);
+  const double c1 = read_lane(c0, 63) + wave_incl_scan((double)p1);
+  // the first id-order position whose cumulative mass exceeds u (sampler.py:87 as an
+  // inverse CDF); the mass only grows at kept positions
+  const double ud = (double)u;
+  const uint64_t m0 = ballot(c0 > ud), m1 = ballot(c1 > ud);
+  int pick = m0 != 0ull ? __builtin_ctzll(m0) : (m1 != 0ull ? 64 + __builtin_ctzll(m1) : -1);
+  int32_t fl = flags;
+  if (pick < 0) {
+    // rounding left the total at or below u: the last kept position with mass
+    const uint64_t l0 = ballot(p0 > 0.0f), l1 = ballot(p1 > 0.0f);
+    const uint64_t q0 = ballot(k0), q1 = ballot(k1);
+    pick = l1 != 0ull ? 127 - __builtin_clzll(l1)
+         : l0 != 0ull ? 63 - __builtin_clzll(l0)
+         : q0 != 0ull ? __builtin_ctzll(q0) : 64 + __builtin_ctzll(q1);
+    fl |= FLAG_LOCATE_FALLBACK;
+  }
+  const uint32_t i0 = read_lane(desc_key_id(b0), pick & 63), i1 = read_lane(desc_key_id(b1), pick & 63);
+  if (lane == 0) {
+    out_ids[row] = (int64_t)(pick < 64 ? i0 : i1);
+    seg_write_info(out_info, row, path, nf, thr, nk, n_cand, fl, vstar, istar);
+  }
+  if (out_probs != nullptr) {
+    float* pr = out_probs + (int64_t)row * V;
+    if (k0) pr[desc_key_id(b0)] = p0;
+    if (k1) pr[desc_key_id(b1)] = p1;
+  }
+}
+
+// Keys of slice s of the list (PER entries) below ki (c) and with a token id below ki's
+// (ci).  Every read is issued before the first compare.
+template <int PER>
+__device__ __forceinline__ void rank_slice(const uint64_t* list, int s, uint64_t ki, int& c, int& ci) {
+  const uint64_t* sl = list + s * PER;
+  uint64_t a[PER];
+#pragma unroll
+  for (int j = 0; j < PER; ++j) a[j] = sl[j];
+#pragma unroll
+  for (int j = 0; j < PER; ++j) {
+    c += a[j] < ki ? 1 : 0;
+    ci += (uint32_t)a[j] < (uint32_t)ki ? 1 : 0;
+  }
+}
+
 // The same selection and draw as wave_finalize over n <= WAVE_CAP survivors, with the
 // ordering done by the whole workgroup (NTH threads, all of which must call it).
 // Entry: list[0..n) holds the sort keys (desc_key of the scaled value and token id),
 // list[n..WAVE_CAP) holds ~0 (it sorts after every key), and a workgroup barrier has
-// passed since both were written; k <= 64.  The keys land in order in
-// sorted[0..n), a region apart from the list.  A key's position is the number of keys
-// below it: G consecutive lanes take one key, each counts one slice of the list, and
-// the group's counts are summed by lane exchanges (no atomics, no second barrier).
-// Wave 0 then runs top-p, softmax and the draw over the top-k prefix.
+// passed since both were written; k <= 64.  out[] is a region apart from the list of
+// 2 * WAVE_CAP entries: the keys land in order in out[0..n), and for n <= 128 also in
+// ascending token-id order in out[WAVE_CAP..), with their sorted positions behind them.
+// A key's position is the number of keys below it: G consecutive lanes take one key,
+// each counts one slice of the list, and the group's counts are summed by lane
+// exchanges (no atomics, no second barrier).  Wave 0 then runs top-p, softmax and the
+// draw over the top-k prefix.
 template <int NTH>
-__device__ __forceinline__ void block_finalize_keys(const uint64_t* list, uint64_t* sorted, int n, int k, bool topp_on,
+__device__ __forceinline__ void block_finalize_keys(const uint64_t* list, uint64_t* out, int n, int k, bool topp_on,
                                                     float p32, float u, int row, int64_t* out_ids, float* out_probs,
                                                     int64_t V, int32_t* out_info, int32_t flags, int32_t n_cand,
                                                     int32_t path) {
   static_assert(NTH == 4 * WAVE_CAP, "8 lanes per key up to WAVE_CAP / 2 keys, 4 lanes per key beyond");
   const int tid = threadIdx.x;
+  uint64_t* sorted = out;
+  uint64_t* byid = out + WAVE_CAP;
+  int32_t* vr = reinterpret_cast<int32_t*>(out + WAVE_CAP + WAVE_CAP / 2);
+  const bool g8 = n <= WAVE_CAP / 2;
   {
-    const bool g8 = n <= WAVE_CAP / 2;
     const int G = g8 ? 8 : 4;
     const int i = g8 ? tid >> 3 : tid >> 2;
     const int s = tid & (G - 1);
-    // slices of an even length: G * per <= WAVE_CAP, so every read stays in the list
-    const int per = ((n + G - 1) / G + 1) & ~1;
     const uint64_t ki = list[i];
-    const uint64_t* sl = list + s * per;
-    int c = 0;
+    int c = 0, ci = 0;
     if (g8) {
-      // per <= 16: every read issued at once (those at j >= per stay inside the list)
-#pragma unroll
-      for (int j = 0; j < 16; ++j) c += (j < per && sl[j] < ki) ? 1 : 0;
+      // slice s: [s * PER, s * PER + PER), PER = ceil(n / 8) rounded up to 2 mod 4 (<= 18),
+      // so the 8 slices start in distinct LDS banks; the padding past n never counts and
+      // waves whose keys all lie past n skip the count.  ci counts the smaller token ids.
+      if (wave_id() * 8 < n) {
+        const int cls = ((n + 7) >> 3) + 1 >> 2;   // PER = 4 * cls + 2
+        if (cls == 0) rank_slice<2>(list, s, ki, c, ci);
+        else if (cls == 1) rank_slice<6>(list, s, ki, c, ci);
+        else if (cls == 2) rank_slice<10>(list, s, ki, c, ci);
+        else if (cls == 3) rank_slice<14>(list, s, ki, c, ci);
+        else rank_slice<18>(list, s, ki, c, ci);
+      }
     } else {
-      for (int j = 0; j < per; j += 2) c += (sl[j] < ki ? 1 : 0) + (sl[j + 1] < ki ? 1 : 0);
+      const uint64_t* sl = list + s * (WAVE_CAP / 4);
+#pragma unroll 8
+      for (int j = 0; j < WAVE_CAP / 4; ++j) c += sl[j] < ki ? 1 : 0;
     }
     c += lane_xor(c, 1);
     c += lane_xor(c, 2);
-    if (g8) c += lane_xor(c, 4);
-    if (s == 0 && i < n) sorted[c] = ki;
+    if (g8) {
+      c += lane_xor(c, 4);
+      ci += lane_xor(ci, 1);
+      ci += lane_xor(ci, 2);
+      ci += lane_xor(ci, 4);
+    }
+    if (s == 0 && i < n) {
+      sorted[c] = ki;
+      if (g8) { byid[ci] = ki; vr[ci] = c; }
+    }
   }
   __syncthreads();
   if (tid >= 64) return;
@@ -584,7 +686,10 @@ __device__ __forceinline__ void block_finalize_keys(const uint64_t* list, uint64
     const int i = base + tid;
     nk += __popcll(ballot(i < n && desc_key_val(sorted[i < n ? i : 0]) >= thr));
   }
-  if (nk <= 64) {
+  if (nk <= 64 && g8) {
+    wave_draw_sorted(a2[0], nk, n, byid, vr, M, thr, topp_on, p32, u, row, out_ids, out_probs, V, out_info, flags,
+                     n_cand, path);
+  } else if (nk <= 64) {
     const uint64_t a1[1] = {a2[0]};
     wave_select_draw<1>(a1, nk, M, thr, topp_on, p32, u, row, out_ids, out_probs, V, out_info, flags, n_cand, path);
   } else if (nk <= 128) {
