@@ -1,6 +1,6 @@
 """Benchmark of the MI355X token sampler (one ns_sample launch per step).
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--cpu-rows R]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--cpu-rows R] [--config C]
 
 Workload: the decode-heavy batch -- 256 sampled rows x vocab 128256, logits
 stored as bfloat16 (N(0, 3^2)) and upcast in the kernel, temperature 1.0,
@@ -16,6 +16,11 @@ events on the stream the kernel is launched on.
 Prints one JSON line: rows/s (whole job), the roofline of the sampling
 kernel against MI355X's 8 TB/s HBM peak, and the CPU baseline (the reference
 sampler's op sequence restated on torch CPU, timed on this host).
+
+``--config C`` times another of the five workloads instead (0: B=8 fp32; 1: B=64
+mixed parameters; 3: B=128 x 256000 fp32, top-p 0.99; 4: 320 of 4096 rows through
+sample indices); its input sets are copies of the workload's own logits rolled
+along the vocabulary, so every set keeps the workload's value distribution.
 """
 from __future__ import annotations
 
@@ -46,8 +51,10 @@ def _pkg(sub=""):
     return importlib.import_module(PKG + ("." + sub if sub else ""))
 
 
-def build_sets(w, dev, n_sets):
-    """Device inputs for ``n_sets`` independent calls over workload ``w``."""
+def build_sets(w, dev, n_sets, roll=False):
+    """Device inputs for ``n_sets`` independent calls over workload ``w`` (sets after the
+    first: fresh N(0, 3^2) logits, or with ``roll`` the workload's own rolled along the
+    vocabulary)."""
     import torch
 
     S = _pkg("sampler")
@@ -58,6 +65,8 @@ def build_sets(w, dev, n_sets):
     for s in range(n_sets):
         if s == 0:
             logits = w.device_logits(dev)
+        elif roll:
+            logits = torch.roll(w.device_logits(dev, rotate=s), shifts=7919 * s, dims=1).contiguous()
         else:
             g = torch.Generator(device=dev)
             g.manual_seed(5150 + s)
@@ -71,7 +80,8 @@ def build_sets(w, dev, n_sets):
         u = w.uniforms if s == 0 else rng.random(w.batch, dtype=np.float32)
         ut = torch.from_numpy(np.asarray(u, dtype=np.float32)).to(dev)
         out = torch.empty(w.batch, dtype=torch.int64, device=dev)
-        sets.append(dict(logits=logits, d=d, max_hist=packed.max_hist, u=ut, out=out))
+        sidx = None if w.sample_indices is None else torch.from_numpy(w.sample_indices).to(dev)
+        sets.append(dict(logits=logits, d=d, max_hist=packed.max_hist, u=ut, out=out, sidx=sidx))
     torch.cuda.synchronize()
     return sets
 
@@ -88,7 +98,7 @@ def make_args(L, st, ws):
     a.n_rows_total = int(logits.shape[0])
     a.vocab = int(logits.shape[1])
     a.row_stride = int(logits.stride(0))
-    a.sample_idx = 0
+    a.sample_idx = 0 if st["sidx"] is None else st["sidx"].data_ptr()
     a.temperature = d["temperature"].data_ptr()
     a.top_k = d["top_k"].data_ptr()
     a.top_p = d["top_p"].data_ptr()
@@ -150,6 +160,8 @@ def main(argv=None):
     ap.add_argument("--warmup", type=int, default=40)
     ap.add_argument("--cpu-rows", type=int, default=256, help="rows in the CPU-baseline sample (0 = skip)")
     ap.add_argument("--cpu-reps", type=int, default=3)
+    ap.add_argument("--config", type=int, default=WORKLOAD_CFG, choices=range(5),
+                    help="workload to time (default: the decode batch the metric is quoted on)")
     ap.add_argument("--copy-mb", type=int, default=0,
                     help="after the timed loop, run 4 plain device copies of this many MiB (a known-size "
                          "reference for HBM byte counters under rocprofv3 --pmc)")
@@ -170,8 +182,8 @@ def main(argv=None):
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
 
-    w = W.make_workload(WORKLOAD_CFG)
-    sets = build_sets(w, dev, ROTATE)
+    w = W.make_workload(args.config)
+    sets = build_sets(w, dev, ROTATE, roll=args.config != WORKLOAD_CFG)
     ws = L.workspace_for(dev, w.batch, w.vocab, L.NS_DTYPE_BF16 if w.bf16_bits is not None else L.NS_DTYPE_F32)
     cargs = [make_args(L, st, ws) for st in sets]
     stream = torch.cuda.current_stream(dev)
@@ -207,13 +219,14 @@ def main(argv=None):
                                repetition_penalty=float(w.repetition_penalty[i])) for i in range(w.batch)]
     hist_lists = [list(map(int, h)) for h in w.histories]
     sampler = S.Sampler(dev)
+    kw = dict(uniforms=sets[0]["u"], sample_indices=sets[0]["sidx"])
     for _ in range(3):
-        sampler.sample(sets[0]["logits"], params, hist_lists, uniforms=sets[0]["u"])
+        sampler.sample(sets[0]["logits"], params, hist_lists, **kw)
     torch.cuda.synchronize()
     nwrap = 10
     t1 = time.perf_counter()
     for _ in range(nwrap):
-        ids = sampler.sample(sets[0]["logits"], params, hist_lists, uniforms=sets[0]["u"])
+        ids = sampler.sample(sets[0]["logits"], params, hist_lists, **kw)
     ids.tolist()
     wrap_ms = (time.perf_counter() - t1) / nwrap * 1e3
 
@@ -227,6 +240,26 @@ def main(argv=None):
         del src, dst
 
     cpu = cpu_baseline(w, args.cpu_rows, args.cpu_reps) if args.cpu_rows > 0 else None
+    if args.config != WORKLOAD_CFG:
+        desc = {0: "batch B=8 x V=128256 fp32, t=0.8 top_k=50 top_p=0.9 penalty=1.1, 64 history ids/row",
+                1: "batch B=64 x V=128256 fp32, mixed per-row parameters (greedy and sampled), 512 Zipf ids/row",
+                3: "batch B=128 x V=256000 fp32 heavy-tailed logits, t=1.2 top_p=0.99, no penalty",
+                4: "320 sampled rows of a 4096 x 128256 fp32 flat tensor (sample indices), mixed parameters, "
+                   "histories U[1,4096]"}[args.config]
+        nb = f"B={w.batch}, V={w.vocab} {w.dtype}"
+        line = {"metric": f"sampled rows/sec at {nb}; achieved HBM GB/s vs peak", "value": rows_per_s,
+                "unit": "rows/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+                "ms_per_step": ms_per_step, "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+                "dtype": "f32", "data": "synthetic (the workload's seeded logits, rolled per input set)",
+                "config": {"workload": desc, "batch": w.batch, "vocab": w.vocab, "rotating_input_sets": ROTATE,
+                           "parallelism": "single GPU"},
+                "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                             "frac": achieved / HBM_PEAK_GBS, "traffic": None},
+                "cpu_baseline": cpu,
+                "extra": {"algorithmic_bytes_per_call": bytes_per_call, "kernel_us": ms_per_step * 1e3,
+                          "wall_s": wall, "wrapper_inclusive_ms": wrap_ms}}
+        print(json.dumps(line), flush=True)
+        return 0
     line = {
         "metric": METRIC,
         "value": rows_per_s,
