@@ -81,7 +81,8 @@ def build_sets(w, dev, n_sets, roll=False):
         ut = torch.from_numpy(np.asarray(u, dtype=np.float32)).to(dev)
         out = torch.empty(w.batch, dtype=torch.int64, device=dev)
         sidx = None if w.sample_indices is None else torch.from_numpy(w.sample_indices).to(dev)
-        sets.append(dict(logits=logits, d=d, max_hist=packed.max_hist, u=ut, out=out, sidx=sidx))
+        sets.append(dict(logits=logits, d=d, max_hist=packed.max_hist, u=ut, out=out, sidx=sidx,
+                         kinds=packed.row_kinds))
     torch.cuda.synchronize()
     return sets
 
@@ -112,6 +113,7 @@ def make_args(L, st, ws):
     a.out_info = 0
     a.workspace = ws.data_ptr()
     a.workspace_bytes = ws.numel()
+    a.row_kinds = st["kinds"]
     return a
 
 

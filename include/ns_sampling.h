@@ -26,7 +26,7 @@
 extern "C" {
 #endif
 
-#define NS_ABI_VERSION 3
+#define NS_ABI_VERSION 4
 
 #define NS_OK 0
 #define NS_ERR_INVALID 1   /* bad argument (message says which) */
@@ -40,10 +40,15 @@ extern "C" {
 #define NS_MODE_SEGMENTED 1   /* greedy and small-k rows split over several workgroups (needs a workspace) */
 #define NS_MODE_PER_ROW 2     /* one workgroup per row for every row */
 
+#define NS_KIND_GREEDY 1      /* row_kinds: greedy rows (temperature 0) */
+#define NS_KIND_SMALL_K 2     /* row_kinds: sampled rows with 1 <= top_k <= 64 and top_k < vocab */
+#define NS_KIND_OTHER 4       /* row_kinds: every other sampled row (top-k off, or top_k > 64) */
+
 #define NS_MAX_VOCAB 262144     /* vocab limit (LDS presence bitmap of vocab/8 bytes) */
 #define NS_MAX_HISTORY 8192     /* per-row history limit (the reference's max_model_len, config.py:52) */
 #define NS_INFO_WORDS 8         /* int32 words per row in out_info */
 #define NS_SEG_MAX_ROWS 16384   /* most rows a segmented call takes (AUTO switches to per-row above) */
+#define NS_WIDE_MAX_ROWS 4096   /* most rows a call splits over segment workgroups (NS_KIND_OTHER rows) */
 
 /* Per-row diagnostics written to out_info[row * NS_INFO_WORDS + w]:
  *   w=0 path (1 greedy, 2 uniform/NaN guard, 3 top-k set, 4 generic set, 5 large draw,
@@ -85,9 +90,14 @@ typedef struct ns_sample_args {
                                    zero-filled before its first use; calls of any shape may share it (the
                                    library leaves its persistent counters at zero after every call), one
                                    call at a time (one stream).  NULL: every row takes the
-                                   one-workgroup-per-row kernel.  Only read in segmented mode. */
+                                   one-workgroup-per-row kernel.  Read in segmented mode and, outside
+                                   NS_MODE_PER_ROW, for the NS_KIND_OTHER rows: those are split over
+                                   segment workgroups across the whole GPU (batches up to
+                                   NS_WIDE_MAX_ROWS rows). */
   uint64_t       workspace_bytes;
   int32_t        mode;          /* NS_MODE_*: which kernels resolve which rows (results are identical) */
+  uint32_t       row_kinds;     /* NS_KIND_* bits of the kinds of rows present, or 0 when unknown: a call
+                                   declared without NS_KIND_OTHER rows skips the launches for them */
 } ns_sample_args;
 
 /* Version of this ABI (NS_ABI_VERSION). */

@@ -21,7 +21,10 @@ NS_INFO_WORDS = 8
 NS_MODE_AUTO = 0
 NS_MODE_SEGMENTED = 1
 NS_MODE_PER_ROW = 2
-ABI_VERSION = 3
+NS_KIND_GREEDY = 1      # row_kinds: greedy rows (temperature 0)
+NS_KIND_SMALL_K = 2     # sampled rows with 1 <= top_k <= 64 and top_k < vocab
+NS_KIND_OTHER = 4       # every other sampled row (top-k off or larger)
+ABI_VERSION = 4
 
 # exported symbols, as declared in include/ns_sampling.h
 EXPORTS = ("ns_abi_version", "ns_sample", "ns_sample_lds_bytes", "ns_sample_workspace_bytes", "ns_last_error")
@@ -52,6 +55,7 @@ class NsSampleArgs(ctypes.Structure):
         ("workspace", ctypes.c_void_p),
         ("workspace_bytes", ctypes.c_uint64),
         ("mode", ctypes.c_int32),
+        ("row_kinds", ctypes.c_uint32),
     ]
 
 
@@ -130,6 +134,24 @@ def workspace_for(device, n_sample: int, vocab: int, dtype: int):
     return ws
 
 
+def row_kinds(temperature, top_k, vocab: int) -> int:
+    """NS_KIND_* bits of the rows described by host arrays of temperatures and top_k values."""
+    import numpy as np
+
+    t = np.asarray(temperature)
+    k = np.asarray(top_k)
+    greedy = t == 0.0
+    small = ~greedy & (k >= 1) & (k <= 64) & (k < vocab)
+    kinds = 0
+    if greedy.any():
+        kinds |= NS_KIND_GREEDY
+    if small.any():
+        kinds |= NS_KIND_SMALL_K
+    if (~greedy & ~small).any():
+        kinds |= NS_KIND_OTHER
+    return kinds
+
+
 def _ptr(t) -> int:
     return 0 if t is None else int(t.data_ptr())
 
@@ -159,7 +181,7 @@ def aligned_rows(logits, sample_idx):
 
 def sample_raw(logits, temperature, top_k, top_p, rep_penalty, uniforms, out_ids, *, sample_idx=None,
                hist_offsets=None, hist_ids=None, max_hist: int = 0, out_probs=None, out_info=None,
-               stream=None, workspace="auto", mode: int = NS_MODE_AUTO) -> None:
+               stream=None, workspace="auto", mode: int = NS_MODE_AUTO, row_kinds: int = 0) -> None:
     """Launch ``ns_sample`` on device tensors (no copies, no synchronisation).
 
     logits: (N, V) float32 or bfloat16 CUDA tensor with unit stride in the last dim.
@@ -167,7 +189,8 @@ def sample_raw(logits, temperature, top_k, top_p, rep_penalty, uniforms, out_ids
     sample_idx: (B,) int64 or None; hist_offsets: (B+1,) int32; hist_ids: int32;
     out_ids: (B,) int64; out_probs: (B, V) float32 or None; out_info: (B, 8) int32 or None.
     workspace: "auto" (a cached per-device workspace), a uint8 CUDA tensor, or None (every row
-    takes the one-workgroup-per-row kernel).
+    takes the one-workgroup-per-row kernel).  row_kinds: NS_KIND_* bits of the rows present
+    (see ``row_kinds``), 0 when unknown.
     """
     import torch
 
@@ -207,6 +230,7 @@ def sample_raw(logits, temperature, top_k, top_p, rep_penalty, uniforms, out_ids
         a.workspace = _ptr(workspace)
         a.workspace_bytes = int(workspace.numel() * workspace.element_size())
     a.mode = int(mode)
+    a.row_kinds = int(row_kinds)
     if stream is None:
         stream = torch.cuda.current_stream(logits.device)
     check(lib.ns_sample(ctypes.byref(a), ctypes.c_void_p(int(stream.cuda_stream))))

@@ -10,7 +10,10 @@
 
 #include "ns_sample_kernel.h"
 #include "ns_segment.h"
+#include "ns_wide.h"
 #include "ns_sampling.h"
+
+static_assert(ns::WIDE_MAX_ROWS == NS_WIDE_MAX_ROWS, "wide-path row limit");
 
 namespace ns {
 
@@ -1132,7 +1135,7 @@ int64_t seg_count(int64_t vocab, int32_t dtype) { return (vocab + seg_elems(dtyp
 int64_t align256(int64_t x) { return (x + 255) / 256 * 256; }
 
 struct WsLayout {
-  int64_t counters, status, stats, cand, total;
+  int64_t counters, status, stats, cand, wrow, hcnt, hmass, total;
 };
 // Workspace layout.  The per-row arrival counters are the only state that outlives a
 // call (each call leaves them at zero): they sit at fixed positions at the start, sized
@@ -1147,7 +1150,12 @@ WsLayout ws_layout(int32_t n_sample, int64_t vocab, int32_t dtype) {
   L.status = align256((int64_t)NS_SEG_MAX_ROWS * 4);
   L.stats = L.status + align256(rows * 4);
   L.cand = L.stats + align256(rows * S * (int64_t)sizeof(ns::SegStat));
-  L.total = L.cand + align256(rows * S * ns::SEG_CAP * 8);
+  // wide path: per-row plans and histograms, for up to NS_WIDE_MAX_ROWS rows
+  const int64_t wrows = rows < NS_WIDE_MAX_ROWS ? rows : NS_WIDE_MAX_ROWS;
+  L.wrow = L.cand + align256(rows * S * ns::SEG_CAP * 8);
+  L.hcnt = L.wrow + align256(wrows * (int64_t)sizeof(ns::WideRow));
+  L.hmass = L.hcnt + align256(wrows * ns::WBINS * 4);
+  L.total = L.hmass + align256(wrows * ns::WBINS * 8);
   return L;
 }
 }  // namespace
@@ -1263,9 +1271,12 @@ int ns_sample(const ns_sample_args* a, hipStream_t stream) {
   bool segmented = a->workspace != nullptr && a->mode != NS_MODE_PER_ROW;
   if (a->mode == NS_MODE_AUTO && ((int64_t)a->n_sample * 8 >= (int64_t)n_cu * 7 || a->n_sample > NS_SEG_MAX_ROWS))
     segmented = false;
-  if (segmented) {
-    if (a->n_sample > NS_SEG_MAX_ROWS)
-      return fail(NS_ERR_INVALID, "segmented mode takes at most " + std::to_string(NS_SEG_MAX_ROWS) + " rows");
+  // wide path for the rows neither the streaming nor the segment kernels take
+  const bool wide = a->workspace != nullptr && a->mode != NS_MODE_PER_ROW && a->n_sample <= NS_WIDE_MAX_ROWS &&
+                    (a->row_kinds == 0u || (a->row_kinds & NS_KIND_OTHER) != 0u);
+  if (segmented && a->n_sample > NS_SEG_MAX_ROWS)
+    return fail(NS_ERR_INVALID, "segmented mode takes at most " + std::to_string(NS_SEG_MAX_ROWS) + " rows");
+  if (segmented || wide) {
     if (a->workspace_bytes < (uint64_t)L.total)
       return fail(NS_ERR_INVALID, "workspace of " + std::to_string(a->workspace_bytes) + " bytes, " +
                                       std::to_string(L.total) + " needed (ns_sample_workspace_bytes)");
@@ -1312,7 +1323,60 @@ int ns_sample(const ns_sample_args* a, hipStream_t stream) {
     if (e != hipSuccess) return fail(NS_ERR_HIP, std::string("segment kernel launch: ") + hipGetErrorString(e));
   }
 
-  // 2) one workgroup per row: every other row, and rows the segment kernel deferred
+  // 2) wide path: rows with top-k off or k > 64, each over the segment workgroups of the
+  //    whole GPU; rows it cannot plan keep status 1
+  if (wide) {
+    const int64_t S = seg_count(a->vocab, a->dtype);
+    if (S > ns::MAX_SEGS) return fail(NS_ERR_INVALID, "vocab too large for the segment workgroups");
+    const int64_t nblk = ((int64_t)a->n_sample + 7) / 8 * 8 * S;
+    unsigned char* ws = static_cast<unsigned char*>(a->workspace);
+    ns::WideParams w{};
+    w.logits = a->logits;
+    w.row_stride = a->row_stride;
+    w.vocab = a->vocab;
+    w.n_rows_total = a->n_rows_total;
+    w.sample_idx = a->sample_idx;
+    w.temperature = a->temperature;
+    w.top_k = a->top_k;
+    w.top_p = a->top_p;
+    w.penalty = a->rep_penalty;
+    w.hist_off = a->hist_offsets;
+    w.hist_ids = a->hist_ids;
+    w.uniforms = a->uniforms;
+    w.out_ids = a->out_ids;
+    w.out_probs = a->out_probs;
+    w.out_info = a->out_info;
+    w.n_sample = a->n_sample;
+    w.S = (int32_t)S;
+    w.init_status = segmented ? 0 : 1;
+    w.counters = reinterpret_cast<int32_t*>(ws + L.counters);
+    w.status = reinterpret_cast<int32_t*>(ws + L.status);
+    w.rows = reinterpret_cast<ns::WideRow*>(ws + L.wrow);
+    w.segs = reinterpret_cast<ns::WideSeg*>(ws + L.stats);
+    w.hcnt = reinterpret_cast<uint32_t*>(ws + L.hcnt);
+    w.hmass = reinterpret_cast<uint64_t*>(ws + L.hmass);
+    w.cand = reinterpret_cast<uint64_t*>(ws + L.cand);
+    p.status = w.status;
+    const dim3 g((unsigned)nblk), bs(ns::SNT);
+    const bool bf = a->dtype == NS_DTYPE_BF16;
+    if (bf) hipLaunchKernelGGL((ns::wide_stats_kernel<ns::BF16>), g, bs, 0, stream, w);
+    else hipLaunchKernelGGL((ns::wide_stats_kernel<ns::F32>), g, bs, 0, stream, w);
+    if (bf) hipLaunchKernelGGL((ns::wide_hist_kernel<ns::BF16>), g, bs, 0, stream, w);
+    else hipLaunchKernelGGL((ns::wide_hist_kernel<ns::F32>), g, bs, 0, stream, w);
+    if (bf) hipLaunchKernelGGL((ns::wide_cut_kernel<ns::BF16>), g, bs, 0, stream, w);
+    else hipLaunchKernelGGL((ns::wide_cut_kernel<ns::F32>), g, bs, 0, stream, w);
+    const dim3 gr((unsigned)a->n_sample), br(ns::NT);
+    if (bf) hipLaunchKernelGGL((ns::wide_final_kernel<ns::BF16>), gr, br, 0, stream, w);
+    else hipLaunchKernelGGL((ns::wide_final_kernel<ns::F32>), gr, br, 0, stream, w);
+    if (a->out_probs != nullptr) {
+      if (bf) hipLaunchKernelGGL((ns::wide_probs_kernel<ns::BF16>), g, bs, 0, stream, w);
+      else hipLaunchKernelGGL((ns::wide_probs_kernel<ns::F32>), g, bs, 0, stream, w);
+    }
+    e = hipGetLastError();
+    if (e != hipSuccess) return fail(NS_ERR_HIP, std::string("wide kernel launch: ") + hipGetErrorString(e));
+  }
+
+  // 3) one workgroup per row: every other row, and rows the segment kernel deferred
   const dim3 grid((unsigned)a->n_sample), block(ns::NT);
   const void* fn = a->dtype == NS_DTYPE_BF16 ? reinterpret_cast<const void*>(&ns::sample_kernel<ns::BF16>)
                                              : reinterpret_cast<const void*>(&ns::sample_kernel<ns::F32>);

@@ -1,0 +1,1139 @@
+// gfx950 wide path: sampled rows whose top-k is off (k <= 0 or k >= V) or larger than
+// KFAST -- the rows the streaming and segment paths leave to one workgroup.  Each row is
+// split over the segment kernel's 16-byte-chunk segments, so every CU works on it, and
+// sampler.py:31-89 runs in up to four launches over (row, segment) workgroups:
+//   1. stats  (the HBM pass): scaled logits y (penalty sampler.py:31-38 with set
+//      semantics, temperature :40-51) -> row max M, finite count, NaN / +inf flags.
+//      The last segment of a row resolves NaN / +inf / all -inf rows (uniform 1/V,
+//      :77-80) and clears the row's histograms.
+//   2. hist   (re-read from L2 / Infinity Cache): count and fixed-point mass histograms
+//      of exp(y - M) in bins of 1/64 below M, and each segment's mass.  The last
+//      segment plans the row: without top-k and top-p it draws at once; otherwise it
+//      finds the bin holding the k-th largest (:56-58) and the bins where the top-p
+//      mass crosses (:60-73).
+//   3. cut    (re-read): the planned bins' elements are compacted per segment, with the
+//      mass of each segment above them.  The last segment orders the compacted
+//      elements (value descending, id ascending) and finds the exact top-k threshold,
+//      the top-p cut as the oracle defines it (float32 prefix of float32 probabilities),
+//      the kept set's mass per segment, and draws.
+//   4. probs  (only with out_probs): every token's final probability.
+// The draw (inverse CDF in token-id order, sampler.py:84-89 against a caller uniform)
+// finds the segment holding u from the per-segment kept masses, then walks that one
+// segment.  Masses are integer sums of exp(y - M) in units of 2^-44, so every pass and
+// every order of accumulation gives the same totals.  Rows this path cannot plan (a
+// k-th largest or top-p crossing more than 32 below the max, more planned elements than
+// WCAND) are left to the per-row kernel (status 1).
+#pragma once
+
+#include "ns_segment.h"
+
+namespace ns {
+
+constexpr int WBINS = 2048;                   // histogram bins below the row max
+constexpr float WSCALE = 64.0f;               // bins per unit of scaled logit (the bins span 32 units)
+constexpr int WCAND = 8192;                   // planned-bin elements one row's finaliser orders
+constexpr int WIDE_MAX_ROWS = 4096;           // rows a call sends through this path
+constexpr double WFX = 17592186044416.0;      // 2^44: fixed-point scale of exp(y - M) <= 1
+constexpr double WFX_INV = 1.0 / 17592186044416.0;
+constexpr int32_t PATH_WIDE = 7;              // out_info path code
+constexpr int WLOC = 4;                       // chunks per thread and step of the locate walk (contiguous)
+
+enum : int32_t { WSTEP_NONE = 0, WSTEP_HIST = 1, WSTEP_CUT = 2, WSTEP_DRAWN = 3, WSTEP_UNIFORM = 4 };
+
+// Per-row plan and result in the workspace (128 bytes).
+struct WideRow {
+  float M;                 // row max of the scaled logits
+  int32_t flags;           // FLAG_* and SFLAG_NAN / SFLAG_PINF
+  int32_t nfin;            // finite scaled logits
+  int32_t step;            // WSTEP_*
+  int32_t blo, bend;       // planned bins [blo, bend]
+  int32_t n_above;         // finite elements in bins < blo
+  int32_t kon;             // top-k applies with a finite threshold (0 < k <= nfin, k < V)
+  uint64_t mass_above;     // fixed-point mass of bins < blo
+  uint64_t mass_tot;       // fixed-point mass of the row
+  float thr;               // top-k threshold (scaled), -inf when top-k keeps every finite value
+  float vstar;             // kept: y > vstar, or y == vstar and id <= istar
+  int32_t istar;
+  int32_t n_kept;
+  double zkept;            // normaliser of the kept set
+  int32_t pad[14];
+};
+static_assert(sizeof(WideRow) == 128, "WideRow layout");
+
+// Per-(row, segment) record, in the segment kernel's statistics slots (32 bytes).
+struct WideSeg {
+  uint64_t mass;           // pass 1: float64 bits of sum exp(y - ymax); pass 2: the segment's mass;
+                           // pass 3: its mass in bins < blo
+  float ymax;              // pass 1: segment max of the finite scaled logits
+  int32_t nfin;            // pass 1: finite scaled logits
+  int32_t flags;           // pass 1: flags
+  int32_t ncand;           // pass 3: planned-bin elements (may exceed SEG_CAP: overflow)
+  int32_t pad[2];
+};
+static_assert(sizeof(WideSeg) == sizeof(SegStat), "WideSeg uses the segment statistics slots");
+
+struct WideParams {
+  const void* logits;
+  int64_t row_stride;
+  int64_t vocab;
+  int64_t n_rows_total;
+  const int64_t* sample_idx;
+  const float* temperature;
+  const int32_t* top_k;
+  const float* top_p;
+  const float* penalty;
+  const int32_t* hist_off;
+  const int32_t* hist_ids;
+  const float* uniforms;
+  int64_t* out_ids;
+  float* out_probs;
+  int32_t* out_info;
+  int32_t n_sample;
+  int32_t S;               // segments per row
+  int32_t init_status;     // pass 1 writes status 1 for the rows it does not take
+  int32_t* counters;       // [rows] arrival counters, zero between launches
+  int32_t* status;         // [rows] 0 = resolved here, 1 = per-row kernel
+  WideRow* rows;           // [rows]
+  WideSeg* segs;           // [rows * S]
+  uint32_t* hcnt;          // [rows * WBINS]
+  uint64_t* hmass;         // [rows * WBINS]
+  uint64_t* cand;          // [rows * S * SEG_CAP]  (float bits << 32) | token id
+};
+
+template <int NKEYS>
+struct WideSmemT {
+  uint32_t bm[SEG_CH * 8 / 32];              // history bitmap of one segment
+  union {
+    struct {
+      uint32_t cnt[WBINS];
+      unsigned long long mass[WBINS];
+    } h;
+    uint64_t keys[NKEYS];                    // the finaliser's ordered elements
+  } u;
+  unsigned long long segfx[MAX_SEGS];
+  int32_t off[MAX_SEGS + 1];
+  unsigned long long ured[NWAVE];
+  double dred[NWAVE];
+  float fred[NWAVE];
+  int32_t ired[NWAVE];
+  int32_t last;
+  int32_t flags;
+  int32_t cnt;
+  int32_t ib[8];
+  float fb[4];
+  double db[4];
+};
+using WideSmem = WideSmemT<1>;               // stats, histogram and probability passes
+using WideSmemCut = WideSmemT<WCAND>;        // the cut pass and its finaliser
+
+// Rows this path takes: sampled (temperature != 0) and not small-k (sampler.py:55).
+__host__ __device__ __forceinline__ bool wide_row(float t, int32_t k, int64_t V) { return !seg_row(t, k, V); }
+
+// Bin of a scaled logit below the row max (WBINS: more than 32 below, or not finite).
+__device__ __forceinline__ int wbin(float M, float y) {
+  const float d = (M - y) * WSCALE;
+  return d < (float)WBINS ? (int)d : WBINS;
+}
+// exp(y - M) in units of 2^-44 (y <= M).
+__device__ __forceinline__ uint64_t wfx(float M, float y) {
+  return (uint64_t)((double)ns_expf(y - M) * WFX);
+}
+
+__device__ __forceinline__ void dc_store_wseg(WideSeg* p, const WideSeg& s) {
+  const uint64_t* w = reinterpret_cast<const uint64_t*>(&s);
+  uint64_t* d = reinterpret_cast<uint64_t*>(p);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) dc_store(d + i, w[i]);
+}
+__device__ __forceinline__ WideSeg dc_load_wseg(const WideSeg* p) {
+  WideSeg s;
+  uint64_t* w = reinterpret_cast<uint64_t*>(&s);
+  const uint64_t* d = reinterpret_cast<const uint64_t*>(p);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) w[i] = dc_load(d + i);
+  return s;
+}
+
+// Block reductions over the NTH / 64 waves of a workgroup (two barriers each).
+template <int NTH = SNT, typename SM>
+__device__ __forceinline__ unsigned long long wsum_u64(unsigned long long v, SM* sm) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += lane_xor(v, o);
+  if (lane_id() == 0) sm->ured[wave_id()] = v;
+  __syncthreads();
+  unsigned long long r = 0ull;
+#pragma unroll
+  for (int w = 0; w < NTH / 64; ++w) r += sm->ured[w];
+  __syncthreads();
+  return r;
+}
+template <int NTH = SNT, typename SM>
+__device__ __forceinline__ double wsum_f64(double v, SM* sm) {
+  v = wave_sum(v);
+  if (lane_id() == 0) sm->dred[wave_id()] = v;
+  __syncthreads();
+  double r = 0.0;
+#pragma unroll
+  for (int w = 0; w < NTH / 64; ++w) r += sm->dred[w];
+  __syncthreads();
+  return r;
+}
+template <int NTH = SNT, typename SM>
+__device__ __forceinline__ int32_t wsum_i(int32_t v, SM* sm) {
+  v = wave_sum(v);
+  if (lane_id() == 0) sm->ired[wave_id()] = v;
+  __syncthreads();
+  int32_t r = 0;
+#pragma unroll
+  for (int w = 0; w < NTH / 64; ++w) r += sm->ired[w];
+  __syncthreads();
+  return r;
+}
+template <int NTH = SNT, typename SM>
+__device__ __forceinline__ float wmax_f(float v, SM* sm) {
+  v = wave_max(v);
+  if (lane_id() == 0) sm->fred[wave_id()] = v;
+  __syncthreads();
+  float r = sm->fred[0];
+#pragma unroll
+  for (int w = 1; w < NTH / 64; ++w) r = __builtin_fmaxf(r, sm->fred[w]);
+  __syncthreads();
+  return r;
+}
+// Exclusive prefix sum over the workgroup's threads; *total receives the sum.
+template <int NTH = SNT, typename SM>
+__device__ __forceinline__ double wexcl_f64(double v, double* total, SM* sm) {
+  const double inc = wave_incl_scan(v);
+  if (lane_id() == 63) sm->dred[wave_id()] = inc;
+  __syncthreads();
+  double off = 0.0, tot = 0.0;
+#pragma unroll
+  for (int w = 0; w < NTH / 64; ++w) {
+    const double t = sm->dred[w];
+    if (w < wave_id()) off += t;
+    tot += t;
+  }
+  __syncthreads();
+  *total = tot;
+  return off + inc - v;
+}
+template <typename U, int NTH = SNT, typename SM>
+__device__ __forceinline__ U wexcl_int(U v, U* total, SM* sm) {
+  const U inc = wave_incl_scan(v);
+  if (lane_id() == 63) {
+    if constexpr (sizeof(U) == 8) sm->ured[wave_id()] = (unsigned long long)inc;
+    else sm->ired[wave_id()] = (int32_t)inc;
+  }
+  __syncthreads();
+  U off = 0, tot = 0;
+#pragma unroll
+  for (int w = 0; w < NTH / 64; ++w) {
+    const U t = sizeof(U) == 8 ? (U)sm->ured[w] : (U)sm->ired[w];
+    if (w < wave_id()) off += t;
+    tot += t;
+  }
+  __syncthreads();
+  *total = tot;
+  return off + inc - v;
+}
+
+// One row's view: parameters, the row pointer, the penalty.
+struct WRowCtx {
+  int row;
+  int64_t V, src;
+  const unsigned char* rowp;
+  float tdiv, rdiv, pen, rpen, topp, u;
+  int32_t k, h0, H;
+  bool pen_on, valid, scale;
+};
+
+template <typename T>
+__device__ __forceinline__ WRowCtx wide_row_ctx(const WideParams& P, int row) {
+  WRowCtx c;
+  c.row = row;
+  c.V = P.vocab;
+  const float temp = P.temperature[row];
+  c.k = P.top_k[row];
+  c.topp = P.top_p[row];
+  c.pen = P.penalty[row];
+  const float u0 = P.uniforms[row];
+  c.u = (u0 >= 0.0f) ? (u0 < 1.0f ? u0 : 0x1.fffffep-1f) : 0.0f;
+  c.src = P.sample_idx ? P.sample_idx[row] : (int64_t)row;
+  int32_t h1 = 0;
+  c.h0 = 0;
+  if (P.hist_off != nullptr) { c.h0 = P.hist_off[row]; h1 = P.hist_off[row + 1]; }
+  c.valid = wide_row(temp, c.k, c.V) && c.src >= 0 && c.src < P.n_rows_total && c.h0 >= 0 && h1 >= c.h0 &&
+            h1 - c.h0 <= MAX_HIST;
+  c.H = h1 - c.h0;
+  c.pen_on = c.pen != 1.0f && c.H > 0;   // sampler.py:33
+  c.tdiv = temp > 0.0f ? __builtin_fmaxf(temp, 1e-6f) : 1.0f;   // sampler.py:42
+  c.rdiv = 1.0f / c.tdiv;
+  c.scale = c.tdiv != 1.0f;
+  c.rpen = 1.0f / c.pen;
+  c.rowp = (const unsigned char*)P.logits + c.src * P.row_stride * T::SZ;
+  return c;
+}
+
+// The history bitmap of elements [e0, e0 + SEG_EL) (set semantics, sampler.py:34-38),
+// and sm->flags cleared.  Every thread must call it (two barriers).  Returns
+// FLAG_BAD_HIST_ID when an id lies outside [0, V).
+template <typename T, int NTH = SNT, typename SM>
+__device__ __forceinline__ int32_t wide_bitmap(const WideParams& P, const WRowCtx& c, int64_t e0, SM* sm) {
+  constexpr int SEG_EL = SEG_CH * T::EPC;
+  const int tid = threadIdx.x;
+  if (tid == 0) sm->flags = 0;
+  if (c.pen_on)
+    for (int i = tid; i < SEG_EL / 32; i += NTH) sm->bm[i] = 0u;
+  __syncthreads();
+  const int32_t* hp = P.hist_ids + c.h0;
+  bool bad = false;
+  for (int j = tid; c.pen_on && j < c.H; j += NTH) {
+    const int32_t id = hp[j];
+    if (id < 0 || (int64_t)id >= c.V) bad = true;
+    else if ((int64_t)id >= e0 && (int64_t)id < e0 + SEG_EL) {
+      const int32_t l = id - (int32_t)e0;
+      atomicOr(&sm->bm[l >> 5], 1u << (l & 31));
+    }
+  }
+  if (bad) atomicOr(&sm->flags, FLAG_BAD_HIST_ID);
+  __syncthreads();
+  return sm->flags;
+}
+
+constexpr int WGRP = 4;   // chunks per thread per step of a segment pass
+
+// Chunk ch of the row (past the row: -inf; the chunk holding the last tokens when V is
+// not a multiple of EPC: its tokens and -inf), through the row's buffer descriptor.
+template <typename T>
+__device__ __forceinline__ uint4 wide_chunk_fix(const WRowCtx& c, int64_t ch, uint4 w) {
+  const int64_t nfull = c.V / T::EPC;
+  if (ch >= nfull) w = ch == nfull && nfull * T::EPC < c.V ? load_tail_chunk<T>(c.rowp, ch, c.V) : seg_ninf<T>();
+  return w;
+}
+
+// The scaled, penalized values of chunk w (tokens id0 .. id0 + EPC - 1; -inf past V):
+// sampler.py:37 then :51 in float32.  The divisions take the correctly rounded
+// multiply-and-correct form; a chunk holding an operand outside its range (zero,
+// huge, tiny, inf, NaN) is recomputed with IEEE divisions, one wave-uniform test per
+// chunk.
+template <typename T>
+__device__ __forceinline__ void chunk_y_exact(const WRowCtx& c, const uint4& w, uint32_t hb, float (&y)[T::EPC]) {
+#pragma unroll
+  for (int e = 0; e < T::EPC; ++e) {
+    float x = T::elem(w, e);
+    if ((hb >> e) & 1u) x = x < 0.0f ? x * c.pen : x / c.pen;
+    y[e] = x / c.tdiv;
+  }
+}
+template <typename T>
+__device__ __forceinline__ void chunk_y(const WRowCtx& c, const uint4& w, uint32_t hb, int64_t id0,
+                                        float (&y)[T::EPC]) {
+  constexpr int EPC = T::EPC;
+  bool slow = false;
+#pragma unroll
+  for (int e = 0; e < EPC; ++e) {
+    float x = T::elem(w, e);
+    if ((hb >> e) & 1u) {
+      if (x < 0.0f) {
+        x = x * c.pen;
+      } else {
+        const float q0 = x * c.rpen;
+        const float aq = __builtin_fabsf(q0);
+        slow |= !(aq >= 0x1.0p-100f && aq <= 0x1.0p+100f);
+        x = __builtin_fmaf(__builtin_fmaf(-q0, c.pen, x), c.rpen, q0);
+      }
+    }
+    if (c.scale) {
+      const float q0 = x * c.rdiv;
+      const float aq = __builtin_fabsf(q0);
+      slow |= !(aq >= 0x1.0p-100f && aq <= 0x1.0p+100f);
+      x = __builtin_fmaf(__builtin_fmaf(-q0, c.tdiv, x), c.rdiv, q0);
+    }
+    y[e] = x;
+  }
+  if (ballot(slow) != 0ull) {
+    asm volatile("");
+    if (slow) chunk_y_exact<T>(c, w, hb, y);
+  }
+#pragma unroll
+  for (int e = 0; e < EPC; ++e)
+    if (id0 + e >= c.V) y[e] = -__builtin_inff();
+}
+
+// f(y, ch) for every chunk ch = c0 + q * SNT + thread of the segment that starts inside
+// the row: y the scaled, penalized values of its EPC tokens (-inf past V).  The chunks
+// stream in steps of WGRP per thread, the next step's loads in flight while one step is
+// processed.
+template <typename T, typename F>
+__device__ __forceinline__ void wide_chunks(const WRowCtx& c, int64_t c0, const uint32_t* bm, F&& f) {
+  constexpr int EPC = T::EPC;
+  const int tid = threadIdx.x;
+  const uint32_t nbytes = (uint32_t)((c.V / EPC) * 16);
+  uint4 cur[WGRP], nxt[WGRP];
+#pragma unroll
+  for (int j = 0; j < WGRP; ++j)
+    cur[j] = buf_load16_at(c.rowp, nbytes, (uint32_t)((c0 + j * SNT) * 16), (uint32_t)tid * 16u);
+#pragma unroll 1
+  for (int g = 0; g < SCPT / WGRP; ++g) {
+    if (g + 1 < SCPT / WGRP) {
+#pragma unroll
+      for (int j = 0; j < WGRP; ++j)
+        nxt[j] = buf_load16_at(c.rowp, nbytes, (uint32_t)((c0 + ((g + 1) * WGRP + j) * SNT) * 16),
+                               (uint32_t)tid * 16u);
+    }
+#pragma unroll
+    for (int j = 0; j < WGRP; ++j) {
+      const int lc = (g * WGRP + j) * SNT + tid;
+      const int64_t ch = c0 + lc;
+      if (ch * EPC < c.V) {
+        float y[EPC];
+        chunk_y<T>(c, wide_chunk_fix<T>(c, ch, cur[j]), c.pen_on ? T::bits(bm, lc) : 0u, ch * EPC, y);
+        f(y, ch);
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < WGRP; ++j) cur[j] = nxt[j];
+  }
+}
+
+// f(y, id) for every token of the segment (ids < V only): y the scaled, penalized logit.
+template <typename T, typename F>
+__device__ __forceinline__ void wide_each(const WRowCtx& c, int64_t c0, const uint32_t* bm, F&& f) {
+  wide_chunks<T>(c, c0, bm, [&](const float (&y)[T::EPC], int64_t ch) {
+#pragma unroll
+    for (int e = 0; e < T::EPC; ++e)
+      if (ch * T::EPC + e < c.V) f(y[e], ch * T::EPC + e);
+  });
+}
+
+// Arrival of a segment workgroup: true in the last one of its row (which resets the
+// counter).  Every wave's device-coherent stores complete before the counter moves.
+template <typename SM>
+__device__ __forceinline__ bool wide_arrive(int32_t* counter, int S, SM* sm) {
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  if (threadIdx.x == 0) sm->last = atomicAdd(counter, 1) == S - 1;
+  __syncthreads();
+  const bool last = sm->last != 0;
+  if (last && threadIdx.x == 0) __hip_atomic_store(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  return last;
+}
+
+// Kept-set predicate of the draw and the probabilities.
+struct WKeep {
+  float thr, vstar;
+  int32_t istar;
+  __device__ __forceinline__ bool operator()(float y, int64_t id) const {
+    if (!(y > -__builtin_inff()) || !(y < __builtin_inff()) || !(y >= thr)) return false;
+    return y > vstar || (y == vstar && id <= (int64_t)istar);
+  }
+};
+
+// The draw inside segment s: the first token (ascending id) whose cumulative kept
+// probability, from pstart (the kept probability of the segments before s), exceeds u.
+// Probabilities are float32(exp(y - M) * rz), rz = 1 / zkept in float64.  The segment
+// is walked in steps of NTH * WLOC chunks, WLOC consecutive chunks per thread.  When
+// rounding leaves u past the segment, the last token with a non-zero probability.
+// Every thread must call it.
+template <typename T, int NTH, typename SM>
+__device__ int64_t wide_locate(const WideParams& P, const WRowCtx& c, int s, double pstart, double rz, float M,
+                               const WKeep& keep, SM* sm, int32_t* fl) {
+  constexpr int EPC = T::EPC;
+  const int tid = threadIdx.x;
+  const int64_t c0 = (int64_t)s * SEG_CH;
+  *fl |= wide_bitmap<T, NTH>(P, c, c0 * EPC, sm);
+  const int64_t nfull = c.V / EPC;
+  if (tid == 0) { sm->ib[0] = 0x7fffffff; sm->ib[1] = -1; }
+  const double ud = (double)c.u;
+  double carry = pstart;
+  for (int step = 0; step < SEG_CH / (NTH * WLOC); ++step) {
+    const int64_t cb = c0 + (int64_t)step * NTH * WLOC + (int64_t)tid * WLOC;   // first chunk of this thread
+    float p[WLOC * EPC];
+#pragma unroll
+    for (int j = 0; j < WLOC; ++j) {
+      const int64_t ch = cb + j;
+      const uint4 w = ch < nfull ? reinterpret_cast<const uint4*>(c.rowp)[ch]
+                                 : (ch == nfull && nfull * EPC < c.V ? load_tail_chunk<T>(c.rowp, ch, c.V)
+                                                                     : seg_ninf<T>());
+      const uint32_t hb = c.pen_on ? T::bits(sm->bm, (int)(ch - c0)) : 0u;
+      float y[EPC];
+      chunk_y<T>(c, w, hb, ch * EPC, y);
+#pragma unroll
+      for (int e = 0; e < EPC; ++e)
+        p[j * EPC + e] = keep(y[e], ch * EPC + e) ? (float)((double)ns_expf(y[e] - M) * rz) : 0.0f;
+    }
+    double own = 0.0;
+#pragma unroll
+    for (int i = 0; i < WLOC * EPC; ++i) own += (double)p[i];
+    double tot;
+    double run = carry + wexcl_f64<NTH>(own, &tot, sm);
+    int32_t first = 0x7fffffff, lastnz = -1;
+#pragma unroll
+    for (int i = 0; i < WLOC * EPC; ++i) {
+      if (p[i] > 0.0f) {
+        run += (double)p[i];
+        const int32_t id = (int32_t)(cb * EPC + i);
+        lastnz = id;
+        if (run > ud && first == 0x7fffffff) first = id;
+      }
+    }
+    if (first != 0x7fffffff) atomicMin(&sm->ib[0], first);
+    if (lastnz >= 0) atomicMax(&sm->ib[1], lastnz);
+    __syncthreads();
+    const bool found = sm->ib[0] != 0x7fffffff;
+    __syncthreads();   // every thread has read the flag before the next step may set it
+    if (found) break;
+    carry += tot;
+  }
+  int64_t tok = sm->ib[0];
+  if (tok == 0x7fffffff) {
+    *fl |= FLAG_LOCATE_FALLBACK;
+    tok = sm->ib[1] >= 0 ? sm->ib[1] : c0 * EPC;
+  }
+  __syncthreads();
+  return tok;
+}
+
+// (row, segment) of this workgroup: all segments of a row share blockIdx % 8 (one XCD).
+__device__ __forceinline__ void wide_rowseg(int S, int* row, int* seg) {
+  const int b = blockIdx.x;
+  const int i8 = b >> 3;
+  const int rg = i8 / S;
+  *seg = i8 - rg * S;
+  *row = rg * 8 + (b & 7);
+}
+
+// ------------------------------------------------------------------ pass 1: stats
+template <typename T>
+__global__ __launch_bounds__(SNT) void wide_stats_kernel(const WideParams P) {
+  __shared__ WideSmem sm;
+  constexpr int EPC = T::EPC;
+  const int tid = threadIdx.x;
+  int row, seg;
+  wide_rowseg(P.S, &row, &seg);
+  if (row >= P.n_sample) return;
+  const WRowCtx c = wide_row_ctx<T>(P, row);
+  if (!c.valid) {
+    if (P.init_status && seg == 0 && tid == 0) P.status[row] = 1;
+    if (seg == 0 && tid == 0) P.rows[row].step = WSTEP_NONE;
+    return;
+  }
+  const int64_t c0 = (int64_t)seg * SEG_CH;
+  int32_t flags = wide_bitmap<T>(P, c, c0 * EPC, &sm);
+  // per thread: finite count, max and sum of exp(y - max) (float64, rescaled by an exact
+  // float64 exp when the max moves, which a thread's first few values do)
+  // (only rows that keep every finite value need the sum: the others histogram the mass
+  // against the row max in the next pass)
+  const bool full_row = !(c.k > 0 && (int64_t)c.k < c.V) && !(c.topp < 1.0f);
+  float mx = -__builtin_inff();
+  double zt = 0.0;
+  int nfin = 0;
+  bool nanf = false, pinf = false;
+  if (full_row) {
+    wide_each<T>(c, c0, sm.bm, [&](float y, int64_t) {
+      nanf |= y != y;
+      pinf |= y == __builtin_inff();
+      if (y > -__builtin_inff() && y < __builtin_inff()) {
+        ++nfin;
+        if (y > mx) {
+          zt = zt * exp((double)mx - (double)y) + 1.0;
+          mx = y;
+        } else {
+          zt += (double)ns_expf(y - mx);
+        }
+      }
+    });
+  } else {
+    wide_each<T>(c, c0, sm.bm, [&](float y, int64_t) {
+      nanf |= y != y;
+      pinf |= y == __builtin_inff();
+      if (y > -__builtin_inff() && y < __builtin_inff()) { ++nfin; mx = __builtin_fmaxf(mx, y); }
+    });
+  }
+  if (ballot(nanf) != 0ull) flags |= SFLAG_NAN;
+  if (ballot(pinf) != 0ull) flags |= SFLAG_PINF;
+  if (lane_id() == 0 && (flags & (SFLAG_NAN | SFLAG_PINF))) atomicOr(&sm.flags, flags);
+  const float smax = wmax_f(mx, &sm);
+  const int32_t snfin = wsum_i(nfin, &sm);
+  const double szt = wsum_f64(nfin > 0 ? zt * exp((double)mx - (double)smax) : 0.0, &sm);
+  flags |= sm.flags;
+  // this segment's share of the row histograms, cleared for pass 2
+  {
+    const int per = (WBINS + P.S - 1) / P.S;
+    for (int b = seg * per + tid; b < (seg + 1) * per && b < WBINS; b += SNT) {
+      P.hcnt[(int64_t)row * WBINS + b] = 0u;
+      P.hmass[(int64_t)row * WBINS + b] = 0ull;
+    }
+  }
+  if (tid == 0) {
+    WideSeg s{};
+    s.mass = (uint64_t)__double_as_longlong(szt);
+    s.ymax = smax;
+    s.nfin = snfin;
+    s.flags = flags;
+    dc_store_wseg(P.segs + (int64_t)row * P.S + seg, s);
+  }
+  if (!wide_arrive(P.counters + row, P.S, &sm)) return;
+  // ---- last segment of the row: M, flags, the NaN / +inf / all -inf rows
+  if (wave_id() == 0) {
+    const bool act = lane_id() < P.S;
+    WideSeg s{};
+    if (act) {
+      s = dc_load_wseg(P.segs + (int64_t)row * P.S + lane_id());
+      sm.u.h.mass[lane_id()] = s.mass;                                   // float64 bits of its sum
+      sm.u.h.cnt[lane_id()] = __float_as_uint(s.ymax);
+    }
+    float M = act ? s.ymax : -__builtin_inff();
+    int32_t nf = act ? s.nfin : 0, fl = act ? s.flags : 0;
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+      M = __builtin_fmaxf(M, lane_xor(M, o));
+      nf += lane_xor(nf, o);
+      fl |= lane_xor(fl, o);
+    }
+    if (lane_id() == 0) { sm.fb[0] = M; sm.ib[0] = nf; sm.ib[1] = fl; }
+  }
+  __syncthreads();
+  const float M = sm.fb[0];
+  const int32_t nf = sm.ib[0], fl = sm.ib[1];
+  WideRow* R = P.rows + row;
+  if ((fl & (SFLAG_NAN | SFLAG_PINF)) || nf == 0) {
+    // the softmax is NaN (a NaN or +inf logit, or every logit -inf): uniform 1/V
+    // (sampler.py:77-80)
+    const int64_t V = c.V;
+    const float qv = (float)(1.0 / (double)V);
+    if (tid == 0) {
+      const double qd = qv, ud = c.u;
+      int64_t i = (int64_t)(ud / qd);
+      while (i > 0 && (double)i * qd > ud) --i;
+      while ((double)(i + 1) * qd <= ud && i < V) ++i;
+      if (i >= V) i = V - 1;
+      P.out_ids[row] = i;
+      const float mrep = (fl & SFLAG_NAN) ? __builtin_nanf("") : (nf == 0 ? -__builtin_inff() : __builtin_inff());
+      seg_write_info(P.out_info, row, PATH_UNIFORM, (int32_t)V, -__builtin_inff(), (int32_t)V, 0, fl & 0xffff, mrep,
+                     -1);
+      P.status[row] = 0;
+      R->step = WSTEP_UNIFORM;
+    }
+    if (P.out_probs != nullptr) {
+      float* pr = P.out_probs + (int64_t)row * V;
+      for (int64_t i = tid; i < V; i += SNT) pr[i] = qv;
+    }
+    return;
+  }
+  const bool kon = c.k > 0 && (int64_t)c.k < c.V && c.k <= nf;   // sampler.py:55
+  const bool pon = c.topp < 1.0f;                                   // sampler.py:63
+  if (!kon && !pon) {
+    // ---- no top-k and no top-p: every finite value is kept; the segments' sums give the
+    // kept mass per segment and the draw runs at once
+    if (tid == 0) {
+      double Z = 0.0;
+      for (int i = 0; i < P.S; ++i) {
+        const float ms = __uint_as_float(sm.u.h.cnt[i]);
+        const double w = ms > -__builtin_inff()
+                             ? __longlong_as_double((long long)sm.u.h.mass[i]) * exp((double)ms - (double)M)
+                             : 0.0;
+        sm.u.h.mass[64 + i] = (unsigned long long)__double_as_longlong(w);
+        Z += w;
+      }
+      const double ud = (double)c.u * Z;
+      double run = 0.0, start = 0.0, laststart = 0.0;
+      int s = -1, lastnz = -1;
+      for (int i = 0; i < P.S; ++i) {
+        const double w = __longlong_as_double((long long)sm.u.h.mass[64 + i]);
+        if (w > 0.0) { lastnz = i; laststart = run; }
+        if (s < 0 && run + w > ud && w > 0.0) { s = i; start = run; }
+        run += w;
+      }
+      if (s < 0) { s = lastnz >= 0 ? lastnz : 0; start = laststart; }
+      sm.ib[2] = s;
+      sm.db[0] = start / Z;
+      sm.db[3] = Z;
+    }
+    __syncthreads();
+    const int s = sm.ib[2];
+    const double start = sm.db[0], Z = sm.db[3];
+    int32_t fl2 = fl & 0xffff;
+    const WKeep keep{-__builtin_inff(), -__builtin_inff(), 0x7fffffff};
+    const int64_t tok = wide_locate<T, SNT>(P, c, s, start, 1.0 / Z, M, keep, &sm, &fl2);
+    if (tid == 0) {
+      P.out_ids[row] = tok;
+      const bool kon0 = c.k > 0 && (int64_t)c.k < c.V;
+      seg_write_info(P.out_info, row, PATH_WIDE, nf, -__builtin_inff(), nf, 0, fl2, -__builtin_inff(), -1);
+      (void)kon0;
+      R->M = M;
+      R->flags = fl;
+      R->nfin = nf;
+      R->thr = -__builtin_inff();
+      R->vstar = -__builtin_inff();
+      R->istar = 0x7fffffff;
+      R->n_kept = nf;
+      R->zkept = Z;
+      R->step = WSTEP_DRAWN;
+      P.status[row] = 0;
+    }
+    return;
+  }
+  if (tid == 0) {
+    R->M = M;
+    R->flags = fl;
+    R->nfin = nf;
+    R->step = WSTEP_HIST;
+  }
+}
+
+// ------------------------------------------------------------------ pass 2: histograms
+template <typename T>
+__global__ __launch_bounds__(SNT) void wide_hist_kernel(const WideParams P) {
+  __shared__ WideSmem sm;
+  constexpr int EPC = T::EPC;
+  const int tid = threadIdx.x;
+  int row, seg;
+  wide_rowseg(P.S, &row, &seg);
+  if (row >= P.n_sample) return;
+  if (P.rows[row].step != WSTEP_HIST) return;
+  const WRowCtx c = wide_row_ctx<T>(P, row);
+  const int64_t c0 = (int64_t)seg * SEG_CH;
+  const float M = P.rows[row].M;
+  for (int b = tid; b < WBINS; b += SNT) { sm.u.h.cnt[b] = 0u; sm.u.h.mass[b] = 0ull; }
+  wide_bitmap<T>(P, c, c0 * EPC, &sm);   // its barriers also order the clearing above
+  unsigned long long own = 0ull;
+  if (c.topp < 1.0f) {
+    wide_each<T>(c, c0, sm.bm, [&](float y, int64_t) {
+      const int b = wbin(M, y);
+      if (b < WBINS) {
+        const uint64_t fx = wfx(M, y);
+        atomicAdd(&sm.u.h.cnt[b], 1u);
+        atomicAdd(&sm.u.h.mass[b], (unsigned long long)fx);
+        own += fx;
+      }
+    });
+  } else {
+    // top-k alone: counts only (its kept mass is summed from the ordered elements and the
+    // compaction pass)
+    wide_each<T>(c, c0, sm.bm, [&](float y, int64_t) {
+      const int b = wbin(M, y);
+      if (b < WBINS) atomicAdd(&sm.u.h.cnt[b], 1u);
+    });
+  }
+  __syncthreads();
+  for (int b = tid; b < WBINS; b += SNT) {
+    const uint32_t n = sm.u.h.cnt[b];
+    if (n != 0u) {
+      atomicAdd(P.hcnt + (int64_t)row * WBINS + b, n);
+      atomicAdd((unsigned long long*)(P.hmass + (int64_t)row * WBINS + b), sm.u.h.mass[b]);
+    }
+  }
+  const unsigned long long smass = wsum_u64(own, &sm);
+  if (tid == 0) {
+    WideSeg s{};
+    s.mass = smass;
+    dc_store_wseg(P.segs + (int64_t)row * P.S + seg, s);
+  }
+  if (!wide_arrive(P.counters + row, P.S, &sm)) return;
+
+  // ---- last segment of the row: the plan
+  WideRow* R = P.rows + row;
+  const int32_t nfin = R->nfin;
+  int32_t fl = R->flags & 0xffff;
+  const int64_t V = c.V;
+  const bool kon0 = c.k > 0 && (int64_t)c.k < V;     // sampler.py:55
+  const bool kon = kon0 && c.k <= nfin;              // otherwise the k-th largest is -inf: keep every value
+  const bool pon = c.topp < 1.0f;                    // sampler.py:63
+  // the row histograms, 4 bins per thread, and their running sums
+  constexpr int BPT = WBINS / SNT;
+  uint32_t hc[BPT];
+  unsigned long long hm[BPT];
+  uint32_t ccnt = 0u;
+  unsigned long long cmass = 0ull;
+#pragma unroll
+  for (int j = 0; j < BPT; ++j) {
+    const int b = tid * BPT + j;
+    hc[j] = __hip_atomic_load(P.hcnt + (int64_t)row * WBINS + b, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    hm[j] = dc_load(P.hmass + (int64_t)row * WBINS + b);
+    ccnt += hc[j];
+    cmass += hm[j];
+  }
+  uint32_t ctot;
+  unsigned long long mtot;
+  const uint32_t cbefore = wexcl_int<uint32_t>(ccnt, &ctot, &sm);
+  const unsigned long long mbefore = wexcl_int<unsigned long long>(cmass, &mtot, &sm);
+  const double Zt = (double)mtot * WFX_INV;
+
+  // ---- top-k bin: the first bin where the running count reaches k
+  if (tid == 0) { sm.ib[3] = WBINS; sm.ib[4] = WBINS; sm.ib[5] = WBINS; }
+  __syncthreads();
+  if (kon) {
+    uint32_t run = cbefore;
+#pragma unroll
+    for (int j = 0; j < BPT; ++j) {
+      const uint32_t prev = run;
+      run += hc[j];
+      if (prev < (uint32_t)c.k && run >= (uint32_t)c.k) sm.ib[3] = tid * BPT + j;
+    }
+  }
+  __syncthreads();
+  const int bk = kon ? sm.ib[3] : WBINS - 1;
+  if (kon && bk >= WBINS) {
+    // the k-th largest lies more than 32 below the max: the per-row kernel takes the row
+    if (tid == 0) { P.status[row] = 1; R->step = WSTEP_NONE; }
+    return;
+  }
+  // ---- top-p bins: the running mass crosses top_p * Z where Z lies between the mass
+  // above the top-k bin and the mass through it; 1e-6 of slack on both sides
+  int blo = bk, bend = bk;
+  if (pon) {
+    // the mass above bin bk and through it (every thread reads the owner's values)
+    if (tid == bk / BPT) {
+      unsigned long long m = mbefore;
+#pragma unroll
+      for (int j = 0; j < BPT; ++j) {
+        if (tid * BPT + j == bk) { sm.db[1] = (double)m * WFX_INV; sm.db[2] = (double)(m + hm[j]) * WFX_INV; }
+        m += hm[j];
+      }
+    }
+    __syncthreads();
+    const double zlo = kon ? sm.db[1] : Zt, zhi = kon ? sm.db[2] : Zt;
+    const double p32 = (double)c.topp;
+    const double tlo = __builtin_fmax((p32 - 1e-6) * zlo, 0.0), thi = (p32 + 1e-6) * zhi;
+    unsigned long long run = mbefore;
+#pragma unroll
+    for (int j = 0; j < BPT; ++j) {
+      const double before = (double)run * WFX_INV;
+      run += hm[j];
+      const double after = (double)run * WFX_INV;
+      if (before <= tlo && after > tlo) atomicMin(&sm.ib[4], tid * BPT + j);
+      if (before <= thi && after > thi) atomicMin(&sm.ib[5], tid * BPT + j);
+    }
+    __syncthreads();
+    blo = sm.ib[4];
+    const int bhi = sm.ib[5];
+    if (blo >= WBINS || (!kon && bhi >= WBINS)) {
+      // the crossing lies more than 32 below the max (or past the whole mass): per-row kernel
+      if (tid == 0) { P.status[row] = 1; R->step = WSTEP_NONE; }
+      return;
+    }
+    if (kon) {
+      if (blo > bk) blo = bk;
+      bend = bk;
+    } else {
+      bend = bhi;
+    }
+  }
+  // elements above the planned bins and in them
+  if (tid == 0) { sm.ib[6] = 0; sm.ib[7] = 0; sm.db[3] = 0.0; }
+  __syncthreads();
+  {
+    uint32_t run = cbefore;
+    unsigned long long mrun = mbefore;
+    int inplan = 0;
+#pragma unroll
+    for (int j = 0; j < BPT; ++j) {
+      const int b = tid * BPT + j;
+      if (b == blo) { sm.ib[6] = (int)run; sm.segfx[0] = mrun; }
+      if (b >= blo && b <= bend) inplan += (int)hc[j];
+      run += hc[j];
+      mrun += hm[j];
+    }
+    if (inplan) atomicAdd(&sm.ib[7], inplan);
+  }
+  __syncthreads();
+  const int nplan = sm.ib[7];
+  if (nplan > WCAND) {
+    if (tid == 0) { P.status[row] = 1; R->step = WSTEP_NONE; }
+    return;
+  }
+  if (tid == 0) {
+    R->blo = blo;
+    R->bend = bend;
+    R->n_above = sm.ib[6];
+    R->mass_above = sm.segfx[0];
+    R->mass_tot = mtot;
+    R->kon = kon ? 1 : 0;
+    R->step = WSTEP_CUT;
+  }
+}
+
+// ------------------------------------------------------------------ pass 3: the planned elements
+// Each segment compacts its elements in the planned bins and its mass above them.
+template <typename T>
+__global__ __launch_bounds__(SNT) void wide_cut_kernel(const WideParams P) {
+  __shared__ WideSmem sm;
+  constexpr int EPC = T::EPC;
+  const int tid = threadIdx.x;
+  const int lane = lane_id();
+  int row, seg;
+  wide_rowseg(P.S, &row, &seg);
+  if (row >= P.n_sample) return;
+  if (P.rows[row].step != WSTEP_CUT) return;
+  const WRowCtx c = wide_row_ctx<T>(P, row);
+  const int64_t c0 = (int64_t)seg * SEG_CH;
+  WideRow* R = P.rows + row;
+  const float M = R->M;
+  const int blo = R->blo, bend = R->bend;
+  wide_bitmap<T>(P, c, c0 * EPC, &sm);
+  if (tid == 0) sm.cnt = 0;
+  __syncthreads();
+  uint64_t* cbase = P.cand + ((int64_t)row * P.S + seg) * SEG_CAP;
+  unsigned long long above = 0ull;
+  wide_chunks<T>(c, c0, sm.bm, [&](const float (&y)[EPC], int64_t ch) {
+    bool any = false;
+#pragma unroll
+    for (int e = 0; e < EPC; ++e) {
+      const int b = wbin(M, y[e]);
+      if (b < blo) above += wfx(M, y[e]);
+      any |= b >= blo && b <= bend;
+    }
+    // the planned elements of the chunk, appended wave-aggregated (one test per chunk)
+    if (ballot(any) != 0ull) {
+#pragma unroll
+      for (int e = 0; e < EPC; ++e) {
+        const int b = wbin(M, y[e]);
+        const bool take = b >= blo && b <= bend;
+        const uint64_t m = ballot(take);
+        if (m != 0ull) {
+          const int leader = __builtin_ctzll(m);
+          int base = 0;
+          if (lane == leader) base = atomicAdd(&sm.cnt, __popcll(m));
+          base = read_lane(base, leader);
+          const int pos = base + lanes_below(m);
+          if (take && pos < SEG_CAP)
+            dc_store(cbase + pos, ((uint64_t)__float_as_uint(y[e]) << 32) | (uint32_t)(ch * EPC + e));
+        }
+      }
+    }
+  });
+  const unsigned long long sabove = wsum_u64(above, &sm);
+  if (tid == 0) {
+    WideSeg s{};
+    s.mass = sabove;
+    s.ncand = sm.cnt;
+    dc_store_wseg(P.segs + (int64_t)row * P.S + seg, s);
+  }
+}
+
+// ------------------------------------------------------------------ pass 3b: the row's cut and draw
+// One 1024-thread workgroup per planned row: the planned elements ordered in LDS (value
+// descending, id ascending), the exact top-k threshold and top-p cut, the kept mass per
+// segment, the draw.
+template <typename T>
+__global__ __launch_bounds__(NT) void wide_final_kernel(const WideParams P) {
+  __shared__ WideSmemCut sm;
+  constexpr int EPC = T::EPC;
+  constexpr int SEG_EL = SEG_CH * EPC;
+  const int tid = threadIdx.x;
+  const int row = blockIdx.x;
+  if (row >= P.n_sample) return;
+  WideRow* R = P.rows + row;
+  if (R->step != WSTEP_CUT) return;
+  const WRowCtx c = wide_row_ctx<T>(P, row);
+  const float M = R->M;
+  int32_t fl = R->flags & 0xffff;
+  const int32_t nfin = R->nfin;
+  const int32_t n_above = R->n_above;
+  const bool kon = R->kon != 0;
+  const bool pon = c.topp < 1.0f;
+  const bool kon0 = c.k > 0 && (int64_t)c.k < c.V;
+  if (tid < P.S) {
+    const WideSeg s = dc_load_wseg(P.segs + (int64_t)row * P.S + tid);
+    sm.segfx[tid] = s.mass;
+    sm.off[tid] = s.ncand;
+  }
+  if (tid == 0) sm.ib[0] = 0;
+  __syncthreads();
+  if (tid == 0) {
+    int o = 0, over = 0;
+    for (int i = 0; i < P.S; ++i) {
+      const int n = sm.off[i];
+      over |= n > SEG_CAP;
+      sm.off[i] = o;
+      o += n < SEG_CAP ? n : SEG_CAP;
+    }
+    sm.off[P.S] = o;
+    sm.ib[0] = over || o > WCAND;
+  }
+  __syncthreads();
+  // the mass above the planned bins: the segments' sums from the compaction pass (the same
+  // fixed-point terms the histogram holds when it holds masses)
+  uint64_t mass_above = 0ull;
+  for (int i = 0; i < P.S; ++i) mass_above += sm.segfx[i];
+  const int n = sm.off[P.S];
+  if (sm.ib[0] || n == 0) {
+    if (tid == 0) { P.status[row] = 1; R->step = WSTEP_NONE; }
+    return;
+  }
+  // the planned elements as sort keys (value descending, id ascending), padded to a power of two
+  const int P2 = next_pow2(n < 2 ? 2 : n);
+  for (int i = tid; i < P2; i += NT) {
+    uint64_t key = ~0ull;
+    if (i < n) {
+      int s = 0;
+      while (s + 1 < P.S && sm.off[s + 1] <= i) ++s;
+      const uint64_t e = dc_load(P.cand + ((int64_t)row * P.S + s) * SEG_CAP + (i - sm.off[s]));
+      key = desc_key(__uint_as_float((uint32_t)(e >> 32)), (uint32_t)e);
+    }
+    sm.u.keys[i] = key;
+  }
+  __syncthreads();
+  for (int size = 2; size <= P2; size <<= 1) {
+    for (int stride = size >> 1; stride > 0; stride >>= 1) {
+      for (int i = tid; i < (P2 >> 1); i += NT) {
+        const int lo = 2 * i - (i & (stride - 1));
+        const int hi = lo + stride;
+        const bool up = (lo & size) == 0;
+        const uint64_t a = sm.u.keys[lo], b = sm.u.keys[hi];
+        if ((a > b) == up) { sm.u.keys[lo] = b; sm.u.keys[hi] = a; }
+      }
+      __syncthreads();
+    }
+  }
+  // ---- top-k threshold: the k-th largest, k - 1 - n_above places into the ordered elements
+  float thr = -__builtin_inff();
+  if (kon) {
+    const int r = c.k - 1 - n_above;
+    if (r < 0 || r >= n) {
+      if (tid == 0) { P.status[row] = 1; R->step = WSTEP_NONE; }
+      return;
+    }
+    thr = desc_key_val(sm.u.keys[r]);
+  }
+  // per element: kept by top-k, its mass, its float32 probability under the top-k set
+  constexpr int EPT = WCAND / NT;
+  const int p0 = tid * EPT;
+  unsigned long long mk = 0ull;
+  int nk_own = 0;
+#pragma unroll
+  for (int j = 0; j < EPT; ++j) {
+    const int pos = p0 + j;
+    if (pos < n) {
+      const float y = desc_key_val(sm.u.keys[pos]);
+      if (y >= thr) { mk += wfx(M, y); ++nk_own; }
+    }
+  }
+  const unsigned long long mtopk = wsum_u64<NT>(mk, &sm);
+  const int32_t n_topk_c = wsum_i<NT>(nk_own, &sm);
+  const int32_t n_topk = kon ? n_above + n_topk_c : nfin;
+  const uint64_t zk_fx = kon ? mass_above + mtopk : R->mass_tot;
+  const double zk = (double)zk_fx * WFX_INV;
+  const double rzk = 1.0 / zk;
+  // ---- top-p: first position whose float32 prefix of float32 probabilities exceeds top_p
+  int J = n_topk_c - 1;          // without top-p: every top-k element is kept
+  if (pon) {
+    const double base = (double)mass_above * WFX_INV * rzk;
+    if (n_above > 0 && (float)base > c.topp) {
+      if (tid == 0) { P.status[row] = 1; R->step = WSTEP_NONE; }
+      return;
+    }
+    float qv[EPT];
+    double qs = 0.0;
+#pragma unroll
+    for (int j = 0; j < EPT; ++j) {
+      const int pos = p0 + j;
+      qv[j] = 0.0f;
+      if (pos < n) {
+        const float y = desc_key_val(sm.u.keys[pos]);
+        if (y >= thr) qv[j] = (float)((double)ns_expf(y - M) * rzk);
+      }
+      qs += (double)qv[j];
+    }
+    double tot;
+    double run = base + wexcl_f64<NT>(qs, &tot, &sm);
+    if (tid == 0) sm.ib[1] = 0x7fffffff;
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < EPT; ++j) {
+      const int pos = p0 + j;
+      if (pos < n && pos < n_topk_c) {
+        run += (double)qv[j];
+        if ((float)run > c.topp) atomicMin(&sm.ib[1], pos);
+      }
+    }
+    __syncthreads();
+    const int cross = sm.ib[1];
+    if (cross != 0x7fffffff) {
+      J = cross;
+    } else if (!kon0) {
+      // top-p alone and no crossing among the planned elements: the plan missed it
+      if (tid == 0) { P.status[row] = 1; R->step = WSTEP_NONE; }
+      return;
+    }
+  }
+  if (J < 0) J = 0;
+  const uint64_t kc = sm.u.keys[J];
+  const float vstar = pon ? desc_key_val(kc) : -__builtin_inff();
+  const int32_t istar = pon ? (int32_t)desc_key_id(kc) : 0x7fffffff;
+  const int32_t n_kept = pon ? n_above + J + 1 : n_topk;
+  const WKeep keep{thr, vstar, istar};
+  // ---- kept mass per segment: above the planned bins plus the kept planned elements
+  unsigned long long mkept = 0ull;
+#pragma unroll
+  for (int j = 0; j < EPT; ++j) {
+    const int pos = p0 + j;
+    if (pos < n && pos <= J) {
+      const uint64_t key = sm.u.keys[pos];
+      const float y = desc_key_val(key);
+      if (y >= thr) {
+        const uint64_t fx = wfx(M, y);
+        mkept += fx;
+        atomicAdd(&sm.segfx[desc_key_id(key) / SEG_EL], (unsigned long long)fx);
+      }
+    }
+  }
+  const unsigned long long mk2 = wsum_u64<NT>(mkept, &sm);
+  const uint64_t zkept_fx = pon ? mass_above + mk2 : zk_fx;
+  const double zkept = (double)zkept_fx * WFX_INV;
+  if (tid == 0) {
+    const double ud = (double)c.u;
+    double run = 0.0, start = 0.0, laststart = 0.0;
+    int s = -1, lastnz = -1;
+    const double rzkept = 1.0 / zkept;
+    for (int i = 0; i < P.S; ++i) {
+      const double p = (double)sm.segfx[i] * WFX_INV * rzkept;
+      if (sm.segfx[i] != 0ull) { lastnz = i; laststart = run; }
+      if (s < 0 && run + p > ud && sm.segfx[i] != 0ull) { s = i; start = run; }
+      run += p;
+    }
+    if (s < 0) { s = lastnz >= 0 ? lastnz : 0; start = laststart; }
+    sm.ib[2] = s;
+    sm.db[0] = start;
+  }
+  __syncthreads();
+  const int s = sm.ib[2];
+  const double start = sm.db[0];
+  const int64_t tok = wide_locate<T, NT>(P, c, s, start, 1.0 / zkept, M, keep, &sm, &fl);
+  if (tid == 0) {
+    P.out_ids[row] = tok;
+    seg_write_info(P.out_info, row, PATH_WIDE, n_kept, kon0 ? thr : -__builtin_inff(), n_topk, n, fl, vstar, istar);
+    R->thr = thr;
+    R->vstar = vstar;
+    R->istar = istar;
+    R->n_kept = n_kept;
+    R->zkept = zkept;
+    R->step = WSTEP_DRAWN;
+    P.status[row] = 0;
+  }
+}
+
+// ------------------------------------------------------------------ pass 4: probabilities
+template <typename T>
+__global__ __launch_bounds__(SNT) void wide_probs_kernel(const WideParams P) {
+  __shared__ WideSmem sm;
+  constexpr int EPC = T::EPC;
+  int row, seg;
+  wide_rowseg(P.S, &row, &seg);
+  if (row >= P.n_sample) return;
+  const WideRow* R = P.rows + row;
+  if (R->step != WSTEP_DRAWN) return;
+  const WRowCtx c = wide_row_ctx<T>(P, row);
+  const int64_t c0 = (int64_t)seg * SEG_CH;
+  wide_bitmap<T>(P, c, c0 * EPC, &sm);
+  const float M = R->M;
+  const double rz = 1.0 / R->zkept;
+  const WKeep keep{R->thr, R->vstar, R->istar};
+  float* pr = P.out_probs + (int64_t)row * c.V;
+  wide_each<T>(c, c0, sm.bm, [&](float y, int64_t id) {
+    pr[id] = keep(y, id) ? (float)((double)ns_expf(y - M) * rz) : 0.0f;
+  });
+}
+
+}  // namespace ns

@@ -77,6 +77,7 @@ class PackedRows:
             else:
                 hist_rows.append(None)
         self.batch = B
+        self.row_kinds = _lib.row_kinds(temp, topk, vocab)
         self.temperature = temp
         self.top_k = topk
         self.top_p = topp
@@ -174,7 +175,7 @@ class Sampler:
         if B > 0:
             _lib.sample_raw(logits, d["temperature"], d["top_k"], d["top_p"], d["rep_penalty"], uniforms, out,
                             sample_idx=sample_indices, hist_offsets=d["hist_offsets"], hist_ids=d["hist_ids"],
-                            max_hist=packed.max_hist, out_probs=probs)
+                            max_hist=packed.max_hist, out_probs=probs, row_kinds=packed.row_kinds)
         return (out, probs) if return_probs else out
 
     @staticmethod
