@@ -1261,7 +1261,8 @@ int ns_sample(const ns_sample_args* a, hipStream_t stream) {
   // Path choice.  Per-row mode: one workgroup per row for every row (greedy and small-k
   // rows that fit in registers stream in one pass); a single launch, best once the batch
   // fills the GPU.  Segmented mode: greedy and small-k rows split over 16-byte-chunk
-  // segments (a few workgroups per row), the per-row kernel after it for the rest.
+  // segments (a few workgroups per row); rows with top-k off or larger take the wide path
+  // over the same segments; the per-row kernel after them for the rest.
   if (a->mode < NS_MODE_AUTO || a->mode > NS_MODE_PER_ROW) return fail(NS_ERR_INVALID, "unknown mode");
   if (a->mode == NS_MODE_SEGMENTED && a->workspace == nullptr)
     return fail(NS_ERR_INVALID, "segmented mode needs a workspace");
@@ -1269,7 +1270,11 @@ int ns_sample(const ns_sample_args* a, hipStream_t stream) {
   e = hipDeviceGetAttribute(&n_cu, hipDeviceAttributeMultiprocessorCount, dev);
   if (e != hipSuccess) return fail(NS_ERR_HIP, std::string("hipDeviceGetAttribute: ") + hipGetErrorString(e));
   bool segmented = a->workspace != nullptr && a->mode != NS_MODE_PER_ROW;
-  if (a->mode == NS_MODE_AUTO && ((int64_t)a->n_sample * 8 >= (int64_t)n_cu * 7 || a->n_sample > NS_SEG_MAX_ROWS))
+  // AUTO: per-row once the batch fills the GPU and rows fit the streaming path's registers;
+  // wider rows keep the segment kernel at every batch size
+  const bool fits = a->dtype == NS_DTYPE_BF16 ? ns::row_fits<ns::BF16>(a->vocab) : ns::row_fits<ns::F32>(a->vocab);
+  if (a->mode == NS_MODE_AUTO &&
+      (((int64_t)a->n_sample * 8 >= (int64_t)n_cu * 7 && fits) || a->n_sample > NS_SEG_MAX_ROWS))
     segmented = false;
   // wide path for the rows neither the streaming nor the segment kernels take
   const bool wide = a->workspace != nullptr && a->mode != NS_MODE_PER_ROW && a->n_sample <= NS_WIDE_MAX_ROWS &&
@@ -1285,7 +1290,9 @@ int ns_sample(const ns_sample_args* a, hipStream_t stream) {
   p.fast = 1;
   p.status = nullptr;
 
-  // 1) segment kernel: greedy and small-k rows
+  // 1) segment kernel: greedy and small-k rows (launched with the wide path's first pass
+  //    when both run)
+  ns::SegParams seg_args{};
   if (segmented) {
     const int64_t S = seg_count(a->vocab, a->dtype);
     if (S > ns::MAX_SEGS) return fail(NS_ERR_INVALID, "vocab too large for the segment kernel");
@@ -1316,11 +1323,14 @@ int ns_sample(const ns_sample_args* a, hipStream_t stream) {
     s.stats = reinterpret_cast<ns::SegStat*>(ws + L.stats);
     s.cand = reinterpret_cast<uint64_t*>(ws + L.cand);
     p.status = s.status;
-    const dim3 g((unsigned)nblk), bs(ns::SNT);
-    if (a->dtype == NS_DTYPE_BF16) hipLaunchKernelGGL((ns::segment_kernel<ns::BF16>), g, bs, 0, stream, s);
-    else hipLaunchKernelGGL((ns::segment_kernel<ns::F32>), g, bs, 0, stream, s);
-    e = hipGetLastError();
-    if (e != hipSuccess) return fail(NS_ERR_HIP, std::string("segment kernel launch: ") + hipGetErrorString(e));
+    seg_args = s;
+    if (!wide) {
+      const dim3 g((unsigned)nblk), bs(ns::SNT);
+      if (a->dtype == NS_DTYPE_BF16) hipLaunchKernelGGL((ns::segment_kernel<ns::BF16>), g, bs, 0, stream, s);
+      else hipLaunchKernelGGL((ns::segment_kernel<ns::F32>), g, bs, 0, stream, s);
+      e = hipGetLastError();
+      if (e != hipSuccess) return fail(NS_ERR_HIP, std::string("segment kernel launch: ") + hipGetErrorString(e));
+    }
   }
 
   // 2) wide path: rows with top-k off or k > 64, each over the segment workgroups of the
@@ -1348,7 +1358,7 @@ int ns_sample(const ns_sample_args* a, hipStream_t stream) {
     w.out_info = a->out_info;
     w.n_sample = a->n_sample;
     w.S = (int32_t)S;
-    w.init_status = segmented ? 0 : 1;
+    w.init_status = 1;
     w.counters = reinterpret_cast<int32_t*>(ws + L.counters);
     w.status = reinterpret_cast<int32_t*>(ws + L.status);
     w.rows = reinterpret_cast<ns::WideRow*>(ws + L.wrow);
@@ -1359,8 +1369,13 @@ int ns_sample(const ns_sample_args* a, hipStream_t stream) {
     p.status = w.status;
     const dim3 g((unsigned)nblk), bs(ns::SNT);
     const bool bf = a->dtype == NS_DTYPE_BF16;
-    if (bf) hipLaunchKernelGGL((ns::wide_stats_kernel<ns::BF16>), g, bs, 0, stream, w);
-    else hipLaunchKernelGGL((ns::wide_stats_kernel<ns::F32>), g, bs, 0, stream, w);
+    if (segmented) {
+      if (bf) hipLaunchKernelGGL((ns::segwide_kernel<ns::BF16>), g, bs, 0, stream, seg_args, w);
+      else hipLaunchKernelGGL((ns::segwide_kernel<ns::F32>), g, bs, 0, stream, seg_args, w);
+    } else {
+      if (bf) hipLaunchKernelGGL((ns::wide_stats_kernel<ns::BF16>), g, bs, 0, stream, w);
+      else hipLaunchKernelGGL((ns::wide_stats_kernel<ns::F32>), g, bs, 0, stream, w);
+    }
     if (bf) hipLaunchKernelGGL((ns::wide_hist_kernel<ns::BF16>), g, bs, 0, stream, w);
     else hipLaunchKernelGGL((ns::wide_hist_kernel<ns::F32>), g, bs, 0, stream, w);
     if (bf) hipLaunchKernelGGL((ns::wide_cut_kernel<ns::BF16>), g, bs, 0, stream, w);

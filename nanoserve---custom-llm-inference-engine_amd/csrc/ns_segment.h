@@ -712,9 +712,9 @@ __device__ __forceinline__ void seg_append(float y, int64_t id, uint64_t* cbase,
   if (pos < SEG_CAP) dc_store(cbase + pos, ((uint64_t)__float_as_uint(y) << 32) | (uint32_t)id);
 }
 
+// The segment kernel's work for this workgroup's (row, segment), with the workgroup's LDS.
 template <typename T>
-__global__ __launch_bounds__(SNT) __attribute__((amdgpu_waves_per_eu(4))) void segment_kernel(const SegParams P) {
-  __shared__ SegSmem sm;
+__device__ __forceinline__ void segment_body(const SegParams& P, SegSmem& sm) {
   constexpr int EPC = T::EPC;
   constexpr int SEG_EL = SEG_CH * EPC;         // elements per segment
   const int tid = threadIdx.x;
@@ -1173,6 +1173,12 @@ __global__ __launch_bounds__(SNT) __attribute__((amdgpu_waves_per_eu(4))) void s
   else
     wave_finalize<4>(sm.list, n2, k, topp_on, topp, 1.0f, 1.0f, u, row, P.out_ids, P.out_probs, V, P.out_info, fl, n1,
                      PATH_WAVE_SET);
+}
+
+template <typename T>
+__global__ __launch_bounds__(SNT) __attribute__((amdgpu_waves_per_eu(4))) void segment_kernel(const SegParams P) {
+  __shared__ SegSmem sm;
+  segment_body<T>(P, sm);
 }
 
 }  // namespace ns

@@ -38,7 +38,7 @@ constexpr double WFX_INV = 1.0 / 17592186044416.0;
 constexpr int32_t PATH_WIDE = 7;              // out_info path code
 constexpr int WLOC = 4;                       // chunks per thread and step of the locate walk (contiguous)
 
-enum : int32_t { WSTEP_NONE = 0, WSTEP_HIST = 1, WSTEP_CUT = 2, WSTEP_DRAWN = 3, WSTEP_UNIFORM = 4 };
+enum : int32_t { WSTEP_NONE = 0, WSTEP_HIST = 1, WSTEP_CUT = 2, WSTEP_DRAWN = 3, WSTEP_UNIFORM = 4, WSTEP_FULL = 5 };
 
 // Per-row plan and result in the workspace (128 bytes).
 struct WideRow {
@@ -505,8 +505,7 @@ __device__ __forceinline__ void wide_rowseg(int S, int* row, int* seg) {
 
 // ------------------------------------------------------------------ pass 1: stats
 template <typename T>
-__global__ __launch_bounds__(SNT) void wide_stats_kernel(const WideParams P) {
-  __shared__ WideSmem sm;
+__device__ __forceinline__ void wide_stats_body(const WideParams& P, WideSmem& sm) {
   constexpr int EPC = T::EPC;
   const int tid = threadIdx.x;
   int row, seg;
@@ -624,53 +623,22 @@ __global__ __launch_bounds__(SNT) void wide_stats_kernel(const WideParams P) {
   const bool kon = c.k > 0 && (int64_t)c.k < c.V && c.k <= nf;   // sampler.py:55
   const bool pon = c.topp < 1.0f;                                   // sampler.py:63
   if (!kon && !pon) {
-    // ---- no top-k and no top-p: every finite value is kept; the segments' sums give the
-    // kept mass per segment and the draw runs at once
-    if (tid == 0) {
-      double Z = 0.0;
-      for (int i = 0; i < P.S; ++i) {
-        const float ms = __uint_as_float(sm.u.h.cnt[i]);
-        const double w = ms > -__builtin_inff()
-                             ? __longlong_as_double((long long)sm.u.h.mass[i]) * exp((double)ms - (double)M)
-                             : 0.0;
-        sm.u.h.mass[64 + i] = (unsigned long long)__double_as_longlong(w);
-        Z += w;
-      }
-      const double ud = (double)c.u * Z;
-      double run = 0.0, start = 0.0, laststart = 0.0;
-      int s = -1, lastnz = -1;
-      for (int i = 0; i < P.S; ++i) {
-        const double w = __longlong_as_double((long long)sm.u.h.mass[64 + i]);
-        if (w > 0.0) { lastnz = i; laststart = run; }
-        if (s < 0 && run + w > ud && w > 0.0) { s = i; start = run; }
-        run += w;
-      }
-      if (s < 0) { s = lastnz >= 0 ? lastnz : 0; start = laststart; }
-      sm.ib[2] = s;
-      sm.db[0] = start / Z;
-      sm.db[3] = Z;
+    // ---- no top-k and no top-p: every finite value is kept.  The segments' sums rescaled to
+    // the row max are the kept mass per segment; the final pass draws.
+    if (tid < P.S) {
+      const float ms = __uint_as_float(sm.u.h.cnt[tid]);
+      const double w = ms > -__builtin_inff()
+                           ? __longlong_as_double((long long)sm.u.h.mass[tid]) * exp((double)ms - (double)M)
+                           : 0.0;
+      WideSeg s2{};
+      s2.mass = (uint64_t)__double_as_longlong(w);
+      dc_store_wseg(P.segs + (int64_t)row * P.S + tid, s2);
     }
-    __syncthreads();
-    const int s = sm.ib[2];
-    const double start = sm.db[0], Z = sm.db[3];
-    int32_t fl2 = fl & 0xffff;
-    const WKeep keep{-__builtin_inff(), -__builtin_inff(), 0x7fffffff};
-    const int64_t tok = wide_locate<T, SNT>(P, c, s, start, 1.0 / Z, M, keep, &sm, &fl2);
     if (tid == 0) {
-      P.out_ids[row] = tok;
-      const bool kon0 = c.k > 0 && (int64_t)c.k < c.V;
-      seg_write_info(P.out_info, row, PATH_WIDE, nf, -__builtin_inff(), nf, 0, fl2, -__builtin_inff(), -1);
-      (void)kon0;
       R->M = M;
       R->flags = fl;
       R->nfin = nf;
-      R->thr = -__builtin_inff();
-      R->vstar = -__builtin_inff();
-      R->istar = 0x7fffffff;
-      R->n_kept = nf;
-      R->zkept = Z;
-      R->step = WSTEP_DRAWN;
-      P.status[row] = 0;
+      R->step = WSTEP_FULL;
     }
     return;
   }
@@ -679,6 +647,33 @@ __global__ __launch_bounds__(SNT) void wide_stats_kernel(const WideParams P) {
     R->flags = fl;
     R->nfin = nf;
     R->step = WSTEP_HIST;
+  }
+}
+
+template <typename T>
+__global__ __launch_bounds__(SNT) __attribute__((amdgpu_waves_per_eu(4))) void wide_stats_kernel(const WideParams P) {
+  __shared__ WideSmem sm;
+  wide_stats_body<T>(P, sm);
+}
+
+// The segment kernel and the wide path's first pass in one launch over the same (row,
+// segment) workgroups: greedy and small-k rows take the segment kernel's work, the others
+// the stats pass (which writes status 1 for the rows neither takes).
+template <typename T>
+__global__ __launch_bounds__(SNT) __attribute__((amdgpu_waves_per_eu(4))) void segwide_kernel(const SegParams SP,
+                                                                                            const WideParams WP) {
+  __shared__ union {
+    SegSmem s;
+    WideSmem w;
+  } sm;
+  int row, seg;
+  wide_rowseg(WP.S, &row, &seg);
+  if (row >= WP.n_sample) return;
+  if (seg_row(WP.temperature[row], WP.top_k[row], WP.vocab)) {
+    if (seg == 0 && threadIdx.x == 0) WP.rows[row].step = WSTEP_NONE;   // no later wide pass for it
+    segment_body<T>(SP, sm.s);
+  } else {
+    wide_stats_body<T>(WP, sm.w);
   }
 }
 
@@ -925,11 +920,50 @@ __global__ __launch_bounds__(NT) void wide_final_kernel(const WideParams P) {
   const int row = blockIdx.x;
   if (row >= P.n_sample) return;
   WideRow* R = P.rows + row;
-  if (R->step != WSTEP_CUT) return;
+  const int32_t step = R->step;
+  if (step != WSTEP_CUT && step != WSTEP_FULL) return;
   const WRowCtx c = wide_row_ctx<T>(P, row);
   const float M = R->M;
   int32_t fl = R->flags & 0xffff;
   const int32_t nfin = R->nfin;
+  if (step == WSTEP_FULL) {
+    // ---- every finite value kept: the segment holding u from the per-segment masses, then
+    // the walk inside it
+    if (tid == 0) {
+      double Z = 0.0;
+      for (int i = 0; i < P.S; ++i) Z += __longlong_as_double((long long)dc_load_wseg(P.segs + (int64_t)row * P.S + i).mass);
+      const double ud = (double)c.u * Z;
+      double run = 0.0, start = 0.0, laststart = 0.0;
+      int s = -1, lastnz = -1;
+      for (int i = 0; i < P.S; ++i) {
+        const double w = __longlong_as_double((long long)dc_load_wseg(P.segs + (int64_t)row * P.S + i).mass);
+        if (w > 0.0) { lastnz = i; laststart = run; }
+        if (s < 0 && run + w > ud && w > 0.0) { s = i; start = run; }
+        run += w;
+      }
+      if (s < 0) { s = lastnz >= 0 ? lastnz : 0; start = laststart; }
+      sm.ib[2] = s;
+      sm.db[0] = start / Z;
+      sm.db[3] = Z;
+    }
+    __syncthreads();
+    const int s = sm.ib[2];
+    const double start = sm.db[0], Z = sm.db[3];
+    const WKeep keep{-__builtin_inff(), -__builtin_inff(), 0x7fffffff};
+    const int64_t tok = wide_locate<T, NT>(P, c, s, start, 1.0 / Z, M, keep, &sm, &fl);
+    if (tid == 0) {
+      P.out_ids[row] = tok;
+      seg_write_info(P.out_info, row, PATH_WIDE, nfin, -__builtin_inff(), nfin, 0, fl, -__builtin_inff(), -1);
+      R->thr = -__builtin_inff();
+      R->vstar = -__builtin_inff();
+      R->istar = 0x7fffffff;
+      R->n_kept = nfin;
+      R->zkept = Z;
+      R->step = WSTEP_DRAWN;
+      P.status[row] = 0;
+    }
+    return;
+  }
   const int32_t n_above = R->n_above;
   const bool kon = R->kon != 0;
   const bool pon = c.topp < 1.0f;
