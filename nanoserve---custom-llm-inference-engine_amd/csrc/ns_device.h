@@ -42,8 +42,8 @@ __device__ __forceinline__ uint32_t desc_key_id(uint64_t k) { return (uint32_t)k
 
 // ---------------------------------------------------------------- wave ops
 // Lane exchange by a constant xor distance s, on the VALU instead of the LDS
-// crossbar (ds_bpermute): DPP quad_perm for s = 1, 2; DPP row shifts plus a
-// select for s = 4, 8; v_permlane16_swap / v_permlane32_swap for s = 16, 32.
+// crossbar (ds_bpermute): DPP quad_perm for s = 1, 2; two DPP mirrors for s = 4;
+// DPP row_ror:8 for s = 8; v_permlane16_swap / v_permlane32_swap for s = 16, 32.
 // s must fold to a constant (it does inside fully unrolled loops).
 __device__ __forceinline__ uint32_t lane_xor_u32(uint32_t v, int s) {
   const int lane = lane_id();
@@ -51,15 +51,11 @@ __device__ __forceinline__ uint32_t lane_xor_u32(uint32_t v, int s) {
     case 1: return __builtin_amdgcn_update_dpp(0u, v, 0xB1, 0xF, 0xF, false);   // quad_perm [1,0,3,2]
     case 2: return __builtin_amdgcn_update_dpp(0u, v, 0x4E, 0xF, 0xF, false);   // quad_perm [2,3,0,1]
     case 4: {
-      const uint32_t up = __builtin_amdgcn_update_dpp(0u, v, 0x104, 0xF, 0xF, false);   // row_shl:4
-      const uint32_t dn = __builtin_amdgcn_update_dpp(0u, v, 0x114, 0xF, 0xF, false);   // row_shr:4
-      return (lane & 4) ? dn : up;
+      // row_half_mirror (l ^ 7 inside 8 lanes), then quad_perm [3,2,1,0] (l ^ 3): l ^ 4
+      const int m = __builtin_amdgcn_mov_dpp((int)v, 0x141, 0xF, 0xF, false);
+      return (uint32_t)__builtin_amdgcn_mov_dpp(m, 0x1B, 0xF, 0xF, false);
     }
-    case 8: {
-      const uint32_t up = __builtin_amdgcn_update_dpp(0u, v, 0x108, 0xF, 0xF, false);   // row_shl:8
-      const uint32_t dn = __builtin_amdgcn_update_dpp(0u, v, 0x118, 0xF, 0xF, false);   // row_shr:8
-      return (lane & 8) ? dn : up;
-    }
+    case 8: return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x128, 0xF, 0xF, false);   // row_ror:8 = l ^ 8
     case 16: {
       const auto r = __builtin_amdgcn_permlane16_swap(v, v, false, false);
       return (lane & 16) ? r[0] : r[1];
@@ -80,6 +76,13 @@ template <typename T> __device__ __forceinline__ T lane_xor(T v, int s) {
     const uint64_t lo = lane_xor_u32((uint32_t)u, s), hi = lane_xor_u32((uint32_t)(u >> 32), s);
     return __builtin_bit_cast(T, (hi << 32) | lo);
   }
+}
+// A wave-uniform double taken from the first active lane (scalar registers).
+__device__ __forceinline__ double uniform_f64(double v) {
+  const uint64_t u = __builtin_bit_cast(uint64_t, v);
+  const uint64_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)u);
+  const uint64_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(u >> 32));
+  return __builtin_bit_cast(double, (hi << 32) | lo);
 }
 // Value of lane `src` (wave-uniform) broadcast to every lane.
 template <typename T> __device__ __forceinline__ T read_lane(T v, int src) {

@@ -80,10 +80,14 @@ struct Levels {
     int b = t <= 0.0 ? 0 : (t >= (double)(NB - 1) ? NB - 1 : (int)t);
     return b;
   }
+  // h, sc, bb and r are block-uniform: the fields are taken from the first lane so they
+  // live in scalar registers
   __device__ __forceinline__ void set(int r, double h, double sc, int bb) {
+    const double hu = uniform_f64(h), su = uniform_f64(sc);
+    const int bu = __builtin_amdgcn_readfirstlane(bb);
 #pragma unroll
     for (int i = 0; i < MAX_LEVELS; ++i)
-      if (i == r) { hi[i] = h; s[i] = sc; b[i] = bb; }
+      if (i == r) { hi[i] = hu; s[i] = su; b[i] = bu; }
     n = r + 1;
   }
   __device__ __forceinline__ bool member(float v) const {
@@ -120,7 +124,7 @@ __device__ __forceinline__ int find_bin(const uint64_t* vals64, const uint32_t* 
 // (chunk or group maxima): histogram over [lo, hi], first bin reaching k, tau =
 // the smallest value in bins up to it.  Returns -inf when fewer than k values.
 template <int NV>
-__device__ float select_tau(const float (&v)[NV], bool active, int k, uint32_t* hcnt, Misc* misc) {
+__device__ __forceinline__ float select_tau(const float (&v)[NV], bool active, int k, uint32_t* hcnt, Misc* misc) {
   float hi = NEG_INF, lo = POS_INF;
   int cnt = 0;
   if (active) {
@@ -179,7 +183,7 @@ __device__ __forceinline__ void zero_probs(const RowOut& o) {
 // Exact selection, top-p and draw over the n entries (x, id) in `cand`.
 // need_topk: keep the entries >= the k-th largest scaled value; need_topp: apply
 // the nucleus cut.  Without either, the entries are the whole kept set.
-__device__ __attribute__((noinline)) void lds_set(int n, bool need_topk, int k, bool need_topp, float p32, float My, float tdiv, float rdiv,
+__device__ __attribute__((always_inline)) inline void lds_set(int n, bool need_topk, int k, bool need_topp, float p32, float My, float tdiv, float rdiv,
                         float u, uint64_t* cand, Misc* misc, const RowOut& o, int32_t path, int32_t flags,
                         float thr_in, int32_t n_topk_in) {
   const int tid = threadIdx.x;
@@ -353,7 +357,7 @@ struct GCtx {
 // histogram), and the inverse-CDF draw over a large kept set.  Every pass
 // re-reads the row (served from L2 / Infinity Cache after P1).
 template <typename T>
-__device__ __attribute__((noinline)) void generic_path(const GCtx g) {
+__device__ __attribute__((always_inline)) inline void generic_path(const GCtx g) {
   const int tid = threadIdx.x;
   const int lane = lane_id();
   const int wid = wave_id();
@@ -804,13 +808,14 @@ __device__ __attribute__((noinline)) void generic_path(const GCtx g) {
 namespace ns {
 
 // Every row kind: P1 streaming with group maxima, the small-k LDS set path and the
-// histogram paths.  Called for rows the streaming path does not take.
-// The kernel's argument block, read in place: passing the struct by value to a
-// non-inlined function would copy it to scratch memory.
+// histogram paths.  Called for rows the streaming path does not take.  Inlined (as is
+// everything it calls): a call would give the kernel a private segment for the callee's
+// saved registers, and a kernel with any private segment dispatches measurably slower
+// even when no wave touches it.  The kernel's argument block is read in place.
 typedef const KParams* KArgs;
 
 template <typename T>
-__device__ __attribute__((noinline)) void row_general(KArgs PA) {
+__device__ __attribute__((always_inline, cold)) inline void row_general(KArgs PA) {
   const KParams P = *PA;
   extern __shared__ __align__(16) unsigned char smem[];
   Misc* misc = reinterpret_cast<Misc*>(smem);
@@ -976,6 +981,19 @@ __device__ __attribute__((noinline)) void row_general(KArgs PA) {
   __syncthreads();
   const int U = misc->xl_n;
   flags |= misc->flags;
+  // small-k rows: the bound from the exact group maxima, which are then kept only
+  // rounded up to bfloat16, two per register, for the candidate pass (a larger value
+  // merely rescans a group)
+  const bool small_topk = !greedy && topk_on && k <= KSMALL;
+  const float tau = small_topk ? select_tau<NGROUP>(gm, rowthr, k, hcnt, misc) : NEG_INF;
+  uint32_t gm2[NGROUP / 2];
+#pragma unroll
+  for (int g = 0; g < NGROUP; ++g) {
+    const uint32_t gb = __float_as_uint(gm[g]);
+    const uint32_t up = (gb >> 31) == 0u && (gb & 0xffffu) != 0u ? (gb >> 16) + 1u : gb >> 16;
+    if (g & 1) gm2[g >> 1] |= up << 16;
+    else gm2[g >> 1] = up;
+  }
 
   // ---- row max over chunks and extras
   float my = rowthr ? tmax : NEG_INF;
@@ -1035,8 +1053,7 @@ __device__ __attribute__((noinline)) void row_general(KArgs PA) {
   }
 
   // ---- top-k with k <= KSMALL: threshold from chunk maxima, candidates to LDS
-  if (topk_on && k <= KSMALL) {
-    const float tau = select_tau<NGROUP>(gm, rowthr, k, hcnt, misc);
+  if (small_topk) {
     const float tc = lower_preimage(tau, tdiv, rdiv);
     if (tid == 0) misc->cand_n = 0;
     __syncthreads();
@@ -1050,8 +1067,9 @@ __device__ __attribute__((noinline)) void row_general(KArgs PA) {
       const int64_t jg = (nrows_j + NGROUP - 1) / NGROUP;
 #pragma unroll
       for (int g = 0; g < NGROUP; ++g) {
-        if (ballot(gm[g] >= tc) != 0ull) {
-          const bool hitg = gm[g] >= tc;
+        const float gmg = __uint_as_float((g & 1) ? (gm2[g >> 1] & 0xffff0000u) : (gm2[g >> 1] << 16));
+        if (ballot(gmg >= tc) != 0ull) {
+          const bool hitg = gmg >= tc;
           const int64_t j0 = g * jg;
           const int64_t j1 = j0 + jg < nrows_j ? j0 + jg : nrows_j;
           for (int64_t j = j0; j < j1; ++j) {
@@ -1110,7 +1128,7 @@ __global__ __launch_bounds__(NT) void sample_kernel(const KParams P) {
         const int st = row_fast<T>(RowArgs{P.logits, P.row_stride, P.vocab, P.hist_ids, P.out_ids, P.out_probs,
                                            P.out_info},
                                    row, src, temp, k, topp, pen, u, h0, h1 - h0, 0, misc, bm, xl_id, xl_val, cand);
-        if (st == 0) return;
+        if (__builtin_expect(st == 0, 1)) return;
       }
     }
   }

@@ -485,7 +485,7 @@ __device__ __forceinline__ void wave_select_draw(const uint64_t (&a)[R], int nk,
 // Every survivor is >= the row's k-th largest scaled value and the row maximum
 // is among them.
 template <int R>
-__device__ void wave_finalize(const uint64_t* list, int n, int k, bool topp_on, float p32, float tdiv, float rdiv,
+__device__ __forceinline__ void wave_finalize(const uint64_t* list, int n, int k, bool topp_on, float p32, float tdiv, float rdiv,
                               float u, int row, int64_t* out_ids, float* out_probs, int64_t V, int32_t* out_info,
                               int32_t flags, int32_t n_cand, int32_t path) {
   const int lane = lane_id();
@@ -518,7 +518,7 @@ __device__ void wave_finalize(const uint64_t* list, int n, int k, bool topp_on, 
 
 // Tail of the workgroup finaliser: wave 0 loads the first nk sorted keys from LDS.
 template <int R>
-__device__ void wave_select_draw_lds(const uint64_t* sorted, int nk, float M, float thr, bool topp_on, float p32,
+__device__ __forceinline__ void wave_select_draw_lds(const uint64_t* sorted, int nk, float M, float thr, bool topp_on, float p32,
                                      float u, int row, int64_t* out_ids, float* out_probs, int64_t V,
                                      int32_t* out_info, int32_t flags, int32_t n_cand, int32_t path) {
   const int lane = lane_id();

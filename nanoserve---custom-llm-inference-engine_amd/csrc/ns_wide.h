@@ -122,6 +122,7 @@ struct WideSmemT {
   int32_t ib[8];
   float fb[4];
   double db[4];
+  uint64_t kb[2];
 };
 using WideSmem = WideSmemT<1>;               // stats, histogram and probability passes
 using WideSmemCut = WideSmemT<WCAND>;        // the cut pass and its finaliser
@@ -436,25 +437,26 @@ struct WKeep {
 // rounding leaves u past the segment, the last token with a non-zero probability.
 // Every thread must call it.
 template <typename T, int NTH, typename SM>
-__device__ int64_t wide_locate(const WideParams& P, const WRowCtx& c, int s, double pstart, double rz, float M,
+__device__ __forceinline__ int64_t wide_locate(const WideParams& P, const WRowCtx& c, int s, double pstart, double rz, float M,
                                const WKeep& keep, SM* sm, int32_t* fl) {
   constexpr int EPC = T::EPC;
   const int tid = threadIdx.x;
   const int64_t c0 = (int64_t)s * SEG_CH;
   *fl |= wide_bitmap<T, NTH>(P, c, c0 * EPC, sm);
-  const int64_t nfull = c.V / EPC;
+  const uint32_t nbytes = (uint32_t)((c.V / EPC) * 16);
   if (tid == 0) { sm->ib[0] = 0x7fffffff; sm->ib[1] = -1; }
   const double ud = (double)c.u;
   double carry = pstart;
   for (int step = 0; step < SEG_CH / (NTH * WLOC); ++step) {
     const int64_t cb = c0 + (int64_t)step * NTH * WLOC + (int64_t)tid * WLOC;   // first chunk of this thread
+    uint4 raw[WLOC];
+#pragma unroll
+    for (int j = 0; j < WLOC; ++j) raw[j] = buf_load16_at(c.rowp, nbytes, (uint32_t)((cb + j) * 16), 0u);
     float p[WLOC * EPC];
 #pragma unroll
     for (int j = 0; j < WLOC; ++j) {
       const int64_t ch = cb + j;
-      const uint4 w = ch < nfull ? reinterpret_cast<const uint4*>(c.rowp)[ch]
-                                 : (ch == nfull && nfull * EPC < c.V ? load_tail_chunk<T>(c.rowp, ch, c.V)
-                                                                     : seg_ninf<T>());
+      const uint4 w = wide_chunk_fix<T>(c, ch, raw[j]);
       const uint32_t hb = c.pen_on ? T::bits(sm->bm, (int)(ch - c0)) : 0u;
       float y[EPC];
       chunk_y<T>(c, w, hb, ch * EPC, y);
@@ -907,6 +909,84 @@ __global__ __launch_bounds__(SNT) void wide_cut_kernel(const WideParams P) {
   }
 }
 
+// Ascending bitonic sort of the keys at positions [0, P2) of the workgroup, E per thread in
+// registers (position tid * E + j in k[j]); P2 a power of two with 64 * E <= P2 <= NT * E.
+// Compare-exchanges at a distance below E stay inside a thread, those below 64 * E go
+// between the lanes of a wave (DPP / permlane, no LDS), the longer ones through `buf`
+// (P2 keys of LDS, stored j-major so every exchange reads and writes consecutive
+// addresses).  Every thread must call it.
+template <int E>
+__device__ __forceinline__ void block_sort_regs(uint64_t (&k)[E], int P2, uint64_t* buf) {
+  // Every compare-exchange keeps the smaller key where flip is 0 and the larger where it is
+  // all ones, comparing the keys xored with flip: the direction never becomes a lane mask
+  // of its own (which the compiler would combine with the comparison on the scalar unit).
+  const int t = threadIdx.x;
+  const int lane = lane_id();
+  const bool act = t * E < P2;
+  for (int size = 2; size <= P2; size <<= 1) {
+    const bool asc_t = ((t * E) & size) == 0;
+    for (int stride = size >> 1; stride >= 64 * E; stride >>= 1) {
+      if (act) {
+#pragma unroll
+        for (int j = 0; j < E; ++j) buf[j * NT + t] = k[j];
+      }
+      __syncthreads();
+      if (act) {
+        const int pt = t ^ (stride / E);
+        const uint64_t flip = (((t & (stride / E)) == 0) == asc_t) ? 0ull : ~0ull;
+#pragma unroll
+        for (int j = 0; j < E; ++j) {
+          const uint64_t o = buf[j * NT + pt];
+          k[j] = (o ^ flip) < (k[j] ^ flip) ? o : k[j];
+        }
+      }
+      __syncthreads();
+    }
+    if (act) {
+#pragma unroll
+      for (int ls = 5; ls >= 0; --ls) {
+        if ((E << ls) < size) {
+          const uint64_t flip = (((lane & (1 << ls)) == 0) == asc_t) ? 0ull : ~0ull;
+#pragma unroll
+          for (int j = 0; j < E; ++j) {
+            const uint64_t o = lane_xor(k[j], 1 << ls);
+            k[j] = (o ^ flip) < (k[j] ^ flip) ? o : k[j];
+          }
+        }
+      }
+#pragma unroll
+      for (int s = E / 2; s >= 1; s >>= 1) {
+        if (s < size) {
+#pragma unroll
+          for (int j = 0; j < E; ++j) {
+            if ((j & s) == 0) {
+              const uint64_t flip = (((t * E + j) & size) == 0) ? 0ull : ~0ull;
+              const uint64_t a = k[j], b = k[j + s];
+              const bool sw = (b ^ flip) < (a ^ flip);
+              k[j] = sw ? b : a;
+              k[j + s] = sw ? a : b;
+            }
+          }
+        }
+      }
+    }
+  }
+}
+
+// The key at position pos of the keys held E per thread (a block broadcast, one barrier;
+// `slot` must not be read by another broadcast in flight).
+template <int E, typename SM>
+__device__ __forceinline__ uint64_t block_key_at(const uint64_t (&k)[E], int pos, uint64_t* slot, SM*) {
+  const int p0 = (int)threadIdx.x * E;
+  if (pos >= p0 && pos < p0 + E) {
+#pragma unroll
+    for (int j = 0; j < E; ++j)
+      if (p0 + j == pos) *slot = k[j];
+  }
+  __syncthreads();
+  return *slot;
+}
+
 // ------------------------------------------------------------------ pass 3b: the row's cut and draw
 // One 1024-thread workgroup per planned row: the planned elements ordered in LDS (value
 // descending, id ascending), the exact top-k threshold and top-p cut, the kept mass per
@@ -996,31 +1076,27 @@ __global__ __launch_bounds__(NT) void wide_final_kernel(const WideParams P) {
     if (tid == 0) { P.status[row] = 1; R->step = WSTEP_NONE; }
     return;
   }
-  // the planned elements as sort keys (value descending, id ascending), padded to a power of two
-  const int P2 = next_pow2(n < 2 ? 2 : n);
-  for (int i = tid; i < P2; i += NT) {
-    uint64_t key = ~0ull;
-    if (i < n) {
-      int s = 0;
-      while (s + 1 < P.S && sm.off[s + 1] <= i) ++s;
-      const uint64_t e = dc_load(P.cand + ((int64_t)row * P.S + s) * SEG_CAP + (i - sm.off[s]));
-      key = desc_key(__uint_as_float((uint32_t)(e >> 32)), (uint32_t)e);
-    }
-    sm.u.keys[i] = key;
-  }
-  __syncthreads();
-  for (int size = 2; size <= P2; size <<= 1) {
-    for (int stride = size >> 1; stride > 0; stride >>= 1) {
-      for (int i = tid; i < (P2 >> 1); i += NT) {
-        const int lo = 2 * i - (i & (stride - 1));
-        const int hi = lo + stride;
-        const bool up = (lo & size) == 0;
-        const uint64_t a = sm.u.keys[lo], b = sm.u.keys[hi];
-        if ((a > b) == up) { sm.u.keys[lo] = b; sm.u.keys[hi] = a; }
+  // the planned elements as sort keys (value descending, id ascending), EPT per thread in
+  // registers at positions tid * EPT + j, ordered over a power of two of positions
+  constexpr int EPT = WCAND / NT;
+  const int p0 = tid * EPT;
+  uint64_t kk[EPT];
+  {
+    int s = 0;
+#pragma unroll
+    for (int j = 0; j < EPT; ++j) {
+      const int i = p0 + j;
+      kk[j] = ~0ull;
+      if (i < n) {
+        while (s + 1 < P.S && sm.off[s + 1] <= i) ++s;
+        const uint64_t e = dc_load(P.cand + ((int64_t)row * P.S + s) * SEG_CAP + (i - sm.off[s]));
+        kk[j] = desc_key(__uint_as_float((uint32_t)(e >> 32)), (uint32_t)e);
       }
-      __syncthreads();
     }
   }
+  int P2 = next_pow2(n < 2 ? 2 : n);
+  if (P2 < 64 * EPT) P2 = 64 * EPT;
+  block_sort_regs<EPT>(kk, P2, sm.u.keys);
   // ---- top-k threshold: the k-th largest, k - 1 - n_above places into the ordered elements
   float thr = -__builtin_inff();
   if (kon) {
@@ -1029,18 +1105,15 @@ __global__ __launch_bounds__(NT) void wide_final_kernel(const WideParams P) {
       if (tid == 0) { P.status[row] = 1; R->step = WSTEP_NONE; }
       return;
     }
-    thr = desc_key_val(sm.u.keys[r]);
+    thr = desc_key_val(block_key_at<EPT>(kk, r, &sm.kb[0], &sm));
   }
   // per element: kept by top-k, its mass, its float32 probability under the top-k set
-  constexpr int EPT = WCAND / NT;
-  const int p0 = tid * EPT;
   unsigned long long mk = 0ull;
   int nk_own = 0;
 #pragma unroll
   for (int j = 0; j < EPT; ++j) {
-    const int pos = p0 + j;
-    if (pos < n) {
-      const float y = desc_key_val(sm.u.keys[pos]);
+    if (p0 + j < n) {
+      const float y = desc_key_val(kk[j]);
       if (y >= thr) { mk += wfx(M, y); ++nk_own; }
     }
   }
@@ -1062,10 +1135,9 @@ __global__ __launch_bounds__(NT) void wide_final_kernel(const WideParams P) {
     double qs = 0.0;
 #pragma unroll
     for (int j = 0; j < EPT; ++j) {
-      const int pos = p0 + j;
       qv[j] = 0.0f;
-      if (pos < n) {
-        const float y = desc_key_val(sm.u.keys[pos]);
+      if (p0 + j < n) {
+        const float y = desc_key_val(kk[j]);
         if (y >= thr) qv[j] = (float)((double)ns_expf(y - M) * rzk);
       }
       qs += (double)qv[j];
@@ -1074,16 +1146,18 @@ __global__ __launch_bounds__(NT) void wide_final_kernel(const WideParams P) {
     double run = base + wexcl_f64<NT>(qs, &tot, &sm);
     if (tid == 0) sm.ib[1] = 0x7fffffff;
     __syncthreads();
+    int cross = 0x7fffffff;
 #pragma unroll
     for (int j = 0; j < EPT; ++j) {
       const int pos = p0 + j;
       if (pos < n && pos < n_topk_c) {
         run += (double)qv[j];
-        if ((float)run > c.topp) atomicMin(&sm.ib[1], pos);
+        if ((float)run > c.topp && cross == 0x7fffffff) cross = pos;
       }
     }
+    if (cross != 0x7fffffff) atomicMin(&sm.ib[1], cross);
     __syncthreads();
-    const int cross = sm.ib[1];
+    cross = sm.ib[1];
     if (cross != 0x7fffffff) {
       J = cross;
     } else if (!kon0) {
@@ -1093,7 +1167,7 @@ __global__ __launch_bounds__(NT) void wide_final_kernel(const WideParams P) {
     }
   }
   if (J < 0) J = 0;
-  const uint64_t kc = sm.u.keys[J];
+  const uint64_t kc = block_key_at<EPT>(kk, J, &sm.kb[1], &sm);
   const float vstar = pon ? desc_key_val(kc) : -__builtin_inff();
   const int32_t istar = pon ? (int32_t)desc_key_id(kc) : 0x7fffffff;
   const int32_t n_kept = pon ? n_above + J + 1 : n_topk;
@@ -1104,12 +1178,11 @@ __global__ __launch_bounds__(NT) void wide_final_kernel(const WideParams P) {
   for (int j = 0; j < EPT; ++j) {
     const int pos = p0 + j;
     if (pos < n && pos <= J) {
-      const uint64_t key = sm.u.keys[pos];
-      const float y = desc_key_val(key);
+      const float y = desc_key_val(kk[j]);
       if (y >= thr) {
         const uint64_t fx = wfx(M, y);
         mkept += fx;
-        atomicAdd(&sm.segfx[desc_key_id(key) / SEG_EL], (unsigned long long)fx);
+        atomicAdd(&sm.segfx[desc_key_id(kk[j]) / SEG_EL], (unsigned long long)fx);
       }
     }
   }
