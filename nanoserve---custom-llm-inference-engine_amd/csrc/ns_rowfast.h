@@ -8,9 +8,10 @@
 //   * Top-k rows with a penalty >= 1 (or none): every chunk of the row is
 //     requested at once (chunk q*NT + t to thread t), the history ids behind it.
 //     Such a penalty never raises a value and keeps NaN / +inf, so the row is
-//     processed raw: chunk maxima as the row lands, the history bitmap from the
-//     ids behind it, then a lower bound of the k-th largest (the k-th largest of
-//     the maxima of every 8-lane group, by a ballot radix select).  Each wave
+//     processed raw: chunk maxima as the row lands, then a lower bound of the
+//     k-th largest (the k-th largest of the maxima of every 8-lane group, by a
+//     ballot radix select in one wave while the others build the history bitmap
+//     from the ids requested ahead of the row).  Each wave
 //     stages its chunks that reach the bound in LDS and expands them into a
 //     candidate list, penalized at history positions; a count check confirms the
 //     list still covers the top-k.  The list is ordered by the whole workgroup
@@ -383,8 +384,17 @@ __device__ __forceinline__ int row_fast(const RowArgs P, const int row, const in
     uniform_row(anynan ? __builtin_nanf("") : __builtin_inff());
     return 0;
   }
-  // the history bitmap (set semantics, sampler.py:34-38), built by every wave (no wave waits
-  // for its atomics before the barrier)
+  // lower bound of the k-th largest raw value: the k-th largest of the group maxima, its
+  // key truncated to the bits a bfloat16 value carries (24 for float32)
+  if (wid == 0) {
+    const uint32_t kp = wave_kth_key<T::SZ == 2 ? 16 : 24>(fkey(fs[lane]), fkey(fs[64 + lane]), k);
+    const float taux = kp <= fkey(-__builtin_inff()) ? -__builtin_inff() : fkey_inv(kp);
+    // x >= tc  <=>  x / t >= RN(taux / t)
+    if (lane == 0) misc->fb[0] = lower_preimage(taux, tdiv, rdiv);
+  }
+  // the history bitmap (set semantics, sampler.py:34-38), built by every wave while wave 0
+  // selects the bound (wave 0 adds its share after it; no wave waits for its atomics before
+  // the barrier)
   if (pen_on) {
     bool bad = false;
     for (int base = 0; base < H; base += RHB * NT) {
@@ -399,14 +409,6 @@ __device__ __forceinline__ int row_fast(const RowArgs P, const int row, const in
       }
     }
     if (bad) atomicOr(&misc->flags, FLAG_BAD_HIST_ID);
-  }
-  // lower bound of the k-th largest raw value: the k-th largest of the group maxima, its
-  // key truncated to the bits a bfloat16 value carries (24 for float32)
-  if (wid == 0) {
-    const uint32_t kp = wave_kth_key<T::SZ == 2 ? 16 : 24>(fkey(fs[lane]), fkey(fs[64 + lane]), k);
-    const float taux = kp <= fkey(-__builtin_inff()) ? -__builtin_inff() : fkey_inv(kp);
-    // x >= tc  <=>  x / t >= RN(taux / t)
-    if (lane == 0) misc->fb[0] = lower_preimage(taux, tdiv, rdiv);
   }
   __syncthreads();   // the bound, the bitmap
   const float tc = misc->fb[0];
