@@ -26,7 +26,7 @@
 extern "C" {
 #endif
 
-#define NS_ABI_VERSION 4
+#define NS_ABI_VERSION 5
 
 #define NS_OK 0
 #define NS_ERR_INVALID 1   /* bad argument (message says which) */
@@ -98,6 +98,14 @@ typedef struct ns_sample_args {
   int32_t        mode;          /* NS_MODE_*: which kernels resolve which rows (results are identical) */
   uint32_t       row_kinds;     /* NS_KIND_* bits of the kinds of rows present, or 0 when unknown: a call
                                    declared without NS_KIND_OTHER rows skips the launches for them */
+  const void*    hist_state;    /* device-resident histories (ns_hist_state_bytes), or NULL.  With it the
+                                   histories are read from the state instead of hist_offsets / hist_ids
+                                   (both must be NULL): row r's history is the id list of request slot
+                                   hist_slot[r], kept on the device across calls (the lists the engine
+                                   rebuilds and copies every step, engine.py:242-246) */
+  const int32_t* hist_slot;     /* [B] request slot of each row, -1 for a row without history */
+  int32_t        hist_n_slots;  /* slots in hist_state */
+  int32_t        hist_capacity; /* token ids per slot */
 } ns_sample_args;
 
 /* Version of this ABI (NS_ABI_VERSION). */
@@ -116,6 +124,25 @@ int ns_sample_workspace_bytes(int32_t n_sample, int64_t vocab, int32_t dtype, ui
 
 /* LDS bytes one workgroup of ns_sample needs for this vocab and history bound. */
 int ns_sample_lds_bytes(int64_t vocab, int32_t max_hist, int32_t* lds_bytes);
+
+/* Device-resident histories: one id list per request slot, capacity ids each, laid out as
+ * int32 lengths[n_slots] (padded to 256 bytes) then int32 ids[n_slots][capacity].  The
+ * caller owns the buffer (zero-filled: every slot empty).  No counterpart in the reference,
+ * which rebuilds every history on the host and copies it each step (engine.py:242-246,
+ * sampler.py:34); these keep them on the device, appended in place. */
+int ns_hist_state_bytes(int32_t n_slots, int32_t capacity, uint64_t* bytes);
+
+/* Set slot `slot`'s history to ids[0..n) (device pointer): a new request's prompt tokens
+ * (engine.py:242-243).  n <= capacity.  Asynchronous on stream. */
+int ns_hist_assign(void* state, int32_t n_slots, int32_t capacity, int32_t slot, const int32_t* ids, int32_t n,
+                   hipStream_t stream);
+
+/* Append token_ids[r] to slot slots[r] for r < n (device pointers): the sampled tokens join
+ * their requests' histories for the next call (scheduler.py:281-284 appending to
+ * output_token_ids).  Rows with a negative slot are skipped; a full slot is left unchanged
+ * and counted in *overflow (device int32, or NULL).  Asynchronous on stream. */
+int ns_hist_append(void* state, int32_t n_slots, int32_t capacity, const int32_t* slots, const int64_t* token_ids,
+                   int32_t n, int32_t* overflow, hipStream_t stream);
 
 /* Last error message of the calling thread ("" if none). */
 const char* ns_last_error(void);

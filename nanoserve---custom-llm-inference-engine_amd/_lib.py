@@ -24,10 +24,11 @@ NS_MODE_PER_ROW = 2
 NS_KIND_GREEDY = 1      # row_kinds: greedy rows (temperature 0)
 NS_KIND_SMALL_K = 2     # sampled rows with 1 <= top_k <= 64 and top_k < vocab
 NS_KIND_OTHER = 4       # every other sampled row (top-k off or larger)
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 # exported symbols, as declared in include/ns_sampling.h
-EXPORTS = ("ns_abi_version", "ns_sample", "ns_sample_lds_bytes", "ns_sample_workspace_bytes", "ns_last_error")
+EXPORTS = ("ns_abi_version", "ns_sample", "ns_sample_lds_bytes", "ns_sample_workspace_bytes", "ns_hist_state_bytes",
+           "ns_hist_assign", "ns_hist_append", "ns_last_error")
 
 
 class NsSampleArgs(ctypes.Structure):
@@ -56,6 +57,10 @@ class NsSampleArgs(ctypes.Structure):
         ("workspace_bytes", ctypes.c_uint64),
         ("mode", ctypes.c_int32),
         ("row_kinds", ctypes.c_uint32),
+        ("hist_state", ctypes.c_void_p),
+        ("hist_slot", ctypes.c_void_p),
+        ("hist_n_slots", ctypes.c_int32),
+        ("hist_capacity", ctypes.c_int32),
     ]
 
 
@@ -84,6 +89,14 @@ def load(path: str = LIB_PATH) -> ctypes.CDLL:
     lib.ns_sample_workspace_bytes.restype = ctypes.c_int
     lib.ns_sample_workspace_bytes.argtypes = [ctypes.c_int32, ctypes.c_int64, ctypes.c_int32,
                                               ctypes.POINTER(ctypes.c_uint64)]
+    lib.ns_hist_state_bytes.restype = ctypes.c_int
+    lib.ns_hist_state_bytes.argtypes = [ctypes.c_int32, ctypes.c_int32, ctypes.POINTER(ctypes.c_uint64)]
+    lib.ns_hist_assign.restype = ctypes.c_int
+    lib.ns_hist_assign.argtypes = [ctypes.c_void_p, ctypes.c_int32, ctypes.c_int32, ctypes.c_int32, ctypes.c_void_p,
+                                   ctypes.c_int32, ctypes.c_void_p]
+    lib.ns_hist_append.restype = ctypes.c_int
+    lib.ns_hist_append.argtypes = [ctypes.c_void_p, ctypes.c_int32, ctypes.c_int32, ctypes.c_void_p, ctypes.c_void_p,
+                                   ctypes.c_int32, ctypes.c_void_p, ctypes.c_void_p]
     lib.ns_last_error.restype = ctypes.c_char_p
     lib.ns_last_error.argtypes = []
     v = lib.ns_abi_version()
@@ -181,7 +194,8 @@ def aligned_rows(logits, sample_idx):
 
 def sample_raw(logits, temperature, top_k, top_p, rep_penalty, uniforms, out_ids, *, sample_idx=None,
                hist_offsets=None, hist_ids=None, max_hist: int = 0, out_probs=None, out_info=None,
-               stream=None, workspace="auto", mode: int = NS_MODE_AUTO, row_kinds: int = 0) -> None:
+               stream=None, workspace="auto", mode: int = NS_MODE_AUTO, row_kinds: int = 0,
+               hist_state=None, hist_slot=None) -> None:
     """Launch ``ns_sample`` on device tensors (no copies, no synchronisation).
 
     logits: (N, V) float32 or bfloat16 CUDA tensor with unit stride in the last dim.
@@ -190,7 +204,9 @@ def sample_raw(logits, temperature, top_k, top_p, rep_penalty, uniforms, out_ids
     out_ids: (B,) int64; out_probs: (B, V) float32 or None; out_info: (B, 8) int32 or None.
     workspace: "auto" (a cached per-device workspace), a uint8 CUDA tensor, or None (every row
     takes the one-workgroup-per-row kernel).  row_kinds: NS_KIND_* bits of the rows present
-    (see ``row_kinds``), 0 when unknown.
+    (see ``row_kinds``), 0 when unknown.  hist_state / hist_slot: device-resident histories
+    (a ``HistoryState`` and the (B,) int32 slot of each row, -1 for none) instead of
+    hist_offsets / hist_ids.
     """
     import torch
 
@@ -231,6 +247,56 @@ def sample_raw(logits, temperature, top_k, top_p, rep_penalty, uniforms, out_ids
         a.workspace_bytes = int(workspace.numel() * workspace.element_size())
     a.mode = int(mode)
     a.row_kinds = int(row_kinds)
+    if hist_state is not None:
+        if hist_offsets is not None or hist_ids is not None:
+            raise ValueError("hist_state excludes hist_offsets / hist_ids")
+        a.hist_state = _ptr(hist_state.buffer)
+        a.hist_slot = _ptr(hist_slot)
+        a.hist_n_slots = int(hist_state.n_slots)
+        a.hist_capacity = int(hist_state.capacity)
     if stream is None:
         stream = torch.cuda.current_stream(logits.device)
     check(lib.ns_sample(ctypes.byref(a), ctypes.c_void_p(int(stream.cuda_stream))))
+
+
+def hist_state_bytes(n_slots: int, capacity: int) -> int:
+    out = ctypes.c_uint64(0)
+    check(load().ns_hist_state_bytes(int(n_slots), int(capacity), ctypes.byref(out)))
+    return int(out.value)
+
+
+class HistoryState:
+    """Device-resident histories: ``n_slots`` request slots of up to ``capacity`` token ids.
+
+    The buffer is the layout ``ns_hist_state_bytes`` describes (lengths, then ids), zero
+    filled, so every slot starts empty.  ``assign`` sets a slot (a request's prompt) and
+    ``append`` adds one sampled token per row; both run on the given stream.
+    """
+
+    def __init__(self, device, n_slots: int, capacity: int):
+        import torch
+
+        self.n_slots = int(n_slots)
+        self.capacity = int(capacity)
+        self.buffer = torch.zeros(hist_state_bytes(self.n_slots, self.capacity), dtype=torch.uint8, device=device)
+        self.overflow = torch.zeros(1, dtype=torch.int32, device=device)
+
+    def assign(self, slot: int, ids, stream=None) -> None:
+        """Slot ``slot`` holds ``ids`` ((n,) int32 device tensor, n <= capacity) from now on."""
+        import torch
+
+        if stream is None:
+            stream = torch.cuda.current_stream(self.buffer.device)
+        n = int(ids.numel()) if ids is not None else 0
+        check(load().ns_hist_assign(_ptr(self.buffer), self.n_slots, self.capacity, int(slot),
+                                    _ptr(ids) if n > 0 else 0, n, ctypes.c_void_p(int(stream.cuda_stream))))
+
+    def append(self, slots, token_ids, stream=None) -> None:
+        """token_ids[r] joins slot slots[r] ((B,) int32 and (B,) int64 device tensors)."""
+        import torch
+
+        if stream is None:
+            stream = torch.cuda.current_stream(self.buffer.device)
+        check(load().ns_hist_append(_ptr(self.buffer), self.n_slots, self.capacity, _ptr(slots), _ptr(token_ids),
+                                    int(slots.numel()), _ptr(self.overflow),
+                                    ctypes.c_void_p(int(stream.cuda_stream))))

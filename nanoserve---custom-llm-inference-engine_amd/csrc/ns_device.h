@@ -77,6 +77,29 @@ template <typename T> __device__ __forceinline__ T lane_xor(T v, int s) {
     return __builtin_bit_cast(T, (hi << 32) | lo);
   }
 }
+// Start h0 and end h1 of sampled row `row`'s history in the id store: CSR offsets
+// (off[row], off[row + 1]), a device-resident request slot s = slot[row] (ids
+// s * cap .. s * cap + len[s]), or none (0, 0).  A slot outside [-1, nslots) or a length
+// outside [0, cap] gives (0, -1), which every kernel treats as an invalid history.
+__device__ __forceinline__ void row_history(const int32_t* off, const int32_t* slot, const int32_t* len,
+                                            int32_t nslots, int32_t cap, int row, int32_t& h0, int32_t& h1) {
+  h0 = 0;
+  h1 = 0;
+  if (off != nullptr) {
+    h0 = off[row];
+    h1 = off[row + 1];
+  } else if (slot != nullptr) {
+    const int32_t s = slot[row];
+    if (s >= nslots || s < -1) {
+      h1 = -1;
+    } else if (s >= 0) {
+      const int32_t n = len[s];
+      h0 = s * cap;
+      h1 = (n >= 0 && n <= cap) ? h0 + n : -1;
+      if (h1 < 0) h0 = 0;
+    }
+  }
+}
 // A wave-uniform double taken from the first active lane (scalar registers).
 __device__ __forceinline__ double uniform_f64(double v) {
   const uint64_t u = __builtin_bit_cast(uint64_t, v);

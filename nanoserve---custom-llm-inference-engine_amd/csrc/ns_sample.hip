@@ -849,7 +849,7 @@ __device__ __attribute__((always_inline, cold)) inline void row_general(KArgs PA
   u = (u >= 0.0f) ? (u < 1.0f ? u : 0x1.fffffep-1f) : 0.0f;
   const int32_t k = P.top_k[row];
   int32_t h0 = 0, h1 = 0;
-  if (P.hist_off != nullptr) { h0 = P.hist_off[row]; h1 = P.hist_off[row + 1]; }
+  row_history(P.hist_off, P.hist_slot, P.hist_len, P.hist_nslots, P.hist_cap, row, h0, h1);
   int32_t flags = 0;
   if (src < 0 || src >= P.n_rows_total) flags |= FLAG_BAD_ROW;
   if (h1 < h0 || h1 - h0 > MAX_HIST || h1 - h0 > P.xcap - 8) flags |= FLAG_HIST_TOO_LONG;
@@ -1111,7 +1111,7 @@ __global__ __launch_bounds__(NT) void sample_kernel(const KParams P) {
   float u = P.uniforms[row];
   const int64_t src = P.sample_idx ? P.sample_idx[row] : (int64_t)row;
   int32_t h0 = 0, h1 = 0;
-  if (P.hist_off != nullptr) { h0 = P.hist_off[row]; h1 = P.hist_off[row + 1]; }
+  row_history(P.hist_off, P.hist_slot, P.hist_len, P.hist_nslots, P.hist_cap, row, h0, h1);
   // rows the segment kernel resolved carry status 0; every other row carries 1
   if (P.status != nullptr && P.status[row] == 0) return;
   if (P.fast) {
@@ -1135,6 +1135,35 @@ __global__ __launch_bounds__(NT) void sample_kernel(const KParams P) {
   row_general<T>((KArgs)__builtin_amdgcn_kernarg_segment_ptr());
 }
 
+// ---- device-resident histories: slot s holds its length in lens[s] and its ids in
+// ids[s * cap .. s * cap + lens[s])
+
+// ids[0..n) become slot `slot`'s history (a request's prompt, engine.py:242-243).
+__global__ __launch_bounds__(256) void hist_assign_kernel(int32_t* lens, int32_t* ids, int32_t cap, int32_t slot,
+                                                          const int32_t* src, int32_t n) {
+  int32_t* dst = ids + (int64_t)slot * cap;
+  for (int i = blockIdx.x * 256 + threadIdx.x; i < n; i += gridDim.x * 256) dst[i] = src[i];
+  if (blockIdx.x == 0 && threadIdx.x == 0) lens[slot] = n;
+}
+
+// Row r's sampled token joins slot slots[r] (scheduler.py:281-284 appending to
+// output_token_ids).  One thread per row; the rows of a call name distinct slots.
+__global__ __launch_bounds__(256) void hist_append_kernel(int32_t* lens, int32_t* ids, int32_t nslots, int32_t cap,
+                                                          const int32_t* slots, const int64_t* tok, int32_t n,
+                                                          int32_t* overflow) {
+  const int r = blockIdx.x * 256 + threadIdx.x;
+  if (r >= n) return;
+  const int32_t s = slots[r];
+  if (s < 0 || s >= nslots) return;
+  const int32_t l = lens[s];
+  if (l < 0 || l >= cap) {
+    if (overflow != nullptr) atomicAdd(overflow, 1);
+    return;
+  }
+  ids[(int64_t)s * cap + l] = (int32_t)tok[r];
+  lens[s] = l + 1;
+}
+
 }  // namespace ns
 
 // =====================================================================================
@@ -1151,6 +1180,19 @@ int fail(int code, const std::string& msg) {
 int64_t seg_elems(int32_t dtype) { return (int64_t)ns::SEG_CH * (dtype == NS_DTYPE_BF16 ? 8 : 4); }
 int64_t seg_count(int64_t vocab, int32_t dtype) { return (vocab + seg_elems(dtype) - 1) / seg_elems(dtype); }
 int64_t align256(int64_t x) { return (x + 255) / 256 * 256; }
+
+// Device-resident history state: int32 lengths[n_slots] padded to 256 bytes, then int32
+// ids[n_slots][capacity].
+int hist_state_check(int32_t n_slots, int32_t capacity) {
+  if (n_slots <= 0) return fail(NS_ERR_INVALID, "hist_n_slots must be > 0");
+  if (capacity <= 0 || capacity > NS_MAX_HISTORY)
+    return fail(NS_ERR_INVALID, "hist_capacity must be in [1, " + std::to_string(NS_MAX_HISTORY) + "]");
+  if ((int64_t)n_slots * capacity > INT32_MAX) return fail(NS_ERR_INVALID, "hist_n_slots * hist_capacity > 2^31 - 1");
+  return NS_OK;
+}
+const int32_t* hist_state_ids(const void* state, int32_t n_slots) {
+  return reinterpret_cast<const int32_t*>(static_cast<const unsigned char*>(state) + align256((int64_t)n_slots * 4));
+}
 
 struct WsLayout {
   int64_t counters, status, stats, cand, wrow, hcnt, hmass, total;
@@ -1181,6 +1223,48 @@ WsLayout ws_layout(int32_t n_sample, int64_t vocab, int32_t dtype) {
 extern "C" {
 
 int ns_abi_version(void) { return NS_ABI_VERSION; }
+
+int ns_hist_state_bytes(int32_t n_slots, int32_t capacity, uint64_t* bytes) {
+  if (bytes == nullptr) return fail(NS_ERR_INVALID, "bytes is NULL");
+  const int rc = hist_state_check(n_slots, capacity);
+  if (rc != NS_OK) return rc;
+  *bytes = (uint64_t)(align256((int64_t)n_slots * 4) + (int64_t)n_slots * capacity * 4);
+  return NS_OK;
+}
+
+int ns_hist_assign(void* state, int32_t n_slots, int32_t capacity, int32_t slot, const int32_t* ids, int32_t n,
+                   hipStream_t stream) {
+  if (state == nullptr) return fail(NS_ERR_INVALID, "state is NULL");
+  int rc = hist_state_check(n_slots, capacity);
+  if (rc != NS_OK) return rc;
+  if (slot < 0 || slot >= n_slots) return fail(NS_ERR_INVALID, "slot out of range");
+  if (n < 0 || n > capacity) return fail(NS_ERR_INVALID, "n must be in [0, capacity]");
+  if (n > 0 && ids == nullptr) return fail(NS_ERR_INVALID, "ids is NULL");
+  int32_t* lens = static_cast<int32_t*>(state);
+  int32_t* store = const_cast<int32_t*>(hist_state_ids(state, n_slots));
+  const unsigned blocks = (unsigned)((n + 255) / 256 > 0 ? ((n + 255) / 256 < 64 ? (n + 255) / 256 : 64) : 1);
+  hipLaunchKernelGGL(ns::hist_assign_kernel, dim3(blocks), dim3(256), 0, stream, lens, store, capacity, slot, ids, n);
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return fail(NS_ERR_HIP, std::string("hist_assign launch: ") + hipGetErrorString(e));
+  return NS_OK;
+}
+
+int ns_hist_append(void* state, int32_t n_slots, int32_t capacity, const int32_t* slots, const int64_t* token_ids,
+                   int32_t n, int32_t* overflow, hipStream_t stream) {
+  if (state == nullptr) return fail(NS_ERR_INVALID, "state is NULL");
+  int rc = hist_state_check(n_slots, capacity);
+  if (rc != NS_OK) return rc;
+  if (n < 0) return fail(NS_ERR_INVALID, "n < 0");
+  if (n == 0) return NS_OK;
+  if (slots == nullptr || token_ids == nullptr) return fail(NS_ERR_INVALID, "slots or token_ids is NULL");
+  int32_t* lens = static_cast<int32_t*>(state);
+  int32_t* store = const_cast<int32_t*>(hist_state_ids(state, n_slots));
+  hipLaunchKernelGGL(ns::hist_append_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream, lens, store,
+                     n_slots, capacity, slots, token_ids, n, overflow);
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return fail(NS_ERR_HIP, std::string("hist_append launch: ") + hipGetErrorString(e));
+  return NS_OK;
+}
 
 const char* ns_last_error(void) { return g_err.c_str(); }
 
@@ -1224,6 +1308,19 @@ int ns_sample(const ns_sample_args* a, hipStream_t stream) {
   if (a->sample_idx == nullptr && a->n_rows_total < a->n_sample)
     return fail(NS_ERR_INVALID, "n_rows_total < n_sample without sample_idx");
   if (a->hist_offsets != nullptr && a->hist_ids == nullptr) return fail(NS_ERR_INVALID, "hist_ids is NULL");
+  // history source: CSR offsets and ids, device-resident request slots, or none
+  const bool slots = a->hist_state != nullptr;
+  if (slots) {
+    if (a->hist_offsets != nullptr || a->hist_ids != nullptr)
+      return fail(NS_ERR_INVALID, "hist_state excludes hist_offsets and hist_ids");
+    if (a->hist_slot == nullptr) return fail(NS_ERR_INVALID, "hist_slot is NULL");
+    const int rs = hist_state_check(a->hist_n_slots, a->hist_capacity);
+    if (rs != NS_OK) return rs;
+  }
+  const bool has_hist = a->hist_offsets != nullptr || slots;
+  const int32_t* h_ids = slots ? hist_state_ids(a->hist_state, a->hist_n_slots) : a->hist_ids;
+  const int32_t* h_len = slots ? static_cast<const int32_t*>(a->hist_state) : nullptr;
+  const int32_t* h_slot = slots ? a->hist_slot : nullptr;
   if (a->max_hist < 0 || a->max_hist > NS_MAX_HISTORY)
     return fail(NS_ERR_INVALID, "max_hist must be in [0, " + std::to_string(NS_MAX_HISTORY) + "]");
   const int esz = a->dtype == NS_DTYPE_F32 ? 4 : 2;
@@ -1232,7 +1329,7 @@ int ns_sample(const ns_sample_args* a, hipStream_t stream) {
   const WsLayout L = ws_layout(a->n_sample, a->vocab, a->dtype);
 
   int32_t lds = 0;
-  int rc = ns_sample_lds_bytes(a->vocab, a->hist_offsets ? a->max_hist : 0, &lds);
+  int rc = ns_sample_lds_bytes(a->vocab, has_hist ? a->max_hist : 0, &lds);
   if (rc != NS_OK) return rc;
   ns::KParams p{};
   p.logits = a->logits;
@@ -1245,14 +1342,18 @@ int ns_sample(const ns_sample_args* a, hipStream_t stream) {
   p.top_p = a->top_p;
   p.penalty = a->rep_penalty;
   p.hist_off = a->hist_offsets;
-  p.hist_ids = a->hist_ids;
+  p.hist_ids = h_ids;
+  p.hist_slot = h_slot;
+  p.hist_len = h_len;
+  p.hist_nslots = a->hist_n_slots;
+  p.hist_cap = a->hist_capacity;
   p.uniforms = a->uniforms;
   p.out_ids = a->out_ids;
   p.out_probs = a->out_probs;
   p.out_info = a->out_info;
   p.n_sample = a->n_sample;
   {
-    const int64_t mh = a->hist_offsets ? a->max_hist : 0;
+    const int64_t mh = has_hist ? a->max_hist : 0;
     const int64_t nbw = (a->vocab + 31) / 32;
     const int64_t uniq = mh < a->vocab ? mh : a->vocab;
     const int64_t xcap = ((uniq + 8 + 3) / 4) * 4;
@@ -1329,7 +1430,11 @@ int ns_sample(const ns_sample_args* a, hipStream_t stream) {
     s.top_p = a->top_p;
     s.penalty = a->rep_penalty;
     s.hist_off = a->hist_offsets;
-    s.hist_ids = a->hist_ids;
+    s.hist_ids = h_ids;
+    s.hist_slot = h_slot;
+    s.hist_len = h_len;
+    s.hist_nslots = a->hist_n_slots;
+    s.hist_cap = a->hist_capacity;
     s.uniforms = a->uniforms;
     s.out_ids = a->out_ids;
     s.out_probs = a->out_probs;
@@ -1369,7 +1474,11 @@ int ns_sample(const ns_sample_args* a, hipStream_t stream) {
     w.top_p = a->top_p;
     w.penalty = a->rep_penalty;
     w.hist_off = a->hist_offsets;
-    w.hist_ids = a->hist_ids;
+    w.hist_ids = h_ids;
+    w.hist_slot = h_slot;
+    w.hist_len = h_len;
+    w.hist_nslots = a->hist_n_slots;
+    w.hist_cap = a->hist_capacity;
     w.uniforms = a->uniforms;
     w.out_ids = a->out_ids;
     w.out_probs = a->out_probs;

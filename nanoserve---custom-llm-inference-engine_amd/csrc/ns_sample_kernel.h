@@ -64,6 +64,9 @@ struct KParams {
   const float* penalty;
   const int32_t* hist_off;
   const int32_t* hist_ids;
+  const int32_t* hist_slot;   // device-resident histories: request slot of each row (-1: none), or NULL
+  const int32_t* hist_len;    // slot lengths (hist_ids then holds hist_nslots * hist_cap ids)
+  int32_t hist_nslots, hist_cap;
   const float* uniforms;
   int64_t* out_ids;
   float* out_probs;

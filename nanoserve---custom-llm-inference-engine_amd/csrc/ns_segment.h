@@ -72,6 +72,9 @@ struct SegParams {
   const float* penalty;
   const int32_t* hist_off;
   const int32_t* hist_ids;
+  const int32_t* hist_slot;   // device-resident histories: request slot of each row (-1: none), or NULL
+  const int32_t* hist_len;    // slot lengths (hist_ids then holds hist_nslots * hist_cap ids)
+  int32_t hist_nslots, hist_cap;
   const float* uniforms;
   int64_t* out_ids;
   float* out_probs;
@@ -281,7 +284,6 @@ struct SegSmem {
   float fred[SNW];
   int32_t ired[SNW];
   int32_t wbase[SNW];
-  int32_t xl_n;
   int32_t cnt;
   int32_t last;
   int32_t flags;
@@ -319,6 +321,22 @@ __device__ __forceinline__ int32_t seg_min_i(int32_t v, SegSmem* sm) {
   for (int w = 1; w < SNW; ++w) r = sm->ired[w] < r ? sm->ired[w] : r;
   __syncthreads();
   return r;
+}
+// Exclusive prefix sum over the 4 waves' threads; *total receives the sum (two barriers).
+__device__ __forceinline__ int32_t seg_excl_i(int32_t v, int32_t* total, SegSmem* sm) {
+  const int32_t inc = wave_incl_scan(v);
+  if (lane_id() == 63) sm->ired[wave_id()] = inc;
+  __syncthreads();
+  int32_t off = 0, tot = 0;
+#pragma unroll
+  for (int w = 0; w < SNW; ++w) {
+    const int32_t t = sm->ired[w];
+    if (w < wave_id()) off += t;
+    tot += t;
+  }
+  __syncthreads();
+  *total = tot;
+  return off + inc - v;
 }
 __device__ __forceinline__ int32_t seg_sum_i(int32_t v, SegSmem* sm) {
   v = wave_sum(v);
@@ -738,7 +756,7 @@ __device__ __forceinline__ void segment_body(const SegParams& P, SegSmem& sm) {
   }
   const int64_t src = P.sample_idx ? P.sample_idx[row] : (int64_t)row;
   int32_t h0 = 0, h1 = 0;
-  if (P.hist_off != nullptr) { h0 = P.hist_off[row]; h1 = P.hist_off[row + 1]; }
+  row_history(P.hist_off, P.hist_slot, P.hist_len, P.hist_nslots, P.hist_cap, row, h0, h1);
   if (src < 0 || src >= P.n_rows_total || h0 < 0 || h1 < h0 || h1 - h0 > MAX_HIST) {
     // invalid row: the per-row kernel reports it
     if (seg == 0 && tid == 0) P.status[row] = 1;
@@ -783,7 +801,7 @@ __device__ __forceinline__ void segment_body(const SegParams& P, SegSmem& sm) {
   int U = 0;
   if (pen_on) {
     for (int i = tid; i < SEG_EL / 32; i += SNT) sm.bm[i] = 0u;
-    if (tid == 0) { sm.flags = 0; sm.xl_n = 0; }
+    if (tid == 0) sm.flags = 0;
     __syncthreads();
     const int32_t* hp = P.hist_ids + h0;
     bool bad = false;
@@ -797,32 +815,45 @@ __device__ __forceinline__ void segment_body(const SegParams& P, SegSmem& sm) {
 #pragma unroll
       for (int s = 0; s < HBATCH; ++s) {
         const int j = base + s * SNT + tid;
-        bool uniq = false;
         if (j < H) {
           const int32_t id = hv[s];
           if (id < 0 || (int64_t)id >= V) {
             bad = true;
           } else if ((int64_t)id >= e0 && (int64_t)id < e0 + SEG_EL) {
             const int32_t l = id - (int32_t)e0;
-            const uint32_t bit = 1u << (l & 31);
-            uniq = (atomicOr(&sm.bm[l >> 5], bit) & bit) == 0u;
+            atomicOr(&sm.bm[l >> 5], 1u << (l & 31));
           }
-        }
-        const uint64_t m = ballot(uniq);
-        if (m != 0ull) {
-          int wb = 0;
-          if (lane == 0) wb = atomicAdd(&sm.xl_n, __popcll(m));
-          wb = read_lane(wb, 0);
-          const int pos = wb + lanes_below(m);
-          if (uniq && pos < XCAP) sm.xl_id[pos] = hv[s];
         }
       }
     }
     if (bad) atomicOr(&sm.flags, FLAG_BAD_HIST_ID);
     __syncthreads();
     flags |= sm.flags;
-    U = sm.xl_n;
+    // the unique ids in ascending order, read off the finished bitmap (a list built by
+    // appending in atomic order would hand the extras to threads in a different order
+    // every run, and with them the segment's bound and candidate count)
+    constexpr int WPT = SEG_EL / 32 / SNT;   // bitmap words per thread
+    static_assert(WPT * SNT * 32 == SEG_EL, "segment bitmap split evenly over the threads");
+    uint32_t wv[WPT];
+    int32_t c = 0;
+#pragma unroll
+    for (int j = 0; j < WPT; ++j) {
+      wv[j] = sm.bm[tid * WPT + j];
+      c += __popc(wv[j]);
+    }
+    int32_t pos = seg_excl_i(c, &U, &sm);
+#pragma unroll
+    for (int j = 0; j < WPT; ++j) {
+      uint32_t m = wv[j];
+      while (m != 0u) {
+        const int b = __builtin_ctz(m);
+        m &= m - 1u;
+        if (pos < XCAP) sm.xl_id[pos] = (int32_t)e0 + (tid * WPT + j) * 32 + b;
+        ++pos;
+      }
+    }
     if (U > XCAP) { flags |= SFLAG_XOVER; U = XCAP; }
+    __syncthreads();   // the list before the extras are gathered
   }
 
   // ---- extras: thread t gathers and penalizes entries t, t+SNT, ... (issued before the chunk work)

@@ -84,6 +84,9 @@ struct WideParams {
   const float* penalty;
   const int32_t* hist_off;
   const int32_t* hist_ids;
+  const int32_t* hist_slot;   // device-resident histories: request slot of each row (-1: none), or NULL
+  const int32_t* hist_len;    // slot lengths (hist_ids then holds hist_nslots * hist_cap ids)
+  int32_t hist_nslots, hist_cap;
   const float* uniforms;
   int64_t* out_ids;
   float* out_probs;
@@ -262,7 +265,7 @@ __device__ __forceinline__ WRowCtx wide_row_ctx(const WideParams& P, int row) {
   c.src = P.sample_idx ? P.sample_idx[row] : (int64_t)row;
   int32_t h1 = 0;
   c.h0 = 0;
-  if (P.hist_off != nullptr) { c.h0 = P.hist_off[row]; h1 = P.hist_off[row + 1]; }
+  row_history(P.hist_off, P.hist_slot, P.hist_len, P.hist_nslots, P.hist_cap, row, c.h0, h1);
   c.valid = wide_row(temp, c.k, c.V) && c.src >= 0 && c.src < P.n_rows_total && c.h0 >= 0 && h1 >= c.h0 &&
             h1 - c.h0 <= MAX_HIST;
   c.H = h1 - c.h0;

@@ -19,6 +19,12 @@ Additions, all keyword-only and optional:
   sampler.py:26) and from the global CUDA generator otherwise.
 * ``logits`` may be float32 or bfloat16 (bf16 is read directly; no
   ``.float()`` copy as at engine.py:236).
+* ``device_histories`` / ``history_requests``: histories kept on the device
+  (``DeviceHistories``) instead of the per-step ``history_token_ids`` lists.
+  The engine rebuilds prompt + output ids for every request and step
+  (engine.py:242-246) and the reference copies them to the device each call
+  (sampler.py:34); here each request's ids are copied once when it starts and
+  every sampled token is appended on the device by the same call.
 
 Differences that the engine cannot observe: the caller's logits are not
 modified in place (the reference's penalty writes into them, sampler.py:38,
@@ -45,37 +51,32 @@ def effective_temperature(t: float) -> float:
 
 
 class PackedRows:
-    """Per-row parameters and CSR histories packed for one ``ns_sample`` call."""
+    """Per-row parameters and CSR histories (or device history slots) packed for one call."""
 
-    def __init__(self, params: Sequence[SamplingParams], histories: Sequence, vocab: int):
+    def __init__(self, params: Sequence[SamplingParams], histories: Sequence, vocab: int,
+                 slots: Optional[np.ndarray] = None, slot_max_hist: int = 0):
         B = len(params)
-        temp = np.empty(B, dtype=np.float32)
-        topk = np.empty(B, dtype=np.int32)
-        topp = np.empty(B, dtype=np.float32)
-        pen = np.empty(B, dtype=np.float32)
+        # greedy rows are encoded as temperature 0 (sampler.py:47-50); others carry the
+        # effective float32 temperature, max(t, 1e-6) if t > 0 else 1 (sampler.py:41-46)
+        t64 = np.asarray([float(p.temperature) for p in params], dtype=np.float64).reshape(B)
+        temp = np.where(t64 == 0.0, 0.0, np.where(t64 > 0.0, np.maximum(t64, 1e-6), 1.0)).astype(np.float32)
+        topk = np.asarray([min(max(int(p.top_k), -1), _I32_MAX) for p in params], dtype=np.int32).reshape(B)
+        topp = np.asarray([float(p.top_p) for p in params], dtype=np.float64).reshape(B).astype(np.float32)
+        rp64 = np.asarray([float(p.repetition_penalty) for p in params], dtype=np.float64).reshape(B)
+        pen = rp64.astype(np.float32)
         lens = np.zeros(B, dtype=np.int64)
-        hist_rows = []
-        for i, p in enumerate(params):
-            t = float(p.temperature)
-            # greedy rows are encoded as temperature 0 (sampler.py:47-50); others carry the
-            # effective float32 temperature (sampler.py:41-46)
-            temp[i] = 0.0 if t == 0.0 else np.float32(effective_temperature(t))
-            k = int(p.top_k)
-            topk[i] = min(max(k, -1), _I32_MAX)
-            topp[i] = np.float32(float(p.top_p))
-            rp = float(p.repetition_penalty)
-            pen[i] = np.float32(rp)
-            h = histories[i] if i < len(histories) else ()
-            # only penalised rows index their history (sampler.py:33)
-            if rp != 1.0 and len(h) > 0:
-                a = np.asarray(h, dtype=np.int64)
-                if a.size and (a.min() < 0 or a.max() >= vocab):
-                    bad = int(a[(a < 0) | (a >= vocab)][0])
-                    raise IndexError(f"history token id {bad} out of range for vocab {vocab} (row {i})")
-                hist_rows.append(a.astype(np.int32))
-                lens[i] = a.size
-            else:
-                hist_rows.append(None)
+        hist_rows = [None] * B
+        if histories is not None:
+            for i in range(min(B, len(histories))):
+                h = histories[i]
+                # only penalised rows index their history (sampler.py:33)
+                if rp64[i] != 1.0 and len(h) > 0:
+                    a = np.asarray(h, dtype=np.int64)
+                    if a.size and (a.min() < 0 or a.max() >= vocab):
+                        bad = int(a[(a < 0) | (a >= vocab)][0])
+                        raise IndexError(f"history token id {bad} out of range for vocab {vocab} (row {i})")
+                    hist_rows[i] = a.astype(np.int32)
+                    lens[i] = a.size
         self.batch = B
         self.row_kinds = _lib.row_kinds(temp, topk, vocab)
         self.temperature = temp
@@ -83,9 +84,13 @@ class PackedRows:
         self.top_p = topp
         self.penalty = pen
         self.max_hist = int(lens.max()) if B else 0
+        self.slots = None
+        if slots is not None:
+            self.slots = np.ascontiguousarray(slots, dtype=np.int32)
+            self.max_hist = int(slot_max_hist)
         if self.max_hist > _lib.NS_MAX_HISTORY:
             raise ValueError(f"history of {self.max_hist} tokens exceeds the supported {_lib.NS_MAX_HISTORY}")
-        if self.max_hist > 0:
+        if self.max_hist > 0 and self.slots is None:
             offs = np.zeros(B + 1, dtype=np.int32)
             np.cumsum(lens, out=offs[1:])
             ids = np.concatenate([r for r in hist_rows if r is not None]) if any(
@@ -101,12 +106,16 @@ class PackedRows:
         B = self.batch
         nh = 0 if self.hist_ids is None else int(self.hist_ids.size)
         no = 0 if self.hist_offsets is None else B + 1
+        if self.slots is not None:   # device histories: the slot of each row in place of the CSR
+            no, nh = B, 0
         buf = np.empty(4 * B + no + nh, dtype=np.int32)
         buf[0:B] = self.temperature.view(np.int32)
         buf[B:2 * B] = self.top_k
         buf[2 * B:3 * B] = self.top_p.view(np.int32)
         buf[3 * B:4 * B] = self.penalty.view(np.int32)
-        if no:
+        if self.slots is not None:
+            buf[4 * B:5 * B] = self.slots
+        elif no:
             buf[4 * B:4 * B + no] = self.hist_offsets
             buf[4 * B + no:] = self.hist_ids
         host = torch.from_numpy(buf)
@@ -118,10 +127,64 @@ class PackedRows:
             "top_k": dev[B:2 * B],
             "top_p": dev[2 * B:3 * B].view(torch.float32),
             "rep_penalty": dev[3 * B:4 * B].view(torch.float32),
-            "hist_offsets": dev[4 * B:4 * B + no] if no else None,
-            "hist_ids": dev[4 * B + no:] if no else None,
+            "hist_offsets": dev[4 * B:4 * B + no] if no and self.slots is None else None,
+            "hist_ids": dev[4 * B + no:] if no and self.slots is None else None,
+            "hist_slot": dev[4 * B:5 * B] if self.slots is not None else None,
         }
         return out
+
+
+class DeviceHistories:
+    """Per-request token histories kept on the device across ``sample`` calls.
+
+    ``open(request_id, prompt_ids)`` gives a request a slot and copies its prompt
+    once; ``Sampler.sample(..., device_histories=self, history_requests=ids)``
+    reads each row's history from its request's slot and appends the sampled
+    token to it on the device (the lists engine.py:242-246 rebuilds every step and
+    sampler.py:34 copies to the device).  ``close(request_id)`` frees the slot.
+    ``capacity`` bounds prompt + generated tokens per request (at most the
+    sampler's 8192-token history limit, the reference's max_model_len).
+    """
+
+    def __init__(self, device, max_requests: int, capacity: int = _lib.NS_MAX_HISTORY):
+        self.device = torch.device(device)
+        self.state = _lib.HistoryState(self.device, max_requests, capacity)
+        self.capacity = int(capacity)
+        self._slot = {}
+        self._free = list(range(int(max_requests) - 1, -1, -1))
+        self._len = np.zeros(int(max_requests), dtype=np.int64)
+
+    def open(self, request_id, prompt_ids: Sequence[int]) -> int:
+        if request_id in self._slot:
+            raise KeyError(f"request {request_id!r} already has a history slot")
+        if not self._free:
+            raise RuntimeError("no free history slot (raise max_requests)")
+        ids = np.asarray(prompt_ids, dtype=np.int64).reshape(-1)
+        if ids.size > self.capacity:
+            raise ValueError(f"prompt of {ids.size} tokens exceeds the history capacity {self.capacity}")
+        slot = self._free.pop()
+        dev_ids = torch.from_numpy(ids.astype(np.int32)).to(self.device) if ids.size else None
+        self.state.assign(slot, dev_ids)
+        self._slot[request_id] = slot
+        self._len[slot] = ids.size
+        return slot
+
+    def close(self, request_id) -> None:
+        slot = self._slot.pop(request_id)
+        self._len[slot] = 0
+        self._free.append(slot)
+
+    def length(self, request_id) -> int:
+        return int(self._len[self._slot[request_id]])
+
+    def slots(self, request_ids: Sequence) -> np.ndarray:
+        return np.fromiter((self._slot[r] for r in request_ids), dtype=np.int32, count=len(request_ids))
+
+    def _appended(self, slots: np.ndarray) -> None:
+        full = self._len[slots] >= self.capacity
+        if full.any():
+            raise RuntimeError(f"history slot {int(slots[full][0])} is full ({self.capacity} tokens)")
+        self._len[slots] += 1
 
 
 class Sampler:
@@ -141,11 +204,16 @@ class Sampler:
         sample_indices: Optional[torch.Tensor] = None,
         uniforms: Optional[torch.Tensor] = None,
         return_probs: bool = False,
+        device_histories: Optional[DeviceHistories] = None,
+        history_requests: Optional[Sequence] = None,
     ):
         """Sample one token per row; returns an int64 tensor on ``logits.device``.
 
         With ``return_probs=True`` returns ``(ids, probs)`` where ``probs`` holds the
-        final (B, V) probabilities of every non-greedy row (sampler.py:76-80).
+        final (B, V) probabilities of every non-greedy row (sampler.py:76-80).  With
+        ``device_histories`` the histories are those of ``history_requests`` (one request
+        per row, each at most once) and ``history_token_ids`` is ignored; the sampled
+        tokens are appended to them.
         """
         if logits.device.type != "cuda":
             raise RuntimeError("the MI355X sampler needs logits on a GPU device")
@@ -158,7 +226,18 @@ class Sampler:
         if sample_indices is None and B != N:
             raise ValueError(f"{B} sampling params for {N} logits rows")
         dev = logits.device
-        packed = PackedRows(sampling_params_list, history_token_ids, V)
+        slots = None
+        if device_histories is not None:
+            if history_requests is None or len(history_requests) != B:
+                raise ValueError("history_requests must name one request per sampled row")
+            slots = device_histories.slots(history_requests)
+            if len(set(slots.tolist())) != B:
+                raise ValueError("history_requests must name each request at most once")
+            device_histories._appended(slots)   # checked before any launch; counted for the next call
+            max_hist = int((device_histories._len[slots] - 1).max()) if B else 0
+            packed = PackedRows(sampling_params_list, None, V, slots=slots, slot_max_hist=max_hist)
+        else:
+            packed = PackedRows(sampling_params_list, history_token_ids, V)
         d = packed.to_device(dev)
         if sample_indices is not None:
             sample_indices = sample_indices.to(device=dev, dtype=torch.int64)
@@ -173,9 +252,13 @@ class Sampler:
         out = torch.empty(B, dtype=torch.int64, device=dev)
         probs = torch.empty((B, V), dtype=torch.float32, device=dev) if return_probs else None
         if B > 0:
+            hs = device_histories.state if device_histories is not None else None
             _lib.sample_raw(logits, d["temperature"], d["top_k"], d["top_p"], d["rep_penalty"], uniforms, out,
                             sample_idx=sample_indices, hist_offsets=d["hist_offsets"], hist_ids=d["hist_ids"],
-                            max_hist=packed.max_hist, out_probs=probs, row_kinds=packed.row_kinds)
+                            max_hist=packed.max_hist, out_probs=probs, row_kinds=packed.row_kinds,
+                            hist_state=hs, hist_slot=d["hist_slot"])
+            if hs is not None:
+                hs.append(d["hist_slot"], out)
         return (out, probs) if return_probs else out
 
     @staticmethod

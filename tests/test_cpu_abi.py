@@ -41,7 +41,7 @@ def test_struct_layout_matches_header():
     body = txt[txt.index("typedef struct ns_sample_args"):txt.index("} ns_sample_args;")]
     names = re.findall(r"^\s*[\w\s\*]+?\b(\w+);", body, flags=re.M)
     assert names == [f[0] for f in L.NsSampleArgs._fields_]
-    assert ctypes.sizeof(L.NsSampleArgs) == 160
+    assert ctypes.sizeof(L.NsSampleArgs) == 184
 
 
 def test_lds_bytes_and_argument_errors():
@@ -60,6 +60,43 @@ def test_lds_bytes_and_argument_errors():
     assert "NULL" in L.last_error()
     a.n_sample = 0
     assert lib.ns_sample(ctypes.byref(a), None) == 0
+
+
+def test_history_state_layout_and_argument_errors():
+    if not os.path.exists(L.LIB_PATH):
+        pytest.skip("library not built")
+    # int32 lengths padded to 256 bytes, then n_slots * capacity int32 ids
+    assert L.hist_state_bytes(3, 100) == 256 + 3 * 100 * 4
+    assert L.hist_state_bytes(64, 8192) == 256 + 64 * 8192 * 4
+    with pytest.raises(L.SamplerLibraryError, match="hist_capacity"):
+        L.hist_state_bytes(4, 9000)
+    with pytest.raises(L.SamplerLibraryError, match="hist_n_slots"):
+        L.hist_state_bytes(0, 10)
+    lib = L.load()
+    assert lib.ns_hist_assign(None, 4, 10, 0, None, 0, None) == 1 and "state" in L.last_error()
+    assert lib.ns_hist_assign(256, 4, 10, 4, None, 0, None) == 1 and "slot" in L.last_error()
+    assert lib.ns_hist_assign(256, 4, 10, 0, None, 11, None) == 1 and "capacity" in L.last_error()
+    assert lib.ns_hist_append(256, 4, 10, None, None, 2, None, None) == 1 and "NULL" in L.last_error()
+    assert lib.ns_hist_append(256, 4, 10, None, None, 0, None, None) == 0
+    # the device histories exclude the CSR ones; a slot table is required (checked before any launch)
+    a = L.NsSampleArgs()
+    a.n_sample, a.dtype, a.vocab, a.row_stride, a.n_rows_total = 1, L.NS_DTYPE_F32, 64, 64, 1
+    a.logits = a.temperature = a.top_k = a.top_p = a.rep_penalty = a.uniforms = a.out_ids = 256
+    a.hist_state, a.hist_n_slots, a.hist_capacity = 256, 4, 16
+    a.hist_offsets, a.hist_ids = 512, 768
+    assert lib.ns_sample(ctypes.byref(a), None) == 1 and "excludes" in L.last_error()
+    a.hist_offsets = a.hist_ids = None
+    assert lib.ns_sample(ctypes.byref(a), None) == 1 and "hist_slot" in L.last_error()
+
+
+def test_packing_with_history_slots():
+    P = C.SamplingParams
+    params = [P(repetition_penalty=1.2), P(), P(temperature=0.0)]
+    pk = S.PackedRows(params, None, vocab=10, slots=np.array([2, -1, 0]), slot_max_hist=7)
+    assert pk.hist_offsets is None and pk.hist_ids is None and pk.max_hist == 7
+    d = pk.to_device("cpu")
+    assert d["hist_slot"].tolist() == [2, -1, 0] and d["hist_offsets"] is None and d["hist_ids"] is None
+    assert d["top_k"].tolist() == [-1, -1, -1]
 
 
 def test_packing_follows_reference_rules():

@@ -1,0 +1,125 @@
+"""GPU: device-resident histories (ns_hist_state_bytes / ns_hist_assign /
+ns_hist_append, the ``DeviceHistories`` class).
+
+Holding the same ids as the CSR histories, they must give bit-identical ids,
+diagnostics and probabilities in every mode (every kernel reads a row's history
+through the same start/length pair).  Over a multi-step decode loop, appending
+each sampled token on the device must track the host-side lists the reference's
+engine rebuilds every step (engine.py:242-246, scheduler.py:281-284).
+"""
+import numpy as np
+import pytest
+import torch
+
+from conftest import pkg
+from parity import PATHS, params_of, run_gpu
+
+W = pkg("workloads")
+L = pkg("_lib")
+S = pkg("sampler")
+
+pytestmark = pytest.mark.gpu
+
+
+def open_all(w, device, extra_slots=3):
+    dh = S.DeviceHistories(device, w.batch + extra_slots, capacity=L.NS_MAX_HISTORY)
+    for r in range(w.batch):
+        dh.open(r, w.histories[r])
+    return dh
+
+
+def run_slots(w, device, dh, workspace, mode):
+    """run_gpu's call with the histories read from ``dh`` (request r on row r), no append."""
+    slots = dh.slots(list(range(w.batch)))
+    max_hist = int(max(dh.length(r) for r in range(w.batch)))
+    packed = S.PackedRows(params_of(w), None, w.vocab, slots=slots, slot_max_hist=max_hist)
+    d = packed.to_device(device)
+    logits = w.device_logits(device)
+    B, V = w.batch, w.vocab
+    u = torch.from_numpy(np.asarray(w.uniforms, dtype=np.float32)).to(device)
+    sidx = torch.from_numpy(w.sample_indices).to(device) if w.sample_indices is not None else None
+    out = torch.full((B,), -7, dtype=torch.int64, device=device)
+    probs = torch.zeros((B, V), dtype=torch.float32, device=device)
+    info = torch.zeros((B, L.NS_INFO_WORDS), dtype=torch.int32, device=device)
+    L.sample_raw(logits, d["temperature"], d["top_k"], d["top_p"], d["rep_penalty"], u, out,
+                 sample_idx=sidx, max_hist=packed.max_hist, out_probs=probs, out_info=info, workspace=workspace,
+                 mode=mode, hist_state=dh.state, hist_slot=d["hist_slot"])
+    torch.cuda.synchronize()
+    return {"ids": out.cpu().numpy(), "probs": probs.cpu(), "info": info.cpu().numpy()}
+
+
+def read_state(dh, request_ids):
+    """The id lists the device holds for these requests."""
+    words = dh.state.buffer.view(torch.int32).cpu().numpy()
+    lens = words[:dh.state.n_slots]
+    base = (dh.state.n_slots * 4 + 255) // 256 * 64
+    out = []
+    for r in request_ids:
+        s = dh.slots([r])[0]
+        out.append(words[base + s * dh.state.capacity: base + s * dh.state.capacity + lens[s]].tolist())
+    return out
+
+
+@pytest.mark.parametrize("path", list(PATHS))
+@pytest.mark.parametrize("cfg", [1, 2, 4])
+def test_device_histories_match_csr(device, cfg, path):
+    w = W.make_workload(cfg, batch=64 if cfg == 2 else None)
+    print(f"[history] config {cfg} B={w.batch} path={path}", flush=True)
+    ws, mode = PATHS[path]
+    ref = run_gpu(w, device, workspace=ws, mode=mode)
+    dh = open_all(w, device)
+    got = run_slots(w, device, dh, ws, mode)
+    assert np.array_equal(got["ids"], ref["ids"])
+    bad = np.nonzero((got["info"] != ref["info"]).any(axis=1))[0]
+    assert bad.size == 0, [(int(i), ref["info"][i].tolist(), got["info"][i].tolist()) for i in bad[:4]]
+    assert torch.equal(got["probs"], ref["probs"])
+
+
+def test_decode_loop_appends_on_device(device):
+    """Four decode steps of the mixed batch: ids equal to the host-history run at every
+    step, and the device lists equal the host lists afterwards."""
+    w = W.make_workload(1)
+    B = w.batch
+    params = params_of(w)
+    base = w.device_logits(device)
+    sampler = S.Sampler(device)
+    host = [list(map(int, h)) for h in w.histories]
+    dh = S.DeviceHistories(device, B + 5, capacity=1024)
+    order = list(range(B))[::-1]                     # slots taken in a different order than rows
+    for r in order:
+        dh.open(r, host[r])
+    rng = np.random.default_rng(77)
+    for step in range(4):
+        print(f"[history] decode step {step}", flush=True)
+        logits = torch.roll(base, shifts=977 * (step + 1), dims=1).contiguous()
+        u = torch.from_numpy(rng.random(B, dtype=np.float32)).to(device)
+        ids_host = sampler.sample(logits, params, host, uniforms=u)
+        ids_dev = sampler.sample(logits, params, None, uniforms=u, device_histories=dh,
+                                 history_requests=list(range(B)))
+        a, b = ids_host.cpu().numpy(), ids_dev.cpu().numpy()
+        assert np.array_equal(a, b), f"step {step}: rows {np.nonzero(a != b)[0][:8]}"
+        for r in range(B):
+            host[r].append(int(a[r]))
+    torch.cuda.synchronize()
+    assert read_state(dh, list(range(B))) == host
+    assert all(dh.length(r) == len(host[r]) for r in range(B))
+    assert int(dh.state.overflow.item()) == 0
+    # a freed slot is reused with the new request's prompt only
+    dh.close(3)
+    dh.open("new", [5, 6, 7])
+    torch.cuda.synchronize()
+    assert read_state(dh, ["new"]) == [[5, 6, 7]]
+
+
+def test_full_slot_is_refused(device):
+    dh = S.DeviceHistories(device, 2, capacity=4)
+    dh.open("a", [1, 2, 3])
+    slots = torch.tensor([dh.slots(["a"])[0]], dtype=torch.int32, device=device)
+    dh.state.append(slots, torch.tensor([9], dtype=torch.int64, device=device))
+    dh.state.append(slots, torch.tensor([8], dtype=torch.int64, device=device))   # full: not appended
+    torch.cuda.synchronize()
+    assert int(dh.state.overflow.item()) == 1
+    words = dh.state.buffer.view(torch.int32).cpu().numpy()
+    s = int(slots[0])
+    assert words[s] == 4
+    assert words[64 + s * 4: 64 + s * 4 + 4].tolist() == [1, 2, 3, 9]
