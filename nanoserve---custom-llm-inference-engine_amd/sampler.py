@@ -25,6 +25,10 @@ Additions, all keyword-only and optional:
   (engine.py:242-246) and the reference copies them to the device each call
   (sampler.py:34); here each request's ids are copied once when it starts and
   every sampled token is appended on the device by the same call.
+* ``async_ids``: return a ``SampledIds`` handle instead of the tensor.  Its ids
+  are copied into pinned host memory behind an event on the same stream, so
+  ``.tolist()`` (engine.py:250) waits only when the engine reads them and the
+  next scheduler step can run meanwhile.
 
 Differences that the engine cannot observe: the caller's logits are not
 modified in place (the reference's penalty writes into them, sampler.py:38,
@@ -134,6 +138,29 @@ class PackedRows:
         return out
 
 
+class SampledIds:
+    """Sampled ids on their way to the host: ``.tolist()`` waits for the copy.
+
+    ``tensor`` is the (B,) int64 device result (for further GPU work); ``ready()``
+    tells without waiting whether the host copy has landed.
+    """
+
+    def __init__(self, tensor: torch.Tensor, host: torch.Tensor, event):
+        self.tensor = tensor
+        self._host = host
+        self._event = event
+
+    def ready(self) -> bool:
+        return bool(self._event.query())
+
+    def tolist(self) -> List[int]:
+        self._event.synchronize()
+        return self._host.tolist()
+
+    def __len__(self) -> int:
+        return int(self.tensor.numel())
+
+
 class DeviceHistories:
     """Per-request token histories kept on the device across ``sample`` calls.
 
@@ -206,6 +233,7 @@ class Sampler:
         return_probs: bool = False,
         device_histories: Optional[DeviceHistories] = None,
         history_requests: Optional[Sequence] = None,
+        async_ids: bool = False,
     ):
         """Sample one token per row; returns an int64 tensor on ``logits.device``.
 
@@ -213,7 +241,9 @@ class Sampler:
         final (B, V) probabilities of every non-greedy row (sampler.py:76-80).  With
         ``device_histories`` the histories are those of ``history_requests`` (one request
         per row, each at most once) and ``history_token_ids`` is ignored; the sampled
-        tokens are appended to them.
+        tokens are appended to them.  With ``async_ids=True`` the result is a
+        ``SampledIds`` handle (its ``.tolist()`` waits for the host copy), and
+        ``(SampledIds, probs)`` with ``return_probs``.
         """
         if logits.device.type != "cuda":
             raise RuntimeError("the MI355X sampler needs logits on a GPU device")
@@ -259,7 +289,18 @@ class Sampler:
                             hist_state=hs, hist_slot=d["hist_slot"])
             if hs is not None:
                 hs.append(d["hist_slot"], out)
-        return (out, probs) if return_probs else out
+        res = self._readback(out) if async_ids else out
+        return (res, probs) if return_probs else res
+
+    def _readback(self, out: torch.Tensor) -> SampledIds:
+        """Copy ``out`` into a pinned host buffer behind an event on the current stream."""
+        # one pinned buffer per call (torch's caching host allocator recycles them once
+        # their handle is gone), so any number of calls may be in flight
+        host = torch.empty(int(out.numel()), dtype=torch.int64, pin_memory=True)
+        host.copy_(out, non_blocking=True)
+        ev = torch.cuda.Event()
+        ev.record(torch.cuda.current_stream(out.device))
+        return SampledIds(out, host, ev)
 
     @staticmethod
     def _draw_uniforms(B: int, dev, generators) -> torch.Tensor:

@@ -123,3 +123,23 @@ def test_full_slot_is_refused(device):
     s = int(slots[0])
     assert words[s] == 4
     assert words[64 + s * 4: 64 + s * 4 + 4].tolist() == [1, 2, 3, 9]
+
+
+def test_async_ids_match_and_overlap(device):
+    """async_ids: the same ids as the synchronous call, readable later, several in flight."""
+    w = W.make_workload(2, batch=64)
+    params = params_of(w)
+    sampler = S.Sampler(device)
+    hist = [list(map(int, h)) for h in w.histories]
+    u = torch.from_numpy(np.asarray(w.uniforms, dtype=np.float32)).to(device)
+    base = w.device_logits(device)
+    sync_ids, handles = [], []
+    for step in range(6):
+        logits = torch.roll(base, shifts=131 * step, dims=1).contiguous()
+        sync_ids.append(sampler.sample(logits, params, hist, uniforms=u).cpu().tolist())
+        handles.append(sampler.sample(logits, params, hist, uniforms=u, async_ids=True))
+    for step, h in enumerate(handles):
+        assert isinstance(h, S.SampledIds) and len(h) == w.batch
+        assert h.tolist() == sync_ids[step]
+        assert h.ready()
+        assert h.tensor.cpu().tolist() == sync_ids[step]
