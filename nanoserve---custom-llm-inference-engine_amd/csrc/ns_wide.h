@@ -47,7 +47,7 @@ struct WideRow {
   int32_t nfin;            // finite scaled logits
   int32_t step;            // WSTEP_*
   int32_t blo, bend;       // planned bins [blo, bend]
-  int32_t n_above;         // finite elements in bins < blo
+  int32_t n_above;         // finite elements in bins < blo (from the count histogram, top-k rows)
   int32_t kon;             // top-k applies with a finite threshold (0 < k <= nfin, k < V)
   uint64_t mass_above;     // fixed-point mass of bins < blo
   uint64_t mass_tot;       // fixed-point mass of the row
@@ -68,7 +68,8 @@ struct WideSeg {
   int32_t nfin;            // pass 1: finite scaled logits
   int32_t flags;           // pass 1: flags
   int32_t ncand;           // pass 3: planned-bin elements (may exceed SEG_CAP: overflow)
-  int32_t pad[2];
+  int32_t nabove;          // pass 3: finite elements in bins < blo
+  int32_t pad;
 };
 static_assert(sizeof(WideSeg) == sizeof(SegStat), "WideSeg uses the segment statistics slots");
 
@@ -138,9 +139,16 @@ __device__ __forceinline__ int wbin(float M, float y) {
   const float d = (M - y) * WSCALE;
   return d < (float)WBINS ? (int)d : WBINS;
 }
-// exp(y - M) in units of 2^-44 (y <= M).
+// exp(y - M) in units of 2^-44 (y <= M), truncated: (uint64_t)(e * 2^44) for the float32
+// e = exp(y - M) in [0, 1], taken from e's exponent and mantissa bits (the product with
+// 2^44 is exact, so the integer is the same as through float64).
 __device__ __forceinline__ uint64_t wfx(float M, float y) {
-  return (uint64_t)((double)ns_expf(y - M) * WFX);
+  const uint32_t b = __float_as_uint(ns_expf(y - M));
+  const int E = (int)(b >> 23);                        // biased exponent (e >= 0)
+  const uint64_t m = (uint64_t)((b & 0x7fffffu) | 0x800000u);
+  if (E >= 106) return m << (E - 106);                 // e * 2^44 = m * 2^(E - 127 - 23 + 44)
+  const int r = 106 - E;
+  return (E > 0 && r < 64) ? (m >> r) : 0ull;          // zero and subnormal e: below 2^-44
 }
 
 __device__ __forceinline__ void dc_store_wseg(WideSeg* p, const WideSeg& s) {
@@ -698,12 +706,22 @@ __global__ __launch_bounds__(SNT) void wide_hist_kernel(const WideParams P) {
   for (int b = tid; b < WBINS; b += SNT) { sm.u.h.cnt[b] = 0u; sm.u.h.mass[b] = 0ull; }
   wide_bitmap<T>(P, c, c0 * EPC, &sm);   // its barriers also order the clearing above
   unsigned long long own = 0ull;
-  if (c.topp < 1.0f) {
+  if (c.topp < 1.0f && c.k > 0 && (int64_t)c.k < c.V) {
     wide_each<T>(c, c0, sm.bm, [&](float y, int64_t) {
       const int b = wbin(M, y);
       if (b < WBINS) {
         const uint64_t fx = wfx(M, y);
         atomicAdd(&sm.u.h.cnt[b], 1u);
+        atomicAdd(&sm.u.h.mass[b], (unsigned long long)fx);
+        own += fx;
+      }
+    });
+  } else if (c.topp < 1.0f) {
+    // top-p alone: masses only (the counts above the plan come from the compaction pass)
+    wide_each<T>(c, c0, sm.bm, [&](float y, int64_t) {
+      const int b = wbin(M, y);
+      if (b < WBINS) {
+        const uint64_t fx = wfx(M, y);
         atomicAdd(&sm.u.h.mass[b], (unsigned long long)fx);
         own += fx;
       }
@@ -719,10 +737,9 @@ __global__ __launch_bounds__(SNT) void wide_hist_kernel(const WideParams P) {
   __syncthreads();
   for (int b = tid; b < WBINS; b += SNT) {
     const uint32_t n = sm.u.h.cnt[b];
-    if (n != 0u) {
-      atomicAdd(P.hcnt + (int64_t)row * WBINS + b, n);
-      atomicAdd((unsigned long long*)(P.hmass + (int64_t)row * WBINS + b), sm.u.h.mass[b]);
-    }
+    const unsigned long long fx = sm.u.h.mass[b];
+    if (n != 0u) atomicAdd(P.hcnt + (int64_t)row * WBINS + b, n);
+    if (fx != 0ull) atomicAdd((unsigned long long*)(P.hmass + (int64_t)row * WBINS + b), fx);
   }
   const unsigned long long smass = wsum_u64(own, &sm);
   if (tid == 0) {
@@ -876,12 +893,13 @@ __global__ __launch_bounds__(SNT) void wide_cut_kernel(const WideParams P) {
   __syncthreads();
   uint64_t* cbase = P.cand + ((int64_t)row * P.S + seg) * SEG_CAP;
   unsigned long long above = 0ull;
+  int32_t nab = 0;
   wide_chunks<T>(c, c0, sm.bm, [&](const float (&y)[EPC], int64_t ch) {
     bool any = false;
 #pragma unroll
     for (int e = 0; e < EPC; ++e) {
       const int b = wbin(M, y[e]);
-      if (b < blo) above += wfx(M, y[e]);
+      if (b < blo) { above += wfx(M, y[e]); ++nab; }
       any |= b >= blo && b <= bend;
     }
     // the planned elements of the chunk, appended wave-aggregated (one test per chunk)
@@ -904,10 +922,12 @@ __global__ __launch_bounds__(SNT) void wide_cut_kernel(const WideParams P) {
     }
   });
   const unsigned long long sabove = wsum_u64(above, &sm);
+  const int32_t snab = wsum_i(nab, &sm);
   if (tid == 0) {
     WideSeg s{};
     s.mass = sabove;
     s.ncand = sm.cnt;
+    s.nabove = snab;
     dc_store_wseg(P.segs + (int64_t)row * P.S + seg, s);
   }
 }
@@ -1047,7 +1067,6 @@ __global__ __launch_bounds__(NT) void wide_final_kernel(const WideParams P) {
     }
     return;
   }
-  const int32_t n_above = R->n_above;
   const bool kon = R->kon != 0;
   const bool pon = c.topp < 1.0f;
   const bool kon0 = c.k > 0 && (int64_t)c.k < c.V;
@@ -1055,21 +1074,27 @@ __global__ __launch_bounds__(NT) void wide_final_kernel(const WideParams P) {
     const WideSeg s = dc_load_wseg(P.segs + (int64_t)row * P.S + tid);
     sm.segfx[tid] = s.mass;
     sm.off[tid] = s.ncand;
+    sm.ired[tid] = s.nabove;
   }
   if (tid == 0) sm.ib[0] = 0;
   __syncthreads();
   if (tid == 0) {
-    int o = 0, over = 0;
+    int o = 0, over = 0, nab = 0;
     for (int i = 0; i < P.S; ++i) {
       const int n = sm.off[i];
       over |= n > SEG_CAP;
       sm.off[i] = o;
       o += n < SEG_CAP ? n : SEG_CAP;
+      nab += sm.ired[i];
     }
     sm.off[P.S] = o;
     sm.ib[0] = over || o > WCAND;
+    sm.ib[3] = nab;
   }
   __syncthreads();
+  // finite elements above the planned bins: the compaction pass's counts (top-p rows do not
+  // histogram counts)
+  const int32_t n_above = sm.ib[3];
   // the mass above the planned bins: the segments' sums from the compaction pass (the same
   // fixed-point terms the histogram holds when it holds masses)
   uint64_t mass_above = 0ull;
