@@ -1195,7 +1195,7 @@ const int32_t* hist_state_ids(const void* state, int32_t n_slots) {
 }
 
 struct WsLayout {
-  int64_t counters, status, stats, cand, wrow, hcnt, hmass, total;
+  int64_t counters, status, stats, cand, wrow, hcnt, hmass, subfx, total;
 };
 // Workspace layout.  The per-row arrival counters are the only state that outlives a
 // call (each call leaves them at zero): they sit at fixed positions at the start, sized
@@ -1215,7 +1215,8 @@ WsLayout ws_layout(int32_t n_sample, int64_t vocab, int32_t dtype) {
   L.wrow = L.cand + align256(rows * S * ns::SEG_CAP * 8);
   L.hcnt = L.wrow + align256(wrows * (int64_t)sizeof(ns::WideRow));
   L.hmass = L.hcnt + align256(wrows * ns::WBINS * 4);
-  L.total = L.hmass + align256(wrows * ns::WBINS * 8);
+  L.subfx = L.hmass + align256(wrows * ns::WBINS * 8);
+  L.total = L.subfx + align256(wrows * S * ns::WSUB * 8);
   return L;
 }
 }  // namespace
@@ -1492,6 +1493,7 @@ int ns_sample(const ns_sample_args* a, hipStream_t stream) {
     w.segs = reinterpret_cast<ns::WideSeg*>(ws + L.stats);
     w.hcnt = reinterpret_cast<uint32_t*>(ws + L.hcnt);
     w.hmass = reinterpret_cast<uint64_t*>(ws + L.hmass);
+    w.subfx = reinterpret_cast<uint64_t*>(ws + L.subfx);
     w.cand = reinterpret_cast<uint64_t*>(ws + L.cand);
     p.status = w.status;
     const dim3 g((unsigned)nblk), bs(ns::SNT);

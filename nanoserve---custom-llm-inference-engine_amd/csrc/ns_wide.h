@@ -36,7 +36,7 @@ constexpr int WIDE_MAX_ROWS = 4096;           // rows a call sends through this 
 constexpr double WFX = 17592186044416.0;      // 2^44: fixed-point scale of exp(y - M) <= 1
 constexpr double WFX_INV = 1.0 / 17592186044416.0;
 constexpr int32_t PATH_WIDE = 7;              // out_info path code
-constexpr int WLOC = 4;                       // chunks per thread and step of the locate walk (contiguous)
+constexpr int WSUB = 4;                       // quarter segments: the unit of the draw's final walk
 
 enum : int32_t { WSTEP_NONE = 0, WSTEP_HIST = 1, WSTEP_CUT = 2, WSTEP_DRAWN = 3, WSTEP_UNIFORM = 4, WSTEP_FULL = 5 };
 
@@ -102,6 +102,7 @@ struct WideParams {
   uint32_t* hcnt;          // [rows * WBINS]
   uint64_t* hmass;         // [rows * WBINS]
   uint64_t* cand;          // [rows * S * SEG_CAP]  (float bits << 32) | token id
+  uint64_t* subfx;         // [rows * S * WSUB] pass 3: mass in bins < blo per quarter segment
 };
 
 template <int NKEYS>
@@ -115,6 +116,7 @@ struct WideSmemT {
     uint64_t keys[NKEYS];                    // the finaliser's ordered elements
   } u;
   unsigned long long segfx[MAX_SEGS];
+  unsigned long long subq[MAX_SEGS * WSUB];  // the finaliser's kept mass per quarter segment
   int32_t off[MAX_SEGS + 1];
   unsigned long long ured[NWAVE];
   double dred[NWAVE];
@@ -376,8 +378,11 @@ __device__ __forceinline__ void chunk_y(const WRowCtx& c, const uint4& w, uint32
 // the row: y the scaled, penalized values of its EPC tokens (-inf past V).  The chunks
 // stream in steps of WGRP per thread, the next step's loads in flight while one step is
 // processed.
-template <typename T, typename F>
-__device__ __forceinline__ void wide_chunks(const WRowCtx& c, int64_t c0, const uint32_t* bm, F&& f) {
+struct NoHook {
+  __device__ __forceinline__ void operator()(int) const {}
+};
+template <typename T, typename F, typename G = NoHook>
+__device__ __forceinline__ void wide_chunks(const WRowCtx& c, int64_t c0, const uint32_t* bm, F&& f, G&& gend = G{}) {
   constexpr int EPC = T::EPC;
   const int tid = threadIdx.x;
   const uint32_t nbytes = (uint32_t)((c.V / EPC) * 16);
@@ -403,6 +408,7 @@ __device__ __forceinline__ void wide_chunks(const WRowCtx& c, int64_t c0, const 
         f(y, ch);
       }
     }
+    gend(g);   // quarter segment g done (chunks g * WGRP * SNT .. + WGRP * SNT of the segment)
 #pragma unroll
     for (int j = 0; j < WGRP; ++j) cur[j] = nxt[j];
   }
@@ -441,31 +447,31 @@ struct WKeep {
   }
 };
 
-// The draw inside segment s: the first token (ascending id) whose cumulative kept
-// probability, from pstart (the kept probability of the segments before s), exceeds u.
-// Probabilities are float32(exp(y - M) * rz), rz = 1 / zkept in float64.  The segment
-// is walked in steps of NTH * WLOC chunks, WLOC consecutive chunks per thread.  When
-// rounding leaves u past the segment, the last token with a non-zero probability.
-// Every thread must call it.
-template <typename T, int NTH, typename SM>
-__device__ __forceinline__ int64_t wide_locate(const WideParams& P, const WRowCtx& c, int s, double pstart, double rz, float M,
-                               const WKeep& keep, SM* sm, int32_t* fl) {
+// The draw inside chunks [c0, c0 + NCH): the first token (ascending id) whose cumulative
+// kept probability, from pstart (the kept probability of the tokens before c0), exceeds u.
+// Probabilities are float32(exp(y - M) * rz), rz = 1 / zkept in float64.  The range is
+// walked in steps of NTH * WL chunks, WL consecutive chunks per thread.  When rounding
+// leaves u past the range, the last token with a non-zero probability.  Every thread must
+// call it.
+template <typename T, int NTH, int WL, int NCH, typename SM>
+__device__ __forceinline__ int64_t wide_locate(const WideParams& P, const WRowCtx& c, int64_t c0, double pstart,
+                                               double rz, float M, const WKeep& keep, SM* sm, int32_t* fl) {
   constexpr int EPC = T::EPC;
+  static_assert(NCH % (NTH * WL) == 0 && NCH <= SEG_CH, "whole steps inside one segment's bitmap");
   const int tid = threadIdx.x;
-  const int64_t c0 = (int64_t)s * SEG_CH;
   *fl |= wide_bitmap<T, NTH>(P, c, c0 * EPC, sm);
   const uint32_t nbytes = (uint32_t)((c.V / EPC) * 16);
   if (tid == 0) { sm->ib[0] = 0x7fffffff; sm->ib[1] = -1; }
   const double ud = (double)c.u;
   double carry = pstart;
-  for (int step = 0; step < SEG_CH / (NTH * WLOC); ++step) {
-    const int64_t cb = c0 + (int64_t)step * NTH * WLOC + (int64_t)tid * WLOC;   // first chunk of this thread
-    uint4 raw[WLOC];
+  for (int step = 0; step < NCH / (NTH * WL); ++step) {
+    const int64_t cb = c0 + (int64_t)step * NTH * WL + (int64_t)tid * WL;   // first chunk of this thread
+    uint4 raw[WL];
 #pragma unroll
-    for (int j = 0; j < WLOC; ++j) raw[j] = buf_load16_at(c.rowp, nbytes, (uint32_t)((cb + j) * 16), 0u);
-    float p[WLOC * EPC];
+    for (int j = 0; j < WL; ++j) raw[j] = buf_load16_at(c.rowp, nbytes, (uint32_t)((cb + j) * 16), 0u);
+    float p[WL * EPC];
 #pragma unroll
-    for (int j = 0; j < WLOC; ++j) {
+    for (int j = 0; j < WL; ++j) {
       const int64_t ch = cb + j;
       const uint4 w = wide_chunk_fix<T>(c, ch, raw[j]);
       const uint32_t hb = c.pen_on ? T::bits(sm->bm, (int)(ch - c0)) : 0u;
@@ -477,12 +483,12 @@ __device__ __forceinline__ int64_t wide_locate(const WideParams& P, const WRowCt
     }
     double own = 0.0;
 #pragma unroll
-    for (int i = 0; i < WLOC * EPC; ++i) own += (double)p[i];
+    for (int i = 0; i < WL * EPC; ++i) own += (double)p[i];
     double tot;
     double run = carry + wexcl_f64<NTH>(own, &tot, sm);
     int32_t first = 0x7fffffff, lastnz = -1;
 #pragma unroll
-    for (int i = 0; i < WLOC * EPC; ++i) {
+    for (int i = 0; i < WL * EPC; ++i) {
       if (p[i] > 0.0f) {
         run += (double)p[i];
         const int32_t id = (int32_t)(cb * EPC + i);
@@ -892,8 +898,9 @@ __global__ __launch_bounds__(SNT) void wide_cut_kernel(const WideParams P) {
   if (tid == 0) sm.cnt = 0;
   __syncthreads();
   uint64_t* cbase = P.cand + ((int64_t)row * P.S + seg) * SEG_CAP;
-  unsigned long long above = 0ull;
+  unsigned long long above = 0ull, aq0 = 0ull, aq1 = 0ull, aq2 = 0ull, aq3 = 0ull;
   int32_t nab = 0;
+  static_assert(SCPT / WGRP == WSUB, "one wide_chunks step per quarter segment");
   wide_chunks<T>(c, c0, sm.bm, [&](const float (&y)[EPC], int64_t ch) {
     bool any = false;
 #pragma unroll
@@ -920,12 +927,46 @@ __global__ __launch_bounds__(SNT) void wide_cut_kernel(const WideParams P) {
         }
       }
     }
+  }, [&](int g) {
+    // the quarter segment's mass above the plan (g is uniform: selects, no indexing)
+    aq0 = g == 0 ? above : aq0;
+    aq1 = g == 1 ? above : aq1;
+    aq2 = g == 2 ? above : aq2;
+    aq3 = g == 3 ? above : aq3;
+    above = 0ull;
   });
-  const unsigned long long sabove = wsum_u64(above, &sm);
-  const int32_t snab = wsum_i(nab, &sm);
+  // the four quarter sums and the count in one block reduction
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    aq0 += lane_xor(aq0, o);
+    aq1 += lane_xor(aq1, o);
+    aq2 += lane_xor(aq2, o);
+    aq3 += lane_xor(aq3, o);
+    nab += lane_xor(nab, o);
+  }
+  static_assert(WSUB * SNW <= NWAVE, "quarter sums of every wave in the reduction slots");
+  if (lane == 0) {
+    sm.ured[wave_id() * WSUB + 0] = aq0;
+    sm.ured[wave_id() * WSUB + 1] = aq1;
+    sm.ured[wave_id() * WSUB + 2] = aq2;
+    sm.ured[wave_id() * WSUB + 3] = aq3;
+    sm.ired[wave_id()] = nab;
+  }
+  __syncthreads();
   if (tid == 0) {
+    unsigned long long q[WSUB] = {0ull, 0ull, 0ull, 0ull};
+    int32_t snab = 0;
+#pragma unroll
+    for (int w = 0; w < SNW; ++w) {
+#pragma unroll
+      for (int i = 0; i < WSUB; ++i) q[i] += sm.ured[w * WSUB + i];
+      snab += sm.ired[w];
+    }
+    uint64_t* sq = P.subfx + ((int64_t)row * P.S + seg) * WSUB;
+#pragma unroll
+    for (int i = 0; i < WSUB; ++i) dc_store(sq + i, q[i]);
     WideSeg s{};
-    s.mass = sabove;
+    s.mass = q[0] + q[1] + q[2] + q[3];
     s.ncand = sm.cnt;
     s.nabove = snab;
     dc_store_wseg(P.segs + (int64_t)row * P.S + seg, s);
@@ -1053,7 +1094,7 @@ __global__ __launch_bounds__(NT) void wide_final_kernel(const WideParams P) {
     const int s = sm.ib[2];
     const double start = sm.db[0], Z = sm.db[3];
     const WKeep keep{-__builtin_inff(), -__builtin_inff(), 0x7fffffff};
-    const int64_t tok = wide_locate<T, NT>(P, c, s, start, 1.0 / Z, M, keep, &sm, &fl);
+    const int64_t tok = wide_locate<T, NT, 1, SEG_CH>(P, c, (int64_t)s * SEG_CH, start, 1.0 / Z, M, keep, &sm, &fl);
     if (tid == 0) {
       P.out_ids[row] = tok;
       seg_write_info(P.out_info, row, PATH_WIDE, nfin, -__builtin_inff(), nfin, 0, fl, -__builtin_inff(), -1);
@@ -1076,6 +1117,7 @@ __global__ __launch_bounds__(NT) void wide_final_kernel(const WideParams P) {
     sm.off[tid] = s.ncand;
     sm.ired[tid] = s.nabove;
   }
+  if (tid < P.S * WSUB) sm.subq[tid] = dc_load(P.subfx + (int64_t)row * P.S * WSUB + tid);
   if (tid == 0) sm.ib[0] = 0;
   __syncthreads();
   if (tid == 0) {
@@ -1210,7 +1252,7 @@ __global__ __launch_bounds__(NT) void wide_final_kernel(const WideParams P) {
       if (y >= thr) {
         const uint64_t fx = wfx(M, y);
         mkept += fx;
-        atomicAdd(&sm.segfx[desc_key_id(kk[j]) / SEG_EL], (unsigned long long)fx);
+        atomicAdd(&sm.subq[desc_key_id(kk[j]) / (SEG_EL / WSUB)], (unsigned long long)fx);
       }
     }
   }
@@ -1222,10 +1264,11 @@ __global__ __launch_bounds__(NT) void wide_final_kernel(const WideParams P) {
     double run = 0.0, start = 0.0, laststart = 0.0;
     int s = -1, lastnz = -1;
     const double rzkept = 1.0 / zkept;
-    for (int i = 0; i < P.S; ++i) {
-      const double p = (double)sm.segfx[i] * WFX_INV * rzkept;
-      if (sm.segfx[i] != 0ull) { lastnz = i; laststart = run; }
-      if (s < 0 && run + p > ud && sm.segfx[i] != 0ull) { s = i; start = run; }
+    // the quarter segment holding u, from the kept mass per quarter
+    for (int i = 0; i < P.S * WSUB; ++i) {
+      const double p = (double)sm.subq[i] * WFX_INV * rzkept;
+      if (sm.subq[i] != 0ull) { lastnz = i; laststart = run; }
+      if (s < 0 && run + p > ud && sm.subq[i] != 0ull) { s = i; start = run; }
       run += p;
     }
     if (s < 0) { s = lastnz >= 0 ? lastnz : 0; start = laststart; }
@@ -1235,7 +1278,8 @@ __global__ __launch_bounds__(NT) void wide_final_kernel(const WideParams P) {
   __syncthreads();
   const int s = sm.ib[2];
   const double start = sm.db[0];
-  const int64_t tok = wide_locate<T, NT>(P, c, s, start, 1.0 / zkept, M, keep, &sm, &fl);
+  constexpr int QCH = SEG_CH / WSUB;   // chunks per quarter segment: one per thread
+  const int64_t tok = wide_locate<T, NT, 1, QCH>(P, c, (int64_t)s * QCH, start, 1.0 / zkept, M, keep, &sm, &fl);
   if (tid == 0) {
     P.out_ids[row] = tok;
     seg_write_info(P.out_info, row, PATH_WIDE, n_kept, kon0 ? thr : -__builtin_inff(), n_topk, n, fl, vstar, istar);
