@@ -40,6 +40,7 @@ if ROOT not in sys.path:
 PKG = "nanoserve---custom-llm-inference-engine_amd"
 
 HBM_PEAK_GBS = 8000.0
+MFMA_BF16_PEAK_TFLOPS = 2500.0   # dense bf16
 ROTATE = 8
 # rocprofv3 FETCH_SIZE + WRITE_SIZE summary of this workload (copy-calibrated HBM bytes per launch)
 PMC_SUMMARY = os.path.join(ROOT, "profiles", "sample_kernel_decode_b256_v128256_bf16_pmc.md")
@@ -115,6 +116,80 @@ def make_args(L, st, ws):
     a.workspace_bytes = ws.numel()
     a.row_kinds = st["kinds"]
     return a
+
+
+def lm_head_handoff(L, lib, dev, w, st, stream, iters=50):
+    """The step's logits producer in front of the sampler: a random-init lm_head (2048 x V
+    bf16, the decode batch's hidden size) as a plain library GEMM, its bf16 output handed to
+    ns_sample directly, against the reference's handoff (engine.py:235-236: ``.float()``,
+    then the sampler on fp32).  Returns microseconds per step for the GEMM alone and for
+    each handoff."""
+    import torch
+
+    H = 2048
+    g = torch.Generator(device=dev)
+    g.manual_seed(4242)
+    hidden = torch.randn((w.batch, H), generator=g, device=dev, dtype=torch.float32).to(torch.bfloat16)
+    # the lm_head weight stored (H, V): a plain row-major right operand, no transposed view
+    weight = (torch.randn((H, w.vocab), generator=g, device=dev, dtype=torch.float32) * (3.0 / H ** 0.5)
+              ).to(torch.bfloat16)
+    lbf = torch.empty((w.batch, w.vocab), dtype=torch.bfloat16, device=dev)
+    lf32 = torch.empty((w.batch, w.vocab), dtype=torch.float32, device=dev)
+    # both workspaces stay referenced here: the cached one may be regrown for the fp32 call
+    ws_bf = L.workspace_for(dev, w.batch, w.vocab, L.NS_DTYPE_BF16)
+    ws32 = L.workspace_for(dev, w.batch, w.vocab, L.NS_DTYPE_F32)
+    a_bf = make_args(L, dict(st, logits=lbf), ws_bf)
+    a_f32 = make_args(L, dict(st, logits=lf32), ws32)
+    sh = ctypes.c_void_p(int(stream.cuda_stream))
+
+    w_vh = weight.t().contiguous()   # the (V, H) lm_head layout ns_lm_head_bf16 reads
+
+    def gemm():
+        torch.mm(hidden, weight, out=lbf)
+
+    def native_gemm():
+        L.lm_head_bf16(hidden, w_vh, out=lbf, stream=stream)
+
+    def native_step():
+        native_gemm()
+        if lib.ns_sample(ctypes.byref(a_bf), sh) != 0:
+            raise RuntimeError(f"ns_sample failed: {L.last_error()}")
+
+    def bf16_step():
+        gemm()
+        if lib.ns_sample(ctypes.byref(a_bf), sh) != 0:
+            raise RuntimeError(f"ns_sample failed: {L.last_error()}")
+
+    def f32_step():
+        gemm()
+        lf32.copy_(lbf)
+        if lib.ns_sample(ctypes.byref(a_f32), sh) != 0:
+            raise RuntimeError(f"ns_sample failed: {L.last_error()}")
+
+    res = {}
+    for name, fn in (("gemm", gemm), ("bf16_handoff", bf16_step), ("f32_handoff", f32_step),
+                     ("native_gemm", native_gemm), ("native_handoff", native_step)):
+        for _ in range(5):
+            fn()
+        torch.cuda.synchronize()
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for _ in range(iters):
+            fn()
+        e1.record(stream)
+        torch.cuda.synchronize()
+        res[name] = e0.elapsed_time(e1) / iters * 1e3
+    gemm_bytes = weight.numel() * 2 + hidden.numel() * 2 + lbf.numel() * 2
+    gemm_flop = 2.0 * w.batch * w.vocab * H
+    out = {"lm_head_gemm_us": res["gemm"], "lm_head_gemm_hbm_gbs": gemm_bytes / (res["gemm"] * 1e-6) / 1e9,
+           "lm_head_bf16_handoff_us": res["bf16_handoff"], "lm_head_f32_handoff_us": res["f32_handoff"],
+           "lm_head_native_gemm_us": res["native_gemm"],
+           "lm_head_native_hbm_frac": gemm_bytes / (res["native_gemm"] * 1e-6) / 1e9 / HBM_PEAK_GBS,
+           "lm_head_native_mfma_frac": gemm_flop / (res["native_gemm"] * 1e-6) / 1e12 / MFMA_BF16_PEAK_TFLOPS,
+           "lm_head_native_handoff_us": res["native_handoff"]}
+    del hidden, weight, w_vh, lbf, lf32, ws_bf, ws32
+    return out
 
 
 def measured_traffic():
@@ -258,6 +333,7 @@ def main(argv=None):
     prev.tolist()
     wrap_pipe_ms = (time.perf_counter() - t1) / nwrap * 1e3
     del dh
+    producer = lm_head_handoff(L, lib, dev, w, sets[0], stream) if args.config == WORKLOAD_CFG else {}
 
     if args.copy_mb > 0:
         n = args.copy_mb * (1 << 20) // 4
@@ -316,7 +392,7 @@ def main(argv=None):
                   "wrapper_inclusive_rows_per_s": w.batch / (wrap_ms * 1e-3),
                   "wrapper_inclusive_ms_device_histories": wrap_dev_ms,
                   "wrapper_inclusive_rows_per_s_device_histories": w.batch / (wrap_dev_ms * 1e-3),
-                  "wrapper_pipelined_ms_device_histories_async_ids": wrap_pipe_ms},
+                  "wrapper_pipelined_ms_device_histories_async_ids": wrap_pipe_ms, **producer},
     }
     print(json.dumps(line), flush=True)
     return 0

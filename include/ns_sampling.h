@@ -144,6 +144,21 @@ int ns_hist_assign(void* state, int32_t n_slots, int32_t capacity, int32_t slot,
 int ns_hist_append(void* state, int32_t n_slots, int32_t capacity, const int32_t* slots, const int64_t* token_ids,
                    int32_t n, int32_t* overflow, hipStream_t stream);
 
+/* The logits producer in front of ns_sample (bf16 lm_head GEMM, MFMA, fp32 accumulation):
+ *   logits[r][v] = bf16_rne( sum_c hidden[rows ? rows[r] : r][c] * weight[v][c] )
+ * for r < m, v < n, c < k.  Replaces the step's gather, GEMM and upcast (engine.py:233-236:
+ * hidden.index_select(0, sample_indices), compute_logits(...).float(); llama.py:136-143:
+ * F.linear(hidden_states, embed_tokens.weight)): the bf16 logits go to ns_sample as they
+ * are, so no float32 copy is written or read.
+ * hidden: bf16 rows of ld_hidden elements; rows: int64[m] device pointer or NULL; weight:
+ * (n, ld_weight) bf16, out_features x in_features (the tied embedding's layout); logits:
+ * (m, ld_logits) bf16.  k a positive multiple of 64; hidden and weight 16-byte aligned with
+ * ld_hidden, ld_weight multiples of 8 and >= k; rows[] in range (not checked: device data).
+ * Asynchronous on stream. */
+int ns_lm_head_bf16(const void* hidden, int64_t ld_hidden, const int64_t* rows, const void* weight,
+                    int64_t ld_weight, void* logits, int64_t ld_logits, int32_t m, int32_t n, int32_t k,
+                    hipStream_t stream);
+
 /* Last error message of the calling thread ("" if none). */
 const char* ns_last_error(void);
 

@@ -28,7 +28,7 @@ ABI_VERSION = 5
 
 # exported symbols, as declared in include/ns_sampling.h
 EXPORTS = ("ns_abi_version", "ns_sample", "ns_sample_lds_bytes", "ns_sample_workspace_bytes", "ns_hist_state_bytes",
-           "ns_hist_assign", "ns_hist_append", "ns_last_error")
+           "ns_hist_assign", "ns_hist_append", "ns_lm_head_bf16", "ns_last_error")
 
 
 class NsSampleArgs(ctypes.Structure):
@@ -97,6 +97,10 @@ def load(path: str = LIB_PATH) -> ctypes.CDLL:
     lib.ns_hist_append.restype = ctypes.c_int
     lib.ns_hist_append.argtypes = [ctypes.c_void_p, ctypes.c_int32, ctypes.c_int32, ctypes.c_void_p, ctypes.c_void_p,
                                    ctypes.c_int32, ctypes.c_void_p, ctypes.c_void_p]
+    lib.ns_lm_head_bf16.restype = ctypes.c_int
+    lib.ns_lm_head_bf16.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64,
+                                    ctypes.c_void_p, ctypes.c_int64, ctypes.c_int32, ctypes.c_int32, ctypes.c_int32,
+                                    ctypes.c_void_p]
     lib.ns_last_error.restype = ctypes.c_char_p
     lib.ns_last_error.argtypes = []
     v = lib.ns_abi_version()
@@ -257,6 +261,37 @@ def sample_raw(logits, temperature, top_k, top_p, rep_penalty, uniforms, out_ids
     if stream is None:
         stream = torch.cuda.current_stream(logits.device)
     check(lib.ns_sample(ctypes.byref(a), ctypes.c_void_p(int(stream.cuda_stream))))
+
+
+def lm_head_bf16(hidden, weight, rows=None, out=None, stream=None):
+    """bf16 logits = hidden[rows] @ weight.T through ns_lm_head_bf16 (fp32 accumulation).
+
+    hidden: (N, H) bf16 with unit stride along H; weight: (V, H) bf16, the lm_head /
+    tied-embedding layout; rows: optional (B,) int64 device tensor of hidden rows (the
+    step's sample positions), else every row; out: optional (B, V) bf16 tensor.
+    """
+    import torch
+
+    if hidden.dtype != torch.bfloat16 or weight.dtype != torch.bfloat16:
+        raise ValueError("hidden and weight must be bfloat16")
+    if hidden.dim() != 2 or weight.dim() != 2 or hidden.shape[1] != weight.shape[1]:
+        raise ValueError(f"shapes {tuple(hidden.shape)} and {tuple(weight.shape)} do not match (N, H) x (V, H)")
+    if hidden.stride(1) != 1 or weight.stride(1) != 1:
+        raise ValueError("hidden and weight need unit stride along the hidden dimension")
+    if rows is not None and (rows.dtype != torch.int64 or rows.dim() != 1 or not rows.is_contiguous()):
+        raise ValueError("rows must be a contiguous (B,) int64 tensor")
+    m = int(rows.numel()) if rows is not None else int(hidden.shape[0])
+    n, k = int(weight.shape[0]), int(weight.shape[1])
+    if out is None:
+        out = torch.empty((m, n), dtype=torch.bfloat16, device=hidden.device)
+    elif out.dtype != torch.bfloat16 or tuple(out.shape) != (m, n) or out.stride(1) != 1:
+        raise ValueError(f"out must be a (B, V) = ({m}, {n}) bf16 tensor with unit column stride")
+    if stream is None:
+        stream = torch.cuda.current_stream(hidden.device)
+    check(load().ns_lm_head_bf16(_ptr(hidden), int(hidden.stride(0)), _ptr(rows) if rows is not None else 0,
+                                 _ptr(weight), int(weight.stride(0)), _ptr(out), int(out.stride(0)), m, n, k,
+                                 ctypes.c_void_p(int(stream.cuda_stream))))
+    return out
 
 
 def hist_state_bytes(n_slots: int, capacity: int) -> int:

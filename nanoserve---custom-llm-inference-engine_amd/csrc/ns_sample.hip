@@ -11,6 +11,7 @@
 #include "ns_sample_kernel.h"
 #include "ns_segment.h"
 #include "ns_wide.h"
+#include "ns_lmhead.h"
 #include "ns_sampling.h"
 
 static_assert(ns::WIDE_MAX_ROWS == NS_WIDE_MAX_ROWS, "wide-path row limit");
@@ -1264,6 +1265,32 @@ int ns_hist_append(void* state, int32_t n_slots, int32_t capacity, const int32_t
                      n_slots, capacity, slots, token_ids, n, overflow);
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) return fail(NS_ERR_HIP, std::string("hist_append launch: ") + hipGetErrorString(e));
+  return NS_OK;
+}
+
+int ns_lm_head_bf16(const void* hidden, int64_t ld_hidden, const int64_t* rows, const void* weight,
+                    int64_t ld_weight, void* logits, int64_t ld_logits, int32_t m, int32_t n, int32_t k,
+                    hipStream_t stream) {
+  if (hidden == nullptr || weight == nullptr || logits == nullptr)
+    return fail(NS_ERR_INVALID, "hidden, weight or logits is NULL");
+  if (m < 0 || n < 0) return fail(NS_ERR_INVALID, "m or n < 0");
+  if (k <= 0 || k % ns::LM_KT != 0) return fail(NS_ERR_INVALID, "k must be a positive multiple of 64");
+  if (ld_hidden < k || ld_weight < k || ld_hidden % 8 != 0 || ld_weight % 8 != 0)
+    return fail(NS_ERR_INVALID, "ld_hidden and ld_weight must be multiples of 8 and >= k");
+  if (ld_logits < n) return fail(NS_ERR_INVALID, "ld_logits < n");
+  if (ld_weight > (int64_t)(0xffffffffu / (2u * ns::LM_NT)))
+    return fail(NS_ERR_INVALID, "ld_weight too large (a workgroup's weight rows span 32-bit offsets)");
+  if (((uintptr_t)hidden | (uintptr_t)weight) % 16 != 0)
+    return fail(NS_ERR_ALIGN, "hidden and weight must be 16-byte aligned");
+  if (m == 0 || n == 0) return NS_OK;
+  const int64_t gy = ((int64_t)m + ns::LM_MT - 1) / ns::LM_MT;
+  if (gy > 65535) return fail(NS_ERR_INVALID, "m too large");
+  ns::LmParams P{static_cast<const uint16_t*>(hidden), ld_hidden, rows, static_cast<const uint16_t*>(weight),
+                 ld_weight, static_cast<uint16_t*>(logits), ld_logits, m, n, k};
+  hipLaunchKernelGGL(ns::lm_head_kernel, dim3((unsigned)((n + ns::LM_NT - 1) / ns::LM_NT), (unsigned)gy),
+                     dim3(ns::LM_THREADS), 0, stream, P);
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return fail(NS_ERR_HIP, std::string("lm_head launch: ") + hipGetErrorString(e));
   return NS_OK;
 }
 

@@ -139,3 +139,22 @@ def test_aligned_rows_pads_misaligned_vocab():
     b9 = torch.ones(2, 9, dtype=torch.bfloat16)             # 18-byte rows: padded to 16 elements
     yb9, _ = L.aligned_rows(b9, None)
     assert yb9.stride(0) == 16 and torch.equal(yb9, b9)
+
+
+def test_lm_head_argument_errors():
+    """ns_lm_head_bf16 rejects bad shapes, strides and alignment before any launch; an empty
+    product is a no-op."""
+    if not os.path.exists(L.LIB_PATH):
+        pytest.skip("library not built")
+    lib = L.load()
+    f = lib.ns_lm_head_bf16
+    h, w, o = 4096, 8192, 12288    # 16-byte aligned stand-in addresses (never dereferenced)
+    assert f(None, 64, None, w, 64, o, 64, 1, 1, 64, None) == 1 and "NULL" in L.last_error()
+    assert f(h, 128, None, w, 128, o, 64, 1, 1, 100, None) == 1 and "multiple of 64" in L.last_error()
+    assert f(h, 60, None, w, 128, o, 64, 1, 1, 64, None) == 1 and "ld_hidden" in L.last_error()
+    assert f(h, 64, None, w, 64, o, 4, 1, 8, 64, None) == 1 and "ld_logits" in L.last_error()
+    assert f(h + 8, 64, None, w, 64, o, 64, 1, 1, 64, None) == 2 and "aligned" in L.last_error()   # NS_ERR_ALIGN
+    assert f(h, 64, None, w, 64, o, 64, -1, 1, 64, None) == 1
+    assert f(h, 64, None, w, 1 << 24, o, 64, 1, 1, 64, None) == 1 and "ld_weight" in L.last_error()
+    assert f(h, 64, None, w, 64, o, 64, 0, 5, 64, None) == 0      # nothing to compute
+    assert f(h, 64, None, w, 64, o, 64, 3, 0, 64, None) == 0
