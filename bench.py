@@ -147,8 +147,17 @@ def lm_head_handoff(L, lib, dev, w, st, stream, iters=50):
     def gemm():
         torch.mm(hidden, weight, out=lbf)
 
+    packed = L.PackedLmHead(w_vh)     # one-time pack, as at model load
+
     def native_gemm():
         L.lm_head_bf16(hidden, w_vh, out=lbf, stream=stream)
+
+    def packed_gemm():
+        L.lm_head_bf16(hidden, packed, out=lbf, stream=stream)
+
+    def reference_gemm():
+        # the reference's call on the (V, H) embedding layout (llama.py:141)
+        torch.nn.functional.linear(hidden, w_vh)
 
     def native_step():
         native_gemm()
@@ -168,7 +177,8 @@ def lm_head_handoff(L, lib, dev, w, st, stream, iters=50):
 
     res = {}
     for name, fn in (("gemm", gemm), ("bf16_handoff", bf16_step), ("f32_handoff", f32_step),
-                     ("native_gemm", native_gemm), ("native_handoff", native_step)):
+                     ("native_gemm", native_gemm), ("native_handoff", native_step), ("packed_gemm", packed_gemm),
+                     ("reference_gemm", reference_gemm)):
         for _ in range(5):
             fn()
         torch.cuda.synchronize()
@@ -187,8 +197,9 @@ def lm_head_handoff(L, lib, dev, w, st, stream, iters=50):
            "lm_head_native_gemm_us": res["native_gemm"],
            "lm_head_native_hbm_frac": gemm_bytes / (res["native_gemm"] * 1e-6) / 1e9 / HBM_PEAK_GBS,
            "lm_head_native_mfma_frac": gemm_flop / (res["native_gemm"] * 1e-6) / 1e12 / MFMA_BF16_PEAK_TFLOPS,
-           "lm_head_native_handoff_us": res["native_handoff"]}
-    del hidden, weight, w_vh, lbf, lf32, ws_bf, ws32
+           "lm_head_native_handoff_us": res["native_handoff"], "lm_head_packed_gemm_us": res["packed_gemm"],
+           "lm_head_reference_layout_gemm_us": res["reference_gemm"]}
+    del hidden, weight, w_vh, packed, lbf, lf32, ws_bf, ws32
     return out
 
 

@@ -159,6 +159,23 @@ int ns_lm_head_bf16(const void* hidden, int64_t ld_hidden, const int64_t* rows, 
                     int64_t ld_weight, void* logits, int64_t ld_logits, int32_t m, int32_t n, int32_t k,
                     hipStream_t stream);
 
+/* Bytes of the packed lm_head weight for n vocab rows of k: the weight as contiguous
+ * 32 KB tiles of 256 rows x 64 (the order the GEMM reads them; rows past n zero).  No
+ * counterpart in the reference (its lm_head reads the (n, k) weight as stored). */
+int ns_lm_head_packed_bytes(int32_t n, int32_t k, uint64_t* bytes);
+
+/* Pack the (n, ld_weight) bf16 lm_head weight into `packed` (ns_lm_head_packed_bytes bytes,
+ * 16-byte aligned), once, at model load: a one-time copy that lets ns_lm_head_bf16_packed
+ * stream the weight at close to the HBM rate.  Asynchronous on stream.  No counterpart in
+ * the reference. */
+int ns_lm_head_pack_bf16(const void* weight, int64_t ld_weight, int32_t n, int32_t k, void* packed,
+                         hipStream_t stream);
+
+/* ns_lm_head_bf16 over the packed weight (same result bit for bit: the same products in
+ * the same order).  Replaces the same reference calls (engine.py:233-236, llama.py:136-143). */
+int ns_lm_head_bf16_packed(const void* hidden, int64_t ld_hidden, const int64_t* rows, const void* packed,
+                           void* logits, int64_t ld_logits, int32_t m, int32_t n, int32_t k, hipStream_t stream);
+
 /* Last error message of the calling thread ("" if none). */
 const char* ns_last_error(void);
 

@@ -28,7 +28,8 @@ ABI_VERSION = 5
 
 # exported symbols, as declared in include/ns_sampling.h
 EXPORTS = ("ns_abi_version", "ns_sample", "ns_sample_lds_bytes", "ns_sample_workspace_bytes", "ns_hist_state_bytes",
-           "ns_hist_assign", "ns_hist_append", "ns_lm_head_bf16", "ns_last_error")
+           "ns_hist_assign", "ns_hist_append", "ns_lm_head_bf16", "ns_lm_head_packed_bytes",
+           "ns_lm_head_pack_bf16", "ns_lm_head_bf16_packed", "ns_last_error")
 
 
 class NsSampleArgs(ctypes.Structure):
@@ -101,6 +102,15 @@ def load(path: str = LIB_PATH) -> ctypes.CDLL:
     lib.ns_lm_head_bf16.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64,
                                     ctypes.c_void_p, ctypes.c_int64, ctypes.c_int32, ctypes.c_int32, ctypes.c_int32,
                                     ctypes.c_void_p]
+    lib.ns_lm_head_packed_bytes.restype = ctypes.c_int
+    lib.ns_lm_head_packed_bytes.argtypes = [ctypes.c_int32, ctypes.c_int32, ctypes.POINTER(ctypes.c_uint64)]
+    lib.ns_lm_head_pack_bf16.restype = ctypes.c_int
+    lib.ns_lm_head_pack_bf16.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_int32, ctypes.c_int32,
+                                         ctypes.c_void_p, ctypes.c_void_p]
+    lib.ns_lm_head_bf16_packed.restype = ctypes.c_int
+    lib.ns_lm_head_bf16_packed.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p, ctypes.c_void_p,
+                                           ctypes.c_void_p, ctypes.c_int64, ctypes.c_int32, ctypes.c_int32,
+                                           ctypes.c_int32, ctypes.c_void_p]
     lib.ns_last_error.restype = ctypes.c_char_p
     lib.ns_last_error.argtypes = []
     v = lib.ns_abi_version()
@@ -263,20 +273,46 @@ def sample_raw(logits, temperature, top_k, top_p, rep_penalty, uniforms, out_ids
     check(lib.ns_sample(ctypes.byref(a), ctypes.c_void_p(int(stream.cuda_stream))))
 
 
+class PackedLmHead:
+    """An lm_head weight ((V, H) bf16) packed once by ns_lm_head_pack_bf16 into contiguous
+    256 x 64 tiles, for ``lm_head_bf16``: the same logits, with the weight streamed at
+    close to the HBM rate.  Holds its own device buffer; the weight itself is not kept."""
+
+    def __init__(self, weight, stream=None):
+        import torch
+
+        if weight.dtype != torch.bfloat16 or weight.dim() != 2 or weight.stride(1) != 1:
+            raise ValueError("weight must be a (V, H) bfloat16 tensor with unit stride along H")
+        self.n, self.k = int(weight.shape[0]), int(weight.shape[1])
+        nbytes = ctypes.c_uint64(0)
+        check(load().ns_lm_head_packed_bytes(self.n, self.k, ctypes.byref(nbytes)))
+        self.buffer = torch.empty(int(nbytes.value), dtype=torch.uint8, device=weight.device)
+        if stream is None:
+            stream = torch.cuda.current_stream(weight.device)
+        check(load().ns_lm_head_pack_bf16(_ptr(weight), int(weight.stride(0)), self.n, self.k, _ptr(self.buffer),
+                                          ctypes.c_void_p(int(stream.cuda_stream))))
+
+    @property
+    def shape(self):
+        return (self.n, self.k)
+
+
 def lm_head_bf16(hidden, weight, rows=None, out=None, stream=None):
     """bf16 logits = hidden[rows] @ weight.T through ns_lm_head_bf16 (fp32 accumulation).
 
     hidden: (N, H) bf16 with unit stride along H; weight: (V, H) bf16, the lm_head /
-    tied-embedding layout; rows: optional (B,) int64 device tensor of hidden rows (the
-    step's sample positions), else every row; out: optional (B, V) bf16 tensor.
+    tied-embedding layout, or a ``PackedLmHead`` of it; rows: optional (B,) int64 device
+    tensor of hidden rows (the step's sample positions), else every row; out: optional
+    (B, V) bf16 tensor.
     """
     import torch
 
-    if hidden.dtype != torch.bfloat16 or weight.dtype != torch.bfloat16:
+    packed = isinstance(weight, PackedLmHead)
+    if hidden.dtype != torch.bfloat16 or (not packed and weight.dtype != torch.bfloat16):
         raise ValueError("hidden and weight must be bfloat16")
-    if hidden.dim() != 2 or weight.dim() != 2 or hidden.shape[1] != weight.shape[1]:
+    if hidden.dim() != 2 or len(weight.shape) != 2 or hidden.shape[1] != weight.shape[1]:
         raise ValueError(f"shapes {tuple(hidden.shape)} and {tuple(weight.shape)} do not match (N, H) x (V, H)")
-    if hidden.stride(1) != 1 or weight.stride(1) != 1:
+    if hidden.stride(1) != 1 or (not packed and weight.stride(1) != 1):
         raise ValueError("hidden and weight need unit stride along the hidden dimension")
     if rows is not None and (rows.dtype != torch.int64 or rows.dim() != 1 or not rows.is_contiguous()):
         raise ValueError("rows must be a contiguous (B,) int64 tensor")
@@ -288,9 +324,14 @@ def lm_head_bf16(hidden, weight, rows=None, out=None, stream=None):
         raise ValueError(f"out must be a (B, V) = ({m}, {n}) bf16 tensor with unit column stride")
     if stream is None:
         stream = torch.cuda.current_stream(hidden.device)
-    check(load().ns_lm_head_bf16(_ptr(hidden), int(hidden.stride(0)), _ptr(rows) if rows is not None else 0,
-                                 _ptr(weight), int(weight.stride(0)), _ptr(out), int(out.stride(0)), m, n, k,
-                                 ctypes.c_void_p(int(stream.cuda_stream))))
+    sh = ctypes.c_void_p(int(stream.cuda_stream))
+    rp = _ptr(rows) if rows is not None else 0
+    if packed:
+        check(load().ns_lm_head_bf16_packed(_ptr(hidden), int(hidden.stride(0)), rp, _ptr(weight.buffer), _ptr(out),
+                                            int(out.stride(0)), m, n, k, sh))
+    else:
+        check(load().ns_lm_head_bf16(_ptr(hidden), int(hidden.stride(0)), rp, _ptr(weight), int(weight.stride(0)),
+                                     _ptr(out), int(out.stride(0)), m, n, k, sh))
     return out
 
 

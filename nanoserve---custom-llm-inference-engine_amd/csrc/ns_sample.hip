@@ -1268,30 +1268,88 @@ int ns_hist_append(void* state, int32_t n_slots, int32_t capacity, const int32_t
   return NS_OK;
 }
 
-int ns_lm_head_bf16(const void* hidden, int64_t ld_hidden, const int64_t* rows, const void* weight,
-                    int64_t ld_weight, void* logits, int64_t ld_logits, int32_t m, int32_t n, int32_t k,
-                    hipStream_t stream) {
+static int lm_check(const void* hidden, int64_t ld_hidden, const void* weight, int64_t ld_weight, const void* logits,
+                    int64_t ld_logits, int32_t m, int32_t n, int32_t k, bool packed) {
   if (hidden == nullptr || weight == nullptr || logits == nullptr)
     return fail(NS_ERR_INVALID, "hidden, weight or logits is NULL");
   if (m < 0 || n < 0) return fail(NS_ERR_INVALID, "m or n < 0");
   if (k <= 0 || k % ns::LM_KT != 0) return fail(NS_ERR_INVALID, "k must be a positive multiple of 64");
-  if (ld_hidden < k || ld_weight < k || ld_hidden % 8 != 0 || ld_weight % 8 != 0)
+  if (ld_hidden < k || ld_hidden % 8 != 0 || (!packed && (ld_weight < k || ld_weight % 8 != 0)))
     return fail(NS_ERR_INVALID, "ld_hidden and ld_weight must be multiples of 8 and >= k");
   if (ld_logits < n) return fail(NS_ERR_INVALID, "ld_logits < n");
-  if (ld_weight > (int64_t)(0xffffffffu / (2u * ns::LM_NT)))
+  if (!packed && ld_weight > (int64_t)(0xffffffffu / (2u * ns::LM_NT)))
     return fail(NS_ERR_INVALID, "ld_weight too large (a workgroup's weight rows span 32-bit offsets)");
   if (((uintptr_t)hidden | (uintptr_t)weight) % 16 != 0)
     return fail(NS_ERR_ALIGN, "hidden and weight must be 16-byte aligned");
-  if (m == 0 || n == 0) return NS_OK;
-  const int64_t gy = ((int64_t)m + ns::LM_MT - 1) / ns::LM_MT;
+  return NS_OK;
+}
+
+static int lm_launch(const void* hidden, int64_t ld_hidden, const int64_t* rows, const void* weight, int64_t ld_weight,
+                     void* logits, int64_t ld_logits, int32_t m, int32_t n, int32_t k, bool packed,
+                     hipStream_t stream) {
+  // waves along the batch: the fewest that hold it (64 rows each), so small batches keep every
+  // wave on products; batches beyond 256 rows take several workgroup rows
+  const int wm = m <= 64 ? 1 : m <= 128 ? 2 : 4;
+  const int64_t gy = ((int64_t)m + 64 * wm - 1) / (64 * wm);
   if (gy > 65535) return fail(NS_ERR_INVALID, "m too large");
   ns::LmParams P{static_cast<const uint16_t*>(hidden), ld_hidden, rows, static_cast<const uint16_t*>(weight),
-                 ld_weight, static_cast<uint16_t*>(logits), ld_logits, m, n, k};
-  hipLaunchKernelGGL(ns::lm_head_kernel, dim3((unsigned)((n + ns::LM_NT - 1) / ns::LM_NT), (unsigned)gy),
-                     dim3(ns::LM_THREADS), 0, stream, P);
+                 packed ? 0 : ld_weight, static_cast<uint16_t*>(logits), ld_logits, m, n, k};
+  const dim3 grid((unsigned)((n + ns::LM_NT - 1) / ns::LM_NT), (unsigned)gy), block(ns::LM_THREADS);
+  if (packed) {
+    if (wm == 1) hipLaunchKernelGGL((ns::lm_head_kernel<1, 4, true>), grid, block, 0, stream, P);
+    else if (wm == 2) hipLaunchKernelGGL((ns::lm_head_kernel<2, 3, true>), grid, block, 0, stream, P);
+    else hipLaunchKernelGGL((ns::lm_head_kernel<4, 2, true>), grid, block, 0, stream, P);
+  } else {
+    if (wm == 1) hipLaunchKernelGGL((ns::lm_head_kernel<1, 4, false>), grid, block, 0, stream, P);
+    else if (wm == 2) hipLaunchKernelGGL((ns::lm_head_kernel<2, 3, false>), grid, block, 0, stream, P);
+    else hipLaunchKernelGGL((ns::lm_head_kernel<4, 2, false>), grid, block, 0, stream, P);
+  }
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) return fail(NS_ERR_HIP, std::string("lm_head launch: ") + hipGetErrorString(e));
   return NS_OK;
+}
+
+int ns_lm_head_bf16(const void* hidden, int64_t ld_hidden, const int64_t* rows, const void* weight,
+                    int64_t ld_weight, void* logits, int64_t ld_logits, int32_t m, int32_t n, int32_t k,
+                    hipStream_t stream) {
+  const int rc = lm_check(hidden, ld_hidden, weight, ld_weight, logits, ld_logits, m, n, k, false);
+  if (rc != NS_OK) return rc;
+  if (m == 0 || n == 0) return NS_OK;
+  return lm_launch(hidden, ld_hidden, rows, weight, ld_weight, logits, ld_logits, m, n, k, false, stream);
+}
+
+int ns_lm_head_packed_bytes(int32_t n, int32_t k, uint64_t* bytes) {
+  if (bytes == nullptr) return fail(NS_ERR_INVALID, "bytes is NULL");
+  if (n < 0) return fail(NS_ERR_INVALID, "n < 0");
+  if (k <= 0 || k % ns::LM_KT != 0) return fail(NS_ERR_INVALID, "k must be a positive multiple of 64");
+  *bytes = (uint64_t)((n + ns::LM_NT - 1) / ns::LM_NT) * (uint64_t)(k / ns::LM_KT) * (uint64_t)ns::LM_TILE_BYTES;
+  return NS_OK;
+}
+
+int ns_lm_head_pack_bf16(const void* weight, int64_t ld_weight, int32_t n, int32_t k, void* packed,
+                         hipStream_t stream) {
+  if (weight == nullptr || packed == nullptr) return fail(NS_ERR_INVALID, "weight or packed is NULL");
+  uint64_t bytes = 0;
+  int rc = ns_lm_head_packed_bytes(n, k, &bytes);
+  if (rc != NS_OK) return rc;
+  if (ld_weight < k || ld_weight % 8 != 0) return fail(NS_ERR_INVALID, "ld_weight must be a multiple of 8 and >= k");
+  if (((uintptr_t)weight | (uintptr_t)packed) % 16 != 0)
+    return fail(NS_ERR_ALIGN, "weight and packed must be 16-byte aligned");
+  if (bytes == 0) return NS_OK;
+  const uint64_t pieces = bytes / 16;
+  hipLaunchKernelGGL(ns::lm_head_pack_kernel, dim3((unsigned)((pieces + 255) / 256)), dim3(256), 0, stream,
+                     static_cast<const uint16_t*>(weight), ld_weight, n, k, static_cast<uint16_t*>(packed));
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return fail(NS_ERR_HIP, std::string("lm_head pack launch: ") + hipGetErrorString(e));
+  return NS_OK;
+}
+
+int ns_lm_head_bf16_packed(const void* hidden, int64_t ld_hidden, const int64_t* rows, const void* packed,
+                           void* logits, int64_t ld_logits, int32_t m, int32_t n, int32_t k, hipStream_t stream) {
+  const int rc = lm_check(hidden, ld_hidden, packed, 0, logits, ld_logits, m, n, k, true);
+  if (rc != NS_OK) return rc;
+  if (m == 0 || n == 0) return NS_OK;
+  return lm_launch(hidden, ld_hidden, rows, packed, 0, logits, ld_logits, m, n, k, true, stream);
 }
 
 const char* ns_last_error(void) { return g_err.c_str(); }

@@ -53,6 +53,21 @@ def test_lm_head_matches_fp32(device, m, vocab, k):
     check(ours, hidden, weight)
 
 
+@pytest.mark.parametrize("m,vocab,k", [(256, 128256, 2048), (64, 128256, 2048), (1, 128256, 2048), (77, 1000, 192),
+                                       (300, 300, 64)])
+def test_packed_weight_gives_the_same_logits(device, m, vocab, k):
+    """The packed layout changes only where the weight is read from: bit-identical logits."""
+    print(f"[lm_head] packed m={m} V={vocab} k={k}", flush=True)
+    hidden, weight = make(device, m, vocab, k, seed=7 + m, scale=3.0)
+    pw = L.PackedLmHead(weight)
+    plain = L.lm_head_bf16(hidden, weight)
+    packed = L.lm_head_bf16(hidden, pw)
+    torch.cuda.synchronize()
+    assert torch.equal(plain.view(torch.int16), packed.view(torch.int16))
+    if m == 256:
+        check(packed, hidden, weight)
+
+
 def test_lm_head_gathers_rows_and_strides(device):
     """Sample positions gathered in the kernel (engine.py:233-234), a padded hidden row
     stride and a logits buffer wider than the vocab."""
