@@ -203,6 +203,48 @@ def lm_head_handoff(L, lib, dev, w, st, stream, iters=50):
     return out
 
 
+def lm_head_sweep(L, dev, batches=(256, 128, 64, 16, 1), iters=20):
+    """The logits producer alone over decode batch sizes: hidden (B, 2048) bf16 times a
+    random-init (128256, 2048) bf16 lm_head, through ns_lm_head_bf16 on the weight as
+    stored, on the packed weight, and through the library GEMM on the reference's layout
+    (F.linear, llama.py:141) and on a transposed copy.  One JSON line per batch size."""
+    import torch
+    import torch.nn.functional as F
+
+    H, V = 2048, 128256
+    g = torch.Generator(device=dev)
+    g.manual_seed(4243)
+    hid = torch.randn((max(batches), H), generator=g, device=dev, dtype=torch.float32).to(torch.bfloat16)
+    w = (torch.randn((V, H), generator=g, device=dev, dtype=torch.float32) * (3.0 / H ** 0.5)).to(torch.bfloat16)
+    w_hv = w.t().contiguous()
+    pw = L.PackedLmHead(w)
+    out = torch.empty((max(batches), V), dtype=torch.bfloat16, device=dev)
+
+    def timed(fn):
+        for _ in range(3):
+            fn()
+        torch.cuda.synchronize()
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(iters):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / iters * 1e3
+
+    for m in batches:
+        h, o = hid[:m], out[:m]
+        r = {"batch": m, "native_us": timed(lambda: L.lm_head_bf16(h, w, out=o)),
+             "packed_us": timed(lambda: L.lm_head_bf16(h, pw, out=o)),
+             "library_reference_layout_us": timed(lambda: F.linear(h, w)),
+             "library_transposed_copy_us": timed(lambda: torch.mm(h, w_hv))}
+        nbytes = V * H * 2 + m * H * 2 + m * V * 2
+        r["packed_hbm_frac"] = nbytes / (r["packed_us"] * 1e-6) / 1e9 / HBM_PEAK_GBS
+        r["packed_mfma_frac"] = 2.0 * m * V * H / (r["packed_us"] * 1e-6) / 1e12 / MFMA_BF16_PEAK_TFLOPS
+        print(json.dumps({"lm_head_sweep": r}), flush=True)
+
+
 def measured_traffic():
     """HBM bytes per launch from the committed rocprofv3 counter summary, or None."""
     try:
@@ -253,6 +295,8 @@ def main(argv=None):
     ap.add_argument("--copy-mb", type=int, default=0,
                     help="after the timed loop, run 4 plain device copies of this many MiB (a known-size "
                          "reference for HBM byte counters under rocprofv3 --pmc)")
+    ap.add_argument("--lm-head-sweep", action="store_true",
+                    help="time only the logits producer (lm_head GEMM) over decode batch sizes and exit")
     args = ap.parse_args(argv)
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: the sampler's rows are independent and this build runs on a single "
@@ -269,6 +313,9 @@ def main(argv=None):
     lib = L.load()
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
+    if args.lm_head_sweep:
+        lm_head_sweep(L, dev)
+        return 0
 
     w = W.make_workload(args.config)
     sets = build_sets(w, dev, ROTATE, roll=args.config != WORKLOAD_CFG)
