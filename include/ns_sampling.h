@@ -172,9 +172,12 @@ int ns_lm_head_pack_bf16(const void* weight, int64_t ld_weight, int32_t n, int32
                          hipStream_t stream);
 
 /* ns_lm_head_bf16 over the packed weight (same result bit for bit: the same products in
- * the same order).  Replaces the same reference calls (engine.py:233-236, llama.py:136-143). */
+ * the same order).  packed_bytes must equal ns_lm_head_packed_bytes(n, k): the buffer was
+ * packed for this (n, k).  Replaces the same reference calls (engine.py:233-236,
+ * llama.py:136-143). */
 int ns_lm_head_bf16_packed(const void* hidden, int64_t ld_hidden, const int64_t* rows, const void* packed,
-                           void* logits, int64_t ld_logits, int32_t m, int32_t n, int32_t k, hipStream_t stream);
+                           uint64_t packed_bytes, void* logits, int64_t ld_logits, int32_t m, int32_t n, int32_t k,
+                           hipStream_t stream);
 
 /* Last error message of the calling thread ("" if none). */
 const char* ns_last_error(void);

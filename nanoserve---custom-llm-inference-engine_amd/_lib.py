@@ -109,8 +109,8 @@ def load(path: str = LIB_PATH) -> ctypes.CDLL:
                                          ctypes.c_void_p, ctypes.c_void_p]
     lib.ns_lm_head_bf16_packed.restype = ctypes.c_int
     lib.ns_lm_head_bf16_packed.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p, ctypes.c_void_p,
-                                           ctypes.c_void_p, ctypes.c_int64, ctypes.c_int32, ctypes.c_int32,
-                                           ctypes.c_int32, ctypes.c_void_p]
+                                           ctypes.c_uint64, ctypes.c_void_p, ctypes.c_int64, ctypes.c_int32,
+                                           ctypes.c_int32, ctypes.c_int32, ctypes.c_void_p]
     lib.ns_last_error.restype = ctypes.c_char_p
     lib.ns_last_error.argtypes = []
     v = lib.ns_abi_version()
@@ -327,8 +327,8 @@ def lm_head_bf16(hidden, weight, rows=None, out=None, stream=None):
     sh = ctypes.c_void_p(int(stream.cuda_stream))
     rp = _ptr(rows) if rows is not None else 0
     if packed:
-        check(load().ns_lm_head_bf16_packed(_ptr(hidden), int(hidden.stride(0)), rp, _ptr(weight.buffer), _ptr(out),
-                                            int(out.stride(0)), m, n, k, sh))
+        check(load().ns_lm_head_bf16_packed(_ptr(hidden), int(hidden.stride(0)), rp, _ptr(weight.buffer),
+                                            int(weight.buffer.numel()), _ptr(out), int(out.stride(0)), m, n, k, sh))
     else:
         check(load().ns_lm_head_bf16(_ptr(hidden), int(hidden.stride(0)), rp, _ptr(weight), int(weight.stride(0)),
                                      _ptr(out), int(out.stride(0)), m, n, k, sh))

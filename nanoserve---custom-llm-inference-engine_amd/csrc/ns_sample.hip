@@ -1345,9 +1345,14 @@ int ns_lm_head_pack_bf16(const void* weight, int64_t ld_weight, int32_t n, int32
 }
 
 int ns_lm_head_bf16_packed(const void* hidden, int64_t ld_hidden, const int64_t* rows, const void* packed,
-                           void* logits, int64_t ld_logits, int32_t m, int32_t n, int32_t k, hipStream_t stream) {
-  const int rc = lm_check(hidden, ld_hidden, packed, 0, logits, ld_logits, m, n, k, true);
+                           uint64_t packed_bytes, void* logits, int64_t ld_logits, int32_t m, int32_t n, int32_t k,
+                           hipStream_t stream) {
+  int rc = lm_check(hidden, ld_hidden, packed, 0, logits, ld_logits, m, n, k, true);
   if (rc != NS_OK) return rc;
+  uint64_t want = 0;
+  rc = ns_lm_head_packed_bytes(n, k, &want);
+  if (rc != NS_OK) return rc;
+  if (packed_bytes != want) return fail(NS_ERR_INVALID, "packed_bytes does not match the packed layout of (n, k)");
   if (m == 0 || n == 0) return NS_OK;
   return lm_launch(hidden, ld_hidden, rows, packed, 0, logits, ld_logits, m, n, k, true, stream);
 }

@@ -164,4 +164,7 @@ def test_lm_head_argument_errors():
     assert lib.ns_lm_head_packed_bytes(257, 64, ctypes.byref(nb)) == 0 and nb.value == 2 * 32768
     assert lib.ns_lm_head_packed_bytes(10, 100, ctypes.byref(nb)) == 1
     assert lib.ns_lm_head_pack_bf16(None, 64, 10, 64, h, None) == 1 and "NULL" in L.last_error()
-    assert lib.ns_lm_head_bf16_packed(h, 64, None, w, o, 64, 1, 1, 65, None) == 1
+    assert lib.ns_lm_head_bf16_packed(h, 64, None, w, 32768, o, 64, 1, 1, 65, None) == 1
+    # a buffer packed for another shape is refused before any launch
+    assert lib.ns_lm_head_bf16_packed(h, 64, None, w, 32768, o, 300, 1, 300, 64, None) == 1
+    assert "packed_bytes" in L.last_error()
