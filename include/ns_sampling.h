@@ -150,12 +150,14 @@ int ns_hist_append(void* state, int32_t n_slots, int32_t capacity, const int32_t
  * hidden.index_select(0, sample_indices), compute_logits(...).float(); llama.py:136-143:
  * F.linear(hidden_states, embed_tokens.weight)): the bf16 logits go to ns_sample as they
  * are, so no float32 copy is written or read.
- * hidden: bf16 rows of ld_hidden elements; rows: int64[m] device pointer or NULL; weight:
+ * hidden: n_hidden bf16 rows of ld_hidden elements; rows: int64[m] device pointer or NULL
+ * (without it the first m rows, m <= n_hidden; a gathered index outside [0, n_hidden) gives
+ * that logits row as NaN, which the sampler reports as a NaN row, instead of a read out of
+ * bounds, where engine.py:234's index_select would raise); weight:
  * (n, ld_weight) bf16, out_features x in_features (the tied embedding's layout); logits:
  * (m, ld_logits) bf16.  k a positive multiple of 64; hidden and weight 16-byte aligned with
- * ld_hidden, ld_weight multiples of 8 and >= k; rows[] in range (not checked: device data).
- * Asynchronous on stream. */
-int ns_lm_head_bf16(const void* hidden, int64_t ld_hidden, const int64_t* rows, const void* weight,
+ * ld_hidden, ld_weight multiples of 8 and >= k.  Asynchronous on stream. */
+int ns_lm_head_bf16(const void* hidden, int64_t ld_hidden, int64_t n_hidden, const int64_t* rows, const void* weight,
                     int64_t ld_weight, void* logits, int64_t ld_logits, int32_t m, int32_t n, int32_t k,
                     hipStream_t stream);
 
@@ -175,7 +177,8 @@ int ns_lm_head_pack_bf16(const void* weight, int64_t ld_weight, int32_t n, int32
  * the same order).  packed_bytes must equal ns_lm_head_packed_bytes(n, k): the buffer was
  * packed for this (n, k).  Replaces the same reference calls (engine.py:233-236,
  * llama.py:136-143). */
-int ns_lm_head_bf16_packed(const void* hidden, int64_t ld_hidden, const int64_t* rows, const void* packed,
+int ns_lm_head_bf16_packed(const void* hidden, int64_t ld_hidden, int64_t n_hidden, const int64_t* rows,
+                           const void* packed,
                            uint64_t packed_bytes, void* logits, int64_t ld_logits, int32_t m, int32_t n, int32_t k,
                            hipStream_t stream);
 

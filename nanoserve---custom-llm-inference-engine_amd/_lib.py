@@ -99,7 +99,8 @@ def load(path: str = LIB_PATH) -> ctypes.CDLL:
     lib.ns_hist_append.argtypes = [ctypes.c_void_p, ctypes.c_int32, ctypes.c_int32, ctypes.c_void_p, ctypes.c_void_p,
                                    ctypes.c_int32, ctypes.c_void_p, ctypes.c_void_p]
     lib.ns_lm_head_bf16.restype = ctypes.c_int
-    lib.ns_lm_head_bf16.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64,
+    lib.ns_lm_head_bf16.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_int64, ctypes.c_void_p, ctypes.c_void_p,
+                                    ctypes.c_int64,
                                     ctypes.c_void_p, ctypes.c_int64, ctypes.c_int32, ctypes.c_int32, ctypes.c_int32,
                                     ctypes.c_void_p]
     lib.ns_lm_head_packed_bytes.restype = ctypes.c_int
@@ -108,7 +109,8 @@ def load(path: str = LIB_PATH) -> ctypes.CDLL:
     lib.ns_lm_head_pack_bf16.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_int32, ctypes.c_int32,
                                          ctypes.c_void_p, ctypes.c_void_p]
     lib.ns_lm_head_bf16_packed.restype = ctypes.c_int
-    lib.ns_lm_head_bf16_packed.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p, ctypes.c_void_p,
+    lib.ns_lm_head_bf16_packed.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_int64, ctypes.c_void_p,
+                                           ctypes.c_void_p,
                                            ctypes.c_uint64, ctypes.c_void_p, ctypes.c_int64, ctypes.c_int32,
                                            ctypes.c_int32, ctypes.c_int32, ctypes.c_void_p]
     lib.ns_last_error.restype = ctypes.c_char_p
@@ -327,10 +329,12 @@ def lm_head_bf16(hidden, weight, rows=None, out=None, stream=None):
     sh = ctypes.c_void_p(int(stream.cuda_stream))
     rp = _ptr(rows) if rows is not None else 0
     if packed:
-        check(load().ns_lm_head_bf16_packed(_ptr(hidden), int(hidden.stride(0)), rp, _ptr(weight.buffer),
+        check(load().ns_lm_head_bf16_packed(_ptr(hidden), int(hidden.stride(0)), int(hidden.shape[0]), rp,
+                                            _ptr(weight.buffer),
                                             int(weight.buffer.numel()), _ptr(out), int(out.stride(0)), m, n, k, sh))
     else:
-        check(load().ns_lm_head_bf16(_ptr(hidden), int(hidden.stride(0)), rp, _ptr(weight), int(weight.stride(0)),
+        check(load().ns_lm_head_bf16(_ptr(hidden), int(hidden.stride(0)), int(hidden.shape[0]), rp, _ptr(weight),
+                                     int(weight.stride(0)),
                                      _ptr(out), int(out.stride(0)), m, n, k, sh))
     return out
 

@@ -51,6 +51,8 @@ struct LmParams {
   const uint16_t* hidden;   // (rows of the hidden tensor, ldh) bf16
   int64_t ldh;
   const int64_t* rows;      // [m] hidden row of each logits row, or NULL: row r
+  int64_t n_hidden;         // rows of the hidden tensor: a gathered index outside [0, n_hidden)
+                            // reads row 0 and its logits row is written as NaN
   const uint16_t* weight;   // (n, ldw) bf16: out_features x in_features; or the packed tiles
   int64_t ldw;              // (0 for the packed layout)
   uint16_t* logits;         // (m, ldl) bf16
@@ -140,7 +142,8 @@ __global__ __launch_bounds__(LM_THREADS, 1) void lm_head_kernel(const LmParams P
   for (int j = 0; j < LM_AL; ++j) {
     int r = m0 + tr + 64 * j;
     r = r < P.m ? r : P.m - 1;
-    const int64_t hr = P.rows != nullptr ? P.rows[r] : (int64_t)r;
+    int64_t hr = P.rows != nullptr ? P.rows[r] : (int64_t)r;
+    hr = hr >= 0 && hr < P.n_hidden ? hr : 0;
     asrc[j] = P.hidden + hr * P.ldh + tp * 8;
   }
 
@@ -215,7 +218,21 @@ __global__ __launch_bounds__(LM_THREADS, 1) void lm_head_kernel(const LmParams P
   for (int d = 0; d < D - 1; ++d)
     if (st + d < nst) stage(st + d, d);
 
-  // 32 x 32 accumulator layout: lane l, element e -> column l % 32, row 8 (e / 4) + 4 (l / 32) + e % 4
+  // 32 x 32 accumulator layout: lane l, element e -> column l % 32, row 8 (e / 4) + 4 (l / 32) + e % 4.
+  // Rows whose gathered index lies outside the hidden tensor are written as NaN.
+  uint32_t bad = 0u;
+  if (P.rows != nullptr) {
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const int row = mw + 32 * i + 8 * (e >> 2) + 4 * h + (e & 3);
+        if (row < P.m) {
+          const int64_t hr = P.rows[row];
+          if (hr < 0 || hr >= P.n_hidden) bad |= 1u << (i * 16 + e);
+        }
+      }
+  }
 #pragma unroll
   for (int i = 0; i < 2; ++i)
 #pragma unroll
@@ -224,7 +241,9 @@ __global__ __launch_bounds__(LM_THREADS, 1) void lm_head_kernel(const LmParams P
 #pragma unroll
       for (int e = 0; e < 16; ++e) {
         const int row = mw + 32 * i + 8 * (e >> 2) + 4 * h + (e & 3);
-        if (row < P.m && col < P.n) P.logits[(int64_t)row * P.ldl + col] = lm_bf16_rne(acc[i][j][e]);
+        if (row < P.m && col < P.n)
+          P.logits[(int64_t)row * P.ldl + col] =
+              ((bad >> (i * 16 + e)) & 1u) ? (uint16_t)0x7fc0u : lm_bf16_rne(acc[i][j][e]);
       }
     }
 }

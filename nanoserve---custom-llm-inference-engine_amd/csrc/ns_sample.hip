@@ -1284,15 +1284,17 @@ static int lm_check(const void* hidden, int64_t ld_hidden, const void* weight, i
   return NS_OK;
 }
 
-static int lm_launch(const void* hidden, int64_t ld_hidden, const int64_t* rows, const void* weight, int64_t ld_weight,
-                     void* logits, int64_t ld_logits, int32_t m, int32_t n, int32_t k, bool packed,
+static int lm_launch(const void* hidden, int64_t ld_hidden, int64_t n_hidden, const int64_t* rows, const void* weight,
+                     int64_t ld_weight, void* logits, int64_t ld_logits, int32_t m, int32_t n, int32_t k, bool packed,
                      hipStream_t stream) {
+  if (n_hidden <= 0) return fail(NS_ERR_INVALID, "n_hidden must be positive");
+  if (rows == nullptr && n_hidden < m) return fail(NS_ERR_INVALID, "n_hidden < m without rows");
   // waves along the batch: the fewest that hold it (64 rows each), so small batches keep every
   // wave on products; batches beyond 256 rows take several workgroup rows
   const int wm = m <= 64 ? 1 : m <= 128 ? 2 : 4;
   const int64_t gy = ((int64_t)m + 64 * wm - 1) / (64 * wm);
   if (gy > 65535) return fail(NS_ERR_INVALID, "m too large");
-  ns::LmParams P{static_cast<const uint16_t*>(hidden), ld_hidden, rows, static_cast<const uint16_t*>(weight),
+  ns::LmParams P{static_cast<const uint16_t*>(hidden), ld_hidden, rows, n_hidden, static_cast<const uint16_t*>(weight),
                  packed ? 0 : ld_weight, static_cast<uint16_t*>(logits), ld_logits, m, n, k};
   const dim3 grid((unsigned)((n + ns::LM_NT - 1) / ns::LM_NT), (unsigned)gy), block(ns::LM_THREADS);
   if (packed) {
@@ -1309,13 +1311,13 @@ static int lm_launch(const void* hidden, int64_t ld_hidden, const int64_t* rows,
   return NS_OK;
 }
 
-int ns_lm_head_bf16(const void* hidden, int64_t ld_hidden, const int64_t* rows, const void* weight,
+int ns_lm_head_bf16(const void* hidden, int64_t ld_hidden, int64_t n_hidden, const int64_t* rows, const void* weight,
                     int64_t ld_weight, void* logits, int64_t ld_logits, int32_t m, int32_t n, int32_t k,
                     hipStream_t stream) {
   const int rc = lm_check(hidden, ld_hidden, weight, ld_weight, logits, ld_logits, m, n, k, false);
   if (rc != NS_OK) return rc;
   if (m == 0 || n == 0) return NS_OK;
-  return lm_launch(hidden, ld_hidden, rows, weight, ld_weight, logits, ld_logits, m, n, k, false, stream);
+  return lm_launch(hidden, ld_hidden, n_hidden, rows, weight, ld_weight, logits, ld_logits, m, n, k, false, stream);
 }
 
 int ns_lm_head_packed_bytes(int32_t n, int32_t k, uint64_t* bytes) {
@@ -1344,7 +1346,7 @@ int ns_lm_head_pack_bf16(const void* weight, int64_t ld_weight, int32_t n, int32
   return NS_OK;
 }
 
-int ns_lm_head_bf16_packed(const void* hidden, int64_t ld_hidden, const int64_t* rows, const void* packed,
+int ns_lm_head_bf16_packed(const void* hidden, int64_t ld_hidden, int64_t n_hidden, const int64_t* rows, const void* packed,
                            uint64_t packed_bytes, void* logits, int64_t ld_logits, int32_t m, int32_t n, int32_t k,
                            hipStream_t stream) {
   int rc = lm_check(hidden, ld_hidden, packed, 0, logits, ld_logits, m, n, k, true);
@@ -1354,7 +1356,7 @@ int ns_lm_head_bf16_packed(const void* hidden, int64_t ld_hidden, const int64_t*
   if (rc != NS_OK) return rc;
   if (packed_bytes != want) return fail(NS_ERR_INVALID, "packed_bytes does not match the packed layout of (n, k)");
   if (m == 0 || n == 0) return NS_OK;
-  return lm_launch(hidden, ld_hidden, rows, packed, 0, logits, ld_logits, m, n, k, true, stream);
+  return lm_launch(hidden, ld_hidden, n_hidden, rows, packed, 0, logits, ld_logits, m, n, k, true, stream);
 }
 
 const char* ns_last_error(void) { return g_err.c_str(); }

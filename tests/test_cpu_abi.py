@@ -149,22 +149,24 @@ def test_lm_head_argument_errors():
     lib = L.load()
     f = lib.ns_lm_head_bf16
     h, w, o = 4096, 8192, 12288    # 16-byte aligned stand-in addresses (never dereferenced)
-    assert f(None, 64, None, w, 64, o, 64, 1, 1, 64, None) == 1 and "NULL" in L.last_error()
-    assert f(h, 128, None, w, 128, o, 64, 1, 1, 100, None) == 1 and "multiple of 64" in L.last_error()
-    assert f(h, 60, None, w, 128, o, 64, 1, 1, 64, None) == 1 and "ld_hidden" in L.last_error()
-    assert f(h, 64, None, w, 64, o, 4, 1, 8, 64, None) == 1 and "ld_logits" in L.last_error()
-    assert f(h + 8, 64, None, w, 64, o, 64, 1, 1, 64, None) == 2 and "aligned" in L.last_error()   # NS_ERR_ALIGN
-    assert f(h, 64, None, w, 64, o, 64, -1, 1, 64, None) == 1
-    assert f(h, 64, None, w, 1 << 24, o, 64, 1, 1, 64, None) == 1 and "ld_weight" in L.last_error()
-    assert f(h, 64, None, w, 64, o, 64, 0, 5, 64, None) == 0      # nothing to compute
-    assert f(h, 64, None, w, 64, o, 64, 3, 0, 64, None) == 0
+    assert f(None, 64, 4, None, w, 64, o, 64, 1, 1, 64, None) == 1 and "NULL" in L.last_error()
+    assert f(h, 128, 4, None, w, 128, o, 64, 1, 1, 100, None) == 1 and "multiple of 64" in L.last_error()
+    assert f(h, 60, 4, None, w, 128, o, 64, 1, 1, 64, None) == 1 and "ld_hidden" in L.last_error()
+    assert f(h, 64, 4, None, w, 64, o, 4, 1, 8, 64, None) == 1 and "ld_logits" in L.last_error()
+    assert f(h + 8, 64, 4, None, w, 64, o, 64, 1, 1, 64, None) == 2 and "aligned" in L.last_error()   # NS_ERR_ALIGN
+    assert f(h, 64, 4, None, w, 64, o, 64, -1, 1, 64, None) == 1
+    assert f(h, 64, 4, None, w, 1 << 24, o, 64, 1, 1, 64, None) == 1 and "ld_weight" in L.last_error()
+    assert f(h, 64, 4, None, w, 64, o, 64, 0, 5, 64, None) == 0      # nothing to compute
+    assert f(h, 64, 4, None, w, 64, o, 64, 3, 0, 64, None) == 0
     nb = ctypes.c_uint64(0)
     assert lib.ns_lm_head_packed_bytes(128256, 2048, ctypes.byref(nb)) == 0
     assert nb.value == 501 * 32 * 256 * 64 * 2          # 256-row blocks x 64-wide stages x 32 KB
     assert lib.ns_lm_head_packed_bytes(257, 64, ctypes.byref(nb)) == 0 and nb.value == 2 * 32768
     assert lib.ns_lm_head_packed_bytes(10, 100, ctypes.byref(nb)) == 1
     assert lib.ns_lm_head_pack_bf16(None, 64, 10, 64, h, None) == 1 and "NULL" in L.last_error()
-    assert lib.ns_lm_head_bf16_packed(h, 64, None, w, 32768, o, 64, 1, 1, 65, None) == 1
+    assert lib.ns_lm_head_bf16_packed(h, 64, 4, None, w, 32768, o, 64, 1, 1, 65, None) == 1
     # a buffer packed for another shape is refused before any launch
-    assert lib.ns_lm_head_bf16_packed(h, 64, None, w, 32768, o, 300, 1, 300, 64, None) == 1
+    assert lib.ns_lm_head_bf16_packed(h, 64, 4, None, w, 32768, o, 300, 1, 300, 64, None) == 1
     assert "packed_bytes" in L.last_error()
+    assert f(h, 64, 0, None, w, 64, o, 64, 1, 1, 64, None) == 1 and "n_hidden" in L.last_error()
+    assert f(h, 64, 2, None, w, 64, o, 64, 3, 1, 64, None) == 1 and "n_hidden" in L.last_error()

@@ -83,6 +83,20 @@ def test_lm_head_gathers_rows_and_strides(device):
     assert bool((out_full[:, 3000:] == 7.0).all())   # nothing written past n
 
 
+def test_gather_index_out_of_range_gives_nan_row(device):
+    """A gathered index outside the hidden tensor reads nothing out of bounds: its logits
+    row is NaN (the sampler then reports a NaN row) and the other rows are unaffected."""
+    hidden, weight = make(device, 40, 700, 128, seed=21)
+    rows = torch.tensor([3, -1, 39, 40, 1 << 40, 7], dtype=torch.int64, device=device)
+    for w in (weight, L.PackedLmHead(weight)):
+        out = L.lm_head_bf16(hidden, w, rows=rows).float()
+        torch.cuda.synchronize()
+        bad = torch.tensor([False, True, False, True, True, False], device=device)
+        assert bool(torch.isnan(out[bad]).all())
+        good = rows[~bad]
+        check(out[~bad].to(torch.bfloat16), hidden, weight, rows=good)
+
+
 def test_lm_head_special_values(device):
     """Inf and NaN inputs propagate as in IEEE arithmetic; large values round to inf."""
     hidden, weight = make(device, 4, 256, 64, seed=5)
