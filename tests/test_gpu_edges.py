@@ -79,3 +79,44 @@ def test_empty_batch(device):
                  sample_idx=torch.zeros(0, dtype=torch.int64, device=device))
     torch.cuda.synchronize()
     assert int(out[0]) == -7
+
+
+@pytest.mark.parametrize("path", list(PATHS))
+def test_invalid_rows_and_history_ids_are_reported(device, path):
+    """A sample index outside the logits tensor gives id -1 with PATH_ERROR and FLAG_BAD_ROW
+    (no read out of bounds); history ids outside [0, V) are ignored and flagged
+    (FLAG_BAD_HIST_ID), and the row samples as the oracle does without them."""
+    V, N = 1000, 6
+    rng = np.random.default_rng(95)
+    flat = (rng.standard_normal((N, V), dtype=np.float32) * 3.0).astype(np.float32)
+    sidx = np.array([0, -1, 5, 6, 2], dtype=np.int64)
+    B = len(sidx)
+    hists = [[1, 2], [3], [-5, 10, V + 3, 20], [4], []]
+    offs = np.zeros(B + 1, dtype=np.int32)
+    offs[1:] = np.cumsum([len(h) for h in hists])
+    ids = np.array([i for h in hists for i in h], dtype=np.int32)
+    t = torch.full((B,), 1.0, device=device)
+    k = torch.full((B,), 50, dtype=torch.int32, device=device)
+    p = torch.full((B,), 0.9, device=device)
+    pen = torch.full((B,), 1.2, device=device)
+    u_np = rng.random(B, dtype=np.float32)
+    u = torch.from_numpy(u_np).to(device)
+    out = torch.full((B,), -7, dtype=torch.int64, device=device)
+    info = torch.zeros((B, L.NS_INFO_WORDS), dtype=torch.int32, device=device)
+    ws, mode = PATHS[path]
+    print(f"[edges] invalid rows path={path}", flush=True)
+    L.sample_raw(torch.from_numpy(flat).to(device), t, k, p, pen, u, out,
+                 sample_idx=torch.from_numpy(sidx).to(device),
+                 hist_offsets=torch.from_numpy(offs).to(device), hist_ids=torch.from_numpy(ids).to(device),
+                 max_hist=4, out_info=info, workspace=ws, mode=mode)
+    torch.cuda.synchronize()
+    g, inf = out.cpu().numpy(), info.cpu().numpy()
+    for r in (1, 3):
+        assert g[r] == -1 and inf[r][0] == 9 and (inf[r][5] & 4), (r, g[r], inf[r].tolist())
+    assert inf[2][5] & 1, inf[2].tolist()
+    good = [0, 2, 4]
+    clean = [[1, 2], [10, 20], []]
+    r = O.sample(flat[sidx[good]], np.ones(3), np.full(3, 50), np.full(3, 0.9), np.full(3, 1.2),
+                 [np.asarray(h, dtype=np.int32) for h in clean], u_np[good])
+    for j, row in enumerate(good):
+        assert g[row] == r.ids[j] or r.exempt[j], (row, g[row], r.ids[j])
