@@ -192,20 +192,33 @@ def aligned_rows(logits, sample_idx):
     rows (NS_ERR_ALIGN).  Vocabularies whose row size is not a multiple of 16
     bytes (an odd fp32 vocab such as 50257) and misaligned views are copied
     here into rows padded to a multiple of 16 bytes: only the sampled rows
-    when ``sample_idx`` is given (which then becomes the identity).  Aligned
-    inputs, every vocab used by the benchmarks among them, are passed through.
+    when ``sample_idx`` is given.  The gather reads clamped indices, so an
+    index outside the tensor reads nothing out of bounds; the returned
+    ``sample_idx`` is the identity for valid rows and -1 for the others, which
+    the kernels report as bad rows (id -1) as they do without the copy.
+    Aligned inputs, every vocab used by the benchmarks among them, are passed
+    through.
     """
     import torch
 
     esz = logits.element_size()
     if logits.data_ptr() % 16 == 0 and (logits.stride(0) * esz) % 16 == 0:
         return logits, sample_idx
-    rows = logits if sample_idx is None else logits.index_select(0, sample_idx.to(torch.int64))
+    new_idx = None
+    if sample_idx is None:
+        rows = logits
+    else:
+        n = int(logits.shape[0])
+        idx = sample_idx.to(torch.int64)
+        valid = (idx >= 0) & (idx < n)
+        rows = logits.index_select(0, idx.clamp(0, max(n - 1, 0)))
+        new_idx = torch.where(valid, torch.arange(idx.numel(), device=idx.device, dtype=torch.int64),
+                              torch.full_like(idx, -1))
     V = int(rows.shape[1])
     per = 16 // esz
     padded = torch.empty((int(rows.shape[0]), (V + per - 1) // per * per), dtype=rows.dtype, device=rows.device)
     padded[:, :V].copy_(rows)
-    return padded[:, :V], None
+    return padded[:, :V], new_idx
 
 
 def sample_raw(logits, temperature, top_k, top_p, rep_penalty, uniforms, out_ids, *, sample_idx=None,

@@ -1149,6 +1149,7 @@ __global__ __launch_bounds__(256) void hist_assign_kernel(int32_t* lens, int32_t
 
 // Row r's sampled token joins slot slots[r] (scheduler.py:281-284 appending to
 // output_token_ids).  One thread per row; the rows of a call name distinct slots.
+// A row that failed (id -1: a sample index outside the logits) appends nothing.
 __global__ __launch_bounds__(256) void hist_append_kernel(int32_t* lens, int32_t* ids, int32_t nslots, int32_t cap,
                                                           const int32_t* slots, const int64_t* tok, int32_t n,
                                                           int32_t* overflow) {
@@ -1156,12 +1157,14 @@ __global__ __launch_bounds__(256) void hist_append_kernel(int32_t* lens, int32_t
   if (r >= n) return;
   const int32_t s = slots[r];
   if (s < 0 || s >= nslots) return;
+  const int64_t t = tok[r];
+  if (t < 0) return;
   const int32_t l = lens[s];
   if (l < 0 || l >= cap) {
     if (overflow != nullptr) atomicAdd(overflow, 1);
     return;
   }
-  ids[(int64_t)s * cap + l] = (int32_t)tok[r];
+  ids[(int64_t)s * cap + l] = (int32_t)t;
   lens[s] = l + 1;
 }
 

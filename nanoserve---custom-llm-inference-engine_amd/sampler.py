@@ -207,10 +207,14 @@ class DeviceHistories:
     def slots(self, request_ids: Sequence) -> np.ndarray:
         return np.fromiter((self._slot[r] for r in request_ids), dtype=np.int32, count=len(request_ids))
 
-    def _appended(self, slots: np.ndarray) -> None:
+    def _check_room(self, slots: np.ndarray) -> None:
+        """Raise before any launch if a slot cannot take one more token."""
         full = self._len[slots] >= self.capacity
         if full.any():
             raise RuntimeError(f"history slot {int(slots[full][0])} is full ({self.capacity} tokens)")
+
+    def _appended(self, slots: np.ndarray) -> None:
+        """Count one appended token per slot, once the append has been issued."""
         self._len[slots] += 1
 
 
@@ -263,8 +267,8 @@ class Sampler:
             slots = device_histories.slots(history_requests)
             if len(set(slots.tolist())) != B:
                 raise ValueError("history_requests must name each request at most once")
-            device_histories._appended(slots)   # checked before any launch; counted for the next call
-            max_hist = int((device_histories._len[slots] - 1).max()) if B else 0
+            device_histories._check_room(slots)   # before any launch; counted once the append is issued
+            max_hist = int(device_histories._len[slots].max()) if B else 0
             packed = PackedRows(sampling_params_list, None, V, slots=slots, slot_max_hist=max_hist)
         else:
             packed = PackedRows(sampling_params_list, history_token_ids, V)
@@ -289,6 +293,7 @@ class Sampler:
                             hist_state=hs, hist_slot=d["hist_slot"])
             if hs is not None:
                 hs.append(d["hist_slot"], out)
+                device_histories._appended(slots)
         res = self._readback(out) if async_ids else out
         return (res, probs) if return_probs else res
 

@@ -257,6 +257,27 @@ def make_workload(cfg: int, batch: Optional[int] = None) -> Workload:
                     n_rows_total=n_total, sample_indices=sample_idx, filler_seed=77_000 + cfg, notes=notes)
 
 
+def make_mixed_decode(batch: int = 256, seed: int = 1005) -> Workload:
+    """A decode batch of bf16 rows (N(0, 3^2) rounded to bf16, vocab 128256) with the
+    mixed per-row parameters of configuration 1 (greedy, top-k off and k > 64 among
+    them) and 512 Zipf history ids per row: a batch large enough for the
+    one-workgroup-per-row launch that still holds rows with top-k off or k > 64."""
+    children = np.random.SeedSequence(seed).spawn(len(STREAMS))
+    r = {name: np.random.Generator(np.random.PCG64(c)) for name, c in zip(STREAMS, children)}
+    V = VOCAB_LLAMA32
+    raw = r["logits"].normal(0.0, 3.0, size=(batch, V)).astype(np.float32)
+    bf16 = f32_to_bf16_bits(raw)
+    rows = bf16_bits_to_f32(bf16)
+    t, k, p, pen = _mixed_params(r["params"], batch)
+    perm = r["hist"].permutation(V)
+    hists = [zipf_ids(r["hist"], 512, V, perm) for _ in range(batch)]
+    u = r["uniform"].random(batch, dtype=np.float32)
+    return Workload(name=f"mixed-bf16-b{batch}", vocab=V, rows=rows, bf16_bits=bf16,
+                    temperature=np.asarray(t, np.float64), top_k=np.asarray(k, np.int64),
+                    top_p=np.asarray(p, np.float64), repetition_penalty=np.asarray(pen, np.float64),
+                    histories=hists, uniforms=u, n_rows_total=batch)
+
+
 def algorithmic_bytes(w: Workload) -> int:
     """Compulsory HBM bytes of one sampler call over ``w``.
 

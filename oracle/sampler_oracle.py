@@ -35,11 +35,26 @@ implementation whose probabilities differ from these in the last ulps:
   ``zone_ids`` lists the token ids at positions ``zone_lo+1 .. zone_hi`` (empty
   when the cut is unambiguous) and ``zone_mass`` their probability mass.
 * ``topp_boundary``: the zone carries more than 1e-5 of mass (one heavy token
-  sits on the cut), so the kept set itself is ambiguous: the row is exempt.
-* ``draw_boundary``: ``u`` lies within ``1e-6 + zone_mass`` of the cumulative
-  mass on either side of the picked token.
+  sits on the cut), so the kept set itself is ambiguous.
+* ``allowed_ids``: every token id an implementation may return for the row.
+  An implementation whose kept set differs from this one only inside the zone
+  renormalises by ``Q'`` instead of ``Q`` (kept masses, both at least
+  ``Qmin``, the sorted prefix mass at ``zone_lo``), so each of its id-order
+  cumulative masses lies within ``2 * zone_mass / Qmin`` of the oracle's
+  (``zone_mass / Qmin`` from the rescaling of the kept tokens, as much again
+  from the zone tokens themselves).  With ``draw_eps = 1e-6 + 2 * zone_mass /
+  Qmin`` (just 1e-6 on rows without a zone), the allowed ids are the kept or
+  zone tokens ``t`` with ``C[t-1] - draw_eps <= u < C[t] + draw_eps``, ``C``
+  the oracle's float64 cumulative mass in token-id order.  For a row with no
+  boundary within ``draw_eps`` of ``u`` that is exactly the oracle's pick.
+* ``draw_boundary``: ``u`` lies within 1e-6 of the cumulative mass on either
+  side of the picked token (the north-star exemption); ``draw_zone``: more
+  than one id is allowed only because of the zone's widening.
+* ``renorm``: ``zone_mass / Qmin``, the relative change of every kept
+  probability an implementation may show on a row with a zone.
 * ``topp_tie_straddle``: tied values straddle the top-p cut.  The GPU path and
-  this oracle agree there (lower id first); the reference's unstable sort may not.
+  this oracle agree there (lower id first), and so does ``torch.sort`` on the
+  GPU, which the reference runs on (stable on ties, measured on ROCm torch).
 
 Pinned by tests/test_oracle_pins.py against closed forms (numpy float32
 penalty and temperature, ``np.partition`` top-k, a numpy stable-argsort top-p,
@@ -82,12 +97,18 @@ class OracleResult:
     nan_row: np.ndarray           # (B,) bool, probabilities replaced by 1/V (sampler.py:77-80)
     topp_boundary: np.ndarray     # (B,) bool
     topp_tie_straddle: np.ndarray # (B,) bool
-    draw_boundary: np.ndarray     # (B,) bool
+    draw_boundary: np.ndarray     # (B,) bool, u within 1e-6 of a cumulative mass next to the pick
+    draw_zone: np.ndarray         # (B,) bool, several ids allowed only through the zone's widening
+    kept_mass: np.ndarray         # (B,) float64 top-p kept prefix mass (1 when top-p is off)
+    renorm: np.ndarray            # (B,) float64 zone_mass / Qmin (0 without a zone)
+    draw_eps: np.ndarray          # (B,) float64 the row's boundary band
+    allowed_ids: list             # B int64 arrays: the ids an implementation may return
 
     @property
     def exempt(self) -> np.ndarray:
-        """Rows whose token id may legitimately differ between implementations."""
-        return (self.topp_boundary | self.draw_boundary) & ~self.greedy
+        """Rows where more than one token id is allowed (never greedy rows)."""
+        n = np.array([len(a) for a in self.allowed_ids], dtype=np.int64)
+        return (n > 1) & ~self.greedy
 
 
 def effective_temperature(t: float) -> float:
@@ -144,6 +165,8 @@ def sample(rows, temperature, top_k, top_p, repetition_penalty, histories, unifo
     zone_ids = [np.zeros(0, dtype=np.int64) for _ in range(B)]
     topp_boundary = np.zeros(B, dtype=bool)
     tie_straddle = np.zeros(B, dtype=bool)
+    kept_mass = np.ones(B, dtype=np.float64)
+    qmin = np.ones(B, dtype=np.float64)
     for i, p in enumerate(top_p):
         if p < 1.0:
             sorted_logits, sorted_idx = torch.sort(logits[i], descending=True, stable=True)
@@ -166,6 +189,8 @@ def sample(rows, temperature, top_k, top_p, repetition_penalty, histories, unifo
                 zone_mass[i] = c64[hi] - c64[lo]
                 zone_ids[i] = sorted_idx[lo + 1:hi + 1].numpy().astype(np.int64)
                 topp_boundary[i] = zone_mass[i] > ZONE_MASS_MAX
+                kept_mass[i] = c64[J]
+                qmin[i] = c64[lo]
             if J + 1 < V and bool(torch.isfinite(sorted_logits[J])):
                 tie_straddle[i] = bool(sorted_logits[J + 1] == sorted_logits[J])
             remove_sorted[..., 1:] = remove_sorted[..., :-1].clone()
@@ -183,32 +208,58 @@ def sample(rows, temperature, top_k, top_p, repetition_penalty, histories, unifo
 
     # sampler.py:82-83 (greedy) and the inverse-CDF draw replacing sampler.py:87
     argmax = torch.argmax(logits, dim=-1).numpy()
-    cdf = probs.double().cumsum(-1).numpy()
     pnp = probs.numpy()
+    nan_np = nan_rows.numpy()
     ids = np.empty(B, dtype=np.int64)
     draw_boundary = np.zeros(B, dtype=bool)
+    draw_zone = np.zeros(B, dtype=bool)
+    renorm = np.zeros(B, dtype=np.float64)
+    draw_eps = np.full(B, BOUNDARY_EPS, dtype=np.float64)
+    allowed = [np.zeros(0, dtype=np.int64) for _ in range(B)]
     for i in range(B):
         if greedy[i]:
             ids[i] = int(argmax[i])
+            allowed[i] = np.array([ids[i]], dtype=np.int64)
             continue
+        cdf = pnp[i].astype(np.float64).cumsum()
         ui = float(u[i])
-        j = int(np.searchsorted(cdf[i], ui, side="right"))
+        j = int(np.searchsorted(cdf, ui, side="right"))
         if j >= V:
             nz = np.flatnonzero(pnp[i] > 0)
             j = int(nz[-1]) if nz.size else V - 1
         ids[i] = j
-        eps = BOUNDARY_EPS + zone_mass[i]
-        near = abs(cdf[i, j] - ui) < eps
+        near = abs(cdf[j] - ui) < BOUNDARY_EPS
         if j > 0:
-            near = near or abs(cdf[i, j - 1] - ui) < eps
+            near = near or abs(cdf[j - 1] - ui) < BOUNDARY_EPS
         draw_boundary[i] = near
+        if zone_mass[i] > 0.0:
+            renorm[i] = zone_mass[i] / max(qmin[i], 1e-300)
+            draw_eps[i] = BOUNDARY_EPS + 2.0 * renorm[i]
+        eps = draw_eps[i]
+        # kept or zone tokens t with C[t-1] - eps <= u < C[t] + eps (C[-1] = 0)
+        a = int(np.searchsorted(cdf, ui - eps, side="right"))
+        b = min(int(np.searchsorted(cdf, ui + eps, side="right")), V - 1)
+        if a <= b:
+            if nan_np[i]:
+                cand = np.arange(a, b + 1, dtype=np.int64)
+            else:
+                keep = np.isfinite(masked[i, a:b + 1].numpy())
+                cand = np.flatnonzero(keep).astype(np.int64) + a
+                z = zone_ids[i]
+                if len(z):
+                    cand = np.union1d(cand, z[(z >= a) & (z <= b)])
+        else:
+            cand = np.zeros(0, dtype=np.int64)
+        allowed[i] = np.union1d(cand, np.array([j], dtype=np.int64)).astype(np.int64)
+        draw_zone[i] = len(allowed[i]) > 1 and not near
 
     n_kept = torch.isfinite(masked).sum(-1).numpy().astype(np.int64)
     return OracleResult(ids=ids, probs=probs, penalized=penalized, scaled=scaled, masked=masked,
                         greedy=greedy, topk_thr=topk_thr, n_kept_topk=n_kept_topk, n_kept=n_kept,
                         topp_cut=topp_cut, zone_lo=zone_lo, zone_hi=zone_hi, zone_mass=zone_mass,
-                        zone_ids=zone_ids, nan_row=nan_rows.numpy(), topp_boundary=topp_boundary,
-                        topp_tie_straddle=tie_straddle, draw_boundary=draw_boundary)
+                        zone_ids=zone_ids, nan_row=nan_np, topp_boundary=topp_boundary,
+                        topp_tie_straddle=tie_straddle, draw_boundary=draw_boundary, draw_zone=draw_zone,
+                        kept_mass=kept_mass, renorm=renorm, draw_eps=draw_eps, allowed_ids=allowed)
 
 
 def sample_workload(w, rows_slice=None) -> OracleResult:

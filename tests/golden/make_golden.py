@@ -2,16 +2,20 @@
 
     python tests/golden/make_golden.py
 
-configs.json -- for each workload (c0, c1, c2, c3 at 32 rows, c4): the SHA-256
-digest of the generated inputs (so a run can confirm it regenerated identical
-logits, parameters, histories and uniforms) and, per sampled row, the oracle's
-token id, top-k threshold bits, kept counts and exemption flags.
+configs.json -- for each workload (c0-c4 at their full sizes, and a bf16 decode
+batch of 256 rows with mixed parameters): the SHA-256 digest of the generated
+inputs (so a run can confirm it regenerated identical logits, parameters,
+histories and uniforms) and, per sampled row, the oracle's token id, the ids an
+implementation may return (the oracle's pick alone unless the uniform lies
+within the row's band of a cumulative-mass boundary), top-k threshold bits,
+kept counts, the ambiguous top-p zone and its renormalisation bound.
 
 tiny_cases.json -- small hand-built rows with their full inputs and expected
 outputs (token id, threshold, kept counts, final probabilities): ties at the
 top-k threshold and across the top-p cut, penalties below and above 1 with
-duplicate history ids, NaN / +inf / -inf logits, greedy rows, temperatures
-below 1e-6 and negative, top_p <= 0, top_k >= V.
+duplicate history ids, NaN / +inf / -inf logits, rows entirely -inf (greedy
+and sampled), greedy rows holding +inf, temperatures below 1e-6 and negative,
+top_p <= 0, top_k >= V.
 
 The reference ships no tests, golden vectors or fixtures of its own; these
 fixtures pin the kernels and the oracle to one another across changes, and the
@@ -32,7 +36,7 @@ sys.path.insert(0, ROOT)
 W = importlib.import_module("nanoserve---custom-llm-inference-engine_amd.workloads")
 from oracle import sampler_oracle as O  # noqa: E402
 
-CONFIGS = ((0, None), (1, None), (2, None), (3, 32), (4, None))
+CONFIGS = ((0, None), (1, None), (2, None), (3, None), (4, None), ("mixed", 256))
 
 
 def f32_bits(x) -> int:
@@ -48,6 +52,9 @@ def row_records(r) -> list:
             "n_kept_topk": int(r.n_kept_topk[i]),
             "n_kept": int(r.n_kept[i]),
             "zone": int(len(r.zone_ids[i])),
+            "zone_ids": [int(v) for v in r.zone_ids[i]],
+            "renorm": float(r.renorm[i]),
+            "allowed": [int(v) for v in r.allowed_ids[i]],
             "greedy": bool(r.greedy[i]),
             "nan_row": bool(r.nan_row[i]),
             "exempt": bool(r.exempt[i]),
@@ -58,7 +65,7 @@ def row_records(r) -> list:
 def make_configs() -> dict:
     res = {}
     for cfg, batch in CONFIGS:
-        w = W.make_workload(cfg, batch=batch)
+        w = W.make_mixed_decode(batch) if cfg == "mixed" else W.make_workload(cfg, batch=batch)
         r = O.sample_workload(w)
         res[w.name] = {"cfg": cfg, "batch_arg": batch, "batch": w.batch, "vocab": w.vocab, "dtype": w.dtype,
                        "digest": w.digest(), "rows": row_records(r)}
@@ -102,6 +109,23 @@ def tiny_cases() -> list:
     x[4, 20] = np.nan
     group("special", x, [1.0, 1.0, 0.8, 1.0, 0.0], [0, 5, 0, 4, 0], [0.9, 1.0, 0.7, 1.0, 1.0], 1.0,
           [[]] * 5, [0.3, 0.6, 0.45, 0.2, 0.8])
+    # rows entirely -inf (the NaN guard for sampled rows, index 0 for greedy ones), with and
+    # without a penalty; greedy rows holding +inf (first +inf wins, a penalty keeps it);
+    # a sampled row holding +inf (NaN softmax); a greedy row of -inf and one NaN
+    V = 40
+    x = np.full((8, V), -np.inf, dtype=np.float32)
+    x[3] = np.round(rng.normal(0, 1, size=V), 3)
+    x[3, 17] = np.inf
+    x[3, 30] = np.inf
+    x[4] = np.round(rng.normal(0, 1, size=V), 3)
+    x[4, 9] = np.inf
+    x[5] = np.round(rng.normal(0, 1, size=V), 3)
+    x[5, 3] = np.inf
+    x[6, 22] = np.nan
+    x[7, 11] = -3.5
+    group("allinf", x, [1.0, 0.0, 0.7, 0.0, 0.0, 1.0, 0.0, 1.0], [0, 0, 5, 0, 0, 10, 0, 1],
+          [1.0, 1.0, 0.9, 1.0, 1.0, 0.95, 1.0, 1.0], [1.0, 1.0, 1.2, 1.0, 1.3, 1.0, 1.0, 1.5],
+          [[], [], [1, 2, 39], [], [9, 9, 20], [], [], [11]], [0.37, 0.5, 0.99, 0.1, 0.2, 0.61, 0.3, 0.8])
     # temperature edge cases and top_p <= 0 (keeps exactly one token), top_k >= V (off)
     V = 257
     x = np.round(rng.normal(0, 3, size=(6, V)), 1).astype(np.float32)

@@ -44,4 +44,6 @@ def tiny_workload(case) -> "W.Workload":
 
 
 def config_workload(rec) -> "W.Workload":
+    if rec["cfg"] == "mixed":
+        return W.make_mixed_decode(int(rec["batch_arg"]))
     return W.make_workload(int(rec["cfg"]), batch=rec["batch_arg"])

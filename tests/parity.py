@@ -1,13 +1,17 @@
 """Parity harness: run the HIP sampler through its C ABI and compare with the oracle.
 
-The comparison bar (per sampled row):
-  * token ids bit-exact, except rows the oracle marks exempt: the uniform lies
-    within ``1e-6 + zone_mass`` of a cumulative-mass boundary next to the pick,
-    or more than 1e-5 of probability sits in the ambiguous top-p zone;
-  * greedy rows: ids bit-exact with no exemption;
+The comparison bar (per sampled row, every row checked):
+  * the token id must be one of the oracle's allowed ids for the row: the
+    oracle's own pick, plus, where the uniform lies within the row's band
+    (1e-6, widened on rows with an ambiguous top-p zone by twice the zone's
+    renormalisation bound) of a cumulative-mass boundary, the kept or zone
+    tokens whose float64 CDF interval lies within that band of the uniform;
+  * greedy rows: ids bit-exact, no exemption;
   * the top-k threshold (scaled logit of the k-th largest) bit-exact;
-  * final probabilities within 1e-5 relative (plus a 1e-12 absolute floor),
-    tokens of the ambiguous top-p zone excepted;
+  * final probabilities within 1e-5 relative (plus a 1e-12 absolute floor) on
+    every sampled row, NaN-guarded and top-p-boundary rows included; tokens of
+    the ambiguous top-p zone are masked and, on rows with a zone, the
+    tolerance grows by the zone's renormalisation bound ``renorm``;
   * kept-token count equal up to the size of the zone.
 """
 from __future__ import annotations
@@ -22,8 +26,11 @@ L = pkg("_lib")
 S = pkg("sampler")
 C = pkg("config")
 
-# kernel modes under test: path name -> (workspace, mode)
-PATHS = {"segmented": ("auto", L.NS_MODE_SEGMENTED), "per-row": (None, L.NS_MODE_PER_ROW)}
+# kernel modes under test: path name -> (workspace, mode).  "shipped" is what
+# Sampler.sample launches: AUTO mode, the cached workspace and the row-kind hint
+# of the call's parameters (run_gpu passes it for that path).
+PATHS = {"segmented": ("auto", L.NS_MODE_SEGMENTED), "per-row": (None, L.NS_MODE_PER_ROW),
+         "shipped": ("auto", L.NS_MODE_AUTO)}
 
 PROB_RTOL = 1e-5
 PROB_ATOL = 1e-12
@@ -34,14 +41,24 @@ def params_of(w):
                              repetition_penalty=float(w.repetition_penalty[i])) for i in range(w.batch)]
 
 
-def run_gpu(w, device, logits=None, want_probs=True, uniforms=None, workspace="auto", mode=None):
+def run_path(w, device, path, **kw):
+    """run_gpu with the workspace, mode and row-kind hint of the named PATHS entry."""
+    ws, mode = PATHS[path]
+    return run_gpu(w, device, workspace=ws, mode=mode, row_kinds="hint" if path == "shipped" else 0, **kw)
+
+
+def run_gpu(w, device, logits=None, want_probs=True, uniforms=None, workspace="auto", mode=None, row_kinds=0):
     """One ns_sample call over workload ``w``; returns ids, probs (CPU) and info words.
 
     ``mode``: NS_MODE_SEGMENTED (greedy and small-k rows split over several
     workgroups, the per-row kernel for the rest), NS_MODE_PER_ROW (one workgroup
     per row), or NS_MODE_AUTO (the default: chosen from the batch size).
+    ``row_kinds``: the NS_KIND_* hint, or "hint" for the one PackedRows derives
+    from the parameters (as Sampler.sample passes it).
     """
     packed = S.PackedRows(params_of(w), w.histories, w.vocab)
+    if isinstance(row_kinds, str):
+        row_kinds = packed.row_kinds
     d = packed.to_device(device)
     if logits is None:
         logits = w.device_logits(device)
@@ -54,7 +71,7 @@ def run_gpu(w, device, logits=None, want_probs=True, uniforms=None, workspace="a
     L.sample_raw(logits, d["temperature"], d["top_k"], d["top_p"], d["rep_penalty"], u, out,
                  sample_idx=sidx, hist_offsets=d["hist_offsets"], hist_ids=d["hist_ids"],
                  max_hist=packed.max_hist, out_probs=probs, out_info=info, workspace=workspace,
-                 mode=L.NS_MODE_AUTO if mode is None else mode)
+                 mode=L.NS_MODE_AUTO if mode is None else mode, row_kinds=int(row_kinds))
     torch.cuda.synchronize()
     return {"ids": out.cpu().numpy(), "probs": None if probs is None else probs.cpu(),
             "info": info.cpu().numpy()}
@@ -68,33 +85,41 @@ def compare(g, r, check_probs: bool = True, max_report: int = 8):
     """Return (failures, stats) comparing GPU output ``g`` with OracleResult ``r``."""
     B = len(r.ids)
     fails = []
-    stats = {"rows": B, "exempt": 0, "greedy": int(r.greedy.sum()), "id_equal": 0, "zone_rows": 0,
-             "max_prob_rel": 0.0}
+    stats = {"rows": B, "exempt": 0, "draw_boundary": 0, "draw_zone": 0, "topp_boundary": 0,
+             "greedy": int(r.greedy.sum()), "id_equal": 0, "zone_rows": 0, "max_allowed": 0, "max_prob_rel": 0.0}
     for i in range(B):
         gi, ri = int(g["ids"][i]), int(r.ids[i])
-        info = g["info"][i]
-        exempt = bool(r.exempt[i])
-        stats["exempt"] += int(exempt)
+        info = g["info"][i] if g.get("info") is not None else None
+        where = f"path {info[0]}, flags {info[5]}" if info is not None else "sampler"
+        allowed = r.allowed_ids[i]
+        greedy = bool(r.greedy[i])
+        stats["exempt"] += int(bool(r.exempt[i]))
+        stats["draw_boundary"] += int(bool(r.draw_boundary[i]) and not greedy)
+        stats["draw_zone"] += int(bool(r.draw_zone[i]))
+        stats["topp_boundary"] += int(bool(r.topp_boundary[i]) and not greedy)
+        stats["max_allowed"] = max(stats["max_allowed"], len(allowed))
         if gi == ri:
             stats["id_equal"] += 1
-        elif r.greedy[i] or not exempt:
-            fails.append(f"row {i}: id {gi} != oracle {ri} (path {info[0]}, flags {info[5]}, greedy {r.greedy[i]})")
-        if r.greedy[i] or r.nan_row[i]:
+        if greedy and gi != ri:
+            fails.append(f"row {i}: greedy id {gi} != oracle {ri} ({where})")
+        elif not greedy and not bool(np.isin(gi, allowed)):
+            fails.append(f"row {i}: id {gi} not among the allowed ids {allowed[:8].tolist()} (oracle {ri}, {where})")
+        if greedy:
             continue
-        if not np.isnan(r.topk_thr[i]):
-            if int(info[2]) != f32_bits(r.topk_thr[i]):
-                g_thr = np.int32(info[2]).view(np.float32)
-                fails.append(f"row {i}: top-k threshold {g_thr!r} != oracle {r.topk_thr[i]!r} (path {info[0]})")
         zone = r.zone_ids[i]
         nz = len(zone)
         stats["zone_rows"] += int(nz > 0)
-        if abs(int(info[1]) - int(r.n_kept[i])) > nz:
-            fails.append(f"row {i}: kept {info[1]} vs oracle {r.n_kept[i]} (zone {nz}, path {info[0]})")
-        if check_probs and g["probs"] is not None and not r.topp_boundary[i]:
+        if info is not None and not r.nan_row[i]:
+            if not np.isnan(r.topk_thr[i]) and int(info[2]) != f32_bits(r.topk_thr[i]):
+                g_thr = np.int32(info[2]).view(np.float32)
+                fails.append(f"row {i}: top-k threshold {g_thr!r} != oracle {r.topk_thr[i]!r} (path {info[0]})")
+            if abs(int(info[1]) - int(r.n_kept[i])) > nz:
+                fails.append(f"row {i}: kept {info[1]} vs oracle {r.n_kept[i]} (zone {nz}, path {info[0]})")
+        if check_probs and g.get("probs") is not None:
             pg = g["probs"][i].double()
             po = r.probs[i].double()
             diff = (pg - po).abs()
-            tol = PROB_RTOL * torch.maximum(pg.abs(), po.abs()) + PROB_ATOL + po.abs() * r.zone_mass[i]
+            tol = PROB_RTOL * torch.maximum(pg.abs(), po.abs()) + PROB_ATOL + po.abs() * float(r.renorm[i])
             if nz:
                 diff[torch.as_tensor(zone)] = 0.0
             bad = diff > tol
@@ -104,7 +129,7 @@ def compare(g, r, check_probs: bool = True, max_report: int = 8):
             if bool(bad.any()):
                 j = int(torch.nonzero(bad)[0, 0])
                 fails.append(f"row {i}: prob[{j}] {float(pg[j])!r} vs oracle {float(po[j])!r} "
-                             f"({int(bad.sum())} tokens off, path {info[0]})")
+                             f"({int(bad.sum())} tokens off, {where})")
     if len(fails) > max_report:
         fails = fails[:max_report] + [f"... {len(fails) - max_report} more"]
     return fails, stats

@@ -2,14 +2,21 @@
 
 Checks that every workload regenerates bit-identically (SHA-256 of logits,
 parameters, histories and uniforms) and that the oracle still produces the
-fixture's token ids, top-k thresholds, kept counts and exemption flags, and
-for the tiny hand-built rows the exact final probabilities.
+fixture's token ids, allowed ids, top-k thresholds, kept counts, top-p zones
+and exemption flags, and for the tiny hand-built rows the exact final
+probabilities.
 """
+import os
+import sys
+
 import numpy as np
 import pytest
 
 import golden_data as G
 from oracle import sampler_oracle as O
+
+sys.path.insert(0, os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden"))
+from make_golden import row_records as G_rows  # noqa: E402
 
 CONFIGS = G.configs()
 TINY = G.tiny()
@@ -37,15 +44,3 @@ def test_tiny_fixture(case):
     for i, e in enumerate(case["expected"]):
         e = {k: v for k, v in e.items() if k != "probs_bits"}
         assert got[i] == e, f"{case['name']} row {i}: {got[i]} != fixture {e}"
-
-
-def G_rows(r):
-    out = []
-    for i in range(len(r.ids)):
-        out.append({
-            "id": int(r.ids[i]),
-            "thr_bits": None if np.isnan(r.topk_thr[i]) else int(np.float32(r.topk_thr[i]).view(np.uint32)),
-            "n_kept_topk": int(r.n_kept_topk[i]), "n_kept": int(r.n_kept[i]), "zone": int(len(r.zone_ids[i])),
-            "greedy": bool(r.greedy[i]), "nan_row": bool(r.nan_row[i]), "exempt": bool(r.exempt[i]),
-        })
-    return out

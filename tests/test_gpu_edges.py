@@ -1,15 +1,15 @@
 """GPU: boundary shapes against the oracle -- the largest vocabulary and history the
 ABI accepts, a one-token vocabulary, a bf16 vocabulary that is not a multiple of the
 16-byte chunk read through a padded row stride, and an empty batch.  Same bar as
-tests/parity.py (ids bit-exact outside exempt rows, thresholds bit-exact, probabilities
-within 1e-5 relative), in both kernel modes.
+tests/parity.py (every id among the oracle's allowed ids, thresholds bit-exact,
+probabilities within 1e-5 relative), in the segmented, per-row and shipped launch sets.
 """
 import numpy as np
 import pytest
 import torch
 
 from conftest import pkg
-from parity import PATHS, compare, run_gpu
+from parity import PATHS, compare, run_gpu, run_path
 
 W = pkg("workloads")
 L = pkg("_lib")
@@ -35,8 +35,7 @@ def workload(name, B, V, seed, hist_len, bf16=False, scale=3.0):
 
 def check(w, device, path, logits=None):
     print(f"[edges] {w.name} B={w.batch} V={w.vocab} path={path}", flush=True)
-    ws, mode = PATHS[path]
-    g = run_gpu(w, device, logits=logits, workspace=ws, mode=mode)
+    g = run_path(w, device, path, logits=logits)
     r = O.sample_workload(w)
     fails, stats = compare(g, r)
     print(f"[edges] {w.name}: {stats}", flush=True)
@@ -104,11 +103,12 @@ def test_invalid_rows_and_history_ids_are_reported(device, path):
     out = torch.full((B,), -7, dtype=torch.int64, device=device)
     info = torch.zeros((B, L.NS_INFO_WORDS), dtype=torch.int32, device=device)
     ws, mode = PATHS[path]
+    kinds = L.row_kinds(np.ones(B), np.full(B, 50), V) if path == "shipped" else 0
     print(f"[edges] invalid rows path={path}", flush=True)
     L.sample_raw(torch.from_numpy(flat).to(device), t, k, p, pen, u, out,
                  sample_idx=torch.from_numpy(sidx).to(device),
                  hist_offsets=torch.from_numpy(offs).to(device), hist_ids=torch.from_numpy(ids).to(device),
-                 max_hist=4, out_info=info, workspace=ws, mode=mode)
+                 max_hist=4, out_info=info, workspace=ws, mode=mode, row_kinds=kinds)
     torch.cuda.synchronize()
     g, inf = out.cpu().numpy(), info.cpu().numpy()
     for r in (1, 3):
@@ -119,4 +119,41 @@ def test_invalid_rows_and_history_ids_are_reported(device, path):
     r = O.sample(flat[sidx[good]], np.ones(3), np.full(3, 50), np.full(3, 0.9), np.full(3, 1.2),
                  [np.asarray(h, dtype=np.int32) for h in clean], u_np[good])
     for j, row in enumerate(good):
-        assert g[row] == r.ids[j] or r.exempt[j], (row, g[row], r.ids[j])
+        assert g[row] in r.allowed_ids[j], (row, g[row], r.ids[j], r.allowed_ids[j].tolist())
+
+
+@pytest.mark.parametrize("path", list(PATHS))
+def test_misaligned_vocab_with_invalid_sample_indices(device, path):
+    """An fp32 vocab of 50257 (rows not 16-byte aligned: the binding copies the sampled
+    rows into padded ones) with sample indices outside the logits tensor: the copy
+    gathers clamped indices, the bad rows still come back as id -1 with FLAG_BAD_ROW,
+    and the valid rows match the oracle."""
+    V, N = 50257, 6
+    rng = np.random.default_rng(96)
+    flat = (rng.standard_normal((N, V), dtype=np.float32) * 3.0).astype(np.float32)
+    sidx = np.array([0, -1, 5, N, 2, -(2 ** 40)], dtype=np.int64)
+    B = len(sidx)
+    t_np, k_np = np.array([1.0, 1.0, 0.0, 0.8, 1.3, 1.0]), np.array([50, 50, 0, 0, 20, 1000])
+    t = torch.from_numpy(t_np.astype(np.float32)).to(device)
+    k = torch.from_numpy(k_np.astype(np.int32)).to(device)
+    p = torch.full((B,), 0.9, device=device)
+    pen = torch.full((B,), 1.0, device=device)
+    u_np = rng.random(B, dtype=np.float32)
+    u = torch.from_numpy(u_np).to(device)
+    out = torch.full((B,), -7, dtype=torch.int64, device=device)
+    info = torch.zeros((B, L.NS_INFO_WORDS), dtype=torch.int32, device=device)
+    ws, mode = PATHS[path]
+    kinds = L.row_kinds(t_np, k_np, V) if path == "shipped" else 0
+    logits = torch.from_numpy(flat).to(device)
+    assert (logits.stride(0) * 4) % 16 != 0
+    print(f"[edges] misaligned vocab with invalid sample indices path={path}", flush=True)
+    L.sample_raw(logits, t, k, p, pen, u, out, sample_idx=torch.from_numpy(sidx).to(device), out_info=info,
+                 workspace=ws, mode=mode, row_kinds=kinds)
+    torch.cuda.synchronize()
+    g, inf = out.cpu().numpy(), info.cpu().numpy()
+    for r in (1, 3, 5):
+        assert g[r] == -1 and inf[r][0] == 9 and (inf[r][5] & 4), (r, g[r], inf[r].tolist())
+    good = [0, 2, 4]
+    r = O.sample(flat[sidx[good]], t_np[good], k_np[good], np.full(3, 0.9), np.ones(3), [[], [], []], u_np[good])
+    for j, row in enumerate(good):
+        assert g[row] in r.allowed_ids[j], (row, g[row], r.ids[j], r.allowed_ids[j].tolist())

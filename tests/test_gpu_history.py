@@ -2,17 +2,21 @@
 ns_hist_append, the ``DeviceHistories`` class).
 
 Holding the same ids as the CSR histories, they must give bit-identical ids,
-diagnostics and probabilities in every mode (every kernel reads a row's history
-through the same start/length pair).  Over a multi-step decode loop, appending
-each sampled token on the device must track the host-side lists the reference's
-engine rebuilds every step (engine.py:242-246, scheduler.py:281-284).
+diagnostics and probabilities in every launch set (every kernel reads a row's
+history through the same start/length pair).  Over a multi-step decode loop,
+appending each sampled token on the device must track the host-side lists the
+reference's engine rebuilds every step (engine.py:242-246,
+scheduler.py:281-284), and every step's ids must meet the oracle run on that
+step's logits, host histories and uniforms.
 """
 import numpy as np
 import pytest
 import torch
 
 from conftest import pkg
-from parity import PATHS, params_of, run_gpu
+from parity import PATHS, compare, params_of, run_path
+
+O = pytest.importorskip("oracle.sampler_oracle")
 
 W = pkg("workloads")
 L = pkg("_lib")
@@ -28,11 +32,13 @@ def open_all(w, device, extra_slots=3):
     return dh
 
 
-def run_slots(w, device, dh, workspace, mode):
+def run_slots(w, device, dh, workspace, mode, row_kinds=0):
     """run_gpu's call with the histories read from ``dh`` (request r on row r), no append."""
     slots = dh.slots(list(range(w.batch)))
     max_hist = int(max(dh.length(r) for r in range(w.batch)))
     packed = S.PackedRows(params_of(w), None, w.vocab, slots=slots, slot_max_hist=max_hist)
+    if isinstance(row_kinds, str):
+        row_kinds = packed.row_kinds
     d = packed.to_device(device)
     logits = w.device_logits(device)
     B, V = w.batch, w.vocab
@@ -43,7 +49,7 @@ def run_slots(w, device, dh, workspace, mode):
     info = torch.zeros((B, L.NS_INFO_WORDS), dtype=torch.int32, device=device)
     L.sample_raw(logits, d["temperature"], d["top_k"], d["top_p"], d["rep_penalty"], u, out,
                  sample_idx=sidx, max_hist=packed.max_hist, out_probs=probs, out_info=info, workspace=workspace,
-                 mode=mode, hist_state=dh.state, hist_slot=d["hist_slot"])
+                 mode=mode, row_kinds=int(row_kinds), hist_state=dh.state, hist_slot=d["hist_slot"])
     torch.cuda.synchronize()
     return {"ids": out.cpu().numpy(), "probs": probs.cpu(), "info": info.cpu().numpy()}
 
@@ -66,9 +72,9 @@ def test_device_histories_match_csr(device, cfg, path):
     w = W.make_workload(cfg, batch=64 if cfg == 2 else None)
     print(f"[history] config {cfg} B={w.batch} path={path}", flush=True)
     ws, mode = PATHS[path]
-    ref = run_gpu(w, device, workspace=ws, mode=mode)
+    ref = run_path(w, device, path)
     dh = open_all(w, device)
-    got = run_slots(w, device, dh, ws, mode)
+    got = run_slots(w, device, dh, ws, mode, row_kinds="hint" if path == "shipped" else 0)
     assert np.array_equal(got["ids"], ref["ids"])
     bad = np.nonzero((got["info"] != ref["info"]).any(axis=1))[0]
     assert bad.size == 0, [(int(i), ref["info"][i].tolist(), got["info"][i].tolist()) for i in bad[:4]]
@@ -76,8 +82,9 @@ def test_device_histories_match_csr(device, cfg, path):
 
 
 def test_decode_loop_appends_on_device(device):
-    """Four decode steps of the mixed batch: ids equal to the host-history run at every
-    step, and the device lists equal the host lists afterwards."""
+    """Four decode steps of the mixed batch: at every step the ids meet the oracle run on
+    the step's logits with the host lists, the device-history call returns the same ids,
+    and the device lists equal the host lists afterwards."""
     w = W.make_workload(1)
     B = w.batch
     params = params_of(w)
@@ -98,6 +105,11 @@ def test_decode_loop_appends_on_device(device):
                                  history_requests=list(range(B)))
         a, b = ids_host.cpu().numpy(), ids_dev.cpu().numpy()
         assert np.array_equal(a, b), f"step {step}: rows {np.nonzero(a != b)[0][:8]}"
+        r = O.sample(logits.cpu().numpy(), w.temperature, w.top_k, w.top_p, w.repetition_penalty,
+                     [np.asarray(h, dtype=np.int32) for h in host], u.cpu().numpy())
+        fails, stats = compare({"ids": a, "probs": None, "info": None}, r)
+        print(f"[history] step {step}: {stats}", flush=True)
+        assert not fails, f"step {step}:\n" + "\n".join(fails)
         for r in range(B):
             host[r].append(int(a[r]))
     torch.cuda.synchronize()

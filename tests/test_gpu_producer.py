@@ -13,7 +13,7 @@ import pytest
 import torch
 
 from conftest import pkg
-from parity import PATHS, compare, run_gpu
+from parity import PATHS, compare, run_path
 
 W = pkg("workloads")
 L = pkg("_lib")
@@ -48,9 +48,8 @@ def test_bf16_gemm_output_matches_the_upcast(device, cfg, path, producer):
     base = W.make_workload(cfg, batch=64 if cfg == 2 else None)
     w, logits = lm_head_workload(base, device, seed=cfg, producer=producer)
     print(f"[producer] {w.name} B={w.batch} V={w.vocab} path={path} producer={producer}", flush=True)
-    ws, mode = PATHS[path]
-    g_bf = run_gpu(w, device, logits=logits, workspace=ws, mode=mode)
-    g_f32 = run_gpu(w, device, logits=logits.float(), workspace=ws, mode=mode)
+    g_bf = run_path(w, device, path, logits=logits)
+    g_f32 = run_path(w, device, path, logits=logits.float())
     r = O.sample_workload(w)
     for name, g in (("bf16", g_bf), ("f32", g_f32)):
         fails, stats = compare(g, r)

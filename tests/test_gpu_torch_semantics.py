@@ -1,0 +1,80 @@
+"""GPU: what torch computes on the device for the reference sampler's own ops.
+
+The reference runs ``Sampler.sample`` on the GPU (config.py:63 ``device="cuda"``).
+The oracle restates it with the arithmetic torch uses on the CPU; these checks
+record where torch on the device (this image's ROCm build) agrees with that
+restatement and where it does not:
+
+* ``score / p.repetition_penalty`` with a Python float (sampler.py:37) is NOT a
+  division on the device: torch multiplies by ``fl32(1.0 / p)``, the reciprocal
+  taken in double precision from the Python float and rounded once.  It differs
+  from the correctly rounded ``x / fl32(p)`` of the CPU (and of the kernels) by
+  one ulp on a share of the inputs; the oracle keeps the division, which is also
+  what "the penalty divides positive logits" states.
+* ``score * p`` (sampler.py:37) and ``logits / temps`` (sampler.py:51, a tensor
+  divisor) are the correctly rounded float32 operations on both.
+* ``torch.sort(descending=True)`` (sampler.py:64) orders tied values by ascending
+  token id on the device: the oracle's stable order at a top-p cut.
+* ``torch.cumsum`` of the sorted probabilities (sampler.py:66) lies within 1e-6 of
+  the oracle's float64-accumulated prefix (the top-p zone's width), and the
+  device softmax (sampler.py:65, :76) within 1e-5 relative of float64.
+"""
+import numpy as np
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+
+
+def _bits(a):
+    return np.ascontiguousarray(a, dtype=np.float32).view(np.uint32)
+
+
+def test_penalty_division_by_python_scalar(device):
+    b = np.arange(65536, dtype=np.uint32) << 16
+    x = b.view(np.float32)
+    x = x[np.isfinite(x)]
+    xg = torch.from_numpy(x).to(device)
+    for p in (1.1, 1.2, 1.05, 1.3, 0.7):
+        got = (xg / p).cpu().numpy()
+        with np.errstate(over="ignore"):
+            recip = (x * np.float32(1.0 / p)).astype(np.float32)
+            exact = (x / np.float32(p)).astype(np.float32)
+        assert np.array_equal(_bits(got), _bits(recip)), p
+        n_diff = int(np.sum(_bits(got) != _bits(exact)))
+        print(f"[torch] x / {p}: device differs from the correctly rounded division on {n_diff} of {x.size}")
+        mul = (xg * p).cpu().numpy()
+        with np.errstate(over="ignore"):
+            assert np.array_equal(_bits(mul), _bits((x * np.float32(p)).astype(np.float32))), p
+
+
+def test_temperature_division_by_tensor(device):
+    rng = np.random.default_rng(3)
+    x = (rng.standard_normal((256, 4096)) * 3).astype(np.float32)
+    t = rng.uniform(1e-3, 2.0, 256).astype(np.float32)
+    got = (torch.from_numpy(x).to(device) / torch.from_numpy(t).to(device).unsqueeze(1)).cpu().numpy()
+    assert np.array_equal(_bits(got), _bits(x / t[:, None]))
+
+
+def test_sort_ties_ascending_id(device):
+    for V in (6000, 128256):
+        v = torch.from_numpy(np.round(np.random.default_rng(V).standard_normal(V) * 4).astype(np.float32)).to(device)
+        sv, si = torch.sort(v, descending=True)
+        svn, sin_ = sv.cpu().numpy(), si.cpu().numpy()
+        same = svn[1:] == svn[:-1]
+        assert same.sum() > 1000
+        assert not np.any(same & (sin_[1:] < sin_[:-1])), V
+
+
+def test_cumsum_and_softmax_accuracy(device):
+    for seed in range(2):
+        r = torch.from_numpy((np.random.default_rng(seed).standard_normal(128256) * 3).astype(np.float32)).to(device)
+        sv, _ = torch.sort(r, descending=True)
+        pr = torch.softmax(sv, dim=-1)
+        cg = torch.cumsum(pr, dim=-1).cpu().double().numpy()
+        prc = pr.cpu()
+        c64 = prc.double().cumsum(-1).float().double().numpy()
+        assert np.max(np.abs(cg - c64)) < 1e-6
+        p64 = torch.softmax(sv.cpu().double(), -1).numpy()
+        rel = np.abs(prc.double().numpy() - p64) / p64
+        assert rel.max() < 1e-5

@@ -1,0 +1,30 @@
+"""CPU: the kernels' correctly rounded division (ns::div_rn, csrc/ns_device.h) against
+IEEE float division, bit for bit.
+
+The kernels divide by a row-uniform divisor t (the temperature, sampler.py:51, and the
+repetition penalty, sampler.py:37) as q0 = RN(x * RN(1/t)), then one fma-based
+correction.  tests/native/div_rn_check.c runs that formula on the CPU with C's fmaf
+over every mantissa of 21 binades (every third exponent from -30 to 30) for 16 fixed
+divisors (the penalties and temperatures the workloads use among them) and random
+ones, both signs, and compares with x / t.
+"""
+import os
+import shutil
+import subprocess
+
+import pytest
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+SRC = os.path.join(HERE, "native", "div_rn_check.c")
+BUILD = os.path.join(HERE, "native", "build")
+
+
+@pytest.mark.skipif(shutil.which("gcc") is None, reason="needs gcc")
+def test_div_rn_matches_ieee_division():
+    os.makedirs(BUILD, exist_ok=True)
+    exe = os.path.join(BUILD, "div_rn_check")
+    subprocess.run(["gcc", "-O2", "-mfma", "-ffp-contract=off", "-o", exe, SRC, "-lm"], check=True)
+    res = subprocess.run([exe, "4"], capture_output=True, text=True, timeout=300)
+    print(res.stdout)
+    assert res.returncode == 0, res.stdout + res.stderr
+    assert "mismatches 0" in res.stdout
