@@ -804,7 +804,7 @@ __device__ __attribute__((always_inline)) inline void generic_path(const GCtx g)
 
 }  // namespace ns
 
-#include "ns_rowfast.h"
+#include "ns_topk.h"
 
 namespace ns {
 
@@ -1132,6 +1132,53 @@ __global__ __launch_bounds__(NT) void sample_kernel(const KParams P) {
         if (__builtin_expect(st == 0, 1)) return;
       }
     }
+  }
+  row_general<T>((KArgs)__builtin_amdgcn_kernarg_segment_ptr());
+}
+
+// One workgroup per sampled row for calls whose rows are all top-k rows with
+// 1 <= k <= KFAST (the host's NS_KIND_SMALL_K hint): the row's loads are issued before the
+// per-row parameters return (topk_stream, ns_topk.h).  A row of another kind, or one that
+// path hands back, is resolved by the general per-row code: the hint never changes a result.
+template <typename T>
+__global__ __launch_bounds__(NT) void topk_kernel(const KParams P) {
+  const int row = blockIdx.x;
+  const int tid = threadIdx.x;
+  const float temp = P.temperature[row];
+  const int32_t k = P.top_k[row];
+  const float topp = P.top_p[row];
+  const float pen = P.penalty[row];
+  float u = P.uniforms[row];
+  const int64_t src = P.sample_idx != nullptr ? P.sample_idx[row] : (int64_t)row;
+  int32_t h0 = 0, h1 = 0;
+  row_history(P.hist_off, P.hist_slot, P.hist_len, P.hist_nslots, P.hist_cap, row, h0, h1);
+  const int32_t H = h1 - h0;
+  const bool pen_on = pen != 1.0f && H > 0;
+  const bool ok = src >= 0 && src < P.n_rows_total && h0 >= 0 && H >= 0 && H <= MAX_HIST && temp != 0.0f &&
+                  k >= 1 && k <= KFAST && (int64_t)k < P.vocab && !(pen_on && !(pen > 1.0f && pen <= 3.40282347e38f));
+  if (ok) {
+    extern __shared__ __align__(16) unsigned char smem[];
+    Misc* misc = reinterpret_cast<Misc*>(smem);
+    uint32_t* bm = reinterpret_cast<uint32_t*>(smem + P.off_bm);
+    uint64_t* cand = reinterpret_cast<uint64_t*>(smem + P.off_cand);
+    // LDS set-up: the list padded with keys that sort last, the group maxima at -inf, the
+    // counters (list length, row flags, arrival tickets), the cleared bitmap;
+    // the barrier orders them before the history bits and the candidates
+    if (tid < WAVE_CAP) cand[tid] = ~0ull;
+    if (tid < NWAVE * 8) reinterpret_cast<float*>(&misc->red)[tid] = -__builtin_inff();
+    if (tid == 0) { misc->flags = 0; misc->cand_n = 0; misc->ib[0] = 0; }
+    if (pen_on) {
+      uint4* bm4 = reinterpret_cast<uint4*>(bm);
+      const int nbw4 = (int)(((P.vocab + 31) / 32 + 3) / 4);   // the bitmap region is padded to 16 bytes
+      for (int i = tid; i < nbw4; i += NT) bm4[i] = make_uint4(0u, 0u, 0u, 0u);
+    }
+    __syncthreads();
+    const unsigned char* rowp = (const unsigned char*)P.logits + src * P.row_stride * T::SZ;
+    u = (u >= 0.0f) ? (u < 1.0f ? u : 0x1.fffffep-1f) : 0.0f;
+    const int st = topk_stream<T>(RowArgs{P.logits, P.row_stride, P.vocab, P.hist_ids, P.out_ids, P.out_probs,
+                                          P.out_info},
+                                  row, rowp, P.hist_ids + h0, temp, k, topp, pen, u, H, misc, bm, cand);
+    if (__builtin_expect(st == 0, 1)) return;
   }
   row_general<T>((KArgs)__builtin_amdgcn_kernarg_segment_ptr());
 }
@@ -1615,14 +1662,27 @@ int ns_sample(const ns_sample_args* a, hipStream_t stream) {
     if (e != hipSuccess) return fail(NS_ERR_HIP, std::string("wide kernel launch: ") + hipGetErrorString(e));
   }
 
-  // 3) one workgroup per row: every other row, and rows the segment kernel deferred
+  // 3) one workgroup per row: every other row, and rows the segment kernel deferred.  A call
+  //    declared to hold only small-k rows, with no kernel before this one, takes the kernel
+  //    that requests each row at entry.
   const dim3 grid((unsigned)a->n_sample), block(ns::NT);
-  const void* fn = a->dtype == NS_DTYPE_BF16 ? reinterpret_cast<const void*>(&ns::sample_kernel<ns::BF16>)
-                                             : reinterpret_cast<const void*>(&ns::sample_kernel<ns::F32>);
+  const bool bf = a->dtype == NS_DTYPE_BF16;
+  const bool topk = !segmented && !wide && a->row_kinds == (uint32_t)NS_KIND_SMALL_K &&
+                    (bf ? ns::topk_fits<ns::BF16>(a->vocab) : ns::topk_fits<ns::F32>(a->vocab));
+  const void* fn = topk ? (bf ? reinterpret_cast<const void*>(&ns::topk_kernel<ns::BF16>)
+                              : reinterpret_cast<const void*>(&ns::topk_kernel<ns::F32>))
+                        : (bf ? reinterpret_cast<const void*>(&ns::sample_kernel<ns::BF16>)
+                              : reinterpret_cast<const void*>(&ns::sample_kernel<ns::F32>));
   e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, lds);
   if (e != hipSuccess) return fail(NS_ERR_HIP, std::string("hipFuncSetAttribute: ") + hipGetErrorString(e));
-  if (a->dtype == NS_DTYPE_BF16) hipLaunchKernelGGL((ns::sample_kernel<ns::BF16>), grid, block, lds, stream, p);
-  else hipLaunchKernelGGL((ns::sample_kernel<ns::F32>), grid, block, lds, stream, p);
+  if (topk) {
+    if (bf) hipLaunchKernelGGL((ns::topk_kernel<ns::BF16>), grid, block, lds, stream, p);
+    else hipLaunchKernelGGL((ns::topk_kernel<ns::F32>), grid, block, lds, stream, p);
+  } else if (bf) {
+    hipLaunchKernelGGL((ns::sample_kernel<ns::BF16>), grid, block, lds, stream, p);
+  } else {
+    hipLaunchKernelGGL((ns::sample_kernel<ns::F32>), grid, block, lds, stream, p);
+  }
   e = hipGetLastError();
   if (e != hipSuccess) return fail(NS_ERR_HIP, std::string("kernel launch: ") + hipGetErrorString(e));
   return NS_OK;

@@ -573,16 +573,18 @@ __device__ __forceinline__ void wave_draw_sorted(uint64_t a, int nk, int n, cons
   float vstar = -__builtin_inff();
   int32_t istar = -1;
   if (topp_on) {
-    const double rz = 1.0 / read_lane(cs, nk - 1);
-    const double cq = wave_incl_scan((double)(float)((double)ev * rz));
-    // first sorted position whose float32 prefix exceeds top_p; it is kept (sampler.py:66-72)
-    const uint64_t m = ballot(lane < nk && (float)cq > p32);
+    // first sorted position whose float32 prefix exceeds top_p; it is kept (sampler.py:66-72).
+    // The prefix of the top-k softmax is taken as the float64 prefix of the numerators times
+    // the reciprocal of their sum: it differs from the sum of float32-rounded probabilities
+    // by about 1e-7, inside the 1e-6 zone where the cut is ambiguous anyway.
+    const double rz = rcp_f64(read_lane(cs, nk - 1));
+    const uint64_t m = ballot(lane < nk && (float)(cs * rz) > p32);
     if (m != 0ull) nf = __builtin_ctzll(m) + 1;
     const uint64_t kc = read_lane(a, nf - 1);
     vstar = desc_key_val(kc);
     istar = (int32_t)desc_key_id(kc);
   }
-  const double rz2 = 1.0 / read_lane(cs, nf - 1);
+  const double rz2 = rcp_f64(read_lane(cs, nf - 1));
   // final probabilities of the kept candidates (sorted position < nf), in id order
   const bool k0 = r0 < nf, k1 = r1 < nf;
   const float p0 = k0 ? (float)((double)ns_expf(desc_key_val(b0) - M) * rz2) : 0.0f;

@@ -1,0 +1,247 @@
+// gfx950 row streaming path for calls whose sampled rows are all top-k rows with
+// 1 <= k <= KFAST (the host's NS_KIND_SMALL_K hint), one 1024-thread workgroup per
+// row: sampler.py:31-89 for such a row with one HBM pass over it.
+//
+// Where it differs from row_fast (ns_rowfast.h), which serves rows of any kind:
+//   * the history bitmap is cleared while the per-row parameters are in flight and
+//     one barrier (which costs nothing: every wave waits for the parameters anyway)
+//     orders it before any bit is set; each lane's two history ids are requested
+//     ahead of its row chunks, so every wave sets its bits (set semantics,
+//     sampler.py:34-38) before its row data lands and the bitmap is complete at
+//     the first barrier after the stream;
+//   * the row is read with the non-temporal cache policy;
+//   * a wave arriving late takes the bound (the k-th largest of the maxima of
+//     8-lane groups published so far, a lower bound of the k-th largest raw
+//     value, mapped through the temperature) while the last waves still stream;
+//   * after the barrier each wave stages its chunks that reach the bound in its
+//     own LDS slots and expands them, one element per lane, into the candidate
+//     list, with no further barrier.
+// The candidate list is then ordered by the whole workgroup and drawn by one wave
+// (block_finalize_keys), exactly as on the other paths.  Rows this path cannot
+// finish (too many candidates, a penalized list short of k) are left to the
+// general per-row code, with the same results.
+#pragma once
+
+#include "ns_rowfast.h"
+
+namespace ns {
+
+constexpr int TK_CPT = RCPT;                // 16-byte chunks per thread (16)
+constexpr int TK_HB = 2;                    // history ids per thread requested with the row
+constexpr int TK_BOUND_TICKET = NWAVE - 3;  // the wave that arrives with this ticket takes the bound
+
+template <typename T>
+__host__ __device__ __forceinline__ bool topk_fits(int64_t V) {
+  return row_fits<T>(V);
+}
+
+// The NaN guard's uniform row (sampler.py:77-80): probability 1/V for every token and the
+// inverse-CDF pick against u over the float64 prefix (i + 1) * fl32(1/V).  Mrep is the value
+// reported in the diagnostics (NaN, +inf or -inf).
+__device__ __forceinline__ void uniform_row_out(const RowOut& o, float u, int32_t flags, float Mrep) {
+  const int64_t V = o.V;
+  const float qv = (float)(1.0 / (double)V);
+  if (threadIdx.x == 0) {
+    const double qd = qv, ud = u;
+    int64_t i = (int64_t)(ud / qd);
+    while (i > 0 && (double)i * qd > ud) --i;
+    while ((double)(i + 1) * qd <= ud && i < V) ++i;
+    if (i >= V) i = V - 1;
+    o.out_ids[o.row] = i;
+  }
+  write_info(o, PATH_UNIFORM, (int32_t)V, -__builtin_inff(), (int32_t)V, 0, flags, Mrep, -1);
+  if (o.out_probs != nullptr) {
+    float* pr = o.out_probs + (int64_t)o.row * V;
+    for (int64_t i = threadIdx.x; i < V; i += NT) pr[i] = qv;
+  }
+}
+
+// The whole row path: every thread of the workgroup calls it after the set-up barrier,
+// with the LDS already prepared (padded list, zero counters, group maxima at -inf, cleared
+// bitmap).  Returns 0 when the row is resolved, 1 when it is left to the general per-row
+// code.
+template <typename T>
+__device__ __forceinline__ int topk_stream(const RowArgs P, const int row, const unsigned char* rowp,
+                                           const int32_t* hp, const float temp, const int32_t k,
+                                           const float topp, const float pen, const float u, const int32_t H,
+                                           Misc* misc, uint32_t* bm, uint64_t* cand) {
+  constexpr int EPC = T::EPC;
+  const int tid = threadIdx.x;
+  const int lane = lane_id();
+  const int wid = wave_id();
+  const int64_t V = P.vocab;
+  const int nf = (int)(V / EPC);                   // chunks without a token past V
+  const int ntail = (int)(V - (int64_t)nf * EPC);  // tokens past the last full chunk
+  const uint4* rowv = reinterpret_cast<const uint4*>(rowp);
+  const bool pen_on = pen != 1.0f && H > 0;        // sampler.py:33
+  const float tdiv = temp > 0.0f ? __builtin_fmaxf(temp, 1e-6f) : 1.0f;   // sampler.py:42
+  const float rdiv = 1.0f / tdiv;
+  const float rpen = 1.0f / pen;
+  auto pen_val = [&](float x) -> float {
+    // sampler.py:37: score * p if score < 0 else score / p (float32, correctly rounded)
+    return x < 0.0f ? x * pen : div_rn(x, pen, rpen);
+  };
+  float* fs = reinterpret_cast<float*>(&misc->red);      // the 128 group maxima
+  int32_t* is = reinterpret_cast<int32_t*>(misc->db);    // per-wave NaN / +inf flags
+  const RowOut o{P.out_ids, P.out_probs, P.out_info, row, V};
+  int32_t flags = 0;
+
+  // the first history ids (positions t and NT + t), then the token past the last full chunk
+  // at this lane (wave 0), then the row: chunk q * NT + t to thread t, zeros past the last
+  // full chunk.  A wave's loads complete in issue order, so the ids come first.
+  int32_t hid[TK_HB];
+  {
+    const __amdgpu_buffer_rsrc_t rh = make_rsrc(hp, pen_on ? (uint32_t)H * 4u : 0u);
+#pragma unroll
+    for (int s = 0; s < TK_HB; ++s)
+      hid[s] = (int32_t)__builtin_amdgcn_raw_buffer_load_b32(rh, (int)((uint32_t)(s * NT + tid) * 4u), 0, 2);
+  }
+  uint32_t xtraw = 0u;
+  if (wid == 0 && ntail > 0) xtraw = gather_raw<T>(make_rsrc(rowp, (uint32_t)(V * T::SZ)), nf * EPC + lane);
+  __builtin_amdgcn_sched_barrier(0);
+  uint4 v[TK_CPT];
+  {
+    const __amdgpu_buffer_rsrc_t r = make_rsrc(rowp, (uint32_t)nf * 16u);
+#pragma unroll
+    for (int q = 0; q < TK_CPT; ++q) {
+      v[q] = buf_load16_nt(r, (uint32_t)(q * NT + tid) * 16u);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  }
+  // the history bitmap (set semantics, sampler.py:34-38) as the ids land, ahead of the row
+  if (pen_on) {
+    bool bad = false;
+    for (int base = 0; base < H; base += TK_HB * NT) {
+#pragma unroll
+      for (int s = 0; s < TK_HB; ++s) {
+        const int j = base + s * NT + tid;
+        const int32_t id = base == 0 ? hid[s] : (j < H ? hp[j] : 0);
+        if (j < H) {
+          if (id < 0 || (int64_t)id >= V) bad = true;
+          else atomicOr(&bm[id >> 5], 1u << (id & 31));
+        }
+      }
+    }
+    if (bad) atomicOr(&misc->flags, FLAG_BAD_HIST_ID);
+  }
+  // every chunk's NaN-propagating maximum as the row lands (-inf past the full chunks), then
+  // the maxima of every 8-lane group (128 values of distinct elements)
+  float cm[TK_CPT];
+  float gmax = -__builtin_inff();
+  bool special = false;
+#pragma unroll
+  for (int q = 0; q < TK_CPT; ++q) {
+    cm[q] = chunk_max<T>(v[q]);
+    if ((q + 1) * NT > nf) past_row(cm[q], q * NT + tid, nf);
+    gmax = __builtin_fmaxf(gmax, cm[q]);
+    special |= !(cm[q] < __builtin_inff());
+  }
+  gmax = __builtin_fmaxf(gmax, lane_xor(gmax, 1));
+  gmax = __builtin_fmaxf(gmax, lane_xor(gmax, 2));
+  gmax = __builtin_fmaxf(gmax, lane_xor(gmax, 4));
+  if ((lane & 7) == 0) fs[wid * 8 + (lane >> 3)] = gmax;
+  float xt = -__builtin_inff();
+  if (wid == 0 && lane < ntail) {
+    xt = raw_float<T>(xtraw);
+    special |= !(xt < __builtin_inff());
+  }
+  // Arrival ticket.  The wave that arrives with TK_BOUND_TICKET takes the bound from the
+  // group maxima published so far (the others still read -inf): the k-th largest of any
+  // subset of them is a lower bound of the row's k-th largest raw value, so the bound can
+  // be taken while the last waves still stream.  Its key is truncated to the bits a
+  // bfloat16 value carries (24 for float32) and mapped through the temperature
+  // (x >= tc  <=>  x / t >= RN(taux / t)).
+  const bool ws = ballot(special) != 0ull;
+  int ticket = 0;
+  if (lane == 0) {
+    is[wid] = ws ? 1 : 0;
+    ticket = __hip_atomic_fetch_add(&misc->ib[0], 1, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_WORKGROUP);
+  }
+  if (__builtin_amdgcn_readfirstlane(ticket) == TK_BOUND_TICKET) {
+    const uint32_t kp = wave_kth_key<T::SZ == 2 ? 16 : 24>(fkey(fs[lane]), fkey(fs[64 + lane]), k);
+    const float taux = kp <= fkey(-__builtin_inff()) ? -__builtin_inff() : fkey_inv(kp);
+    const float b = lower_preimage(taux, tdiv, rdiv);
+    if (lane == 0) misc->fb[0] = b;
+  }
+  __syncthreads();   // group maxima, flags, the bitmap, the bound
+  int spec = 0;
+#pragma unroll
+  for (int w = 0; w < NWAVE; ++w) spec |= is[w];
+  flags |= misc->flags;
+  if (spec != 0) {
+    // NaN / +inf among the logits (the penalty keeps both): the softmax is NaN, uniform
+    // 1/V (sampler.py:77-80).  Rare: the row is read again to tell NaN from +inf.
+    bool nanf = false;
+    for (int c = tid; c < nf; c += NT) {
+      const uint4 w = rowv[c];
+#pragma unroll
+      for (int e = 0; e < EPC; ++e) nanf |= T::elem(w, e) != T::elem(w, e);
+    }
+    if (wid == 0) nanf |= xt != xt;
+    const int anynan = block_max_i64(nanf ? 1 : 0, &misc->red) != 0;
+    uniform_row_out(o, u, flags, anynan ? __builtin_nanf("") : __builtin_inff());
+    return 0;
+  }
+  const float tc = misc->fb[0];
+  // fewer than k finite group maxima (a row of mostly -inf): the general code takes it
+  if (!(tc > -__builtin_inff())) { __syncthreads(); return 1; }
+  // Chunks whose maximum reaches tc go to the wave's own LDS slots, then the wave expands
+  // them into candidates, one element per lane, straight as sort keys (scaled value
+  // descending, token id ascending): elements penalized at history positions
+  // (sampler.py:37) and kept when they still reach tc.  A penalty >= 1 never raises a value,
+  // so every element of the top-k reaches tc after the penalty too; when k of them do, the
+  // list holds the whole top-k and its ties.  Every step after the stream runs in all 16
+  // waves, four to a SIMD, so it is kept to few instructions per wave.
+  uint4* hdat = reinterpret_cast<uint4*>(cand + HIT_OFF64) + wid * HIT_PER_WAVE;
+  int32_t* hidx = reinterpret_cast<int32_t*>(cand + HIT_IDX_OFF64) + wid * HIT_PER_WAVE;
+  int nh = 0;             // this wave's hit chunks (wave-uniform)
+#pragma unroll
+  for (int q = 0; q < TK_CPT; ++q) {
+    const bool hit = cm[q] >= tc;   // -inf past the row, and tc > -inf
+    const uint64_t m = ballot(hit);
+    if (m != 0ull) {
+      const int pos = nh + lanes_below(m);
+      if (hit && pos < HIT_PER_WAVE) { hdat[pos] = v[q]; hidx[pos] = q * NT + tid; }
+      nh += __popcll(m);
+    }
+  }
+  const bool unit_t = tdiv == 1.0f;
+  auto take_key = [&](float x, uint32_t id, bool live) {
+    if (live && pen_on && ((bm[id >> 5] >> (id & 31)) & 1u)) x = pen_val(x);
+    const bool t = live && x >= tc && x > -__builtin_inff();
+    const float y = unit_t ? x : div_rn(t ? x : 1.0f, tdiv, rdiv);
+    const uint64_t key = desc_key(y, id);
+    const uint64_t m = ballot(t);
+    if (m == 0ull) return;
+    const int leader = __builtin_ctzll(m);
+    int base = 0;
+    if (lane == leader) base = atomicAdd(&misc->cand_n, __popcll(m));
+    base = read_lane(base, leader);
+    const int pos = base + lanes_below(m);
+    if (t && pos < WAVE_CAP) cand[pos] = key;   // past it: counted only
+  };
+  if (nh > HIT_PER_WAVE) {
+    // more hit chunks than slots: the count goes past WAVE_CAP and the general code
+    // takes the row
+    if (lane == 0) atomicAdd(&misc->cand_n, WAVE_CAP + 1);
+  } else {
+    for (int j = lane; j < ((nh * EPC + 63) & ~63); j += 64) {
+      const bool live = j < nh * EPC;
+      const int slot = live ? j / EPC : 0, e = j % EPC;
+      const int32_t ci = hidx[slot];
+      const uint4 ch = hdat[slot];
+      const float x = elem_sel<T>(ch, e);
+      take_key(x, (uint32_t)(ci * EPC + e), live && x >= tc);
+    }
+  }
+  if (ntail > 0 && wid == 0) take_key(xt, (uint32_t)(nf * EPC + lane), lane < ntail);
+  __syncthreads();   // the list complete
+  const int n = misc->cand_n;
+  if (n > WAVE_CAP || n < k) { __syncthreads(); return 1; }
+  zero_probs(o);
+  block_finalize_keys<NT>(cand, cand + WAVE_CAP, n, k, topp < 1.0f, topp, u, row, P.out_ids, P.out_probs, V,
+                          P.out_info, flags, n, PATH_WAVE_SET);
+  return 0;
+}
+
+}  // namespace ns

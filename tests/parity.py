@@ -28,9 +28,17 @@ C = pkg("config")
 
 # kernel modes under test: path name -> (workspace, mode).  "shipped" is what
 # Sampler.sample launches: AUTO mode, the cached workspace and the row-kind hint
-# of the call's parameters (run_gpu passes it for that path).
+# of the call's parameters.  "topk" is per-row mode declared to hold only small-k
+# rows: every call takes the kernel that requests each row at entry, and rows of
+# other kinds (greedy, top-k off, penalties below 1) its fallback to the general
+# per-row code (the hint never changes a result).
 PATHS = {"segmented": ("auto", L.NS_MODE_SEGMENTED), "per-row": (None, L.NS_MODE_PER_ROW),
-         "shipped": ("auto", L.NS_MODE_AUTO)}
+         "shipped": ("auto", L.NS_MODE_AUTO), "topk": (None, L.NS_MODE_PER_ROW)}
+
+
+def path_kinds(path):
+    """The row_kinds argument run_gpu takes for the named path."""
+    return "hint" if path == "shipped" else (L.NS_KIND_SMALL_K if path == "topk" else 0)
 
 PROB_RTOL = 1e-5
 PROB_ATOL = 1e-12
@@ -44,7 +52,7 @@ def params_of(w):
 def run_path(w, device, path, **kw):
     """run_gpu with the workspace, mode and row-kind hint of the named PATHS entry."""
     ws, mode = PATHS[path]
-    return run_gpu(w, device, workspace=ws, mode=mode, row_kinds="hint" if path == "shipped" else 0, **kw)
+    return run_gpu(w, device, workspace=ws, mode=mode, row_kinds=path_kinds(path), **kw)
 
 
 def run_gpu(w, device, logits=None, want_probs=True, uniforms=None, workspace="auto", mode=None, row_kinds=0):

@@ -132,7 +132,12 @@ def test_aligned_rows_pads_misaligned_vocab():
     assert torch.equal(y, x)
     sel = torch.tensor([2, 0], dtype=torch.int64)
     y2, idx2 = L.aligned_rows(x, sel)
-    assert idx2 is None and torch.equal(y2, x[[2, 0]]) and (y2.stride(0) * 4) % 16 == 0
+    assert idx2.tolist() == [0, 1] and torch.equal(y2, x[[2, 0]]) and (y2.stride(0) * 4) % 16 == 0
+    # indices outside the tensor: the gather reads clamped rows and the kernel index marks them -1
+    bad = torch.tensor([1, -1, 3, 2, -(2 ** 40)], dtype=torch.int64)
+    y3, idx3 = L.aligned_rows(x, bad)
+    assert idx3.tolist() == [0, -1, -1, 3, -1]
+    assert torch.equal(y3[0], x[1]) and torch.equal(y3[3], x[2])
     b = torch.zeros(4, 24, dtype=torch.bfloat16)            # 48-byte rows: already aligned
     yb, ib = L.aligned_rows(b, sel)
     assert yb.data_ptr() == b.data_ptr() and ib is sel

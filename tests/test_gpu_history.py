@@ -14,7 +14,7 @@ import pytest
 import torch
 
 from conftest import pkg
-from parity import PATHS, compare, params_of, run_path
+from parity import PATHS, compare, params_of, path_kinds, run_path
 
 O = pytest.importorskip("oracle.sampler_oracle")
 
@@ -74,7 +74,7 @@ def test_device_histories_match_csr(device, cfg, path):
     ws, mode = PATHS[path]
     ref = run_path(w, device, path)
     dh = open_all(w, device)
-    got = run_slots(w, device, dh, ws, mode, row_kinds="hint" if path == "shipped" else 0)
+    got = run_slots(w, device, dh, ws, mode, row_kinds=path_kinds(path))
     assert np.array_equal(got["ids"], ref["ids"])
     bad = np.nonzero((got["info"] != ref["info"]).any(axis=1))[0]
     assert bad.size == 0, [(int(i), ref["info"][i].tolist(), got["info"][i].tolist()) for i in bad[:4]]
