@@ -1140,18 +1140,52 @@ __global__ __launch_bounds__(NT) void sample_kernel(const KParams P) {
 // 1 <= k <= KFAST (the host's NS_KIND_SMALL_K hint): the row's loads are issued before the
 // per-row parameters return (topk_stream, ns_topk.h).  A row of another kind, or one that
 // path hands back, is resolved by the general per-row code: the hint never changes a result.
+// Word i of a device array through a vector buffer load at a lane offset the compiler cannot
+// prove uniform: the load goes out with the wave's other vector loads, in issue order,
+// instead of through the scalar cache.  The value is the same in every lane.
+__device__ __forceinline__ uint32_t vload_word(const void* base, int32_t i, uint32_t zero) {
+  return __builtin_amdgcn_raw_buffer_load_b32(make_rsrc(base, (uint32_t)(i + 1) * 4u), (int)(zero + (uint32_t)i * 4u),
+                                              0, 0);
+}
+
 template <typename T>
 __global__ __launch_bounds__(NT) void topk_kernel(const KParams P) {
   const int row = blockIdx.x;
-  const int tid = threadIdx.x;
-  const float temp = P.temperature[row];
-  const int32_t k = P.top_k[row];
-  const float topp = P.top_p[row];
-  const float pen = P.penalty[row];
-  float u = P.uniforms[row];
-  const int64_t src = P.sample_idx != nullptr ? P.sample_idx[row] : (int64_t)row;
-  int32_t h0 = 0, h1 = 0;
-  row_history(P.hist_off, P.hist_slot, P.hist_len, P.hist_nslots, P.hist_cap, row, h0, h1);
+  // Without sample indices or device-resident history slots the row and its history range
+  // need no dependent load: the per-row parameters are requested first (vector loads, served
+  // in issue order ahead of the row) and the row's first chunks right behind them, before the
+  // parameters return.  Rows n_sample <= n_rows_total there (checked on the host).
+  const bool early = P.sample_idx == nullptr && P.hist_slot == nullptr;
+  float temp, topp, pen, u;
+  int32_t k, h0 = 0, h1 = 0;
+  uint4 v[TK_CPT];
+  int64_t src = row;
+  if (early) {
+    uint32_t zero;
+    asm volatile("v_mov_b32 %0, 0" : "=v"(zero));
+    const uint32_t wt = vload_word(P.temperature, row, zero), wk = vload_word(P.top_k, row, zero);
+    const uint32_t wp = vload_word(P.top_p, row, zero), wr = vload_word(P.penalty, row, zero);
+    const uint32_t wu = vload_word(P.uniforms, row, zero);
+    uint32_t w0 = 0u, w1 = 0u;
+    if (P.hist_off != nullptr) { w0 = vload_word(P.hist_off, row, zero); w1 = vload_word(P.hist_off, row + 1, zero); }
+    __builtin_amdgcn_sched_barrier(0);
+    topk_issue_early<T>(v, (const unsigned char*)P.logits + (int64_t)row * P.row_stride * T::SZ, P.vocab);
+    temp = __uint_as_float(__builtin_amdgcn_readfirstlane(wt));
+    k = (int32_t)__builtin_amdgcn_readfirstlane(wk);
+    topp = __uint_as_float(__builtin_amdgcn_readfirstlane(wp));
+    pen = __uint_as_float(__builtin_amdgcn_readfirstlane(wr));
+    u = __uint_as_float(__builtin_amdgcn_readfirstlane(wu));
+    h0 = (int32_t)__builtin_amdgcn_readfirstlane(w0);
+    h1 = (int32_t)__builtin_amdgcn_readfirstlane(w1);
+  } else {
+    temp = P.temperature[row];
+    k = P.top_k[row];
+    topp = P.top_p[row];
+    pen = P.penalty[row];
+    u = P.uniforms[row];
+    row_history(P.hist_off, P.hist_slot, P.hist_len, P.hist_nslots, P.hist_cap, row, h0, h1);
+    if (P.sample_idx != nullptr) src = P.sample_idx[row];
+  }
   const int32_t H = h1 - h0;
   const bool pen_on = pen != 1.0f && H > 0;
   const bool ok = src >= 0 && src < P.n_rows_total && h0 >= 0 && H >= 0 && H <= MAX_HIST && temp != 0.0f &&
@@ -1161,23 +1195,11 @@ __global__ __launch_bounds__(NT) void topk_kernel(const KParams P) {
     Misc* misc = reinterpret_cast<Misc*>(smem);
     uint32_t* bm = reinterpret_cast<uint32_t*>(smem + P.off_bm);
     uint64_t* cand = reinterpret_cast<uint64_t*>(smem + P.off_cand);
-    // LDS set-up: the list padded with keys that sort last, the group maxima at -inf, the
-    // counters (list length, row flags, arrival tickets), the cleared bitmap;
-    // the barrier orders them before the history bits and the candidates
-    if (tid < WAVE_CAP) cand[tid] = ~0ull;
-    if (tid < NWAVE * 8) reinterpret_cast<float*>(&misc->red)[tid] = -__builtin_inff();
-    if (tid == 0) { misc->flags = 0; misc->cand_n = 0; misc->ib[0] = 0; }
-    if (pen_on) {
-      uint4* bm4 = reinterpret_cast<uint4*>(bm);
-      const int nbw4 = (int)(((P.vocab + 31) / 32 + 3) / 4);   // the bitmap region is padded to 16 bytes
-      for (int i = tid; i < nbw4; i += NT) bm4[i] = make_uint4(0u, 0u, 0u, 0u);
-    }
-    __syncthreads();
     const unsigned char* rowp = (const unsigned char*)P.logits + src * P.row_stride * T::SZ;
     u = (u >= 0.0f) ? (u < 1.0f ? u : 0x1.fffffep-1f) : 0.0f;
     const int st = topk_stream<T>(RowArgs{P.logits, P.row_stride, P.vocab, P.hist_ids, P.out_ids, P.out_probs,
                                           P.out_info},
-                                  row, rowp, P.hist_ids + h0, temp, k, topp, pen, u, H, misc, bm, cand);
+                                  row, rowp, v, early, P.hist_ids + h0, temp, k, topp, pen, u, H, misc, bm, cand);
     if (__builtin_expect(st == 0, 1)) return;
   }
   row_general<T>((KArgs)__builtin_amdgcn_kernarg_segment_ptr());

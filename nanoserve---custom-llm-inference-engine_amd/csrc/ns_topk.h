@@ -3,16 +3,16 @@
 // row: sampler.py:31-89 for such a row with one HBM pass over it.
 //
 // Where it differs from row_fast (ns_rowfast.h), which serves rows of any kind:
-//   * the history bitmap is cleared while the per-row parameters are in flight and
-//     one barrier (which costs nothing: every wave waits for the parameters anyway)
-//     orders it before any bit is set; each lane's two history ids are requested
-//     ahead of its row chunks, so every wave sets its bits (set semantics,
-//     sampler.py:34-38) before its row data lands and the bitmap is complete at
-//     the first barrier after the stream;
+//   * without sample indices the row's first chunks are requested at entry, before
+//     the per-row parameters return; each lane's two history ids are requested as
+//     soon as they do, ahead of the rest of its row chunks, so every wave sets its
+//     bits (set semantics, sampler.py:34-38) before most of its row data lands and
+//     the bitmap is complete at the first barrier after the stream;
 //   * the row is read with the non-temporal cache policy;
-//   * a wave arriving late takes the bound (the k-th largest of the maxima of
-//     8-lane groups published so far, a lower bound of the k-th largest raw
-//     value, mapped through the temperature) while the last waves still stream;
+//   * the bound (the k-th largest of the 128 maxima of 8-lane groups, a lower
+//     bound of the k-th largest raw value, mapped through the temperature) is
+//     taken by the last wave to finish its share of the row, before the barrier
+//     that waits for it, not by one wave after that barrier;
 //   * after the barrier each wave stages its chunks that reach the bound in its
 //     own LDS slots and expands them, one element per lane, into the candidate
 //     list, with no further barrier.
@@ -28,7 +28,7 @@ namespace ns {
 
 constexpr int TK_CPT = RCPT;                // 16-byte chunks per thread (16)
 constexpr int TK_HB = 2;                    // history ids per thread requested with the row
-constexpr int TK_BOUND_TICKET = NWAVE - 3;  // the wave that arrives with this ticket takes the bound
+constexpr int TK_EARLY = 4;                 // chunks per thread requested before the parameters return
 
 template <typename T>
 __host__ __device__ __forceinline__ bool topk_fits(int64_t V) {
@@ -56,15 +56,27 @@ __device__ __forceinline__ void uniform_row_out(const RowOut& o, float u, int32_
   }
 }
 
-// The whole row path: every thread of the workgroup calls it after the set-up barrier,
-// with the LDS already prepared (padded list, zero counters, group maxima at -inf, cleared
-// bitmap).  Returns 0 when the row is resolved, 1 when it is left to the general per-row
-// code.
+// The row's first chunks, requested at kernel entry when the row is known before the
+// parameters return (no sample indices): chunk q * NT + t to thread t for q < TK_EARLY.
+template <typename T>
+__device__ __forceinline__ void topk_issue_early(uint4 (&v)[TK_CPT], const unsigned char* rowp, int64_t V) {
+  const __amdgpu_buffer_rsrc_t r = make_rsrc(rowp, (uint32_t)(V / T::EPC) * 16u);
+#pragma unroll
+  for (int q = 0; q < TK_EARLY; ++q) {
+    v[q] = buf_load16_nt(r, (uint32_t)(q * NT + threadIdx.x) * 16u);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+}
+
+// The whole row path: every thread of the workgroup calls it.  `v` holds the first TK_EARLY
+// chunks when `early` (requested by the caller at entry).  Returns 0 when the row is
+// resolved, 1 when it is left to the general per-row code.
 template <typename T>
 __device__ __forceinline__ int topk_stream(const RowArgs P, const int row, const unsigned char* rowp,
-                                           const int32_t* hp, const float temp, const int32_t k,
-                                           const float topp, const float pen, const float u, const int32_t H,
-                                           Misc* misc, uint32_t* bm, uint64_t* cand) {
+                                           uint4 (&v)[TK_CPT], const bool early, const int32_t* hp,
+                                           const float temp, const int32_t k, const float topp, const float pen,
+                                           const float u, const int32_t H, Misc* misc, uint32_t* bm,
+                                           uint64_t* cand) {
   constexpr int EPC = T::EPC;
   const int tid = threadIdx.x;
   const int lane = lane_id();
@@ -86,9 +98,24 @@ __device__ __forceinline__ int topk_stream(const RowArgs P, const int row, const
   const RowOut o{P.out_ids, P.out_probs, P.out_info, row, V};
   int32_t flags = 0;
 
+  // LDS set-up: the list padded with keys that sort last, the counters (list length, row
+  // flags, arrival tickets), the cleared bitmap.  The barrier
+  // orders them before the history bits and the candidates; it comes before the bulk of the
+  // row is requested (a wave that has issued all its loads reaches it only as the stream
+  // drains, the CU's outstanding requests being limited).
+  if (tid < WAVE_CAP) cand[tid] = ~0ull;
+  if (tid == 0) { misc->flags = 0; misc->cand_n = 0; misc->ib[0] = 0; }
+  if (pen_on) {
+    uint4* bm4 = reinterpret_cast<uint4*>(bm);
+    const int nbw4 = (int)(((V + 31) / 32 + 3) / 4);   // the bitmap region is padded to 16 bytes
+    for (int i = tid; i < nbw4; i += NT) bm4[i] = make_uint4(0u, 0u, 0u, 0u);
+  }
+  __syncthreads();
   // the first history ids (positions t and NT + t), then the token past the last full chunk
-  // at this lane (wave 0), then the row: chunk q * NT + t to thread t, zeros past the last
-  // full chunk.  A wave's loads complete in issue order, so the ids come first.
+  // at this lane (wave 0), then the rest of the row: chunk q * NT + t to thread t, zeros past
+  // the last full chunk.  A wave's loads complete in issue order, so the ids come ahead of
+  // all but the few chunks requested at entry.
+  if (!early) topk_issue_early<T>(v, rowp, V);
   int32_t hid[TK_HB];
   {
     const __amdgpu_buffer_rsrc_t rh = make_rsrc(hp, pen_on ? (uint32_t)H * 4u : 0u);
@@ -99,11 +126,10 @@ __device__ __forceinline__ int topk_stream(const RowArgs P, const int row, const
   uint32_t xtraw = 0u;
   if (wid == 0 && ntail > 0) xtraw = gather_raw<T>(make_rsrc(rowp, (uint32_t)(V * T::SZ)), nf * EPC + lane);
   __builtin_amdgcn_sched_barrier(0);
-  uint4 v[TK_CPT];
   {
     const __amdgpu_buffer_rsrc_t r = make_rsrc(rowp, (uint32_t)nf * 16u);
 #pragma unroll
-    for (int q = 0; q < TK_CPT; ++q) {
+    for (int q = TK_EARLY; q < TK_CPT; ++q) {
       v[q] = buf_load16_nt(r, (uint32_t)(q * NT + tid) * 16u);
       __builtin_amdgcn_sched_barrier(0);
     }
@@ -124,8 +150,15 @@ __device__ __forceinline__ int topk_stream(const RowArgs P, const int row, const
     }
     if (bad) atomicOr(&misc->flags, FLAG_BAD_HIST_ID);
   }
-  // every chunk's NaN-propagating maximum as the row lands (-inf past the full chunks), then
-  // the maxima of every 8-lane group (128 values of distinct elements)
+  // Every chunk's NaN-propagating maximum as the row lands (-inf past the full chunks), then
+  // the maxima of the wave's 8-lane groups, published with an arrival ticket; the last wave
+  // to arrive takes the bound from the 128 published maxima (the barrier below waits for it
+  // anyway).  They are maxima of distinct elements, so the k-th largest of them is a lower
+  // bound of the row's k-th largest raw value.  Its key is truncated to the bits a bfloat16
+  // value carries (24 for float32) and mapped through the temperature
+  // (x >= tc  <=>  x / t >= RN(taux / t)).  Measured: a bound over the first 12 to 15 chunks
+  // of each thread, taken while the last chunks still stream, is weaker and makes the whole
+  // call slower.
   float cm[TK_CPT];
   float gmax = -__builtin_inff();
   bool special = false;
@@ -133,36 +166,30 @@ __device__ __forceinline__ int topk_stream(const RowArgs P, const int row, const
   for (int q = 0; q < TK_CPT; ++q) {
     cm[q] = chunk_max<T>(v[q]);
     if ((q + 1) * NT > nf) past_row(cm[q], q * NT + tid, nf);
-    gmax = __builtin_fmaxf(gmax, cm[q]);
     special |= !(cm[q] < __builtin_inff());
+    gmax = __builtin_fmaxf(gmax, cm[q]);
   }
   gmax = __builtin_fmaxf(gmax, lane_xor(gmax, 1));
   gmax = __builtin_fmaxf(gmax, lane_xor(gmax, 2));
   gmax = __builtin_fmaxf(gmax, lane_xor(gmax, 4));
   if ((lane & 7) == 0) fs[wid * 8 + (lane >> 3)] = gmax;
+  {
+    int ticket = 0;
+    if (lane == 0) ticket = __hip_atomic_fetch_add(&misc->ib[0], 1, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_WORKGROUP);
+    if (__builtin_amdgcn_readfirstlane(ticket) == NWAVE - 1) {
+      const uint32_t kp = wave_kth_key<T::SZ == 2 ? 16 : 24>(fkey(fs[lane]), fkey(fs[64 + lane]), k);
+      const float taux = kp <= fkey(-__builtin_inff()) ? -__builtin_inff() : fkey_inv(kp);
+      const float b = lower_preimage(taux, tdiv, rdiv);
+      if (lane == 0) misc->fb[0] = b;
+    }
+  }
   float xt = -__builtin_inff();
   if (wid == 0 && lane < ntail) {
     xt = raw_float<T>(xtraw);
     special |= !(xt < __builtin_inff());
   }
-  // Arrival ticket.  The wave that arrives with TK_BOUND_TICKET takes the bound from the
-  // group maxima published so far (the others still read -inf): the k-th largest of any
-  // subset of them is a lower bound of the row's k-th largest raw value, so the bound can
-  // be taken while the last waves still stream.  Its key is truncated to the bits a
-  // bfloat16 value carries (24 for float32) and mapped through the temperature
-  // (x >= tc  <=>  x / t >= RN(taux / t)).
   const bool ws = ballot(special) != 0ull;
-  int ticket = 0;
-  if (lane == 0) {
-    is[wid] = ws ? 1 : 0;
-    ticket = __hip_atomic_fetch_add(&misc->ib[0], 1, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_WORKGROUP);
-  }
-  if (__builtin_amdgcn_readfirstlane(ticket) == TK_BOUND_TICKET) {
-    const uint32_t kp = wave_kth_key<T::SZ == 2 ? 16 : 24>(fkey(fs[lane]), fkey(fs[64 + lane]), k);
-    const float taux = kp <= fkey(-__builtin_inff()) ? -__builtin_inff() : fkey_inv(kp);
-    const float b = lower_preimage(taux, tdiv, rdiv);
-    if (lane == 0) misc->fb[0] = b;
-  }
+  if (lane == 0) is[wid] = ws ? 1 : 0;
   __syncthreads();   // group maxima, flags, the bitmap, the bound
   int spec = 0;
 #pragma unroll
