@@ -27,7 +27,9 @@ NS_KIND_OTHER = 4       # every other sampled row (top-k off or larger)
 ABI_VERSION = 5
 
 # exported symbols, as declared in include/ns_sampling.h
-EXPORTS = ("ns_abi_version", "ns_sample", "ns_sample_lds_bytes", "ns_sample_workspace_bytes", "ns_hist_state_bytes",
+NS_NOALLOC_SCRATCH_BYTES = 32 << 20   # ns_sample_noalloc's device scratch per GPU
+EXPORTS = ("ns_abi_version", "ns_sample", "ns_sample_noalloc", "ns_sample_lds_bytes", "ns_sample_workspace_bytes",
+           "ns_hist_state_bytes",
            "ns_hist_assign", "ns_hist_append", "ns_lm_head_bf16", "ns_lm_head_packed_bytes",
            "ns_lm_head_pack_bf16", "ns_lm_head_bf16_packed", "ns_last_error")
 
@@ -85,6 +87,8 @@ def load(path: str = LIB_PATH) -> ctypes.CDLL:
     lib.ns_abi_version.argtypes = []
     lib.ns_sample.restype = ctypes.c_int
     lib.ns_sample.argtypes = [ctypes.POINTER(NsSampleArgs), ctypes.c_void_p]
+    lib.ns_sample_noalloc.restype = ctypes.c_int
+    lib.ns_sample_noalloc.argtypes = [ctypes.POINTER(NsSampleArgs), ctypes.c_void_p]
     lib.ns_sample_lds_bytes.restype = ctypes.c_int
     lib.ns_sample_lds_bytes.argtypes = [ctypes.c_int64, ctypes.c_int32, ctypes.POINTER(ctypes.c_int32)]
     lib.ns_sample_workspace_bytes.restype = ctypes.c_int

@@ -6,6 +6,7 @@
 #include <cmath>
 #include <cstdio>
 #include <cstring>
+#include <mutex>
 #include <string>
 
 #include "ns_sample_kernel.h"
@@ -1205,6 +1206,12 @@ __global__ __launch_bounds__(NT) void topk_kernel(const KParams P) {
   row_general<T>((KArgs)__builtin_amdgcn_kernarg_segment_ptr());
 }
 
+// Zero n16 16-byte words at p (the no-allocation entry point's scratch, once per device).
+__global__ __launch_bounds__(256) void scratch_clear_kernel(uint4* p, int64_t n16) {
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n16; i += (int64_t)gridDim.x * 256)
+    p[i] = make_uint4(0u, 0u, 0u, 0u);
+}
+
 // ---- device-resident histories: slot s holds its length in lens[s] and its ids in
 // ids[s * cap .. s * cap + lens[s])
 
@@ -1266,6 +1273,14 @@ int hist_state_check(int32_t n_slots, int32_t capacity) {
 const int32_t* hist_state_ids(const void* state, int32_t n_slots) {
   return reinterpret_cast<const int32_t*>(static_cast<const unsigned char*>(state) + align256((int64_t)n_slots * 4));
 }
+
+// The no-allocation entry point's workspace: one array per GPU, resident for the life of the
+// process.  Host code never uses its name as an address; the address on each device comes
+// from hipGetSymbolAddress, once per device, with that device current.
+static __device__ __align__(256) unsigned char scratch[NS_NOALLOC_SCRATCH_BYTES];
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
 
 struct WsLayout {
   int64_t counters, status, stats, cand, wrow, hcnt, hmass, subfx, total;
@@ -1432,6 +1447,47 @@ int ns_lm_head_bf16_packed(const void* hidden, int64_t ld_hidden, int64_t n_hidd
 }
 
 const char* ns_last_error(void) { return g_err.c_str(); }
+
+int ns_sample_noalloc(const ns_sample_args* a, hipStream_t stream) {
+  if (a == nullptr) return fail(NS_ERR_INVALID, "args is NULL");
+  if (a->workspace != nullptr || a->workspace_bytes != 0)
+    return fail(NS_ERR_INVALID, "workspace must be NULL: ns_sample_noalloc uses the library's device scratch");
+  if (a->n_sample < 0) return fail(NS_ERR_INVALID, "n_sample < 0");
+  if (a->n_sample == 0) return NS_OK;
+  if (a->vocab <= 0 || a->vocab > NS_MAX_VOCAB)
+    return fail(NS_ERR_INVALID, "vocab must be in [1, " + std::to_string(NS_MAX_VOCAB) + "]");
+  if (a->dtype != NS_DTYPE_F32 && a->dtype != NS_DTYPE_BF16) return fail(NS_ERR_INVALID, "dtype must be f32 or bf16");
+  const int64_t need = ws_layout(a->n_sample, a->vocab, a->dtype).total;
+  if (need > (int64_t)NS_NOALLOC_SCRATCH_BYTES)
+    return fail(NS_ERR_INVALID, "this call needs " + std::to_string(need) + " bytes of workspace, above the " +
+                                    std::to_string((int64_t)NS_NOALLOC_SCRATCH_BYTES) +
+                                    "-byte scratch of ns_sample_noalloc (use ns_sample with a workspace)");
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return fail(NS_ERR_HIP, std::string("hipGetDevice: ") + hipGetErrorString(e));
+  if (dev < 0 || dev >= kMaxDevices) return fail(NS_ERR_INVALID, "device index beyond the scratch table");
+  void* ptr = nullptr;
+  {
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    ptr = g_scratch_ptr[dev];
+    if (ptr == nullptr) {
+      // first call on this device: the array's address here, and its counters cleared (the
+      // sampling kernels leave them at zero after every call)
+      e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+      if (e != hipSuccess || ptr == nullptr)
+        return fail(NS_ERR_HIP, std::string("hipGetSymbolAddress(scratch): ") + hipGetErrorString(e));
+      hipLaunchKernelGGL(ns::scratch_clear_kernel, dim3(1024), dim3(256), 0, stream, static_cast<uint4*>(ptr),
+                         (int64_t)(NS_NOALLOC_SCRATCH_BYTES / 16));
+      e = hipGetLastError();
+      if (e != hipSuccess) return fail(NS_ERR_HIP, std::string("scratch clear launch: ") + hipGetErrorString(e));
+      g_scratch_ptr[dev] = ptr;
+    }
+  }
+  ns_sample_args b = *a;
+  b.workspace = ptr;
+  b.workspace_bytes = (uint64_t)NS_NOALLOC_SCRATCH_BYTES;
+  return ns_sample(&b, stream);
+}
 
 int ns_sample_lds_bytes(int64_t vocab, int32_t max_hist, int32_t* lds_bytes) {
   if (lds_bytes == nullptr) return fail(NS_ERR_INVALID, "lds_bytes is NULL");
