@@ -43,7 +43,8 @@ HBM_PEAK_GBS = 8000.0
 MFMA_BF16_PEAK_TFLOPS = 2500.0   # dense bf16
 ROTATE = 8
 # rocprofv3 FETCH_SIZE + WRITE_SIZE summary of this workload (copy-calibrated HBM bytes per launch)
-PMC_SUMMARY = os.path.join(ROOT, "profiles", "sample_kernel_decode_b256_v128256_bf16_pmc.md")
+PMC_SUMMARY = os.path.join(ROOT, "profiles", "topk_kernel_decode_b256_v128256_bf16_pmc.md")
+CSRC = os.path.join(ROOT, PKG, "csrc")
 WORKLOAD_CFG = 2
 METRIC = "sampled rows/sec at B=256, V=128256 fp32; achieved HBM GB/s vs peak"
 
@@ -245,16 +246,82 @@ def lm_head_sweep(L, dev, batches=(256, 128, 64, 16, 1), iters=20):
         print(json.dumps({"lm_head_sweep": r}), flush=True)
 
 
+def kernel_source_hash():
+    """sha256 (first 16 hex digits) over the sampler's kernel sources, in name order."""
+    import hashlib
+
+    h = hashlib.sha256()
+    for name in sorted(os.listdir(CSRC)):
+        if name.endswith((".hip", ".h")) and name != "ns_probe.hip":
+            with open(os.path.join(CSRC, name), "rb") as f:
+                h.update(name.encode() + b"\0" + f.read())
+    return h.hexdigest()[:16]
+
+
 def measured_traffic():
-    """HBM bytes per launch from the committed rocprofv3 counter summary, or None."""
+    """HBM bytes per launch from the committed rocprofv3 counter summary -- only when the
+    summary was taken on the kernel sources present now (its ``source_sha16`` line), else None."""
+    vals = {}
     try:
         with open(PMC_SUMMARY) as f:
             for line in f:
-                if line.startswith("traffic_bytes_per_launch:"):
-                    return int(line.split(":", 1)[1])
+                if ":" in line and line.split(":", 1)[0] in ("traffic_bytes_per_launch", "source_sha16"):
+                    k, v = line.split(":", 1)
+                    vals[k] = v.strip()
+    except OSError:
+        return None
+    if vals.get("source_sha16") != kernel_source_hash() or "traffic_bytes_per_launch" not in vals:
+        return None
+    return int(vals["traffic_bytes_per_launch"])
+
+
+def cpu_model():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
     except OSError:
         pass
     return None
+
+
+def read_floor(L, sets, stream, iters=200):
+    """Time of a kernel that only streams the input sets' logits rows, in the sampler's
+    layout and cache policy (libns_probe.so): the floor of a one-pass kernel over the same
+    bytes, measured on this GPU.  Returns microseconds per call, or None when the rows do not
+    fit the probe (more than 256 KiB per row, or sample indices)."""
+    import torch
+
+    so = os.path.join(ROOT, PKG, "libns_probe.so")
+    lg = sets[0]["logits"]
+    row_bytes = lg.shape[1] * lg.element_size()
+    if not os.path.exists(so) or sets[0]["sidx"] is not None or row_bytes % 16 or row_bytes > 16 * 1024 * 16:
+        return None
+    lib = ctypes.CDLL(so)
+    lib.ns_probe_read_rows.restype = ctypes.c_int
+    lib.ns_probe_read_rows.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_int64, ctypes.c_int32,
+                                       ctypes.c_void_p, ctypes.c_void_p]
+    out = torch.empty(lg.shape[0], dtype=torch.int32, device=lg.device)
+    sh = ctypes.c_void_p(int(stream.cuda_stream))
+
+    def call(i):
+        x = sets[i % len(sets)]["logits"]
+        if lib.ns_probe_read_rows(x.data_ptr(), x.stride(0) * x.element_size(), row_bytes, x.shape[0],
+                                  out.data_ptr(), sh) != 0:
+            raise RuntimeError("ns_probe_read_rows refused its arguments")
+
+    for i in range(20):
+        call(i)
+    torch.cuda.synchronize()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for i in range(iters):
+        call(i)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / iters * 1e3
 
 
 def cpu_baseline(w, rows: int, reps: int):
@@ -278,9 +345,37 @@ def cpu_baseline(w, rows: int, reps: int):
         O.reference_restatement_multinomial(x, *args, generator=gen)
         times.append(time.perf_counter() - t0)
     med = float(np.median(times))
-    return {"value": rows / med, "unit": "rows/s", "cores": cores, "kind": "port",
+    return {"value": rows / med, "unit": "rows/s", "cores": cores, "kind": "port", "cpu_model": cpu_model(),
             "sample": f"{rows} rows of the same workload (fp32 logits, the reference's .float() input), "
-                      f"median of {reps} runs of {med:.2f} s; torch {torch.__version__} CPU"}
+                      f"median of {reps} runs of {med:.3f} s; torch {torch.__version__} CPU"}
+
+
+def small_batch_leg(L, lib, dev, stream, steps=400, cpu_reps=20):
+    """The reference's CPU-runnable case (B=8 x V=128256 fp32, t=0.8 top_k=50 top_p=0.9,
+    penalty 1.1 over 64 ids): ns_sample's kernel time on it, and the CPU sampler on the same rows."""
+    import torch
+
+    w = _pkg("workloads").make_workload(0)
+    sets = build_sets(w, dev, ROTATE, roll=True)
+    ws = L.workspace_for(dev, w.batch, w.vocab, L.NS_DTYPE_F32)
+    cargs = [make_args(L, st, ws) for st in sets]
+    sh = ctypes.c_void_p(int(stream.cuda_stream))
+    for i in range(40):
+        if lib.ns_sample(ctypes.byref(cargs[i % ROTATE]), sh) != 0:
+            raise RuntimeError(f"ns_sample failed: {L.last_error()}")
+    torch.cuda.synchronize()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for i in range(steps):
+        lib.ns_sample(ctypes.byref(cargs[i % ROTATE]), sh)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    us = e0.elapsed_time(e1) / steps * 1e3
+    cpu = cpu_baseline(w, w.batch, cpu_reps) if cpu_reps > 0 else None
+    return {"small_batch_b8_kernel_us": us, "small_batch_b8_rows_per_s": w.batch / (us * 1e-6),
+            "small_batch_b8_hbm_frac": _pkg("workloads").algorithmic_bytes(w) / (us * 1e-6) / 1e9 / HBM_PEAK_GBS,
+            "small_batch_b8_cpu_baseline": cpu}
 
 
 def main(argv=None):
@@ -392,6 +487,10 @@ def main(argv=None):
     wrap_pipe_ms = (time.perf_counter() - t1) / nwrap * 1e3
     del dh
     producer = lm_head_handoff(L, lib, dev, w, sets[0], stream) if args.config == WORKLOAD_CFG else {}
+    floor_us = read_floor(L, sets, stream)
+    floor = {} if floor_us is None else {
+        "read_floor_us": floor_us, "read_floor_frac_of_peak": bytes_per_call / (floor_us * 1e-6) / 1e9 / HBM_PEAK_GBS,
+        "kernel_over_read_floor": ms_per_step * 1e3 / floor_us}
 
     if args.copy_mb > 0:
         n = args.copy_mb * (1 << 20) // 4
@@ -403,6 +502,8 @@ def main(argv=None):
         del src, dst
 
     cpu = cpu_baseline(w, args.cpu_rows, args.cpu_reps) if args.cpu_rows > 0 else None
+    small = small_batch_leg(L, lib, dev, stream, cpu_reps=20 if args.cpu_rows > 0 else 0) \
+        if args.config == WORKLOAD_CFG else {}
     if args.config != WORKLOAD_CFG:
         desc = {0: "batch B=8 x V=128256 fp32, t=0.8 top_k=50 top_p=0.9 penalty=1.1, 64 history ids/row",
                 1: "batch B=64 x V=128256 fp32, mixed per-row parameters (greedy and sampled), 512 Zipf ids/row",
@@ -422,7 +523,7 @@ def main(argv=None):
                 "extra": {"algorithmic_bytes_per_call": bytes_per_call, "kernel_us": ms_per_step * 1e3,
                           "wall_s": wall, "wrapper_inclusive_ms": wrap_ms,
                           "wrapper_inclusive_ms_device_histories": wrap_dev_ms,
-                          "wrapper_pipelined_ms_device_histories_async_ids": wrap_pipe_ms}}
+                          "wrapper_pipelined_ms_device_histories_async_ids": wrap_pipe_ms, **floor}}
         print(json.dumps(line), flush=True)
         return 0
     line = {
@@ -450,7 +551,8 @@ def main(argv=None):
                   "wrapper_inclusive_rows_per_s": w.batch / (wrap_ms * 1e-3),
                   "wrapper_inclusive_ms_device_histories": wrap_dev_ms,
                   "wrapper_inclusive_rows_per_s_device_histories": w.batch / (wrap_dev_ms * 1e-3),
-                  "wrapper_pipelined_ms_device_histories_async_ids": wrap_pipe_ms, **producer},
+                  "wrapper_pipelined_ms_device_histories_async_ids": wrap_pipe_ms,
+                  "kernel_source_sha16": kernel_source_hash(), **floor, **small, **producer},
     }
     print(json.dumps(line), flush=True)
     return 0

@@ -17,6 +17,9 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(HERE)
 SRC = os.path.join(HERE, "csrc", "ns_sample.hip")
 OUT = os.path.join(HERE, "libns_sampling.so")
+# the benchmark's bandwidth reference (not part of the sampler's ABI)
+PROBE_SRC = os.path.join(HERE, "csrc", "ns_probe.hip")
+PROBE_OUT = os.path.join(HERE, "libns_probe.so")
 ARCH = os.environ.get("NS_OFFLOAD_ARCH", "gfx950")
 
 
@@ -25,14 +28,14 @@ def hipcc() -> str:
     return os.path.join(rocm, "bin", "hipcc")
 
 
-def build(verbose: bool = False) -> str:
-    tmp = OUT + ".tmp"
+def _compile(src: str, out: str, verbose: bool) -> None:
+    tmp = out + ".tmp"
     cmd = [
         hipcc(), f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC", "-shared",
         "-ffp-contract=off", "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
         "-Wno-unused-command-line-argument",
         "-I", os.path.join(ROOT, "include"), "-I", os.path.join(HERE, "csrc"),
-        SRC, "-o", tmp,
+        src, "-o", tmp,
     ]
     if verbose:
         print(" ".join(cmd), flush=True)
@@ -40,7 +43,12 @@ def build(verbose: bool = False) -> str:
     if res.returncode != 0:
         sys.stderr.write(res.stdout + res.stderr)
         raise RuntimeError(f"hipcc failed with exit code {res.returncode}")
-    os.replace(tmp, OUT)
+    os.replace(tmp, out)
+
+
+def build(verbose: bool = False) -> str:
+    _compile(SRC, OUT, verbose)
+    _compile(PROBE_SRC, PROBE_OUT, verbose)
     return OUT
 
 

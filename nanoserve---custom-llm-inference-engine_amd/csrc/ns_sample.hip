@@ -1282,6 +1282,19 @@ constexpr int kMaxDevices = 64;
 std::mutex g_scratch_mu;
 void* g_scratch_ptr[kMaxDevices] = {};
 
+// Per-device facts the sampler needs on every call, read once per device: the LDS limit and
+// the CU count, and each one-workgroup-per-row kernel's dynamic-LDS limit raised to the
+// device's maximum (a call never needs more than the device allows).
+struct DevInfo {
+  int max_lds = 0;
+  int n_cu = 0;
+  bool ready = false;
+};
+std::mutex g_dev_mu;
+DevInfo g_dev[kMaxDevices];
+
+int device_info(int dev, DevInfo& out);
+
 struct WsLayout {
   int64_t counters, status, stats, cand, wrow, hcnt, hmass, subfx, total;
 };
@@ -1306,6 +1319,28 @@ WsLayout ws_layout(int32_t n_sample, int64_t vocab, int32_t dtype) {
   L.subfx = L.hmass + align256(wrows * ns::WBINS * 8);
   L.total = L.subfx + align256(wrows * S * ns::WSUB * 8);
   return L;
+}
+int device_info(int dev, DevInfo& out) {
+  if (dev < 0 || dev >= kMaxDevices) return fail(NS_ERR_INVALID, "device index beyond the device table");
+  std::lock_guard<std::mutex> lock(g_dev_mu);
+  DevInfo& d = g_dev[dev];
+  if (!d.ready) {
+    hipError_t e = hipDeviceGetAttribute(&d.max_lds, hipDeviceAttributeMaxSharedMemoryPerBlock, dev);
+    if (e != hipSuccess) return fail(NS_ERR_HIP, std::string("hipDeviceGetAttribute: ") + hipGetErrorString(e));
+    e = hipDeviceGetAttribute(&d.n_cu, hipDeviceAttributeMultiprocessorCount, dev);
+    if (e != hipSuccess) return fail(NS_ERR_HIP, std::string("hipDeviceGetAttribute: ") + hipGetErrorString(e));
+    const void* fns[] = {reinterpret_cast<const void*>(&ns::sample_kernel<ns::BF16>),
+                         reinterpret_cast<const void*>(&ns::sample_kernel<ns::F32>),
+                         reinterpret_cast<const void*>(&ns::topk_kernel<ns::BF16>),
+                         reinterpret_cast<const void*>(&ns::topk_kernel<ns::F32>)};
+    for (const void* fn : fns) {
+      e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, d.max_lds);
+      if (e != hipSuccess) return fail(NS_ERR_HIP, std::string("hipFuncSetAttribute: ") + hipGetErrorString(e));
+    }
+    d.ready = true;
+  }
+  out = d;
+  return NS_OK;
 }
 }  // namespace
 
@@ -1591,9 +1626,10 @@ int ns_sample(const ns_sample_args* a, hipStream_t stream) {
   int dev = 0;
   hipError_t e = hipGetDevice(&dev);
   if (e != hipSuccess) return fail(NS_ERR_HIP, std::string("hipGetDevice: ") + hipGetErrorString(e));
-  int max_lds = 0;
-  e = hipDeviceGetAttribute(&max_lds, hipDeviceAttributeMaxSharedMemoryPerBlock, dev);
-  if (e != hipSuccess) return fail(NS_ERR_HIP, std::string("hipDeviceGetAttribute: ") + hipGetErrorString(e));
+  DevInfo di;
+  rc = device_info(dev, di);
+  if (rc != NS_OK) return rc;
+  const int max_lds = di.max_lds;
   if (lds > max_lds)
     return fail(NS_ERR_INVALID, "LDS requirement " + std::to_string(lds) + " exceeds device limit " +
                                     std::to_string(max_lds));
@@ -1606,9 +1642,7 @@ int ns_sample(const ns_sample_args* a, hipStream_t stream) {
   if (a->mode < NS_MODE_AUTO || a->mode > NS_MODE_PER_ROW) return fail(NS_ERR_INVALID, "unknown mode");
   if (a->mode == NS_MODE_SEGMENTED && a->workspace == nullptr)
     return fail(NS_ERR_INVALID, "segmented mode needs a workspace");
-  int n_cu = 0;
-  e = hipDeviceGetAttribute(&n_cu, hipDeviceAttributeMultiprocessorCount, dev);
-  if (e != hipSuccess) return fail(NS_ERR_HIP, std::string("hipDeviceGetAttribute: ") + hipGetErrorString(e));
+  const int n_cu = di.n_cu;
   bool segmented = a->workspace != nullptr && a->mode != NS_MODE_PER_ROW;
   // AUTO: per-row once the batch fills the GPU and rows fit the streaming path's registers;
   // wider rows keep the segment kernel at every batch size
@@ -1747,12 +1781,6 @@ int ns_sample(const ns_sample_args* a, hipStream_t stream) {
   const bool bf = a->dtype == NS_DTYPE_BF16;
   const bool topk = !segmented && !wide && a->row_kinds == (uint32_t)NS_KIND_SMALL_K &&
                     (bf ? ns::topk_fits<ns::BF16>(a->vocab) : ns::topk_fits<ns::F32>(a->vocab));
-  const void* fn = topk ? (bf ? reinterpret_cast<const void*>(&ns::topk_kernel<ns::BF16>)
-                              : reinterpret_cast<const void*>(&ns::topk_kernel<ns::F32>))
-                        : (bf ? reinterpret_cast<const void*>(&ns::sample_kernel<ns::BF16>)
-                              : reinterpret_cast<const void*>(&ns::sample_kernel<ns::F32>));
-  e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, lds);
-  if (e != hipSuccess) return fail(NS_ERR_HIP, std::string("hipFuncSetAttribute: ") + hipGetErrorString(e));
   if (topk) {
     if (bf) hipLaunchKernelGGL((ns::topk_kernel<ns::BF16>), grid, block, lds, stream, p);
     else hipLaunchKernelGGL((ns::topk_kernel<ns::F32>), grid, block, lds, stream, p);
