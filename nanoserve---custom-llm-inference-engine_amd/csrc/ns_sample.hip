@@ -817,7 +817,7 @@ namespace ns {
 typedef const KParams* KArgs;
 
 template <typename T>
-__device__ __attribute__((always_inline, cold)) inline void row_general(KArgs PA) {
+__device__ __attribute__((always_inline, cold)) inline void row_general(KArgs PA, const int row) {
   const KParams P = *PA;
   extern __shared__ __align__(16) unsigned char smem[];
   Misc* misc = reinterpret_cast<Misc*>(smem);
@@ -834,7 +834,6 @@ __device__ __attribute__((always_inline, cold)) inline void row_general(KArgs PA
   const int wid = wave_id();
   const bool rowthr = tid < RT;
   const bool hwave = wid == NWAVE - 1;
-  const int row = blockIdx.x;
   const int64_t V = P.vocab;
   constexpr int EPC = T::EPC;
   const int64_t nch = V / EPC;
@@ -1134,7 +1133,7 @@ __global__ __launch_bounds__(NT) void sample_kernel(const KParams P) {
       }
     }
   }
-  row_general<T>((KArgs)__builtin_amdgcn_kernarg_segment_ptr());
+  row_general<T>((KArgs)__builtin_amdgcn_kernarg_segment_ptr(), row);
 }
 
 // One workgroup per sampled row for calls whose rows are all top-k rows with
@@ -1149,7 +1148,7 @@ __device__ __forceinline__ uint32_t vload_word(const void* base, int32_t i, uint
                                               0, 0);
 }
 
-template <typename T>
+template <typename T, int NPH>
 __global__ __launch_bounds__(NT) void topk_kernel(const KParams P) {
   const int row = blockIdx.x;
   // Without sample indices or device-resident history slots the row and its history range
@@ -1170,7 +1169,7 @@ __global__ __launch_bounds__(NT) void topk_kernel(const KParams P) {
     uint32_t w0 = 0u, w1 = 0u;
     if (P.hist_off != nullptr) { w0 = vload_word(P.hist_off, row, zero); w1 = vload_word(P.hist_off, row + 1, zero); }
     __builtin_amdgcn_sched_barrier(0);
-    topk_issue_early<T>(v, (const unsigned char*)P.logits + (int64_t)row * P.row_stride * T::SZ, P.vocab);
+    topk_issue_early<T, NPH>(v, (const unsigned char*)P.logits + (int64_t)row * P.row_stride * T::SZ, P.vocab);
     temp = __uint_as_float(__builtin_amdgcn_readfirstlane(wt));
     k = (int32_t)__builtin_amdgcn_readfirstlane(wk);
     topp = __uint_as_float(__builtin_amdgcn_readfirstlane(wp));
@@ -1198,13 +1197,19 @@ __global__ __launch_bounds__(NT) void topk_kernel(const KParams P) {
     uint64_t* cand = reinterpret_cast<uint64_t*>(smem + P.off_cand);
     const unsigned char* rowp = (const unsigned char*)P.logits + src * P.row_stride * T::SZ;
     u = (u >= 0.0f) ? (u < 1.0f ? u : 0x1.fffffep-1f) : 0.0f;
-    const int st = topk_stream<T>(RowArgs{P.logits, P.row_stride, P.vocab, P.hist_ids, P.out_ids, P.out_probs,
+    const int st = topk_stream<T, NPH>(RowArgs{P.logits, P.row_stride, P.vocab, P.hist_ids, P.out_ids, P.out_probs,
                                           P.out_info},
                                   row, rowp, v, early, P.hist_ids + h0, temp, k, topp, pen, u, H, misc, bm, cand);
     if (__builtin_expect(st == 0, 1)) return;
   }
-  row_general<T>((KArgs)__builtin_amdgcn_kernarg_segment_ptr());
+  row_general<T>((KArgs)__builtin_amdgcn_kernarg_segment_ptr(), row);
 }
+
+}  // namespace ns
+
+#include "ns_split.h"
+
+namespace ns {
 
 // Zero n16 16-byte words at p (the no-allocation entry point's scratch, once per device).
 __global__ __launch_bounds__(256) void scratch_clear_kernel(uint4* p, int64_t n16) {
@@ -1261,6 +1266,27 @@ int64_t seg_elems(int32_t dtype) { return (int64_t)ns::SEG_CH * (dtype == NS_DTY
 int64_t seg_count(int64_t vocab, int32_t dtype) { return (vocab + seg_elems(dtype) - 1) / seg_elems(dtype); }
 int64_t align256(int64_t x) { return (x + 255) / 256 * 256; }
 
+// Split-path geometry for n rows of V tokens: S slices of equal length (to a chunk) per row,
+// as many as fill about one workgroup per CU, at most SP_MAXS, and at least NT chunks each
+// (every thread holds a chunk, so the bound comes from 128 full 8-lane groups: for k <= 64
+// about 90 elements reach it); cpt, a power of two up to TK_CPT, covers the longest slice.  Returns S (1: no split; more than SP_MAXS: the rows
+// are too long for the slices).
+int split_geometry(int64_t n, int64_t V, int32_t dtype, int n_cu, int32_t& cpt, int32_t& nch_out) {
+  const int64_t epc = dtype == NS_DTYPE_BF16 ? 8 : 4;
+  const int64_t nch = (V + epc - 1) / epc;
+  nch_out = (int32_t)(nch < INT32_MAX ? nch : INT32_MAX);
+  int64_t S = n > 0 ? (n_cu + n - 1) / n : 1;
+  if (S > ns::SP_MAXS) S = ns::SP_MAXS;
+  if (S > nch / ns::NT) S = nch / ns::NT;
+  const int64_t longest_cap = (int64_t)ns::NT * ns::TK_CPT;
+  if (S < (nch + longest_cap - 1) / longest_cap) S = (nch + longest_cap - 1) / longest_cap;
+  if (S < 1) S = 1;
+  const int64_t longest = (nch + S - 1) / S;
+  cpt = 1;
+  while ((int64_t)cpt * ns::NT < longest && cpt < ns::TK_CPT) cpt *= 2;
+  return S > ns::SP_MAXS ? ns::SP_MAXS + 1 : (int)S;
+}
+
 // Device-resident history state: int32 lengths[n_slots] padded to 256 bytes, then int32
 // ids[n_slots][capacity].
 int hist_state_check(int32_t n_slots, int32_t capacity) {
@@ -1296,7 +1322,7 @@ DevInfo g_dev[kMaxDevices];
 int device_info(int dev, DevInfo& out);
 
 struct WsLayout {
-  int64_t counters, status, stats, cand, wrow, hcnt, hmass, subfx, total;
+  int64_t counters, status, stats, cand, wrow, hcnt, hmass, subfx, slist, smeta, total;
 };
 // Workspace layout.  The per-row arrival counters are the only state that outlives a
 // call (each call leaves them at zero): they sit at fixed positions at the start, sized
@@ -1317,7 +1343,11 @@ WsLayout ws_layout(int32_t n_sample, int64_t vocab, int32_t dtype) {
   L.hcnt = L.wrow + align256(wrows * (int64_t)sizeof(ns::WideRow));
   L.hmass = L.hcnt + align256(wrows * ns::WBINS * 4);
   L.subfx = L.hmass + align256(wrows * ns::WBINS * 8);
-  L.total = L.subfx + align256(wrows * S * ns::WSUB * 8);
+  // split path: each slice's ordered keys and its word of flags, for up to SP_MAX_ROWS rows
+  const int64_t srows = rows < ns::SP_MAX_ROWS ? rows : ns::SP_MAX_ROWS;
+  L.slist = L.subfx + align256(wrows * S * ns::WSUB * 8);
+  L.smeta = L.slist + align256(srows * ns::SP_MAXS * ns::SP_LIST * 8);
+  L.total = L.smeta + align256(srows * ns::SP_MAXS * (int64_t)sizeof(ns::SplitMeta));
   return L;
 }
 int device_info(int dev, DevInfo& out) {
@@ -1331,8 +1361,12 @@ int device_info(int dev, DevInfo& out) {
     if (e != hipSuccess) return fail(NS_ERR_HIP, std::string("hipDeviceGetAttribute: ") + hipGetErrorString(e));
     const void* fns[] = {reinterpret_cast<const void*>(&ns::sample_kernel<ns::BF16>),
                          reinterpret_cast<const void*>(&ns::sample_kernel<ns::F32>),
-                         reinterpret_cast<const void*>(&ns::topk_kernel<ns::BF16>),
-                         reinterpret_cast<const void*>(&ns::topk_kernel<ns::F32>)};
+                         reinterpret_cast<const void*>(&ns::topk_kernel<ns::BF16, 1>),
+                         reinterpret_cast<const void*>(&ns::topk_kernel<ns::F32, 1>),
+                         reinterpret_cast<const void*>(&ns::topk_kernel<ns::BF16, 2>),
+                         reinterpret_cast<const void*>(&ns::topk_kernel<ns::F32, 2>),
+                         reinterpret_cast<const void*>(&ns::split_kernel<ns::BF16>),
+                         reinterpret_cast<const void*>(&ns::split_kernel<ns::F32>)};
     for (const void* fn : fns) {
       e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, d.max_lds);
       if (e != hipSuccess) return fail(NS_ERR_HIP, std::string("hipFuncSetAttribute: ") + hipGetErrorString(e));
@@ -1650,11 +1684,46 @@ int ns_sample(const ns_sample_args* a, hipStream_t stream) {
   if (a->mode == NS_MODE_AUTO &&
       (((int64_t)a->n_sample * 8 >= (int64_t)n_cu * 7 && fits) || a->n_sample > NS_SEG_MAX_ROWS))
     segmented = false;
+  // AUTO: a call declared to hold only small-k rows of up to two streaming phases (512 KiB)
+  // takes the one-workgroup-per-row top-k kernel at every batch size: a workgroup streams
+  // such a row in less time than several workgroups need to hand their shares over
+  const int tk_phases = a->dtype == NS_DTYPE_BF16 ? ns::topk_phases<ns::BF16>(a->vocab)
+                                                  : ns::topk_phases<ns::F32>(a->vocab);
+  if (a->mode == NS_MODE_AUTO && a->row_kinds == (uint32_t)NS_KIND_SMALL_K && tk_phases <= 2) segmented = false;
   // wide path for the rows neither the streaming nor the segment kernels take
   const bool wide = a->workspace != nullptr && a->mode != NS_MODE_PER_ROW && a->n_sample <= NS_WIDE_MAX_ROWS &&
                     (a->row_kinds == 0u || (a->row_kinds & NS_KIND_OTHER) != 0u);
   if (segmented && a->n_sample > NS_SEG_MAX_ROWS)
     return fail(NS_ERR_INVALID, "segmented mode takes at most " + std::to_string(NS_SEG_MAX_ROWS) + " rows");
+  // a call declared to hold only small-k rows, which segmented mode would split: one launch
+  // of the split-row kernel, each row over S slices merged by its last workgroup
+  int32_t sp_cpt = 1, sp_nch = 0;
+  const int sp_S = split_geometry(a->n_sample, a->vocab, a->dtype, n_cu, sp_cpt, sp_nch);
+  const bool split = segmented && a->row_kinds == (uint32_t)NS_KIND_SMALL_K && a->n_sample <= ns::SP_MAX_ROWS &&
+                     sp_S >= 2 && sp_S <= ns::SP_MAXS;
+  if (split) {
+    segmented = false;
+    if (a->workspace_bytes < (uint64_t)L.total)
+      return fail(NS_ERR_INVALID, "workspace of " + std::to_string(a->workspace_bytes) + " bytes, " +
+                                      std::to_string(L.total) + " needed (ns_sample_workspace_bytes)");
+    if (((uintptr_t)a->workspace % 256) != 0) return fail(NS_ERR_ALIGN, "workspace must be 256-byte aligned");
+    unsigned char* ws = static_cast<unsigned char*>(a->workspace);
+    ns::SplitParams sp{};
+    p.status = nullptr;
+    sp.p = p;
+    sp.lists = reinterpret_cast<uint64_t*>(ws + L.slist);
+    sp.meta = reinterpret_cast<ns::SplitMeta*>(ws + L.smeta);
+    sp.counters = reinterpret_cast<int32_t*>(ws + L.counters);
+    sp.S = sp_S;
+    sp.cpt = sp_cpt;
+    sp.nch = sp_nch;
+    const dim3 g((unsigned)(((int64_t)a->n_sample + 7) / 8 * 8 * sp_S)), bs(ns::NT);
+    if (a->dtype == NS_DTYPE_BF16) hipLaunchKernelGGL((ns::split_kernel<ns::BF16>), g, bs, lds, stream, sp);
+    else hipLaunchKernelGGL((ns::split_kernel<ns::F32>), g, bs, lds, stream, sp);
+    e = hipGetLastError();
+    if (e != hipSuccess) return fail(NS_ERR_HIP, std::string("split kernel launch: ") + hipGetErrorString(e));
+    return NS_OK;
+  }
   if (segmented || wide) {
     if (a->workspace_bytes < (uint64_t)L.total)
       return fail(NS_ERR_INVALID, "workspace of " + std::to_string(a->workspace_bytes) + " bytes, " +
@@ -1779,11 +1848,13 @@ int ns_sample(const ns_sample_args* a, hipStream_t stream) {
   //    that requests each row at entry.
   const dim3 grid((unsigned)a->n_sample), block(ns::NT);
   const bool bf = a->dtype == NS_DTYPE_BF16;
-  const bool topk = !segmented && !wide && a->row_kinds == (uint32_t)NS_KIND_SMALL_K &&
-                    (bf ? ns::topk_fits<ns::BF16>(a->vocab) : ns::topk_fits<ns::F32>(a->vocab));
-  if (topk) {
-    if (bf) hipLaunchKernelGGL((ns::topk_kernel<ns::BF16>), grid, block, lds, stream, p);
-    else hipLaunchKernelGGL((ns::topk_kernel<ns::F32>), grid, block, lds, stream, p);
+  const bool topk = !segmented && !wide && a->row_kinds == (uint32_t)NS_KIND_SMALL_K && tk_phases <= 2;
+  if (topk && tk_phases <= 1) {
+    if (bf) hipLaunchKernelGGL((ns::topk_kernel<ns::BF16, 1>), grid, block, lds, stream, p);
+    else hipLaunchKernelGGL((ns::topk_kernel<ns::F32, 1>), grid, block, lds, stream, p);
+  } else if (topk) {
+    if (bf) hipLaunchKernelGGL((ns::topk_kernel<ns::BF16, 2>), grid, block, lds, stream, p);
+    else hipLaunchKernelGGL((ns::topk_kernel<ns::F32, 2>), grid, block, lds, stream, p);
   } else if (bf) {
     hipLaunchKernelGGL((ns::sample_kernel<ns::BF16>), grid, block, lds, stream, p);
   } else {

@@ -644,11 +644,11 @@ __device__ __forceinline__ void rank_slice(const uint64_t* list, int s, uint64_t
 // each counts one slice of the list, and the group's counts are summed by lane
 // exchanges (no atomics, no second barrier).  Wave 0 then runs top-p, softmax and the
 // draw over the top-k prefix.
+// The ordering step alone: out[0..n) the keys in order, and for n <= WAVE_CAP / 2 also
+// out[WAVE_CAP..) in ascending token-id order with their sorted positions behind them.
+// Same entry conditions as block_finalize_keys; the caller places the barrier after it.
 template <int NTH>
-__device__ __forceinline__ void block_finalize_keys(const uint64_t* list, uint64_t* out, int n, int k, bool topp_on,
-                                                    float p32, float u, int row, int64_t* out_ids, float* out_probs,
-                                                    int64_t V, int32_t* out_info, int32_t flags, int32_t n_cand,
-                                                    int32_t path) {
+__device__ __forceinline__ void block_rank_keys(const uint64_t* list, uint64_t* out, int n) {
   static_assert(NTH == 4 * WAVE_CAP, "8 lanes per key up to WAVE_CAP / 2 keys, 4 lanes per key beyond");
   const int tid = threadIdx.x;
   uint64_t* sorted = out;
@@ -666,7 +666,7 @@ __device__ __forceinline__ void block_finalize_keys(const uint64_t* list, uint64
       // so the 8 slices start in distinct LDS banks; the padding past n never counts and
       // waves whose keys all lie past n skip the count.  ci counts the smaller token ids.
       if (wave_id() * 8 < n) {
-        const int cls = ((n + 7) >> 3) + 1 >> 2;   // PER = 4 * cls + 2
+        const int cls = (((n + 7) >> 3) + 1) >> 2;   // PER = 4 * cls + 2
         if (cls == 0) rank_slice<2>(list, s, ki, c, ci);
         else if (cls == 1) rank_slice<6>(list, s, ki, c, ci);
         else if (cls == 2) rank_slice<10>(list, s, ki, c, ci);
@@ -691,6 +691,19 @@ __device__ __forceinline__ void block_finalize_keys(const uint64_t* list, uint64
       if (g8) { byid[ci] = ki; vr[ci] = c; }
     }
   }
+}
+
+template <int NTH>
+__device__ __forceinline__ void block_finalize_keys(const uint64_t* list, uint64_t* out, int n, int k, bool topp_on,
+                                                    float p32, float u, int row, int64_t* out_ids, float* out_probs,
+                                                    int64_t V, int32_t* out_info, int32_t flags, int32_t n_cand,
+                                                    int32_t path) {
+  const int tid = threadIdx.x;
+  uint64_t* sorted = out;
+  uint64_t* byid = out + WAVE_CAP;
+  int32_t* vr = reinterpret_cast<int32_t*>(out + WAVE_CAP + WAVE_CAP / 2);
+  const bool g8 = n <= WAVE_CAP / 2;
+  block_rank_keys<NTH>(list, out, n);
   __syncthreads();
   if (tid >= 64) return;
   // the first 128 sorted keys in registers: row maximum, k-th largest, kept count

@@ -22,6 +22,8 @@
 // general per-row code, with the same results.
 #pragma once
 
+#include <type_traits>
+
 #include "ns_rowfast.h"
 
 namespace ns {
@@ -30,9 +32,19 @@ constexpr int TK_CPT = RCPT;                // 16-byte chunks per thread (16)
 constexpr int TK_HB = 2;                    // history ids per thread requested with the row
 constexpr int TK_EARLY = 4;                 // chunks per thread requested before the parameters return
 
+constexpr int TK_PH = NT * TK_CPT;          // chunks of one phase (one register load per thread)
+
 template <typename T>
 __host__ __device__ __forceinline__ bool topk_fits(int64_t V) {
   return row_fits<T>(V);
+}
+
+// Phases of TK_PH chunks a row of V tokens takes (the partial chunk counted).  Rows of up to
+// two phases are streamed by one workgroup.
+template <typename T>
+__host__ __device__ __forceinline__ int topk_phases(int64_t V) {
+  const int64_t nch = (V + T::EPC - 1) / T::EPC;
+  return (int)((nch + TK_PH - 1) / TK_PH);
 }
 
 // The NaN guard's uniform row (sampler.py:77-80): probability 1/V for every token and the
@@ -56,22 +68,58 @@ __device__ __forceinline__ void uniform_row_out(const RowOut& o, float u, int32_
   }
 }
 
+// A row chunk with the cache policy of its phase: non-temporal for the last phase (read once,
+// from registers), the default policy before it (its chunks that reach the bound are read
+// again, from the L2).
+template <int NPH>
+__device__ __forceinline__ uint4 topk_load(__amdgpu_buffer_rsrc_t r, uint32_t voff) {
+  if constexpr (NPH == 1) return buf_load16_nt(r, voff);
+  else return buf_load16(r, voff, 0u);
+}
+
 // The row's first chunks, requested at kernel entry when the row is known before the
 // parameters return (no sample indices): chunk q * NT + t to thread t for q < TK_EARLY.
-template <typename T>
+template <typename T, int NPH = 1>
 __device__ __forceinline__ void topk_issue_early(uint4 (&v)[TK_CPT], const unsigned char* rowp, int64_t V) {
-  const __amdgpu_buffer_rsrc_t r = make_rsrc(rowp, (uint32_t)(V / T::EPC) * 16u);
+  const int64_t nf = V / T::EPC;
+  const __amdgpu_buffer_rsrc_t r = make_rsrc(rowp, (uint32_t)(nf < TK_PH ? nf : TK_PH) * 16u);
 #pragma unroll
   for (int q = 0; q < TK_EARLY; ++q) {
-    v[q] = buf_load16_nt(r, (uint32_t)(q * NT + threadIdx.x) * 16u);
+    v[q] = topk_load<NPH>(r, (uint32_t)(q * NT + threadIdx.x) * 16u);
     __builtin_amdgcn_sched_barrier(0);
   }
 }
 
+// The k-th largest of the wave's 256 keys (a0..a3 in every lane), truncated to its top NB
+// bits, as wave_kth_key.
+template <int NB>
+__device__ __forceinline__ uint32_t wave_kth_key4(uint32_t a0, uint32_t a1, uint32_t a2, uint32_t a3, int k) {
+  uint32_t p = 0u;
+#pragma unroll
+  for (int b = 31; b >= 32 - NB; --b) {
+    const uint32_t c = p | (1u << b);
+    const int cnt = __popcll(ballot(a0 >= c)) + __popcll(ballot(a1 >= c)) + __popcll(ballot(a2 >= c)) +
+                    __popcll(ballot(a3 >= c));
+    p = cnt >= k ? c : p;
+  }
+  return p;
+}
+
+// A chunk maximum kept as the top 16 bits of its order key, rounded up (the value it stands
+// for is >= the maximum, so a chunk is never missed by a test against a bound), and back.
+__device__ __forceinline__ uint32_t key16_up(float m) {
+  const uint32_t kk = fkey(m);
+  return kk >= 0xffff0000u ? 0xffffu : (kk + 0xffffu) >> 16;
+}
+__device__ __forceinline__ float key16_val(uint32_t k16) { return fkey_inv(k16 << 16); }
+
 // The whole row path: every thread of the workgroup calls it.  `v` holds the first TK_EARLY
 // chunks when `early` (requested by the caller at entry).  Returns 0 when the row is
-// resolved, 1 when it is left to the general per-row code.
-template <typename T>
+// resolved, 1 when it is left to the general per-row code.  NPH = 2: the row streams in two
+// phases of TK_PH chunks through the same registers; the first phase's chunk maxima are
+// kept (rounded up, 16 bits each), the bound is taken over both phases' group maxima, and
+// the first phase's chunks that reach it are read again from the L2.
+template <typename T, int NPH = 1>
 __device__ __forceinline__ int topk_stream(const RowArgs P, const int row, const unsigned char* rowp,
                                            uint4 (&v)[TK_CPT], const bool early, const int32_t* hp,
                                            const float temp, const int32_t k, const float topp, const float pen,
@@ -93,7 +141,8 @@ __device__ __forceinline__ int topk_stream(const RowArgs P, const int row, const
     // sampler.py:37: score * p if score < 0 else score / p (float32, correctly rounded)
     return x < 0.0f ? x * pen : div_rn(x, pen, rpen);
   };
-  float* fs = reinterpret_cast<float*>(&misc->red);      // the 128 group maxima
+  // the group maxima (128 per phase): two phases use the staging region, free until the bound
+  float* fs = NPH == 1 ? reinterpret_cast<float*>(&misc->red) : reinterpret_cast<float*>(cand + HIT_OFF64);
   int32_t* is = reinterpret_cast<int32_t*>(misc->db);    // per-wave NaN / +inf flags
   const RowOut o{P.out_ids, P.out_probs, P.out_info, row, V};
   int32_t flags = 0;
@@ -115,7 +164,7 @@ __device__ __forceinline__ int topk_stream(const RowArgs P, const int row, const
   // at this lane (wave 0), then the rest of the row: chunk q * NT + t to thread t, zeros past
   // the last full chunk.  A wave's loads complete in issue order, so the ids come ahead of
   // all but the few chunks requested at entry.
-  if (!early) topk_issue_early<T>(v, rowp, V);
+  if (!early) topk_issue_early<T, NPH>(v, rowp, V);
   int32_t hid[TK_HB];
   {
     const __amdgpu_buffer_rsrc_t rh = make_rsrc(hp, pen_on ? (uint32_t)H * 4u : 0u);
@@ -127,10 +176,10 @@ __device__ __forceinline__ int topk_stream(const RowArgs P, const int row, const
   if (wid == 0 && ntail > 0) xtraw = gather_raw<T>(make_rsrc(rowp, (uint32_t)(V * T::SZ)), nf * EPC + lane);
   __builtin_amdgcn_sched_barrier(0);
   {
-    const __amdgpu_buffer_rsrc_t r = make_rsrc(rowp, (uint32_t)nf * 16u);
+    const __amdgpu_buffer_rsrc_t r = make_rsrc(rowp, (uint32_t)(nf < TK_PH ? nf : TK_PH) * 16u);
 #pragma unroll
     for (int q = TK_EARLY; q < TK_CPT; ++q) {
-      v[q] = buf_load16_nt(r, (uint32_t)(q * NT + tid) * 16u);
+      v[q] = topk_load<NPH>(r, (uint32_t)(q * NT + tid) * 16u);
       __builtin_amdgcn_sched_barrier(0);
     }
   }
@@ -162,22 +211,51 @@ __device__ __forceinline__ int topk_stream(const RowArgs P, const int row, const
   float cm[TK_CPT];
   float gmax = -__builtin_inff();
   bool special = false;
+  uint32_t pk[TK_CPT / 2];   // two phases: the first phase's chunk maxima, 16 bits each
+  if constexpr (NPH == 2) {
+    // the first phase reduced to its chunk maxima, then the second phase, chunks
+    // TK_PH + q * NT + t, through the same registers (refilling each register as soon as its
+    // first-phase chunk is reduced measured no faster)
+    const __amdgpu_buffer_rsrc_t r2 = make_rsrc(rowp + (int64_t)TK_PH * 16, (uint32_t)(nf > TK_PH ? nf - TK_PH : 0) * 16u);
+#pragma unroll
+    for (int q = 0; q < TK_CPT; ++q) {
+      cm[q] = chunk_max<T>(v[q]);
+      if ((q + 1) * NT > nf) past_row(cm[q], q * NT + tid, nf);
+      special |= !(cm[q] < __builtin_inff());
+      gmax = __builtin_fmaxf(gmax, cm[q]);
+      if (q & 1) pk[q >> 1] = key16_up(cm[q - 1]) | (key16_up(cm[q]) << 16);
+    }
+#pragma unroll
+    for (int q = 0; q < TK_CPT; ++q) {
+      v[q] = buf_load16_nt(r2, (uint32_t)(q * NT + tid) * 16u);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    gmax = __builtin_fmaxf(gmax, lane_xor(gmax, 1));
+    gmax = __builtin_fmaxf(gmax, lane_xor(gmax, 2));
+    gmax = __builtin_fmaxf(gmax, lane_xor(gmax, 4));
+    if ((lane & 7) == 0) fs[wid * 8 + (lane >> 3)] = gmax;
+    gmax = -__builtin_inff();
+  }
+  constexpr int C0 = NPH == 2 ? TK_PH : 0;   // first chunk held in the registers now
 #pragma unroll
   for (int q = 0; q < TK_CPT; ++q) {
     cm[q] = chunk_max<T>(v[q]);
-    if ((q + 1) * NT > nf) past_row(cm[q], q * NT + tid, nf);
+    if (C0 + (q + 1) * NT > nf) past_row(cm[q], C0 + q * NT + tid, nf);
     special |= !(cm[q] < __builtin_inff());
     gmax = __builtin_fmaxf(gmax, cm[q]);
   }
   gmax = __builtin_fmaxf(gmax, lane_xor(gmax, 1));
   gmax = __builtin_fmaxf(gmax, lane_xor(gmax, 2));
   gmax = __builtin_fmaxf(gmax, lane_xor(gmax, 4));
-  if ((lane & 7) == 0) fs[wid * 8 + (lane >> 3)] = gmax;
+  if ((lane & 7) == 0) fs[(NPH - 1) * 128 + wid * 8 + (lane >> 3)] = gmax;
   {
     int ticket = 0;
     if (lane == 0) ticket = __hip_atomic_fetch_add(&misc->ib[0], 1, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_WORKGROUP);
     if (__builtin_amdgcn_readfirstlane(ticket) == NWAVE - 1) {
-      const uint32_t kp = wave_kth_key<T::SZ == 2 ? 16 : 24>(fkey(fs[lane]), fkey(fs[64 + lane]), k);
+      const uint32_t kp =
+          NPH == 1 ? wave_kth_key<T::SZ == 2 ? 16 : 24>(fkey(fs[lane]), fkey(fs[64 + lane]), k)
+                   : wave_kth_key4<T::SZ == 2 ? 16 : 24>(fkey(fs[lane]), fkey(fs[64 + lane]), fkey(fs[128 + lane]),
+                                                         fkey(fs[192 + lane]), k);
       const float taux = kp <= fkey(-__builtin_inff()) ? -__builtin_inff() : fkey_inv(kp);
       const float b = lower_preimage(taux, tdiv, rdiv);
       if (lane == 0) misc->fb[0] = b;
@@ -209,7 +287,7 @@ __device__ __forceinline__ int topk_stream(const RowArgs P, const int row, const
     uniform_row_out(o, u, flags, anynan ? __builtin_nanf("") : __builtin_inff());
     return 0;
   }
-  const float tc = misc->fb[0];
+  float tc = misc->fb[0];
   // fewer than k finite group maxima (a row of mostly -inf): the general code takes it
   if (!(tc > -__builtin_inff())) { __syncthreads(); return 1; }
   // Chunks whose maximum reaches tc go to the wave's own LDS slots, then the wave expands
@@ -221,17 +299,6 @@ __device__ __forceinline__ int topk_stream(const RowArgs P, const int row, const
   // waves, four to a SIMD, so it is kept to few instructions per wave.
   uint4* hdat = reinterpret_cast<uint4*>(cand + HIT_OFF64) + wid * HIT_PER_WAVE;
   int32_t* hidx = reinterpret_cast<int32_t*>(cand + HIT_IDX_OFF64) + wid * HIT_PER_WAVE;
-  int nh = 0;             // this wave's hit chunks (wave-uniform)
-#pragma unroll
-  for (int q = 0; q < TK_CPT; ++q) {
-    const bool hit = cm[q] >= tc;   // -inf past the row, and tc > -inf
-    const uint64_t m = ballot(hit);
-    if (m != 0ull) {
-      const int pos = nh + lanes_below(m);
-      if (hit && pos < HIT_PER_WAVE) { hdat[pos] = v[q]; hidx[pos] = q * NT + tid; }
-      nh += __popcll(m);
-    }
-  }
   const bool unit_t = tdiv == 1.0f;
   auto take_key = [&](float x, uint32_t id, bool live) {
     if (live && pen_on && ((bm[id >> 5] >> (id & 31)) & 1u)) x = pen_val(x);
@@ -247,23 +314,144 @@ __device__ __forceinline__ int topk_stream(const RowArgs P, const int row, const
     const int pos = base + lanes_below(m);
     if (t && pos < WAVE_CAP) cand[pos] = key;   // past it: counted only
   };
-  if (nh > HIT_PER_WAVE) {
-    // more hit chunks than slots: the count goes past WAVE_CAP and the general code
-    // takes the row
-    if (lane == 0) atomicAdd(&misc->cand_n, WAVE_CAP + 1);
-  } else {
-    for (int j = lane; j < ((nh * EPC + 63) & ~63); j += 64) {
-      const bool live = j < nh * EPC;
-      const int slot = live ? j / EPC : 0, e = j % EPC;
-      const int32_t ci = hidx[slot];
-      const uint4 ch = hdat[slot];
-      const float x = elem_sel<T>(ch, e);
-      take_key(x, (uint32_t)(ci * EPC + e), live && x >= tc);
+  // Staging and expansion.  With `reread`, every chunk that reaches tc is staged by index
+  // (top bit set) and read again from memory: the row's registers are no longer live.
+  auto collect = [&](auto reread) {
+    constexpr bool RR = decltype(reread)::value;
+    int nh = 0;             // this wave's hit chunks (wave-uniform)
+    if constexpr (NPH == 2) {
+      // first-phase chunks whose kept maximum reaches tc: only their index is staged, with
+      // the top bit set (the expansion reads them again)
+#pragma unroll
+      for (int q = 0; q < TK_CPT; ++q) {
+        const bool hit = key16_val((pk[q >> 1] >> ((q & 1) * 16)) & 0xffffu) >= tc;
+        const uint64_t m = ballot(hit);
+        if (m != 0ull) {
+          const int pos = nh + lanes_below(m);
+          if (hit && pos < HIT_PER_WAVE) hidx[pos] = (int32_t)(0x80000000u | (uint32_t)(q * NT + tid));
+          nh += __popcll(m);
+        }
+      }
     }
-  }
-  if (ntail > 0 && wid == 0) take_key(xt, (uint32_t)(nf * EPC + lane), lane < ntail);
+#pragma unroll
+    for (int q = 0; q < TK_CPT; ++q) {
+      const bool hit = cm[q] >= tc;   // -inf past the row, and tc > -inf
+      const uint64_t m = ballot(hit);
+      if (m != 0ull) {
+        const int pos = nh + lanes_below(m);
+        if (hit && pos < HIT_PER_WAVE) {
+          if constexpr (RR) {
+            hidx[pos] = (int32_t)(0x80000000u | (uint32_t)(C0 + q * NT + tid));
+          } else {
+            hdat[pos] = v[q];
+            hidx[pos] = C0 + q * NT + tid;
+          }
+        }
+        nh += __popcll(m);
+      }
+    }
+    if (nh > HIT_PER_WAVE) {
+      // more hit chunks than slots: the count goes past WAVE_CAP and the general code
+      // takes the row
+      if (lane == 0) atomicAdd(&misc->cand_n, WAVE_CAP + 1);
+    } else {
+      for (int j = lane; j < ((nh * EPC + 63) & ~63); j += 64) {
+        const bool live = j < nh * EPC;
+        const int slot = live ? j / EPC : 0, e = j % EPC;
+        int32_t ci = hidx[slot];
+        uint4 ch;
+        if ((NPH == 2 || RR) && ci < 0) {   // staged by index: read again
+          ci &= 0x7fffffff;
+          ch = rowv[ci];
+        } else {
+          ch = hdat[slot];
+        }
+        const float x = elem_sel<T>(ch, e);
+        take_key(x, (uint32_t)(ci * EPC + e), live && x >= tc);
+      }
+    }
+    if (ntail > 0 && wid == 0) take_key(xt, (uint32_t)(nf * EPC + lane), lane < ntail);
+  };
+  collect(std::false_type{});
   __syncthreads();   // the list complete
-  const int n = misc->cand_n;
+  int n = misc->cand_n;
+  if (n < k && pen_on) {
+    // The penalty took the list under k keys (history tokens among the largest values): the
+    // bound again, from the maxima of penalized values (the bitmap is complete), and the list
+    // again, every staged chunk read from memory.  At least k penalized values reach the new
+    // bound.  Two phases: the first phase is read again whole (its kept maxima are rounded up,
+    // not lower bounds); its chunks are then staged against the kept maxima as before, which
+    // the penalty never raises.
+    if constexpr (NPH == 2) {
+      float g1 = -__builtin_inff();
+      for (int q0 = 0; q0 < TK_CPT; q0 += 4) {
+        uint4 w[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) w[j] = rowv[(q0 + j) * NT + tid];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const uint32_t hb = T::bits(bm, (q0 + j) * NT + tid);
+#pragma unroll
+          for (int e = 0; e < EPC; ++e) {
+            const float x = T::elem(w[j], e);
+            g1 = __builtin_fmaxf(g1, ((hb >> e) & 1u) ? pen_val(x) : x);
+          }
+        }
+      }
+      g1 = __builtin_fmaxf(g1, lane_xor(g1, 1));
+      g1 = __builtin_fmaxf(g1, lane_xor(g1, 2));
+      g1 = __builtin_fmaxf(g1, lane_xor(g1, 4));
+      if ((lane & 7) == 0) fs[wid * 8 + (lane >> 3)] = g1;
+    }
+    // the chunks in registers: those holding history tokens read again for their penalized
+    // maxima, four at a time
+    float g2 = -__builtin_inff();
+#pragma unroll
+    for (int q0 = 0; q0 < TK_CPT; q0 += 4) {
+      uint32_t hbq[4];
+      uint4 w[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int c = C0 + (q0 + j) * NT + tid;
+        hbq[j] = c < nf ? T::bits(bm, c) : 0u;
+        w[j] = make_uint4(0u, 0u, 0u, 0u);
+        if (hbq[j] != 0u) w[j] = rowv[c];
+      }
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        if (hbq[j] != 0u) {
+          float mx = -__builtin_inff();
+#pragma unroll
+          for (int e = 0; e < EPC; ++e) {
+            const float x = T::elem(w[j], e);
+            mx = __builtin_fmaxf(mx, ((hbq[j] >> e) & 1u) ? pen_val(x) : x);
+          }
+          cm[q0 + j] = mx;
+        }
+        g2 = __builtin_fmaxf(g2, cm[q0 + j]);
+      }
+    }
+    g2 = __builtin_fmaxf(g2, lane_xor(g2, 1));
+    g2 = __builtin_fmaxf(g2, lane_xor(g2, 2));
+    g2 = __builtin_fmaxf(g2, lane_xor(g2, 4));
+    if ((lane & 7) == 0) fs[(NPH - 1) * 128 + wid * 8 + (lane >> 3)] = g2;
+    if (tid < WAVE_CAP) cand[tid] = ~0ull;
+    if (tid == 0) misc->cand_n = 0;
+    __syncthreads();
+    if (wid == 0) {
+      const uint32_t kp =
+          NPH == 1 ? wave_kth_key<T::SZ == 2 ? 16 : 24>(fkey(fs[lane]), fkey(fs[64 + lane]), k)
+                   : wave_kth_key4<T::SZ == 2 ? 16 : 24>(fkey(fs[lane]), fkey(fs[64 + lane]), fkey(fs[128 + lane]),
+                                                         fkey(fs[192 + lane]), k);
+      const float taux = kp <= fkey(-__builtin_inff()) ? -__builtin_inff() : fkey_inv(kp);
+      if (lane == 0) misc->fb[0] = lower_preimage(taux, tdiv, rdiv);
+    }
+    __syncthreads();
+    tc = misc->fb[0];
+    if (tc > -__builtin_inff()) collect(std::true_type{});
+    __syncthreads();
+    n = misc->cand_n;
+  }
   if (n > WAVE_CAP || n < k) { __syncthreads(); return 1; }
   zero_probs(o);
   block_finalize_keys<NT>(cand, cand + WAVE_CAP, n, k, topp < 1.0f, topp, u, row, P.out_ids, P.out_probs, V,

@@ -31,14 +31,18 @@ C = pkg("config")
 # of the call's parameters.  "topk" is per-row mode declared to hold only small-k
 # rows: every call takes the kernel that requests each row at entry, and rows of
 # other kinds (greedy, top-k off, penalties below 1) its fallback to the general
-# per-row code (the hint never changes a result).
+# per-row code (the hint never changes a result).  "split" is segmented mode declared
+# to hold only small-k rows: calls of up to 64 rows take the split-row kernel (each row
+# over several workgroups, merged by the last to arrive), and rows of other kinds its
+# fallback to the general per-row code.
 PATHS = {"segmented": ("auto", L.NS_MODE_SEGMENTED), "per-row": (None, L.NS_MODE_PER_ROW),
-         "shipped": ("auto", L.NS_MODE_AUTO), "topk": (None, L.NS_MODE_PER_ROW)}
+         "shipped": ("auto", L.NS_MODE_AUTO), "topk": (None, L.NS_MODE_PER_ROW),
+         "split": ("auto", L.NS_MODE_SEGMENTED)}
 
 
 def path_kinds(path):
     """The row_kinds argument run_gpu takes for the named path."""
-    return "hint" if path == "shipped" else (L.NS_KIND_SMALL_K if path == "topk" else 0)
+    return "hint" if path == "shipped" else (L.NS_KIND_SMALL_K if path in ("topk", "split") else 0)
 
 PROB_RTOL = 1e-5
 PROB_ATOL = 1e-12

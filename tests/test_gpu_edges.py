@@ -9,7 +9,7 @@ import pytest
 import torch
 
 from conftest import pkg
-from parity import PATHS, compare, run_gpu, run_path
+from parity import PATHS, compare, path_kinds, run_gpu, run_path
 
 W = pkg("workloads")
 L = pkg("_lib")
@@ -103,8 +103,7 @@ def test_invalid_rows_and_history_ids_are_reported(device, path):
     out = torch.full((B,), -7, dtype=torch.int64, device=device)
     info = torch.zeros((B, L.NS_INFO_WORDS), dtype=torch.int32, device=device)
     ws, mode = PATHS[path]
-    kinds = L.row_kinds(np.ones(B), np.full(B, 50), V) if path == "shipped" else (
-        L.NS_KIND_SMALL_K if path == "topk" else 0)
+    kinds = L.row_kinds(np.ones(B), np.full(B, 50), V) if path == "shipped" else path_kinds(path)
     print(f"[edges] invalid rows path={path}", flush=True)
     L.sample_raw(torch.from_numpy(flat).to(device), t, k, p, pen, u, out,
                  sample_idx=torch.from_numpy(sidx).to(device),
@@ -144,7 +143,7 @@ def test_misaligned_vocab_with_invalid_sample_indices(device, path):
     out = torch.full((B,), -7, dtype=torch.int64, device=device)
     info = torch.zeros((B, L.NS_INFO_WORDS), dtype=torch.int32, device=device)
     ws, mode = PATHS[path]
-    kinds = L.row_kinds(t_np, k_np, V) if path == "shipped" else (L.NS_KIND_SMALL_K if path == "topk" else 0)
+    kinds = L.row_kinds(t_np, k_np, V) if path == "shipped" else path_kinds(path)
     logits = torch.from_numpy(flat).to(device)
     assert (logits.stride(0) * 4) % 16 != 0
     print(f"[edges] misaligned vocab with invalid sample indices path={path}", flush=True)

@@ -47,7 +47,7 @@ def _check(w, device, path="segmented", **kw):
 @pytest.mark.parametrize("cfg", [0, 2])
 def test_config_topk_rows(device, cfg, path):
     g, r, stats = _check(W.make_workload(cfg), device, path)
-    if cfg == 2 or path in ("segmented", "shipped"):
+    if cfg == 2 or path in ("segmented", "shipped", "split"):
         assert stats["paths"].get(6, 0) == len(r.ids)   # every row finalised inside one wave
 
 
