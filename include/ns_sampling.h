@@ -26,7 +26,7 @@
 extern "C" {
 #endif
 
-#define NS_ABI_VERSION 5
+#define NS_ABI_VERSION 6
 
 #define NS_OK 0
 #define NS_ERR_INVALID 1   /* bad argument (message says which) */
@@ -156,6 +156,17 @@ int ns_hist_assign(void* state, int32_t n_slots, int32_t capacity, int32_t slot,
  * and counted in *overflow (device int32, or NULL).  Asynchronous on stream. */
 int ns_hist_append(void* state, int32_t n_slots, int32_t capacity, const int32_t* slots, const int64_t* token_ids,
                    int32_t n, int32_t* overflow, hipStream_t stream);
+
+/* The draw's uniforms for seeded requests (SamplingParams.seed, nanoserve/config.py:79, which
+ * the reference declares but never reads; its sampler.py:26 accepts per-row generators and
+ * ignores them): uniforms[rows ? rows[j] : j] = Philox4x32-10 (Salmon et al., SC 2011) of the
+ * counter (steps[j] low, steps[j] high, 0x4E53534D, 0) under the key (seeds[j] low, seeds[j]
+ * high), first output word >> 8, times 2^-24: a float32 in [0, 1).  steps[j] is the number of
+ * tokens in the row's history, so a request draws the same uniform for the same history on
+ * every call and a new one at every decode step.  seeds, steps: n device values; rows: n device
+ * row indices, or NULL.  Asynchronous on stream; the uniforms then go to ns_sample. */
+int ns_seeded_uniforms(const uint64_t* seeds, const int64_t* steps, const int32_t* rows, int32_t n, float* uniforms,
+                       hipStream_t stream);
 
 /* The logits producer in front of ns_sample (bf16 lm_head GEMM, MFMA, fp32 accumulation):
  *   logits[r][v] = bf16_rne( sum_c hidden[rows ? rows[r] : r][c] * weight[v][c] )

@@ -24,13 +24,13 @@ NS_MODE_PER_ROW = 2
 NS_KIND_GREEDY = 1      # row_kinds: greedy rows (temperature 0)
 NS_KIND_SMALL_K = 2     # sampled rows with 1 <= top_k <= 64 and top_k < vocab
 NS_KIND_OTHER = 4       # every other sampled row (top-k off or larger)
-ABI_VERSION = 5
+ABI_VERSION = 6
 
 # exported symbols, as declared in include/ns_sampling.h
 NS_NOALLOC_SCRATCH_BYTES = 32 << 20   # ns_sample_noalloc's device scratch per GPU
 EXPORTS = ("ns_abi_version", "ns_sample", "ns_sample_noalloc", "ns_sample_lds_bytes", "ns_sample_workspace_bytes",
            "ns_hist_state_bytes",
-           "ns_hist_assign", "ns_hist_append", "ns_lm_head_bf16", "ns_lm_head_packed_bytes",
+           "ns_hist_assign", "ns_hist_append", "ns_seeded_uniforms", "ns_lm_head_bf16", "ns_lm_head_packed_bytes",
            "ns_lm_head_pack_bf16", "ns_lm_head_bf16_packed", "ns_last_error")
 
 
@@ -102,6 +102,9 @@ def load(path: str = LIB_PATH) -> ctypes.CDLL:
     lib.ns_hist_append.restype = ctypes.c_int
     lib.ns_hist_append.argtypes = [ctypes.c_void_p, ctypes.c_int32, ctypes.c_int32, ctypes.c_void_p, ctypes.c_void_p,
                                    ctypes.c_int32, ctypes.c_void_p, ctypes.c_void_p]
+    lib.ns_seeded_uniforms.restype = ctypes.c_int
+    lib.ns_seeded_uniforms.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int32,
+                                       ctypes.c_void_p, ctypes.c_void_p]
     lib.ns_lm_head_bf16.restype = ctypes.c_int
     lib.ns_lm_head_bf16.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_int64, ctypes.c_void_p, ctypes.c_void_p,
                                     ctypes.c_int64,
@@ -354,6 +357,36 @@ def lm_head_bf16(hidden, weight, rows=None, out=None, stream=None):
                                      int(weight.stride(0)),
                                      _ptr(out), int(out.stride(0)), m, n, k, sh))
     return out
+
+
+def seeded_uniforms(seeds, steps, rows, out, stream=None) -> None:
+    """out[rows[j]] = the Philox4x32-10 uniform of (seeds[j], steps[j]) (ns_seeded_uniforms).
+
+    ``seeds``: host sequence of Python ints (taken modulo 2^64); ``steps``: host sequence of
+    history lengths; ``rows``: host sequence of row indices into ``out`` ((B,) float32 device
+    tensor).  The three arrays travel to the device in one copy.
+    """
+    import numpy as np
+    import torch
+
+    n = len(rows)
+    if n == 0:
+        return
+    if not (len(seeds) == len(steps) == n):
+        raise ValueError("seeds, steps and rows must have one entry per seeded row")
+    for r in rows:
+        if not 0 <= int(r) < out.numel():
+            raise ValueError("seeded row index outside the uniforms tensor")
+    host = np.empty(3 * n, dtype=np.int64)
+    host[:n] = np.array([int(x) & 0xFFFFFFFFFFFFFFFF for x in seeds], dtype=np.uint64).view(np.int64)
+    host[n:2 * n] = np.asarray(steps, dtype=np.int64)
+    host[2 * n:] = np.asarray(rows, dtype=np.int64)
+    dev = torch.from_numpy(host).to(out.device)
+    rows32 = dev[2 * n:].to(torch.int32)
+    if stream is None:
+        stream = torch.cuda.current_stream(out.device)
+    check(load().ns_seeded_uniforms(_ptr(dev), _ptr(dev) + 8 * n, _ptr(rows32), n, _ptr(out),
+                                    ctypes.c_void_p(int(stream.cuda_stream))))
 
 
 def hist_state_bytes(n_slots: int, capacity: int) -> int:

@@ -3,9 +3,12 @@
 Same fields, types and defaults as the reference's ``SamplingParams``
 (nanoserve/config.py:68-79), so request objects built by the reference's API
 layer (nanoserve/api/server.py:51-67) can be handed to this sampler unchanged.
-Only ``temperature``, ``top_p``, ``top_k``, ``repetition_penalty`` and ``seed``
-are read by the sampler; ``max_tokens``, ``stop_token_ids``, ``stop`` and
-``ignore_eos`` belong to the scheduler (nanoserve/scheduler/scheduler.py:295-306).
+The sampler reads ``temperature``, ``top_p``, ``top_k`` and
+``repetition_penalty``, and ``seed`` when no uniforms are passed: a seeded row
+draws a Philox4x32-10 uniform keyed by the seed and counted by the row's
+history length (the reference declares ``seed`` but never reads it).
+``max_tokens``, ``stop_token_ids``, ``stop`` and ``ignore_eos`` belong to the
+scheduler (nanoserve/scheduler/scheduler.py:295-306).
 """
 from __future__ import annotations
 

@@ -13,6 +13,7 @@
 #include "ns_segment.h"
 #include "ns_wide.h"
 #include "ns_lmhead.h"
+#include "ns_rng.h"
 #include "ns_sampling.h"
 
 static_assert(ns::WIDE_MAX_ROWS == NS_WIDE_MAX_ROWS, "wide-path row limit");
@@ -1211,6 +1212,14 @@ __global__ __launch_bounds__(NT) void topk_kernel(const KParams P) {
 
 namespace ns {
 
+// uniforms[rows ? rows[j] : j] = seeded_uniform(seeds[j], steps[j]) for j < n.
+__global__ __launch_bounds__(256) void seeded_uniforms_kernel(const uint64_t* seeds, const int64_t* steps,
+                                                               const int32_t* rows, int32_t n, float* uniforms) {
+  const int j = blockIdx.x * 256 + threadIdx.x;
+  if (j >= n) return;
+  uniforms[rows != nullptr ? rows[j] : j] = seeded_uniform(seeds[j], steps[j]);
+}
+
 // Zero n16 16-byte words at p (the no-allocation entry point's scratch, once per device).
 __global__ __launch_bounds__(256) void scratch_clear_kernel(uint4* p, int64_t n16) {
   for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n16; i += (int64_t)gridDim.x * 256)
@@ -1404,6 +1413,19 @@ int ns_hist_assign(void* state, int32_t n_slots, int32_t capacity, int32_t slot,
   hipLaunchKernelGGL(ns::hist_assign_kernel, dim3(blocks), dim3(256), 0, stream, lens, store, capacity, slot, ids, n);
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) return fail(NS_ERR_HIP, std::string("hist_assign launch: ") + hipGetErrorString(e));
+  return NS_OK;
+}
+
+int ns_seeded_uniforms(const uint64_t* seeds, const int64_t* steps, const int32_t* rows, int32_t n, float* uniforms,
+                       hipStream_t stream) {
+  if (n < 0) return fail(NS_ERR_INVALID, "n must be >= 0");
+  if (n == 0) return NS_OK;
+  if (seeds == nullptr || steps == nullptr || uniforms == nullptr)
+    return fail(NS_ERR_INVALID, "seeds, steps and uniforms must not be NULL");
+  hipLaunchKernelGGL(ns::seeded_uniforms_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream, seeds, steps,
+                     rows, n, uniforms);
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return fail(NS_ERR_HIP, std::string("seeded_uniforms launch: ") + hipGetErrorString(e));
   return NS_OK;
 }
 

@@ -14,9 +14,12 @@ Additions, all keyword-only and optional:
   ``sample_indices``, scheduler.py:240-246), so the caller can pass the whole
   flat logits tensor and skip the ``index_select`` at engine.py:235.
 * ``uniforms``: one float32 in [0, 1) per sampled row for the inverse-CDF
-  draw.  When omitted they are drawn on the device from ``generators[i]``
-  where given (the reference accepts ``generators`` but never uses them,
-  sampler.py:26) and from the global CUDA generator otherwise.
+  draw.  When omitted, a row whose ``SamplingParams.seed`` is set draws a
+  Philox4x32-10 uniform keyed by the seed and counted by its history length
+  (``ns_seeded_uniforms``: the same seed and history give the same token on
+  every call); the other rows draw from ``generators[i]`` where given (the
+  reference accepts ``generators`` and ``seed`` but uses neither,
+  sampler.py:26, config.py:79) and from the global CUDA generator otherwise.
 * ``logits`` may be float32 or bfloat16 (bf16 is read directly; no
   ``.float()`` copy as at engine.py:236).
 * ``device_histories`` / ``history_requests``: histories kept on the device
@@ -278,7 +281,17 @@ class Sampler:
             if sample_indices.numel() != B:
                 raise ValueError("sample_indices must have one entry per sampling params")
         if uniforms is None:
-            uniforms = self._draw_uniforms(B, dev, generators)
+            # rows whose request carries a seed draw a Philox uniform keyed by it and counted by
+            # the history length (reproducible); the rest from ``generators`` or the device RNG
+            seeded = [i for i, p in enumerate(sampling_params_list) if p.seed is not None]
+            uniforms = self._draw_uniforms(B, dev, generators, skip=set(seeded))
+            if seeded:
+                if device_histories is not None:
+                    steps = [int(device_histories._len[int(slots[i])]) for i in seeded]
+                else:
+                    steps = [len(history_token_ids[i]) if history_token_ids is not None and
+                             history_token_ids[i] is not None else 0 for i in seeded]
+                _lib.seeded_uniforms([sampling_params_list[i].seed for i in seeded], steps, seeded, uniforms)
         else:
             uniforms = uniforms.to(device=dev, dtype=torch.float32).contiguous()
             if uniforms.numel() != B:
@@ -308,10 +321,12 @@ class Sampler:
         return SampledIds(out, host, ev)
 
     @staticmethod
-    def _draw_uniforms(B: int, dev, generators) -> torch.Tensor:
+    def _draw_uniforms(B: int, dev, generators, skip=frozenset()) -> torch.Tensor:
+        if len(skip) == B:
+            return torch.empty(B, device=dev, dtype=torch.float32)   # every row seeded
         u = torch.rand(B, device=dev, dtype=torch.float32)
         if generators is not None:
             for i, g in enumerate(generators[:B]):
-                if g is not None:
+                if g is not None and i not in skip:
                     u[i] = torch.rand(1, generator=g, device=g.device, dtype=torch.float32).to(dev)[0]
         return u
