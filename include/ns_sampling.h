@@ -49,7 +49,7 @@ extern "C" {
 #define NS_INFO_WORDS 8         /* int32 words per row in out_info */
 #define NS_SEG_MAX_ROWS 16384   /* most rows a segmented call takes (AUTO switches to per-row above) */
 #define NS_WIDE_MAX_ROWS 4096   /* most rows a call splits over segment workgroups (NS_KIND_OTHER rows) */
-#define NS_NOALLOC_SCRATCH_BYTES (32ull << 20)   /* device scratch of ns_sample_noalloc, per GPU */
+#define NS_NOALLOC_SCRATCH_BYTES (80ull << 20)   /* device scratch of ns_sample_noalloc, per GPU */
 
 /* Per-row diagnostics written to out_info[row * NS_INFO_WORDS + w]:
  *   w=0 path (1 greedy, 2 uniform/NaN guard, 3 top-k set, 4 generic set, 5 large draw,
@@ -123,7 +123,7 @@ int ns_sample(const ns_sample_args* args, hipStream_t stream);
 /* ns_sample without a caller workspace, for callers that cannot allocate device memory
  * (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).  No
  * counterpart in the reference.  args->workspace must be NULL and workspace_bytes 0: the call
- * uses a fixed device array of NS_NOALLOC_SCRATCH_BYTES (32 MiB) that the library holds on
+ * uses a fixed device array of NS_NOALLOC_SCRATCH_BYTES (80 MiB) that the library holds on
  * each GPU it runs on until the process ends, and allocates nothing.  Calls whose workspace
  * (ns_sample_workspace_bytes) exceeds it are rejected with NS_ERR_INVALID (the benchmark
  * shapes need at most 28 MiB).  The first call on a device takes the array's address there

@@ -27,7 +27,7 @@ NS_KIND_OTHER = 4       # every other sampled row (top-k off or larger)
 ABI_VERSION = 6
 
 # exported symbols, as declared in include/ns_sampling.h
-NS_NOALLOC_SCRATCH_BYTES = 32 << 20   # ns_sample_noalloc's device scratch per GPU
+NS_NOALLOC_SCRATCH_BYTES = 80 << 20   # ns_sample_noalloc's device scratch per GPU
 EXPORTS = ("ns_abi_version", "ns_sample", "ns_sample_noalloc", "ns_sample_lds_bytes", "ns_sample_workspace_bytes",
            "ns_hist_state_bytes",
            "ns_hist_assign", "ns_hist_append", "ns_seeded_uniforms", "ns_lm_head_bf16", "ns_lm_head_packed_bytes",

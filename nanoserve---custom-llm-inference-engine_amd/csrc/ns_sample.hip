@@ -1331,7 +1331,7 @@ DevInfo g_dev[kMaxDevices];
 int device_info(int dev, DevInfo& out);
 
 struct WsLayout {
-  int64_t counters, status, stats, cand, wrow, hcnt, hmass, subfx, slist, smeta, total;
+  int64_t counters, status, stats, cand, wrow, shist, slist, smeta, total;
 };
 // Workspace layout.  The per-row arrival counters are the only state that outlives a
 // call (each call leaves them at zero): they sit at fixed positions at the start, sized
@@ -1349,12 +1349,11 @@ WsLayout ws_layout(int32_t n_sample, int64_t vocab, int32_t dtype) {
   // wide path: per-row plans and histograms, for up to NS_WIDE_MAX_ROWS rows
   const int64_t wrows = rows < NS_WIDE_MAX_ROWS ? rows : NS_WIDE_MAX_ROWS;
   L.wrow = L.cand + align256(rows * S * ns::SEG_CAP * 8);
-  L.hcnt = L.wrow + align256(wrows * (int64_t)sizeof(ns::WideRow));
-  L.hmass = L.hcnt + align256(wrows * ns::WBINS * 4);
-  L.subfx = L.hmass + align256(wrows * ns::WBINS * 8);
+  // each wide row's segment histograms (pass 1 to its planner and cut pass)
+  L.shist = L.wrow + align256(wrows * (int64_t)sizeof(ns::WideRow));
   // split path: each slice's ordered keys and its word of flags, for up to SP_MAX_ROWS rows
   const int64_t srows = rows < ns::SP_MAX_ROWS ? rows : ns::SP_MAX_ROWS;
-  L.slist = L.subfx + align256(wrows * S * ns::WSUB * 8);
+  L.slist = L.shist + align256(wrows * S * ns::WBINS * 8);
   L.smeta = L.slist + align256(srows * ns::SP_MAXS * ns::SP_LIST * 8);
   L.total = L.smeta + align256(srows * ns::SP_MAXS * (int64_t)sizeof(ns::SplitMeta));
   return L;
@@ -1836,9 +1835,7 @@ int ns_sample(const ns_sample_args* a, hipStream_t stream) {
     w.status = reinterpret_cast<int32_t*>(ws + L.status);
     w.rows = reinterpret_cast<ns::WideRow*>(ws + L.wrow);
     w.segs = reinterpret_cast<ns::WideSeg*>(ws + L.stats);
-    w.hcnt = reinterpret_cast<uint32_t*>(ws + L.hcnt);
-    w.hmass = reinterpret_cast<uint64_t*>(ws + L.hmass);
-    w.subfx = reinterpret_cast<uint64_t*>(ws + L.subfx);
+    w.shist = reinterpret_cast<uint64_t*>(ws + L.shist);
     w.cand = reinterpret_cast<uint64_t*>(ws + L.cand);
     p.status = w.status;
     const dim3 g((unsigned)nblk), bs(ns::SNT);
@@ -1850,8 +1847,6 @@ int ns_sample(const ns_sample_args* a, hipStream_t stream) {
       if (bf) hipLaunchKernelGGL((ns::wide_stats_kernel<ns::BF16>), g, bs, 0, stream, w);
       else hipLaunchKernelGGL((ns::wide_stats_kernel<ns::F32>), g, bs, 0, stream, w);
     }
-    if (bf) hipLaunchKernelGGL((ns::wide_hist_kernel<ns::BF16>), g, bs, 0, stream, w);
-    else hipLaunchKernelGGL((ns::wide_hist_kernel<ns::F32>), g, bs, 0, stream, w);
     if (bf) hipLaunchKernelGGL((ns::wide_cut_kernel<ns::BF16>), g, bs, 0, stream, w);
     else hipLaunchKernelGGL((ns::wide_cut_kernel<ns::F32>), g, bs, 0, stream, w);
     const dim3 gr((unsigned)a->n_sample), br(ns::NT);

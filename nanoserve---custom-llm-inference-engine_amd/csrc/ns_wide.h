@@ -1,28 +1,32 @@
 // gfx950 wide path: sampled rows whose top-k is off (k <= 0 or k >= V) or larger than
 // KFAST -- the rows the streaming and segment paths leave to one workgroup.  Each row is
 // split over the segment kernel's 16-byte-chunk segments, so every CU works on it, and
-// sampler.py:31-89 runs in up to four launches over (row, segment) workgroups:
-//   1. stats  (the HBM pass): scaled logits y (penalty sampler.py:31-38 with set
-//      semantics, temperature :40-51) -> row max M, finite count, NaN / +inf flags.
-//      The last segment of a row resolves NaN / +inf / all -inf rows (uniform 1/V,
-//      :77-80) and clears the row's histograms.
-//   2. hist   (re-read from L2 / Infinity Cache): count and fixed-point mass histograms
-//      of exp(y - M) in bins of 1/64 below M, and each segment's mass.  The last
-//      segment plans the row: without top-k and top-p it draws at once; otherwise it
-//      finds the bin holding the k-th largest (:56-58) and the bins where the top-p
-//      mass crosses (:60-73).
-//   3. cut    (re-read): the planned bins' elements are compacted per segment, with the
-//      mass of each segment above them.  The last segment orders the compacted
-//      elements (value descending, id ascending) and finds the exact top-k threshold,
-//      the top-p cut as the oracle defines it (float32 prefix of float32 probabilities),
-//      the kept set's mass per segment, and draws.
+// sampler.py:31-89 runs in up to three launches over (row, segment) workgroups, then one
+// per row:
+//   1. stats  (the HBM pass, the segment read twice, the second time from the L2): scaled
+//      logits y (penalty sampler.py:31-38 with set semantics, temperature :40-51) -> the
+//      segment's max m, finite count, NaN / +inf flags; then its histogram of counts and
+//      masses exp(y - m) on the absolute grid of bins floor(64 y), the 2048 bins below
+//      its max, exported.  The last segment of a row resolves NaN / +inf / all -inf rows
+//      (uniform 1/V, :77-80), merges the segments' histograms (bin b below the row's top
+//      bin floor(64 M) is bin b - (floor(64 M) - floor(64 m)) of a segment, its mass
+//      scaled by exp(m - M)) and plans the row: without top-k and top-p it draws at once;
+//      otherwise it finds the bin holding the k-th largest (:56-58) and the bins where the
+//      top-p mass crosses (:60-73).
+//   2. cut    (re-read): the planned bins' elements are compacted per segment, with the
+//      count of those above them; each segment's mass above them is the sum of its own
+//      histogram's bins (no exponential per element).
+//   3. final  (one workgroup per row): orders the compacted elements (value descending,
+//      id ascending) and finds the exact top-k threshold, the top-p cut as the oracle
+//      defines it (float32 prefix of float32 probabilities), the kept set's mass per
+//      segment, and draws: the segment holding u from the per-segment kept masses, then
+//      a walk over that segment (inverse CDF in token-id order, sampler.py:84-89 against
+//      a caller uniform).
 //   4. probs  (only with out_probs): every token's final probability.
-// The draw (inverse CDF in token-id order, sampler.py:84-89 against a caller uniform)
-// finds the segment holding u from the per-segment kept masses, then walks that one
-// segment.  Masses are integer sums of exp(y - M) in units of 2^-44, so every pass and
-// every order of accumulation gives the same totals.  Rows this path cannot plan (a
-// k-th largest or top-p crossing more than 32 below the max, more planned elements than
-// WCAND) are left to the per-row kernel (status 1).
+// A segment's masses are integer sums of exp(y - m) in units of 2^-44 and every merge
+// runs in a fixed order, so every run gives the same totals.  Rows this path cannot plan
+// (a k-th largest or top-p crossing more than 32 below the max, |M| of 2^18 or more, more
+// planned elements than WCAND) are left to the per-row kernel (status 1).
 #pragma once
 
 #include "ns_segment.h"
@@ -36,9 +40,10 @@ constexpr int WIDE_MAX_ROWS = 4096;           // rows a call sends through this 
 constexpr double WFX = 17592186044416.0;      // 2^44: fixed-point scale of exp(y - M) <= 1
 constexpr double WFX_INV = 1.0 / 17592186044416.0;
 constexpr int32_t PATH_WIDE = 7;              // out_info path code
-constexpr int WSUB = 4;                       // quarter segments: the unit of the draw's final walk
+constexpr float WMAX_PLAN = 262144.0f;         // rows with |M| at or above it (2^18: bin edges k / 64 stop
+                                              // being exact floats past 2^24 / 64) are not planned
 
-enum : int32_t { WSTEP_NONE = 0, WSTEP_HIST = 1, WSTEP_CUT = 2, WSTEP_DRAWN = 3, WSTEP_UNIFORM = 4, WSTEP_FULL = 5 };
+enum : int32_t { WSTEP_NONE = 0, WSTEP_CUT = 2, WSTEP_DRAWN = 3, WSTEP_UNIFORM = 4, WSTEP_FULL = 5 };
 
 // Per-row plan and result in the workspace (128 bytes).
 struct WideRow {
@@ -62,13 +67,13 @@ static_assert(sizeof(WideRow) == 128, "WideRow layout");
 
 // Per-(row, segment) record, in the segment kernel's statistics slots (32 bytes).
 struct WideSeg {
-  uint64_t mass;           // pass 1: float64 bits of sum exp(y - ymax); pass 2: the segment's mass;
-                           // pass 3: its mass in bins < blo
+  uint64_t mass;           // pass 1: float64 bits of sum exp(y - ymax) (rows that keep every value);
+                           // cut pass: its mass in bins < blo
   float ymax;              // pass 1: segment max of the finite scaled logits
   int32_t nfin;            // pass 1: finite scaled logits
   int32_t flags;           // pass 1: flags
-  int32_t ncand;           // pass 3: planned-bin elements (may exceed SEG_CAP: overflow)
-  int32_t nabove;          // pass 3: finite elements in bins < blo
+  int32_t ncand;           // cut pass: planned-bin elements (may exceed SEG_CAP: overflow)
+  int32_t nabove;          // cut pass: finite elements in bins < blo
   int32_t pad;
 };
 static_assert(sizeof(WideSeg) == sizeof(SegStat), "WideSeg uses the segment statistics slots");
@@ -99,10 +104,9 @@ struct WideParams {
   int32_t* status;         // [rows] 0 = resolved here, 1 = per-row kernel
   WideRow* rows;           // [rows]
   WideSeg* segs;           // [rows * S]
-  uint32_t* hcnt;          // [rows * WBINS]
-  uint64_t* hmass;         // [rows * WBINS]
+  uint64_t* shist;         // [rows * S * WBINS] pass 1: each segment's histogram below its top bin,
+                           //   (count << 32) | float32 bits of the mass in units of exp(m)
   uint64_t* cand;          // [rows * S * SEG_CAP]  (float bits << 32) | token id
-  uint64_t* subfx;         // [rows * S * WSUB] pass 3: mass in bins < blo per quarter segment
 };
 
 template <int NKEYS>
@@ -116,7 +120,7 @@ struct WideSmemT {
     uint64_t keys[NKEYS];                    // the finaliser's ordered elements
   } u;
   unsigned long long segfx[MAX_SEGS];
-  unsigned long long subq[MAX_SEGS * WSUB];  // the finaliser's kept mass per quarter segment
+  unsigned long long subq[MAX_SEGS];         // the finaliser's kept mass per segment
   int32_t off[MAX_SEGS + 1];
   unsigned long long ured[NWAVE];
   double dred[NWAVE];
@@ -136,10 +140,17 @@ using WideSmemCut = WideSmemT<WCAND>;        // the cut pass and its finaliser
 // Rows this path takes: sampled (temperature != 0) and not small-k (sampler.py:55).
 __host__ __device__ __forceinline__ bool wide_row(float t, int32_t k, int64_t V) { return !seg_row(t, k, V); }
 
-// Bin of a scaled logit below the row max (WBINS: more than 32 below, or not finite).
-__device__ __forceinline__ int wbin(float M, float y) {
-  const float d = (M - y) * WSCALE;
-  return d < (float)WBINS ? (int)d : WBINS;
+// The absolute bin grid: floor(64 y), clamped far outside the plannable range (the scaling
+// is exact, so the bin of a value is the same wherever it is computed).
+__device__ __forceinline__ int wgrid(float y) {
+  return (int)__builtin_floorf(__builtin_fminf(__builtin_fmaxf(y * WSCALE, -1.0e9f), 1.0e9f));
+}
+// Bin of a scaled logit below the top bin tb (= wgrid of the row's or the segment's max;
+// WBINS: 2048 or more bins below, or not finite).
+__device__ __forceinline__ int wbin(int tb, float y) {
+  if (!(y > -__builtin_inff())) return WBINS;
+  const int d = tb - wgrid(y);
+  return d < WBINS ? d : WBINS;
 }
 // exp(y - M) in units of 2^-44 (y <= M), truncated: (uint64_t)(e * 2^44) for the float32
 // e = exp(y - M) in [0, 1], taken from e's exponent and mantissa bits (the product with
@@ -151,6 +162,18 @@ __device__ __forceinline__ uint64_t wfx(float M, float y) {
   if (E >= 106) return m << (E - 106);                 // e * 2^44 = m * 2^(E - 127 - 23 + 44)
   const int r = 106 - E;
   return (E > 0 && r < 64) ? (m >> r) : 0ull;          // zero and subnormal e: below 2^-44
+}
+
+// The same fixed-point mass through the hardware base-2 exponential: exp2((y - M) log2 e),
+// within a few units in the last place of expf (the rounding of y - M, which both carry,
+// dominates); for the histograms, whose bins only plan the row.
+__device__ __forceinline__ uint64_t wfx_hw(float M, float y) {
+  const uint32_t b = __float_as_uint(__builtin_amdgcn_exp2f((y - M) * 1.4426950408889634f));
+  const int E = (int)(b >> 23);
+  const uint64_t m = (uint64_t)((b & 0x7fffffu) | 0x800000u);
+  if (E >= 106) return m << (E - 106);
+  const int r = 106 - E;
+  return (E > 0 && r < 64) ? (m >> r) : 0ull;
 }
 
 __device__ __forceinline__ void dc_store_wseg(WideSeg* p, const WideSeg& s) {
@@ -522,258 +545,26 @@ __device__ __forceinline__ void wide_rowseg(int S, int* row, int* seg) {
   *row = rg * 8 + (b & 7);
 }
 
-// ------------------------------------------------------------------ pass 1: stats
-template <typename T>
-__device__ __forceinline__ void wide_stats_body(const WideParams& P, WideSmem& sm) {
-  constexpr int EPC = T::EPC;
+// ------------------------------------------------------------------ the plan
+// The row's plan from its histograms (8 bins per thread of the SNT threads, bin tid * 8 + j
+// in hc[j], hm[j]): every thread of the last segment calls it.  Rows whose crossing lies
+// past the histograms, or with more planned elements than WCAND, are left to the per-row
+// kernel.
+template <int BPT>
+__device__ __forceinline__ void wide_plan(const WideParams& P, const WRowCtx& c, WideRow* R, int row, int32_t nfin,
+                                          int32_t fl, float M, const uint32_t (&hc)[BPT],
+                                          const unsigned long long (&hm)[BPT], WideSmem& sm) {
+  static_assert(BPT * SNT == WBINS, "8 bins per thread");
   const int tid = threadIdx.x;
-  int row, seg;
-  wide_rowseg(P.S, &row, &seg);
-  if (row >= P.n_sample) return;
-  const WRowCtx c = wide_row_ctx<T>(P, row);
-  if (!c.valid) {
-    if (P.init_status && seg == 0 && tid == 0) P.status[row] = 1;
-    if (seg == 0 && tid == 0) P.rows[row].step = WSTEP_NONE;
-    return;
-  }
-  const int64_t c0 = (int64_t)seg * SEG_CH;
-  int32_t flags = wide_bitmap<T>(P, c, c0 * EPC, &sm);
-  // per thread: finite count, max and sum of exp(y - max) (float64, rescaled by an exact
-  // float64 exp when the max moves, which a thread's first few values do)
-  // (only rows that keep every finite value need the sum: the others histogram the mass
-  // against the row max in the next pass)
-  const bool full_row = !(c.k > 0 && (int64_t)c.k < c.V) && !(c.topp < 1.0f);
-  float mx = -__builtin_inff();
-  double zt = 0.0;
-  int nfin = 0;
-  bool nanf = false, pinf = false;
-  if (full_row) {
-    wide_each<T>(c, c0, sm.bm, [&](float y, int64_t) {
-      nanf |= y != y;
-      pinf |= y == __builtin_inff();
-      if (y > -__builtin_inff() && y < __builtin_inff()) {
-        ++nfin;
-        if (y > mx) {
-          zt = zt * exp((double)mx - (double)y) + 1.0;
-          mx = y;
-        } else {
-          zt += (double)ns_expf(y - mx);
-        }
-      }
-    });
-  } else {
-    wide_each<T>(c, c0, sm.bm, [&](float y, int64_t) {
-      nanf |= y != y;
-      pinf |= y == __builtin_inff();
-      if (y > -__builtin_inff() && y < __builtin_inff()) { ++nfin; mx = __builtin_fmaxf(mx, y); }
-    });
-  }
-  if (ballot(nanf) != 0ull) flags |= SFLAG_NAN;
-  if (ballot(pinf) != 0ull) flags |= SFLAG_PINF;
-  if (lane_id() == 0 && (flags & (SFLAG_NAN | SFLAG_PINF))) atomicOr(&sm.flags, flags);
-  const float smax = wmax_f(mx, &sm);
-  const int32_t snfin = wsum_i(nfin, &sm);
-  const double szt = wsum_f64(nfin > 0 ? zt * exp((double)mx - (double)smax) : 0.0, &sm);
-  flags |= sm.flags;
-  // this segment's share of the row histograms, cleared for pass 2
-  {
-    const int per = (WBINS + P.S - 1) / P.S;
-    for (int b = seg * per + tid; b < (seg + 1) * per && b < WBINS; b += SNT) {
-      P.hcnt[(int64_t)row * WBINS + b] = 0u;
-      P.hmass[(int64_t)row * WBINS + b] = 0ull;
-    }
-  }
-  if (tid == 0) {
-    WideSeg s{};
-    s.mass = (uint64_t)__double_as_longlong(szt);
-    s.ymax = smax;
-    s.nfin = snfin;
-    s.flags = flags;
-    dc_store_wseg(P.segs + (int64_t)row * P.S + seg, s);
-  }
-  if (!wide_arrive(P.counters + row, P.S, &sm)) return;
-  // ---- last segment of the row: M, flags, the NaN / +inf / all -inf rows
-  if (wave_id() == 0) {
-    const bool act = lane_id() < P.S;
-    WideSeg s{};
-    if (act) {
-      s = dc_load_wseg(P.segs + (int64_t)row * P.S + lane_id());
-      sm.u.h.mass[lane_id()] = s.mass;                                   // float64 bits of its sum
-      sm.u.h.cnt[lane_id()] = __float_as_uint(s.ymax);
-    }
-    float M = act ? s.ymax : -__builtin_inff();
-    int32_t nf = act ? s.nfin : 0, fl = act ? s.flags : 0;
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) {
-      M = __builtin_fmaxf(M, lane_xor(M, o));
-      nf += lane_xor(nf, o);
-      fl |= lane_xor(fl, o);
-    }
-    if (lane_id() == 0) { sm.fb[0] = M; sm.ib[0] = nf; sm.ib[1] = fl; }
-  }
-  __syncthreads();
-  const float M = sm.fb[0];
-  const int32_t nf = sm.ib[0], fl = sm.ib[1];
-  WideRow* R = P.rows + row;
-  if ((fl & (SFLAG_NAN | SFLAG_PINF)) || nf == 0) {
-    // the softmax is NaN (a NaN or +inf logit, or every logit -inf): uniform 1/V
-    // (sampler.py:77-80)
-    const int64_t V = c.V;
-    const float qv = (float)(1.0 / (double)V);
-    if (tid == 0) {
-      const double qd = qv, ud = c.u;
-      int64_t i = (int64_t)(ud / qd);
-      while (i > 0 && (double)i * qd > ud) --i;
-      while ((double)(i + 1) * qd <= ud && i < V) ++i;
-      if (i >= V) i = V - 1;
-      P.out_ids[row] = i;
-      const float mrep = (fl & SFLAG_NAN) ? __builtin_nanf("") : (nf == 0 ? -__builtin_inff() : __builtin_inff());
-      seg_write_info(P.out_info, row, PATH_UNIFORM, (int32_t)V, -__builtin_inff(), (int32_t)V, 0, fl & 0xffff, mrep,
-                     -1);
-      P.status[row] = 0;
-      R->step = WSTEP_UNIFORM;
-    }
-    if (P.out_probs != nullptr) {
-      float* pr = P.out_probs + (int64_t)row * V;
-      for (int64_t i = tid; i < V; i += SNT) pr[i] = qv;
-    }
-    return;
-  }
-  const bool kon = c.k > 0 && (int64_t)c.k < c.V && c.k <= nf;   // sampler.py:55
-  const bool pon = c.topp < 1.0f;                                   // sampler.py:63
-  if (!kon && !pon) {
-    // ---- no top-k and no top-p: every finite value is kept.  The segments' sums rescaled to
-    // the row max are the kept mass per segment; the final pass draws.
-    if (tid < P.S) {
-      const float ms = __uint_as_float(sm.u.h.cnt[tid]);
-      const double w = ms > -__builtin_inff()
-                           ? __longlong_as_double((long long)sm.u.h.mass[tid]) * exp((double)ms - (double)M)
-                           : 0.0;
-      WideSeg s2{};
-      s2.mass = (uint64_t)__double_as_longlong(w);
-      dc_store_wseg(P.segs + (int64_t)row * P.S + tid, s2);
-    }
-    if (tid == 0) {
-      R->M = M;
-      R->flags = fl;
-      R->nfin = nf;
-      R->step = WSTEP_FULL;
-    }
-    return;
-  }
-  if (tid == 0) {
-    R->M = M;
-    R->flags = fl;
-    R->nfin = nf;
-    R->step = WSTEP_HIST;
-  }
-}
-
-template <typename T>
-__global__ __launch_bounds__(SNT) __attribute__((amdgpu_waves_per_eu(4))) void wide_stats_kernel(const WideParams P) {
-  __shared__ WideSmem sm;
-  wide_stats_body<T>(P, sm);
-}
-
-// The segment kernel and the wide path's first pass in one launch over the same (row,
-// segment) workgroups: greedy and small-k rows take the segment kernel's work, the others
-// the stats pass (which writes status 1 for the rows neither takes).
-template <typename T>
-__global__ __launch_bounds__(SNT) __attribute__((amdgpu_waves_per_eu(4))) void segwide_kernel(const SegParams SP,
-                                                                                            const WideParams WP) {
-  __shared__ union {
-    SegSmem s;
-    WideSmem w;
-  } sm;
-  int row, seg;
-  wide_rowseg(WP.S, &row, &seg);
-  if (row >= WP.n_sample) return;
-  if (seg_row(WP.temperature[row], WP.top_k[row], WP.vocab)) {
-    if (seg == 0 && threadIdx.x == 0) WP.rows[row].step = WSTEP_NONE;   // no later wide pass for it
-    segment_body<T>(SP, sm.s);
-  } else {
-    wide_stats_body<T>(WP, sm.w);
-  }
-}
-
-// ------------------------------------------------------------------ pass 2: histograms
-template <typename T>
-__global__ __launch_bounds__(SNT) void wide_hist_kernel(const WideParams P) {
-  __shared__ WideSmem sm;
-  constexpr int EPC = T::EPC;
-  const int tid = threadIdx.x;
-  int row, seg;
-  wide_rowseg(P.S, &row, &seg);
-  if (row >= P.n_sample) return;
-  if (P.rows[row].step != WSTEP_HIST) return;
-  const WRowCtx c = wide_row_ctx<T>(P, row);
-  const int64_t c0 = (int64_t)seg * SEG_CH;
-  const float M = P.rows[row].M;
-  for (int b = tid; b < WBINS; b += SNT) { sm.u.h.cnt[b] = 0u; sm.u.h.mass[b] = 0ull; }
-  wide_bitmap<T>(P, c, c0 * EPC, &sm);   // its barriers also order the clearing above
-  unsigned long long own = 0ull;
-  if (c.topp < 1.0f && c.k > 0 && (int64_t)c.k < c.V) {
-    wide_each<T>(c, c0, sm.bm, [&](float y, int64_t) {
-      const int b = wbin(M, y);
-      if (b < WBINS) {
-        const uint64_t fx = wfx(M, y);
-        atomicAdd(&sm.u.h.cnt[b], 1u);
-        atomicAdd(&sm.u.h.mass[b], (unsigned long long)fx);
-        own += fx;
-      }
-    });
-  } else if (c.topp < 1.0f) {
-    // top-p alone: masses only (the counts above the plan come from the compaction pass)
-    wide_each<T>(c, c0, sm.bm, [&](float y, int64_t) {
-      const int b = wbin(M, y);
-      if (b < WBINS) {
-        const uint64_t fx = wfx(M, y);
-        atomicAdd(&sm.u.h.mass[b], (unsigned long long)fx);
-        own += fx;
-      }
-    });
-  } else {
-    // top-k alone: counts only (its kept mass is summed from the ordered elements and the
-    // compaction pass)
-    wide_each<T>(c, c0, sm.bm, [&](float y, int64_t) {
-      const int b = wbin(M, y);
-      if (b < WBINS) atomicAdd(&sm.u.h.cnt[b], 1u);
-    });
-  }
-  __syncthreads();
-  for (int b = tid; b < WBINS; b += SNT) {
-    const uint32_t n = sm.u.h.cnt[b];
-    const unsigned long long fx = sm.u.h.mass[b];
-    if (n != 0u) atomicAdd(P.hcnt + (int64_t)row * WBINS + b, n);
-    if (fx != 0ull) atomicAdd((unsigned long long*)(P.hmass + (int64_t)row * WBINS + b), fx);
-  }
-  const unsigned long long smass = wsum_u64(own, &sm);
-  if (tid == 0) {
-    WideSeg s{};
-    s.mass = smass;
-    dc_store_wseg(P.segs + (int64_t)row * P.S + seg, s);
-  }
-  if (!wide_arrive(P.counters + row, P.S, &sm)) return;
-
-  // ---- last segment of the row: the plan
-  WideRow* R = P.rows + row;
-  const int32_t nfin = R->nfin;
-  int32_t fl = R->flags & 0xffff;
   const int64_t V = c.V;
   const bool kon0 = c.k > 0 && (int64_t)c.k < V;     // sampler.py:55
   const bool kon = kon0 && c.k <= nfin;              // otherwise the k-th largest is -inf: keep every value
   const bool pon = c.topp < 1.0f;                    // sampler.py:63
-  // the row histograms, 4 bins per thread, and their running sums
-  constexpr int BPT = WBINS / SNT;
-  uint32_t hc[BPT];
-  unsigned long long hm[BPT];
+  // the row histograms' running sums
   uint32_t ccnt = 0u;
   unsigned long long cmass = 0ull;
 #pragma unroll
   for (int j = 0; j < BPT; ++j) {
-    const int b = tid * BPT + j;
-    hc[j] = __hip_atomic_load(P.hcnt + (int64_t)row * WBINS + b, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    hm[j] = dc_load(P.hmass + (int64_t)row * WBINS + b);
     ccnt += hc[j];
     cmass += hm[j];
   }
@@ -873,12 +664,290 @@ __global__ __launch_bounds__(SNT) void wide_hist_kernel(const WideParams P) {
     R->mass_above = sm.segfx[0];
     R->mass_tot = mtot;
     R->kon = kon ? 1 : 0;
+    R->M = M;
+    R->flags = fl;
+    R->nfin = nfin;
     R->step = WSTEP_CUT;
   }
 }
 
-// ------------------------------------------------------------------ pass 3: the planned elements
-// Each segment compacts its elements in the planned bins and its mass above them.
+
+// ------------------------------------------------------------------ pass 1: stats
+template <typename T>
+__device__ __forceinline__ void wide_stats_body(const WideParams& P, WideSmem& sm) {
+  constexpr int EPC = T::EPC;
+  const int tid = threadIdx.x;
+  int row, seg;
+  wide_rowseg(P.S, &row, &seg);
+  if (row >= P.n_sample) return;
+  const WRowCtx c = wide_row_ctx<T>(P, row);
+  if (!c.valid) {
+    if (P.init_status && seg == 0 && tid == 0) P.status[row] = 1;
+    if (seg == 0 && tid == 0) P.rows[row].step = WSTEP_NONE;
+    return;
+  }
+  const int64_t c0 = (int64_t)seg * SEG_CH;
+  int32_t flags = wide_bitmap<T>(P, c, c0 * EPC, &sm);
+  // per thread: finite count, max and sum of exp(y - max) (float64, rescaled by an exact
+  // float64 exp when the max moves, which a thread's first few values do)
+  // (only rows that keep every finite value need the sum: the others histogram the mass
+  // against the segment max below)
+  const bool full_row = !(c.k > 0 && (int64_t)c.k < c.V) && !(c.topp < 1.0f);
+  float mx = -__builtin_inff();
+  double zt = 0.0;
+  int nfin = 0;
+  bool nanf = false, pinf = false;
+  if (full_row) {
+    wide_each<T>(c, c0, sm.bm, [&](float y, int64_t) {
+      nanf |= y != y;
+      pinf |= y == __builtin_inff();
+      if (y > -__builtin_inff() && y < __builtin_inff()) {
+        ++nfin;
+        if (y > mx) {
+          zt = zt * exp((double)mx - (double)y) + 1.0;
+          mx = y;
+        } else {
+          zt += (double)ns_expf(y - mx);
+        }
+      }
+    });
+  }
+  // float32 rows with a plan hold the segment in registers (chunk c0 + q * SNT + t to thread
+  // t), the scaled values in place of the raw ones, for both sweeps; bfloat16 rows (twice
+  // the values per register) stream it twice, the second time from the L2
+  constexpr bool REGS = EPC == 4;
+  uint4 v[SCPT];
+  if (!full_row && !REGS) {
+    wide_each<T>(c, c0, sm.bm, [&](float y, int64_t) {
+      nanf |= y != y;
+      pinf |= y == __builtin_inff();
+      if (y > -__builtin_inff() && y < __builtin_inff()) { ++nfin; mx = __builtin_fmaxf(mx, y); }
+    });
+  }
+  if (!full_row && REGS) {
+    const uint32_t nbytes = (uint32_t)((c.V / EPC) * 16);
+#pragma unroll
+    for (int q = 0; q < SCPT; ++q)
+      v[q] = buf_load16_at(c.rowp, nbytes, (uint32_t)((c0 + q * SNT) * 16), (uint32_t)tid * 16u);
+#pragma unroll
+    for (int q = 0; q < SCPT; ++q) {
+      const int lc = q * SNT + tid;
+      const int64_t ch = c0 + lc;
+      float y[EPC];
+#pragma unroll
+      for (int e = 0; e < EPC; ++e) y[e] = -__builtin_inff();
+      if (ch * EPC < c.V) chunk_y<T>(c, wide_chunk_fix<T>(c, ch, v[q]), c.pen_on ? T::bits(sm.bm, lc) : 0u, ch * EPC, y);
+#pragma unroll
+      for (int e = 0; e < EPC; ++e) {
+        nanf |= y[e] != y[e];
+        pinf |= y[e] == __builtin_inff();
+        if (y[e] > -__builtin_inff() && y[e] < __builtin_inff()) { ++nfin; mx = __builtin_fmaxf(mx, y[e]); }
+      }
+      v[q] = make_uint4(__float_as_uint(y[0]), __float_as_uint(y[1]), __float_as_uint(y[2]), __float_as_uint(y[3 % EPC]));
+    }
+  }
+  if (ballot(nanf) != 0ull) flags |= SFLAG_NAN;
+  if (ballot(pinf) != 0ull) flags |= SFLAG_PINF;
+  if (lane_id() == 0 && (flags & (SFLAG_NAN | SFLAG_PINF))) atomicOr(&sm.flags, flags);
+  const float smax = wmax_f(mx, &sm);
+  const int32_t snfin = wsum_i(nfin, &sm);
+  const double szt = wsum_f64(nfin > 0 ? zt * exp((double)mx - (double)smax) : 0.0, &sm);
+  flags |= sm.flags;
+  if (!full_row) {
+    // the segment's histogram on the absolute grid below its top bin: counts (top-k rows)
+    // and fixed-point masses exp(y - smax), from the registers; exported as (count, float32
+    // mass) words for the row's planner
+    for (int b = tid; b < WBINS; b += SNT) { sm.u.h.cnt[b] = 0u; sm.u.h.mass[b] = 0ull; }
+    __syncthreads();
+    const bool cnt_on = c.k > 0 && (int64_t)c.k < c.V;
+    if (smax > -__builtin_inff() && smax < __builtin_inff()) {
+      const int tb = wgrid(smax);
+      auto bin_one = [&](float y) {
+        const int b = wbin(tb, y);
+        if (b < WBINS) {
+          atomicAdd(&sm.u.h.mass[b], (unsigned long long)wfx_hw(smax, y));
+          if (cnt_on) atomicAdd(&sm.u.h.cnt[b], 1u);
+        }
+      };
+      if constexpr (REGS) {
+#pragma unroll
+        for (int q = 0; q < SCPT; ++q) {
+          bin_one(__uint_as_float(v[q].x));
+          bin_one(__uint_as_float(v[q].y));
+          bin_one(__uint_as_float(v[q].z));
+          bin_one(__uint_as_float(v[q].w));
+        }
+      } else {
+        wide_each<T>(c, c0, sm.bm, [&](float y, int64_t) { bin_one(y); });
+      }
+    }
+    __syncthreads();
+    uint64_t* ex = P.shist + ((int64_t)row * P.S + seg) * WBINS;
+    for (int b = tid; b < WBINS; b += SNT) {
+      const float mf = (float)((double)sm.u.h.mass[b] * WFX_INV);
+      dc_store(ex + b, ((uint64_t)sm.u.h.cnt[b] << 32) | __float_as_uint(mf));
+    }
+  }
+  if (tid == 0) {
+    WideSeg s{};
+    s.mass = (uint64_t)__double_as_longlong(szt);
+    s.ymax = smax;
+    s.nfin = snfin;
+    s.flags = flags;
+    dc_store_wseg(P.segs + (int64_t)row * P.S + seg, s);
+  }
+  if (!wide_arrive(P.counters + row, P.S, &sm)) return;
+  // ---- last segment of the row: M, flags, the NaN / +inf / all -inf rows
+  if (wave_id() == 0) {
+    const bool act = lane_id() < P.S;
+    WideSeg s{};
+    if (act) {
+      s = dc_load_wseg(P.segs + (int64_t)row * P.S + lane_id());
+      sm.u.h.mass[lane_id()] = s.mass;                                   // float64 bits of its sum
+      sm.u.h.cnt[lane_id()] = __float_as_uint(s.ymax);
+    }
+    float M = act ? s.ymax : -__builtin_inff();
+    int32_t nf = act ? s.nfin : 0, fl = act ? s.flags : 0;
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+      M = __builtin_fmaxf(M, lane_xor(M, o));
+      nf += lane_xor(nf, o);
+      fl |= lane_xor(fl, o);
+    }
+    if (lane_id() == 0) { sm.fb[0] = M; sm.ib[0] = nf; sm.ib[1] = fl; }
+  }
+  __syncthreads();
+  const float M = sm.fb[0];
+  const int32_t nf = sm.ib[0], fl = sm.ib[1];
+  WideRow* R = P.rows + row;
+  if ((fl & (SFLAG_NAN | SFLAG_PINF)) || nf == 0) {
+    // the softmax is NaN (a NaN or +inf logit, or every logit -inf): uniform 1/V
+    // (sampler.py:77-80)
+    const int64_t V = c.V;
+    const float qv = (float)(1.0 / (double)V);
+    if (tid == 0) {
+      const double qd = qv, ud = c.u;
+      int64_t i = (int64_t)(ud / qd);
+      while (i > 0 && (double)i * qd > ud) --i;
+      while ((double)(i + 1) * qd <= ud && i < V) ++i;
+      if (i >= V) i = V - 1;
+      P.out_ids[row] = i;
+      const float mrep = (fl & SFLAG_NAN) ? __builtin_nanf("") : (nf == 0 ? -__builtin_inff() : __builtin_inff());
+      seg_write_info(P.out_info, row, PATH_UNIFORM, (int32_t)V, -__builtin_inff(), (int32_t)V, 0, fl & 0xffff, mrep,
+                     -1);
+      P.status[row] = 0;
+      R->step = WSTEP_UNIFORM;
+    }
+    if (P.out_probs != nullptr) {
+      float* pr = P.out_probs + (int64_t)row * V;
+      for (int64_t i = tid; i < V; i += SNT) pr[i] = qv;
+    }
+    return;
+  }
+  const bool kon = c.k > 0 && (int64_t)c.k < c.V && c.k <= nf;   // sampler.py:55
+  const bool pon = c.topp < 1.0f;                                   // sampler.py:63
+  if (!kon && !pon) {
+    // ---- no top-k and no top-p: every finite value is kept.  The segments' sums rescaled to
+    // the row max are the kept mass per segment; the final pass draws.
+    if (tid < P.S) {
+      const float ms = __uint_as_float(sm.u.h.cnt[tid]);
+      const double w = ms > -__builtin_inff()
+                           ? __longlong_as_double((long long)sm.u.h.mass[tid]) * exp((double)ms - (double)M)
+                           : 0.0;
+      WideSeg s2{};
+      s2.mass = (uint64_t)__double_as_longlong(w);
+      dc_store_wseg(P.segs + (int64_t)row * P.S + tid, s2);
+    }
+    if (tid == 0) {
+      R->M = M;
+      R->flags = fl;
+      R->nfin = nf;
+      R->step = WSTEP_FULL;
+    }
+    return;
+  }
+  if (!(__builtin_fabsf(M) < WMAX_PLAN)) {
+    // bin indices of values this large are not planned: the per-row kernel takes the row
+    if (tid == 0) { P.status[row] = 1; R->step = WSTEP_NONE; }
+    return;
+  }
+  // ---- the row histograms: the segments' histograms merged onto the row's grid, 8 bins per
+  // thread (bin b below the row's top bin is bin b - ds of a segment whose top bin lies ds
+  // below the row's; its mass in units of exp(m) scaled by exp(m - M)), in a fixed order
+  const int TB = wgrid(M);
+  constexpr int BPT = WBINS / SNT;
+  uint32_t hc[BPT];
+  unsigned long long hm[BPT];
+  {
+    double acc[BPT];
+#pragma unroll
+    for (int j = 0; j < BPT; ++j) { acc[j] = 0.0; hc[j] = 0u; }
+    // two segments' words in flight per step (the loads of a step are issued together)
+    constexpr int SG = 2;
+    for (int sg0 = 0; sg0 < P.S; sg0 += SG) {
+      uint64_t w[SG][BPT];
+      double sc[SG];
+#pragma unroll
+      for (int q = 0; q < SG; ++q) {
+        const int sg = sg0 + q;
+        const float ms = sg < P.S ? __uint_as_float(sm.u.h.cnt[sg]) : -__builtin_inff();
+        // a segment without finite values, or 2048 bins or more below the row's top: nothing
+        const int ds = ms > -__builtin_inff() ? TB - wgrid(ms) : WBINS;
+        sc[q] = ds < WBINS ? exp((double)ms - (double)M) : 0.0;
+        const uint64_t* ex = P.shist + ((int64_t)row * P.S + sg) * WBINS;
+#pragma unroll
+        for (int j = 0; j < BPT; ++j) {
+          const int jj = tid * BPT + j - ds;
+          w[q][j] = (ds < WBINS && jj >= 0) ? dc_load(ex + jj) : 0ull;
+        }
+      }
+#pragma unroll
+      for (int q = 0; q < SG; ++q) {
+#pragma unroll
+        for (int j = 0; j < BPT; ++j) {
+          acc[j] += (double)__uint_as_float((uint32_t)w[q][j]) * sc[q];
+          hc[j] += (uint32_t)(w[q][j] >> 32);
+        }
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < BPT; ++j) hm[j] = (unsigned long long)(acc[j] * WFX);
+  }
+  wide_plan<BPT>(P, c, R, row, nf, fl, M, hc, hm, sm);
+}
+
+
+
+template <typename T>
+__global__ __launch_bounds__(SNT) __attribute__((amdgpu_waves_per_eu(4))) void wide_stats_kernel(const WideParams P) {
+  __shared__ WideSmem sm;
+  wide_stats_body<T>(P, sm);
+}
+
+// The segment kernel and the wide path's first pass in one launch over the same (row,
+// segment) workgroups: greedy and small-k rows take the segment kernel's work, the others
+// the stats pass (which writes status 1 for the rows neither takes).
+template <typename T>
+__global__ __launch_bounds__(SNT) __attribute__((amdgpu_waves_per_eu(4))) void segwide_kernel(const SegParams SP,
+                                                                                            const WideParams WP) {
+  __shared__ union {
+    SegSmem s;
+    WideSmem w;
+  } sm;
+  int row, seg;
+  wide_rowseg(WP.S, &row, &seg);
+  if (row >= WP.n_sample) return;
+  if (seg_row(WP.temperature[row], WP.top_k[row], WP.vocab)) {
+    if (seg == 0 && threadIdx.x == 0) WP.rows[row].step = WSTEP_NONE;   // no later wide pass for it
+    segment_body<T>(SP, sm.s);
+  } else {
+    wide_stats_body<T>(WP, sm.w);
+  }
+}
+
+// ------------------------------------------------------------------ pass 2: the planned elements
+// Each segment compacts its elements in the planned bins, counts those above them, and sums
+// its histogram's mass above them.
 template <typename T>
 __global__ __launch_bounds__(SNT) void wide_cut_kernel(const WideParams P) {
   __shared__ WideSmem sm;
@@ -893,28 +962,31 @@ __global__ __launch_bounds__(SNT) void wide_cut_kernel(const WideParams P) {
   const int64_t c0 = (int64_t)seg * SEG_CH;
   WideRow* R = P.rows + row;
   const float M = R->M;
+  const int TB = wgrid(M);
   const int blo = R->blo, bend = R->bend;
+  const float ms = dc_load_wseg(P.segs + (int64_t)row * P.S + seg).ymax;   // this segment's max (pass 1)
   wide_bitmap<T>(P, c, c0 * EPC, &sm);
   if (tid == 0) sm.cnt = 0;
   __syncthreads();
   uint64_t* cbase = P.cand + ((int64_t)row * P.S + seg) * SEG_CAP;
-  unsigned long long above = 0ull, aq0 = 0ull, aq1 = 0ull, aq2 = 0ull, aq3 = 0ull;
   int32_t nab = 0;
-  static_assert(SCPT / WGRP == WSUB, "one wide_chunks step per quarter segment");
+  // bin b < blo  <=>  floor(64 y) > TB - blo  <=>  y >= (TB - blo + 1) / 64, and b <= bend
+  // <=>  y >= (TB - bend) / 64: the grid's edges are exact floats, so two compares per
+  // element classify it exactly as wbin does
+  const float y_above = (float)(TB - blo + 1) * (1.0f / WSCALE);
+  const float y_plan = (float)(TB - bend) * (1.0f / WSCALE);
   wide_chunks<T>(c, c0, sm.bm, [&](const float (&y)[EPC], int64_t ch) {
     bool any = false;
 #pragma unroll
     for (int e = 0; e < EPC; ++e) {
-      const int b = wbin(M, y[e]);
-      if (b < blo) { above += wfx(M, y[e]); ++nab; }
-      any |= b >= blo && b <= bend;
+      nab += y[e] >= y_above ? 1 : 0;
+      any |= y[e] >= y_plan && y[e] < y_above;
     }
     // the planned elements of the chunk, appended wave-aggregated (one test per chunk)
     if (ballot(any) != 0ull) {
 #pragma unroll
       for (int e = 0; e < EPC; ++e) {
-        const int b = wbin(M, y[e]);
-        const bool take = b >= blo && b <= bend;
+        const bool take = y[e] >= y_plan && y[e] < y_above;
         const uint64_t m = ballot(take);
         if (m != 0ull) {
           const int leader = __builtin_ctzll(m);
@@ -927,46 +999,21 @@ __global__ __launch_bounds__(SNT) void wide_cut_kernel(const WideParams P) {
         }
       }
     }
-  }, [&](int g) {
-    // the quarter segment's mass above the plan (g is uniform: selects, no indexing)
-    aq0 = g == 0 ? above : aq0;
-    aq1 = g == 1 ? above : aq1;
-    aq2 = g == 2 ? above : aq2;
-    aq3 = g == 3 ? above : aq3;
-    above = 0ull;
   });
-  // the four quarter sums and the count in one block reduction
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) {
-    aq0 += lane_xor(aq0, o);
-    aq1 += lane_xor(aq1, o);
-    aq2 += lane_xor(aq2, o);
-    aq3 += lane_xor(aq3, o);
-    nab += lane_xor(nab, o);
+  // the mass above the plan: this segment's histogram bins below row bin blo (its bin jj is
+  // row bin jj + ds), in units of exp(ms), scaled to exp(M)
+  double part = 0.0;
+  if (ms > -__builtin_inff()) {
+    const int ds = TB - wgrid(ms);
+    const uint64_t* ex = P.shist + ((int64_t)row * P.S + seg) * WBINS;
+    const int lim = blo - ds < WBINS ? blo - ds : WBINS;
+    for (int jj = tid; jj < lim; jj += SNT) part += (double)__uint_as_float((uint32_t)dc_load(ex + jj));
   }
-  static_assert(WSUB * SNW <= NWAVE, "quarter sums of every wave in the reduction slots");
-  if (lane == 0) {
-    sm.ured[wave_id() * WSUB + 0] = aq0;
-    sm.ured[wave_id() * WSUB + 1] = aq1;
-    sm.ured[wave_id() * WSUB + 2] = aq2;
-    sm.ured[wave_id() * WSUB + 3] = aq3;
-    sm.ired[wave_id()] = nab;
-  }
-  __syncthreads();
+  const double above = wsum_f64(part, &sm) * (ms > -__builtin_inff() ? exp((double)ms - (double)M) : 0.0);
+  const int32_t snab = wsum_i(nab, &sm);
   if (tid == 0) {
-    unsigned long long q[WSUB] = {0ull, 0ull, 0ull, 0ull};
-    int32_t snab = 0;
-#pragma unroll
-    for (int w = 0; w < SNW; ++w) {
-#pragma unroll
-      for (int i = 0; i < WSUB; ++i) q[i] += sm.ured[w * WSUB + i];
-      snab += sm.ired[w];
-    }
-    uint64_t* sq = P.subfx + ((int64_t)row * P.S + seg) * WSUB;
-#pragma unroll
-    for (int i = 0; i < WSUB; ++i) dc_store(sq + i, q[i]);
     WideSeg s{};
-    s.mass = q[0] + q[1] + q[2] + q[3];
+    s.mass = (uint64_t)(above * WFX);
     s.ncand = sm.cnt;
     s.nabove = snab;
     dc_store_wseg(P.segs + (int64_t)row * P.S + seg, s);
@@ -1117,7 +1164,7 @@ __global__ __launch_bounds__(NT) void wide_final_kernel(const WideParams P) {
     sm.off[tid] = s.ncand;
     sm.ired[tid] = s.nabove;
   }
-  if (tid < P.S * WSUB) sm.subq[tid] = dc_load(P.subfx + (int64_t)row * P.S * WSUB + tid);
+  if (tid < P.S) sm.subq[tid] = dc_load_wseg(P.segs + (int64_t)row * P.S + tid).mass;   // mass above the plan
   if (tid == 0) sm.ib[0] = 0;
   __syncthreads();
   if (tid == 0) {
@@ -1252,7 +1299,7 @@ __global__ __launch_bounds__(NT) void wide_final_kernel(const WideParams P) {
       if (y >= thr) {
         const uint64_t fx = wfx(M, y);
         mkept += fx;
-        atomicAdd(&sm.subq[desc_key_id(kk[j]) / (SEG_EL / WSUB)], (unsigned long long)fx);
+        atomicAdd(&sm.subq[desc_key_id(kk[j]) / SEG_EL], (unsigned long long)fx);
       }
     }
   }
@@ -1264,8 +1311,8 @@ __global__ __launch_bounds__(NT) void wide_final_kernel(const WideParams P) {
     double run = 0.0, start = 0.0, laststart = 0.0;
     int s = -1, lastnz = -1;
     const double rzkept = 1.0 / zkept;
-    // the quarter segment holding u, from the kept mass per quarter
-    for (int i = 0; i < P.S * WSUB; ++i) {
+    // the segment holding u, from the kept mass per segment
+    for (int i = 0; i < P.S; ++i) {
       const double p = (double)sm.subq[i] * WFX_INV * rzkept;
       if (sm.subq[i] != 0ull) { lastnz = i; laststart = run; }
       if (s < 0 && run + p > ud && sm.subq[i] != 0ull) { s = i; start = run; }
@@ -1278,8 +1325,8 @@ __global__ __launch_bounds__(NT) void wide_final_kernel(const WideParams P) {
   __syncthreads();
   const int s = sm.ib[2];
   const double start = sm.db[0];
-  constexpr int QCH = SEG_CH / WSUB;   // chunks per quarter segment: one per thread
-  const int64_t tok = wide_locate<T, NT, 1, QCH>(P, c, (int64_t)s * QCH, start, 1.0 / zkept, M, keep, &sm, &fl);
+  // the walk over that segment: four consecutive chunks per thread, one step
+  const int64_t tok = wide_locate<T, NT, 4, SEG_CH>(P, c, (int64_t)s * SEG_CH, start, 1.0 / zkept, M, keep, &sm, &fl);
   if (tid == 0) {
     P.out_ids[row] = tok;
     seg_write_info(P.out_info, row, PATH_WIDE, n_kept, kon0 ? thr : -__builtin_inff(), n_topk, n, fl, vstar, istar);
