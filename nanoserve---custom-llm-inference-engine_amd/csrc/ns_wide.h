@@ -29,6 +29,8 @@
 // planned elements than WCAND) are left to the per-row kernel (status 1).
 #pragma once
 
+#include <type_traits>
+
 #include "ns_segment.h"
 
 namespace ns {
@@ -1194,150 +1196,161 @@ __global__ __launch_bounds__(NT) void wide_final_kernel(const WideParams P) {
     return;
   }
   // the planned elements as sort keys (value descending, id ascending), EPT per thread in
-  // registers at positions tid * EPT + j, ordered over a power of two of positions
-  constexpr int EPT = WCAND / NT;
-  const int p0 = tid * EPT;
-  uint64_t kk[EPT];
-  {
-    int s = 0;
-#pragma unroll
-    for (int j = 0; j < EPT; ++j) {
-      const int i = p0 + j;
-      kk[j] = ~0ull;
-      if (i < n) {
-        while (s + 1 < P.S && sm.off[s + 1] <= i) ++s;
-        const uint64_t e = dc_load(P.cand + ((int64_t)row * P.S + s) * SEG_CAP + (i - sm.off[s]));
-        kk[j] = desc_key(__uint_as_float((uint32_t)(e >> 32)), (uint32_t)e);
+  // registers at positions tid * EPT + j, ordered over a power of two of positions; EPT the
+  // fewest keys per thread that hold them all (a handful of planned elements is ordered
+  // inside one wave)
+  auto tail = [&](auto ept) {
+    constexpr int EPT = decltype(ept)::value;
+    const int p0 = tid * EPT;
+    uint64_t kk[EPT];
+    {
+      int s = 0;
+  #pragma unroll
+      for (int j = 0; j < EPT; ++j) {
+        const int i = p0 + j;
+        kk[j] = ~0ull;
+        if (i < n) {
+          while (s + 1 < P.S && sm.off[s + 1] <= i) ++s;
+          const uint64_t e = dc_load(P.cand + ((int64_t)row * P.S + s) * SEG_CAP + (i - sm.off[s]));
+          kk[j] = desc_key(__uint_as_float((uint32_t)(e >> 32)), (uint32_t)e);
+        }
       }
     }
-  }
-  int P2 = next_pow2(n < 2 ? 2 : n);
-  if (P2 < 64 * EPT) P2 = 64 * EPT;
-  block_sort_regs<EPT>(kk, P2, sm.u.keys);
-  // ---- top-k threshold: the k-th largest, k - 1 - n_above places into the ordered elements
-  float thr = -__builtin_inff();
-  if (kon) {
-    const int r = c.k - 1 - n_above;
-    if (r < 0 || r >= n) {
-      if (tid == 0) { P.status[row] = 1; R->step = WSTEP_NONE; }
-      return;
+    int P2 = next_pow2(n < 2 ? 2 : n);
+    if (P2 < 64 * EPT) P2 = 64 * EPT;
+    block_sort_regs<EPT>(kk, P2, sm.u.keys);
+    // ---- top-k threshold: the k-th largest, k - 1 - n_above places into the ordered elements
+    float thr = -__builtin_inff();
+    if (kon) {
+      const int r = c.k - 1 - n_above;
+      if (r < 0 || r >= n) {
+        if (tid == 0) { P.status[row] = 1; R->step = WSTEP_NONE; }
+        return;
+      }
+      thr = desc_key_val(block_key_at<EPT>(kk, r, &sm.kb[0], &sm));
     }
-    thr = desc_key_val(block_key_at<EPT>(kk, r, &sm.kb[0], &sm));
-  }
-  // per element: kept by top-k, its mass, its float32 probability under the top-k set
-  unsigned long long mk = 0ull;
-  int nk_own = 0;
-#pragma unroll
-  for (int j = 0; j < EPT; ++j) {
-    if (p0 + j < n) {
-      const float y = desc_key_val(kk[j]);
-      if (y >= thr) { mk += wfx(M, y); ++nk_own; }
-    }
-  }
-  const unsigned long long mtopk = wsum_u64<NT>(mk, &sm);
-  const int32_t n_topk_c = wsum_i<NT>(nk_own, &sm);
-  const int32_t n_topk = kon ? n_above + n_topk_c : nfin;
-  const uint64_t zk_fx = kon ? mass_above + mtopk : R->mass_tot;
-  const double zk = (double)zk_fx * WFX_INV;
-  const double rzk = 1.0 / zk;
-  // ---- top-p: first position whose float32 prefix of float32 probabilities exceeds top_p
-  int J = n_topk_c - 1;          // without top-p: every top-k element is kept
-  if (pon) {
-    const double base = (double)mass_above * WFX_INV * rzk;
-    if (n_above > 0 && (float)base > c.topp) {
-      if (tid == 0) { P.status[row] = 1; R->step = WSTEP_NONE; }
-      return;
-    }
-    float qv[EPT];
-    double qs = 0.0;
-#pragma unroll
+    // per element: kept by top-k, its mass, its float32 probability under the top-k set
+    unsigned long long mk = 0ull;
+    int nk_own = 0;
+  #pragma unroll
     for (int j = 0; j < EPT; ++j) {
-      qv[j] = 0.0f;
       if (p0 + j < n) {
         const float y = desc_key_val(kk[j]);
-        if (y >= thr) qv[j] = (float)((double)ns_expf(y - M) * rzk);
+        if (y >= thr) { mk += wfx(M, y); ++nk_own; }
       }
-      qs += (double)qv[j];
     }
-    double tot;
-    double run = base + wexcl_f64<NT>(qs, &tot, &sm);
-    if (tid == 0) sm.ib[1] = 0x7fffffff;
-    __syncthreads();
-    int cross = 0x7fffffff;
-#pragma unroll
+    const unsigned long long mtopk = wsum_u64<NT>(mk, &sm);
+    const int32_t n_topk_c = wsum_i<NT>(nk_own, &sm);
+    const int32_t n_topk = kon ? n_above + n_topk_c : nfin;
+    const uint64_t zk_fx = kon ? mass_above + mtopk : R->mass_tot;
+    const double zk = (double)zk_fx * WFX_INV;
+    const double rzk = 1.0 / zk;
+    // ---- top-p: first position whose float32 prefix of float32 probabilities exceeds top_p
+    int J = n_topk_c - 1;          // without top-p: every top-k element is kept
+    if (pon) {
+      const double base = (double)mass_above * WFX_INV * rzk;
+      if (n_above > 0 && (float)base > c.topp) {
+        if (tid == 0) { P.status[row] = 1; R->step = WSTEP_NONE; }
+        return;
+      }
+      float qv[EPT];
+      double qs = 0.0;
+  #pragma unroll
+      for (int j = 0; j < EPT; ++j) {
+        qv[j] = 0.0f;
+        if (p0 + j < n) {
+          const float y = desc_key_val(kk[j]);
+          if (y >= thr) qv[j] = (float)((double)ns_expf(y - M) * rzk);
+        }
+        qs += (double)qv[j];
+      }
+      double tot;
+      double run = base + wexcl_f64<NT>(qs, &tot, &sm);
+      if (tid == 0) sm.ib[1] = 0x7fffffff;
+      __syncthreads();
+      int cross = 0x7fffffff;
+  #pragma unroll
+      for (int j = 0; j < EPT; ++j) {
+        const int pos = p0 + j;
+        if (pos < n && pos < n_topk_c) {
+          run += (double)qv[j];
+          if ((float)run > c.topp && cross == 0x7fffffff) cross = pos;
+        }
+      }
+      if (cross != 0x7fffffff) atomicMin(&sm.ib[1], cross);
+      __syncthreads();
+      cross = sm.ib[1];
+      if (cross != 0x7fffffff) {
+        J = cross;
+      } else if (!kon0) {
+        // top-p alone and no crossing among the planned elements: the plan missed it
+        if (tid == 0) { P.status[row] = 1; R->step = WSTEP_NONE; }
+        return;
+      }
+    }
+    if (J < 0) J = 0;
+    const uint64_t kc = block_key_at<EPT>(kk, J, &sm.kb[1], &sm);
+    const float vstar = pon ? desc_key_val(kc) : -__builtin_inff();
+    const int32_t istar = pon ? (int32_t)desc_key_id(kc) : 0x7fffffff;
+    const int32_t n_kept = pon ? n_above + J + 1 : n_topk;
+    const WKeep keep{thr, vstar, istar};
+    // ---- kept mass per segment: above the planned bins plus the kept planned elements
+    unsigned long long mkept = 0ull;
+  #pragma unroll
     for (int j = 0; j < EPT; ++j) {
       const int pos = p0 + j;
-      if (pos < n && pos < n_topk_c) {
-        run += (double)qv[j];
-        if ((float)run > c.topp && cross == 0x7fffffff) cross = pos;
+      if (pos < n && pos <= J) {
+        const float y = desc_key_val(kk[j]);
+        if (y >= thr) {
+          const uint64_t fx = wfx(M, y);
+          mkept += fx;
+          atomicAdd(&sm.subq[desc_key_id(kk[j]) / SEG_EL], (unsigned long long)fx);
+        }
       }
     }
-    if (cross != 0x7fffffff) atomicMin(&sm.ib[1], cross);
+    const unsigned long long mk2 = wsum_u64<NT>(mkept, &sm);
+    const uint64_t zkept_fx = pon ? mass_above + mk2 : zk_fx;
+    const double zkept = (double)zkept_fx * WFX_INV;
+    if (tid == 0) {
+      const double ud = (double)c.u;
+      double run = 0.0, start = 0.0, laststart = 0.0;
+      int s = -1, lastnz = -1;
+      const double rzkept = 1.0 / zkept;
+      // the segment holding u, from the kept mass per segment
+      for (int i = 0; i < P.S; ++i) {
+        const double p = (double)sm.subq[i] * WFX_INV * rzkept;
+        if (sm.subq[i] != 0ull) { lastnz = i; laststart = run; }
+        if (s < 0 && run + p > ud && sm.subq[i] != 0ull) { s = i; start = run; }
+        run += p;
+      }
+      if (s < 0) { s = lastnz >= 0 ? lastnz : 0; start = laststart; }
+      sm.ib[2] = s;
+      sm.db[0] = start;
+    }
     __syncthreads();
-    cross = sm.ib[1];
-    if (cross != 0x7fffffff) {
-      J = cross;
-    } else if (!kon0) {
-      // top-p alone and no crossing among the planned elements: the plan missed it
-      if (tid == 0) { P.status[row] = 1; R->step = WSTEP_NONE; }
-      return;
+    const int s = sm.ib[2];
+    const double start = sm.db[0];
+    // the walk over that segment: two consecutive float32 chunks per thread a step (one
+    // bfloat16 chunk: the same registers)
+    constexpr int WL = EPC == 4 ? 2 : 1;
+    const int64_t tok = wide_locate<T, NT, WL, SEG_CH>(P, c, (int64_t)s * SEG_CH, start, 1.0 / zkept, M, keep, &sm, &fl);
+    if (tid == 0) {
+      P.out_ids[row] = tok;
+      seg_write_info(P.out_info, row, PATH_WIDE, n_kept, kon0 ? thr : -__builtin_inff(), n_topk, n, fl, vstar, istar);
+      R->thr = thr;
+      R->vstar = vstar;
+      R->istar = istar;
+      R->n_kept = n_kept;
+      R->zkept = zkept;
+      R->step = WSTEP_DRAWN;
+      P.status[row] = 0;
     }
-  }
-  if (J < 0) J = 0;
-  const uint64_t kc = block_key_at<EPT>(kk, J, &sm.kb[1], &sm);
-  const float vstar = pon ? desc_key_val(kc) : -__builtin_inff();
-  const int32_t istar = pon ? (int32_t)desc_key_id(kc) : 0x7fffffff;
-  const int32_t n_kept = pon ? n_above + J + 1 : n_topk;
-  const WKeep keep{thr, vstar, istar};
-  // ---- kept mass per segment: above the planned bins plus the kept planned elements
-  unsigned long long mkept = 0ull;
-#pragma unroll
-  for (int j = 0; j < EPT; ++j) {
-    const int pos = p0 + j;
-    if (pos < n && pos <= J) {
-      const float y = desc_key_val(kk[j]);
-      if (y >= thr) {
-        const uint64_t fx = wfx(M, y);
-        mkept += fx;
-        atomicAdd(&sm.subq[desc_key_id(kk[j]) / SEG_EL], (unsigned long long)fx);
-      }
-    }
-  }
-  const unsigned long long mk2 = wsum_u64<NT>(mkept, &sm);
-  const uint64_t zkept_fx = pon ? mass_above + mk2 : zk_fx;
-  const double zkept = (double)zkept_fx * WFX_INV;
-  if (tid == 0) {
-    const double ud = (double)c.u;
-    double run = 0.0, start = 0.0, laststart = 0.0;
-    int s = -1, lastnz = -1;
-    const double rzkept = 1.0 / zkept;
-    // the segment holding u, from the kept mass per segment
-    for (int i = 0; i < P.S; ++i) {
-      const double p = (double)sm.subq[i] * WFX_INV * rzkept;
-      if (sm.subq[i] != 0ull) { lastnz = i; laststart = run; }
-      if (s < 0 && run + p > ud && sm.subq[i] != 0ull) { s = i; start = run; }
-      run += p;
-    }
-    if (s < 0) { s = lastnz >= 0 ? lastnz : 0; start = laststart; }
-    sm.ib[2] = s;
-    sm.db[0] = start;
-  }
-  __syncthreads();
-  const int s = sm.ib[2];
-  const double start = sm.db[0];
-  // the walk over that segment: four consecutive chunks per thread, one step
-  const int64_t tok = wide_locate<T, NT, 4, SEG_CH>(P, c, (int64_t)s * SEG_CH, start, 1.0 / zkept, M, keep, &sm, &fl);
-  if (tid == 0) {
-    P.out_ids[row] = tok;
-    seg_write_info(P.out_info, row, PATH_WIDE, n_kept, kon0 ? thr : -__builtin_inff(), n_topk, n, fl, vstar, istar);
-    R->thr = thr;
-    R->vstar = vstar;
-    R->istar = istar;
-    R->n_kept = n_kept;
-    R->zkept = zkept;
-    R->step = WSTEP_DRAWN;
-    P.status[row] = 0;
-  }
+
+  };
+  if (n <= NT) tail(std::integral_constant<int, 1>{});
+  else if (n <= 2 * NT) tail(std::integral_constant<int, 2>{});
+  else if (n <= 4 * NT) tail(std::integral_constant<int, 4>{});
+  else tail(std::integral_constant<int, WCAND / NT>{});
 }
 
 // ------------------------------------------------------------------ pass 4: probabilities
