@@ -26,7 +26,7 @@
 extern "C" {
 #endif
 
-#define NS_ABI_VERSION 6
+#define NS_ABI_VERSION 7
 
 #define NS_OK 0
 #define NS_ERR_INVALID 1   /* bad argument (message says which) */
@@ -137,6 +137,21 @@ int ns_sample_workspace_bytes(int32_t n_sample, int64_t vocab, int32_t dtype, ui
 
 /* LDS bytes one workgroup of ns_sample needs for this vocab and history bound. */
 int ns_sample_lds_bytes(int64_t vocab, int32_t max_hist, int32_t* lds_bytes);
+
+/* Debug output, outside any sampling call: out[r * ld_out + v] (float32, v < vocab) = the
+ * penalized, temperature-scaled logit of sampled row r, i.e. the reference's logits after
+ * sampler.py:31-38 and :41-51 (the tensor its top-k and softmax read), computed by one of the
+ * routines ns_sample's kernels use:
+ *   formula 0  the streaming, top-k, split-row and segment kernels (NS_DEBUG_STREAM)
+ *   formula 1  the wide path (NS_DEBUG_WIDE)
+ *   formula 2  the per-row general code (NS_DEBUG_GENERAL)
+ * args as for ns_sample (uniforms, out_ids, mode, workspace and row_kinds are not read; the
+ * pointer checks are the same).  A row whose sample index or history is invalid is written
+ * as NaN.  No counterpart in the reference, where the tensor is an intermediate. */
+#define NS_DEBUG_STREAM 0
+#define NS_DEBUG_WIDE 1
+#define NS_DEBUG_GENERAL 2
+int ns_debug_scaled(const ns_sample_args* args, int32_t formula, float* out, int64_t ld_out, hipStream_t stream);
 
 /* Device-resident histories: one id list per request slot, capacity ids each, laid out as
  * int32 lengths[n_slots] (padded to 256 bytes) then int32 ids[n_slots][capacity].  The

@@ -24,14 +24,15 @@ NS_MODE_PER_ROW = 2
 NS_KIND_GREEDY = 1      # row_kinds: greedy rows (temperature 0)
 NS_KIND_SMALL_K = 2     # sampled rows with 1 <= top_k <= 64 and top_k < vocab
 NS_KIND_OTHER = 4       # every other sampled row (top-k off or larger)
-ABI_VERSION = 6
+NS_DEBUG_STREAM, NS_DEBUG_WIDE, NS_DEBUG_GENERAL = 0, 1, 2   # ns_debug_scaled routines
+ABI_VERSION = 7
 
 # exported symbols, as declared in include/ns_sampling.h
 NS_NOALLOC_SCRATCH_BYTES = 80 << 20   # ns_sample_noalloc's device scratch per GPU
 EXPORTS = ("ns_abi_version", "ns_sample", "ns_sample_noalloc", "ns_sample_lds_bytes", "ns_sample_workspace_bytes",
            "ns_hist_state_bytes",
            "ns_hist_assign", "ns_hist_append", "ns_seeded_uniforms", "ns_lm_head_bf16", "ns_lm_head_packed_bytes",
-           "ns_lm_head_pack_bf16", "ns_lm_head_bf16_packed", "ns_last_error")
+           "ns_lm_head_pack_bf16", "ns_lm_head_bf16_packed", "ns_debug_scaled", "ns_last_error")
 
 
 class NsSampleArgs(ctypes.Structure):
@@ -102,6 +103,9 @@ def load(path: str = LIB_PATH) -> ctypes.CDLL:
     lib.ns_hist_append.restype = ctypes.c_int
     lib.ns_hist_append.argtypes = [ctypes.c_void_p, ctypes.c_int32, ctypes.c_int32, ctypes.c_void_p, ctypes.c_void_p,
                                    ctypes.c_int32, ctypes.c_void_p, ctypes.c_void_p]
+    lib.ns_debug_scaled.restype = ctypes.c_int
+    lib.ns_debug_scaled.argtypes = [ctypes.POINTER(NsSampleArgs), ctypes.c_int32, ctypes.c_void_p, ctypes.c_int64,
+                                    ctypes.c_void_p]
     lib.ns_seeded_uniforms.restype = ctypes.c_int
     lib.ns_seeded_uniforms.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int32,
                                        ctypes.c_void_p, ctypes.c_void_p]
@@ -231,7 +235,7 @@ def aligned_rows(logits, sample_idx):
 def sample_raw(logits, temperature, top_k, top_p, rep_penalty, uniforms, out_ids, *, sample_idx=None,
                hist_offsets=None, hist_ids=None, max_hist: int = 0, out_probs=None, out_info=None,
                stream=None, workspace="auto", mode: int = NS_MODE_AUTO, row_kinds: int = 0,
-               hist_state=None, hist_slot=None) -> None:
+               hist_state=None, hist_slot=None, debug_scaled=None) -> None:
     """Launch ``ns_sample`` on device tensors (no copies, no synchronisation).
 
     logits: (N, V) float32 or bfloat16 CUDA tensor with unit stride in the last dim.
@@ -243,6 +247,9 @@ def sample_raw(logits, temperature, top_k, top_p, rep_penalty, uniforms, out_ids
     (see ``row_kinds``), 0 when unknown.  hist_state / hist_slot: device-resident histories
     (a ``HistoryState`` and the (B,) int32 slot of each row, -1 for none) instead of
     hist_offsets / hist_ids.
+    debug_scaled: a pair (formula, out) with out a (B, >= V) float32 tensor of unit stride
+    along V: instead of sampling, ``ns_debug_scaled`` writes each row's penalized,
+    temperature-scaled logits there, computed by routine ``formula`` (NS_DEBUG_*).
     """
     import torch
 
@@ -292,6 +299,13 @@ def sample_raw(logits, temperature, top_k, top_p, rep_penalty, uniforms, out_ids
         a.hist_capacity = int(hist_state.capacity)
     if stream is None:
         stream = torch.cuda.current_stream(logits.device)
+    if debug_scaled is not None:
+        formula, out = debug_scaled
+        if out.dtype != torch.float32 or out.dim() != 2 or out.stride(1) != 1 or int(out.shape[0]) < B:
+            raise ValueError("debug output must be a (B, >= V) float32 tensor with unit stride along V")
+        check(lib.ns_debug_scaled(ctypes.byref(a), int(formula), _ptr(out), int(out.stride(0)),
+                                  ctypes.c_void_p(int(stream.cuda_stream))))
+        return
     check(lib.ns_sample(ctypes.byref(a), ctypes.c_void_p(int(stream.cuda_stream))))
 
 

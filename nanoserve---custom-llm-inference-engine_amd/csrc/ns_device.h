@@ -330,21 +330,35 @@ __device__ __forceinline__ double rcp_f64(double x) {
 // ------------------------------------------------- exact division x / t
 // Correctly rounded quotient by a row-uniform divisor t > 0 with precomputed
 // r = RN(1/t): q0 = RN(x*r); rem = fma(-q0, t, x) is exact; q = RN(q0 + rem*r)
-// (Markstein's correction theorem for a correctly rounded reciprocal).  Outside
-// the range where the theorem's no-underflow/no-overflow conditions hold the
-// IEEE division is used.  Bit-exactness against IEEE x/t is tested on the CPU
-// over every float32 mantissa for a set of divisors.
+// (Markstein's correction theorem for a correctly rounded reciprocal).  The theorem's
+// conditions: r normal and correctly rounded (t in [2^-100, 2^100]), q0 and q normal
+// (|q0| in [2^-100, 2^100]), and rem exact, which holds when it is a multiple of the
+// smallest subnormal: rem is a multiple of ulp(q0) * ulp(t), at least |x| * 2^-48, so
+// |x| >= 2^-100 suffices; |q0| >= 2^-99 * r gives that.  div_lo(t, r) folds these into
+// one lower bound on |q0| (+inf: never), computed once per divisor; outside it the IEEE
+// division is used.  Bit-exactness against IEEE x/t is tested on the CPU over every
+// binade of the float range for a set of divisors.
+__host__ __device__ __forceinline__ float div_lo(float t, float r) {
+  return (t >= 0x1.0p-100f && t <= 0x1.0p+100f) ? __builtin_fmaxf(0x1.0p-100f, 0x1.0p-99f * r)
+                                                 : __builtin_inff();
+}
 __device__ __forceinline__ float div_rn(float x, float t, float r) {
   float q0 = x * r;
   float rem = __builtin_fmaf(-q0, t, x);
   float q = __builtin_fmaf(rem, r, q0);
   float aq = __builtin_fabsf(q0);
-  bool slow = !(aq >= 0x1.0p-100f && aq <= 0x1.0p+100f);
+  bool slow = !(aq >= div_lo(t, r) && aq <= 0x1.0p+100f);
   if (__ballot(slow) != 0ull) {  // wave-uniform branch: the IEEE division is never speculated
     asm volatile("");             // (the empty asm keeps the compiler from if-converting it)
     if (slow) q = x / t;
   }
   return q;
+}
+
+// The repetition penalty of one history token (sampler.py:37: score * p if score < 0 else
+// score / p), float32 and correctly rounded; rpen = RN(1/pen).
+__device__ __forceinline__ float pen_rn(float x, float pen, float rpen) {
+  return x < 0.0f ? x * pen : div_rn(x, pen, rpen);
 }
 
 }  // namespace ns

@@ -186,10 +186,7 @@ __device__ __forceinline__ int row_fast(const RowArgs P, const int row, const in
   const float tdiv = temp > 0.0f ? __builtin_fmaxf(temp, 1e-6f) : 1.0f;   // sampler.py:42
   const float rdiv = 1.0f / tdiv;
   const float rpen = 1.0f / pen;
-  auto pen_val = [&](float x) -> float {
-    // sampler.py:37: score * p if score < 0 else score / p (float32, correctly rounded)
-    return x < 0.0f ? x * pen : div_rn(x, pen, rpen);
-  };
+  auto pen_val = [&](float x) -> float { return pen_rn(x, pen, rpen); };
   float* fs = reinterpret_cast<float*>(&misc->red);      // 128 floats of scratch
   BlockScratch* red = &misc->red;
 

@@ -1258,6 +1258,82 @@ __global__ __launch_bounds__(256) void hist_append_kernel(int32_t* lens, int32_t
   lens[s] = l + 1;
 }
 
+// ---- the penalized, temperature-scaled logits of each row (sampler.py:31-38 then :41-51),
+// written whole by one of the routines the sampling kernels compute them with:
+//   DBG_STREAM  pen_val then div_rn (the streaming, top-k, split and segment kernels);
+//   DBG_WIDE    chunk_y (the wide path: multiply-and-correct, IEEE on a chunk out of range);
+//   DBG_GENERAL penalize (IEEE division) then div_rn (the per-row general code).
+// One workgroup per row; the history bitmap of the whole row in LDS.  A row whose history
+// or sample index is invalid is written as NaN.  Not on any sampling path: it exists so
+// that each routine can be compared bit for bit with the float32 tensor expression.
+enum { DBG_STREAM = 0, DBG_WIDE = 1, DBG_GENERAL = 2 };
+
+template <typename T>
+__global__ __launch_bounds__(1024) void debug_scaled_kernel(KParams p, int32_t formula, float* out, int64_t ld_out) {
+  extern __shared__ uint32_t bm[];
+  constexpr int EPC = T::EPC;
+  const int row = blockIdx.x;
+  const int tid = threadIdx.x;
+  const int64_t V = p.vocab;
+  const int64_t nbw = (V + 31) / 32;
+  float* orow = out + (int64_t)row * ld_out;
+  const int64_t src = p.sample_idx ? p.sample_idx[row] : (int64_t)row;
+  int32_t h0 = 0, h1 = 0;
+  row_history(p.hist_off, p.hist_slot, p.hist_len, p.hist_nslots, p.hist_cap, row, h0, h1);
+  if (src < 0 || src >= p.n_rows_total || h0 < 0 || h1 < h0) {
+    for (int64_t i = tid; i < V; i += 1024) orow[i] = __builtin_nanf("");
+    return;
+  }
+  for (int64_t i = tid; i < nbw; i += 1024) bm[i] = 0u;
+  __syncthreads();
+  for (int32_t i = h0 + tid; i < h1; i += 1024) {
+    const int32_t id = p.hist_ids[i];
+    if (id >= 0 && id < V) atomicOr(&bm[id >> 5], 1u << (id & 31));
+  }
+  __syncthreads();
+
+  const float temp = p.temperature[row];
+  const float pen = p.penalty[row];
+  WRowCtx c{};
+  c.row = row;
+  c.V = V;
+  c.src = src;
+  c.rowp = static_cast<const unsigned char*>(p.logits) + src * p.row_stride * T::SZ;
+  c.pen = pen;
+  c.rpen = 1.0f / pen;
+  c.tdiv = temp > 0.0f ? __builtin_fmaxf(temp, 1e-6f) : 1.0f;   // sampler.py:42
+  c.rdiv = 1.0f / c.tdiv;
+  c.scale = c.tdiv != 1.0f;
+  c.lo_t = div_lo(c.tdiv, c.rdiv);
+  c.lo_pen = div_lo(pen, c.rpen);
+  c.pen_on = pen != 1.0f && h1 > h0;                           // sampler.py:33
+  const int64_t nch = (V + EPC - 1) / EPC;
+  const int64_t nfull = V / EPC;
+  const uint4* rowv = reinterpret_cast<const uint4*>(c.rowp);
+  // every lane of a wave takes the same number of steps (chunk_y votes across the wave)
+  for (int64_t c0 = 0; c0 < nch; c0 += 1024) {
+    const int64_t ch = c0 + tid;
+    uint4 w = ch < nfull ? rowv[ch] : seg_ninf<T>();
+    w = wide_chunk_fix<T>(c, ch, w);
+    const uint32_t hb = (ch < nch && c.pen_on) ? T::bits(bm, ch) : 0u;
+    float y[EPC];
+    if (formula == DBG_WIDE) {
+      chunk_y<T>(c, w, hb, ch * EPC, y);
+    } else {
+#pragma unroll
+      for (int e = 0; e < EPC; ++e) {
+        float x = T::elem(w, e);
+        if ((hb >> e) & 1u)
+          x = formula == DBG_GENERAL ? penalize(x, pen) : pen_rn(x, pen, c.rpen);
+        y[e] = div_rn(x, c.tdiv, c.rdiv);
+      }
+    }
+#pragma unroll
+    for (int e = 0; e < EPC; ++e)
+      if (ch * EPC + e < V) orow[ch * EPC + e] = y[e];
+  }
+}
+
 }  // namespace ns
 
 // =====================================================================================
@@ -1384,6 +1460,61 @@ int device_info(int dev, DevInfo& out) {
   out = d;
   return NS_OK;
 }
+// Checks the arguments every entry point that reads an ns_sample_args shares (n_sample > 0)
+// and fills p's pointers and sizes; has_hist: the call carries histories.
+int sample_params(const ns_sample_args* a, ns::KParams& p, bool& has_hist) {
+  if (a->logits == nullptr || a->temperature == nullptr || a->top_k == nullptr || a->top_p == nullptr ||
+      a->rep_penalty == nullptr || a->uniforms == nullptr || a->out_ids == nullptr)
+    return fail(NS_ERR_INVALID, "a required pointer is NULL");
+  if (a->dtype != NS_DTYPE_F32 && a->dtype != NS_DTYPE_BF16) return fail(NS_ERR_INVALID, "dtype must be f32 or bf16");
+  if (a->vocab <= 0 || a->vocab > NS_MAX_VOCAB)
+    return fail(NS_ERR_INVALID, "vocab must be in [1, " + std::to_string(NS_MAX_VOCAB) + "]");
+  if (a->row_stride < a->vocab) return fail(NS_ERR_INVALID, "row_stride < vocab");
+  if (a->n_rows_total <= 0) return fail(NS_ERR_INVALID, "n_rows_total <= 0");
+  if (a->sample_idx == nullptr && a->n_rows_total < a->n_sample)
+    return fail(NS_ERR_INVALID, "n_rows_total < n_sample without sample_idx");
+  if (a->hist_offsets != nullptr && a->hist_ids == nullptr) return fail(NS_ERR_INVALID, "hist_ids is NULL");
+  // history source: CSR offsets and ids, device-resident request slots, or none
+  const bool slots = a->hist_state != nullptr;
+  if (slots) {
+    if (a->hist_offsets != nullptr || a->hist_ids != nullptr)
+      return fail(NS_ERR_INVALID, "hist_state excludes hist_offsets and hist_ids");
+    if (a->hist_slot == nullptr) return fail(NS_ERR_INVALID, "hist_slot is NULL");
+    const int rs = hist_state_check(a->hist_n_slots, a->hist_capacity);
+    if (rs != NS_OK) return rs;
+  }
+  has_hist = a->hist_offsets != nullptr || slots;
+  const int32_t* h_ids = slots ? hist_state_ids(a->hist_state, a->hist_n_slots) : a->hist_ids;
+  const int32_t* h_len = slots ? static_cast<const int32_t*>(a->hist_state) : nullptr;
+  const int32_t* h_slot = slots ? a->hist_slot : nullptr;
+  if (a->max_hist < 0 || a->max_hist > NS_MAX_HISTORY)
+    return fail(NS_ERR_INVALID, "max_hist must be in [0, " + std::to_string(NS_MAX_HISTORY) + "]");
+  const int esz = a->dtype == NS_DTYPE_F32 ? 4 : 2;
+  if (((uintptr_t)a->logits % 16) != 0 || ((a->row_stride * esz) % 16) != 0)
+    return fail(NS_ERR_ALIGN, "logits rows must start on 16-byte boundaries (base and row stride)");
+  p.logits = a->logits;
+  p.row_stride = a->row_stride;
+  p.vocab = a->vocab;
+  p.n_rows_total = a->n_rows_total;
+  p.sample_idx = a->sample_idx;
+  p.temperature = a->temperature;
+  p.top_k = a->top_k;
+  p.top_p = a->top_p;
+  p.penalty = a->rep_penalty;
+  p.hist_off = a->hist_offsets;
+  p.hist_ids = h_ids;
+  p.hist_slot = h_slot;
+  p.hist_len = h_len;
+  p.hist_nslots = a->hist_n_slots;
+  p.hist_cap = a->hist_capacity;
+  p.uniforms = a->uniforms;
+  p.out_ids = a->out_ids;
+  p.out_probs = a->out_probs;
+  p.out_info = a->out_info;
+  p.n_sample = a->n_sample;
+  return NS_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -1608,61 +1739,15 @@ int ns_sample(const ns_sample_args* a, hipStream_t stream) {
   if (a == nullptr) return fail(NS_ERR_INVALID, "args is NULL");
   if (a->n_sample < 0) return fail(NS_ERR_INVALID, "n_sample < 0");
   if (a->n_sample == 0) return NS_OK;
-  if (a->logits == nullptr || a->temperature == nullptr || a->top_k == nullptr || a->top_p == nullptr ||
-      a->rep_penalty == nullptr || a->uniforms == nullptr || a->out_ids == nullptr)
-    return fail(NS_ERR_INVALID, "a required pointer is NULL");
-  if (a->dtype != NS_DTYPE_F32 && a->dtype != NS_DTYPE_BF16) return fail(NS_ERR_INVALID, "dtype must be f32 or bf16");
-  if (a->vocab <= 0 || a->vocab > NS_MAX_VOCAB)
-    return fail(NS_ERR_INVALID, "vocab must be in [1, " + std::to_string(NS_MAX_VOCAB) + "]");
-  if (a->row_stride < a->vocab) return fail(NS_ERR_INVALID, "row_stride < vocab");
-  if (a->n_rows_total <= 0) return fail(NS_ERR_INVALID, "n_rows_total <= 0");
-  if (a->sample_idx == nullptr && a->n_rows_total < a->n_sample)
-    return fail(NS_ERR_INVALID, "n_rows_total < n_sample without sample_idx");
-  if (a->hist_offsets != nullptr && a->hist_ids == nullptr) return fail(NS_ERR_INVALID, "hist_ids is NULL");
-  // history source: CSR offsets and ids, device-resident request slots, or none
-  const bool slots = a->hist_state != nullptr;
-  if (slots) {
-    if (a->hist_offsets != nullptr || a->hist_ids != nullptr)
-      return fail(NS_ERR_INVALID, "hist_state excludes hist_offsets and hist_ids");
-    if (a->hist_slot == nullptr) return fail(NS_ERR_INVALID, "hist_slot is NULL");
-    const int rs = hist_state_check(a->hist_n_slots, a->hist_capacity);
-    if (rs != NS_OK) return rs;
-  }
-  const bool has_hist = a->hist_offsets != nullptr || slots;
-  const int32_t* h_ids = slots ? hist_state_ids(a->hist_state, a->hist_n_slots) : a->hist_ids;
-  const int32_t* h_len = slots ? static_cast<const int32_t*>(a->hist_state) : nullptr;
-  const int32_t* h_slot = slots ? a->hist_slot : nullptr;
-  if (a->max_hist < 0 || a->max_hist > NS_MAX_HISTORY)
-    return fail(NS_ERR_INVALID, "max_hist must be in [0, " + std::to_string(NS_MAX_HISTORY) + "]");
-  const int esz = a->dtype == NS_DTYPE_F32 ? 4 : 2;
-  if (((uintptr_t)a->logits % 16) != 0 || ((a->row_stride * esz) % 16) != 0)
-    return fail(NS_ERR_ALIGN, "logits rows must start on 16-byte boundaries (base and row stride)");
+  ns::KParams p{};
+  bool has_hist = false;
+  int rc = sample_params(a, p, has_hist);
+  if (rc != NS_OK) return rc;
   const WsLayout L = ws_layout(a->n_sample, a->vocab, a->dtype);
 
   int32_t lds = 0;
-  int rc = ns_sample_lds_bytes(a->vocab, has_hist ? a->max_hist : 0, &lds);
+  rc = ns_sample_lds_bytes(a->vocab, has_hist ? a->max_hist : 0, &lds);
   if (rc != NS_OK) return rc;
-  ns::KParams p{};
-  p.logits = a->logits;
-  p.row_stride = a->row_stride;
-  p.vocab = a->vocab;
-  p.n_rows_total = a->n_rows_total;
-  p.sample_idx = a->sample_idx;
-  p.temperature = a->temperature;
-  p.top_k = a->top_k;
-  p.top_p = a->top_p;
-  p.penalty = a->rep_penalty;
-  p.hist_off = a->hist_offsets;
-  p.hist_ids = h_ids;
-  p.hist_slot = h_slot;
-  p.hist_len = h_len;
-  p.hist_nslots = a->hist_n_slots;
-  p.hist_cap = a->hist_capacity;
-  p.uniforms = a->uniforms;
-  p.out_ids = a->out_ids;
-  p.out_probs = a->out_probs;
-  p.out_info = a->out_info;
-  p.n_sample = a->n_sample;
   {
     const int64_t mh = has_hist ? a->max_hist : 0;
     const int64_t nbw = (a->vocab + 31) / 32;
@@ -1775,9 +1860,9 @@ int ns_sample(const ns_sample_args* a, hipStream_t stream) {
     s.top_p = a->top_p;
     s.penalty = a->rep_penalty;
     s.hist_off = a->hist_offsets;
-    s.hist_ids = h_ids;
-    s.hist_slot = h_slot;
-    s.hist_len = h_len;
+    s.hist_ids = p.hist_ids;
+    s.hist_slot = p.hist_slot;
+    s.hist_len = p.hist_len;
     s.hist_nslots = a->hist_n_slots;
     s.hist_cap = a->hist_capacity;
     s.uniforms = a->uniforms;
@@ -1819,9 +1904,9 @@ int ns_sample(const ns_sample_args* a, hipStream_t stream) {
     w.top_p = a->top_p;
     w.penalty = a->rep_penalty;
     w.hist_off = a->hist_offsets;
-    w.hist_ids = h_ids;
-    w.hist_slot = h_slot;
-    w.hist_len = h_len;
+    w.hist_ids = p.hist_ids;
+    w.hist_slot = p.hist_slot;
+    w.hist_len = p.hist_len;
     w.hist_nslots = a->hist_n_slots;
     w.hist_cap = a->hist_capacity;
     w.uniforms = a->uniforms;
@@ -1879,6 +1964,28 @@ int ns_sample(const ns_sample_args* a, hipStream_t stream) {
   }
   e = hipGetLastError();
   if (e != hipSuccess) return fail(NS_ERR_HIP, std::string("kernel launch: ") + hipGetErrorString(e));
+  return NS_OK;
+}
+
+int ns_debug_scaled(const ns_sample_args* a, int32_t formula, float* out, int64_t ld_out, hipStream_t stream) {
+  if (a == nullptr) return fail(NS_ERR_INVALID, "args is NULL");
+  if (a->n_sample < 0) return fail(NS_ERR_INVALID, "n_sample < 0");
+  if (a->n_sample == 0) return NS_OK;
+  if (formula < ns::DBG_STREAM || formula > ns::DBG_GENERAL) return fail(NS_ERR_INVALID, "unknown formula");
+  if (out == nullptr) return fail(NS_ERR_INVALID, "out is NULL");
+  if (ld_out < a->vocab) return fail(NS_ERR_INVALID, "ld_out < vocab");
+  ns::KParams p{};
+  bool has_hist = false;
+  const int rc = sample_params(a, p, has_hist);
+  if (rc != NS_OK) return rc;
+  const size_t lds = (size_t)((a->vocab + 31) / 32) * 4;
+  const dim3 grid((unsigned)a->n_sample), block(1024);
+  if (a->dtype == NS_DTYPE_BF16)
+    hipLaunchKernelGGL((ns::debug_scaled_kernel<ns::BF16>), grid, block, lds, stream, p, formula, out, ld_out);
+  else
+    hipLaunchKernelGGL((ns::debug_scaled_kernel<ns::F32>), grid, block, lds, stream, p, formula, out, ld_out);
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return fail(NS_ERR_HIP, std::string("debug kernel launch: ") + hipGetErrorString(e));
   return NS_OK;
 }
 

@@ -806,10 +806,7 @@ __device__ __forceinline__ void segment_body(const SegParams& P, SegSmem& sm) {
   const float tdiv = temp > 0.0f ? __builtin_fmaxf(temp, 1e-6f) : 1.0f;   // sampler.py:42
   const float rdiv = 1.0f / tdiv;
   const float rpen = 1.0f / pen;
-  auto pen_val = [&](float x) -> float {
-    // sampler.py:37: score * p if score < 0 else score / p (float32, correctly rounded)
-    return x < 0.0f ? x * pen : div_rn(x, pen, rpen);
-  };
+  auto pen_val = [&](float x) -> float { return pen_rn(x, pen, rpen); };
   int32_t flags = 0;
 
   // ---- history: bitmap of the segment and the unique ids in it (set semantics)

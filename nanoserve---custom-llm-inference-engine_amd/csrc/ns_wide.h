@@ -282,6 +282,7 @@ struct WRowCtx {
   int64_t V, src;
   const unsigned char* rowp;
   float tdiv, rdiv, pen, rpen, topp, u;
+  float lo_t, lo_pen;   // div_lo of the temperature and of the penalty
   int32_t k, h0, H;
   bool pen_on, valid, scale;
 };
@@ -309,6 +310,8 @@ __device__ __forceinline__ WRowCtx wide_row_ctx(const WideParams& P, int row) {
   c.rdiv = 1.0f / c.tdiv;
   c.scale = c.tdiv != 1.0f;
   c.rpen = 1.0f / c.pen;
+  c.lo_t = div_lo(c.tdiv, c.rdiv);
+  c.lo_pen = div_lo(c.pen, c.rpen);
   c.rowp = (const unsigned char*)P.logits + c.src * P.row_stride * T::SZ;
   return c;
 }
@@ -378,14 +381,14 @@ __device__ __forceinline__ void chunk_y(const WRowCtx& c, const uint4& w, uint32
       } else {
         const float q0 = x * c.rpen;
         const float aq = __builtin_fabsf(q0);
-        slow |= !(aq >= 0x1.0p-100f && aq <= 0x1.0p+100f);
+        slow |= !(aq >= c.lo_pen && aq <= 0x1.0p+100f);
         x = __builtin_fmaf(__builtin_fmaf(-q0, c.pen, x), c.rpen, q0);
       }
     }
     if (c.scale) {
       const float q0 = x * c.rdiv;
       const float aq = __builtin_fabsf(q0);
-      slow |= !(aq >= 0x1.0p-100f && aq <= 0x1.0p+100f);
+      slow |= !(aq >= c.lo_t && aq <= 0x1.0p+100f);
       x = __builtin_fmaf(__builtin_fmaf(-q0, c.tdiv, x), c.rdiv, q0);
     }
     y[e] = x;

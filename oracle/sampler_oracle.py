@@ -127,6 +127,16 @@ def _apply_penalty(logits: torch.Tensor, penalties: Sequence[float], histories: 
             logits[i].index_copy_(0, ids, score)
 
 
+def penalized_scaled(logits: torch.Tensor, temperature, penalties, histories):
+    """sampler.py:31-38 then :41-51 on a (B, V) float32 tensor (left unchanged): the logits
+    after the repetition penalty, and after the penalty and the temperature division."""
+    logits = logits.clone()
+    _apply_penalty(logits, [float(p) for p in penalties], histories)
+    penalized = logits.clone()
+    temps = torch.tensor([effective_temperature(float(t)) for t in temperature], dtype=logits.dtype)
+    return penalized, logits / temps.unsqueeze(1)
+
+
 def sample(rows, temperature, top_k, top_p, repetition_penalty, histories, uniforms) -> OracleResult:
     """Run the restated sampler on ``rows`` (B, V) float32 (numpy or CPU tensor)."""
     logits = torch.as_tensor(np.asarray(rows, dtype=np.float32)).clone()
@@ -137,13 +147,8 @@ def sample(rows, temperature, top_k, top_p, repetition_penalty, histories, unifo
     penalties = [float(x) for x in repetition_penalty]
     u = np.asarray(uniforms, dtype=np.float32)
 
-    _apply_penalty(logits, penalties, histories)
-    penalized = logits.clone()
-
-    # sampler.py:41-51
-    temps = torch.tensor([effective_temperature(t) for t in temperature], dtype=logits.dtype)
+    penalized, logits = penalized_scaled(logits, temperature, penalties, histories)
     greedy = np.array([t == 0.0 for t in temperature], dtype=bool)
-    logits = logits / temps.unsqueeze(1)
     scaled = logits.clone()
 
     # sampler.py:53-58

@@ -3,10 +3,14 @@ IEEE float division, bit for bit.
 
 The kernels divide by a row-uniform divisor t (the temperature, sampler.py:51, and the
 repetition penalty, sampler.py:37) as q0 = RN(x * RN(1/t)), then one fma-based
-correction.  tests/native/div_rn_check.c runs that formula on the CPU with C's fmaf
-over every mantissa of 21 binades (every third exponent from -30 to 30) for 16 fixed
-divisors (the penalties and temperatures the workloads use among them) and random
-ones, both signs, and compares with x / t.
+correction, with IEEE division where the correction theorem's conditions fail.
+tests/native/div_rn_check.c runs that formula on the CPU with C's fmaf over every binade
+of the float range (a stride of mantissas in each, every mantissa in three, subnormal
+bit patterns, zeros, infinities, NaN) for 28 fixed divisors (the workloads' penalties and
+temperatures, the temperature clamp, divisors next to the range limits) and random ones,
+both signs, and compares with x / t.  The earlier range rule, which tested |q0| alone,
+must fail the same check (its remainder is inexact for |x| < 2^-100 under divisors
+below 1): the check can tell the two apart.
 """
 import os
 import shutil
@@ -28,3 +32,6 @@ def test_div_rn_matches_ieee_division():
     print(res.stdout)
     assert res.returncode == 0, res.stdout + res.stderr
     assert "mismatches 0" in res.stdout
+    old = subprocess.run([exe, "0", "old"], capture_output=True, text=True, timeout=300)
+    print(old.stdout)
+    assert old.returncode == 1 and "mismatch t=" in old.stdout, old.stdout + old.stderr
