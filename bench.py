@@ -461,7 +461,7 @@ def main(argv=None):
     wrap_ms = (time.perf_counter() - t1) / nwrap * 1e3
     # the same calls with the histories kept on the device (copied once per request, each
     # sampled token appended in place): the per-step host work is the parameters only
-    dh = S.DeviceHistories(dev, w.batch, capacity=_pkg("_lib").NS_MAX_HISTORY)
+    dh = S.DeviceHistories(dev, w.batch, capacity=_pkg("_lib").NS_LDS_HISTORY)
     for i, h in enumerate(hist_lists):
         dh.open(i, h)
     reqs = list(range(w.batch))

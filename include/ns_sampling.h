@@ -26,7 +26,7 @@
 extern "C" {
 #endif
 
-#define NS_ABI_VERSION 7
+#define NS_ABI_VERSION 8
 
 #define NS_OK 0
 #define NS_ERR_INVALID 1   /* bad argument (message says which) */
@@ -45,7 +45,11 @@ extern "C" {
 #define NS_KIND_OTHER 4       /* row_kinds: every other sampled row (top-k off, or top_k > 64) */
 
 #define NS_MAX_VOCAB 262144     /* vocab limit (LDS presence bitmap of vocab/8 bytes) */
-#define NS_MAX_HISTORY 8192     /* per-row history limit (the reference's max_model_len, config.py:52) */
+#define NS_MAX_HISTORY (1 << 20) /* per-row history limit, in ids (the reference's max_model_len is 8192,
+                                    config.py:52); longer rows are reported, not sampled */
+#define NS_LDS_HISTORY 8192     /* longest history whose distinct ids the general per-row code keeps in
+                                   LDS; a call with a larger max_hist keeps them in its workspace (sized
+                                   by ns_sample_workspace_bytes from max_hist) and is refused without one */
 #define NS_INFO_WORDS 8         /* int32 words per row in out_info */
 #define NS_SEG_MAX_ROWS 16384   /* most rows a segmented call takes (AUTO switches to per-row above) */
 #define NS_WIDE_MAX_ROWS 4096   /* most rows a call splits over segment workgroups (NS_KIND_OTHER rows) */
@@ -81,7 +85,8 @@ typedef struct ns_sample_args {
   const float*   rep_penalty;   /* [B] SamplingParams.repetition_penalty; 1 disables (sampler.py:33) */
   const int32_t* hist_offsets;  /* [B+1] CSR offsets into hist_ids, or NULL for no histories */
   const int32_t* hist_ids;      /* token ids of each row's history (history_token_ids, sampler.py:25) */
-  int32_t        max_hist;      /* upper bound on any row's history length (sizes LDS), <= NS_MAX_HISTORY */
+  int32_t        max_hist;      /* upper bound on any row's history length (sizes LDS and, above
+                                   NS_LDS_HISTORY, the workspace), <= NS_MAX_HISTORY */
   const float*   uniforms;      /* [B] uniforms in [0, 1) replacing torch.multinomial's RNG (sampler.py:87) */
   int64_t*       out_ids;       /* [B] sampled token ids (the LongTensor returned at sampler.py:89) */
   float*         out_probs;     /* [B, vocab] final probabilities (sampler.py:76-80), or NULL; greedy rows
@@ -132,8 +137,9 @@ int ns_sample(const ns_sample_args* args, hipStream_t stream);
  * other threads) race.  Results are those of ns_sample with a workspace. */
 int ns_sample_noalloc(const ns_sample_args* args, hipStream_t stream);
 
-/* Workspace bytes ns_sample needs for n_sample rows of this vocab and logits dtype. */
-int ns_sample_workspace_bytes(int32_t n_sample, int64_t vocab, int32_t dtype, uint64_t* bytes);
+/* Workspace bytes ns_sample needs for n_sample rows of this vocab and logits dtype, with
+ * histories of up to max_hist ids (the call's max_hist; 0 without histories). */
+int ns_sample_workspace_bytes(int32_t n_sample, int64_t vocab, int32_t dtype, int32_t max_hist, uint64_t* bytes);
 
 /* LDS bytes one workgroup of ns_sample needs for this vocab and history bound. */
 int ns_sample_lds_bytes(int64_t vocab, int32_t max_hist, int32_t* lds_bytes);

@@ -16,7 +16,8 @@ NS_OK = 0
 NS_DTYPE_F32 = 0
 NS_DTYPE_BF16 = 1
 NS_MAX_VOCAB = 262144
-NS_MAX_HISTORY = 8192
+NS_MAX_HISTORY = 1 << 20   # per-row history limit (ids)
+NS_LDS_HISTORY = 8192      # longest history the general per-row code keeps in LDS (longer: in the workspace)
 NS_INFO_WORDS = 8
 NS_MODE_AUTO = 0
 NS_MODE_SEGMENTED = 1
@@ -25,7 +26,7 @@ NS_KIND_GREEDY = 1      # row_kinds: greedy rows (temperature 0)
 NS_KIND_SMALL_K = 2     # sampled rows with 1 <= top_k <= 64 and top_k < vocab
 NS_KIND_OTHER = 4       # every other sampled row (top-k off or larger)
 NS_DEBUG_STREAM, NS_DEBUG_WIDE, NS_DEBUG_GENERAL = 0, 1, 2   # ns_debug_scaled routines
-ABI_VERSION = 7
+ABI_VERSION = 8
 
 # exported symbols, as declared in include/ns_sampling.h
 NS_NOALLOC_SCRATCH_BYTES = 80 << 20   # ns_sample_noalloc's device scratch per GPU
@@ -93,7 +94,7 @@ def load(path: str = LIB_PATH) -> ctypes.CDLL:
     lib.ns_sample_lds_bytes.restype = ctypes.c_int
     lib.ns_sample_lds_bytes.argtypes = [ctypes.c_int64, ctypes.c_int32, ctypes.POINTER(ctypes.c_int32)]
     lib.ns_sample_workspace_bytes.restype = ctypes.c_int
-    lib.ns_sample_workspace_bytes.argtypes = [ctypes.c_int32, ctypes.c_int64, ctypes.c_int32,
+    lib.ns_sample_workspace_bytes.argtypes = [ctypes.c_int32, ctypes.c_int64, ctypes.c_int32, ctypes.c_int32,
                                               ctypes.POINTER(ctypes.c_uint64)]
     lib.ns_hist_state_bytes.restype = ctypes.c_int
     lib.ns_hist_state_bytes.argtypes = [ctypes.c_int32, ctypes.c_int32, ctypes.POINTER(ctypes.c_uint64)]
@@ -148,16 +149,16 @@ def lds_bytes(vocab: int, max_hist: int) -> int:
     return int(out.value)
 
 
-def workspace_bytes(n_sample: int, vocab: int, dtype: int) -> int:
+def workspace_bytes(n_sample: int, vocab: int, dtype: int, max_hist: int = 0) -> int:
     out = ctypes.c_uint64(0)
-    check(load().ns_sample_workspace_bytes(int(n_sample), int(vocab), int(dtype), ctypes.byref(out)))
+    check(load().ns_sample_workspace_bytes(int(n_sample), int(vocab), int(dtype), int(max_hist), ctypes.byref(out)))
     return int(out.value)
 
 
 _WS = {}
 
 
-def workspace_for(device, n_sample: int, vocab: int, dtype: int):
+def workspace_for(device, n_sample: int, vocab: int, dtype: int, max_hist: int = 0):
     """A cached zero-filled workspace tensor on ``device`` large enough for this call.
 
     One workspace per device, used on the current stream; it is regrown (and
@@ -165,7 +166,7 @@ def workspace_for(device, n_sample: int, vocab: int, dtype: int):
     """
     import torch
 
-    need = workspace_bytes(n_sample, vocab, dtype)
+    need = workspace_bytes(n_sample, vocab, dtype, max_hist)
     key = str(device)
     ws = _WS.get(key)
     if ws is None or ws.numel() < need:
@@ -284,7 +285,8 @@ def sample_raw(logits, temperature, top_k, top_p, rep_penalty, uniforms, out_ids
     a.out_probs = _ptr(out_probs)
     a.out_info = _ptr(out_info)
     if isinstance(workspace, str) and workspace == "auto":
-        workspace = workspace_for(logits.device, B, a.vocab, dt)
+        workspace = workspace_for(logits.device, B, a.vocab, dt,
+                                  max_hist if (hist_offsets is not None or hist_state is not None) else 0)
     if workspace is not None:
         a.workspace = _ptr(workspace)
         a.workspace_bytes = int(workspace.numel() * workspace.element_size())

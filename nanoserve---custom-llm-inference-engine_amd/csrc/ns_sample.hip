@@ -17,6 +17,8 @@
 #include "ns_sampling.h"
 
 static_assert(ns::WIDE_MAX_ROWS == NS_WIDE_MAX_ROWS, "wide-path row limit");
+static_assert(ns::MAX_HIST == NS_MAX_HISTORY, "per-row history limit");
+static_assert(ns::LDS_HIST == NS_LDS_HISTORY, "history kept in LDS by the general code");
 
 namespace ns {
 
@@ -823,8 +825,6 @@ __device__ __attribute__((always_inline, cold)) inline void row_general(KArgs PA
   extern __shared__ __align__(16) unsigned char smem[];
   Misc* misc = reinterpret_cast<Misc*>(smem);
   uint32_t* bm = reinterpret_cast<uint32_t*>(smem + P.off_bm);
-  float* xl_val = reinterpret_cast<float*>(smem + P.off_xl);
-  int32_t* xl_id = reinterpret_cast<int32_t*>(smem + P.off_xl + 4u * (uint32_t)P.xcap);
   uint64_t* cand = reinterpret_cast<uint64_t*>(smem + P.off_cand);
   uint32_t* hcnt = reinterpret_cast<uint32_t*>(smem + P.off_hist);
   uint64_t* hmass = reinterpret_cast<uint64_t*>(smem + P.off_hist + 4u * NB);
@@ -852,21 +852,35 @@ __device__ __attribute__((always_inline, cold)) inline void row_general(KArgs PA
   const int32_t k = P.top_k[row];
   int32_t h0 = 0, h1 = 0;
   row_history(P.hist_off, P.hist_slot, P.hist_len, P.hist_nslots, P.hist_cap, row, h0, h1);
+  const int32_t H = h1 - h0;
+  const bool pen_on = (pen != 1.0f) && H > 0;                            // sampler.py:33
+  // the extras list (unique history ids, then the tail) in LDS, or for a history with
+  // more distinct ids than LDS holds, in the row's region of the workspace
+  const int64_t umax = pen_on ? (H < V ? H : V) : 0;
+  const bool xl_lds = umax <= P.xcap - 8;
   int32_t flags = 0;
   if (src < 0 || src >= P.n_rows_total) flags |= FLAG_BAD_ROW;
-  if (h1 < h0 || h1 - h0 > MAX_HIST || h1 - h0 > P.xcap - 8) flags |= FLAG_HIST_TOO_LONG;
+  if (h1 < h0 || H > MAX_HIST || (!xl_lds && (P.xl_glob == nullptr || umax > P.xg_cap - 8)))
+    flags |= FLAG_HIST_TOO_LONG;
   if (flags != 0) {
     if (tid == 0) P.out_ids[row] = -1;
     write_info(o, PATH_ERROR, 0, 0.0f, 0, 0, flags, 0.0f, -1);
     return;
+  }
+  float* xl_val;
+  int32_t* xl_id;
+  if (xl_lds) {
+    xl_val = reinterpret_cast<float*>(smem + P.off_xl);
+    xl_id = reinterpret_cast<int32_t*>(smem + P.off_xl + 4u * (uint32_t)P.xcap);
+  } else {
+    xl_val = P.xl_glob + (int64_t)row * 2 * P.xg_cap;
+    xl_id = reinterpret_cast<int32_t*>(xl_val + P.xg_cap);
   }
   const unsigned char* rowp = (const unsigned char*)P.logits + src * P.row_stride * T::SZ;
   const uint4* rowv = reinterpret_cast<const uint4*>(rowp);
   const bool greedy = temp == 0.0f;
   const float tdiv = temp > 0.0f ? __builtin_fmaxf(temp, 1e-6f) : 1.0f;  // sampler.py:42
   const float rdiv = 1.0f / tdiv;
-  const int32_t H = h1 - h0;
-  const bool pen_on = (pen != 1.0f) && H > 0;                            // sampler.py:33
   const bool topk_on = k > 0 && (int64_t)k < V;                          // sampler.py:55
   const bool topp_on = topp < 1.0f;                                      // sampler.py:63
   const float p32 = topp;
@@ -890,29 +904,33 @@ __device__ __attribute__((always_inline, cold)) inline void row_general(KArgs PA
   if (tid == 0) { misc->xl_n = 0; misc->cand_n = 0; misc->flags = 0; }
   __syncthreads();
 
-  // ---- phase 1: presence bitmap and unique history ids (set semantics, sampler.py:34-38)
+  // ---- phase 1: presence bitmap and unique history ids (set semantics, sampler.py:34-38);
+  // the first 8192 ids from registers, any further ones streamed in batches of NT
   if (pen_on) {
-#pragma unroll
-    for (int s = 0; s < HPT; ++s) {
-      if (s * NT < H) {
-        const int32_t id = hid[s];
-        const bool act = s * NT + tid < H;
-        const bool valid = act && id >= 0 && (int64_t)id < V;
-        if (act && !valid) atomicOr(&misc->flags, FLAG_BAD_HIST_ID);
-        bool uniq = false;
-        if (valid) {
-          const uint32_t bit = 1u << (id & 31);
-          const uint32_t old = atomicOr(&bm[id >> 5], bit);
-          uniq = (old & bit) == 0u;
-        }
-        const uint64_t m = ballot(uniq);
-        if (m != 0ull) {
-          int base = 0;
-          if (lane == 0) base = atomicAdd(&misc->xl_n, __popcll(m));
-          base = __shfl(base, 0);
-          if (uniq) xl_id[base + lanes_below(m)] = id;
-        }
+    auto mark = [&](int32_t id, bool act) {   // every lane of the wave calls it
+      const bool valid = act && id >= 0 && (int64_t)id < V;
+      if (act && !valid) atomicOr(&misc->flags, FLAG_BAD_HIST_ID);
+      bool uniq = false;
+      if (valid) {
+        const uint32_t bit = 1u << (id & 31);
+        const uint32_t old = atomicOr(&bm[id >> 5], bit);
+        uniq = (old & bit) == 0u;
       }
+      const uint64_t m = ballot(uniq);
+      if (m != 0ull) {
+        int base = 0;
+        if (lane == 0) base = atomicAdd(&misc->xl_n, __popcll(m));
+        base = __shfl(base, 0);
+        if (uniq) xl_id[base + lanes_below(m)] = id;
+      }
+    };
+#pragma unroll
+    for (int s = 0; s < HPT; ++s)
+      if (s * NT < H) mark(hid[s], s * NT + tid < H);
+    const int32_t* hp = P.hist_ids + h0;
+    for (int32_t b = HPT * NT; b < H; b += NT) {
+      const bool act = b + tid < H;
+      mark(act ? hp[b + tid] : -1, act);
     }
   }
   __syncthreads();
@@ -1119,7 +1137,8 @@ __global__ __launch_bounds__(NT) void sample_kernel(const KParams P) {
   if (P.fast) {
     // greedy and small-k rows that fit in registers: one streaming pass
     if (seg_row(temp, k, P.vocab) && row_fits<T>(P.vocab)) {
-      if (src >= 0 && src < P.n_rows_total && h0 >= 0 && h1 >= h0 && h1 - h0 <= MAX_HIST && h1 - h0 <= P.xcap - 8) {
+      if (src >= 0 && src < P.n_rows_total && h0 >= 0 && h1 >= h0 && h1 - h0 <= MAX_HIST &&
+          (pen == 1.0f || (h1 - h0 < P.vocab ? h1 - h0 : P.vocab) <= P.xcap - 8)) {
         extern __shared__ __align__(16) unsigned char smem[];
         Misc* misc = reinterpret_cast<Misc*>(smem);
         uint32_t* bm = reinterpret_cast<uint32_t*>(smem + P.off_bm);
@@ -1406,14 +1425,41 @@ DevInfo g_dev[kMaxDevices];
 
 int device_info(int dev, DevInfo& out);
 
+// LDS layout of the one-workgroup-per-row kernels: Misc, the row's history bitmap, the
+// extras (unique history ids up to LDS_HIST, then the tail), the candidates, the histogram.
+struct LdsLayout {
+  uint32_t off_bm, off_xl, off_cand, off_hist, total;
+  int32_t xcap;
+};
+LdsLayout lds_layout(int64_t vocab, int32_t max_hist) {
+  const int64_t nbw = (vocab + 31) / 32;
+  int64_t uniq = max_hist < vocab ? max_hist : vocab;
+  if (uniq > ns::LDS_HIST) uniq = ns::LDS_HIST;
+  const int64_t xcap = ((uniq + 8 + 3) / 4) * 4;
+  LdsLayout l;
+  int64_t off = ((int64_t)sizeof(ns::Misc) + 15) / 16 * 16;
+  l.off_bm = (uint32_t)off;
+  off += (nbw * 4 + 15) / 16 * 16;
+  l.off_xl = (uint32_t)off;
+  l.xcap = (int32_t)xcap;
+  off += (xcap * 8 + 15) / 16 * 16;
+  l.off_cand = (uint32_t)off;
+  off += (int64_t)ns::CAP * 8;
+  l.off_hist = (uint32_t)off;
+  off += (int64_t)ns::NB * 12;
+  l.total = (uint32_t)off;
+  return l;
+}
+
 struct WsLayout {
-  int64_t counters, status, stats, cand, wrow, shist, slist, smeta, total;
+  int64_t counters, status, stats, cand, wrow, shist, slist, smeta, xlong, total;
+  int32_t xg_cap;   // extras per row in the xlong region (0: none)
 };
 // Workspace layout.  The per-row arrival counters are the only state that outlives a
 // call (each call leaves them at zero): they sit at fixed positions at the start, sized
 // for NS_SEG_MAX_ROWS rows, so calls of any shape sharing one workspace always find
 // zeroed counters.  Everything behind them is rewritten by every call before it is read.
-WsLayout ws_layout(int32_t n_sample, int64_t vocab, int32_t dtype) {
+WsLayout ws_layout(int32_t n_sample, int64_t vocab, int32_t dtype, int32_t max_hist) {
   const int64_t n = n_sample < NS_SEG_MAX_ROWS ? n_sample : NS_SEG_MAX_ROWS;
   const int64_t rows = (n + 7) / 8 * 8;
   const int64_t S = seg_count(vocab, dtype);
@@ -1431,7 +1477,12 @@ WsLayout ws_layout(int32_t n_sample, int64_t vocab, int32_t dtype) {
   const int64_t srows = rows < ns::SP_MAX_ROWS ? rows : ns::SP_MAX_ROWS;
   L.slist = L.shist + align256(wrows * S * ns::WBINS * 8);
   L.smeta = L.slist + align256(srows * ns::SP_MAXS * ns::SP_LIST * 8);
-  L.total = L.smeta + align256(srows * ns::SP_MAXS * (int64_t)sizeof(ns::SplitMeta));
+  L.xlong = L.smeta + align256(srows * ns::SP_MAXS * (int64_t)sizeof(ns::SplitMeta));
+  // histories longer than the general code's LDS list: each row's unique ids and their
+  // penalized values (and the tail) in a region of its own, for every row of the call
+  const int64_t uniq = max_hist < vocab ? max_hist : vocab;
+  L.xg_cap = max_hist > ns::LDS_HIST ? (int32_t)(((uniq + 8 + 3) / 4) * 4) : 0;
+  L.total = L.xlong + align256((int64_t)n_sample * L.xg_cap * 8);
   return L;
 }
 int device_info(int dev, DevInfo& out) {
@@ -1678,7 +1729,9 @@ int ns_sample_noalloc(const ns_sample_args* a, hipStream_t stream) {
   if (a->vocab <= 0 || a->vocab > NS_MAX_VOCAB)
     return fail(NS_ERR_INVALID, "vocab must be in [1, " + std::to_string(NS_MAX_VOCAB) + "]");
   if (a->dtype != NS_DTYPE_F32 && a->dtype != NS_DTYPE_BF16) return fail(NS_ERR_INVALID, "dtype must be f32 or bf16");
-  const int64_t need = ws_layout(a->n_sample, a->vocab, a->dtype).total;
+  if (a->max_hist < 0 || a->max_hist > NS_MAX_HISTORY) return fail(NS_ERR_INVALID, "max_hist out of range");
+  const bool hist = a->hist_offsets != nullptr || a->hist_state != nullptr;
+  const int64_t need = ws_layout(a->n_sample, a->vocab, a->dtype, hist ? a->max_hist : 0).total;
   if (need > (int64_t)NS_NOALLOC_SCRATCH_BYTES)
     return fail(NS_ERR_INVALID, "this call needs " + std::to_string(need) + " bytes of workspace, above the " +
                                     std::to_string((int64_t)NS_NOALLOC_SCRATCH_BYTES) +
@@ -1714,24 +1767,17 @@ int ns_sample_lds_bytes(int64_t vocab, int32_t max_hist, int32_t* lds_bytes) {
   if (lds_bytes == nullptr) return fail(NS_ERR_INVALID, "lds_bytes is NULL");
   if (vocab <= 0 || vocab > NS_MAX_VOCAB) return fail(NS_ERR_INVALID, "vocab out of range");
   if (max_hist < 0 || max_hist > NS_MAX_HISTORY) return fail(NS_ERR_INVALID, "max_hist out of range");
-  const int64_t nbw = (vocab + 31) / 32;
-  const int64_t uniq = max_hist < vocab ? max_hist : vocab;
-  const int64_t xcap = ((uniq + 8 + 3) / 4) * 4;
-  int64_t off = ((int64_t)sizeof(ns::Misc) + 15) / 16 * 16;
-  off += (nbw * 4 + 15) / 16 * 16;
-  off += (xcap * 8 + 15) / 16 * 16;
-  off += (int64_t)ns::CAP * 8;
-  off += (int64_t)ns::NB * 12;
-  *lds_bytes = (int32_t)off;
+  *lds_bytes = (int32_t)lds_layout(vocab, max_hist).total;
   return NS_OK;
 }
 
-int ns_sample_workspace_bytes(int32_t n_sample, int64_t vocab, int32_t dtype, uint64_t* bytes) {
+int ns_sample_workspace_bytes(int32_t n_sample, int64_t vocab, int32_t dtype, int32_t max_hist, uint64_t* bytes) {
   if (bytes == nullptr) return fail(NS_ERR_INVALID, "bytes is NULL");
   if (n_sample < 0) return fail(NS_ERR_INVALID, "n_sample < 0");
   if (vocab <= 0 || vocab > NS_MAX_VOCAB) return fail(NS_ERR_INVALID, "vocab out of range");
   if (dtype != NS_DTYPE_F32 && dtype != NS_DTYPE_BF16) return fail(NS_ERR_INVALID, "dtype must be f32 or bf16");
-  *bytes = (uint64_t)ws_layout(n_sample, vocab, dtype).total;
+  if (max_hist < 0 || max_hist > NS_MAX_HISTORY) return fail(NS_ERR_INVALID, "max_hist out of range");
+  *bytes = (uint64_t)ws_layout(n_sample, vocab, dtype, max_hist).total;
   return NS_OK;
 }
 
@@ -1743,25 +1789,26 @@ int ns_sample(const ns_sample_args* a, hipStream_t stream) {
   bool has_hist = false;
   int rc = sample_params(a, p, has_hist);
   if (rc != NS_OK) return rc;
-  const WsLayout L = ws_layout(a->n_sample, a->vocab, a->dtype);
-
-  int32_t lds = 0;
-  rc = ns_sample_lds_bytes(a->vocab, has_hist ? a->max_hist : 0, &lds);
-  if (rc != NS_OK) return rc;
-  {
-    const int64_t mh = has_hist ? a->max_hist : 0;
-    const int64_t nbw = (a->vocab + 31) / 32;
-    const int64_t uniq = mh < a->vocab ? mh : a->vocab;
-    const int64_t xcap = ((uniq + 8 + 3) / 4) * 4;
-    uint32_t off = (uint32_t)(((int64_t)sizeof(ns::Misc) + 15) / 16 * 16);
-    p.off_bm = off;
-    off += (uint32_t)((nbw * 4 + 15) / 16 * 16);
-    p.off_xl = off;
-    p.xcap = (int32_t)xcap;
-    off += (uint32_t)((xcap * 8 + 15) / 16 * 16);
-    p.off_cand = off;
-    off += (uint32_t)ns::CAP * 8u;
-    p.off_hist = off;
+  const int32_t mh = has_hist ? a->max_hist : 0;
+  const WsLayout L = ws_layout(a->n_sample, a->vocab, a->dtype, mh);
+  const LdsLayout ll = lds_layout(a->vocab, mh);
+  const int32_t lds = (int32_t)ll.total;
+  p.off_bm = ll.off_bm;
+  p.off_xl = ll.off_xl;
+  p.xcap = ll.xcap;
+  p.off_cand = ll.off_cand;
+  p.off_hist = ll.off_hist;
+  // rows with more distinct history ids than LDS holds keep them in the workspace
+  if (L.xg_cap > 0 && a->workspace == nullptr)
+    return fail(NS_ERR_INVALID, "max_hist " + std::to_string(mh) + " above " + std::to_string(NS_LDS_HISTORY) +
+                                    " needs a workspace (ns_sample_workspace_bytes with max_hist)");
+  if (L.xg_cap > 0) {
+    if (a->workspace_bytes < (uint64_t)L.total)
+      return fail(NS_ERR_INVALID, "workspace of " + std::to_string(a->workspace_bytes) + " bytes, " +
+                                      std::to_string(L.total) + " needed (ns_sample_workspace_bytes)");
+    if (((uintptr_t)a->workspace % 256) != 0) return fail(NS_ERR_ALIGN, "workspace must be 256-byte aligned");
+    p.xl_glob = reinterpret_cast<float*>(static_cast<unsigned char*>(a->workspace) + L.xlong);
+    p.xg_cap = L.xg_cap;
   }
   int dev = 0;
   hipError_t e = hipGetDevice(&dev);

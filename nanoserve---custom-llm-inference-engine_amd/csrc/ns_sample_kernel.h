@@ -36,9 +36,10 @@ constexpr int RT = NT - 64;      // row threads (waves 0..14)
 constexpr int CAP = 4096;        // LDS candidate capacity
 constexpr int NB = 2048;         // histogram bins
 constexpr int KSMALL = 1024;     // largest k handled by the chunk-maxima threshold
-constexpr int HPT = 8;           // history ids per thread (max history 8192)
+constexpr int HPT = 8;           // history ids per thread held in registers (one batch of 8192)
 constexpr int GATHER = 2;        // history-value gathers in flight per history-wave lane
-constexpr int MAX_HIST = HPT * NT;
+constexpr int LDS_HIST = HPT * NT;   // longest history whose unique ids the general code keeps in LDS
+constexpr int MAX_HIST = 1 << 20;    // per-row history limit (longer ids stream in batches)
 constexpr int NGROUP = 8;        // streaming mode: chunk-maxima groups per thread
 constexpr int MAX_LEVELS = 4;    // histogram refinement rounds
 constexpr int INFO_WORDS = 8;
@@ -74,7 +75,9 @@ struct KParams {
   const int32_t* status;   // [n_sample] from the segment kernel (0 = resolved there), or NULL: every row
   int32_t n_sample;
   int32_t fast;            // 1: greedy and small-k rows that fit in registers take the streaming path
-  int32_t xcap;            // extras capacity (unique history + tail)
+  int32_t xcap;            // extras capacity in LDS (unique history + tail)
+  float* xl_glob;          // per-row extras in the workspace for longer histories (2 * xg_cap words a row), or NULL
+  int32_t xg_cap;          // their capacity (unique history + tail)
   uint32_t off_bm, off_xl, off_cand, off_hist;   // LDS byte offsets
 };
 

@@ -928,6 +928,8 @@ __device__ __forceinline__ void segment_body(const SegParams& P, SegSmem& sm) {
 
   if (greedy) {
     __syncthreads();
+    // the waves' flags, read before the reductions below reuse their words
+    const int32_t wfl = sm.ired[0] | sm.ired[1] | sm.ired[2] | sm.ired[3];
     // masked maximum and its first index (NaN counts as the max, sampler.py:82-83):
     // the masked chunk maxima, then an element scan (re-read from L2) of the first
     // chunk of each thread that reaches the segment maximum.
@@ -963,7 +965,7 @@ __device__ __forceinline__ void segment_body(const SegParams& P, SegSmem& sm) {
     const int32_t best = seg_min_i(gi, &sm);
     st.ymax = Mx;
     st.amax = best;
-    st.flags = flags | sm.ired[0] | sm.ired[1] | sm.ired[2] | sm.ired[3];
+    st.flags = flags | wfl;
   } else {
     // ---- lower bound of the k-th largest: ceil(k/4)-th largest thread value per wave, min over waves
     const int kw = (k + SNW - 1) / SNW;
@@ -1048,9 +1050,13 @@ __device__ __forceinline__ void segment_body(const SegParams& P, SegSmem& sm) {
       const bool hit = act && (nanm ? (ym != ym) : (ym == M));
       const int32_t am = wave_min(hit ? s.amax : 0x7fffffff);
       if (lane == 0) {
-        P.out_ids[row] = am == 0x7fffffff ? 0 : am;
-        P.status[row] = 0;
-        seg_write_info(P.out_info, row, PATH_GREEDY, 1, -__builtin_inff(), 0, 0, fl & 0xffff, M, am);
+        if (fl & SFLAG_XOVER) {
+          P.status[row] = 1;   // a segment's distinct history ids outgrew its list: per-row kernel
+        } else {
+          P.out_ids[row] = am == 0x7fffffff ? 0 : am;
+          P.status[row] = 0;
+          seg_write_info(P.out_info, row, PATH_GREEDY, 1, -__builtin_inff(), 0, 0, fl & 0xffff, M, am);
+        }
       }
     } else {
       const float tau = wave_max(act ? s.tau : -__builtin_inff());

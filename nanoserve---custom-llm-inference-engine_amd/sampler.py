@@ -172,11 +172,11 @@ class DeviceHistories:
     reads each row's history from its request's slot and appends the sampled
     token to it on the device (the lists engine.py:242-246 rebuilds every step and
     sampler.py:34 copies to the device).  ``close(request_id)`` frees the slot.
-    ``capacity`` bounds prompt + generated tokens per request (at most the
-    sampler's 8192-token history limit, the reference's max_model_len).
+    ``capacity`` bounds prompt + generated tokens per request: by default 8192,
+    the reference's max_model_len; at most the sampler's per-row limit of 2^20.
     """
 
-    def __init__(self, device, max_requests: int, capacity: int = _lib.NS_MAX_HISTORY):
+    def __init__(self, device, max_requests: int, capacity: int = _lib.NS_LDS_HISTORY):
         self.device = torch.device(device)
         self.state = _lib.HistoryState(self.device, max_requests, capacity)
         self.capacity = int(capacity)

@@ -52,7 +52,17 @@ def test_lds_bytes_and_argument_errors():
     with pytest.raises(L.SamplerLibraryError, match="vocab"):
         L.lds_bytes(0, 0)
     with pytest.raises(L.SamplerLibraryError, match="max_hist"):
-        L.lds_bytes(1000, 9000)
+        L.lds_bytes(1000, L.NS_MAX_HISTORY + 1)
+    # histories past NS_LDS_HISTORY take no more LDS; their distinct ids (and the tail) go to
+    # a workspace region of min(max_hist, vocab) + 8 entries of 8 bytes per row
+    assert L.lds_bytes(128256, L.NS_MAX_HISTORY) == L.lds_bytes(128256, L.NS_LDS_HISTORY)
+    for dt in (L.NS_DTYPE_F32, L.NS_DTYPE_BF16):
+        base = L.workspace_bytes(256, 128256, dt)
+        assert L.workspace_bytes(256, 128256, dt, L.NS_LDS_HISTORY) == base
+        assert L.workspace_bytes(256, 128256, dt, 16384) == base + 256 * (16384 + 8) * 8
+        assert L.workspace_bytes(3, 1000, dt, L.NS_MAX_HISTORY) == L.workspace_bytes(3, 1000, dt) + 24320   # align256(3 * 1008 * 8)
+    with pytest.raises(L.SamplerLibraryError, match="max_hist"):
+        L.workspace_bytes(8, 1000, L.NS_DTYPE_F32, L.NS_MAX_HISTORY + 1)
     lib = L.load()
     a = L.NsSampleArgs()
     a.n_sample = 1
@@ -68,8 +78,11 @@ def test_history_state_layout_and_argument_errors():
     # int32 lengths padded to 256 bytes, then n_slots * capacity int32 ids
     assert L.hist_state_bytes(3, 100) == 256 + 3 * 100 * 4
     assert L.hist_state_bytes(64, 8192) == 256 + 64 * 8192 * 4
+    assert L.hist_state_bytes(4, 16384) == 256 + 4 * 16384 * 4
     with pytest.raises(L.SamplerLibraryError, match="hist_capacity"):
-        L.hist_state_bytes(4, 9000)
+        L.hist_state_bytes(4, L.NS_MAX_HISTORY + 1)
+    with pytest.raises(L.SamplerLibraryError, match="2\\^31"):
+        L.hist_state_bytes(4096, L.NS_MAX_HISTORY)
     with pytest.raises(L.SamplerLibraryError, match="hist_n_slots"):
         L.hist_state_bytes(0, 10)
     lib = L.load()

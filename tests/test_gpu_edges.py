@@ -45,8 +45,8 @@ def check(w, device, path, logits=None):
 
 @pytest.mark.parametrize("path", list(PATHS))
 def test_largest_vocab_and_history(device, path):
-    """V = NS_MAX_VOCAB (fp32) with NS_MAX_HISTORY ids per row (duplicates included)."""
-    w = workload("max-vocab-history", 6, L.NS_MAX_VOCAB, seed=91, hist_len=L.NS_MAX_HISTORY)
+    """V = NS_MAX_VOCAB (fp32) with NS_LDS_HISTORY ids per row (duplicates included)."""
+    w = workload("max-vocab-history", 6, L.NS_MAX_VOCAB, seed=91, hist_len=L.NS_LDS_HISTORY)
     check(w, device, path)
 
 

@@ -26,7 +26,7 @@ pytestmark = pytest.mark.gpu
 
 
 def open_all(w, device, extra_slots=3):
-    dh = S.DeviceHistories(device, w.batch + extra_slots, capacity=L.NS_MAX_HISTORY)
+    dh = S.DeviceHistories(device, w.batch + extra_slots, capacity=L.NS_LDS_HISTORY)
     for r in range(w.batch):
         dh.open(r, w.histories[r])
     return dh
