@@ -302,7 +302,7 @@ def read_floor(L, sets, stream, iters=200):
     lib.ns_probe_read_rows.restype = ctypes.c_int
     lib.ns_probe_read_rows.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_int64, ctypes.c_int32,
                                        ctypes.c_void_p, ctypes.c_void_p]
-    out = torch.empty(lg.shape[0], dtype=torch.int32, device=lg.device)
+    out = torch.empty(lg.shape[0] * 16, dtype=torch.int32, device=lg.device)   # one word per wave
     sh = ctypes.c_void_p(int(stream.cuda_stream))
 
     def call(i):
