@@ -34,6 +34,10 @@ def _compile(src: str, out: str, verbose: bool) -> None:
         hipcc(), f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC", "-shared",
         "-ffp-contract=off", "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
         "-Wno-unused-command-line-argument",
+        # every atomic on a uniform address is aggregated in the source already (one lane per
+        # wave); the compiler's own aggregation only wraps those single-lane atomics in
+        # another exec-mask count (measured: the wide path 5-7% faster without it)
+        "-mllvm", "-amdgpu-atomic-optimizer-strategy=None",
         "-I", os.path.join(ROOT, "include"), "-I", os.path.join(HERE, "csrc"),
         src, "-o", tmp,
     ]

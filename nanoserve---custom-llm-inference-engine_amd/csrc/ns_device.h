@@ -119,6 +119,20 @@ template <typename T> __device__ __forceinline__ T read_lane(T v, int src) {
     return __builtin_bit_cast(T, (hi << 32) | lo);
   }
 }
+// DPP broadcast CTRL (0x142: lane 15 of each row to the next row; 0x143: lane 31 to rows 2 and
+// 3) into the rows of RMASK; the other rows receive 0.
+template <int CTRL, int RMASK, typename T> __device__ __forceinline__ T row_bcast_zero(T v) {
+  static_assert(sizeof(T) == 4 || sizeof(T) == 8, "row_bcast_zero: 32- or 64-bit values");
+  if constexpr (sizeof(T) == 4) {
+    const uint32_t u = __builtin_bit_cast(uint32_t, v);
+    return __builtin_bit_cast(T, (uint32_t)__builtin_amdgcn_update_dpp(0u, u, CTRL, RMASK, 0xF, false));
+  } else {
+    const uint64_t u = __builtin_bit_cast(uint64_t, v);
+    const uint64_t lo = (uint32_t)__builtin_amdgcn_update_dpp(0u, (uint32_t)u, CTRL, RMASK, 0xF, false);
+    const uint64_t hi = (uint32_t)__builtin_amdgcn_update_dpp(0u, (uint32_t)(u >> 32), CTRL, RMASK, 0xF, false);
+    return __builtin_bit_cast(T, (hi << 32) | lo);
+  }
+}
 // Lane l receives lane l - s of its 16-lane row, or 0 where l - s leaves the row.
 template <typename T> __device__ __forceinline__ T row_shr_zero(T v, int s) {
   static_assert(sizeof(T) == 4 || sizeof(T) == 8, "row_shr_zero: 32- or 64-bit values");
@@ -167,16 +181,15 @@ template <typename T> __device__ __forceinline__ T wave_min(T v) {
 // Inclusive prefix sum over the 64 lanes: Hillis-Steele inside each 16-lane
 // row (DPP row_shr), then the three lower row totals added by readlane.
 template <typename T> __device__ __forceinline__ T wave_incl_scan(T v) {
-  const int l = lane_id();
-#pragma unroll
-  for (int o = 1; o < 16; o <<= 1) {
-    const T w = row_shr_zero(v, o);
-    if ((l & 15) >= o) v += w;
-  }
-  const T t0 = read_lane(v, 15), t1 = read_lane(v, 31), t2 = read_lane(v, 47);
-  if (l >= 16) v += t0;
-  if (l >= 32) v += t1;
-  if (l >= 48) v += t2;
+  // inside each row: lanes past the row's start read 0, so every lane adds unconditionally
+  v += row_shr_zero(v, 1);
+  v += row_shr_zero(v, 2);
+  v += row_shr_zero(v, 4);
+  v += row_shr_zero(v, 8);
+  // across rows: row 1 and row 3 add the last lane of the row before them, then rows 2 and 3
+  // add lane 31 (rows 0 and 1 together)
+  v += row_bcast_zero<0x142, 0xA>(v);
+  v += row_bcast_zero<0x143, 0xC>(v);
   return v;
 }
 __device__ __forceinline__ uint64_t ballot(bool p) { return __ballot(p); }

@@ -568,6 +568,8 @@ __device__ __forceinline__ void wave_draw_sorted(uint64_t a, int nk, int n, cons
   const int r0 = lane < n ? vr[lane] : 64;
   const int r1 = 64 + lane < n ? vr[64 + lane] : 64;
   const float ev = lane < nk ? ns_expf(desc_key_val(a) - M) : 0.0f;
+  // the numerators in id order, ahead of the cut they do not depend on
+  const float e0 = ns_expf(desc_key_val(b0) - M), e1 = ns_expf(desc_key_val(b1) - M);
   const double cs = wave_incl_scan((double)ev);
   int nf = nk;
   float vstar = -__builtin_inff();
@@ -587,8 +589,8 @@ __device__ __forceinline__ void wave_draw_sorted(uint64_t a, int nk, int n, cons
   const double rz2 = rcp_f64(read_lane(cs, nf - 1));
   // final probabilities of the kept candidates (sorted position < nf), in id order
   const bool k0 = r0 < nf, k1 = r1 < nf;
-  const float p0 = k0 ? (float)((double)ns_expf(desc_key_val(b0) - M) * rz2) : 0.0f;
-  const float p1 = k1 ? (float)((double)ns_expf(desc_key_val(b1) - M) * rz2) : 0.0f;
+  const float p0 = k0 ? (float)((double)e0 * rz2) : 0.0f;
+  const float p1 = k1 ? (float)((double)e1 * rz2) : 0.0f;
   const double c0 = wave_incl_scan((double)p0);
   const double c1 = read_lane(c0, 63) + wave_incl_scan((double)p1);
   // the first id-order position whose cumulative mass exceeds u (sampler.py:87 as an

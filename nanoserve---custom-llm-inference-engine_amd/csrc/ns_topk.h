@@ -270,7 +270,7 @@ __device__ __forceinline__ int topk_stream(const RowArgs P, const int row, const
 #pragma unroll
   for (int w = 0; w < NWAVE; ++w) spec |= is[w];
   flags |= misc->flags;
-  if (spec != 0) {
+  if (__builtin_expect(spec != 0, 0)) {
     // NaN / +inf among the logits (the penalty keeps both): the softmax is NaN, uniform
     // 1/V (sampler.py:77-80).  Rare: the row is read again to tell NaN from +inf.
     bool nanf = false;
@@ -286,7 +286,7 @@ __device__ __forceinline__ int topk_stream(const RowArgs P, const int row, const
   }
   float tc = misc->fb[0];
   // fewer than k finite group maxima (a row of mostly -inf): the general code takes it
-  if (!(tc > -__builtin_inff())) { __syncthreads(); return 1; }
+  if (__builtin_expect(!(tc > -__builtin_inff()), 0)) { __syncthreads(); return 1; }
   // Chunks whose maximum reaches tc go to the wave's own LDS slots, then the wave expands
   // them into candidates, one element per lane, straight as sort keys (scaled value
   // descending, token id ascending): elements penalized at history positions
@@ -347,7 +347,7 @@ __device__ __forceinline__ int topk_stream(const RowArgs P, const int row, const
         nh += __popcll(m);
       }
     }
-    if (nh > HIT_PER_WAVE) {
+    if (__builtin_expect(nh > HIT_PER_WAVE, 0)) {
       // more hit chunks than slots: the count goes past WAVE_CAP and the general code
       // takes the row
       if (lane == 0) atomicAdd(&misc->cand_n, WAVE_CAP + 1);
@@ -372,7 +372,7 @@ __device__ __forceinline__ int topk_stream(const RowArgs P, const int row, const
   collect(std::false_type{});
   __syncthreads();   // the list complete
   int n = misc->cand_n;
-  if (n < k && pen_on) {
+  if (__builtin_expect(n < k && pen_on, 0)) {
     // The penalty took the list under k keys (history tokens among the largest values): the
     // bound again, from the maxima of penalized values (the bitmap is complete), and the list
     // again, every staged chunk read from memory.  At least k penalized values reach the new
@@ -449,7 +449,7 @@ __device__ __forceinline__ int topk_stream(const RowArgs P, const int row, const
     __syncthreads();
     n = misc->cand_n;
   }
-  if (n > WAVE_CAP || n < k) { __syncthreads(); return 1; }
+  if (__builtin_expect(n > WAVE_CAP || n < k, 0)) { __syncthreads(); return 1; }
   zero_probs(o);
   block_finalize_keys<NT>(cand, cand + WAVE_CAP, n, k, topp < 1.0f, topp, u, row, P.out_ids, P.out_probs, V,
                           P.out_info, flags, n, PATH_WAVE_SET);
