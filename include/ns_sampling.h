@@ -26,7 +26,7 @@
 extern "C" {
 #endif
 
-#define NS_ABI_VERSION 8
+#define NS_ABI_VERSION 9
 
 #define NS_OK 0
 #define NS_ERR_INVALID 1   /* bad argument (message says which) */
@@ -104,7 +104,7 @@ typedef struct ns_sample_args {
   int32_t        mode;          /* NS_MODE_*: which kernels resolve which rows (results are identical) */
   uint32_t       row_kinds;     /* NS_KIND_* bits of the kinds of rows present, or 0 when unknown: a call
                                    declared without NS_KIND_OTHER rows skips the launches for them */
-  const void*    hist_state;    /* device-resident histories (ns_hist_state_bytes), or NULL.  With it the
+  void*          hist_state;    /* device-resident histories (ns_hist_state_bytes), or NULL.  With it the
                                    histories are read from the state instead of hist_offsets / hist_ids
                                    (both must be NULL): row r's history is the id list of request slot
                                    hist_slot[r], kept on the device across calls (the lists the engine
@@ -112,6 +112,14 @@ typedef struct ns_sample_args {
   const int32_t* hist_slot;     /* [B] request slot of each row, -1 for a row without history */
   int32_t        hist_n_slots;  /* slots in hist_state */
   int32_t        hist_capacity; /* token ids per slot */
+  int32_t        hist_append;   /* nonzero (needs hist_state): the kernel that writes row r's id also
+                                   appends it to slot hist_slot[r], as ns_hist_append would after the
+                                   call (scheduler.py:281-284), so the next call sees it without a
+                                   further launch.  The rows of such a call name distinct slots; rows
+                                   with a negative slot or a failed id (-1) append nothing; a full slot
+                                   is left unchanged and counted in *hist_overflow.  0: the state is
+                                   only read. */
+  int32_t*       hist_overflow; /* device int32 counting the full slots of hist_append, or NULL */
 } ns_sample_args;
 
 /* Version of this ABI (NS_ABI_VERSION). */

@@ -26,7 +26,7 @@ NS_KIND_GREEDY = 1      # row_kinds: greedy rows (temperature 0)
 NS_KIND_SMALL_K = 2     # sampled rows with 1 <= top_k <= 64 and top_k < vocab
 NS_KIND_OTHER = 4       # every other sampled row (top-k off or larger)
 NS_DEBUG_STREAM, NS_DEBUG_WIDE, NS_DEBUG_GENERAL = 0, 1, 2   # ns_debug_scaled routines
-ABI_VERSION = 8
+ABI_VERSION = 9
 
 # exported symbols, as declared in include/ns_sampling.h
 NS_NOALLOC_SCRATCH_BYTES = 80 << 20   # ns_sample_noalloc's device scratch per GPU
@@ -66,6 +66,8 @@ class NsSampleArgs(ctypes.Structure):
         ("hist_slot", ctypes.c_void_p),
         ("hist_n_slots", ctypes.c_int32),
         ("hist_capacity", ctypes.c_int32),
+        ("hist_append", ctypes.c_int32),
+        ("hist_overflow", ctypes.c_void_p),
     ]
 
 
@@ -236,7 +238,8 @@ def aligned_rows(logits, sample_idx):
 def sample_raw(logits, temperature, top_k, top_p, rep_penalty, uniforms, out_ids, *, sample_idx=None,
                hist_offsets=None, hist_ids=None, max_hist: int = 0, out_probs=None, out_info=None,
                stream=None, workspace="auto", mode: int = NS_MODE_AUTO, row_kinds: int = 0,
-               hist_state=None, hist_slot=None, debug_scaled=None) -> None:
+               hist_state=None, hist_slot=None, hist_append: bool = False, hist_overflow=None,
+               debug_scaled=None) -> None:
     """Launch ``ns_sample`` on device tensors (no copies, no synchronisation).
 
     logits: (N, V) float32 or bfloat16 CUDA tensor with unit stride in the last dim.
@@ -247,7 +250,9 @@ def sample_raw(logits, temperature, top_k, top_p, rep_penalty, uniforms, out_ids
     takes the one-workgroup-per-row kernel).  row_kinds: NS_KIND_* bits of the rows present
     (see ``row_kinds``), 0 when unknown.  hist_state / hist_slot: device-resident histories
     (a ``HistoryState`` and the (B,) int32 slot of each row, -1 for none) instead of
-    hist_offsets / hist_ids.
+    hist_offsets / hist_ids.  hist_append: the kernels also append each row's sampled id to
+    its slot (HistoryState.append fused into the call; the rows name distinct slots);
+    hist_overflow: a (1,) int32 tensor counting full slots, or None.
     debug_scaled: a pair (formula, out) with out a (B, >= V) float32 tensor of unit stride
     along V: instead of sampling, ``ns_debug_scaled`` writes each row's penalized,
     temperature-scaled logits there, computed by routine ``formula`` (NS_DEBUG_*).
@@ -299,6 +304,11 @@ def sample_raw(logits, temperature, top_k, top_p, rep_penalty, uniforms, out_ids
         a.hist_slot = _ptr(hist_slot)
         a.hist_n_slots = int(hist_state.n_slots)
         a.hist_capacity = int(hist_state.capacity)
+    if hist_append:
+        if hist_state is None:
+            raise ValueError("hist_append needs hist_state")
+        a.hist_append = 1
+        a.hist_overflow = _ptr(hist_overflow)
     if stream is None:
         stream = torch.cuda.current_stream(logits.device)
     if debug_scaled is not None:

@@ -81,6 +81,38 @@ template <typename T> __device__ __forceinline__ T lane_xor(T v, int s) {
 // (off[row], off[row + 1]), a device-resident request slot s = slot[row] (ids
 // s * cap .. s * cap + len[s]), or none (0, 0).  A slot outside [-1, nslots) or a length
 // outside [0, cap] gives (0, -1), which every kernel treats as an invalid history.
+// Where a row's sampled token goes: out_ids[row], and with device-resident histories that
+// append in place, the end of the row's request slot (the next step's history,
+// engine.py:242-246 with scheduler.py:281-284 appending each sampled id).  One thread per row
+// calls put_id, once, where the row's token is final; a failed row (id -1) appends nothing,
+// a full slot is counted in *overflow and not written.  Slot lengths are read by the row's
+// own workgroups before that point and by no other row (the rows of a call name distinct
+// slots).
+struct IdSink {
+  int64_t* out;
+  const int32_t* slot;   // hist_slot, or NULL: no append
+  int32_t* lens;
+  int32_t* ids;
+  int32_t* overflow;     // or NULL
+  int32_t cap, nslots;
+};
+__device__ __forceinline__ void append_id(const IdSink& s, int row, int64_t id) {
+  if (s.slot == nullptr || id < 0) return;
+  const int32_t sl = s.slot[row];
+  if (sl < 0 || sl >= s.nslots) return;
+  const int32_t l = s.lens[sl];
+  if (l >= 0 && l < s.cap) {
+    s.ids[(int64_t)sl * s.cap + l] = (int32_t)id;
+    s.lens[sl] = l + 1;
+  } else if (s.overflow != nullptr) {
+    atomicAdd(s.overflow, 1);
+  }
+}
+__device__ __forceinline__ void put_id(const IdSink& s, int row, int64_t id) {
+  s.out[row] = id;
+  append_id(s, row, id);
+}
+
 __device__ __forceinline__ void row_history(const int32_t* off, const int32_t* slot, const int32_t* len,
                                             int32_t nslots, int32_t cap, int row, int32_t& h0, int32_t& h1) {
   h0 = 0;

@@ -159,7 +159,7 @@ struct RowArgs {
   int64_t row_stride;
   int64_t vocab;
   const int32_t* hist_ids;
-  int64_t* out_ids;
+  IdSink out_ids;
   float* out_probs;
   int32_t* out_info;
 };
@@ -202,7 +202,7 @@ __device__ __forceinline__ int row_fast(const RowArgs P, const int row, const in
       while (i > 0 && (double)i * qd > ud) --i;
       while ((double)(i + 1) * qd <= ud && i < V) ++i;
       if (i >= V) i = V - 1;
-      P.out_ids[row] = i;
+      put_id(P.out_ids, row, i);
     }
     write_info(o, PATH_UNIFORM, (int32_t)V, -__builtin_inff(), (int32_t)V, 0, flags, Mrep, -1);
     if (P.out_probs != nullptr) {
@@ -303,7 +303,7 @@ __device__ __forceinline__ int row_fast(const RowArgs P, const int row, const in
       if ((nanm ? (x != x) : (x == Mx)) && (int64_t)xl_id[i] < gi) gi = xl_id[i];
     }
     const int64_t best = block_min_i64(gi, red);
-    if (tid == 0) P.out_ids[row] = best == INT64_MAX ? 0 : best;
+    if (tid == 0) put_id(P.out_ids, row, best == INT64_MAX ? 0 : best);
     write_info(o, PATH_GREEDY, 1, -__builtin_inff(), 0, 0, flags, Mx, (int32_t)best);
     // nothing of this path is left in flight where the top-k path starts (the compiler
     // merges their exits and would otherwise wait for the row there)

@@ -163,7 +163,7 @@ __device__ __forceinline__ float select_tau(const float (&v)[NV], bool active, i
 }
 
 struct RowOut {
-  int64_t* out_ids;
+  IdSink out_ids;
   float* out_probs;
   int32_t* out_info;
   int row;
@@ -329,7 +329,7 @@ __device__ __attribute__((always_inline)) inline void lds_set(int n, bool need_t
   int pick = misc->ib[3];
   if (pick < 0) pick = lastpos >= 0 ? (int)lastpos : 0;
   const int64_t token = (int64_t)(cand[pick] >> 32);
-  if (tid == 0) o.out_ids[o.row] = token;
+  if (tid == 0) put_id(o.out_ids, o.row, token);
   write_info(o, path, nf, thr, n_topk, n, flags, vstar, istar);
   if (o.out_probs != nullptr) {
     zero_probs(o);
@@ -348,7 +348,7 @@ struct GCtx {
   uint32_t* hcnt;
   uint64_t* hmass;
   Misc* misc;
-  int64_t* out_ids;
+  IdSink out_ids;
   float* out_probs;
   int32_t* out_info;
   int64_t V, nch, nrows_j;
@@ -384,7 +384,7 @@ __device__ __attribute__((always_inline)) inline void generic_path(const GCtx g)
   const float pen = g.pen, tdiv = g.tdiv, rdiv = g.rdiv, p32 = g.p32, Mx = g.Mx, My = g.My, u = g.u;
   const bool pen_on = g.pen_on, topk_on = g.topk_on, topp_on = g.topp_on;
   const RowOut o{g.out_ids, g.out_probs, g.out_info, row, V};
-  struct { int64_t* out_ids; float* out_probs; } P{g.out_ids, g.out_probs};
+  struct { IdSink out_ids; float* out_probs; } P{g.out_ids, g.out_probs};
 
   // ================= generic path: histogram passes over re-read data =================
   // Extras (history wave) contribute through `xl_each`.
@@ -775,7 +775,7 @@ __device__ __attribute__((always_inline)) inline void generic_path(const GCtx g)
         token = misc->ib[7] >= 0 ? misc->ib[7] : lastid;
       }
     }
-    if (tid == 0) P.out_ids[row] = token < 0 ? 0 : token;
+    if (tid == 0) put_id(P.out_ids, row, token < 0 ? 0 : token);
     write_info(o, PATH_LARGE_DRAW, (int32_t)n_kept, thr_y, n_topk, -1, flags, vstar, (int32_t)istar);
     if (P.out_probs != nullptr) {
       const double Z = misc->db[1];
@@ -863,7 +863,7 @@ __device__ __attribute__((always_inline, cold)) inline void row_general(KArgs PA
   if (h1 < h0 || H > MAX_HIST || (!xl_lds && (P.xl_glob == nullptr || umax > P.xg_cap - 8)))
     flags |= FLAG_HIST_TOO_LONG;
   if (flags != 0) {
-    if (tid == 0) P.out_ids[row] = -1;
+    if (tid == 0) put_id(P.out_ids, row, -1);
     write_info(o, PATH_ERROR, 0, 0.0f, 0, 0, flags, 0.0f, -1);
     return;
   }
@@ -1048,7 +1048,7 @@ __device__ __attribute__((always_inline, cold)) inline void row_general(KArgs PA
         if ((nanrow ? (x != x) : (x == Mx)) && xl_id[i] < best) best = xl_id[i];
       }
     best = block_min_i64(best, red);
-    if (tid == 0) P.out_ids[row] = best == INT64_MAX ? 0 : best;
+    if (tid == 0) put_id(P.out_ids, row, best == INT64_MAX ? 0 : best);
     write_info(o, PATH_GREEDY, 1, NEG_INF, 0, 0, flags, Mx, (int32_t)best);
     return;
   }
@@ -1062,7 +1062,7 @@ __device__ __attribute__((always_inline, cold)) inline void row_general(KArgs PA
       while (i > 0 && (double)i * qd > ud) --i;
       while ((double)(i + 1) * qd <= ud && i < V) ++i;
       if (i >= V) i = V - 1;
-      P.out_ids[row] = i;
+      put_id(P.out_ids, row, i);
     }
     write_info(o, PATH_UNIFORM, (int32_t)V, NEG_INF, (int32_t)V, 0, flags, My, -1);
     if (P.out_probs != nullptr) {
@@ -1559,7 +1559,17 @@ int sample_params(const ns_sample_args* a, ns::KParams& p, bool& has_hist) {
   p.hist_nslots = a->hist_n_slots;
   p.hist_cap = a->hist_capacity;
   p.uniforms = a->uniforms;
-  p.out_ids = a->out_ids;
+  p.out_ids = ns::IdSink{a->out_ids, nullptr, nullptr, nullptr, nullptr, 0, 0};
+  if (a->hist_append != 0) {
+    // the kernel that writes a row's id also appends it to the row's slot
+    if (!slots) return fail(NS_ERR_INVALID, "hist_append needs hist_state");
+    p.out_ids.slot = a->hist_slot;
+    p.out_ids.lens = static_cast<int32_t*>(a->hist_state);
+    p.out_ids.ids = const_cast<int32_t*>(h_ids);
+    p.out_ids.overflow = a->hist_overflow;
+    p.out_ids.cap = a->hist_capacity;
+    p.out_ids.nslots = a->hist_n_slots;
+  }
   p.out_probs = a->out_probs;
   p.out_info = a->out_info;
   p.n_sample = a->n_sample;
@@ -1913,7 +1923,7 @@ int ns_sample(const ns_sample_args* a, hipStream_t stream) {
     s.hist_nslots = a->hist_n_slots;
     s.hist_cap = a->hist_capacity;
     s.uniforms = a->uniforms;
-    s.out_ids = a->out_ids;
+    s.out_ids = p.out_ids;
     s.out_probs = a->out_probs;
     s.out_info = a->out_info;
     s.n_sample = a->n_sample;
@@ -1957,7 +1967,7 @@ int ns_sample(const ns_sample_args* a, hipStream_t stream) {
     w.hist_nslots = a->hist_n_slots;
     w.hist_cap = a->hist_capacity;
     w.uniforms = a->uniforms;
-    w.out_ids = a->out_ids;
+    w.out_ids = p.out_ids;
     w.out_probs = a->out_probs;
     w.out_info = a->out_info;
     w.n_sample = a->n_sample;

@@ -69,7 +69,7 @@ struct KParams {
   const int32_t* hist_len;    // slot lengths (hist_ids then holds hist_nslots * hist_cap ids)
   int32_t hist_nslots, hist_cap;
   const float* uniforms;
-  int64_t* out_ids;
+  IdSink out_ids;
   float* out_probs;
   int32_t* out_info;
   const int32_t* status;   // [n_sample] from the segment kernel (0 = resolved there), or NULL: every row

@@ -76,7 +76,7 @@ struct SegParams {
   const int32_t* hist_len;    // slot lengths (hist_ids then holds hist_nslots * hist_cap ids)
   int32_t hist_nslots, hist_cap;
   const float* uniforms;
-  int64_t* out_ids;
+  IdSink out_ids;
   float* out_probs;
   int32_t* out_info;
   int32_t n_sample;
@@ -378,7 +378,7 @@ __device__ __forceinline__ uint64_t wave_elem(const uint64_t (&a)[R], int i) {
 // value (-inf when fewer than k candidates); entries at i >= nk are ignored.
 template <int R>
 __device__ __forceinline__ void wave_select_draw(const uint64_t (&a)[R], int nk, float M, float thr, bool topp_on,
-                                                 float p32, float u, int row, int64_t* out_ids, float* out_probs,
+                                                 float p32, float u, int row, const IdSink& out_ids, float* out_probs,
                                                  int64_t V, int32_t* out_info, int32_t flags, int32_t n_cand,
                                                  int32_t path) {
   const int lane = lane_id();
@@ -482,7 +482,7 @@ __device__ __forceinline__ void wave_select_draw(const uint64_t (&a)[R], int nk,
       idp = (pick >> 6) == r ? t : idp;
     }
     if (lane == 0) {
-      out_ids[row] = (int64_t)idp;
+      put_id(out_ids, row, (int64_t)idp);
       seg_write_info(out_info, row, path, nf, thr, nk, n_cand, fl, vstar, istar);
     }
   }
@@ -504,7 +504,7 @@ __device__ __forceinline__ void wave_select_draw(const uint64_t (&a)[R], int nk,
 // is among them.
 template <int R>
 __device__ __forceinline__ void wave_finalize(const uint64_t* list, int n, int k, bool topp_on, float p32, float tdiv, float rdiv,
-                              float u, int row, int64_t* out_ids, float* out_probs, int64_t V, int32_t* out_info,
+                              float u, int row, const IdSink& out_ids, float* out_probs, int64_t V, int32_t* out_info,
                               int32_t flags, int32_t n_cand, int32_t path) {
   const int lane = lane_id();
   uint64_t a[R];
@@ -537,7 +537,7 @@ __device__ __forceinline__ void wave_finalize(const uint64_t* list, int n, int k
 // Tail of the workgroup finaliser: wave 0 loads the first nk sorted keys from LDS.
 template <int R>
 __device__ __forceinline__ void wave_select_draw_lds(const uint64_t* sorted, int nk, float M, float thr, bool topp_on, float p32,
-                                     float u, int row, int64_t* out_ids, float* out_probs, int64_t V,
+                                     float u, int row, const IdSink& out_ids, float* out_probs, int64_t V,
                                      int32_t* out_info, int32_t flags, int32_t n_cand, int32_t path) {
   const int lane = lane_id();
   uint64_t a[R];
@@ -560,7 +560,7 @@ __device__ __forceinline__ void wave_select_draw_lds(const uint64_t* sorted, int
 // reciprocal of the normaliser.
 __device__ __forceinline__ void wave_draw_sorted(uint64_t a, int nk, int n, const uint64_t* byid, const int32_t* vr,
                                                  float M, float thr, bool topp_on, float p32, float u, int row,
-                                                 int64_t* out_ids, float* out_probs, int64_t V, int32_t* out_info,
+                                                 const IdSink& out_ids, float* out_probs, int64_t V, int32_t* out_info,
                                                  int32_t flags, int32_t n_cand, int32_t path) {
   const int lane = lane_id();
   const uint64_t b0 = lane < n ? byid[lane] : ~0ull;
@@ -610,7 +610,7 @@ __device__ __forceinline__ void wave_draw_sorted(uint64_t a, int nk, int n, cons
   }
   const uint32_t i0 = read_lane(desc_key_id(b0), pick & 63), i1 = read_lane(desc_key_id(b1), pick & 63);
   if (lane == 0) {
-    out_ids[row] = (int64_t)(pick < 64 ? i0 : i1);
+    put_id(out_ids, row, (int64_t)(pick < 64 ? i0 : i1));
     seg_write_info(out_info, row, path, nf, thr, nk, n_cand, fl, vstar, istar);
   }
   if (out_probs != nullptr) {
@@ -697,7 +697,7 @@ __device__ __forceinline__ void block_rank_keys(const uint64_t* list, uint64_t* 
 
 template <int NTH>
 __device__ __forceinline__ void block_finalize_keys(const uint64_t* list, uint64_t* out, int n, int k, bool topp_on,
-                                                    float p32, float u, int row, int64_t* out_ids, float* out_probs,
+                                                    float p32, float u, int row, const IdSink& out_ids, float* out_probs,
                                                     int64_t V, int32_t* out_info, int32_t flags, int32_t n_cand,
                                                     int32_t path) {
   const int tid = threadIdx.x;
@@ -1055,7 +1055,7 @@ __device__ __forceinline__ void segment_body(const SegParams& P, SegSmem& sm) {
         if (fl & SFLAG_XOVER) {
           P.status[row] = 1;   // a segment's distinct history ids outgrew its list: per-row kernel
         } else {
-          P.out_ids[row] = am == 0x7fffffff ? 0 : am;
+          put_id(P.out_ids, row, am == 0x7fffffff ? 0 : am);
           P.status[row] = 0;
           seg_write_info(P.out_info, row, PATH_GREEDY, 1, -__builtin_inff(), 0, 0, fl & 0xffff, M, am);
         }
@@ -1093,7 +1093,7 @@ __device__ __forceinline__ void segment_body(const SegParams& P, SegSmem& sm) {
       while (i > 0 && (double)i * qd > ud) --i;
       while ((double)(i + 1) * qd <= ud && i < V) ++i;
       if (i >= V) i = V - 1;
-      P.out_ids[row] = i;
+      put_id(P.out_ids, row, i);
       P.status[row] = 0;
       seg_write_info(P.out_info, row, PATH_UNIFORM, (int32_t)V, -__builtin_inff(), (int32_t)V, 0, fl, Mrep, -1);
     }

@@ -59,7 +59,7 @@ __device__ __forceinline__ void uniform_row_out(const RowOut& o, float u, int32_
     while (i > 0 && (double)i * qd > ud) --i;
     while ((double)(i + 1) * qd <= ud && i < V) ++i;
     if (i >= V) i = V - 1;
-    o.out_ids[o.row] = i;
+    put_id(o.out_ids, o.row, i);
   }
   write_info(o, PATH_UNIFORM, (int32_t)V, -__builtin_inff(), (int32_t)V, 0, flags, Mrep, -1);
   if (o.out_probs != nullptr) {

@@ -63,7 +63,9 @@ struct WideRow {
   int32_t istar;
   int32_t n_kept;
   double zkept;            // normaliser of the kept set
-  int32_t pad[14];
+  int32_t hlen;            // the row's history length when it was planned (the probs pass reads
+                           // it: a device-resident history may have grown by the drawn token)
+  int32_t pad[13];
 };
 static_assert(sizeof(WideRow) == 128, "WideRow layout");
 
@@ -96,7 +98,7 @@ struct WideParams {
   const int32_t* hist_len;    // slot lengths (hist_ids then holds hist_nslots * hist_cap ids)
   int32_t hist_nslots, hist_cap;
   const float* uniforms;
-  int64_t* out_ids;
+  IdSink out_ids;
   float* out_probs;
   int32_t* out_info;
   int32_t n_sample;
@@ -672,6 +674,7 @@ __device__ __forceinline__ void wide_plan(const WideParams& P, const WRowCtx& c,
     R->M = M;
     R->flags = fl;
     R->nfin = nfin;
+    R->hlen = c.H;
     R->step = WSTEP_CUT;
   }
 }
@@ -836,7 +839,7 @@ __device__ __forceinline__ void wide_stats_body(const WideParams& P, WideSmem& s
       while (i > 0 && (double)i * qd > ud) --i;
       while ((double)(i + 1) * qd <= ud && i < V) ++i;
       if (i >= V) i = V - 1;
-      P.out_ids[row] = i;
+      put_id(P.out_ids, row, i);
       const float mrep = (fl & SFLAG_NAN) ? __builtin_nanf("") : (nf == 0 ? -__builtin_inff() : __builtin_inff());
       seg_write_info(P.out_info, row, PATH_UNIFORM, (int32_t)V, -__builtin_inff(), (int32_t)V, 0, fl & 0xffff, mrep,
                      -1);
@@ -867,6 +870,7 @@ __device__ __forceinline__ void wide_stats_body(const WideParams& P, WideSmem& s
       R->M = M;
       R->flags = fl;
       R->nfin = nf;
+      R->hlen = c.H;
       R->step = WSTEP_FULL;
     }
     return;
@@ -1148,7 +1152,7 @@ __global__ __launch_bounds__(NT) void wide_final_kernel(const WideParams P) {
     const WKeep keep{-__builtin_inff(), -__builtin_inff(), 0x7fffffff};
     const int64_t tok = wide_locate<T, NT, 1, SEG_CH>(P, c, (int64_t)s * SEG_CH, start, 1.0 / Z, M, keep, &sm, &fl);
     if (tid == 0) {
-      P.out_ids[row] = tok;
+      put_id(P.out_ids, row, tok);
       seg_write_info(P.out_info, row, PATH_WIDE, nfin, -__builtin_inff(), nfin, 0, fl, -__builtin_inff(), -1);
       R->thr = -__builtin_inff();
       R->vstar = -__builtin_inff();
@@ -1338,7 +1342,7 @@ __global__ __launch_bounds__(NT) void wide_final_kernel(const WideParams P) {
     constexpr int WL = EPC == 4 ? 2 : 1;
     const int64_t tok = wide_locate<T, NT, WL, SEG_CH>(P, c, (int64_t)s * SEG_CH, start, 1.0 / zkept, M, keep, &sm, &fl);
     if (tid == 0) {
-      P.out_ids[row] = tok;
+      put_id(P.out_ids, row, tok);
       seg_write_info(P.out_info, row, PATH_WIDE, n_kept, kon0 ? thr : -__builtin_inff(), n_topk, n, fl, vstar, istar);
       R->thr = thr;
       R->vstar = vstar;
@@ -1366,7 +1370,9 @@ __global__ __launch_bounds__(SNT) void wide_probs_kernel(const WideParams P) {
   if (row >= P.n_sample) return;
   const WideRow* R = P.rows + row;
   if (R->step != WSTEP_DRAWN) return;
-  const WRowCtx c = wide_row_ctx<T>(P, row);
+  WRowCtx c = wide_row_ctx<T>(P, row);
+  c.H = R->hlen;                             // the history the row was sampled with
+  c.pen_on = c.pen != 1.0f && c.H > 0;
   const int64_t c0 = (int64_t)seg * SEG_CH;
   wide_bitmap<T>(P, c, c0 * EPC, &sm);
   const float M = R->M;

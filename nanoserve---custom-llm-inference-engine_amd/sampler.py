@@ -27,7 +27,7 @@ Additions, all keyword-only and optional:
   The engine rebuilds prompt + output ids for every request and step
   (engine.py:242-246) and the reference copies them to the device each call
   (sampler.py:34); here each request's ids are copied once when it starts and
-  every sampled token is appended on the device by the same call.
+  every sampled token is appended on the device by the kernel that draws it.
 * ``async_ids``: return a ``SampledIds`` handle instead of the tensor.  Its ids
   are copied into pinned host memory behind an event on the same stream, so
   ``.tolist()`` (engine.py:250) waits only when the engine reads them and the
@@ -303,9 +303,8 @@ class Sampler:
             _lib.sample_raw(logits, d["temperature"], d["top_k"], d["top_p"], d["rep_penalty"], uniforms, out,
                             sample_idx=sample_indices, hist_offsets=d["hist_offsets"], hist_ids=d["hist_ids"],
                             max_hist=packed.max_hist, out_probs=probs, row_kinds=packed.row_kinds,
-                            hist_state=hs, hist_slot=d["hist_slot"])
+                            hist_state=hs, hist_slot=d["hist_slot"], hist_append=hs is not None)
             if hs is not None:
-                hs.append(d["hist_slot"], out)
                 device_histories._appended(slots)
         res = self._readback(out) if async_ids else out
         return (res, probs) if return_probs else res

@@ -41,7 +41,7 @@ def test_struct_layout_matches_header():
     body = txt[txt.index("typedef struct ns_sample_args"):txt.index("} ns_sample_args;")]
     names = re.findall(r"^\s*[\w\s\*]+?\b(\w+);", body, flags=re.M)
     assert names == [f[0] for f in L.NsSampleArgs._fields_]
-    assert ctypes.sizeof(L.NsSampleArgs) == 184
+    assert ctypes.sizeof(L.NsSampleArgs) == 200
 
 
 def test_lds_bytes_and_argument_errors():
@@ -100,6 +100,9 @@ def test_history_state_layout_and_argument_errors():
     assert lib.ns_sample(ctypes.byref(a), None) == 1 and "excludes" in L.last_error()
     a.hist_offsets = a.hist_ids = None
     assert lib.ns_sample(ctypes.byref(a), None) == 1 and "hist_slot" in L.last_error()
+    # appending the sampled ids in the kernels needs the device-resident histories
+    a.hist_state, a.hist_n_slots, a.hist_capacity, a.hist_append = None, 0, 0, 1
+    assert lib.ns_sample(ctypes.byref(a), None) == 1 and "hist_append needs hist_state" in L.last_error()
 
 
 def test_packing_with_history_slots():

@@ -7,7 +7,10 @@ history through the same start/length pair).  Over a multi-step decode loop,
 appending each sampled token on the device must track the host-side lists the
 reference's engine rebuilds every step (engine.py:242-246,
 scheduler.py:281-284), and every step's ids must meet the oracle run on that
-step's logits, host histories and uniforms.
+step's logits, host histories and uniforms.  The append fused into the sampling
+kernels (hist_append) must leave the same lists, ids, diagnostics and
+probabilities as the call without it followed by ns_hist_append, in every
+launch set, over two steps (the second reads the appended ids).
 """
 import numpy as np
 import pytest
@@ -32,8 +35,9 @@ def open_all(w, device, extra_slots=3):
     return dh
 
 
-def run_slots(w, device, dh, workspace, mode, row_kinds=0):
-    """run_gpu's call with the histories read from ``dh`` (request r on row r), no append."""
+def run_slots(w, device, dh, workspace, mode, row_kinds=0, append=False, overflow=None):
+    """run_gpu's call with the histories read from ``dh`` (request r on row r); with
+    ``append`` the kernels also append each row's id to its slot."""
     slots = dh.slots(list(range(w.batch)))
     max_hist = int(max(dh.length(r) for r in range(w.batch)))
     packed = S.PackedRows(params_of(w), None, w.vocab, slots=slots, slot_max_hist=max_hist)
@@ -49,8 +53,11 @@ def run_slots(w, device, dh, workspace, mode, row_kinds=0):
     info = torch.zeros((B, L.NS_INFO_WORDS), dtype=torch.int32, device=device)
     L.sample_raw(logits, d["temperature"], d["top_k"], d["top_p"], d["rep_penalty"], u, out,
                  sample_idx=sidx, max_hist=packed.max_hist, out_probs=probs, out_info=info, workspace=workspace,
-                 mode=mode, row_kinds=int(row_kinds), hist_state=dh.state, hist_slot=d["hist_slot"])
+                 mode=mode, row_kinds=int(row_kinds), hist_state=dh.state, hist_slot=d["hist_slot"],
+                 hist_append=append, hist_overflow=overflow)
     torch.cuda.synchronize()
+    if append:
+        dh._appended(slots)
     return {"ids": out.cpu().numpy(), "probs": probs.cpu(), "info": info.cpu().numpy()}
 
 
@@ -79,6 +86,63 @@ def test_device_histories_match_csr(device, cfg, path):
     bad = np.nonzero((got["info"] != ref["info"]).any(axis=1))[0]
     assert bad.size == 0, [(int(i), ref["info"][i].tolist(), got["info"][i].tolist()) for i in bad[:4]]
     assert torch.equal(got["probs"], ref["probs"])
+
+
+@pytest.mark.parametrize("path", list(PATHS))
+@pytest.mark.parametrize("cfg", [1, 2, 3, 4])
+def test_fused_append_matches_separate_append(device, cfg, path):
+    w = W.make_workload(cfg, batch=64 if cfg == 2 else (48 if cfg == 3 else None))
+    ws, mode = PATHS[path]
+    sep, fused = open_all(w, device), open_all(w, device)
+    reqs = list(range(w.batch))
+    over = torch.zeros(1, dtype=torch.int32, device=device)
+    for step in range(2):
+        print(f"[history] fused append: config {cfg} B={w.batch} path={path} step {step}", flush=True)
+        a = run_slots(w, device, sep, ws, mode, row_kinds=path_kinds(path))
+        slots = torch.from_numpy(sep.slots(reqs)).to(device)
+        sep.state.append(slots, torch.from_numpy(a["ids"]).to(device))
+        sep._appended(sep.slots(reqs))
+        b = run_slots(w, device, fused, ws, mode, row_kinds=path_kinds(path), append=True, overflow=over)
+        assert np.array_equal(a["ids"], b["ids"]), f"step {step}: rows {np.nonzero(a['ids'] != b['ids'])[0][:8]}"
+        bad = np.nonzero((a["info"] != b["info"]).any(axis=1))[0]
+        assert bad.size == 0, [(int(i), a["info"][i].tolist(), b["info"][i].tolist()) for i in bad[:4]]
+        assert torch.equal(a["probs"], b["probs"])
+        torch.cuda.synchronize()
+        assert read_state(fused, reqs) == read_state(sep, reqs)
+        assert all(fused.length(r) == len(h) for r, h in zip(reqs, read_state(fused, reqs)))
+    assert int(over.item()) == 0 and int(sep.state.overflow.item()) == 0
+
+
+def test_fused_append_counts_full_slots(device):
+    """A full slot keeps its ids and is counted; rows without a slot append nothing."""
+    w = W.make_workload(1)
+    B = w.batch
+    cap = max(len(h) for h in w.histories)
+    dh = S.DeviceHistories(device, B + 1, capacity=cap)
+    for r in range(B):
+        dh.open(r, w.histories[r] if r % 3 == 0 else w.histories[r][:cap - 20])
+    full = [r for r in range(B) if dh.length(r) == cap]
+    assert full and len(full) < B
+    before = read_state(dh, list(range(B)))
+    slots = dh.slots(list(range(B))).copy()
+    slots[1] = -1
+    if 1 in full:
+        full.remove(1)
+    packed = S.PackedRows(params_of(w), None, w.vocab, slots=slots, slot_max_hist=cap)
+    d = packed.to_device(device)
+    u = torch.from_numpy(np.asarray(w.uniforms, dtype=np.float32)).to(device)
+    out = torch.full((B,), -7, dtype=torch.int64, device=device)
+    over = torch.zeros(1, dtype=torch.int32, device=device)
+    L.sample_raw(w.device_logits(device), d["temperature"], d["top_k"], d["top_p"], d["rep_penalty"], u, out,
+                 max_hist=cap, hist_state=dh.state, hist_slot=d["hist_slot"], hist_append=True, hist_overflow=over,
+                 row_kinds=packed.row_kinds)
+    torch.cuda.synchronize()
+    ids = out.cpu().numpy()
+    after = read_state(dh, list(range(B)))
+    assert int(over.item()) == len(full)
+    for r in range(B):
+        want = before[r] if (r == 1 or r in full) else before[r] + [int(ids[r])]
+        assert after[r] == want, r
 
 
 def test_decode_loop_appends_on_device(device):
