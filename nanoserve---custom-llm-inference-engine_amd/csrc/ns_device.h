@@ -296,6 +296,17 @@ __device__ __forceinline__ int64_t block_max_i64(int64_t v, BlockScratch* s) {
   __syncthreads();
   return r;
 }
+// Whether any thread of the workgroup holds v (one word per wave; two barriers).
+__device__ __forceinline__ bool block_any(bool v, BlockScratch* s) {
+  int32_t* words = reinterpret_cast<int32_t*>(s);
+  const bool w = ballot(v) != 0ull;
+  if (lane_id() == 0) words[wave_id()] = w ? 1 : 0;
+  __syncthreads();
+  const int l = lane_id();
+  const bool r = ballot(l < NWAVE && words[l < NWAVE ? l : 0] != 0) != 0ull;
+  __syncthreads();
+  return r;
+}
 // Exclusive prefix over threads in thread order (double); *total receives the block sum.
 __device__ __forceinline__ double block_excl_scan(double v, double* total, BlockScratch* s) {
   double inc = wave_incl_scan(v);
@@ -398,6 +409,20 @@ __device__ __forceinline__ float div_rn(float x, float t, float r) {
     if (slow) q = x / t;
   }
   return q;
+}
+
+// The NaN guard's uniform row (sampler.py:77-80).  Every token's probability is the float32
+// 1/V: RN32(1/V) equals RN32(RN64(1/V)) for every V up to 2^18 (every one checked on the CPU),
+// so the float32 division gives torch's value.  The pick is the i with i * q <= u < (i + 1) * q
+// in float64 (exact: i < 2^18 times a 24-bit q), V - 1 if none; the loops reach it from any
+// start, and u * V is within one step of it.
+__device__ __forceinline__ float uniform_q(int64_t V) { return 1.0f / (float)V; }
+__device__ __forceinline__ int64_t uniform_pick(float u, float q, int64_t V) {
+  const double qd = q, ud = u;
+  int64_t i = (int64_t)(ud * (double)V);
+  while (i > 0 && (double)i * qd > ud) --i;
+  while ((double)(i + 1) * qd <= ud && i < V) ++i;
+  return i >= V ? V - 1 : i;
 }
 
 // The repetition penalty of one history token (sampler.py:37: score * p if score < 0 else

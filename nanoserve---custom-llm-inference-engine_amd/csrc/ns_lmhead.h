@@ -180,16 +180,17 @@ __global__ __launch_bounds__(LM_THREADS, 1) void lm_head_kernel(const LmParams P
     const uint16_t* at = sa[buf] + (wm * 64 + r32) * LM_PITCH + 32 * h;
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
-      lm_bf16x8 a[2], b[JT];
+      lm_bf16x8 a[2];
 #pragma unroll
       for (int i = 0; i < 2; ++i) a[i] = *reinterpret_cast<const lm_bf16x8*>(at + 32 * i * LM_PITCH + 8 * s);
 #pragma unroll
-      for (int j = 0; j < JT; ++j) b[j] = *reinterpret_cast<const lm_bf16x8*>(wt + 32 * j * LM_PITCH + 8 * s);
-#pragma unroll
-      for (int j = 0; j < JT; ++j)
+      for (int j = 0; j < JT; ++j) {
+        // one weight operand at a time (JT = 4: the accumulators leave no room for more)
+        const lm_bf16x8 b = *reinterpret_cast<const lm_bf16x8*>(wt + 32 * j * LM_PITCH + 8 * s);
 #pragma unroll
         for (int i = 0; i < 2; ++i)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[i], b[j], acc[i][j], 0, 0, 0);
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[i], b, acc[i][j], 0, 0, 0);
+      }
     }
   };
   // one stage: stage st + D is issued into the set that held stage st (already in LDS),
@@ -210,9 +211,21 @@ __global__ __launch_bounds__(LM_THREADS, 1) void lm_head_kernel(const LmParams P
   store(ar[0], wr[0], 0);
   lm_lds_barrier();
   int st = 0;
-  for (; st + D <= nst; st += D) {
+  if constexpr (WM == 4) {
+    // at least D stages (the host takes WM = 4 only for k >= 64 D): the pipelined loop runs at
+    // least once, and no path around it holds the prefetched stages (there the register
+    // allocator, with the 128 accumulators live, would spill them)
+    __builtin_assume(nst >= D);
+    do {
 #pragma unroll
-    for (int d = 0; d < D; ++d) stage(st + d, d);
+      for (int d = 0; d < D; ++d) stage(st + d, d);
+      st += D;
+    } while (st + D <= nst);
+  } else {
+    for (; st + D <= nst; st += D) {
+#pragma unroll
+      for (int d = 0; d < D; ++d) stage(st + d, d);
+    }
   }
 #pragma unroll
   for (int d = 0; d < D - 1; ++d)

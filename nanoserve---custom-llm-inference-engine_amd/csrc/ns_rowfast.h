@@ -195,15 +195,8 @@ __device__ __forceinline__ int row_fast(const RowArgs P, const int row, const in
   const int nf = (int)nfull;
   const RowOut o{P.out_ids, P.out_probs, P.out_info, row, V};
   auto uniform_row = [&](float Mrep) {
-    const float qv = (float)(1.0 / (double)V);
-    if (tid == 0) {
-      const double qd = qv, ud = u;
-      int64_t i = (int64_t)(ud / qd);
-      while (i > 0 && (double)i * qd > ud) --i;
-      while ((double)(i + 1) * qd <= ud && i < V) ++i;
-      if (i >= V) i = V - 1;
-      put_id(P.out_ids, row, i);
-    }
+    const float qv = uniform_q(V);
+    if (tid == 0) put_id(P.out_ids, row, uniform_pick(u, qv, V));
     write_info(o, PATH_UNIFORM, (int32_t)V, -__builtin_inff(), (int32_t)V, 0, flags, Mrep, -1);
     if (P.out_probs != nullptr) {
       float* pr = P.out_probs + (int64_t)row * V;
@@ -377,7 +370,7 @@ __device__ __forceinline__ int row_fast(const RowArgs P, const int row, const in
       for (int e = 0; e < EPC; ++e) nanf |= T::elem(w, e) != T::elem(w, e);
     }
     if (wid == 0) nanf |= xt != xt;
-    const int anynan = block_max_i64(nanf ? 1 : 0, red) != 0;
+    const bool anynan = block_any(nanf, red);
     uniform_row(anynan ? __builtin_nanf("") : __builtin_inff());
     return 0;
   }

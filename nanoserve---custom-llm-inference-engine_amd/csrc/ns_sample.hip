@@ -1055,15 +1055,8 @@ __device__ __attribute__((always_inline, cold)) inline void row_general(KArgs PA
 
   // ---- rows whose softmax is NaN: uniform 1/V over the vocabulary (sampler.py:77-80)
   if (!(__builtin_fabsf(My) <= FLT_MAXV)) {
-    const float q = (float)(1.0 / (double)V);
-    const double qd = q, ud = u;
-    if (tid == 0) {
-      int64_t i = (int64_t)(ud / qd);
-      while (i > 0 && (double)i * qd > ud) --i;
-      while ((double)(i + 1) * qd <= ud && i < V) ++i;
-      if (i >= V) i = V - 1;
-      put_id(P.out_ids, row, i);
-    }
+    const float q = uniform_q(V);
+    if (tid == 0) put_id(P.out_ids, row, uniform_pick(u, q, V));
     write_info(o, PATH_UNIFORM, (int32_t)V, NEG_INF, (int32_t)V, 0, flags, My, -1);
     if (P.out_probs != nullptr) {
       float* pr = P.out_probs + (int64_t)row * V;
@@ -1660,7 +1653,10 @@ static int lm_launch(const void* hidden, int64_t ld_hidden, int64_t n_hidden, co
   if (rows == nullptr && n_hidden < m) return fail(NS_ERR_INVALID, "n_hidden < m without rows");
   // waves along the batch: the fewest that hold it (64 rows each), so small batches keep every
   // wave on products; batches beyond 256 rows take several workgroup rows
-  const int wm = m <= 64 ? 1 : m <= 128 ? 2 : 4;
+  int wm = m <= 64 ? 1 : m <= 128 ? 2 : 4;
+  // WM = 4 keeps two weight stages in flight and needs at least two (k >= 128); a smaller k
+  // takes workgroup rows of WM = 2 (the same sums in the same order)
+  if (wm == 4 && k < 2 * ns::LM_KT) wm = 2;
   const int64_t gy = ((int64_t)m + 64 * wm - 1) / (64 * wm);
   if (gy > 65535) return fail(NS_ERR_INVALID, "m too large");
   ns::LmParams P{static_cast<const uint16_t*>(hidden), ld_hidden, rows, n_hidden, static_cast<const uint16_t*>(weight),

@@ -1086,14 +1086,9 @@ __device__ __forceinline__ void segment_body(const SegParams& P, SegSmem& sm) {
 
   auto uniform_row = [&](float Mrep) {
     // rows whose softmax is NaN: uniform 1/V over the vocabulary (sampler.py:77-80)
-    const float qv = (float)(1.0 / (double)V);
+    const float qv = uniform_q(V);
     if (tid == 0) {
-      const double qd = qv, ud = u;
-      int64_t i = (int64_t)(ud / qd);
-      while (i > 0 && (double)i * qd > ud) --i;
-      while ((double)(i + 1) * qd <= ud && i < V) ++i;
-      if (i >= V) i = V - 1;
-      put_id(P.out_ids, row, i);
+      put_id(P.out_ids, row, uniform_pick(u, qv, V));
       P.status[row] = 0;
       seg_write_info(P.out_info, row, PATH_UNIFORM, (int32_t)V, -__builtin_inff(), (int32_t)V, 0, fl, Mrep, -1);
     }

@@ -192,7 +192,7 @@ __device__ __forceinline__ int32_t split_slice(const unsigned char* rowp, const 
       }
     }
     nanf |= xt != xt;
-    const int anynan = block_max_i64(nanf ? 1 : 0, &misc->red) != 0;
+    const bool anynan = block_any(nanf, &misc->red);
     return anynan ? SPF_NAN : SPF_PINF;
   }
   float tc = misc->fb[0];

@@ -52,15 +52,8 @@ __host__ __device__ __forceinline__ int topk_phases(int64_t V) {
 // reported in the diagnostics (NaN, +inf or -inf).
 __device__ __forceinline__ void uniform_row_out(const RowOut& o, float u, int32_t flags, float Mrep) {
   const int64_t V = o.V;
-  const float qv = (float)(1.0 / (double)V);
-  if (threadIdx.x == 0) {
-    const double qd = qv, ud = u;
-    int64_t i = (int64_t)(ud / qd);
-    while (i > 0 && (double)i * qd > ud) --i;
-    while ((double)(i + 1) * qd <= ud && i < V) ++i;
-    if (i >= V) i = V - 1;
-    put_id(o.out_ids, o.row, i);
-  }
+  const float qv = uniform_q(V);
+  if (threadIdx.x == 0) put_id(o.out_ids, o.row, uniform_pick(u, qv, V));
   write_info(o, PATH_UNIFORM, (int32_t)V, -__builtin_inff(), (int32_t)V, 0, flags, Mrep, -1);
   if (o.out_probs != nullptr) {
     float* pr = o.out_probs + (int64_t)o.row * V;
@@ -280,7 +273,7 @@ __device__ __forceinline__ int topk_stream(const RowArgs P, const int row, const
       for (int e = 0; e < EPC; ++e) nanf |= T::elem(w, e) != T::elem(w, e);
     }
     if (wid == 0) nanf |= xt != xt;
-    const int anynan = block_max_i64(nanf ? 1 : 0, &misc->red) != 0;
+    const bool anynan = block_any(nanf, &misc->red);
     uniform_row_out(o, u, flags, anynan ? __builtin_nanf("") : __builtin_inff());
     return 0;
   }

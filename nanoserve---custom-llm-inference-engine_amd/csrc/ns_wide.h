@@ -832,14 +832,9 @@ __device__ __forceinline__ void wide_stats_body(const WideParams& P, WideSmem& s
     // the softmax is NaN (a NaN or +inf logit, or every logit -inf): uniform 1/V
     // (sampler.py:77-80)
     const int64_t V = c.V;
-    const float qv = (float)(1.0 / (double)V);
+    const float qv = uniform_q(V);
     if (tid == 0) {
-      const double qd = qv, ud = c.u;
-      int64_t i = (int64_t)(ud / qd);
-      while (i > 0 && (double)i * qd > ud) --i;
-      while ((double)(i + 1) * qd <= ud && i < V) ++i;
-      if (i >= V) i = V - 1;
-      put_id(P.out_ids, row, i);
+      put_id(P.out_ids, row, uniform_pick(c.u, qv, V));
       const float mrep = (fl & SFLAG_NAN) ? __builtin_nanf("") : (nf == 0 ? -__builtin_inff() : __builtin_inff());
       seg_write_info(P.out_info, row, PATH_UNIFORM, (int32_t)V, -__builtin_inff(), (int32_t)V, 0, fl & 0xffff, mrep,
                      -1);

@@ -35,3 +35,15 @@ def test_div_rn_matches_ieee_division():
     old = subprocess.run([exe, "0", "old"], capture_output=True, text=True, timeout=300)
     print(old.stdout)
     assert old.returncode == 1 and "mismatch t=" in old.stdout, old.stdout + old.stderr
+
+
+def test_uniform_row_probability_single_rounding():
+    """The NaN guard's uniform row (sampler.py:77-80) gives every token torch's float32 1/V,
+    the float64 quotient rounded to float32.  The kernels divide in float32 (ns::uniform_q):
+    the two roundings agree for every vocabulary size up to the ABI's limit of 2^18."""
+    import numpy as np
+
+    v = np.arange(1, 2**18 + 1, dtype=np.float64)
+    twice = (1.0 / v).astype(np.float32)
+    once = np.float32(1.0) / v.astype(np.float32)
+    assert np.array_equal(twice.view(np.uint32), once.view(np.uint32))
