@@ -200,6 +200,11 @@ __device__ __forceinline__ float wave_min_nan(float v) {
   for (int o = 32; o > 0; o >>= 1) v = fmin_nan(v, lane_xor(v, o));
   return v;
 }
+template <typename T> __device__ __forceinline__ T wave_or(T v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v |= lane_xor(v, o);
+  return v;
+}
 template <typename T> __device__ __forceinline__ T wave_max(T v) {
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) { T w = lane_xor(v, o); v = w > v ? w : v; }

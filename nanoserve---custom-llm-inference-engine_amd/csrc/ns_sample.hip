@@ -1115,6 +1115,9 @@ __device__ __attribute__((always_inline, cold)) inline void row_general(KArgs PA
 template <typename T>
 __global__ __launch_bounds__(NT) void sample_kernel(const KParams P) {
   const int row = blockIdx.x;
+  // rows the segment kernel or the wide path resolved carry status 0 (every other row 1):
+  // those workgroups end before anything else is read
+  if (P.status != nullptr && P.status[row] == 0) return;
   // every per-row parameter is requested before any is used: one round trip to memory
   // ahead of the row's stream instead of a chain of dependent ones
   const float temp = P.temperature[row];
@@ -1125,8 +1128,6 @@ __global__ __launch_bounds__(NT) void sample_kernel(const KParams P) {
   const int64_t src = P.sample_idx ? P.sample_idx[row] : (int64_t)row;
   int32_t h0 = 0, h1 = 0;
   row_history(P.hist_off, P.hist_slot, P.hist_len, P.hist_nslots, P.hist_cap, row, h0, h1);
-  // rows the segment kernel resolved carry status 0; every other row carries 1
-  if (P.status != nullptr && P.status[row] == 0) return;
   if (P.fast) {
     // greedy and small-k rows that fit in registers: one streaming pass
     if (seg_row(temp, k, P.vocab) && row_fits<T>(P.vocab)) {

@@ -1042,9 +1042,7 @@ __device__ __forceinline__ void segment_body(const SegParams& P, SegSmem& sm) {
     const bool act = lane < S;
     SegStat s;
     if (act) s = dc_load_stat(rs + lane);
-    int32_t fl = act ? s.flags : 0;
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) fl |= lane_xor(fl, o);
+    const int32_t fl = wave_or(act ? s.flags : 0);
     if (greedy) {
       const float ym = act ? s.ymax : -__builtin_inff();
       const float M = wave_max_nan(ym);

@@ -381,9 +381,7 @@ __global__ __launch_bounds__(NT) void split_kernel(const SplitParams SP) {
     // key below it is in the row's top-k set); each list's keys at or above G (a prefix)
     const bool act = lane < S;
     const int32_t ms = act ? (int32_t)(uint32_t)w0 : 0, fls = (int32_t)(uint32_t)(w0 >> 32);
-    int32_t orf = fls;
-#pragma unroll
-    for (int s2 = 32; s2 > 0; s2 >>= 1) orf |= lane_xor(orf, s2);
+    const int32_t orf = wave_or(fls);
     const uint64_t* ul = uni + lane * SP_LIST;
     const float g = wave_max(act && ms >= k ? desc_key_val(ul[k - 1]) : -__builtin_inff());
     int lo = 0, hi = ms;

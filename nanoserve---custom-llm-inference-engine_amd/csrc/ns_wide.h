@@ -488,22 +488,31 @@ __device__ __forceinline__ int64_t wide_locate(const WideParams& P, const WRowCt
                                                double rz, float M, const WKeep& keep, SM* sm, int32_t* fl) {
   constexpr int EPC = T::EPC;
   static_assert(NCH % (NTH * WL) == 0 && NCH <= SEG_CH, "whole steps inside one segment's bitmap");
+  constexpr int NSTEP = NCH / (NTH * WL);
+  static_assert(NSTEP * WL <= 4, "the segment's chunks of a thread fit 16 registers");
   const int tid = threadIdx.x;
-  *fl |= wide_bitmap<T, NTH>(P, c, c0 * EPC, sm);
   const uint32_t nbytes = (uint32_t)((c.V / EPC) * 16);
+  // every step's chunks are requested first, with the history ids of the bitmap: one round
+  // trip to memory for the whole walk
+  uint4 raw[NSTEP][WL];
+#pragma unroll
+  for (int step = 0; step < NSTEP; ++step)
+#pragma unroll
+    for (int j = 0; j < WL; ++j)
+      raw[step][j] = buf_load16_at(c.rowp, nbytes,
+                                   (uint32_t)((c0 + (int64_t)step * NTH * WL + (int64_t)tid * WL + j) * 16), 0u);
+  *fl |= wide_bitmap<T, NTH>(P, c, c0 * EPC, sm);
   if (tid == 0) { sm->ib[0] = 0x7fffffff; sm->ib[1] = -1; }
   const double ud = (double)c.u;
   double carry = pstart;
-  for (int step = 0; step < NCH / (NTH * WL); ++step) {
-    const int64_t cb = c0 + (int64_t)step * NTH * WL + (int64_t)tid * WL;   // first chunk of this thread
-    uint4 raw[WL];
 #pragma unroll
-    for (int j = 0; j < WL; ++j) raw[j] = buf_load16_at(c.rowp, nbytes, (uint32_t)((cb + j) * 16), 0u);
+  for (int step = 0; step < NSTEP; ++step) {
+    const int64_t cb = c0 + (int64_t)step * NTH * WL + (int64_t)tid * WL;   // first chunk of this thread
     float p[WL * EPC];
 #pragma unroll
     for (int j = 0; j < WL; ++j) {
       const int64_t ch = cb + j;
-      const uint4 w = wide_chunk_fix<T>(c, ch, raw[j]);
+      const uint4 w = wide_chunk_fix<T>(c, ch, raw[step][j]);
       const uint32_t hb = c.pen_on ? T::bits(sm->bm, (int)(ch - c0)) : 0u;
       float y[EPC];
       chunk_y<T>(c, w, hb, ch * EPC, y);
@@ -1123,15 +1132,17 @@ __global__ __launch_bounds__(NT) void wide_final_kernel(const WideParams P) {
   const int32_t nfin = R->nfin;
   if (step == WSTEP_FULL) {
     // ---- every finite value kept: the segment holding u from the per-segment masses, then
-    // the walk inside it
+    // the walk inside it (the masses read in parallel, then summed in segment order)
+    if (tid < P.S) sm.subq[tid] = dc_load_wseg(P.segs + (int64_t)row * P.S + tid).mass;
+    __syncthreads();
     if (tid == 0) {
       double Z = 0.0;
-      for (int i = 0; i < P.S; ++i) Z += __longlong_as_double((long long)dc_load_wseg(P.segs + (int64_t)row * P.S + i).mass);
+      for (int i = 0; i < P.S; ++i) Z += __longlong_as_double((long long)sm.subq[i]);
       const double ud = (double)c.u * Z;
       double run = 0.0, start = 0.0, laststart = 0.0;
       int s = -1, lastnz = -1;
       for (int i = 0; i < P.S; ++i) {
-        const double w = __longlong_as_double((long long)dc_load_wseg(P.segs + (int64_t)row * P.S + i).mass);
+        const double w = __longlong_as_double((long long)sm.subq[i]);
         if (w > 0.0) { lastnz = i; laststart = run; }
         if (s < 0 && run + w > ud && w > 0.0) { s = i; start = run; }
         run += w;
