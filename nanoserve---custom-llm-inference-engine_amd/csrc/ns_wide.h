@@ -157,27 +157,23 @@ __device__ __forceinline__ int wbin(int tb, float y) {
   return d < WBINS ? d : WBINS;
 }
 // exp(y - M) in units of 2^-44 (y <= M), truncated: (uint64_t)(e * 2^44) for the float32
-// e = exp(y - M) in [0, 1], taken from e's exponent and mantissa bits (the product with
-// 2^44 is exact, so the integer is the same as through float64).
-__device__ __forceinline__ uint64_t wfx(float M, float y) {
-  const uint32_t b = __float_as_uint(ns_expf(y - M));
-  const int E = (int)(b >> 23);                        // biased exponent (e >= 0)
-  const uint64_t m = (uint64_t)((b & 0x7fffffu) | 0x800000u);
-  if (E >= 106) return m << (E - 106);                 // e * 2^44 = m * 2^(E - 127 - 23 + 44)
-  const int r = 106 - E;
-  return (E > 0 && r < 64) ? (m >> r) : 0ull;          // zero and subnormal e: below 2^-44
+// e = exp(y - M) in [0, 1] (the product with 2^44 is exact, so the integer is the same as
+// through float64).  It is formed in two 32-bit halves with exact float operations:
+// x = e * 2^12 (at most 4096), hi = trunc(x), lo = trunc((x - hi) * 2^32) (x - hi is exact,
+// and so is the scaling); hi * 2^32 + lo = trunc(e * 2^44).
+__device__ __forceinline__ uint64_t fx44(float e) {
+  const float x = e * 4096.0f;
+  const uint32_t hi = (uint32_t)x;
+  const uint32_t lo = (uint32_t)((x - (float)hi) * 4294967296.0f);
+  return ((uint64_t)hi << 32) | lo;
 }
+__device__ __forceinline__ uint64_t wfx(float M, float y) { return fx44(ns_expf(y - M)); }
 
 // The same fixed-point mass through the hardware base-2 exponential: exp2((y - M) log2 e),
 // within a few units in the last place of expf (the rounding of y - M, which both carry,
 // dominates); for the histograms, whose bins only plan the row.
 __device__ __forceinline__ uint64_t wfx_hw(float M, float y) {
-  const uint32_t b = __float_as_uint(__builtin_amdgcn_exp2f((y - M) * 1.4426950408889634f));
-  const int E = (int)(b >> 23);
-  const uint64_t m = (uint64_t)((b & 0x7fffffu) | 0x800000u);
-  if (E >= 106) return m << (E - 106);
-  const int r = 106 - E;
-  return (E > 0 && r < 64) ? (m >> r) : 0ull;
+  return fx44(__builtin_amdgcn_exp2f((y - M) * 1.4426950408889634f));
 }
 
 __device__ __forceinline__ void dc_store_wseg(WideSeg* p, const WideSeg& s) {
