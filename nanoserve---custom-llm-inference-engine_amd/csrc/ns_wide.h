@@ -149,12 +149,14 @@ __host__ __device__ __forceinline__ bool wide_row(float t, int32_t k, int64_t V)
 __device__ __forceinline__ int wgrid(float y) {
   return (int)__builtin_floorf(__builtin_fminf(__builtin_fmaxf(y * WSCALE, -1.0e9f), 1.0e9f));
 }
-// Bin of a scaled logit below the top bin tb (= wgrid of the row's or the segment's max;
-// WBINS: 2048 or more bins below, or not finite).
+// Bin of a scaled logit below the top bin tb (= wgrid of the row's or the segment's max,
+// finite; WBINS: 2048 or more bins below, or not finite).  No branch: -inf and NaN reach a
+// distance past WBINS through wgrid's clamp (fmax returns the number for a NaN operand),
+// +inf a negative one (tb and the clamped index lie within 1e9, so the difference does not
+// overflow); the unsigned comparison sends both to WBINS.
 __device__ __forceinline__ int wbin(int tb, float y) {
-  if (!(y > -__builtin_inff())) return WBINS;
   const int d = tb - wgrid(y);
-  return d < WBINS ? d : WBINS;
+  return (uint32_t)d < (uint32_t)WBINS ? d : WBINS;
 }
 // exp(y - M) in units of 2^-44 (y <= M), truncated: (uint64_t)(e * 2^44) for the float32
 // e = exp(y - M) in [0, 1] (the product with 2^44 is exact, so the integer is the same as
@@ -371,25 +373,33 @@ __device__ __forceinline__ void chunk_y(const WRowCtx& c, const uint4& w, uint32
   constexpr int EPC = T::EPC;
   bool slow = false;
 #pragma unroll
-  for (int e = 0; e < EPC; ++e) {
-    float x = T::elem(w, e);
-    if ((hb >> e) & 1u) {
-      if (x < 0.0f) {
-        x = x * c.pen;
-      } else {
-        const float q0 = x * c.rpen;
-        const float aq = __builtin_fabsf(q0);
-        slow |= !(aq >= c.lo_pen && aq <= 0x1.0p+100f);
-        x = __builtin_fmaf(__builtin_fmaf(-q0, c.pen, x), c.rpen, q0);
+  for (int e = 0; e < EPC; ++e) y[e] = T::elem(w, e);
+  if (hb != 0u) {
+    // history positions in this chunk (few chunks have any): the penalty per element
+#pragma unroll
+    for (int e = 0; e < EPC; ++e) {
+      if ((hb >> e) & 1u) {
+        const float x = y[e];
+        if (x < 0.0f) {
+          y[e] = x * c.pen;
+        } else {
+          const float q0 = x * c.rpen;
+          const float aq = __builtin_fabsf(q0);
+          slow |= !(aq >= c.lo_pen && aq <= 0x1.0p+100f);
+          y[e] = __builtin_fmaf(__builtin_fmaf(-q0, c.pen, x), c.rpen, q0);
+        }
       }
     }
-    if (c.scale) {
+  }
+  if (c.scale) {
+#pragma unroll
+    for (int e = 0; e < EPC; ++e) {
+      const float x = y[e];
       const float q0 = x * c.rdiv;
       const float aq = __builtin_fabsf(q0);
       slow |= !(aq >= c.lo_t && aq <= 0x1.0p+100f);
-      x = __builtin_fmaf(__builtin_fmaf(-q0, c.tdiv, x), c.rdiv, q0);
+      y[e] = __builtin_fmaf(__builtin_fmaf(-q0, c.tdiv, x), c.rdiv, q0);
     }
-    y[e] = x;
   }
   if (ballot(slow) != 0ull) {
     asm volatile("");
@@ -752,9 +762,12 @@ __device__ __forceinline__ void wide_stats_body(const WideParams& P, WideSmem& s
       if (ch * EPC < c.V) chunk_y<T>(c, wide_chunk_fix<T>(c, ch, v[q]), c.pen_on ? T::bits(sm.bm, lc) : 0u, ch * EPC, y);
 #pragma unroll
       for (int e = 0; e < EPC; ++e) {
+        // branch-free: fmax passes over NaN, -inf never raises the maximum, +inf is left out
         nanf |= y[e] != y[e];
         pinf |= y[e] == __builtin_inff();
-        if (y[e] > -__builtin_inff() && y[e] < __builtin_inff()) { ++nfin; mx = __builtin_fmaxf(mx, y[e]); }
+        const bool fin = __builtin_fabsf(y[e]) < __builtin_inff();
+        nfin += fin ? 1 : 0;
+        mx = __builtin_fmaxf(mx, y[e] < __builtin_inff() ? y[e] : -__builtin_inff());
       }
       v[q] = make_uint4(__float_as_uint(y[0]), __float_as_uint(y[1]), __float_as_uint(y[2]), __float_as_uint(y[3 % EPC]));
     }
