@@ -444,7 +444,7 @@ __device__ __forceinline__ void wide_chunks(const WRowCtx& c, int64_t c0, const 
         f(y, ch);
       }
     }
-    gend(g);   // quarter segment g done (chunks g * WGRP * SNT .. + WGRP * SNT of the segment)
+    gend(g);   // step g done (chunks g * WGRP * SNT .. + WGRP * SNT of the segment)
 #pragma unroll
     for (int j = 0; j < WGRP; ++j) cur[j] = nxt[j];
   }
