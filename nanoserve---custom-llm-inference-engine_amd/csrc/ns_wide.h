@@ -1252,17 +1252,23 @@ __global__ __launch_bounds__(NT) void wide_final_kernel(const WideParams P) {
       thr = desc_key_val(block_key_at<EPT>(kk, r, &sm.kb[0], &sm));
     }
     // per element: kept by top-k, its mass, its float32 probability under the top-k set
-    unsigned long long mk = 0ull;
-    int nk_own = 0;
+    // (without top-k every planned element, all finite, is a top-k element, and the top-k
+    // mass is not used: the row-uniform branch skips both block sums)
+    unsigned long long mtopk = 0ull;
+    int32_t n_topk_c = n;
+    if (kon) {
+      unsigned long long mk = 0ull;
+      int nk_own = 0;
   #pragma unroll
-    for (int j = 0; j < EPT; ++j) {
-      if (p0 + j < n) {
-        const float y = desc_key_val(kk[j]);
-        if (y >= thr) { mk += wfx(M, y); ++nk_own; }
+      for (int j = 0; j < EPT; ++j) {
+        if (p0 + j < n) {
+          const float y = desc_key_val(kk[j]);
+          if (y >= thr) { mk += wfx(M, y); ++nk_own; }
+        }
       }
+      mtopk = wsum_u64<NT>(mk, &sm);
+      n_topk_c = wsum_i<NT>(nk_own, &sm);
     }
-    const unsigned long long mtopk = wsum_u64<NT>(mk, &sm);
-    const int32_t n_topk_c = wsum_i<NT>(nk_own, &sm);
     const int32_t n_topk = kon ? n_above + n_topk_c : nfin;
     const uint64_t zk_fx = kon ? mass_above + mtopk : R->mass_tot;
     const double zk = (double)zk_fx * WFX_INV;
@@ -1287,9 +1293,8 @@ __global__ __launch_bounds__(NT) void wide_final_kernel(const WideParams P) {
         qs += (double)qv[j];
       }
       double tot;
+      if (tid == 0) sm.ib[1] = 0x7fffffff;   // ordered before the atomics below by the scan's barriers
       double run = base + wexcl_f64<NT>(qs, &tot, &sm);
-      if (tid == 0) sm.ib[1] = 0x7fffffff;
-      __syncthreads();
       int cross = 0x7fffffff;
   #pragma unroll
       for (int j = 0; j < EPT; ++j) {
@@ -1333,21 +1338,24 @@ __global__ __launch_bounds__(NT) void wide_final_kernel(const WideParams P) {
     const unsigned long long mk2 = wsum_u64<NT>(mkept, &sm);
     const uint64_t zkept_fx = pon ? mass_above + mk2 : zk_fx;
     const double zkept = (double)zkept_fx * WFX_INV;
-    if (tid == 0) {
+    if (wave_id() == 0) {
+      // the segment holding u, from the kept mass per segment (S <= 64: one lane each, a
+      // prefix over the lanes): the first segment with kept mass whose end passes u, else the
+      // last with kept mass
+      const int l = lane_id();
+      const bool act = l < P.S;
+      const uint64_t q = act ? sm.subq[l] : 0ull;
+      const double p = act ? (double)q * WFX_INV * (1.0 / zkept) : 0.0;
+      const double incl = wave_incl_scan(p);
       const double ud = (double)c.u;
-      double run = 0.0, start = 0.0, laststart = 0.0;
-      int s = -1, lastnz = -1;
-      const double rzkept = 1.0 / zkept;
-      // the segment holding u, from the kept mass per segment
-      for (int i = 0; i < P.S; ++i) {
-        const double p = (double)sm.subq[i] * WFX_INV * rzkept;
-        if (sm.subq[i] != 0ull) { lastnz = i; laststart = run; }
-        if (s < 0 && run + p > ud && sm.subq[i] != 0ull) { s = i; start = run; }
-        run += p;
+      const uint64_t nz = ballot(act && q != 0ull);
+      const uint64_t hit = ballot(act && q != 0ull && incl > ud);
+      const int s = hit != 0ull ? __builtin_ctzll(hit) : (nz != 0ull ? 63 - __builtin_clzll(nz) : 0);
+      const double start = read_lane(incl - p, s);
+      if (l == 0) {
+        sm.ib[2] = s;
+        sm.db[0] = start;
       }
-      if (s < 0) { s = lastnz >= 0 ? lastnz : 0; start = laststart; }
-      sm.ib[2] = s;
-      sm.db[0] = start;
     }
     __syncthreads();
     const int s = sm.ib[2];
