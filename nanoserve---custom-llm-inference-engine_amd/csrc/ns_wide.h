@@ -1165,7 +1165,9 @@ __global__ __launch_bounds__(NT) void wide_final_kernel(const WideParams P) {
     const int s = sm.ib[2];
     const double start = sm.db[0], Z = sm.db[3];
     const WKeep keep{-__builtin_inff(), -__builtin_inff(), 0x7fffffff};
-    const int64_t tok = wide_locate<T, NT, 1, SEG_CH>(P, c, (int64_t)s * SEG_CH, start, 1.0 / Z, M, keep, &sm, &fl);
+    // two consecutive float32 chunks per thread a step, as for the planned rows below
+    const int64_t tok =
+        wide_locate<T, NT, EPC == 4 ? 2 : 1, SEG_CH>(P, c, (int64_t)s * SEG_CH, start, 1.0 / Z, M, keep, &sm, &fl);
     if (tid == 0) {
       put_id(P.out_ids, row, tok);
       seg_write_info(P.out_info, row, PATH_WIDE, nfin, -__builtin_inff(), nfin, 0, fl, -__builtin_inff(), -1);
