@@ -905,7 +905,7 @@ __device__ __forceinline__ void wide_stats_body(const WideParams& P, WideSmem& s
 #pragma unroll
     for (int j = 0; j < BPT; ++j) { acc[j] = 0.0; hc[j] = 0u; }
     // two segments' words in flight per step (the loads of a step are issued together)
-    constexpr int SG = 2;
+    constexpr int SG = 4;
     for (int sg0 = 0; sg0 < P.S; sg0 += SG) {
       uint64_t w[SG][BPT];
       double sc[SG];
