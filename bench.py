@@ -378,6 +378,55 @@ def small_batch_leg(L, lib, dev, stream, steps=400, cpu_reps=20):
             "small_batch_b8_cpu_baseline": cpu}
 
 
+def paged_attention_leg(dev, stream, steps=200, seqs=64, ctx=2048):
+    """Paged attention at a decode step of Llama-3.2-3B's layout (24 query heads, 8 KV heads, head_dim
+    128, block_size 16, bf16): ``seqs`` rows of ``ctx`` positions each, physical blocks shuffled, two
+    caches alternated so consecutive calls do not hit the previous call's KV in the last-level cache.
+    Algorithmic bytes: every visible key and value row once (seqs * ctx * 8 heads * 128 * 2 B * 2)
+    plus the query read and the output write."""
+    import torch
+
+    A = _pkg("paged_attention")
+    hq, hkv, d, bs = 24, 8, 128, 16
+    nblk = seqs * ctx // bs
+    g = torch.Generator(device=dev)
+    g.manual_seed(7)
+    caches = [(torch.randn(nblk, bs, hkv, d, device=dev, generator=g, dtype=torch.bfloat16),
+               torch.randn(nblk, bs, hkv, d, device=dev, generator=g, dtype=torch.bfloat16)) for _ in range(2)]
+    bt = torch.randperm(nblk, device=dev, generator=g).to(torch.int32).view(seqs, ctx // bs)
+    q = torch.randn(seqs, hq, d, device=dev, generator=g, dtype=torch.bfloat16)
+    sl = torch.full((seqs,), ctx, dtype=torch.int32, device=dev)
+    ql = torch.ones(seqs, dtype=torch.int32, device=dev)
+    qsl = torch.arange(seqs + 1, dtype=torch.int32, device=dev)
+    out = torch.empty_like(q)
+    ws = torch.empty(max(A.workspace_bytes(seqs, hq, hkv, d, ctx), 1), dtype=torch.uint8, device=dev)
+
+    def call(i):
+        k, v = caches[i % 2]
+        A.paged_attention_hip(q, k, v, bt, sl, qsl, ql, d ** -0.5, bs, max_seq_len=ctx, out=out, workspace=ws,
+                              stream=stream.cuda_stream)
+
+    for i in range(20):
+        call(i)
+    torch.cuda.synchronize()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for i in range(steps):
+        call(i)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    us = e0.elapsed_time(e1) / steps * 1e3
+    nbytes = seqs * ctx * hkv * d * 2 * 2 + 2 * q.numel() * 2
+    gbs = nbytes / (us * 1e-6) / 1e9
+    del caches
+    return {"paged_attention_decode_b%d_ctx%d_us" % (seqs, ctx): us,
+            "paged_attention_decode_algorithmic_bytes": nbytes,
+            "paged_attention_decode_hbm_gbs": gbs,
+            "paged_attention_decode_hbm_frac": gbs / HBM_PEAK_GBS,
+            "paged_attention_decode_tokens_per_s": seqs / (us * 1e-6)}
+
+
 def main(argv=None):
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -392,6 +441,8 @@ def main(argv=None):
                          "reference for HBM byte counters under rocprofv3 --pmc)")
     ap.add_argument("--lm-head-sweep", action="store_true",
                     help="time only the logits producer (lm_head GEMM) over decode batch sizes and exit")
+    ap.add_argument("--paged-attention", action="store_true",
+                    help="time only the paged-attention decode leg (64 rows x 2048 positions) and exit")
     args = ap.parse_args(argv)
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: the sampler's rows are independent and this build runs on a single "
@@ -410,6 +461,9 @@ def main(argv=None):
     torch.cuda.set_device(dev)
     if args.lm_head_sweep:
         lm_head_sweep(L, dev)
+        return 0
+    if args.paged_attention:
+        print(json.dumps(paged_attention_leg(dev, torch.cuda.current_stream(dev))), flush=True)
         return 0
 
     w = W.make_workload(args.config)
@@ -504,6 +558,7 @@ def main(argv=None):
     cpu = cpu_baseline(w, args.cpu_rows, args.cpu_reps) if args.cpu_rows > 0 else None
     small = small_batch_leg(L, lib, dev, stream, cpu_reps=20 if args.cpu_rows > 0 else 0) \
         if args.config == WORKLOAD_CFG else {}
+    attention = paged_attention_leg(dev, stream) if args.config == WORKLOAD_CFG else {}
     if args.config != WORKLOAD_CFG:
         desc = {0: "batch B=8 x V=128256 fp32, t=0.8 top_k=50 top_p=0.9 penalty=1.1, 64 history ids/row",
                 1: "batch B=64 x V=128256 fp32, mixed per-row parameters (greedy and sampled), 512 Zipf ids/row",
@@ -552,7 +607,7 @@ def main(argv=None):
                   "wrapper_inclusive_ms_device_histories": wrap_dev_ms,
                   "wrapper_inclusive_rows_per_s_device_histories": w.batch / (wrap_dev_ms * 1e-3),
                   "wrapper_pipelined_ms_device_histories_async_ids": wrap_pipe_ms,
-                  "kernel_source_sha16": kernel_source_hash(), **floor, **small, **producer},
+                  "kernel_source_sha16": kernel_source_hash(), **floor, **small, **producer, **attention},
     }
     print(json.dumps(line), flush=True)
     return 0

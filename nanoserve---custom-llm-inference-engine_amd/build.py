@@ -17,6 +17,9 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(HERE)
 SRC = os.path.join(HERE, "csrc", "ns_sample.hip")
 OUT = os.path.join(HERE, "libns_sampling.so")
+# paged attention (its own ABI, include/ns_paged_attention.h)
+PA_SRC = os.path.join(HERE, "csrc", "ns_paged_attention.hip")
+PA_OUT = os.path.join(HERE, "libns_paged_attention.so")
 # the benchmark's bandwidth reference (not part of the sampler's ABI)
 PROBE_SRC = os.path.join(HERE, "csrc", "ns_probe.hip")
 PROBE_OUT = os.path.join(HERE, "libns_probe.so")
@@ -52,6 +55,7 @@ def _compile(src: str, out: str, verbose: bool) -> None:
 
 def build(verbose: bool = False) -> str:
     _compile(SRC, OUT, verbose)
+    _compile(PA_SRC, PA_OUT, verbose)
     _compile(PROBE_SRC, PROBE_OUT, verbose)
     return OUT
 

@@ -1,0 +1,525 @@
+// Paged attention for gfx950 (decode and chunked prefill).
+//
+// Follows nanoserve/kernels/paged_attention_triton.py:19-106 (per query token: online softmax over
+// the sequence's KV blocks, GQA by h / NUM_KV_GROUPS, causal cut at the query's own KV position,
+// zero output when no key is visible) and the launcher's index set-up (:109-131: sequence of each
+// query token, its absolute KV position), re-designed for MI355X:
+//
+//  * One 256-thread workgroup per (query token, KV head, KV partition) computes every query head of
+//    that KV head (G = num_heads_q / num_kv_heads of them), so each key and value row is read from
+//    HBM once per query token instead of once per query head as the reference's per-(token, head)
+//    programs do. Decode attention moves ~4 flops per byte: HBM bound, VALU arithmetic.
+//  * Lane layout per wave step: 16 KV positions, 8 lanes per position, each lane holding a
+//    head_dim/8 slice (32 contiguous bytes of a bf16 row at head_dim 128: two 16-byte loads). The
+//    slice's partial dot products are summed across the 8 lanes with ds_swizzle (no LDS traffic).
+//  * Exact two-pass softmax inside a partition: scores (already in log2 units) go to LDS, one max
+//    and one exp2 pass over LDS, then the value pass. Partitions of a long sequence (split-KV,
+//    sized on the host so that the grid holds >= 2048 workgroups) are merged by a second small
+//    launch with the usual max-rescaled sums; a query that fits one partition is written directly.
+//  * The sequence of a query token and its KV position are computed in the kernel (binary search
+//    over query_start_loc), so a call needs no host copy of the batch layout.
+
+#include <hip/hip_runtime.h>
+#include <stdarg.h>
+#include <stdint.h>
+#include <stdio.h>
+#include <string.h>
+
+#include "ns_paged_attention.h"
+
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kWaves = kThreads / 64;
+constexpr int kStepTokens = 16;         // KV positions per wave step (8 lanes each, two rounds)
+constexpr int kMaxPart = 512;           // largest KV partition (LDS score buffer)
+constexpr int kMinPart = 64;
+constexpr int kTargetGroups = 2048;     // workgroups a launch aims for before splitting stops
+constexpr float kLog2e = 1.4426950408889634f;
+
+thread_local char g_err[512];
+
+int fail(const char* fmt, ...) __attribute__((format(printf, 1, 2)));
+int fail(const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof(g_err), fmt, ap);
+  va_end(ap);
+  return 1;
+}
+
+struct PaParams {
+  const void* q;
+  const void* k;
+  const void* v;
+  void* out;
+  const int32_t* bt;
+  const int32_t* seq_lens;
+  const int32_t* qsl;
+  const int32_t* qlens;
+  int32_t* status;
+  float* ws_acc;    // (total_q, Hq, max_parts, D) unnormalised partition outputs
+  float* ws_ml;     // (total_q, Hq, max_parts, 2) partition max (log2 units) and sum
+  int64_t sq_tok, sq_head, sk_blk, sk_tok, sk_head, sv_blk, sv_tok, sv_head, so_tok, so_head, sbt;
+  int32_t num_seqs, hq, hkv, block_size, num_blocks, max_blocks_per_seq, part_tokens, max_parts;
+  float scale_log2;  // scale * log2(e): scores in log2 units, exp2 for the softmax
+};
+
+// ---- element loads / stores -------------------------------------------------------------------
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+struct Bf16 {};
+struct F16 {};
+
+template <typename T> struct Elem;
+template <> struct Elem<float> { static constexpr int bytes = 4; };
+template <> struct Elem<Bf16> { static constexpr int bytes = 2; };
+template <> struct Elem<F16> { static constexpr int bytes = 2; };
+
+// Load N consecutive elements (N * bytes a multiple of 16, 16-byte aligned) as float.
+template <typename T, int N>
+__device__ __forceinline__ void load_row(const void* base, int64_t elem_off, float (&x)[N]) {
+  constexpr int kVec = N * Elem<T>::bytes / 16;
+  const u32x4* p = reinterpret_cast<const u32x4*>(reinterpret_cast<const char*>(base) + elem_off * Elem<T>::bytes);
+  u32x4 w[kVec];
+#pragma unroll
+  for (int i = 0; i < kVec; ++i) w[i] = p[i];
+  const uint32_t* u = reinterpret_cast<const uint32_t*>(w);
+  if constexpr (Elem<T>::bytes == 4) {
+#pragma unroll
+    for (int i = 0; i < N; ++i) x[i] = __uint_as_float(u[i]);
+  } else if constexpr (__is_same(T, Bf16)) {
+#pragma unroll
+    for (int i = 0; i < N / 2; ++i) {
+      x[2 * i] = __uint_as_float(u[i] << 16);
+      x[2 * i + 1] = __uint_as_float(u[i] & 0xFFFF0000u);
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < N / 2; ++i) {
+      const _Float16 lo = __builtin_bit_cast(_Float16, (uint16_t)(u[i] & 0xFFFFu));
+      const _Float16 hi = __builtin_bit_cast(_Float16, (uint16_t)(u[i] >> 16));
+      x[2 * i] = (float)lo;
+      x[2 * i + 1] = (float)hi;
+    }
+  }
+}
+
+template <typename T>
+__device__ __forceinline__ void store_one(void* base, int64_t elem_off, float x) {
+  if constexpr (Elem<T>::bytes == 4) {
+    reinterpret_cast<float*>(base)[elem_off] = x;
+  } else if constexpr (__is_same(T, Bf16)) {
+    // round to nearest even; NaN stays a quiet NaN
+    uint32_t u = __float_as_uint(x);
+    uint16_t h;
+    if ((u & 0x7FFFFFFFu) > 0x7F800000u) {
+      h = (uint16_t)((u >> 16) | 0x40u);
+    } else {
+      u += 0x7FFFu + ((u >> 16) & 1u);
+      h = (uint16_t)(u >> 16);
+    }
+    reinterpret_cast<uint16_t*>(base)[elem_off] = h;
+  } else {
+    reinterpret_cast<_Float16*>(base)[elem_off] = (_Float16)x;
+  }
+}
+
+// ---- lane exchanges ---------------------------------------------------------------------------
+
+// Sum over the 8 lanes of an aligned lane octet: ds_swizzle in bitmask mode (xor 1, 2, 4).
+__device__ __forceinline__ float octet_sum(float x) {
+  x += __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(x), 0x041F));
+  x += __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(x), 0x081F));
+  x += __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(x), 0x101F));
+  return x;
+}
+
+// Sum over the lanes that share lane & 7 (xor 8, 16, 32).
+__device__ __forceinline__ float slot_sum(float x) {
+  x += __shfl_xor(x, 8);
+  x += __shfl_xor(x, 16);
+  x += __shfl_xor(x, 32);
+  return x;
+}
+
+__device__ __forceinline__ float wave_max(float x) {
+#pragma unroll
+  for (int s = 1; s < 64; s <<= 1) x = fmaxf(x, __shfl_xor(x, s));
+  return x;
+}
+
+__device__ __forceinline__ float wave_sum(float x) {
+#pragma unroll
+  for (int s = 1; s < 64; s <<= 1) x += __shfl_xor(x, s);
+  return x;
+}
+
+// ---- batch layout -----------------------------------------------------------------------------
+
+struct QueryPlace {
+  int seq;
+  int kv_len;  // visible KV positions: min(kv_pos + 1, seq_len), at least 0
+};
+
+// Sequence of query token qi: the largest s with query_start_loc[s] <= qi (empty sequences share
+// their start with the next one, so the largest index is the one that owns qi), as the reference's
+// repeat_interleave over query_lens (paged_attention_triton.py:109-112); its KV position
+// seq_len - q_len + (qi - start) (:115-131), the causal and in-sequence cuts (:64-66).
+__device__ __forceinline__ QueryPlace place_query(const PaParams& p, int qi) {
+  int lo = 0, hi = p.num_seqs - 1;
+  while (lo < hi) {
+    const int mid = (lo + hi + 1) >> 1;
+    if (p.qsl[mid] <= qi) lo = mid; else hi = mid - 1;
+  }
+  const int seq_len = p.seq_lens[lo];
+  const int kv_pos = seq_len - p.qlens[lo] + (qi - p.qsl[lo]);
+  int kv_len = kv_pos + 1 < seq_len ? kv_pos + 1 : seq_len;
+  if (kv_len < 0) kv_len = 0;
+  return {lo, kv_len};
+}
+
+// ---- partition kernel ---------------------------------------------------------------------------
+
+template <typename T, int D, int G>
+__global__ __launch_bounds__(kThreads) void pa_partition_kernel(PaParams p) {
+  constexpr int DS = D / 8;  // dims per lane
+  __shared__ float s_score[G * kMaxPart];
+  __shared__ float s_red[kWaves * G * D];
+  __shared__ float s_m[G], s_l[G];
+
+  const int qi = blockIdx.x, kvh = blockIdx.y, part = blockIdx.z;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int slot = lane >> 3;  // position within a half step
+  const int dl = lane & 7;     // dim slice
+  const QueryPlace qp = place_query(p, qi);
+  const int n_parts = (qp.kv_len + p.part_tokens - 1) / p.part_tokens;
+
+  if (part == 0 && n_parts > p.max_parts && threadIdx.x == 0 && p.status)
+    atomicOr(p.status, NS_PA_STATUS_SEQ_TOO_LONG);
+  if (part >= n_parts) {
+    if (part == 0) {  // no visible key: zeros (the reference's l == 0 guard, :103-104)
+      for (int i = threadIdx.x; i < G * D; i += kThreads)
+        store_one<T>(p.out, (int64_t)qi * p.so_tok + (int64_t)(kvh * G + i / D) * p.so_head + i % D, 0.f);
+    }
+    return;
+  }
+  const int t0 = part * p.part_tokens;
+  const int t1 = min(qp.kv_len, t0 + p.part_tokens);
+  const int n = t1 - t0;
+  const int32_t* bt_row = p.bt + (int64_t)qp.seq * p.sbt;
+
+  // query slices, pre-scaled into log2 units
+  float qv[G][DS];
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    load_row<T, DS>(p.q, (int64_t)qi * p.sq_tok + (int64_t)(kvh * G + g) * p.sq_head + dl * DS, qv[g]);
+#pragma unroll
+    for (int i = 0; i < DS; ++i) qv[g][i] *= p.scale_log2;
+  }
+
+  // pass 1: scores -> LDS (wave w takes steps w, w + 4, ...)
+  bool bad = false;
+  for (int base = wave * kStepTokens; base < n; base += kWaves * kStepTokens) {
+    float kx[2][DS];
+    bool ok[2];
+#pragma unroll
+    for (int r = 0; r < 2; ++r) {
+      const int j = base + r * 8 + slot;
+      const int t = t0 + j;
+      ok[r] = false;
+      if (j < n) {
+        const int bi = t / p.block_size;
+        const int blk = bi < p.max_blocks_per_seq ? bt_row[bi] : -1;
+        if (blk >= 0 && blk < p.num_blocks) {
+          ok[r] = true;
+          load_row<T, DS>(p.k, (int64_t)blk * p.sk_blk + (int64_t)(t % p.block_size) * p.sk_tok +
+                                   (int64_t)kvh * p.sk_head + dl * DS, kx[r]);
+        } else {
+          bad = true;
+        }
+      }
+      if (!ok[r]) {
+#pragma unroll
+        for (int i = 0; i < DS; ++i) kx[r][i] = 0.f;
+      }
+    }
+#pragma unroll
+    for (int r = 0; r < 2; ++r) {
+      const int j = base + r * 8 + slot;
+#pragma unroll
+      for (int g = 0; g < G; ++g) {
+        float s = 0.f;
+#pragma unroll
+        for (int i = 0; i < DS; ++i) s = fmaf(qv[g][i], kx[r][i], s);
+        s = octet_sum(s);
+        if (dl == g && j < n) s_score[g * kMaxPart + j] = ok[r] ? s : -INFINITY;
+      }
+    }
+  }
+  if (bad && p.status) atomicOr(p.status, NS_PA_STATUS_BAD_BLOCK);
+  __syncthreads();
+
+  // pass 2: per-head max and exp2, in place (wave w takes heads w, w + 4)
+  for (int g = wave; g < G; g += kWaves) {
+    float m = -INFINITY;
+    for (int j = lane; j < n; j += 64) m = fmaxf(m, s_score[g * kMaxPart + j]);
+    m = wave_max(m);
+    float l = 0.f;
+    for (int j = lane; j < n; j += 64) {
+      const float e = m == -INFINITY ? 0.f : exp2f(s_score[g * kMaxPart + j] - m);
+      s_score[g * kMaxPart + j] = e;
+      l += e;
+    }
+    l = wave_sum(l);
+    if (lane == 0) {
+      s_m[g] = m;
+      s_l[g] = l;
+    }
+  }
+  __syncthreads();
+
+  // pass 3: probability-weighted values
+  float acc[G][DS];
+#pragma unroll
+  for (int g = 0; g < G; ++g)
+#pragma unroll
+    for (int i = 0; i < DS; ++i) acc[g][i] = 0.f;
+  for (int base = wave * kStepTokens; base < n; base += kWaves * kStepTokens) {
+    float vx[2][DS];
+    bool ok[2];
+#pragma unroll
+    for (int r = 0; r < 2; ++r) {
+      const int j = base + r * 8 + slot;
+      const int t = t0 + j;
+      ok[r] = false;
+      if (j < n) {
+        const int bi = t / p.block_size;
+        const int blk = bi < p.max_blocks_per_seq ? bt_row[bi] : -1;
+        if (blk >= 0 && blk < p.num_blocks) {
+          ok[r] = true;
+          load_row<T, DS>(p.v, (int64_t)blk * p.sv_blk + (int64_t)(t % p.block_size) * p.sv_tok +
+                                   (int64_t)kvh * p.sv_head + dl * DS, vx[r]);
+        }
+      }
+    }
+#pragma unroll
+    for (int r = 0; r < 2; ++r) {
+      if (!ok[r]) continue;
+      const int j = base + r * 8 + slot;
+#pragma unroll
+      for (int g = 0; g < G; ++g) {
+        const float w = s_score[g * kMaxPart + j];
+#pragma unroll
+        for (int i = 0; i < DS; ++i) acc[g][i] = fmaf(w, vx[r][i], acc[g][i]);
+      }
+    }
+  }
+  // sum the 8 position slots of the wave, then the waves through LDS
+#pragma unroll
+  for (int g = 0; g < G; ++g)
+#pragma unroll
+    for (int i = 0; i < DS; ++i) acc[g][i] = slot_sum(acc[g][i]);
+  if (slot == 0) {
+#pragma unroll
+    for (int g = 0; g < G; ++g)
+#pragma unroll
+      for (int i = 0; i < DS; ++i) s_red[(wave * G + g) * D + dl * DS + i] = acc[g][i];
+  }
+  __syncthreads();
+
+  const bool direct = n_parts == 1;
+  for (int e = threadIdx.x; e < G * D; e += kThreads) {
+    const int g = e / D, d = e % D;
+    float o = 0.f;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) o += s_red[(w * G + g) * D + d];
+    const int h = kvh * G + g;
+    if (direct) {
+      const float l = s_l[g];
+      store_one<T>(p.out, (int64_t)qi * p.so_tok + (int64_t)h * p.so_head + d, l > 0.f ? o / l : 0.f);
+    } else if (p.ws_acc && part < p.max_parts) {
+      const int64_t slot_idx = ((int64_t)qi * p.hq + h) * p.max_parts + part;
+      p.ws_acc[slot_idx * D + d] = o;
+      if (d == 0) {
+        p.ws_ml[slot_idx * 2] = s_m[g];
+        p.ws_ml[slot_idx * 2 + 1] = s_l[g];
+      }
+    }
+  }
+}
+
+// ---- partition merge --------------------------------------------------------------------------
+
+// One workgroup of D threads per (query token, query head) whose query spans several partitions.
+template <typename T, int D>
+__global__ __launch_bounds__(128) void pa_merge_kernel(PaParams p) {
+  const int qi = blockIdx.x, h = blockIdx.y, d = threadIdx.x;
+  const QueryPlace qp = place_query(p, qi);
+  int n_parts = (qp.kv_len + p.part_tokens - 1) / p.part_tokens;
+  if (n_parts <= 1 || d >= D) return;
+  if (n_parts > p.max_parts) n_parts = p.max_parts;
+  const int64_t base = ((int64_t)qi * p.hq + h) * p.max_parts;
+  float m = -INFINITY;
+  for (int i = 0; i < n_parts; ++i) m = fmaxf(m, p.ws_ml[(base + i) * 2]);
+  float l = 0.f, o = 0.f;
+  if (m != -INFINITY) {
+    for (int i = 0; i < n_parts; ++i) {
+      const float mi = p.ws_ml[(base + i) * 2];
+      const float w = mi == -INFINITY ? 0.f : exp2f(mi - m);
+      l = fmaf(w, p.ws_ml[(base + i) * 2 + 1], l);
+      o = fmaf(w, p.ws_acc[(base + i) * D + d], o);
+    }
+  }
+  store_one<T>(p.out, (int64_t)qi * p.so_tok + (int64_t)h * p.so_head + d, l > 0.f ? o / l : 0.f);
+}
+
+// ---- host side ---------------------------------------------------------------------------------
+
+int part_tokens_for(int32_t total_q, int32_t hkv, int32_t max_seq_len) {
+  int part = kMaxPart;
+  while (part > kMinPart) {
+    const int64_t parts = ((int64_t)max_seq_len + part - 1) / part;
+    if ((int64_t)total_q * hkv * parts >= kTargetGroups) break;
+    part >>= 1;
+  }
+  return part;
+}
+
+int check_sizes(int32_t total_q, int32_t hq, int32_t hkv, int32_t head_dim, int32_t max_seq_len) {
+  if (total_q < 0) return fail("total_q must be >= 0 (got %d)", total_q);
+  if (hq <= 0 || hkv <= 0 || hq % hkv != 0)
+    return fail("num_heads_q (%d) must be a positive multiple of num_kv_heads (%d)", hq, hkv);
+  const int g = hq / hkv;
+  if (g != 1 && g != 2 && g != 3 && g != 4 && g != 8)
+    return fail("query heads per KV head must be 1, 2, 3, 4 or 8 (got %d)", g);
+  if (head_dim != 64 && head_dim != 128) return fail("head_dim must be 64 or 128 (got %d)", head_dim);
+  if (max_seq_len < 0) return fail("max_seq_len must be >= 0 (got %d)", max_seq_len);
+  if (hkv > 65535 || hq > 65535) return fail("too many heads (grid y is at most 65535)");
+  return 0;
+}
+
+uint64_t workspace_bytes(int32_t total_q, int32_t hq, int32_t hkv, int32_t head_dim, int32_t max_seq_len) {
+  const int part = part_tokens_for(total_q, hkv, max_seq_len);
+  const int64_t max_parts = ((int64_t)max_seq_len + part - 1) / part;
+  if (max_parts <= 1) return 0;
+  return (uint64_t)total_q * hq * max_parts * (head_dim + 2) * sizeof(float);
+}
+
+template <typename T, int D, int G>
+void launch(const PaParams& p, int total_q, hipStream_t stream) {
+  dim3 grid(total_q, p.hkv, p.max_parts > 0 ? p.max_parts : 1);
+  hipLaunchKernelGGL((pa_partition_kernel<T, D, G>), grid, dim3(kThreads), 0, stream, p);
+  if (p.max_parts > 1)
+    hipLaunchKernelGGL((pa_merge_kernel<T, D>), dim3(total_q, p.hq), dim3(128), 0, stream, p);
+}
+
+template <typename T, int D>
+void launch_g(const PaParams& p, int total_q, int g, hipStream_t stream) {
+  switch (g) {
+    case 1: launch<T, D, 1>(p, total_q, stream); break;
+    case 2: launch<T, D, 2>(p, total_q, stream); break;
+    case 3: launch<T, D, 3>(p, total_q, stream); break;
+    case 4: launch<T, D, 4>(p, total_q, stream); break;
+    default: launch<T, D, 8>(p, total_q, stream); break;
+  }
+}
+
+template <typename T>
+void launch_d(const PaParams& p, int total_q, int d, int g, hipStream_t stream) {
+  if (d == 64) launch_g<T, 64>(p, total_q, g, stream);
+  else launch_g<T, 128>(p, total_q, g, stream);
+}
+
+}  // namespace
+
+extern "C" {
+
+int ns_pa_abi_version(void) { return NS_PA_ABI_VERSION; }
+
+const char* ns_pa_last_error(void) { return g_err; }
+
+int ns_paged_attention_workspace_bytes(int32_t total_q, int32_t num_heads_q, int32_t num_kv_heads,
+                                       int32_t head_dim, int32_t max_seq_len, uint64_t* bytes) {
+  if (!bytes) return fail("bytes is NULL");
+  if (check_sizes(total_q, num_heads_q, num_kv_heads, head_dim, max_seq_len)) return 1;
+  *bytes = workspace_bytes(total_q, num_heads_q, num_kv_heads, head_dim, max_seq_len);
+  return 0;
+}
+
+int ns_paged_attention(const ns_paged_attn_args* a, hipStream_t stream) {
+  if (!a) return fail("args is NULL");
+  if (check_sizes(a->total_q, a->num_heads_q, a->num_kv_heads, a->head_dim, a->max_seq_len)) return 1;
+  if (a->dtype != NS_PA_DTYPE_F32 && a->dtype != NS_PA_DTYPE_BF16 && a->dtype != NS_PA_DTYPE_F16)
+    return fail("dtype must be NS_PA_DTYPE_F32, _BF16 or _F16 (got %d)", a->dtype);
+  if (a->total_q == 0) return 0;
+  if (a->num_seqs <= 0) return fail("num_seqs must be > 0 when total_q > 0 (got %d)", a->num_seqs);
+  if (a->block_size <= 0) return fail("block_size must be > 0 (got %d)", a->block_size);
+  if (a->num_blocks <= 0) return fail("num_blocks must be > 0 (got %d)", a->num_blocks);
+  if (!a->query || !a->k_cache || !a->v_cache || !a->out || !a->block_tables || !a->seq_lens ||
+      !a->query_start_loc || !a->query_lens)
+    return fail("a tensor pointer is NULL");
+  const int esz = a->dtype == NS_PA_DTYPE_F32 ? 4 : 2;
+  // 16-byte vector loads of each lane's head_dim/8 slice: rows and strides 16-byte aligned
+  const int64_t strides[] = {a->stride_q_token, a->stride_q_head, a->stride_k_block, a->stride_k_token,
+                             a->stride_k_head, a->stride_v_block, a->stride_v_token, a->stride_v_head};
+  for (int64_t s : strides)
+    if ((s * esz) % 16 != 0) return fail("query/cache strides must be multiples of 16 bytes");
+  if (((uintptr_t)a->query | (uintptr_t)a->k_cache | (uintptr_t)a->v_cache) % 16 != 0)
+    return fail("query and cache pointers must be 16-byte aligned");
+  if (a->stride_bt_seq < 0) return fail("stride_bt_seq must be >= 0");
+  if (a->max_blocks_per_seq < 0) return fail("max_blocks_per_seq must be >= 0");
+  const uint64_t need = workspace_bytes(a->total_q, a->num_heads_q, a->num_kv_heads, a->head_dim, a->max_seq_len);
+  if (need > 0 && (!a->workspace || a->workspace_bytes < need))
+    return fail("workspace of %llu bytes needed (got %llu)", (unsigned long long)need,
+                (unsigned long long)a->workspace_bytes);
+  const int part = part_tokens_for(a->total_q, a->num_kv_heads, a->max_seq_len);
+  const int64_t max_parts = ((int64_t)a->max_seq_len + part - 1) / part;
+  if (max_parts > 65535) return fail("max_seq_len too large");
+
+  PaParams p;
+  p.q = a->query;
+  p.k = a->k_cache;
+  p.v = a->v_cache;
+  p.out = a->out;
+  p.bt = a->block_tables;
+  p.seq_lens = a->seq_lens;
+  p.qsl = a->query_start_loc;
+  p.qlens = a->query_lens;
+  p.status = a->status;
+  p.ws_acc = reinterpret_cast<float*>(a->workspace);
+  p.ws_ml = need ? p.ws_acc + (uint64_t)a->total_q * a->num_heads_q * max_parts * a->head_dim : nullptr;
+  p.sq_tok = a->stride_q_token;
+  p.sq_head = a->stride_q_head;
+  p.sk_blk = a->stride_k_block;
+  p.sk_tok = a->stride_k_token;
+  p.sk_head = a->stride_k_head;
+  p.sv_blk = a->stride_v_block;
+  p.sv_tok = a->stride_v_token;
+  p.sv_head = a->stride_v_head;
+  p.so_tok = a->stride_o_token;
+  p.so_head = a->stride_o_head;
+  p.sbt = a->stride_bt_seq;
+  p.num_seqs = a->num_seqs;
+  p.hq = a->num_heads_q;
+  p.hkv = a->num_kv_heads;
+  p.block_size = a->block_size;
+  p.num_blocks = a->num_blocks;
+  p.max_blocks_per_seq = a->max_blocks_per_seq;
+  p.part_tokens = part;
+  p.max_parts = (int32_t)max_parts;
+  p.scale_log2 = a->scale * kLog2e;
+
+  const int g = a->num_heads_q / a->num_kv_heads;
+  switch (a->dtype) {
+    case NS_PA_DTYPE_F32: launch_d<float>(p, a->total_q, a->head_dim, g, stream); break;
+    case NS_PA_DTYPE_BF16: launch_d<Bf16>(p, a->total_q, a->head_dim, g, stream); break;
+    default: launch_d<F16>(p, a->total_q, a->head_dim, g, stream); break;
+  }
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return fail("kernel launch failed: %s", hipGetErrorString(e));
+  return 0;
+}
+
+}  // extern "C"

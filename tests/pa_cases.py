@@ -1,0 +1,83 @@
+"""Seeded inputs for the paged-attention tests: paged KV caches with shuffled physical blocks,
+block tables, and the batch layout the reference's engine builds (query_start_loc, query_lens)."""
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import torch
+
+DECODE_LLAMA32_3B = dict(hq=24, hkv=8, d=128, block_size=16)
+
+
+def make_case(seed, seq_lens, query_lens, hq=24, hkv=8, d=128, block_size=16, dtype=torch.bfloat16,
+              spare_blocks=5, spare_cols=2, qkv_view=False):
+    """CPU tensors of a paged-attention call; values exactly representable in ``dtype``."""
+    rng = np.random.default_rng(seed)
+    seq_lens = [int(x) for x in seq_lens]
+    query_lens = [int(x) for x in query_lens]
+    num_seqs = len(seq_lens)
+    per_seq = [math.ceil(x / block_size) for x in seq_lens]
+    cols = max(per_seq + [1]) + spare_cols
+    num_blocks = sum(per_seq) + spare_blocks
+    perm = rng.permutation(num_blocks)
+    bt = np.zeros((num_seqs, cols), dtype=np.int32)
+    at = 0
+    for s, n in enumerate(per_seq):
+        bt[s, :n] = perm[at:at + n]
+        at += n
+    total_q = sum(query_lens)
+    qsl = np.zeros(num_seqs + 1, dtype=np.int32)
+    qsl[1:] = np.cumsum(query_lens)
+    k = torch.from_numpy(rng.standard_normal((num_blocks, block_size, hkv, d), dtype=np.float32)).to(dtype)
+    v = torch.from_numpy(rng.standard_normal((num_blocks, block_size, hkv, d), dtype=np.float32)).to(dtype)
+    if qkv_view:
+        # the layout the reference's Attention.forward hands over: a view into the fused QKV output
+        qkv = torch.from_numpy(rng.standard_normal((total_q, (hq + 2 * hkv) * d), dtype=np.float32)).to(dtype)
+        q = qkv[:, :hq * d].view(total_q, hq, d)
+    else:
+        q = torch.from_numpy(rng.standard_normal((total_q, hq, d), dtype=np.float32)).to(dtype)
+    return dict(query=q, k_cache=k, v_cache=v, block_tables=torch.from_numpy(bt),
+                seq_lens=torch.tensor(seq_lens, dtype=torch.int32), query_start_loc=torch.from_numpy(qsl),
+                query_lens=torch.tensor(query_lens, dtype=torch.int32), scale=1.0 / math.sqrt(d),
+                block_size=block_size)
+
+
+def oracle_args(case):
+    """The case as float64/int numpy arrays for the oracle."""
+    out = {}
+    for key, val in case.items():
+        out[key] = val.double().numpy() if isinstance(val, torch.Tensor) and val.is_floating_point() else (
+            val.numpy() if isinstance(val, torch.Tensor) else val)
+    return out
+
+
+def to_device(case, device):
+    out = {}
+    for key, val in case.items():
+        if isinstance(val, torch.Tensor):
+            if key == "query" and not val.is_contiguous():
+                # keep the strided view: move its base and re-take the view on the device
+                base = val._base if val._base is not None else val
+                dev_base = base.to(device)
+                out[key] = dev_base.as_strided(val.shape, val.stride(), val.storage_offset())
+            else:
+                out[key] = val.to(device)
+        else:
+            out[key] = val
+    return out
+
+
+# output tolerance per dtype: the kernels compute in float32 and round the output once
+TOL = {torch.float32: (1e-5, 1e-4), torch.float16: (1e-4, 2.0 ** -9), torch.bfloat16: (1e-4, 2.0 ** -7)}
+
+
+def assert_close_to_oracle(out, ref, dtype):
+    atol, rtol = TOL[dtype]
+    got = out.double().cpu().numpy()
+    err = np.abs(got - ref)
+    bound = atol + rtol * np.abs(ref)
+    bad = err > bound
+    assert not bad.any(), (
+        f"{int(bad.sum())} of {bad.size} outputs outside atol {atol} + rtol {rtol}; worst |err| "
+        f"{float(err.max()):.3g} at {np.unravel_index(int(np.argmax(err - bound)), err.shape)}")

@@ -1,0 +1,115 @@
+"""GPU parity of the HIP paged-attention kernels (through the C-ABI) against the CPU oracle
+(float64 restatement of nanoserve/kernels/paged_attention_triton.py:19-131). Tolerances: float32
+output atol 1e-5 + rtol 1e-4; float16 atol 1e-4 + rtol 2^-9; bfloat16 atol 1e-4 + rtol 2^-7 (one
+rounding of the float32 result to the output type, plus float32 arithmetic)."""
+import numpy as np
+import pytest
+import torch
+
+from conftest import pkg
+from pa_cases import assert_close_to_oracle, make_case, oracle_args, to_device
+from oracle import paged_attention_oracle as PA
+
+pytestmark = pytest.mark.gpu
+A = pkg("paged_attention")
+
+
+def run(case, device, **kw):
+    c = to_device(case, device)
+    print(f"paged attention: q {tuple(case['query'].shape)} {case['query'].dtype} seqs {case['seq_lens'].tolist()} "
+          f"q_lens {case['query_lens'].tolist()}", flush=True)
+    out = A.paged_attention_hip(c["query"], c["k_cache"], c["v_cache"], c["block_tables"], c["seq_lens"],
+                                c["query_start_loc"], c["query_lens"], c["scale"], c["block_size"], **kw)
+    torch.cuda.synchronize()
+    return out
+
+
+def check(case, device, **kw):
+    out = run(case, device, **kw)
+    ref = PA.paged_attention(**oracle_args(case))
+    assert_close_to_oracle(out, ref, case["query"].dtype)
+    return out
+
+
+def test_decode_llama32_3b_split_partitions(device):
+    # 8 decode rows, lengths around block edges and long enough to be split and merged
+    case = make_case(10, [1, 15, 16, 17, 100, 513, 1500, 4000], [1] * 8)
+    check(case, device)
+
+
+def test_decode_batch_64_ctx_2048(device):
+    # the benchmark's shape: 64 decode rows of 2048 positions, Llama-3.2-3B heads, bf16
+    case = make_case(11, [2048] * 64, [1] * 64, spare_blocks=0, spare_cols=0)
+    check(case, device)
+
+
+def test_chunked_prefill_mix(device):
+    # full prefill (causal), decode, chunked prefill, an empty sequence, a short full prefill
+    case = make_case(12, [37, 64, 300, 20, 9], [37, 1, 45, 0, 9])
+    check(case, device)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("hq,hkv,d", [(8, 8, 128), (16, 8, 64), (32, 8, 128), (32, 4, 64), (24, 8, 64)])
+def test_head_layouts_and_dtypes(device, dtype, hq, hkv, d):
+    case = make_case(13 + hq + d, [70, 1, 260, 33], [1, 1, 30, 33], hq=hq, hkv=hkv, d=d, block_size=16,
+                     dtype=dtype)
+    check(case, device)
+
+
+@pytest.mark.parametrize("block_size", [1, 8, 32])
+def test_block_sizes(device, block_size):
+    case = make_case(20 + block_size, [45, 130, 7], [1, 3, 7], block_size=block_size)
+    check(case, device)
+
+
+def test_strided_query_view_of_fused_qkv(device):
+    # query as the view into the fused QKV output that Attention.forward passes
+    case = make_case(30, [50, 200], [50, 1], qkv_view=True)
+    assert not case["query"].is_contiguous()
+    check(case, device)
+
+
+def test_zero_visible_keys_gives_zeros(device):
+    # a sequence of length 0 holding one query token (malformed batch): the reference's l == 0 guard
+    case = make_case(31, [0, 20], [1, 1])
+    out = check(case, device)
+    assert torch.count_nonzero(out[0].float()).item() == 0
+
+
+def test_long_rows_through_merge_and_repeat_bit_exact(device):
+    case = make_case(32, [8192, 3], [1, 1], hq=32, hkv=8, d=128)
+    a = check(case, device)
+    b = run(case, device)
+    assert torch.equal(a, b)
+
+
+def test_status_flags_bad_block_and_short_max_seq_len(device):
+    case = make_case(33, [40, 40], [1, 1])
+    nb = case["k_cache"].shape[0]
+    bad = {k: (v.clone() if isinstance(v, torch.Tensor) else v) for k, v in case.items()}
+    bad["block_tables"][0, 1] = nb + 7  # out of the cache: the kernel skips those keys and flags it
+    status = torch.zeros(1, dtype=torch.int32, device=device)
+    out = run(bad, device, status=status)
+    assert status.item() & A.STATUS_BAD_BLOCK
+    ref = PA.paged_attention(**oracle_args(case))
+    # the other sequence is untouched by the bad entry
+    assert_close_to_oracle(out[1:], ref[1:], case["query"].dtype)
+    status.zero_()
+    run(case, device, status=status)
+    assert status.item() == 0
+    # a max_seq_len below a sequence's length: flagged when the grid cannot cover that sequence
+    # (400 positions need 7 partitions of 64, the grid sized for 16 positions holds one)
+    long_case = make_case(36, [400, 40], [1, 1])
+    run(long_case, device, status=status, max_seq_len=16)
+    assert status.item() & A.STATUS_SEQ_TOO_LONG
+
+
+def test_empty_batch_and_argument_errors(device):
+    case = make_case(34, [5], [0])
+    out = run(case, device)
+    assert out.shape[0] == 0
+    c = to_device(make_case(35, [5], [1]), device)
+    with pytest.raises(A.PagedAttentionError, match="block_size"):
+        A.paged_attention_hip(c["query"], c["k_cache"], c["v_cache"], c["block_tables"], c["seq_lens"],
+                              c["query_start_loc"], c["query_lens"], c["scale"], 8)

@@ -1,0 +1,80 @@
+"""CPU checks of the paged-attention boundary: the library loads, exports what
+include/ns_paged_attention.h declares, its argument struct matches the header, and it refuses
+invalid arguments before touching a GPU."""
+import ctypes
+import os
+import re
+
+import pytest
+
+from conftest import ROOT, pkg
+
+PA = pkg("paged_attention")
+HEADER = os.path.join(ROOT, "include", "ns_paged_attention.h")
+
+
+def header_functions():
+    txt = open(HEADER).read()
+    return sorted(set(re.findall(r"^\s*(?:int|const char\*)\s+(ns_\w+)\s*\(", txt, flags=re.M)))
+
+
+def built():
+    if not os.path.exists(PA.LIB_PATH):
+        pytest.skip("library not built (run __graft_entry__.build())")
+
+
+def test_header_declares_the_binding_exports():
+    assert header_functions() == sorted(PA.EXPORTS)
+
+
+def test_library_exports_every_header_symbol():
+    built()
+    lib = ctypes.CDLL(PA.LIB_PATH)
+    for name in header_functions():
+        assert hasattr(lib, name), name
+    assert PA.load().ns_pa_abi_version() == PA.ABI_VERSION
+
+
+def test_struct_layout_matches_header():
+    txt = open(HEADER).read()
+    body = txt[txt.index("typedef struct ns_paged_attn_args"):txt.index("} ns_paged_attn_args;")]
+    names = []
+    for decl in re.findall(r"^\s*([^/{}]+?);", body, flags=re.M):
+        names += [n.strip().lstrip("*") for n in re.sub(r"^.*?\b(\w+)\s*(,|$)", r"\1\2", decl, count=1).split(",")]
+    assert names == [f[0] for f in PA.NsPagedAttnArgs._fields_]
+    assert ctypes.sizeof(PA.NsPagedAttnArgs) == 224
+
+
+def test_workspace_sizes():
+    built()
+    # a grid already wide enough (256 queries x 8 KV heads at one 512-position partition): no workspace
+    assert PA.workspace_bytes(256, 24, 8, 128, 512) == 0
+    # 64 decode rows of 512 positions: 512 workgroups, so split into four 128-position partitions
+    assert PA.workspace_bytes(64, 24, 8, 128, 512) == 64 * 24 * 4 * (128 + 2) * 4
+    # a single long decode row is split into 64-position partitions: (D + 2) floats per partition and head
+    assert PA.workspace_bytes(1, 24, 8, 128, 8192) == 1 * 24 * (8192 // 64) * (128 + 2) * 4
+    with pytest.raises(PA.PagedAttentionError, match="multiple"):
+        PA.workspace_bytes(1, 24, 7, 128, 16)
+    with pytest.raises(PA.PagedAttentionError, match="head_dim"):
+        PA.workspace_bytes(1, 24, 8, 96, 16)
+    with pytest.raises(PA.PagedAttentionError, match="1, 2, 3, 4 or 8"):
+        PA.workspace_bytes(1, 40, 8, 128, 16)
+
+
+def test_argument_errors_without_a_gpu():
+    built()
+    lib = PA.load()
+    a = PA.NsPagedAttnArgs()
+    a.total_q, a.num_seqs, a.num_heads_q, a.num_kv_heads, a.head_dim = 1, 1, 24, 8, 128
+    a.block_size, a.num_blocks, a.max_seq_len, a.dtype = 16, 4, 16, PA.NS_PA_DTYPE_BF16
+    assert lib.ns_paged_attention(ctypes.byref(a), None) != 0
+    assert b"NULL" in lib.ns_pa_last_error()
+    a.dtype = 7
+    assert lib.ns_paged_attention(ctypes.byref(a), None) != 0
+    assert b"dtype" in lib.ns_pa_last_error()
+    a.dtype, a.block_size = PA.NS_PA_DTYPE_BF16, 0
+    assert lib.ns_paged_attention(ctypes.byref(a), None) != 0
+    assert b"block_size" in lib.ns_pa_last_error()
+    # an empty batch is a no-op
+    a.total_q = 0
+    assert lib.ns_paged_attention(ctypes.byref(a), None) == 0
