@@ -252,7 +252,7 @@ def kernel_source_hash():
 
     h = hashlib.sha256()
     for name in sorted(os.listdir(CSRC)):
-        if name.endswith((".hip", ".h")) and name != "ns_probe.hip":
+        if name.endswith((".hip", ".h")) and name not in ("ns_probe.hip", "ns_paged_attention.hip"):
             with open(os.path.join(CSRC, name), "rb") as f:
                 h.update(name.encode() + b"\0" + f.read())
     return h.hexdigest()[:16]
@@ -378,6 +378,19 @@ def small_batch_leg(L, lib, dev, stream, steps=400, cpu_reps=20):
             "small_batch_b8_cpu_baseline": cpu}
 
 
+def copy_reference(dev, mb):
+    """4 plain device copies of ``mb`` MiB: a known-size reference for HBM byte counters."""
+    import torch
+
+    n = mb * (1 << 20) // 4
+    src = torch.ones(n, dtype=torch.float32, device=dev)
+    dst = torch.empty_like(src)
+    for _ in range(4):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    del src, dst
+
+
 def paged_attention_leg(dev, stream, steps=200, seqs=64, ctx=2048):
     """Paged attention at a decode step of Llama-3.2-3B's layout (24 query heads, 8 KV heads, head_dim
     128, block_size 16, bf16): ``seqs`` rows of ``ctx`` positions each, physical blocks shuffled, two
@@ -463,7 +476,9 @@ def main(argv=None):
         lm_head_sweep(L, dev)
         return 0
     if args.paged_attention:
-        print(json.dumps(paged_attention_leg(dev, torch.cuda.current_stream(dev))), flush=True)
+        print(json.dumps(paged_attention_leg(dev, torch.cuda.current_stream(dev), steps=args.steps)), flush=True)
+        if args.copy_mb > 0:
+            copy_reference(dev, args.copy_mb)
         return 0
 
     w = W.make_workload(args.config)
@@ -547,13 +562,7 @@ def main(argv=None):
         "kernel_over_read_floor": ms_per_step * 1e3 / floor_us}
 
     if args.copy_mb > 0:
-        n = args.copy_mb * (1 << 20) // 4
-        src = torch.ones(n, dtype=torch.float32, device=dev)
-        dst = torch.empty_like(src)
-        for _ in range(4):
-            dst.copy_(src)
-        torch.cuda.synchronize()
-        del src, dst
+        copy_reference(dev, args.copy_mb)
 
     cpu = cpu_baseline(w, args.cpu_rows, args.cpu_reps) if args.cpu_rows > 0 else None
     small = small_batch_leg(L, lib, dev, stream, cpu_reps=20 if args.cpu_rows > 0 else 0) \

@@ -31,7 +31,8 @@ namespace {
 
 constexpr int kThreads = 256;
 constexpr int kWaves = kThreads / 64;
-constexpr int kStepTokens = 16;         // KV positions per wave step (8 lanes each, two rounds)
+constexpr int kSub = 2;                 // KV positions per lane per batch (8 lanes per position)
+constexpr int kBatch = 8 * kSub;        // KV positions per wave batch
 constexpr int kMaxPart = 512;           // largest KV partition (LDS score buffer)
 constexpr int kMinPart = 64;
 constexpr int kTargetGroups = 2048;     // workgroups a launch aims for before splitting stops
@@ -77,15 +78,24 @@ template <> struct Elem<float> { static constexpr int bytes = 4; };
 template <> struct Elem<Bf16> { static constexpr int bytes = 2; };
 template <> struct Elem<F16> { static constexpr int bytes = 2; };
 
-// Load N consecutive elements (N * bytes a multiple of 16, 16-byte aligned) as float.
+// N consecutive elements (N * bytes a multiple of 16, 16-byte aligned) as raw 16-byte words ...
 template <typename T, int N>
-__device__ __forceinline__ void load_row(const void* base, int64_t elem_off, float (&x)[N]) {
-  constexpr int kVec = N * Elem<T>::bytes / 16;
-  const u32x4* p = reinterpret_cast<const u32x4*>(reinterpret_cast<const char*>(base) + elem_off * Elem<T>::bytes);
+struct Raw {
+  static constexpr int kVec = N * Elem<T>::bytes / 16;
   u32x4 w[kVec];
+};
+
+template <typename T, int N>
+__device__ __forceinline__ void load_raw(const void* base, int64_t elem_off, Raw<T, N>& r) {
+  const u32x4* p = reinterpret_cast<const u32x4*>(reinterpret_cast<const char*>(base) + elem_off * Elem<T>::bytes);
 #pragma unroll
-  for (int i = 0; i < kVec; ++i) w[i] = p[i];
-  const uint32_t* u = reinterpret_cast<const uint32_t*>(w);
+  for (int i = 0; i < Raw<T, N>::kVec; ++i) r.w[i] = p[i];
+}
+
+// ... converted to float
+template <typename T, int N>
+__device__ __forceinline__ void to_float(const Raw<T, N>& r, float (&x)[N]) {
+  const uint32_t* u = reinterpret_cast<const uint32_t*>(r.w);
   if constexpr (Elem<T>::bytes == 4) {
 #pragma unroll
     for (int i = 0; i < N; ++i) x[i] = __uint_as_float(u[i]);
@@ -188,6 +198,7 @@ __global__ __launch_bounds__(kThreads) void pa_partition_kernel(PaParams p) {
   __shared__ float s_score[G * kMaxPart];
   __shared__ float s_red[kWaves * G * D];
   __shared__ float s_m[G], s_l[G];
+  __shared__ int s_blk[kMaxPart + 2];  // physical block of each block-table entry the partition spans
 
   const int qi = blockIdx.x, kvh = blockIdx.y, part = blockIdx.z;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
@@ -210,55 +221,68 @@ __global__ __launch_bounds__(kThreads) void pa_partition_kernel(PaParams p) {
   const int n = t1 - t0;
   const int32_t* bt_row = p.bt + (int64_t)qp.seq * p.sbt;
 
+  // the partition's slice of the block table, validated once, into LDS
+  const int bi0 = t0 / p.block_size;
+  const int nbi = (t1 - 1) / p.block_size - bi0 + 1;
+  for (int i = threadIdx.x; i < nbi; i += kThreads) {
+    const int bi = bi0 + i;
+    int blk = bi < p.max_blocks_per_seq ? bt_row[bi] : -1;
+    if (blk < 0 || blk >= p.num_blocks) {
+      blk = -1;
+      if (p.status) atomicOr(p.status, NS_PA_STATUS_BAD_BLOCK);
+    }
+    s_blk[i] = blk;
+  }
+
   // query slices, pre-scaled into log2 units
   float qv[G][DS];
 #pragma unroll
   for (int g = 0; g < G; ++g) {
-    load_row<T, DS>(p.q, (int64_t)qi * p.sq_tok + (int64_t)(kvh * G + g) * p.sq_head + dl * DS, qv[g]);
+    Raw<T, DS> r;
+    load_raw<T, DS>(p.q, (int64_t)qi * p.sq_tok + (int64_t)(kvh * G + g) * p.sq_head + dl * DS, r);
+    to_float<T, DS>(r, qv[g]);
 #pragma unroll
     for (int i = 0; i < DS; ++i) qv[g][i] *= p.scale_log2;
   }
+  __syncthreads();
 
-  // pass 1: scores -> LDS (wave w takes steps w, w + 4, ...)
-  bool bad = false;
-  for (int base = wave * kStepTokens; base < n; base += kWaves * kStepTokens) {
-    float kx[2][DS];
-    bool ok[2];
+  // Position j of the partition for sub-row r of the batch starting at base; its physical block
+  // from LDS (-1: past the partition or an invalid entry).
+  auto block_of = [&](int j, int& off) -> int {
+    if (j >= n) return -1;
+    const int t = t0 + j;
+    off = t % p.block_size;
+    return s_blk[t / p.block_size - bi0];
+  };
+
+  // pass 1: scores -> LDS. A wave takes batches of kBatch positions (wave w: batches w, w + 4, ...);
+  // each lane requests its kSub rows of the batch before any arithmetic.
+  for (int base = wave * kBatch; base < n; base += kWaves * kBatch) {
+    Raw<T, DS> raw[kSub];
+    int blk[kSub];
 #pragma unroll
-    for (int r = 0; r < 2; ++r) {
-      const int j = base + r * 8 + slot;
-      const int t = t0 + j;
-      ok[r] = false;
-      if (j < n) {
-        const int bi = t / p.block_size;
-        const int blk = bi < p.max_blocks_per_seq ? bt_row[bi] : -1;
-        if (blk >= 0 && blk < p.num_blocks) {
-          ok[r] = true;
-          load_row<T, DS>(p.k, (int64_t)blk * p.sk_blk + (int64_t)(t % p.block_size) * p.sk_tok +
-                                   (int64_t)kvh * p.sk_head + dl * DS, kx[r]);
-        } else {
-          bad = true;
-        }
-      }
-      if (!ok[r]) {
-#pragma unroll
-        for (int i = 0; i < DS; ++i) kx[r][i] = 0.f;
-      }
+    for (int r = 0; r < kSub; ++r) {
+      int off = 0;
+      blk[r] = block_of(base + r * 8 + slot, off);
+      if (blk[r] >= 0)
+        load_raw<T, DS>(p.k, (int64_t)blk[r] * p.sk_blk + (int64_t)off * p.sk_tok + (int64_t)kvh * p.sk_head + dl * DS,
+                        raw[r]);
     }
 #pragma unroll
-    for (int r = 0; r < 2; ++r) {
+    for (int r = 0; r < kSub; ++r) {
+      float kx[DS];
+      to_float<T, DS>(raw[r], kx);
       const int j = base + r * 8 + slot;
 #pragma unroll
       for (int g = 0; g < G; ++g) {
-        float s = 0.f;
+        float sc = 0.f;
 #pragma unroll
-        for (int i = 0; i < DS; ++i) s = fmaf(qv[g][i], kx[r][i], s);
-        s = octet_sum(s);
-        if (dl == g && j < n) s_score[g * kMaxPart + j] = ok[r] ? s : -INFINITY;
+        for (int i = 0; i < DS; ++i) sc = fmaf(qv[g][i], kx[i], sc);
+        sc = octet_sum(sc);
+        if (dl == g && j < n) s_score[g * kMaxPart + j] = blk[r] >= 0 ? sc : -INFINITY;
       }
     }
   }
-  if (bad && p.status) atomicOr(p.status, NS_PA_STATUS_BAD_BLOCK);
   __syncthreads();
 
   // pass 2: per-head max and exp2, in place (wave w takes heads w, w + 4)
@@ -280,39 +304,34 @@ __global__ __launch_bounds__(kThreads) void pa_partition_kernel(PaParams p) {
   }
   __syncthreads();
 
-  // pass 3: probability-weighted values
+  // pass 3: probability-weighted values, the same batches
   float acc[G][DS];
 #pragma unroll
   for (int g = 0; g < G; ++g)
 #pragma unroll
     for (int i = 0; i < DS; ++i) acc[g][i] = 0.f;
-  for (int base = wave * kStepTokens; base < n; base += kWaves * kStepTokens) {
-    float vx[2][DS];
-    bool ok[2];
+  for (int base = wave * kBatch; base < n; base += kWaves * kBatch) {
+    Raw<T, DS> raw[kSub];
+    int blk[kSub];
 #pragma unroll
-    for (int r = 0; r < 2; ++r) {
-      const int j = base + r * 8 + slot;
-      const int t = t0 + j;
-      ok[r] = false;
-      if (j < n) {
-        const int bi = t / p.block_size;
-        const int blk = bi < p.max_blocks_per_seq ? bt_row[bi] : -1;
-        if (blk >= 0 && blk < p.num_blocks) {
-          ok[r] = true;
-          load_row<T, DS>(p.v, (int64_t)blk * p.sv_blk + (int64_t)(t % p.block_size) * p.sv_tok +
-                                   (int64_t)kvh * p.sv_head + dl * DS, vx[r]);
-        }
-      }
+    for (int r = 0; r < kSub; ++r) {
+      int off = 0;
+      blk[r] = block_of(base + r * 8 + slot, off);
+      if (blk[r] >= 0)
+        load_raw<T, DS>(p.v, (int64_t)blk[r] * p.sv_blk + (int64_t)off * p.sv_tok + (int64_t)kvh * p.sv_head + dl * DS,
+                        raw[r]);
     }
 #pragma unroll
-    for (int r = 0; r < 2; ++r) {
-      if (!ok[r]) continue;
+    for (int r = 0; r < kSub; ++r) {
+      if (blk[r] < 0) continue;
+      float vx[DS];
+      to_float<T, DS>(raw[r], vx);
       const int j = base + r * 8 + slot;
 #pragma unroll
       for (int g = 0; g < G; ++g) {
         const float w = s_score[g * kMaxPart + j];
 #pragma unroll
-        for (int i = 0; i < DS; ++i) acc[g][i] = fmaf(w, vx[r][i], acc[g][i]);
+        for (int i = 0; i < DS; ++i) acc[g][i] = fmaf(w, vx[i], acc[g][i]);
       }
     }
   }
