@@ -413,10 +413,11 @@ def paged_attention_leg(dev, stream, steps=200, seqs=64, ctx=2048):
     qsl = torch.arange(seqs + 1, dtype=torch.int32, device=dev)
     out = torch.empty_like(q)
     ws = torch.empty(max(A.workspace_bytes(seqs, hq, hkv, d, ctx), 1), dtype=torch.uint8, device=dev)
+    cnt = torch.zeros(seqs * hkv, dtype=torch.int32, device=dev)
 
     def call(i):
         k, v = caches[i % 2]
-        A.paged_attention_hip(q, k, v, bt, sl, qsl, ql, d ** -0.5, bs, max_seq_len=ctx, out=out, workspace=ws,
+        A.paged_attention_hip(q, k, v, bt, sl, qsl, ql, d ** -0.5, bs, max_seq_len=ctx, out=out, workspace=ws, counters=cnt,
                               stream=stream.cuda_stream)
 
     for i in range(20):

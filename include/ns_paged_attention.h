@@ -32,7 +32,7 @@
 extern "C" {
 #endif
 
-#define NS_PA_ABI_VERSION 1
+#define NS_PA_ABI_VERSION 2
 
 #define NS_PA_DTYPE_F32 0
 #define NS_PA_DTYPE_BF16 1
@@ -56,6 +56,10 @@ typedef struct ns_paged_attn_args {
   int32_t*       status;           /* optional, one word: NS_PA_STATUS_* bits */
   void*          workspace;        /* ns_paged_attention_workspace_bytes() bytes, or NULL if 0 */
   uint64_t       workspace_bytes;
+  int32_t*       counters;         /* when the workspace is needed: total_q * num_kv_heads arrival
+                                      counters, zero-filled before first use and left zeroed by
+                                      every call (whatever its shape), so one buffer serves all
+                                      calls of one stream */
   int64_t        stride_q_token, stride_q_head;
   int64_t        stride_k_block, stride_k_token, stride_k_head;
   int64_t        stride_v_block, stride_v_token, stride_v_head;
@@ -80,15 +84,17 @@ int ns_pa_abi_version(void);
 /* Message of the last failed call on this thread. */
 const char* ns_pa_last_error(void);
 
-/* Workspace bytes a call with these sizes needs (0 when every query fits one KV partition).
- * Returns 0 on success, nonzero on invalid sizes. */
+/* Workspace bytes a call with these sizes needs (0 when every query fits one KV partition): the
+ * partials of split rows (no initial contents needed). A call that needs a workspace also needs the
+ * counters buffer. Returns 0 on success, nonzero on invalid sizes. */
 int ns_paged_attention_workspace_bytes(int32_t total_q, int32_t num_heads_q, int32_t num_kv_heads,
                                        int32_t head_dim, int32_t max_seq_len, uint64_t* bytes);
 
 /* Paged attention (paged_attention_triton.py:134-170, paged_attention_torch.py:31-100): one
- * workgroup per (query token, KV head, KV partition) computes all query heads of that KV head, so
- * each key and value row is read once per query token; partitions are merged by a second launch
- * when a query spans more than one. Returns 0 on success, nonzero on invalid arguments. */
+ * launch; one workgroup per (query token, KV head, KV partition) computes all query heads of that
+ * KV head, so each key and value row is read once per query token; when a query spans several
+ * partitions the last of them to finish merges them. Returns 0 on success, nonzero on invalid
+ * arguments. */
 int ns_paged_attention(const ns_paged_attn_args* args, hipStream_t stream);
 
 #ifdef __cplusplus

@@ -14,8 +14,9 @@
 //    slice's partial dot products are summed across the 8 lanes with ds_swizzle (no LDS traffic).
 //  * Exact two-pass softmax inside a partition: scores (already in log2 units) go to LDS, one max
 //    and one exp2 pass over LDS, then the value pass. Partitions of a long sequence (split-KV,
-//    sized on the host so that the grid holds >= 2048 workgroups) are merged by a second small
-//    launch with the usual max-rescaled sums; a query that fits one partition is written directly.
+//    sized on the host so that the grid holds >= 2048 workgroups) are merged by the last of the
+//    row's workgroups to arrive (max-rescaled sums); a query that fits one partition is written
+//    directly. One launch per call.
 //  * The sequence of a query token and its KV position are computed in the kernel (binary search
 //    over query_start_loc), so a call needs no host copy of the batch layout.
 
@@ -61,6 +62,8 @@ struct PaParams {
   int32_t* status;
   float* ws_acc;    // (total_q, Hq, max_parts, D) unnormalised partition outputs
   float* ws_ml;     // (total_q, Hq, max_parts, 2) partition max (log2 units) and sum
+  int32_t* counters;  // (total_q, Hkv) arrivals of split rows' partitions; zero between calls
+                      // (a buffer of its own: any call shape leaves every counter at zero)
   int64_t sq_tok, sq_head, sk_blk, sk_tok, sk_head, sv_blk, sv_tok, sv_head, so_tok, so_head, sbt;
   int32_t num_seqs, hq, hkv, block_size, num_blocks, max_blocks_per_seq, part_tokens, max_parts;
   float scale_log2;  // scale * log2(e): scores in log2 units, exp2 for the softmax
@@ -164,6 +167,15 @@ __device__ __forceinline__ float wave_sum(float x) {
 #pragma unroll
   for (int s = 1; s < 64; s <<= 1) x += __shfl_xor(x, s);
   return x;
+}
+
+// Stores and loads of the partition partials at agent scope: the workgroups of one row run on
+// different XCDs, whose L2s are not coherent with each other for plain accesses.
+__device__ __forceinline__ void st_dev(float* p, float v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float ld_dev(const float* p) {
+  return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // ---- batch layout -----------------------------------------------------------------------------
@@ -360,38 +372,80 @@ __global__ __launch_bounds__(kThreads) void pa_partition_kernel(PaParams p) {
       store_one<T>(p.out, (int64_t)qi * p.so_tok + (int64_t)h * p.so_head + d, l > 0.f ? o / l : 0.f);
     } else if (p.ws_acc && part < p.max_parts) {
       const int64_t slot_idx = ((int64_t)qi * p.hq + h) * p.max_parts + part;
-      p.ws_acc[slot_idx * D + d] = o;
+      st_dev(&p.ws_acc[slot_idx * D + d], o);
       if (d == 0) {
-        p.ws_ml[slot_idx * 2] = s_m[g];
-        p.ws_ml[slot_idx * 2 + 1] = s_l[g];
+        st_dev(&p.ws_ml[slot_idx * 2], s_m[g]);
+        st_dev(&p.ws_ml[slot_idx * 2 + 1], s_l[g]);
       }
     }
   }
-}
+  if (direct || !p.ws_acc || part >= p.max_parts) return;
 
-// ---- partition merge --------------------------------------------------------------------------
-
-// One workgroup of D threads per (query token, query head) whose query spans several partitions.
-template <typename T, int D>
-__global__ __launch_bounds__(128) void pa_merge_kernel(PaParams p) {
-  const int qi = blockIdx.x, h = blockIdx.y, d = threadIdx.x;
-  const QueryPlace qp = place_query(p, qi);
-  int n_parts = (qp.kv_len + p.part_tokens - 1) / p.part_tokens;
-  if (n_parts <= 1 || d >= D) return;
-  if (n_parts > p.max_parts) n_parts = p.max_parts;
-  const int64_t base = ((int64_t)qi * p.hq + h) * p.max_parts;
-  float m = -INFINITY;
-  for (int i = 0; i < n_parts; ++i) m = fmaxf(m, p.ws_ml[(base + i) * 2]);
-  float l = 0.f, o = 0.f;
-  if (m != -INFINITY) {
-    for (int i = 0; i < n_parts; ++i) {
-      const float mi = p.ws_ml[(base + i) * 2];
-      const float w = mi == -INFINITY ? 0.f : exp2f(mi - m);
-      l = fmaf(w, p.ws_ml[(base + i) * 2 + 1], l);
-      o = fmaf(w, p.ws_acc[(base + i) * D + d], o);
+  // Split row: the last of its partitions to arrive merges them (max-rescaled sums, one pass)
+  // and resets the row's counter. Every store above completes before the counter moves.
+  const int arrivals = n_parts < p.max_parts ? n_parts : p.max_parts;
+  __shared__ int s_last;
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  int32_t* counter = p.counters + (int64_t)qi * p.hkv + kvh;
+  if (threadIdx.x == 0) s_last = atomicAdd(counter, 1) == arrivals - 1;
+  __syncthreads();
+  if (!s_last) return;
+  if (threadIdx.x == 0) __hip_atomic_store(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  if (arrivals <= kMaxPart) {
+    // weights w_i / L of the partitions into LDS (one wave per head, lanes over partitions), then
+    // every output is an independent weighted sum of the partitions' unnormalised outputs
+    for (int g = wave; g < G; g += kWaves) {
+      const int64_t base = ((int64_t)qi * p.hq + kvh * G + g) * p.max_parts;
+      float m = -INFINITY;
+      for (int i = lane; i < arrivals; i += 64) m = fmaxf(m, ld_dev(&p.ws_ml[(base + i) * 2]));
+      m = wave_max(m);
+      float l = 0.f;
+      for (int i = lane; i < arrivals; i += 64) {
+        const float mi = ld_dev(&p.ws_ml[(base + i) * 2]);
+        const float w = (m == -INFINITY || mi == -INFINITY) ? 0.f : exp2f(mi - m);
+        s_score[g * kMaxPart + i] = w;
+        l = fmaf(w, ld_dev(&p.ws_ml[(base + i) * 2 + 1]), l);
+      }
+      l = wave_sum(l);
+      if (lane == 0) s_l[g] = l;
     }
+    __syncthreads();
+    for (int e = threadIdx.x; e < G * D; e += kThreads) {
+      const int g = e / D, d = e % D;
+      const int h = kvh * G + g;
+      const int64_t base = ((int64_t)qi * p.hq + h) * p.max_parts;
+      float o = 0.f;
+#pragma unroll 4
+      for (int i = 0; i < arrivals; ++i) o = fmaf(s_score[g * kMaxPart + i], ld_dev(&p.ws_acc[(base + i) * D + d]), o);
+      const float l = s_l[g];
+      store_one<T>(p.out, (int64_t)qi * p.so_tok + (int64_t)h * p.so_head + d, l > 0.f ? o / l : 0.f);
+    }
+    return;
   }
-  store_one<T>(p.out, (int64_t)qi * p.so_tok + (int64_t)h * p.so_head + d, l > 0.f ? o / l : 0.f);
+  // more partitions than the LDS weight table holds: one pass of max-rescaled sums per output
+  for (int e = threadIdx.x; e < G * D; e += kThreads) {
+    const int g = e / D, d = e % D;
+    const int h = kvh * G + g;
+    const int64_t base = ((int64_t)qi * p.hq + h) * p.max_parts;
+    float m = -INFINITY, l = 0.f, o = 0.f;
+    for (int i = 0; i < arrivals; ++i) {
+      const float mi = ld_dev(&p.ws_ml[(base + i) * 2]);
+      const float li = ld_dev(&p.ws_ml[(base + i) * 2 + 1]);
+      const float ai = ld_dev(&p.ws_acc[(base + i) * D + d]);
+      if (mi == -INFINITY) continue;  // a partition whose keys were all skipped
+      if (mi > m) {
+        const float r = m == -INFINITY ? 0.f : exp2f(m - mi);
+        l *= r;
+        o *= r;
+        m = mi;
+      }
+      const float w = exp2f(mi - m);
+      l = fmaf(w, li, l);
+      o = fmaf(w, ai, o);
+    }
+    store_one<T>(p.out, (int64_t)qi * p.so_tok + (int64_t)h * p.so_head + d, l > 0.f ? o / l : 0.f);
+  }
 }
 
 // ---- host side ---------------------------------------------------------------------------------
@@ -430,8 +484,6 @@ template <typename T, int D, int G>
 void launch(const PaParams& p, int total_q, hipStream_t stream) {
   dim3 grid(total_q, p.hkv, p.max_parts > 0 ? p.max_parts : 1);
   hipLaunchKernelGGL((pa_partition_kernel<T, D, G>), grid, dim3(kThreads), 0, stream, p);
-  if (p.max_parts > 1)
-    hipLaunchKernelGGL((pa_merge_kernel<T, D>), dim3(total_q, p.hq), dim3(128), 0, stream, p);
 }
 
 template <typename T, int D>
@@ -493,6 +545,7 @@ int ns_paged_attention(const ns_paged_attn_args* a, hipStream_t stream) {
   if (need > 0 && (!a->workspace || a->workspace_bytes < need))
     return fail("workspace of %llu bytes needed (got %llu)", (unsigned long long)need,
                 (unsigned long long)a->workspace_bytes);
+  if (need > 0 && !a->counters) return fail("a call with split rows needs the zero-filled counters buffer");
   const int part = part_tokens_for(a->total_q, a->num_kv_heads, a->max_seq_len);
   const int64_t max_parts = ((int64_t)a->max_seq_len + part - 1) / part;
   if (max_parts > 65535) return fail("max_seq_len too large");
@@ -509,6 +562,7 @@ int ns_paged_attention(const ns_paged_attn_args* a, hipStream_t stream) {
   p.status = a->status;
   p.ws_acc = reinterpret_cast<float*>(a->workspace);
   p.ws_ml = need ? p.ws_acc + (uint64_t)a->total_q * a->num_heads_q * max_parts * a->head_dim : nullptr;
+  p.counters = a->counters;
   p.sq_tok = a->stride_q_token;
   p.sq_head = a->stride_q_head;
   p.sk_blk = a->stride_k_block;

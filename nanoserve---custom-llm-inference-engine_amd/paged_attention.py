@@ -23,7 +23,7 @@ from typing import Optional
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libns_paged_attention.so")
 
-ABI_VERSION = 1
+ABI_VERSION = 2
 NS_PA_DTYPE_F32 = 0
 NS_PA_DTYPE_BF16 = 1
 NS_PA_DTYPE_F16 = 2
@@ -53,6 +53,7 @@ class NsPagedAttnArgs(ctypes.Structure):
         ("status", ctypes.c_void_p),
         ("workspace", ctypes.c_void_p),
         ("workspace_bytes", ctypes.c_uint64),
+        ("counters", ctypes.c_void_p),
         ("stride_q_token", ctypes.c_int64),
         ("stride_q_head", ctypes.c_int64),
         ("stride_k_block", ctypes.c_int64),
@@ -115,6 +116,23 @@ def workspace_bytes(total_q: int, num_heads_q: int, num_kv_heads: int, head_dim:
     return int(out.value)
 
 
+_COUNTERS = {}
+
+
+def counters_for(device, n: int):
+    """A zero-filled int32 buffer of at least ``n`` arrival counters kept per device. Every call
+    leaves its counters at zero whatever its shape, so the buffer stays valid for all calls of one
+    stream; it only grows."""
+    import torch
+
+    key = torch.device(device).index or 0
+    buf = _COUNTERS.get(key)
+    if buf is None or buf.numel() < n:
+        buf = torch.zeros(max(n, 1 << 16), dtype=torch.int32, device=device)
+        _COUNTERS[key] = buf
+    return buf
+
+
 def _dtype_code(dtype) -> int:
     import torch
 
@@ -132,7 +150,7 @@ def _i32(t, device):
 
 def paged_attention_hip(query, k_cache, v_cache, block_tables, seq_lens, query_start_loc, query_lens,
                         scale: float, block_size: int, *, max_seq_len: Optional[int] = None,
-                        out=None, workspace=None, status=None, stream=None):
+                        out=None, workspace=None, counters=None, status=None, stream=None):
     """Attention of every query token over its sequence's paged KV (the reference's
     ``paged_attention_triton``; same arguments, same result up to float32 rounding order).
 
@@ -140,7 +158,9 @@ def paged_attention_hip(query, k_cache, v_cache, block_tables, seq_lens, query_s
     block_tables int (num_seqs, max_blocks_per_seq); seq_lens, query_lens int (num_seqs);
     query_start_loc int (num_seqs + 1). ``status``, if given, is an int32 device tensor of one
     element that the kernel ORs STATUS_* bits into (a block id outside the cache, a sequence longer
-    than ``max_seq_len``): a caller that wants the check reads it after the call.
+    than ``max_seq_len``): a caller that wants the check reads it after the call. ``workspace``
+    (uint8, any contents) and ``counters`` (int32, zero-filled once; every call leaves it so) are
+    allocated per call, resp. taken from this module's per-device buffer, when not given.
     """
     import torch
 
@@ -176,14 +196,20 @@ def paged_attention_hip(query, k_cache, v_cache, block_tables, seq_lens, query_s
     elif out.shape != query.shape or out.dtype != query.dtype or out.device != dev:
         raise PagedAttentionError("out must match query's shape, dtype and device")
     need = workspace_bytes(total_q, hq, hkv, d, max_seq_len)
-    if need and (workspace is None or workspace.numel() * workspace.element_size() < need):
+    if need and workspace is None:
         workspace = torch.empty(need, dtype=torch.uint8, device=dev)
+    elif need and workspace.numel() * workspace.element_size() < need:
+        raise PagedAttentionError(f"workspace of {need} bytes needed")
+    if need and counters is None:
+        counters = counters_for(dev, total_q * hkv)
+    elif need and (counters.dtype != torch.int32 or counters.device != dev or counters.numel() < total_q * hkv):
+        raise PagedAttentionError(f"counters must be an int32 device tensor of at least {total_q * hkv} entries")
     if status is not None and (status.dtype != torch.int32 or status.device != dev or status.numel() < 1):
         raise PagedAttentionError("status must be an int32 device tensor")
     a = NsPagedAttnArgs(
         query.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(), out.data_ptr(), bt.data_ptr(), sl.data_ptr(),
         qsl.data_ptr(), ql.data_ptr(), status.data_ptr() if status is not None else None,
-        workspace.data_ptr() if need else None, need,
+        workspace.data_ptr() if need else None, need, counters.data_ptr() if need else None,
         query.stride(0), query.stride(1), k_cache.stride(0), k_cache.stride(1), k_cache.stride(2),
         v_cache.stride(0), v_cache.stride(1), v_cache.stride(2), out.stride(0), out.stride(1),
         bt.stride(0) if bt.dim() == 2 else 0,

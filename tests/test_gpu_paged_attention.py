@@ -113,3 +113,32 @@ def test_empty_batch_and_argument_errors(device):
     with pytest.raises(A.PagedAttentionError, match="block_size"):
         A.paged_attention_hip(c["query"], c["k_cache"], c["v_cache"], c["block_tables"], c["seq_lens"],
                               c["query_start_loc"], c["query_lens"], c["scale"], 8)
+
+
+def test_split_rows_leave_the_counters_at_zero(device):
+    # split rows are merged by their last partition's workgroup through arrival counters; each call
+    # must leave them at zero, so repeated calls of different shapes on one counters buffer (and a
+    # reused workspace holding an earlier call's partials) stay exact
+    counters = torch.zeros(4096, dtype=torch.int32, device=device)
+    ws = torch.full((32 << 20,), 0x7F, dtype=torch.uint8, device=device)  # largest need: 15.9 MB
+    for seed, lens in ((37, [3000, 700, 5000]), (38, [64] * 70 + [9000]), (39, [2500] * 3)):
+        case = make_case(seed, lens, [1] * len(lens))
+        q = case["query"]
+        assert A.workspace_bytes(q.shape[0], q.shape[1], case["k_cache"].shape[2], q.shape[2], max(lens)) > 0
+        ref = PA.paged_attention(**oracle_args(case))
+        outs = []
+        for _ in range(2):
+            out = run(case, device, workspace=ws, counters=counters)
+            assert_close_to_oracle(out, ref, q.dtype)
+            outs.append(out)
+        assert torch.equal(outs[0], outs[1])
+        assert torch.count_nonzero(counters).item() == 0
+
+
+def test_more_partitions_than_the_lds_weight_table(device):
+    # one KV head and one long row: 625 partitions of 64 positions, more than the merging
+    # workgroup's LDS weight table (512 entries) holds, so the one-pass rescaled merge runs
+    case = make_case(40, [40000], [1], hq=8, hkv=1, d=128)
+    q = case["query"]
+    assert A.workspace_bytes(1, 8, 1, 128, 40000) == 1 * 8 * 625 * (128 + 2) * 4
+    check(case, device)

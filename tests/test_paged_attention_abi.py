@@ -42,7 +42,7 @@ def test_struct_layout_matches_header():
     for decl in re.findall(r"^\s*([^/{}]+?);", body, flags=re.M):
         names += [n.strip().lstrip("*") for n in re.sub(r"^.*?\b(\w+)\s*(,|$)", r"\1\2", decl, count=1).split(",")]
     assert names == [f[0] for f in PA.NsPagedAttnArgs._fields_]
-    assert ctypes.sizeof(PA.NsPagedAttnArgs) == 224
+    assert ctypes.sizeof(PA.NsPagedAttnArgs) == 232
 
 
 def test_workspace_sizes():
@@ -50,6 +50,7 @@ def test_workspace_sizes():
     # a grid already wide enough (256 queries x 8 KV heads at one 512-position partition): no workspace
     assert PA.workspace_bytes(256, 24, 8, 128, 512) == 0
     # 64 decode rows of 512 positions: 512 workgroups, so split into four 128-position partitions
+    # (partials: head_dim + 2 floats per query token, query head and partition)
     assert PA.workspace_bytes(64, 24, 8, 128, 512) == 64 * 24 * 4 * (128 + 2) * 4
     # a single long decode row is split into 64-position partitions: (D + 2) floats per partition and head
     assert PA.workspace_bytes(1, 24, 8, 128, 8192) == 1 * 24 * (8192 // 64) * (128 + 2) * 4
