@@ -14,7 +14,7 @@
 //    slice's partial dot products are summed across the 8 lanes with ds_swizzle (no LDS traffic).
 //  * Exact two-pass softmax inside a partition: scores (already in log2 units) go to LDS, one max
 //    and one exp2 pass over LDS, then the value pass. Partitions of a long sequence (split-KV,
-//    sized on the host so that the grid holds >= 2048 workgroups) are merged by the last of the
+//    sized on the host so that the grid holds >= 1024 workgroups) are merged by the last of the
 //    row's workgroups to arrive (max-rescaled sums); a query that fits one partition is written
 //    directly. One launch per call.
 //  * The sequence of a query token and its KV position are computed in the kernel (binary search
@@ -34,9 +34,9 @@ constexpr int kThreads = 256;
 constexpr int kWaves = kThreads / 64;
 constexpr int kSub = 2;                 // KV positions per lane per batch (8 lanes per position)
 constexpr int kBatch = 8 * kSub;        // KV positions per wave batch
-constexpr int kMaxPart = 512;           // largest KV partition (LDS score buffer)
+constexpr int kMaxPart = 1024;          // largest KV partition (LDS score buffer)
 constexpr int kMinPart = 64;
-constexpr int kTargetGroups = 2048;     // workgroups a launch aims for before splitting stops
+constexpr int kTargetGroups = 1024;     // workgroups a launch aims for before splitting stops
 constexpr float kLog2e = 1.4426950408889634f;
 
 thread_local char g_err[512];

@@ -136,9 +136,8 @@ def test_split_rows_leave_the_counters_at_zero(device):
 
 
 def test_more_partitions_than_the_lds_weight_table(device):
-    # one KV head and one long row: 625 partitions of 64 positions, more than the merging
-    # workgroup's LDS weight table (512 entries) holds, so the one-pass rescaled merge runs
-    case = make_case(40, [40000], [1], hq=8, hkv=1, d=128)
-    q = case["query"]
-    assert A.workspace_bytes(1, 8, 1, 128, 40000) == 1 * 8 * 625 * (128 + 2) * 4
+    # one KV head and one long row: 1094 partitions of 64 positions, more than the merging
+    # workgroup's LDS weight table (1024 entries) holds, so the one-pass rescaled merge runs
+    case = make_case(40, [70000], [1], hq=8, hkv=1, d=128)
+    assert A.workspace_bytes(1, 8, 1, 128, 70000) == 1 * 8 * 1094 * (128 + 2) * 4
     check(case, device)

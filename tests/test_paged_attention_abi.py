@@ -47,11 +47,11 @@ def test_struct_layout_matches_header():
 
 def test_workspace_sizes():
     built()
-    # a grid already wide enough (256 queries x 8 KV heads at one 512-position partition): no workspace
-    assert PA.workspace_bytes(256, 24, 8, 128, 512) == 0
-    # 64 decode rows of 512 positions: 512 workgroups, so split into four 128-position partitions
+    # a grid already wide enough (256 queries x 8 KV heads at one 1024-position partition): no workspace
+    assert PA.workspace_bytes(256, 24, 8, 128, 1024) == 0
+    # 64 decode rows of 512 positions: 512 workgroups, so split into two 256-position partitions
     # (partials: head_dim + 2 floats per query token, query head and partition)
-    assert PA.workspace_bytes(64, 24, 8, 128, 512) == 64 * 24 * 4 * (128 + 2) * 4
+    assert PA.workspace_bytes(64, 24, 8, 128, 512) == 64 * 24 * 2 * (128 + 2) * 4
     # a single long decode row is split into 64-position partitions: (D + 2) floats per partition and head
     assert PA.workspace_bytes(1, 24, 8, 128, 8192) == 1 * 24 * (8192 // 64) * (128 + 2) * 4
     with pytest.raises(PA.PagedAttentionError, match="multiple"):
