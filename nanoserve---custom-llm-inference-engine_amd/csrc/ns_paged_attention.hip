@@ -66,6 +66,7 @@ struct PaParams {
                       // (a buffer of its own: any call shape leaves every counter at zero)
   int64_t sq_tok, sq_head, sk_blk, sk_tok, sk_head, sv_blk, sv_tok, sv_head, so_tok, so_head, sbt;
   int32_t num_seqs, hq, hkv, block_size, num_blocks, max_blocks_per_seq, part_tokens, max_parts;
+  int32_t bs_shift;  // log2(block_size) when it is a power of two, else -1
   float scale_log2;  // scale * log2(e): scores in log2 units, exp2 for the softmax
 };
 
@@ -263,8 +264,15 @@ __global__ __launch_bounds__(kThreads) void pa_partition_kernel(PaParams p) {
   auto block_of = [&](int j, int& off) -> int {
     if (j >= n) return -1;
     const int t = t0 + j;
-    off = t % p.block_size;
-    return s_blk[t / p.block_size - bi0];
+    int bi;
+    if (p.bs_shift >= 0) {  // the usual case (16): a shift and a mask instead of an integer division
+      bi = t >> p.bs_shift;
+      off = t & (p.block_size - 1);
+    } else {
+      bi = t / p.block_size;
+      off = t - bi * p.block_size;
+    }
+    return s_blk[bi - bi0];
   };
 
   // pass 1: scores -> LDS. A wave takes batches of kBatch positions (wave w: batches w, w + 4, ...);
@@ -295,6 +303,21 @@ __global__ __launch_bounds__(kThreads) void pa_partition_kernel(PaParams p) {
       }
     }
   }
+  // the wave's first value batch is requested before the softmax pass: the workgroups of a CU
+  // reach that pass together, and the requests keep the memory pipe busy across it
+  Raw<T, DS> vraw[kSub];
+  int vblk[kSub];
+  auto request_values = [&](int base) {
+#pragma unroll
+    for (int r = 0; r < kSub; ++r) {
+      int off = 0;
+      vblk[r] = block_of(base + r * 8 + slot, off);
+      if (vblk[r] >= 0)
+        load_raw<T, DS>(p.v, (int64_t)vblk[r] * p.sv_blk + (int64_t)off * p.sv_tok + (int64_t)kvh * p.sv_head + dl * DS,
+                        vraw[r]);
+    }
+  };
+  request_values(wave * kBatch);
   __syncthreads();
 
   // pass 2: per-head max and exp2, in place (wave w takes heads w, w + 4)
@@ -323,21 +346,12 @@ __global__ __launch_bounds__(kThreads) void pa_partition_kernel(PaParams p) {
 #pragma unroll
     for (int i = 0; i < DS; ++i) acc[g][i] = 0.f;
   for (int base = wave * kBatch; base < n; base += kWaves * kBatch) {
-    Raw<T, DS> raw[kSub];
-    int blk[kSub];
+    if (base != wave * kBatch) request_values(base);
 #pragma unroll
     for (int r = 0; r < kSub; ++r) {
-      int off = 0;
-      blk[r] = block_of(base + r * 8 + slot, off);
-      if (blk[r] >= 0)
-        load_raw<T, DS>(p.v, (int64_t)blk[r] * p.sv_blk + (int64_t)off * p.sv_tok + (int64_t)kvh * p.sv_head + dl * DS,
-                        raw[r]);
-    }
-#pragma unroll
-    for (int r = 0; r < kSub; ++r) {
-      if (blk[r] < 0) continue;
+      if (vblk[r] < 0) continue;
       float vx[DS];
-      to_float<T, DS>(raw[r], vx);
+      to_float<T, DS>(vraw[r], vx);
       const int j = base + r * 8 + slot;
 #pragma unroll
       for (int g = 0; g < G; ++g) {
@@ -578,6 +592,10 @@ int ns_paged_attention(const ns_paged_attn_args* a, hipStream_t stream) {
   p.hq = a->num_heads_q;
   p.hkv = a->num_kv_heads;
   p.block_size = a->block_size;
+  p.bs_shift = -1;
+  if ((a->block_size & (a->block_size - 1)) == 0)
+    for (int sh = 0; sh < 31; ++sh)
+      if ((1 << sh) == a->block_size) p.bs_shift = sh;
   p.num_blocks = a->num_blocks;
   p.max_blocks_per_seq = a->max_blocks_per_seq;
   p.part_tokens = part;

@@ -57,7 +57,7 @@ def test_head_layouts_and_dtypes(device, dtype, hq, hkv, d):
     check(case, device)
 
 
-@pytest.mark.parametrize("block_size", [1, 8, 32])
+@pytest.mark.parametrize("block_size", [1, 7, 8, 12, 32])
 def test_block_sizes(device, block_size):
     case = make_case(20 + block_size, [45, 130, 7], [1, 3, 7], block_size=block_size)
     check(case, device)
