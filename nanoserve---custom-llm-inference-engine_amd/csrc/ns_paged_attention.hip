@@ -24,7 +24,6 @@
 #include <stdarg.h>
 #include <stdint.h>
 #include <stdio.h>
-#include <string.h>
 
 #include "ns_paged_attention.h"
 
