@@ -441,6 +441,45 @@ def paged_attention_leg(dev, stream, steps=200, seqs=64, ctx=2048):
             "paged_attention_decode_tokens_per_s": seqs / (us * 1e-6)}
 
 
+def paged_attention_cpu_baseline(seqs=64, ctx=2048, reps=3):
+    """The reference's SDPA backend (paged_attention_torch.py:31-100: per sequence, gather the KV
+    through the block table, repeat the KV heads, scaled_dot_product_attention) restated in torch on
+    the host CPU, on the same decode step as the GPU leg (bf16, shuffled blocks). Median of ``reps``."""
+    import torch
+    import torch.nn.functional as F
+
+    hq, hkv, d, bs = 24, 8, 128, 16
+    g = torch.Generator()
+    g.manual_seed(7)
+    nblk = seqs * ctx // bs
+    k_cache = torch.randn(nblk, bs, hkv, d, generator=g).to(torch.bfloat16)
+    v_cache = torch.randn(nblk, bs, hkv, d, generator=g).to(torch.bfloat16)
+    bt = torch.randperm(nblk, generator=g).to(torch.int32).view(seqs, ctx // bs)
+    q = torch.randn(seqs, hq, d, generator=g).to(torch.bfloat16)
+
+    def step():
+        out = torch.empty_like(q)
+        for i in range(seqs):
+            k = k_cache.index_select(0, bt[i]).reshape(-1, hkv, d).repeat_interleave(hq // hkv, dim=1)
+            v = v_cache.index_select(0, bt[i]).reshape(-1, hkv, d).repeat_interleave(hq // hkv, dim=1)
+            a = F.scaled_dot_product_attention(q[i:i + 1].transpose(0, 1).unsqueeze(0), k.transpose(0, 1).unsqueeze(0),
+                                               v.transpose(0, 1).unsqueeze(0), scale=d ** -0.5)
+            out[i] = a.squeeze(0).transpose(0, 1)[0]
+        return out
+
+    step()
+    times = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        step()
+        times.append(time.perf_counter() - t0)
+    sec = sorted(times)[len(times) // 2]
+    return {"value": seqs / sec, "unit": "decode rows/s", "cores": torch.get_num_threads(), "kind": "port",
+            "cpu_model": cpu_model(),
+            "sample": f"the full {seqs} x {ctx} bf16 decode step through the SDPA backend restated in torch "
+                      f"(paged_attention_torch.py:31-100), median of {reps} runs of {sec:.3f} s; torch {torch.__version__} CPU"}
+
+
 def main(argv=None):
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -569,6 +608,8 @@ def main(argv=None):
     small = small_batch_leg(L, lib, dev, stream, cpu_reps=20 if args.cpu_rows > 0 else 0) \
         if args.config == WORKLOAD_CFG else {}
     attention = paged_attention_leg(dev, stream) if args.config == WORKLOAD_CFG else {}
+    if attention and args.cpu_rows > 0:
+        attention["paged_attention_cpu_baseline"] = paged_attention_cpu_baseline()
     if args.config != WORKLOAD_CFG:
         desc = {0: "batch B=8 x V=128256 fp32, t=0.8 top_k=50 top_p=0.9 penalty=1.1, 64 history ids/row",
                 1: "batch B=64 x V=128256 fp32, mixed per-row parameters (greedy and sampled), 512 Zipf ids/row",
