@@ -1,7 +1,7 @@
 """CPU oracle: a restatement of NanoServe's paged attention.
 
-TEST INFRASTRUCTURE ONLY: imported by ``tests/`` (the checker of the HIP paged-attention
-kernels), never by the product.
+TEST INFRASTRUCTURE ONLY: imported by ``tests/`` and ``__graft_entry__.smoke()`` as the checker of
+the HIP paged-attention kernel, never by the product.
 
 Follows the reference's two backends, which compute the same function:
   * nanoserve/kernels/paged_attention_triton.py:19-106 -- per query token and query head, KV head
