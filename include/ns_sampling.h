@@ -26,7 +26,7 @@
 extern "C" {
 #endif
 
-#define NS_ABI_VERSION 9
+#define NS_ABI_VERSION 10
 
 #define NS_OK 0
 #define NS_ERR_INVALID 1   /* bad argument (message says which) */
@@ -39,6 +39,9 @@ extern "C" {
 #define NS_MODE_AUTO 0        /* per-row once the batch fills the GPU, else segmented (needs a workspace) */
 #define NS_MODE_SEGMENTED 1   /* greedy and small-k rows split over several workgroups (needs a workspace) */
 #define NS_MODE_PER_ROW 2     /* one workgroup per row for every row */
+
+#define NS_PENALTY_DIVIDE 0      /* penalty_rounding: score / p correctly rounded (torch on the CPU) */
+#define NS_PENALTY_RECIPROCAL 1  /* penalty_rounding: score * rep_penalty_recip[r] (torch on a GPU) */
 
 #define NS_KIND_GREEDY 1      /* row_kinds: greedy rows (temperature 0) */
 #define NS_KIND_SMALL_K 2     /* row_kinds: sampled rows with 1 <= top_k <= 64 and top_k < vocab */
@@ -120,6 +123,15 @@ typedef struct ns_sample_args {
                                    is left unchanged and counted in *hist_overflow.  0: the state is
                                    only read. */
   int32_t*       hist_overflow; /* device int32 counting the full slots of hist_append, or NULL */
+  int32_t        penalty_rounding; /* NS_PENALTY_*: how the penalty's positive branch score / p
+                                   (sampler.py:37, p a Python float) rounds.  The reference runs it
+                                   with torch on its configured device (config.py:63, "cuda" by
+                                   default); there torch multiplies by the float32 reciprocal of the
+                                   Python float, while on the CPU it divides.  Negative scores are
+                                   multiplied by rep_penalty[r] either way. */
+  const float*   rep_penalty_recip; /* [B] with NS_PENALTY_RECIPROCAL: each row's fl32(1 / p), the
+                                   reciprocal of the float64 penalty rounded once to float32 (what
+                                   torch on a GPU multiplies by); not read with NS_PENALTY_DIVIDE */
 } ns_sample_args;
 
 /* Version of this ABI (NS_ABI_VERSION). */

@@ -26,7 +26,10 @@ NS_KIND_GREEDY = 1      # row_kinds: greedy rows (temperature 0)
 NS_KIND_SMALL_K = 2     # sampled rows with 1 <= top_k <= 64 and top_k < vocab
 NS_KIND_OTHER = 4       # every other sampled row (top-k off or larger)
 NS_DEBUG_STREAM, NS_DEBUG_WIDE, NS_DEBUG_GENERAL = 0, 1, 2   # ns_debug_scaled routines
-ABI_VERSION = 9
+NS_PENALTY_DIVIDE = 0       # penalty_rounding: score / p correctly rounded (torch on the CPU)
+NS_PENALTY_RECIPROCAL = 1   # penalty_rounding: score * fl32(1 / p) (torch on a GPU)
+PENALTY_ROUNDING = {"division": NS_PENALTY_DIVIDE, "reciprocal": NS_PENALTY_RECIPROCAL}
+ABI_VERSION = 10
 
 # exported symbols, as declared in include/ns_sampling.h
 NS_NOALLOC_SCRATCH_BYTES = 80 << 20   # ns_sample_noalloc's device scratch per GPU
@@ -68,6 +71,8 @@ class NsSampleArgs(ctypes.Structure):
         ("hist_capacity", ctypes.c_int32),
         ("hist_append", ctypes.c_int32),
         ("hist_overflow", ctypes.c_void_p),
+        ("penalty_rounding", ctypes.c_int32),
+        ("rep_penalty_recip", ctypes.c_void_p),
     ]
 
 
@@ -235,11 +240,21 @@ def aligned_rows(logits, sample_idx):
     return padded[:, :V], new_idx
 
 
+def penalty_reciprocals(penalties):
+    """fl32(1 / p) of float64 penalties, the reciprocal rounded once: what torch on a GPU
+    multiplies by for ``score / p`` with a Python float p (sampler.py:37)."""
+    import numpy as np
+
+    p = np.asarray(penalties, dtype=np.float64)
+    with np.errstate(divide="ignore"):
+        return (1.0 / p).astype(np.float32)
+
+
 def sample_raw(logits, temperature, top_k, top_p, rep_penalty, uniforms, out_ids, *, sample_idx=None,
                hist_offsets=None, hist_ids=None, max_hist: int = 0, out_probs=None, out_info=None,
                stream=None, workspace="auto", mode: int = NS_MODE_AUTO, row_kinds: int = 0,
                hist_state=None, hist_slot=None, hist_append: bool = False, hist_overflow=None,
-               debug_scaled=None) -> None:
+               debug_scaled=None, penalty_rounding: int = NS_PENALTY_DIVIDE, rep_penalty_recip=None) -> None:
     """Launch ``ns_sample`` on device tensors (no copies, no synchronisation).
 
     logits: (N, V) float32 or bfloat16 CUDA tensor with unit stride in the last dim.
@@ -256,6 +271,10 @@ def sample_raw(logits, temperature, top_k, top_p, rep_penalty, uniforms, out_ids
     debug_scaled: a pair (formula, out) with out a (B, >= V) float32 tensor of unit stride
     along V: instead of sampling, ``ns_debug_scaled`` writes each row's penalized,
     temperature-scaled logits there, computed by routine ``formula`` (NS_DEBUG_*).
+    penalty_rounding: NS_PENALTY_DIVIDE (score / p correctly rounded, as torch on the CPU) or
+    NS_PENALTY_RECIPROCAL (score * rep_penalty_recip[r], as torch on a GPU);
+    rep_penalty_recip: (B,) float32, each row's fl32(1 / p) from the float64 penalty (see
+    ``penalty_reciprocals``), needed with NS_PENALTY_RECIPROCAL.
     """
     import torch
 
@@ -297,6 +316,8 @@ def sample_raw(logits, temperature, top_k, top_p, rep_penalty, uniforms, out_ids
         a.workspace_bytes = int(workspace.numel() * workspace.element_size())
     a.mode = int(mode)
     a.row_kinds = int(row_kinds)
+    a.penalty_rounding = int(penalty_rounding)
+    a.rep_penalty_recip = _ptr(rep_penalty_recip)
     if hist_state is not None:
         if hist_offsets is not None or hist_ids is not None:
             raise ValueError("hist_state excludes hist_offsets / hist_ids")

@@ -431,9 +431,11 @@ __device__ __forceinline__ int64_t uniform_pick(float u, float q, int64_t V) {
 }
 
 // The repetition penalty of one history token (sampler.py:37: score * p if score < 0 else
-// score / p), float32 and correctly rounded; rpen = RN(1/pen).
-__device__ __forceinline__ float pen_rn(float x, float pen, float rpen) {
-  return x < 0.0f ? x * pen : div_rn(x, pen, rpen);
+// score / p), float32; rpen = RN(1/pen).  recip = false: the division correctly rounded (torch
+// on the CPU); recip = true: x * rpen (torch on a GPU divides a tensor by a Python float that
+// way).  recip is the same for every lane of a launch.
+__device__ __forceinline__ float pen_rn(float x, float pen, float rpen, bool recip) {
+  return x < 0.0f ? x * pen : (recip ? x * rpen : div_rn(x, pen, rpen));
 }
 
 }  // namespace ns

@@ -162,6 +162,7 @@ struct RowArgs {
   IdSink out_ids;
   float* out_probs;
   int32_t* out_info;
+  const float* pen_rcp;   // [B] RN(1/p) for the reciprocal penalty, or NULL (division)
 };
 
 // Returns 0 when the row is resolved, 1 when it is left to the general per-row code:
@@ -185,8 +186,9 @@ __device__ __forceinline__ int row_fast(const RowArgs P, const int row, const in
   const bool greedy = temp == 0.0f;
   const float tdiv = temp > 0.0f ? __builtin_fmaxf(temp, 1e-6f) : 1.0f;   // sampler.py:42
   const float rdiv = 1.0f / tdiv;
-  const float rpen = 1.0f / pen;
-  auto pen_val = [&](float x) -> float { return pen_rn(x, pen, rpen); };
+  const bool recip = P.pen_rcp != nullptr;
+  const float rpen = recip ? P.pen_rcp[row] : 1.0f / pen;
+  auto pen_val = [&](float x) -> float { return pen_rn(x, pen, rpen, recip); };
   float* fs = reinterpret_cast<float*>(&misc->red);      // 128 floats of scratch
   BlockScratch* red = &misc->red;
 

@@ -353,8 +353,8 @@ struct GCtx {
   int32_t* out_info;
   int64_t V, nch, nrows_j;
   int row, U, k, flags;
-  float pen, tdiv, rdiv, p32, Mx, My, u;
-  bool pen_on, topk_on, topp_on;
+  float pen, rpen, tdiv, rdiv, p32, Mx, My, u;   // rpen: RN(1/p), read only when recip
+  bool pen_on, topk_on, topp_on, recip;
 };
 
 // Rows not resolved by the greedy, NaN-guard or small-k paths: top-k for
@@ -745,7 +745,7 @@ __device__ __attribute__((always_inline)) inline void generic_path(const GCtx g)
 #pragma unroll
       for (int e = 0; e < EPC; ++e) {
         float x = T::elem(w, e);
-        if ((hb >> e) & 1u) x = penalize(x, pen);
+        if ((hb >> e) & 1u) x = penalize(x, pen, g.rpen, g.recip);
         float ev = 0.0f;
         if (ok && keep(x, c * EPC + e)) ev = ns_expf(div_rn(x, tdiv, rdiv) - My);
         xe[e] = ev;
@@ -847,6 +847,7 @@ __device__ __attribute__((always_inline, cold)) inline void row_general(KArgs PA
   const float temp = P.temperature[row];
   const float topp = P.top_p[row];
   const float pen = P.penalty[row];
+  const float rpen_g = P.pen_rcp != nullptr ? P.pen_rcp[row] : 0.0f;   // the reciprocal penalty's RN(1/p)
   float u = P.uniforms[row];
   u = (u >= 0.0f) ? (u < 1.0f ? u : 0x1.fffffep-1f) : 0.0f;
   const int32_t k = P.top_k[row];
@@ -954,7 +955,7 @@ __device__ __attribute__((always_inline, cold)) inline void row_general(KArgs PA
 #pragma unroll
         for (int s = 0; s < GATHER; ++s) {
           int i = base + s * 64 + lane;
-          if (i < U) xl_val[i] = penalize(xv[s], pen);
+          if (i < U) xl_val[i] = penalize(xv[s], pen, rpen_g, P.pen_rcp != nullptr);
         }
       }
     }
@@ -1109,7 +1110,8 @@ __device__ __attribute__((always_inline, cold)) inline void row_general(KArgs PA
   }
 
   generic_path<T>(GCtx{rowv, bm, xl_val, xl_id, cand, hcnt, hmass, misc, P.out_ids, P.out_probs, P.out_info,
-                      V, nch, nrows_j, row, U, k, flags, pen, tdiv, rdiv, p32, Mx, My, u, pen_on, topk_on, topp_on});
+                      V, nch, nrows_j, row, U, k, flags, pen, rpen_g, tdiv, rdiv, p32, Mx, My, u, pen_on, topk_on,
+                      topp_on, P.pen_rcp != nullptr});
 }
 
 template <typename T>
@@ -1141,7 +1143,7 @@ __global__ __launch_bounds__(NT) void sample_kernel(const KParams P) {
         uint64_t* cand = reinterpret_cast<uint64_t*>(smem + P.off_cand);
         u = (u >= 0.0f) ? (u < 1.0f ? u : 0x1.fffffep-1f) : 0.0f;
         const int st = row_fast<T>(RowArgs{P.logits, P.row_stride, P.vocab, P.hist_ids, P.out_ids, P.out_probs,
-                                           P.out_info},
+                                           P.out_info, P.pen_rcp},
                                    row, src, temp, k, topp, pen, u, h0, h1 - h0, 0, misc, bm, xl_id, xl_val, cand);
         if (__builtin_expect(st == 0, 1)) return;
       }
@@ -1212,7 +1214,7 @@ __global__ __launch_bounds__(NT) void topk_kernel(const KParams P) {
     const unsigned char* rowp = (const unsigned char*)P.logits + src * P.row_stride * T::SZ;
     u = (u >= 0.0f) ? (u < 1.0f ? u : 0x1.fffffep-1f) : 0.0f;
     const int st = topk_stream<T, NPH>(RowArgs{P.logits, P.row_stride, P.vocab, P.hist_ids, P.out_ids, P.out_probs,
-                                          P.out_info},
+                                          P.out_info, P.pen_rcp},
                                   row, rowp, v, early, P.hist_ids + h0, temp, k, topp, pen, u, H, misc, bm, cand);
     if (__builtin_expect(st == 0, 1)) return;
   }
@@ -1313,7 +1315,8 @@ __global__ __launch_bounds__(1024) void debug_scaled_kernel(KParams p, int32_t f
   c.src = src;
   c.rowp = static_cast<const unsigned char*>(p.logits) + src * p.row_stride * T::SZ;
   c.pen = pen;
-  c.rpen = 1.0f / pen;
+  c.recip = p.pen_rcp != nullptr;
+  c.rpen = c.recip ? p.pen_rcp[row] : 1.0f / pen;
   c.tdiv = temp > 0.0f ? __builtin_fmaxf(temp, 1e-6f) : 1.0f;   // sampler.py:42
   c.rdiv = 1.0f / c.tdiv;
   c.scale = c.tdiv != 1.0f;
@@ -1337,7 +1340,7 @@ __global__ __launch_bounds__(1024) void debug_scaled_kernel(KParams p, int32_t f
       for (int e = 0; e < EPC; ++e) {
         float x = T::elem(w, e);
         if ((hb >> e) & 1u)
-          x = formula == DBG_GENERAL ? penalize(x, pen) : pen_rn(x, pen, c.rpen);
+          x = formula == DBG_GENERAL ? penalize(x, pen, c.rpen, c.recip) : pen_rn(x, pen, c.rpen, c.recip);
         y[e] = div_rn(x, c.tdiv, c.rdiv);
       }
     }
@@ -1546,6 +1549,15 @@ int sample_params(const ns_sample_args* a, ns::KParams& p, bool& has_hist) {
   p.top_k = a->top_k;
   p.top_p = a->top_p;
   p.penalty = a->rep_penalty;
+  if (a->penalty_rounding == NS_PENALTY_DIVIDE) {
+    p.pen_rcp = nullptr;
+  } else if (a->penalty_rounding == NS_PENALTY_RECIPROCAL) {
+    if (a->rep_penalty_recip == nullptr)
+      return fail(NS_ERR_INVALID, "NS_PENALTY_RECIPROCAL needs rep_penalty_recip");
+    p.pen_rcp = a->rep_penalty_recip;
+  } else {
+    return fail(NS_ERR_INVALID, "penalty_rounding must be NS_PENALTY_DIVIDE or NS_PENALTY_RECIPROCAL");
+  }
   p.hist_off = a->hist_offsets;
   p.hist_ids = h_ids;
   p.hist_slot = h_slot;
@@ -1913,6 +1925,7 @@ int ns_sample(const ns_sample_args* a, hipStream_t stream) {
     s.top_k = a->top_k;
     s.top_p = a->top_p;
     s.penalty = a->rep_penalty;
+    s.pen_rcp = p.pen_rcp;
     s.hist_off = a->hist_offsets;
     s.hist_ids = p.hist_ids;
     s.hist_slot = p.hist_slot;
@@ -1957,6 +1970,7 @@ int ns_sample(const ns_sample_args* a, hipStream_t stream) {
     w.top_k = a->top_k;
     w.top_p = a->top_p;
     w.penalty = a->rep_penalty;
+    w.pen_rcp = p.pen_rcp;
     w.hist_off = a->hist_offsets;
     w.hist_ids = p.hist_ids;
     w.hist_slot = p.hist_slot;

@@ -63,6 +63,8 @@ struct KParams {
   const int32_t* top_k;
   const float* top_p;
   const float* penalty;
+  const float* pen_rcp;   // [B] RN(1/p) per row: the penalty's positive branch as x * pen_rcp[row]
+                          // (NS_PENALTY_RECIPROCAL), or NULL: the division
   const int32_t* hist_off;
   const int32_t* hist_ids;
   const int32_t* hist_slot;   // device-resident histories: request slot of each row (-1: none), or NULL
@@ -149,9 +151,10 @@ __device__ __forceinline__ float chunk_max(const uint4& c) {
   return m;
 }
 
-__device__ __forceinline__ float penalize(float x, float pen) {
-  // sampler.py:37: torch.where(score < 0, score * p, score / p), float32
-  return x < 0.0f ? x * pen : x / pen;
+__device__ __forceinline__ float penalize(float x, float pen, float rpen, bool recip) {
+  // sampler.py:37: torch.where(score < 0, score * p, score / p), float32; recip: the positive
+  // branch as x * rpen, rpen = RN(1/p), as torch computes it on a GPU
+  return x < 0.0f ? x * pen : (recip ? x * rpen : x / pen);
 }
 
 // Smallest x with RN(x / tdiv) == RN(tau / tdiv): every x whose scaled value

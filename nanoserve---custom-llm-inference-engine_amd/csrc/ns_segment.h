@@ -70,6 +70,8 @@ struct SegParams {
   const int32_t* top_k;
   const float* top_p;
   const float* penalty;
+  const float* pen_rcp;   // [B] RN(1/p) per row: the penalty's positive branch as x * pen_rcp[row]
+                          // (NS_PENALTY_RECIPROCAL), or NULL: the division
   const int32_t* hist_off;
   const int32_t* hist_ids;
   const int32_t* hist_slot;   // device-resident histories: request slot of each row (-1: none), or NULL
@@ -807,8 +809,9 @@ __device__ __forceinline__ void segment_body(const SegParams& P, SegSmem& sm) {
   const bool greedy = temp == 0.0f;
   const float tdiv = temp > 0.0f ? __builtin_fmaxf(temp, 1e-6f) : 1.0f;   // sampler.py:42
   const float rdiv = 1.0f / tdiv;
-  const float rpen = 1.0f / pen;
-  auto pen_val = [&](float x) -> float { return pen_rn(x, pen, rpen); };
+  const bool recip = P.pen_rcp != nullptr;
+  const float rpen = recip ? P.pen_rcp[row] : 1.0f / pen;
+  auto pen_val = [&](float x) -> float { return pen_rn(x, pen, rpen, recip); };
   int32_t flags = 0;
 
   // ---- history: bitmap of the segment and the unique ids in it (set semantics)

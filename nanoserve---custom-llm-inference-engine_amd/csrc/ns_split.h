@@ -64,7 +64,8 @@ template <typename T>
 __device__ __forceinline__ int32_t split_slice(const unsigned char* rowp, const int64_t V, const int c0, const int c1,
                                                const int cpt,
                                                const int32_t* hp, const int32_t H, const float temp, const int32_t k,
-                                               const float pen, Misc* misc, uint32_t* bm, uint64_t* cand,
+                                               const float pen, const float* rcp, Misc* misc, uint32_t* bm,
+                                               uint64_t* cand,
                                                uint64_t* gl, int32_t& m_out, int32_t& rflags) {
   constexpr int EPC = T::EPC;
   const int tid = threadIdx.x;
@@ -79,8 +80,9 @@ __device__ __forceinline__ int32_t split_slice(const unsigned char* rowp, const 
   const bool pen_on = pen != 1.0f && H > 0;        // sampler.py:33
   const float tdiv = temp > 0.0f ? __builtin_fmaxf(temp, 1e-6f) : 1.0f;   // sampler.py:42
   const float rdiv = 1.0f / tdiv;
-  const float rpen = 1.0f / pen;
-  auto pen_val = [&](float x) -> float { return pen_rn(x, pen, rpen); };
+  const bool recip = rcp != nullptr;
+  const float rpen = recip ? *rcp : 1.0f / pen;
+  auto pen_val = [&](float x) -> float { return pen_rn(x, pen, rpen, recip); };
   float* fs = reinterpret_cast<float*>(&misc->red);      // the 128 group maxima
   int32_t* is = reinterpret_cast<int32_t*>(misc->db);    // per-wave NaN / +inf flags
 
@@ -348,7 +350,9 @@ __global__ __launch_bounds__(NT) void split_kernel(const SplitParams SP) {
   if (ok) {
     const unsigned char* rowp = (const unsigned char*)SP.p.logits + src * SP.p.row_stride * T::SZ;
     const int c0 = (int)((int64_t)sl * SP.nch / S), c1 = (int)((int64_t)(sl + 1) * SP.nch / S);
-    fl = split_slice<T>(rowp, V, c0, c1, SP.cpt, SP.p.hist_ids + h0, H, temp, k, pen, misc, bm, cand, gl, m, rfl);
+    fl = split_slice<T>(rowp, V, c0, c1, SP.cpt, SP.p.hist_ids + h0, H, temp, k, pen,
+                        SP.p.pen_rcp != nullptr ? SP.p.pen_rcp + row : nullptr, misc, bm,
+                        cand, gl, m, rfl);
   }
   // hand over, then the arrival ticket: every wave waits for its device-coherent stores
   // before the barrier, the counter increment follows them

@@ -129,8 +129,9 @@ __device__ __forceinline__ int topk_stream(const RowArgs P, const int row, const
   const bool pen_on = pen != 1.0f && H > 0;        // sampler.py:33
   const float tdiv = temp > 0.0f ? __builtin_fmaxf(temp, 1e-6f) : 1.0f;   // sampler.py:42
   const float rdiv = 1.0f / tdiv;
-  const float rpen = 1.0f / pen;
-  auto pen_val = [&](float x) -> float { return pen_rn(x, pen, rpen); };
+  const bool recip = P.pen_rcp != nullptr;
+  const float rpen = recip ? P.pen_rcp[row] : 1.0f / pen;
+  auto pen_val = [&](float x) -> float { return pen_rn(x, pen, rpen, recip); };
   // the group maxima (128 per phase): two phases use the staging region, free until the bound
   float* fs = NPH == 1 ? reinterpret_cast<float*>(&misc->red) : reinterpret_cast<float*>(cand + HIT_OFF64);
   int32_t* is = reinterpret_cast<int32_t*>(misc->db);    // per-wave NaN / +inf flags

@@ -92,6 +92,8 @@ struct WideParams {
   const int32_t* top_k;
   const float* top_p;
   const float* penalty;
+  const float* pen_rcp;   // [B] RN(1/p) per row: the penalty's positive branch as x * pen_rcp[row]
+                          // (NS_PENALTY_RECIPROCAL), or NULL: the division
   const int32_t* hist_off;
   const int32_t* hist_ids;
   const int32_t* hist_slot;   // device-resident histories: request slot of each row (-1: none), or NULL
@@ -284,7 +286,7 @@ struct WRowCtx {
   float tdiv, rdiv, pen, rpen, topp, u;
   float lo_t, lo_pen;   // div_lo of the temperature and of the penalty
   int32_t k, h0, H;
-  bool pen_on, valid, scale;
+  bool pen_on, valid, scale, recip;
 };
 
 template <typename T>
@@ -309,7 +311,8 @@ __device__ __forceinline__ WRowCtx wide_row_ctx(const WideParams& P, int row) {
   c.tdiv = temp > 0.0f ? __builtin_fmaxf(temp, 1e-6f) : 1.0f;   // sampler.py:42
   c.rdiv = 1.0f / c.tdiv;
   c.scale = c.tdiv != 1.0f;
-  c.rpen = 1.0f / c.pen;
+  c.recip = P.pen_rcp != nullptr;
+  c.rpen = c.recip ? P.pen_rcp[row] : 1.0f / c.pen;
   c.lo_t = div_lo(c.tdiv, c.rdiv);
   c.lo_pen = div_lo(c.pen, c.rpen);
   c.rowp = (const unsigned char*)P.logits + c.src * P.row_stride * T::SZ;
@@ -363,7 +366,7 @@ __device__ __forceinline__ void chunk_y_exact(const WRowCtx& c, const uint4& w, 
 #pragma unroll
   for (int e = 0; e < T::EPC; ++e) {
     float x = T::elem(w, e);
-    if ((hb >> e) & 1u) x = x < 0.0f ? x * c.pen : x / c.pen;
+    if ((hb >> e) & 1u) x = x < 0.0f ? x * c.pen : (c.recip ? x * c.rpen : x / c.pen);
     y[e] = x / c.tdiv;
   }
 }
@@ -382,6 +385,8 @@ __device__ __forceinline__ void chunk_y(const WRowCtx& c, const uint4& w, uint32
         const float x = y[e];
         if (x < 0.0f) {
           y[e] = x * c.pen;
+        } else if (c.recip) {
+          y[e] = x * c.rpen;
         } else {
           const float q0 = x * c.rpen;
           const float aq = __builtin_fabsf(q0);

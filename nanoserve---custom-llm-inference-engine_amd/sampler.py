@@ -61,7 +61,7 @@ class PackedRows:
     """Per-row parameters and CSR histories (or device history slots) packed for one call."""
 
     def __init__(self, params: Sequence[SamplingParams], histories: Sequence, vocab: int,
-                 slots: Optional[np.ndarray] = None, slot_max_hist: int = 0):
+                 slots: Optional[np.ndarray] = None, slot_max_hist: int = 0, penalty_rounding: str = "division"):
         B = len(params)
         # greedy rows are encoded as temperature 0 (sampler.py:47-50); others carry the
         # effective float32 temperature, max(t, 1e-6) if t > 0 else 1 (sampler.py:41-46)
@@ -90,6 +90,10 @@ class PackedRows:
         self.top_k = topk
         self.top_p = topp
         self.penalty = pen
+        # the reciprocal penalty multiplies by fl32(1 / p), p the float64 parameter (sampler.py:37
+        # as torch computes it on a GPU)
+        self.penalty_rounding = _lib.PENALTY_ROUNDING[penalty_rounding]
+        self.penalty_recip = (_lib.penalty_reciprocals(rp64) if penalty_rounding == "reciprocal" else None)
         self.max_hist = int(lens.max()) if B else 0
         self.slots = None
         if slots is not None:
@@ -115,7 +119,8 @@ class PackedRows:
         no = 0 if self.hist_offsets is None else B + 1
         if self.slots is not None:   # device histories: the slot of each row in place of the CSR
             no, nh = B, 0
-        buf = np.empty(4 * B + no + nh, dtype=np.int32)
+        nr = B if self.penalty_recip is not None else 0
+        buf = np.empty(4 * B + no + nh + nr, dtype=np.int32)
         buf[0:B] = self.temperature.view(np.int32)
         buf[B:2 * B] = self.top_k
         buf[2 * B:3 * B] = self.top_p.view(np.int32)
@@ -124,7 +129,9 @@ class PackedRows:
             buf[4 * B:5 * B] = self.slots
         elif no:
             buf[4 * B:4 * B + no] = self.hist_offsets
-            buf[4 * B + no:] = self.hist_ids
+            buf[4 * B + no:4 * B + no + nh] = self.hist_ids
+        if nr:
+            buf[4 * B + no + nh:] = self.penalty_recip.view(np.int32)
         host = torch.from_numpy(buf)
         if torch.device(device).type == "cuda":
             host = host.pin_memory()
@@ -135,8 +142,9 @@ class PackedRows:
             "top_p": dev[2 * B:3 * B].view(torch.float32),
             "rep_penalty": dev[3 * B:4 * B].view(torch.float32),
             "hist_offsets": dev[4 * B:4 * B + no] if no and self.slots is None else None,
-            "hist_ids": dev[4 * B + no:] if no and self.slots is None else None,
+            "hist_ids": dev[4 * B + no:4 * B + no + nh] if no and self.slots is None else None,
             "hist_slot": dev[4 * B:5 * B] if self.slots is not None else None,
+            "rep_penalty_recip": dev[4 * B + no + nh:].view(torch.float32) if nr else None,
         }
         return out
 
@@ -222,10 +230,19 @@ class DeviceHistories:
 
 
 class Sampler:
-    """Drop-in for nanoserve.scheduler.sampler.Sampler (sampler.py:17-19)."""
+    """Drop-in for nanoserve.scheduler.sampler.Sampler (sampler.py:17-19).
 
-    def __init__(self, device: torch.device):
+    ``penalty_rounding`` (keyword-only): how the repetition penalty's ``score / p``
+    (sampler.py:37) rounds.  ``"division"`` (default): correctly rounded, as torch computes it on
+    the CPU and as the source line reads.  ``"reciprocal"``: ``score * fl32(1 / fl32(p))``, as
+    torch computes it on a GPU, the reference's default device (config.py:63).
+    """
+
+    def __init__(self, device: torch.device, *, penalty_rounding: str = "division"):
         self.device = device
+        if penalty_rounding not in _lib.PENALTY_ROUNDING:
+            raise ValueError(f"penalty_rounding must be one of {sorted(_lib.PENALTY_ROUNDING)}")
+        self.penalty_rounding = penalty_rounding
         _lib.load()  # fail loudly at construction if the native library is missing
 
     def sample(
@@ -272,9 +289,10 @@ class Sampler:
                 raise ValueError("history_requests must name each request at most once")
             device_histories._check_room(slots)   # before any launch; counted once the append is issued
             max_hist = int(device_histories._len[slots].max()) if B else 0
-            packed = PackedRows(sampling_params_list, None, V, slots=slots, slot_max_hist=max_hist)
+            packed = PackedRows(sampling_params_list, None, V, slots=slots, slot_max_hist=max_hist,
+                                penalty_rounding=self.penalty_rounding)
         else:
-            packed = PackedRows(sampling_params_list, history_token_ids, V)
+            packed = PackedRows(sampling_params_list, history_token_ids, V, penalty_rounding=self.penalty_rounding)
         d = packed.to_device(dev)
         if sample_indices is not None:
             sample_indices = sample_indices.to(device=dev, dtype=torch.int64)
@@ -303,7 +321,8 @@ class Sampler:
             _lib.sample_raw(logits, d["temperature"], d["top_k"], d["top_p"], d["rep_penalty"], uniforms, out,
                             sample_idx=sample_indices, hist_offsets=d["hist_offsets"], hist_ids=d["hist_ids"],
                             max_hist=packed.max_hist, out_probs=probs, row_kinds=packed.row_kinds,
-                            hist_state=hs, hist_slot=d["hist_slot"], hist_append=hs is not None)
+                            hist_state=hs, hist_slot=d["hist_slot"], hist_append=hs is not None,
+                            penalty_rounding=packed.penalty_rounding, rep_penalty_recip=d["rep_penalty_recip"])
             if hs is not None:
                 device_histories._appended(slots)
         res = self._readback(out) if async_ids else out

@@ -30,31 +30,34 @@ implementation whose probabilities differ from these in the last ulps:
 * the top-p *zone*: the sorted positions ``[zone_lo, zone_hi]`` whose float32
   prefix sum lies within 1e-6 of ``float32(top_p)`` (``zone_lo`` = first
   position with prefix > p - 1e-6, ``zone_hi`` = first with prefix > p + 1e-6).
-  An implementation accurate to 1e-6 cuts somewhere inside it, so positions up
-  to ``zone_lo`` are kept and positions after ``zone_hi`` removed by both;
-  ``zone_ids`` lists the token ids at positions ``zone_lo+1 .. zone_hi`` (empty
-  when the cut is unambiguous) and ``zone_mass`` their probability mass.
-* ``topp_boundary``: the zone carries more than 1e-5 of mass (one heavy token
-  sits on the cut), so the kept set itself is ambiguous.
-* ``allowed_ids``: every token id an implementation may return for the row.
-  An implementation whose kept set differs from this one only inside the zone
-  renormalises by ``Q'`` instead of ``Q`` (kept masses, both at least
-  ``Qmin``, the sorted prefix mass at ``zone_lo``), so each of its id-order
-  cumulative masses lies within ``2 * zone_mass / Qmin`` of the oracle's
-  (``zone_mass / Qmin`` from the rescaling of the kept tokens, as much again
-  from the zone tokens themselves).  With ``draw_eps = 1e-6 + 2 * zone_mass /
-  Qmin`` (just 1e-6 on rows without a zone), the allowed ids are the kept or
-  zone tokens ``t`` with ``C[t-1] - draw_eps <= u < C[t] + draw_eps``, ``C``
-  the oracle's float64 cumulative mass in token-id order.  For a row with no
-  boundary within ``draw_eps`` of ``u`` that is exactly the oracle's pick.
+  An implementation accurate to 1e-6 cuts somewhere inside it.  A row whose
+  top-k survivors all hold one value has no zone: every implementation
+  computes exp(0) = 1 for each and 1/n for each probability, so the arithmetic
+  fixes the cut (two tied survivors at top_p = 0.5: the prefix 0.5 is not
+  > 0.5, both are kept).
+* the admissible cuts: every cut ``c`` in the zone (the last kept sorted
+  position; ``c + 1`` tokens kept) is an alternative result of the row, with its
+  own kept set, probabilities (``alternative()``) and allowed ids.  A row
+  without a zone has one alternative, the oracle's own cut.  ``alt_kept[i]``
+  lists the kept counts, ``alt_allowed[i]`` the allowed ids of each.
+* allowed ids of one alternative: the kept tokens ``t`` with
+  ``C[t-1] - 1e-6 <= u < C[t] + 1e-6`` (``C`` that alternative's float64
+  cumulative mass in token-id order, ``C[-1] = 0``), plus its own pick.  For a
+  row with no boundary within 1e-6 of ``u`` that is exactly the pick.
+  ``allowed_ids[i]`` is their union over the row's alternatives: what an
+  implementation may return when its kept count is not known.
 * ``draw_boundary``: ``u`` lies within 1e-6 of the cumulative mass on either
-  side of the picked token (the north-star exemption); ``draw_zone``: more
-  than one id is allowed only because of the zone's widening.
-* ``renorm``: ``zone_mass / Qmin``, the relative change of every kept
-  probability an implementation may show on a row with a zone.
+  side of the picked token (the north-star exemption).
+* ``topp_boundary``: the zone carries more than 1e-5 of mass.
 * ``topp_tie_straddle``: tied values straddle the top-p cut.  The GPU path and
   this oracle agree there (lower id first), and so does ``torch.sort`` on the
   GPU, which the reference runs on (stable on ties, measured on ROCm torch).
+
+The repetition penalty's division (sampler.py:37, ``score / p`` with ``p`` a
+Python float) rounds differently by device: torch on the CPU divides
+(correctly rounded), torch on a GPU multiplies by the float32 reciprocal
+(``x * fl32(1 / fl32(p))``, measured on the MI355X).  ``penalty_rounding``
+selects ``"division"`` (the default) or ``"reciprocal"``.
 
 Pinned by tests/test_oracle_pins.py against closed forms (numpy float32
 penalty and temperature, ``np.partition`` top-k, a numpy stable-argsort top-p,
@@ -92,17 +95,17 @@ class OracleResult:
     topp_cut: np.ndarray          # (B,) int64 last kept position in the sorted order, -1 when top-p is off
     zone_lo: np.ndarray           # (B,) int64 first sorted position of the 1e-6 top-p zone (-1: off)
     zone_hi: np.ndarray           # (B,) int64 last sorted position of the zone
-    zone_mass: np.ndarray         # (B,) float64 probability mass inside the zone
-    zone_ids: list                # B arrays of token ids inside the zone
+    zone_mass: np.ndarray         # (B,) float64 probability mass of sorted positions zone_lo+1 .. zone_hi
+    zone_ids: list                # B arrays of token ids at sorted positions zone_lo+1 .. zone_hi
     nan_row: np.ndarray           # (B,) bool, probabilities replaced by 1/V (sampler.py:77-80)
-    topp_boundary: np.ndarray     # (B,) bool
+    topp_boundary: np.ndarray     # (B,) bool, the zone carries more than 1e-5 of mass
     topp_tie_straddle: np.ndarray # (B,) bool
     draw_boundary: np.ndarray     # (B,) bool, u within 1e-6 of a cumulative mass next to the pick
-    draw_zone: np.ndarray         # (B,) bool, several ids allowed only through the zone's widening
     kept_mass: np.ndarray         # (B,) float64 top-p kept prefix mass (1 when top-p is off)
-    renorm: np.ndarray            # (B,) float64 zone_mass / Qmin (0 without a zone)
-    draw_eps: np.ndarray          # (B,) float64 the row's boundary band
-    allowed_ids: list             # B int64 arrays: the ids an implementation may return
+    allowed_ids: list             # B int64 arrays: the union of the alternatives' allowed ids
+    alt_kept: list                # B int64 arrays: the kept count of each admissible top-p cut
+    alt_allowed: list             # B lists of int64 arrays: the allowed ids of each alternative
+    uniforms: np.ndarray          # (B,) float32 the draw's uniforms
 
     @property
     def exempt(self) -> np.ndarray:
@@ -110,34 +113,101 @@ class OracleResult:
         n = np.array([len(a) for a in self.allowed_ids], dtype=np.int64)
         return (n > 1) & ~self.greedy
 
+    def alternative(self, i: int, n_kept: int):
+        """(probabilities, allowed ids) of row ``i`` under the admissible cut keeping ``n_kept``
+        tokens; ``None`` if ``n_kept`` is not one of ``alt_kept[i]``."""
+        ks = self.alt_kept[i].tolist()
+        if int(n_kept) not in ks:
+            return None
+        j = ks.index(int(n_kept))
+        if int(n_kept) == int(self.n_kept[i]):
+            return self.probs[i], self.alt_allowed[i][j]
+        probs, allowed, _ = _cut_alternative(_topk_row(self.scaled[i], self.topk_thr[i]), int(n_kept) - 1,
+                                             float(self.uniforms[i]))
+        return probs, allowed
+
 
 def effective_temperature(t: float) -> float:
     """sampler.py:42: ``max(t, 1e-6) if t > 0 else 1.0``."""
     return max(t, 1e-6) if t > 0 else 1.0
 
 
-def _apply_penalty(logits: torch.Tensor, penalties: Sequence[float], histories: Sequence) -> None:
-    """sampler.py:31-38, in place on ``logits``."""
+PENALTY_ROUNDINGS = ("division", "reciprocal")
+
+
+def _apply_penalty(logits: torch.Tensor, penalties: Sequence[float], histories: Sequence,
+                   penalty_rounding: str = "division") -> None:
+    """sampler.py:31-38, in place on ``logits``.  ``"division"``: ``score / p`` correctly
+    rounded, as torch computes it on the CPU; ``"reciprocal"``: ``score * fl32(1 / fl32(p))``,
+    as torch computes a tensor divided by a Python float on a GPU."""
+    if penalty_rounding not in PENALTY_ROUNDINGS:
+        raise ValueError(f"penalty_rounding must be one of {PENALTY_ROUNDINGS}")
     for i, p in enumerate(penalties):
         hist = histories[i]
         if p != 1.0 and len(hist) > 0:
             ids = torch.as_tensor(np.asarray(hist, dtype=np.int64))
             score = logits[i].index_select(0, ids)
-            score = torch.where(score < 0, score * p, score / p)
+            if penalty_rounding == "division":
+                pos = score / p
+            else:
+                pos = score * float(np.float32(1.0) / np.float32(p))
+            score = torch.where(score < 0, score * p, pos)
             logits[i].index_copy_(0, ids, score)
 
 
-def penalized_scaled(logits: torch.Tensor, temperature, penalties, histories):
+def penalized_scaled(logits: torch.Tensor, temperature, penalties, histories, penalty_rounding="division"):
     """sampler.py:31-38 then :41-51 on a (B, V) float32 tensor (left unchanged): the logits
     after the repetition penalty, and after the penalty and the temperature division."""
     logits = logits.clone()
-    _apply_penalty(logits, [float(p) for p in penalties], histories)
+    _apply_penalty(logits, [float(p) for p in penalties], histories, penalty_rounding)
     penalized = logits.clone()
     temps = torch.tensor([effective_temperature(float(t)) for t in temperature], dtype=logits.dtype)
     return penalized, logits / temps.unsqueeze(1)
 
 
-def sample(rows, temperature, top_k, top_p, repetition_penalty, histories, uniforms) -> OracleResult:
+def _topk_row(scaled_row: torch.Tensor, thr) -> torch.Tensor:
+    """sampler.py:58: the scaled row with the values below the top-k threshold removed."""
+    if np.isnan(thr):
+        return scaled_row.clone()
+    t = torch.tensor(float(thr), dtype=scaled_row.dtype)
+    return torch.where(scaled_row < t, torch.full_like(scaled_row, -float("inf")), scaled_row)
+
+
+def _draw(probs_row: np.ndarray, u: float):
+    """Inverse CDF (replacing sampler.py:87): the pick, the float64 CDF in token-id order."""
+    V = probs_row.size
+    cdf = probs_row.astype(np.float64).cumsum()
+    j = int(np.searchsorted(cdf, u, side="right"))
+    if j >= V:
+        nz = np.flatnonzero(probs_row > 0)
+        j = int(nz[-1]) if nz.size else V - 1
+    return j, cdf
+
+
+def _allowed(cdf: np.ndarray, kept: np.ndarray, u: float, pick: int) -> np.ndarray:
+    """Kept tokens t with C[t-1] - 1e-6 <= u < C[t] + 1e-6 (C[-1] = 0), and the pick."""
+    V = cdf.size
+    a = int(np.searchsorted(cdf, u - BOUNDARY_EPS, side="right"))
+    b = min(int(np.searchsorted(cdf, u + BOUNDARY_EPS, side="right")), V - 1)
+    cand = np.flatnonzero(kept[a:b + 1]).astype(np.int64) + a if a <= b else np.zeros(0, dtype=np.int64)
+    return np.union1d(cand, np.array([pick], dtype=np.int64)).astype(np.int64)
+
+
+def _cut_alternative(topk_row: torch.Tensor, cut: int, u: float, sorted_idx=None):
+    """Row after top-k, cut after sorted position ``cut`` (value descending, id ascending):
+    its final probabilities, allowed ids and pick (sampler.py:64-80 with a given cut)."""
+    if sorted_idx is None:
+        _, sorted_idx = torch.sort(topk_row, descending=True, stable=True)
+    masked = topk_row.clone()
+    masked[sorted_idx[cut + 1:]] = -float("inf")
+    probs = softmax_exact(masked)
+    pnp = probs.numpy()
+    pick, cdf = _draw(pnp, u)
+    return probs, _allowed(cdf, np.isfinite(masked.numpy()), u, pick), pick
+
+
+def sample(rows, temperature, top_k, top_p, repetition_penalty, histories, uniforms,
+           penalty_rounding: str = "division") -> OracleResult:
     """Run the restated sampler on ``rows`` (B, V) float32 (numpy or CPU tensor)."""
     logits = torch.as_tensor(np.asarray(rows, dtype=np.float32)).clone()
     B, V = logits.shape
@@ -147,7 +217,7 @@ def sample(rows, temperature, top_k, top_p, repetition_penalty, histories, unifo
     penalties = [float(x) for x in repetition_penalty]
     u = np.asarray(uniforms, dtype=np.float32)
 
-    penalized, logits = penalized_scaled(logits, temperature, penalties, histories)
+    penalized, logits = penalized_scaled(logits, temperature, penalties, histories, penalty_rounding)
     greedy = np.array([t == 0.0 for t in temperature], dtype=bool)
     scaled = logits.clone()
 
@@ -171,7 +241,7 @@ def sample(rows, temperature, top_k, top_p, repetition_penalty, histories, unifo
     topp_boundary = np.zeros(B, dtype=bool)
     tie_straddle = np.zeros(B, dtype=bool)
     kept_mass = np.ones(B, dtype=np.float64)
-    qmin = np.ones(B, dtype=np.float64)
+    alt_cuts = [[] for _ in range(B)]     # (cut, allowed ids) of the admissible cuts but the oracle's own
     for i, p in enumerate(top_p):
         if p < 1.0:
             sorted_logits, sorted_idx = torch.sort(logits[i], descending=True, stable=True)
@@ -187,6 +257,10 @@ def sample(rows, temperature, top_k, top_p, repetition_penalty, histories, unifo
 
             J = first_above(p32)
             lo, hi = first_above(p32 - BOUNDARY_EPS), first_above(p32 + BOUNDARY_EPS)
+            n_fin = int(torch.isfinite(sorted_logits).sum())
+            # every survivor holds one value: probabilities 1/n in any arithmetic, no zone
+            if n_fin > 0 and bool(sorted_logits[0] == sorted_logits[n_fin - 1]):
+                lo = hi = J
             topp_cut[i], zone_lo[i], zone_hi[i] = J, lo, hi
             if not np.isnan(c64[-1]):
                 # the cut lands in [lo, hi]: position lo is kept either way, so the
@@ -195,7 +269,9 @@ def sample(rows, temperature, top_k, top_p, repetition_penalty, histories, unifo
                 zone_ids[i] = sorted_idx[lo + 1:hi + 1].numpy().astype(np.int64)
                 topp_boundary[i] = zone_mass[i] > ZONE_MASS_MAX
                 kept_mass[i] = c64[J]
-                qmin[i] = c64[lo]
+                ui = float(u[i])
+                alt_cuts[i] = [(c, _cut_alternative(logits[i], c, ui, sorted_idx)[1])
+                               for c in range(lo, min(hi, n_fin - 1) + 1) if c != J]
             if J + 1 < V and bool(torch.isfinite(sorted_logits[J])):
                 tie_straddle[i] = bool(sorted_logits[J + 1] == sorted_logits[J])
             remove_sorted[..., 1:] = remove_sorted[..., :-1].clone()
@@ -215,63 +291,50 @@ def sample(rows, temperature, top_k, top_p, repetition_penalty, histories, unifo
     argmax = torch.argmax(logits, dim=-1).numpy()
     pnp = probs.numpy()
     nan_np = nan_rows.numpy()
+    n_kept = torch.isfinite(masked).sum(-1).numpy().astype(np.int64)
     ids = np.empty(B, dtype=np.int64)
     draw_boundary = np.zeros(B, dtype=bool)
-    draw_zone = np.zeros(B, dtype=bool)
-    renorm = np.zeros(B, dtype=np.float64)
-    draw_eps = np.full(B, BOUNDARY_EPS, dtype=np.float64)
     allowed = [np.zeros(0, dtype=np.int64) for _ in range(B)]
+    alt_kept = [np.array([n_kept[i]], dtype=np.int64) for i in range(B)]
+    alt_allowed = [[] for _ in range(B)]
     for i in range(B):
         if greedy[i]:
             ids[i] = int(argmax[i])
             allowed[i] = np.array([ids[i]], dtype=np.int64)
+            alt_allowed[i] = [allowed[i]]
             continue
-        cdf = pnp[i].astype(np.float64).cumsum()
         ui = float(u[i])
-        j = int(np.searchsorted(cdf, ui, side="right"))
-        if j >= V:
-            nz = np.flatnonzero(pnp[i] > 0)
-            j = int(nz[-1]) if nz.size else V - 1
+        j, cdf = _draw(pnp[i], ui)
         ids[i] = j
         near = abs(cdf[j] - ui) < BOUNDARY_EPS
         if j > 0:
             near = near or abs(cdf[j - 1] - ui) < BOUNDARY_EPS
         draw_boundary[i] = near
-        if zone_mass[i] > 0.0:
-            renorm[i] = zone_mass[i] / max(qmin[i], 1e-300)
-            draw_eps[i] = BOUNDARY_EPS + 2.0 * renorm[i]
-        eps = draw_eps[i]
-        # kept or zone tokens t with C[t-1] - eps <= u < C[t] + eps (C[-1] = 0)
-        a = int(np.searchsorted(cdf, ui - eps, side="right"))
-        b = min(int(np.searchsorted(cdf, ui + eps, side="right")), V - 1)
-        if a <= b:
-            if nan_np[i]:
-                cand = np.arange(a, b + 1, dtype=np.int64)
-            else:
-                keep = np.isfinite(masked[i, a:b + 1].numpy())
-                cand = np.flatnonzero(keep).astype(np.int64) + a
-                z = zone_ids[i]
-                if len(z):
-                    cand = np.union1d(cand, z[(z >= a) & (z <= b)])
-        else:
-            cand = np.zeros(0, dtype=np.int64)
-        allowed[i] = np.union1d(cand, np.array([j], dtype=np.int64)).astype(np.int64)
-        draw_zone[i] = len(allowed[i]) > 1 and not near
+        kept = np.ones(V, dtype=bool) if nan_np[i] else np.isfinite(masked[i].numpy())
+        own = _allowed(cdf, kept, ui, j)
+        counts, sets = [int(n_kept[i])], [own]
+        for c, a_allowed in alt_cuts[i]:
+            counts.append(c + 1)
+            sets.append(a_allowed)
+        order = np.argsort(counts, kind="stable")
+        alt_kept[i] = np.asarray(counts, dtype=np.int64)[order]
+        alt_allowed[i] = [sets[o] for o in order]
+        allowed[i] = np.unique(np.concatenate(sets)).astype(np.int64)
 
-    n_kept = torch.isfinite(masked).sum(-1).numpy().astype(np.int64)
     return OracleResult(ids=ids, probs=probs, penalized=penalized, scaled=scaled, masked=masked,
                         greedy=greedy, topk_thr=topk_thr, n_kept_topk=n_kept_topk, n_kept=n_kept,
                         topp_cut=topp_cut, zone_lo=zone_lo, zone_hi=zone_hi, zone_mass=zone_mass,
                         zone_ids=zone_ids, nan_row=nan_np, topp_boundary=topp_boundary,
-                        topp_tie_straddle=tie_straddle, draw_boundary=draw_boundary, draw_zone=draw_zone,
-                        kept_mass=kept_mass, renorm=renorm, draw_eps=draw_eps, allowed_ids=allowed)
+                        topp_tie_straddle=tie_straddle, draw_boundary=draw_boundary,
+                        kept_mass=kept_mass, allowed_ids=allowed, alt_kept=alt_kept, alt_allowed=alt_allowed,
+                        uniforms=u.copy())
 
 
-def sample_workload(w, rows_slice=None) -> OracleResult:
+def sample_workload(w, rows_slice=None, penalty_rounding: str = "division") -> OracleResult:
     """Oracle over a ``workloads.Workload`` (optionally a slice of its rows)."""
     sl = rows_slice if rows_slice is not None else slice(None)
     return sample(w.rows[sl], w.temperature[sl], w.top_k[sl], w.top_p[sl], w.repetition_penalty[sl],
-                  w.histories[sl], w.uniforms[sl])
+                  w.histories[sl], w.uniforms[sl], penalty_rounding=penalty_rounding)
 
 
 def reference_restatement_multinomial(logits: torch.Tensor, temperature, top_k, top_p, repetition_penalty,

@@ -5,13 +5,15 @@
 configs.json -- for each workload (c0-c4 at their full sizes, and a bf16 decode
 batch of 256 rows with mixed parameters): the SHA-256 digest of the generated
 inputs (so a run can confirm it regenerated identical logits, parameters,
-histories and uniforms) and, per sampled row, the oracle's token id, the ids an
-implementation may return (the oracle's pick alone unless the uniform lies
-within the row's band of a cumulative-mass boundary), top-k threshold bits,
-kept counts, the ambiguous top-p zone and its renormalisation bound.
+histories and uniforms) and, per sampled row, the oracle's token id, top-k
+threshold bits, kept counts, and the row's admissible top-p cuts (one unless its
+prefix sum comes within 1e-6 of top_p): each cut's kept count and the ids an
+implementation keeping that many tokens may return (the cut's own pick alone
+unless the uniform lies within 1e-6 of one of its cumulative-mass boundaries).
 
 tiny_cases.json -- small hand-built rows with their full inputs and expected
-outputs (token id, threshold, kept counts, final probabilities): ties at the
+outputs (token id, threshold, kept counts, final probabilities of each admissible
+top-p cut): ties at the
 top-k threshold and across the top-p cut, penalties below and above 1 with
 duplicate history ids, NaN / +inf / -inf logits, rows entirely -inf (greedy
 and sampled), greedy rows holding +inf, temperatures below 1e-6 and negative,
@@ -52,14 +54,21 @@ def row_records(r) -> list:
             "n_kept_topk": int(r.n_kept_topk[i]),
             "n_kept": int(r.n_kept[i]),
             "zone": int(len(r.zone_ids[i])),
-            "zone_ids": [int(v) for v in r.zone_ids[i]],
-            "renorm": float(r.renorm[i]),
             "allowed": [int(v) for v in r.allowed_ids[i]],
+            "alt_kept": [int(v) for v in r.alt_kept[i]],
+            "alt_allowed": [[int(v) for v in a] for a in r.alt_allowed[i]],
             "greedy": bool(r.greedy[i]),
             "nan_row": bool(r.nan_row[i]),
             "exempt": bool(r.exempt[i]),
         })
     return out
+
+
+def alt_probs_bits(r, i) -> list:
+    """Final probability bits of each admissible cut of row ``i`` (in ``alt_kept`` order)."""
+    if r.greedy[i] or r.nan_row[i]:
+        return [[f32_bits(v) for v in r.probs[i].numpy()]]
+    return [[f32_bits(v) for v in r.alternative(i, int(k))[0].numpy()] for k in r.alt_kept[i]]
 
 
 def make_configs() -> dict:
@@ -143,6 +152,7 @@ def tiny_cases() -> list:
         rec = row_records(r)
         for i, d in enumerate(rec):
             d["probs_bits"] = [f32_bits(v) for v in r.probs[i].numpy()]
+            d["alt_probs_bits"] = alt_probs_bits(r, i)
         out.append({
             "name": g["name"], "vocab": int(g["rows"].shape[1]),
             "rows_bits": [[f32_bits(v) for v in row] for row in g["rows"]],

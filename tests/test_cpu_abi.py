@@ -4,6 +4,8 @@ arguments without touching a GPU; the host packing mirrors the reference."""
 import ctypes
 import os
 import re
+import subprocess
+import tempfile
 
 import numpy as np
 import pytest
@@ -41,7 +43,22 @@ def test_struct_layout_matches_header():
     body = txt[txt.index("typedef struct ns_sample_args"):txt.index("} ns_sample_args;")]
     names = re.findall(r"^\s*[\w\s\*]+?\b(\w+);", body, flags=re.M)
     assert names == [f[0] for f in L.NsSampleArgs._fields_]
-    assert ctypes.sizeof(L.NsSampleArgs) == 200
+    # every field's offset and the size, as the C compiler lays the header's struct out
+    src = "#include <stdio.h>\n#include <stddef.h>\n#include \"ns_sampling.h\"\nint main(void) {\n"
+    src += '  printf("%zu\\n", sizeof(ns_sample_args));\n'
+    for n in names:
+        src += f'  printf("%zu\\n", offsetof(ns_sample_args, {n}));\n'
+    src += "  return 0;\n}\n"
+    with tempfile.TemporaryDirectory() as d:
+        c, exe = os.path.join(d, "layout.c"), os.path.join(d, "layout")
+        with open(c, "w") as f:
+            f.write(src)
+        rocm = os.environ.get("ROCM_PATH", "/opt/rocm")
+        subprocess.run(["gcc", "-D__HIP_PLATFORM_AMD__", "-I", os.path.dirname(HEADER), "-I",
+                        os.path.join(rocm, "include"), c, "-o", exe], check=True)
+        got = [int(v) for v in subprocess.run([exe], check=True, capture_output=True, text=True).stdout.split()]
+    assert got[0] == ctypes.sizeof(L.NsSampleArgs)
+    assert got[1:] == [getattr(L.NsSampleArgs, n).offset for n in names]
 
 
 def test_lds_bytes_and_argument_errors():

@@ -25,17 +25,17 @@ L = pkg("_lib")
 _ORACLE = {}
 
 
-def _oracle(w):
-    key = (w.name, w.batch)
+def _oracle(w, rounding="division"):
+    key = (w.name, w.batch, rounding)
     if key not in _ORACLE:
-        _ORACLE[key] = O.sample_workload(w)
+        _ORACLE[key] = O.sample_workload(w, penalty_rounding=rounding)
     return _ORACLE[key]
 
 
-def _check(w, device, path="segmented", **kw):
-    print(f"[parity] {w.name} B={w.batch} V={w.vocab} dtype={w.dtype} path={path}", flush=True)
-    g = run_path(w, device, path, **kw)
-    r = _oracle(w)
+def _check(w, device, path="segmented", rounding="division", **kw):
+    print(f"[parity] {w.name} B={w.batch} V={w.vocab} dtype={w.dtype} path={path} penalty={rounding}", flush=True)
+    g = run_path(w, device, path, penalty_rounding=rounding, **kw)
+    r = _oracle(w, rounding)
     fails, stats = compare(g, r)
     stats["paths"] = {int(c): int((g["info"][:, 0] == c).sum()) for c in np.unique(g["info"][:, 0])}
     print(f"[parity] {w.name} {path}: {stats}", flush=True)
@@ -71,6 +71,15 @@ def test_mixed_bf16_decode_batch(device, path):
     set the wide rows (top-k off or k > 64) go to wide_stats_kernel and the rest to
     the one-workgroup-per-row kernel."""
     _check(W.make_mixed_decode(256), device, path)
+
+
+@pytest.mark.parametrize("path", list(PATHS))
+@pytest.mark.parametrize("cfg", [0, 1, 2, 4, "mixed"])
+def test_penalty_reciprocal_rounding(device, cfg, path):
+    """NS_PENALTY_RECIPROCAL: the penalty's positive branch as torch computes it on a GPU, the
+    reference's default device (x * fl32(1 / p)), against the oracle in the same mode."""
+    w = W.make_mixed_decode(256) if cfg == "mixed" else W.make_workload(cfg)
+    _check(w, device, path, rounding="reciprocal")
 
 
 @pytest.mark.parametrize("path", list(PATHS))

@@ -8,7 +8,9 @@ NS_DEBUG_WIDE) and the general per-row code's (IEEE division for the penalty,
 NS_DEBUG_GENERAL).  Per-row and segmented mode differ only in which of these kernels
 run, so each routine is compared with the oracle's float32 tensor expression (the
 tensor ``OracleResult.scaled`` holds), every element, in both history sources (CSR
-histories, and device-resident request slots).  The bar: equal float32 bits; a NaN
+histories, and device-resident request slots), under both penalty roundings (the
+division torch computes on the CPU, and the reciprocal multiply it computes on a GPU,
+NS_PENALTY_RECIPROCAL).  The bar: equal float32 bits; a NaN
 matches a NaN (torch and the GPU may carry different NaN payloads, which no later step
 reads).  Workloads: the batch-8 fp32 decode batch, the mixed decode batch, the
 batch-256 bf16 decode batch with 2048-id histories, the chunked-prefill batch (sample
@@ -35,13 +37,13 @@ FORMULAS = {"stream": L.NS_DEBUG_STREAM, "wide": L.NS_DEBUG_WIDE, "general": L.N
 SOURCES = ("csr", "slots")
 
 
-def oracle_scaled(w):
+def oracle_scaled(w, rounding="division"):
     """The oracle's scaled logits of workload ``w`` (the computation OracleResult.scaled holds)."""
     rows = torch.as_tensor(np.asarray(w.rows, dtype=np.float32))
-    return O.penalized_scaled(rows, w.temperature, w.repetition_penalty, w.histories)[1]
+    return O.penalized_scaled(rows, w.temperature, w.repetition_penalty, w.histories, rounding)[1]
 
 
-def debug_scaled(w, device, formula, source, logits):
+def debug_scaled(w, device, formula, source, logits, rounding="division"):
     """One ns_debug_scaled call over ``w``; the (B, V) float32 bits on the host."""
     B, V = w.batch, w.vocab
     if source == "slots":
@@ -49,10 +51,10 @@ def debug_scaled(w, device, formula, source, logits):
         for r in range(B):
             dh.open(r, w.histories[r])
         packed = S.PackedRows(params_of(w), None, V, slots=dh.slots(list(range(B))),
-                              slot_max_hist=max(len(h) for h in w.histories))
+                              slot_max_hist=max(len(h) for h in w.histories), penalty_rounding=rounding)
         extra = {"hist_state": dh.state}
     else:
-        packed = S.PackedRows(params_of(w), w.histories, V)
+        packed = S.PackedRows(params_of(w), w.histories, V, penalty_rounding=rounding)
         extra = {}
     d = packed.to_device(device)
     if source == "slots":
@@ -64,7 +66,8 @@ def debug_scaled(w, device, formula, source, logits):
     sidx = torch.from_numpy(w.sample_indices).to(device) if w.sample_indices is not None else None
     out = torch.full((B, V), float("nan"), dtype=torch.float32, device=device)
     L.sample_raw(logits, d["temperature"], d["top_k"], d["top_p"], d["rep_penalty"], u, ids, sample_idx=sidx,
-                 max_hist=packed.max_hist, workspace=None, debug_scaled=(formula, out), **extra)
+                 max_hist=packed.max_hist, workspace=None, debug_scaled=(formula, out),
+                 penalty_rounding=packed.penalty_rounding, rep_penalty_recip=d["rep_penalty_recip"], **extra)
     torch.cuda.synchronize()
     return out.cpu().numpy().view(np.uint32)
 
@@ -81,23 +84,26 @@ def compare_bits(name, got, want):
                     f"{gf[r, c]!r} ({got[r, c]:#010x}) vs oracle {wf[r, c]!r} ({want[r, c]:#010x})")
 
 
-def check_workload(w, device):
-    want = oracle_scaled(w)
+def check_workload(w, device, rounding="division"):
+    want = oracle_scaled(w, rounding)
     logits = w.device_logits(device)
     for source in SOURCES:
         for fname, formula in FORMULAS.items():
-            print(f"[scaled] {w.name} B={w.batch} V={w.vocab} dtype={w.dtype} {fname} {source}", flush=True)
-            compare_bits(f"{w.name} {fname} {source}", debug_scaled(w, device, formula, source, logits), want)
+            print(f"[scaled] {w.name} B={w.batch} V={w.vocab} dtype={w.dtype} {fname} {source} {rounding}", flush=True)
+            compare_bits(f"{w.name} {fname} {source} {rounding}",
+                         debug_scaled(w, device, formula, source, logits, rounding), want)
 
 
+@pytest.mark.parametrize("rounding", ["division", "reciprocal"])
 @pytest.mark.parametrize("cfg", [0, 1, 2, 4])
-def test_configs(device, cfg):
-    check_workload(W.make_workload(cfg), device)
+def test_configs(device, cfg, rounding):
+    check_workload(W.make_workload(cfg), device, rounding)
 
 
+@pytest.mark.parametrize("rounding", ["division", "reciprocal"])
 @pytest.mark.parametrize("case", G.tiny(), ids=[c["name"] for c in G.tiny()])
-def test_tiny_cases(device, case):
-    check_workload(G.tiny_workload(case), device)
+def test_tiny_cases(device, case, rounding):
+    check_workload(G.tiny_workload(case), device, rounding)
 
 
 def random_bits_workload(name, B, V, seed, bf16):
@@ -121,10 +127,11 @@ def random_bits_workload(name, B, V, seed, bf16):
                       histories=hists, uniforms=rng.random(B, dtype=np.float32), n_rows_total=B)
 
 
+@pytest.mark.parametrize("rounding", ["division", "reciprocal"])
 @pytest.mark.parametrize("bf16", [False, True])
-def test_random_bit_patterns(device, bf16):
+def test_random_bit_patterns(device, bf16, rounding):
     check_workload(random_bits_workload(f"scaled-bits{'-bf16' if bf16 else ''}", 24, 8195, 901 + int(bf16), bf16),
-                   device)
+                   device, rounding)
 
 
 def test_invalid_rows_written_as_nan(device):

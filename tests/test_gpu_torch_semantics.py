@@ -8,9 +8,10 @@ restatement and where it does not:
 * ``score / p.repetition_penalty`` with a Python float (sampler.py:37) is NOT a
   division on the device: torch multiplies by ``fl32(1.0 / p)``, the reciprocal
   taken in double precision from the Python float and rounded once.  It differs
-  from the correctly rounded ``x / fl32(p)`` of the CPU (and of the kernels) by
-  one ulp on a share of the inputs; the oracle keeps the division, which is also
-  what "the penalty divides positive logits" states.
+  from the correctly rounded ``x / fl32(p)`` of the CPU by one ulp on a share of
+  the inputs.  The oracle and the kernels offer both: the division by default,
+  the reciprocal with ``penalty_rounding="reciprocal"`` (NS_PENALTY_RECIPROCAL),
+  and the reference's own penalty lines run on the device equal that mode.
 * ``score * p`` (sampler.py:37) and ``logits / temps`` (sampler.py:51, a tensor
   divisor) are the correctly rounded float32 operations on both.
 * ``torch.sort(descending=True)`` (sampler.py:64) orders tied values by ascending
@@ -46,6 +47,34 @@ def test_penalty_division_by_python_scalar(device):
         mul = (xg * p).cpu().numpy()
         with np.errstate(over="ignore"):
             assert np.array_equal(_bits(mul), _bits((x * np.float32(p)).astype(np.float32))), p
+
+
+def test_reference_penalty_on_device_is_the_reciprocal_mode(device):
+    """sampler.py:31-38 as written, run by torch on the GPU (the reference's default device), on
+    the c2 rows with their Zipf histories, equals the oracle's reciprocal penalty bit for bit,
+    and differs from its division mode on some elements."""
+    import importlib
+
+    W = importlib.import_module("nanoserve---custom-llm-inference-engine_amd.workloads")
+    from oracle import sampler_oracle as O
+
+    w = W.make_workload(2, batch=32)
+    logits = torch.from_numpy(np.ascontiguousarray(w.rows, dtype=np.float32)).to(device)
+    for i in range(w.batch):
+        p = float(w.repetition_penalty[i])
+        ids = torch.from_numpy(np.asarray(w.histories[i], dtype=np.int64)).to(device)
+        if p != 1.0 and ids.numel() > 0:
+            score = logits[i].index_select(0, ids)
+            score = torch.where(score < 0, score * p, score / p)
+            logits[i].index_copy_(0, ids, score)
+    got = logits.cpu().numpy()
+    rows = torch.from_numpy(np.ascontiguousarray(w.rows, dtype=np.float32))
+    recip = O.penalized_scaled(rows, w.temperature, w.repetition_penalty, w.histories, "reciprocal")[0].numpy()
+    div = O.penalized_scaled(rows, w.temperature, w.repetition_penalty, w.histories, "division")[0].numpy()
+    assert np.array_equal(_bits(got), _bits(recip))
+    n_diff = int(np.sum(_bits(got) != _bits(div)))
+    print(f"[torch] reference penalty on the device vs the division: {n_diff} elements differ")
+    assert n_diff > 0
 
 
 def test_temperature_division_by_tensor(device):

@@ -186,6 +186,82 @@ def test_topp_cumsum_accumulates_in_float64():
     assert len(want) < len(x)
 
 
+def test_topp_exact_ties_have_no_zone():
+    """Survivors that all tie have probabilities 1/n in any arithmetic, so the cut is fixed:
+    two tied tokens at top_p 0.5 give prefixes 0.5 and 1.0, 0.5 is not > 0.5, both stay
+    (Fraction brute force); a 1e-6 zone would have admitted keeping one."""
+    x = np.array([2.0, 7.0, 7.0, 1.0, -3.0], dtype=F32)
+    r = run(x, k=1, p=0.5, t=1.3, u=0.75)
+    assert brute_topp(np.where(x == 7.0, x, -np.inf), 0.5) == {1, 2}
+    assert r.alt_kept[0].tolist() == [2] and int(r.n_kept[0]) == 2
+    assert r.probs[0].numpy()[[1, 2]].tolist() == [0.5, 0.5]
+    assert r.allowed_ids[0].tolist() == [2]                  # u = 0.75 lies inside token 2's interval
+    # four ties at top_p 0.5: prefixes 0.25, 0.5, 0.75; the crossing token (prefix 0.5 is not
+    # > 0.5) stays, so three are kept, and no alternative either
+    r = run([3.0, 3.0, 3.0, 3.0], p=0.5, u=0.1)
+    assert brute_topp([3.0] * 4, 0.5) == {0, 1, 2}
+    assert r.alt_kept[0].tolist() == [3]
+
+
+def _closed_form_alternative(y, n_keep, u):
+    """Probabilities and allowed ids of keeping the n_keep largest values (id ascending on
+    ties), in float64 with math.fsum, and the inverse-CDF candidates within 1e-6 of u."""
+    order = sorted(range(len(y)), key=lambda i: (-float(y[i]), i))[:n_keep]
+    e = np.zeros(len(y))
+    m = max(float(y[i]) for i in order)
+    for i in order:
+        e[i] = math.exp(float(y[i]) - m)
+    q = (e / math.fsum(e)).astype(F32)
+    c = np.cumsum(q.astype(np.float64))
+    ok = [t for t in order if (c[t - 1] if t else 0.0) - 1e-6 <= u < c[t] + 1e-6]
+    return q, ok
+
+
+def test_topp_admissible_cuts_closed_form():
+    """A prefix sum within 1e-6 of top_p makes two cuts admissible.  Each alternative's
+    probabilities are the float64 softmax over its own kept set (closed form, not the oracle's
+    code) and its allowed ids the CDF intervals within 1e-6 of u; a cut outside the zone is
+    not admissible."""
+    # probabilities 0.5, 0.3, 0.2 (sorted ids 0, 2, 1): prefixes 0.5, 0.8, 1.0
+    x = np.log(np.array([0.5, 0.2, 0.3], dtype=np.float64)).astype(F32)
+    q = O.softmax_exact(torch.from_numpy(x)).numpy()
+    top_p = float(np.float32(np.float64(q[0]) + np.float64(q[2])) - np.float32(4e-7))  # 0.8 - 4e-7
+    for u in (0.1, 0.49, 0.6, 0.95):
+        r = run(x, p=top_p, u=u)
+        assert r.alt_kept[0].tolist() == [2, 3], r.alt_kept[0]
+        assert r.alternative(0, 1) is None and r.alternative(0, 4) is None
+        for n_keep in (2, 3):
+            probs, allowed = r.alternative(0, n_keep)
+            qc, ok = _closed_form_alternative(x.astype(np.float64), n_keep, u)
+            np.testing.assert_allclose(probs.numpy(), qc, rtol=1e-6, atol=0)
+            assert sorted(allowed.tolist()) == sorted(ok), (u, n_keep, allowed, ok)
+        assert set(r.allowed_ids[0].tolist()) == set(r.alternative(0, 2)[1].tolist()) | set(
+            r.alternative(0, 3)[1].tolist())
+    # away from the zone: one alternative, and it is the oracle's own result
+    r = run(x, p=0.7, u=0.6)
+    assert r.alt_kept[0].tolist() == [int(r.n_kept[0])] == [2]
+
+
+def test_penalty_reciprocal_rounding_closed_form():
+    """penalty_rounding="reciprocal": positive logits times float32(1 / float32(p)) (torch on a
+    GPU for ``score / p``), negative ones times p as before; it differs from the division."""
+    rng = np.random.default_rng(11)
+    x = rng.normal(0, 3, size=8192).astype(F32)
+    ids = np.arange(0, 8192, 2)
+    for pv in (1.1, 1.2, 0.8, 1.3):
+        rows = O.sample(x[None], [1.0], [-1], [1.0], [pv], [ids.tolist()], np.array([0.5], dtype=F32),
+                        penalty_rounding="reciprocal")
+        want = x.copy()
+        sel = x[ids]
+        want[ids] = np.where(sel < 0, sel * F32(pv), sel * (F32(1) / F32(pv)))
+        assert np.array_equal(rows.penalized[0].numpy().view(np.int32), want.view(np.int32)), pv
+        div = O.sample(x[None], [1.0], [-1], [1.0], [pv], [ids.tolist()], np.array([0.5], dtype=F32))
+        assert not torch.equal(rows.penalized, div.penalized), pv
+    with pytest.raises(ValueError):
+        O.sample(x[None], [1.0], [-1], [1.0], [1.1], [ids.tolist()], np.array([0.5], dtype=F32),
+                 penalty_rounding="fp64")
+
+
 # ------------------------------------------------- softmax, NaN, argmax, draw
 def test_softmax_closed_form_and_masked_zeros():
     rng = np.random.default_rng(3)
