@@ -55,8 +55,9 @@ implementation whose probabilities differ from these in the last ulps:
 
 The repetition penalty's division (sampler.py:37, ``score / p`` with ``p`` a
 Python float) rounds differently by device: torch on the CPU divides
-(correctly rounded), torch on a GPU multiplies by the float32 reciprocal
-(``x * fl32(1 / fl32(p))``, measured on the MI355X).  ``penalty_rounding``
+(correctly rounded), torch on a GPU multiplies by the reciprocal of the
+Python float taken in float64 and rounded once (``x * fl32(1 / p)``, measured on
+the MI355X).  ``penalty_rounding``
 selects ``"division"`` (the default) or ``"reciprocal"``.
 
 Pinned by tests/test_oracle_pins.py against closed forms (numpy float32
@@ -138,8 +139,9 @@ PENALTY_ROUNDINGS = ("division", "reciprocal")
 def _apply_penalty(logits: torch.Tensor, penalties: Sequence[float], histories: Sequence,
                    penalty_rounding: str = "division") -> None:
     """sampler.py:31-38, in place on ``logits``.  ``"division"``: ``score / p`` correctly
-    rounded, as torch computes it on the CPU; ``"reciprocal"``: ``score * fl32(1 / fl32(p))``,
-    as torch computes a tensor divided by a Python float on a GPU."""
+    rounded, as torch computes it on the CPU; ``"reciprocal"``: ``score * fl32(1 / p)``, the
+    float64 reciprocal of the Python float rounded once, as torch computes a tensor divided by
+    a Python float on a GPU."""
     if penalty_rounding not in PENALTY_ROUNDINGS:
         raise ValueError(f"penalty_rounding must be one of {PENALTY_ROUNDINGS}")
     for i, p in enumerate(penalties):
@@ -150,7 +152,7 @@ def _apply_penalty(logits: torch.Tensor, penalties: Sequence[float], histories: 
             if penalty_rounding == "division":
                 pos = score / p
             else:
-                pos = score * float(np.float32(1.0) / np.float32(p))
+                pos = score * float(np.float32(1.0 / p))
             score = torch.where(score < 0, score * p, pos)
             logits[i].index_copy_(0, ids, score)
 

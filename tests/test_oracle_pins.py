@@ -243,8 +243,9 @@ def test_topp_admissible_cuts_closed_form():
 
 
 def test_penalty_reciprocal_rounding_closed_form():
-    """penalty_rounding="reciprocal": positive logits times float32(1 / float32(p)) (torch on a
-    GPU for ``score / p``), negative ones times p as before; it differs from the division."""
+    """penalty_rounding="reciprocal": positive logits times float32(1 / p), the float64
+    reciprocal rounded once (torch on a GPU for ``score / p``), negative ones times p as before;
+    it differs from the division, and for p = 1.1 from the float32 reciprocal 1 / float32(p)."""
     rng = np.random.default_rng(11)
     x = rng.normal(0, 3, size=8192).astype(F32)
     ids = np.arange(0, 8192, 2)
@@ -253,10 +254,14 @@ def test_penalty_reciprocal_rounding_closed_form():
                         penalty_rounding="reciprocal")
         want = x.copy()
         sel = x[ids]
-        want[ids] = np.where(sel < 0, sel * F32(pv), sel * (F32(1) / F32(pv)))
+        want[ids] = np.where(sel < 0, sel * F32(pv), sel * F32(1.0 / pv))
         assert np.array_equal(rows.penalized[0].numpy().view(np.int32), want.view(np.int32)), pv
         div = O.sample(x[None], [1.0], [-1], [1.0], [pv], [ids.tolist()], np.array([0.5], dtype=F32))
         assert not torch.equal(rows.penalized, div.penalized), pv
+        if pv == 1.1:
+            assert F32(1.0 / pv) != F32(1) / F32(pv)
+            single = x[ids] * (F32(1) / F32(pv))
+            assert np.any(single[x[ids] > 0] != rows.penalized[0].numpy()[ids][x[ids] > 0])
     with pytest.raises(ValueError):
         O.sample(x[None], [1.0], [-1], [1.0], [1.1], [ids.tolist()], np.array([0.5], dtype=F32),
                  penalty_rounding="fp64")
