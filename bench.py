@@ -204,6 +204,38 @@ def lm_head_handoff(L, lib, dev, w, st, stream, iters=50):
     return out
 
 
+def engine_step_legs(sampler, w, dh, reqs, kw, logits, steps=200):
+    """The engine's sampling step with its host work (engine.py:238-254): the next step's
+    SamplingParams list built and packed (``Sampler.pack``), device histories appended in the
+    kernel.  Synchronous: sample, read the ids (``.tolist()``), then the host work of the next
+    step.  Pipelined: sample with ``async_ids``, do the next step's host work while the GPU
+    samples and the ids travel, then read them.  Returns milliseconds per step for each."""
+    C = _pkg("config")
+
+    def host_work():
+        params = [C.SamplingParams(temperature=float(w.temperature[i]), top_k=int(w.top_k[i]),
+                                   top_p=float(w.top_p[i]), repetition_penalty=float(w.repetition_penalty[i]))
+                  for i in range(w.batch)]
+        return sampler.pack(params, None, w.vocab, device_histories=dh, history_requests=reqs)
+
+    def run(pipelined):
+        packed = host_work()
+        for _ in range(5):
+            sampler.sample(logits, packed, None, device_histories=dh, **kw).tolist()
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            if pipelined:
+                h = sampler.sample(logits, packed, None, device_histories=dh, async_ids=True, **kw)
+                packed = host_work()
+                h.tolist()
+            else:
+                sampler.sample(logits, packed, None, device_histories=dh, **kw).tolist()
+                packed = host_work()
+        return (time.perf_counter() - t0) / steps * 1e3
+
+    return run(False), run(True)
+
+
 def lm_head_sweep(L, dev, batches=(256, 128, 64, 16, 1), iters=20):
     """The logits producer alone over decode batch sizes: hidden (B, 2048) bf16 times a
     random-init (128256, 2048) bf16 lm_head, through ns_lm_head_bf16 on the weight as
@@ -582,18 +614,7 @@ def main(argv=None):
         ids = sampler.sample(sets[0]["logits"], params, None, device_histories=dh, history_requests=reqs, **kw)
     ids.tolist()
     wrap_dev_ms = (time.perf_counter() - t1) / nwrap * 1e3
-    # pipelined: each step reads the previous step's ids (async readback), as an engine that
-    # overlaps the copy with its next scheduling step would
-    t1 = time.perf_counter()
-    prev = None
-    for _ in range(nwrap):
-        h = sampler.sample(sets[0]["logits"], params, None, device_histories=dh, history_requests=reqs,
-                           async_ids=True, **kw)
-        if prev is not None:
-            prev.tolist()
-        prev = h
-    prev.tolist()
-    wrap_pipe_ms = (time.perf_counter() - t1) / nwrap * 1e3
+    step_sync_ms, step_pipe_ms = engine_step_legs(sampler, w, dh, reqs, kw, sets[0]["logits"])
     del dh
     producer = lm_head_handoff(L, lib, dev, w, sets[0], stream) if args.config == WORKLOAD_CFG else {}
     floor_us = read_floor(L, sets, stream)
@@ -629,7 +650,8 @@ def main(argv=None):
                 "extra": {"algorithmic_bytes_per_call": bytes_per_call, "kernel_us": ms_per_step * 1e3,
                           "wall_s": wall, "wrapper_inclusive_ms": wrap_ms,
                           "wrapper_inclusive_ms_device_histories": wrap_dev_ms,
-                          "wrapper_pipelined_ms_device_histories_async_ids": wrap_pipe_ms, **floor}}
+                          "engine_step_sync_ids_ms": step_sync_ms, "engine_step_async_ids_ms": step_pipe_ms,
+                          **floor}}
         print(json.dumps(line), flush=True)
         return 0
     line = {
@@ -657,7 +679,7 @@ def main(argv=None):
                   "wrapper_inclusive_rows_per_s": w.batch / (wrap_ms * 1e-3),
                   "wrapper_inclusive_ms_device_histories": wrap_dev_ms,
                   "wrapper_inclusive_rows_per_s_device_histories": w.batch / (wrap_dev_ms * 1e-3),
-                  "wrapper_pipelined_ms_device_histories_async_ids": wrap_pipe_ms,
+                  "engine_step_sync_ids_ms": step_sync_ms, "engine_step_async_ids_ms": step_pipe_ms,
                   "kernel_source_sha16": kernel_source_hash(), **floor, **small, **producer, **attention},
     }
     print(json.dumps(line), flush=True)

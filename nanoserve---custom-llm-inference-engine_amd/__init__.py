@@ -10,6 +10,7 @@ The directory name is not a Python identifier; import it with
 repository root on ``sys.path``).
 """
 from .config import SamplingParams
-from .sampler import DeviceHistories, PackedRows, SampledIds, Sampler, effective_temperature
+from .sampler import DeviceHistories, PackedRows, ReadbackRing, SampledIds, Sampler, effective_temperature
 
-__all__ = ["Sampler", "SamplingParams", "PackedRows", "DeviceHistories", "SampledIds", "effective_temperature"]
+__all__ = ["Sampler", "SamplingParams", "PackedRows", "DeviceHistories", "SampledIds", "ReadbackRing",
+           "effective_temperature"]

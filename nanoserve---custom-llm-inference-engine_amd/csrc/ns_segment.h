@@ -1033,7 +1033,7 @@ __device__ __forceinline__ void segment_body(const SegParams& P, SegSmem& sm) {
   // increment follows them.
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
-  if (tid == 0) sm.last = atomicAdd(&P.counters[row], 1) == S - 1;
+  if (tid == 0) sm.last = arrive_last(&P.counters[row], S);
   __syncthreads();
   if (!sm.last) return;
   if (tid == 0) __hip_atomic_store(&P.counters[row], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);

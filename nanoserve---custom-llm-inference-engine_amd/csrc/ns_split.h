@@ -361,7 +361,7 @@ __global__ __launch_bounds__(NT) void split_kernel(const SplitParams SP) {
              ((uint64_t)(uint32_t)(fl | (rfl << 8)) << 32) | (uint32_t)m);
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
-  if (tid == 0) misc->ib[1] = atomicAdd(&SP.counters[row], 1) == S - 1 ? 1 : 0;
+  if (tid == 0) misc->ib[1] = arrive_last(&SP.counters[row], S) ? 1 : 0;
   __syncthreads();
   if (misc->ib[1] == 0) return;
   if (tid == 0) __hip_atomic_store(&SP.counters[row], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);

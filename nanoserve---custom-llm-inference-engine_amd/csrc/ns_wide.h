@@ -471,7 +471,7 @@ template <typename SM>
 __device__ __forceinline__ bool wide_arrive(int32_t* counter, int S, SM* sm) {
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
-  if (threadIdx.x == 0) sm->last = atomicAdd(counter, 1) == S - 1;
+  if (threadIdx.x == 0) sm->last = arrive_last(counter, S);
   __syncthreads();
   const bool last = sm->last != 0;
   if (last && threadIdx.x == 0) __hip_atomic_store(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);

@@ -119,16 +119,20 @@ def workspace_bytes(total_q: int, num_heads_q: int, num_kv_heads: int, head_dim:
 _COUNTERS = {}
 
 
-def counters_for(device, n: int):
-    """A zero-filled int32 buffer of at least ``n`` arrival counters kept per device. Every call
-    leaves its counters at zero whatever its shape, so the buffer stays valid for all calls of one
-    stream; it only grows."""
+def counters_for(device, n: int, stream=None):
+    """A zero-filled int32 buffer of at least ``n`` arrival counters kept per device and stream
+    (calls on one stream run one after another; calls on two streams may overlap, so they never
+    share counters).  Every call leaves its counters at zero whatever its shape, so the buffer
+    stays valid for all calls of its stream; it only grows, zero-filled on ``stream``."""
     import torch
 
-    key = torch.device(device).index or 0
+    dev = torch.device(device)
+    s = stream if stream is not None else torch.cuda.current_stream(dev)
+    key = (dev.index or 0, int(s.cuda_stream))
     buf = _COUNTERS.get(key)
     if buf is None or buf.numel() < n:
-        buf = torch.zeros(max(n, 1 << 16), dtype=torch.int32, device=device)
+        with torch.cuda.stream(s):
+            buf = torch.zeros(max(n, 1 << 16), dtype=torch.int32, device=dev)
         _COUNTERS[key] = buf
     return buf
 
@@ -160,7 +164,9 @@ def paged_attention_hip(query, k_cache, v_cache, block_tables, seq_lens, query_s
     element that the kernel ORs STATUS_* bits into (a block id outside the cache, a sequence longer
     than ``max_seq_len``): a caller that wants the check reads it after the call. ``workspace``
     (uint8, any contents) and ``counters`` (int32, zero-filled once; every call leaves it so) are
-    allocated per call, resp. taken from this module's per-device buffer, when not given.
+    allocated per call, resp. taken from this module's per-device, per-stream buffer, when not
+    given.  ``stream``: a ``torch.cuda.Stream`` or a raw HIP stream handle, default the current
+    stream; the call's own temporaries are made on it, so nothing orders them against another.
     """
     import torch
 
@@ -168,6 +174,23 @@ def paged_attention_hip(query, k_cache, v_cache, block_tables, seq_lens, query_s
     dev = query.device
     if dev.type != "cuda":
         raise PagedAttentionError("paged_attention_hip needs device tensors")
+    if stream is None:
+        s = torch.cuda.current_stream(dev)
+    elif isinstance(stream, torch.cuda.Stream):
+        s = stream
+    else:
+        s = torch.cuda.ExternalStream(int(stream), device=dev)
+    with torch.cuda.stream(s):
+        return _paged_attention_on(lib, s, query, k_cache, v_cache, block_tables, seq_lens, query_start_loc,
+                                   query_lens, scale, block_size, max_seq_len, out, workspace, counters, status)
+
+
+def _paged_attention_on(lib, s, query, k_cache, v_cache, block_tables, seq_lens, query_start_loc, query_lens,
+                        scale, block_size, max_seq_len, out, workspace, counters, status):
+    """paged_attention_hip with ``s`` the current stream: every temporary below is made on it."""
+    import torch
+
+    dev = query.device
     total_q, hq, d = query.shape
     nb, bs, hkv, dk = k_cache.shape
     if v_cache.shape != k_cache.shape or dk != d:
@@ -195,13 +218,15 @@ def paged_attention_hip(query, k_cache, v_cache, block_tables, seq_lens, query_s
         out = torch.empty_like(query)
     elif out.shape != query.shape or out.dtype != query.dtype or out.device != dev:
         raise PagedAttentionError("out must match query's shape, dtype and device")
+    elif out.stride(-1) != 1:
+        raise PagedAttentionError("out must have a unit head_dim stride")
     need = workspace_bytes(total_q, hq, hkv, d, max_seq_len)
     if need and workspace is None:
         workspace = torch.empty(need, dtype=torch.uint8, device=dev)
     elif need and workspace.numel() * workspace.element_size() < need:
         raise PagedAttentionError(f"workspace of {need} bytes needed")
     if need and counters is None:
-        counters = counters_for(dev, total_q * hkv)
+        counters = counters_for(dev, total_q * hkv, s)
     elif need and (counters.dtype != torch.int32 or counters.device != dev or counters.numel() < total_q * hkv):
         raise PagedAttentionError(f"counters must be an int32 device tensor of at least {total_q * hkv} entries")
     if status is not None and (status.dtype != torch.int32 or status.device != dev or status.numel() < 1):
@@ -215,9 +240,7 @@ def paged_attention_hip(query, k_cache, v_cache, block_tables, seq_lens, query_s
         bt.stride(0) if bt.dim() == 2 else 0,
         total_q, num_seqs, hq, hkv, d, bs, nb, bt.shape[1] if bt.dim() == 2 else 0, max_seq_len,
         _dtype_code(query.dtype), float(scale))
-    if stream is None:
-        stream = torch.cuda.current_stream(dev).cuda_stream
-    _check(lib.ns_paged_attention(ctypes.byref(a), ctypes.c_void_p(stream)))
+    _check(lib.ns_paged_attention(ctypes.byref(a), ctypes.c_void_p(int(s.cuda_stream))))
     return out
 
 

@@ -29,9 +29,9 @@ Additions, all keyword-only and optional:
   (sampler.py:34); here each request's ids are copied once when it starts and
   every sampled token is appended on the device by the kernel that draws it.
 * ``async_ids``: return a ``SampledIds`` handle instead of the tensor.  Its ids
-  are copied into pinned host memory behind an event on the same stream, so
-  ``.tolist()`` (engine.py:250) waits only when the engine reads them and the
-  next scheduler step can run meanwhile.
+  are copied into a pinned host buffer of the sampler's ``ReadbackRing`` behind
+  an event on the same stream, so ``.tolist()`` (engine.py:250) waits only when
+  the engine reads them and the next step's host work can run meanwhile.
 
 Differences that the engine cannot observe: the caller's logits are not
 modified in place (the reference's penalty writes into them, sampler.py:38,
@@ -73,9 +73,14 @@ class PackedRows:
         pen = rp64.astype(np.float32)
         lens = np.zeros(B, dtype=np.int64)
         hist_rows = [None] * B
+        # every row's history length (the seeded uniform's counter), penalized or not
+        self.history_lengths = [0] * B
+        self.seeds = [p.seed for p in params]
+        self.vocab = int(vocab)
         if histories is not None:
             for i in range(min(B, len(histories))):
                 h = histories[i]
+                self.history_lengths[i] = len(h) if h is not None else 0
                 # only penalised rows index their history (sampler.py:33)
                 if rp64[i] != 1.0 and len(h) > 0:
                     a = np.asarray(h, dtype=np.int64)
@@ -149,6 +154,55 @@ class PackedRows:
         return out
 
 
+class _ReadbackSlot:
+    """One pinned host buffer and its event, reused by successive ``SampledIds``."""
+
+    __slots__ = ("host", "event", "owner")
+
+    def __init__(self, n: int):
+        self.host = torch.empty(max(int(n), 256), dtype=torch.int64, pin_memory=True)
+        self.event = torch.cuda.Event()
+        self.owner = None
+
+
+class ReadbackRing:
+    """A fixed ring of pinned host buffers and events for ``async_ids``: nothing is allocated
+    per call once the ring has filled (a buffer grows only for a larger batch).
+
+    A slot is reused ``depth`` calls later.  If its previous handle has not been read by then,
+    that handle first copies its ids out of the slot (waiting for its own copy), so a handle
+    stays readable however long it is kept; an engine that reads each step's ids before the
+    step after next never waits there.
+    """
+
+    def __init__(self, depth: int = 4):
+        if depth < 1:
+            raise ValueError("depth must be at least 1")
+        self.depth = int(depth)
+        self._slots: List[_ReadbackSlot] = []
+        self._next = 0
+
+    def readback(self, out: torch.Tensor) -> "SampledIds":
+        """Queue the copy of ``out`` (int64, on the GPU) into the next slot behind an event on
+        the current stream of ``out``'s device."""
+        n = int(out.numel())
+        if len(self._slots) < self.depth:
+            self._slots.append(_ReadbackSlot(n))
+            slot = self._slots[-1]
+        else:
+            slot = self._slots[self._next]
+            self._next = (self._next + 1) % self.depth
+            if slot.owner is not None:
+                slot.owner._detach()
+            if slot.host.numel() < n:
+                slot.host = torch.empty(n, dtype=torch.int64, pin_memory=True)
+        slot.host[:n].copy_(out, non_blocking=True)
+        slot.event.record(torch.cuda.current_stream(out.device))
+        h = SampledIds(out, slot, n)
+        slot.owner = h
+        return h
+
+
 class SampledIds:
     """Sampled ids on their way to the host: ``.tolist()`` waits for the copy.
 
@@ -156,20 +210,30 @@ class SampledIds:
     tells without waiting whether the host copy has landed.
     """
 
-    def __init__(self, tensor: torch.Tensor, host: torch.Tensor, event):
+    def __init__(self, tensor: torch.Tensor, slot: "_ReadbackSlot", n: int):
         self.tensor = tensor
-        self._host = host
-        self._event = event
+        self._slot = slot
+        self._n = n
+        self._ids: Optional[List[int]] = None
+
+    def _detach(self) -> None:
+        """Copy the ids out of the ring slot before the slot is reused."""
+        if self._ids is None:
+            self._slot.event.synchronize()
+            self._ids = self._slot.host[:self._n].tolist()
+        self._slot = None
 
     def ready(self) -> bool:
-        return bool(self._event.query())
+        return self._ids is not None or bool(self._slot.event.query())
 
     def tolist(self) -> List[int]:
-        self._event.synchronize()
-        return self._host.tolist()
+        if self._ids is None:
+            self._slot.event.synchronize()
+            self._ids = self._slot.host[:self._n].tolist()
+        return list(self._ids)
 
     def __len__(self) -> int:
-        return int(self.tensor.numel())
+        return self._n
 
 
 class DeviceHistories:
@@ -234,8 +298,9 @@ class Sampler:
 
     ``penalty_rounding`` (keyword-only): how the repetition penalty's ``score / p``
     (sampler.py:37) rounds.  ``"division"`` (default): correctly rounded, as torch computes it on
-    the CPU and as the source line reads.  ``"reciprocal"``: ``score * fl32(1 / fl32(p))``, as
-    torch computes it on a GPU, the reference's default device (config.py:63).
+    the CPU and as the source line reads.  ``"reciprocal"``: ``score * fl32(1 / p)`` (the float64
+    reciprocal rounded once), as torch computes it on a GPU, the reference's default device
+    (config.py:63).
     """
 
     def __init__(self, device: torch.device, *, penalty_rounding: str = "division"):
@@ -243,6 +308,7 @@ class Sampler:
         if penalty_rounding not in _lib.PENALTY_ROUNDING:
             raise ValueError(f"penalty_rounding must be one of {sorted(_lib.PENALTY_ROUNDING)}")
         self.penalty_rounding = penalty_rounding
+        self._ring: Optional[ReadbackRing] = None   # pinned buffers and events of async_ids
         _lib.load()  # fail loudly at construction if the native library is missing
 
     def sample(
@@ -261,6 +327,8 @@ class Sampler:
     ):
         """Sample one token per row; returns an int64 tensor on ``logits.device``.
 
+        ``sampling_params_list`` may also be the ``PackedRows`` of ``pack()`` (its
+        ``history_token_ids`` and ``history_requests`` were taken there).
         With ``return_probs=True`` returns ``(ids, probs)`` where ``probs`` holds the
         final (B, V) probabilities of every non-greedy row (sampler.py:76-80).  With
         ``device_histories`` the histories are those of ``history_requests`` (one request
@@ -275,41 +343,70 @@ class Sampler:
             raise ValueError("logits must be 2-D (rows, vocab)")
         if logits.stride(1) != 1:
             logits = logits.contiguous()
-        B = len(sampling_params_list)
+        prepacked = isinstance(sampling_params_list, PackedRows)
+        B = sampling_params_list.batch if prepacked else len(sampling_params_list)
         N, V = logits.shape
         if sample_indices is None and B != N:
             raise ValueError(f"{B} sampling params for {N} logits rows")
         dev = logits.device
+        if prepacked:
+            packed = sampling_params_list
+            if packed.vocab != V:
+                raise ValueError(f"rows packed for vocab {packed.vocab}, logits have {V}")
+            if packed.penalty_rounding != _lib.PENALTY_ROUNDING[self.penalty_rounding]:
+                raise ValueError("rows packed with another penalty rounding")
+            if (packed.slots is not None) != (device_histories is not None):
+                raise ValueError("rows packed with device histories need device_histories, and only they")
         slots = None
         if device_histories is not None:
-            if history_requests is None or len(history_requests) != B:
-                raise ValueError("history_requests must name one request per sampled row")
-            slots = device_histories.slots(history_requests)
-            if len(set(slots.tolist())) != B:
-                raise ValueError("history_requests must name each request at most once")
+            if prepacked:
+                slots = packed.slots
+            else:
+                if history_requests is None or len(history_requests) != B:
+                    raise ValueError("history_requests must name one request per sampled row")
+                slots = device_histories.slots(history_requests)
+                if len(set(slots.tolist())) != B:
+                    raise ValueError("history_requests must name each request at most once")
             device_histories._check_room(slots)   # before any launch; counted once the append is issued
             max_hist = int(device_histories._len[slots].max()) if B else 0
-            packed = PackedRows(sampling_params_list, None, V, slots=slots, slot_max_hist=max_hist,
-                                penalty_rounding=self.penalty_rounding)
-        else:
+            if prepacked:
+                packed.max_hist = max_hist
+            else:
+                packed = PackedRows(sampling_params_list, None, V, slots=slots, slot_max_hist=max_hist,
+                                    penalty_rounding=self.penalty_rounding)
+        elif not prepacked:
             packed = PackedRows(sampling_params_list, history_token_ids, V, penalty_rounding=self.penalty_rounding)
         d = packed.to_device(dev)
         if sample_indices is not None:
-            sample_indices = sample_indices.to(device=dev, dtype=torch.int64)
+            # a row outside the logits is refused here, as the reference's index_select
+            # (engine.py:234) would raise: for a host list or CPU tensor without a sync; for a
+            # device tensor only when device histories are appended to (one sync), since the
+            # kernel gives such a row id -1 and appends nothing, which the host lengths must know
+            if not (isinstance(sample_indices, torch.Tensor) and sample_indices.device.type == "cuda"):
+                si = np.asarray(sample_indices.cpu() if isinstance(sample_indices, torch.Tensor) else sample_indices,
+                                dtype=np.int64).reshape(-1)
+                if si.size and (si.min() < 0 or si.max() >= N):
+                    raise IndexError(f"sample index {int(si[(si < 0) | (si >= N)][0])} out of range for {N} rows")
+                sample_indices = torch.from_numpy(si).to(dev)
+            else:
+                sample_indices = sample_indices.to(device=dev, dtype=torch.int64)
+                if device_histories is not None and sample_indices.numel() > 0:
+                    lo, hi = (int(v) for v in torch.aminmax(sample_indices))
+                    if lo < 0 or hi >= N:
+                        raise IndexError(f"sample index {lo if lo < 0 else hi} out of range for {N} rows")
             if sample_indices.numel() != B:
                 raise ValueError("sample_indices must have one entry per sampling params")
         if uniforms is None:
             # rows whose request carries a seed draw a Philox uniform keyed by it and counted by
             # the history length (reproducible); the rest from ``generators`` or the device RNG
-            seeded = [i for i, p in enumerate(sampling_params_list) if p.seed is not None]
+            seeded = [i for i, s in enumerate(packed.seeds) if s is not None]
             uniforms = self._draw_uniforms(B, dev, generators, skip=set(seeded))
             if seeded:
                 if device_histories is not None:
                     steps = [int(device_histories._len[int(slots[i])]) for i in seeded]
                 else:
-                    steps = [len(history_token_ids[i]) if history_token_ids is not None and
-                             history_token_ids[i] is not None else 0 for i in seeded]
-                _lib.seeded_uniforms([sampling_params_list[i].seed for i in seeded], steps, seeded, uniforms)
+                    steps = [packed.history_lengths[i] for i in seeded]
+                _lib.seeded_uniforms([packed.seeds[i] for i in seeded], steps, seeded, uniforms)
         else:
             uniforms = uniforms.to(device=dev, dtype=torch.float32).contiguous()
             if uniforms.numel() != B:
@@ -328,15 +425,33 @@ class Sampler:
         res = self._readback(out) if async_ids else out
         return (res, probs) if return_probs else res
 
+    def pack(self, sampling_params_list: List[SamplingParams], history_token_ids=None, vocab: int = 0, *,
+             device_histories: Optional[DeviceHistories] = None,
+             history_requests: Optional[Sequence] = None) -> PackedRows:
+        """The host half of ``sample``: the per-row parameters and histories packed for one call.
+
+        ``sample(logits, packed, None, ...)`` takes the result in place of the parameters list
+        (with the same ``device_histories``), so an engine can pack the next step's rows while
+        the GPU samples this one and ``SampledIds`` carries its ids home (engine.py:238-250).
+        """
+        if device_histories is None:
+            return PackedRows(sampling_params_list, history_token_ids, vocab, penalty_rounding=self.penalty_rounding)
+        B = len(sampling_params_list)
+        if history_requests is None or len(history_requests) != B:
+            raise ValueError("history_requests must name one request per sampled row")
+        slots = device_histories.slots(history_requests)
+        if len(set(slots.tolist())) != B:
+            raise ValueError("history_requests must name each request at most once")
+        return PackedRows(sampling_params_list, None, vocab, slots=slots,
+                          slot_max_hist=int(device_histories._len[slots].max()) if B else 0,
+                          penalty_rounding=self.penalty_rounding)
+
     def _readback(self, out: torch.Tensor) -> SampledIds:
-        """Copy ``out`` into a pinned host buffer behind an event on the current stream."""
-        # one pinned buffer per call (torch's caching host allocator recycles them once
-        # their handle is gone), so any number of calls may be in flight
-        host = torch.empty(int(out.numel()), dtype=torch.int64, pin_memory=True)
-        host.copy_(out, non_blocking=True)
-        ev = torch.cuda.Event()
-        ev.record(torch.cuda.current_stream(out.device))
-        return SampledIds(out, host, ev)
+        """Copy ``out`` into the next pinned buffer of the sampler's ring behind an event on the
+        current stream (no allocation once the ring has filled)."""
+        if self._ring is None:
+            self._ring = ReadbackRing()
+        return self._ring.readback(out)
 
     @staticmethod
     def _draw_uniforms(B: int, dev, generators, skip=frozenset()) -> torch.Tensor:

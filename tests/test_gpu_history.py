@@ -219,3 +219,54 @@ def test_async_ids_match_and_overlap(device):
         assert h.tolist() == sync_ids[step]
         assert h.ready()
         assert h.tensor.cpu().tolist() == sync_ids[step]
+
+
+def test_out_of_range_sample_index_is_refused_and_lengths_stay(device):
+    """A sample index outside the logits is refused before any launch (the reference's
+    index_select at engine.py:234 raises there), from a host list and from a device tensor with
+    device histories, so the host lengths never count an append the kernel skipped."""
+    w = W.make_workload(1, batch=8)
+    params = params_of(w)
+    sampler = S.Sampler(device)
+    dh = S.DeviceHistories(device, 8, capacity=1024)
+    for r in range(8):
+        dh.open(r, list(map(int, w.histories[r])))
+    before = [dh.length(r) for r in range(8)]
+    logits = w.device_logits(device)
+    u = torch.from_numpy(np.asarray(w.uniforms, dtype=np.float32)).to(device)
+    bad = list(range(8))
+    bad[5] = 8
+    for sidx in (bad, torch.tensor(bad, device=device), [-1] + list(range(1, 8))):
+        with pytest.raises(IndexError):
+            sampler.sample(logits, params, None, sample_indices=sidx, uniforms=u, device_histories=dh,
+                           history_requests=list(range(8)))
+    assert [dh.length(r) for r in range(8)] == before
+    torch.cuda.synchronize()
+    assert read_state(dh, list(range(8))) == [list(map(int, h)) for h in w.histories]
+    # a valid call afterwards appends once per row
+    ids = sampler.sample(logits, params, None, sample_indices=list(range(8)), uniforms=u, device_histories=dh,
+                         history_requests=list(range(8)))
+    assert [dh.length(r) for r in range(8)] == [b + 1 for b in before]
+    assert read_state(dh, list(range(8))) == [list(map(int, h)) + [int(i)] for h, i in zip(w.histories,
+                                                                                          ids.tolist())]
+
+
+def test_readback_ring_reuses_its_buffers(device):
+    """async_ids through the ring: more handles in flight than the ring's depth, read late and
+    out of order, all equal the synchronous ids; the ring holds depth buffers, no more."""
+    w = W.make_workload(2, batch=32)
+    params = params_of(w)
+    sampler = S.Sampler(device)
+    hist = [list(map(int, h)) for h in w.histories]
+    base = w.device_logits(device)
+    u = torch.from_numpy(np.asarray(w.uniforms, dtype=np.float32)).to(device)
+    handles, want = [], []
+    for step in range(11):
+        logits = torch.roll(base, shifts=313 * step, dims=1).contiguous()
+        want.append(sampler.sample(logits, params, hist, uniforms=u).tolist())
+        handles.append(sampler.sample(logits, params, hist, uniforms=u, async_ids=True))
+    ring = sampler._ring
+    assert len(ring._slots) == ring.depth
+    for step in [10, 3, 0, 7, 9, 1, 2, 4, 5, 6, 8]:
+        assert handles[step].tolist() == want[step], step
+        assert handles[step].ready()

@@ -141,3 +141,28 @@ def test_more_partitions_than_the_lds_weight_table(device):
     case = make_case(40, [70000], [1], hq=8, hkv=1, d=128)
     assert A.workspace_bytes(1, 8, 1, 128, 70000) == 1 * 8 * 1094 * (128 + 2) * 4
     check(case, device)
+
+
+def test_side_stream_and_output_stride(device):
+    """A call on a side stream (its temporaries and counters made on that stream) equals the
+    call on the current stream bit for bit; an output whose head_dim stride is not 1 is refused
+    (the kernel writes out[token, head, d] with a unit stride along d)."""
+    case = make_case(21, [1500, 7, 300], [1, 1, 20])
+    want = run(case, device)
+    side = torch.cuda.Stream(device=device)
+    c = to_device(case, device)
+    torch.cuda.synchronize()
+    got = A.paged_attention_hip(c["query"], c["k_cache"], c["v_cache"], c["block_tables"], c["seq_lens"],
+                                c["query_start_loc"], c["query_lens"], c["scale"], c["block_size"], stream=side)
+    side.synchronize()
+    assert torch.equal(got, want)
+    raw = A.paged_attention_hip(c["query"], c["k_cache"], c["v_cache"], c["block_tables"], c["seq_lens"],
+                                c["query_start_loc"], c["query_lens"], c["scale"], c["block_size"],
+                                stream=side.cuda_stream)
+    side.synchronize()
+    assert torch.equal(raw, want)
+    q = c["query"]
+    bad = torch.empty((q.shape[0], q.shape[1], q.shape[2] * 2), dtype=q.dtype, device=device)[:, :, ::2]
+    with pytest.raises(A.PagedAttentionError, match="unit head_dim stride"):
+        A.paged_attention_hip(q, c["k_cache"], c["v_cache"], c["block_tables"], c["seq_lens"],
+                              c["query_start_loc"], c["query_lens"], c["scale"], c["block_size"], out=bad)
