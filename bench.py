@@ -307,6 +307,59 @@ def measured_traffic():
     return int(vals["traffic_bytes_per_launch"])
 
 
+STAMP_NAMES = ("entry", "wave0_streamed", "last_wave_streamed", "bound_barrier", "list_barrier", "order_barrier",
+               "drawn")
+
+
+def phase_stamps(L, dev, w, sets, ws, stream, reps=20, calls=20):
+    """Where the top-k kernel's time goes, from its phase stamps: libns_sampling_stamps.so is
+    the sampler built with NS_PHASE_STAMPS, whose top-k kernel stores the shader clock
+    (s_memtime) of each workgroup at entry, when wave 0 and when the last wave have streamed and
+    reduced their share of the row, after the bound's barrier, after the candidate list's
+    barrier, after the ordering's barrier and when the id is drawn.  ``reps`` times: ``calls``
+    back-to-back calls over the rotating input sets, then the last call's stamps (every
+    workgroup's, in steady state) are read.  Returns the median clocks of each phase over all
+    rows and repetitions, and the same in microseconds at the clock rate that makes the median
+    workgroup's span equal the per-call time measured by events in the same run."""
+    import torch
+
+    so = os.path.join(ROOT, PKG, "libns_sampling_stamps.so")
+    lib = ctypes.CDLL(so)
+    lib.ns_sample.restype = ctypes.c_int
+    lib.ns_phase_stamps_set.restype = ctypes.c_int
+    buf = torch.zeros(w.batch * 8, dtype=torch.int64, device=dev)
+    if lib.ns_phase_stamps_set(ctypes.c_void_p(buf.data_ptr())) != 0:
+        raise RuntimeError("ns_phase_stamps_set failed")
+    cargs = [make_args(L, st, ws) for st in sets]
+    sh = ctypes.c_void_p(int(stream.cuda_stream))
+    rows = []
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    t_ms = 0.0
+    for r in range(reps):
+        torch.cuda.synchronize()
+        e0.record(stream)
+        for i in range(calls):
+            if lib.ns_sample(ctypes.byref(cargs[(r * calls + i) % ROTATE]), sh) != 0:
+                raise RuntimeError("stamped ns_sample failed")
+        e1.record(stream)
+        torch.cuda.synchronize()
+        t_ms += e0.elapsed_time(e1)
+        rows.append(buf.view(w.batch, 8).cpu().numpy().astype(np.int64))
+    lib.ns_phase_stamps_set(ctypes.c_void_p(0))
+    st = np.concatenate(rows)[:, :len(STAMP_NAMES)]
+    d = np.diff(st, axis=1)
+    us_per_call = t_ms / (reps * calls) * 1e3
+    span = float(np.median(st[:, -1] - st[:, 0]))
+    per_us = span / us_per_call
+    out = {"stamped_kernel_us": us_per_call, "median_workgroup_span_clocks": span, "clocks_per_us": per_us}
+    for j in range(d.shape[1]):
+        name = f"{STAMP_NAMES[j]}->{STAMP_NAMES[j + 1]}"
+        out[name + "_clocks"] = float(np.median(d[:, j]))
+        out[name + "_us"] = float(np.median(d[:, j])) / per_us
+    return out
+
+
 def cpu_model():
     try:
         with open("/proc/cpuinfo") as f:
@@ -528,6 +581,8 @@ def main(argv=None):
                     help="time only the logits producer (lm_head GEMM) over decode batch sizes and exit")
     ap.add_argument("--paged-attention", action="store_true",
                     help="time only the paged-attention decode leg (64 rows x 2048 positions) and exit")
+    ap.add_argument("--phase-stamps", action="store_true",
+                    help="print where the top-k kernel's time goes (the stamps library) and exit")
     args = ap.parse_args(argv)
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: the sampler's rows are independent and this build runs on a single "
@@ -560,6 +615,10 @@ def main(argv=None):
     stream = torch.cuda.current_stream(dev)
     sh = ctypes.c_void_p(int(stream.cuda_stream))
     bytes_per_call = W.algorithmic_bytes(w)
+    if args.phase_stamps:
+        print(json.dumps({"phase_stamps": phase_stamps(L, dev, w, sets, ws, stream), "config": args.config}),
+              flush=True)
+        return 0
 
     def step(i):
         rc = lib.ns_sample(ctypes.byref(cargs[i % ROTATE]), sh)

@@ -23,6 +23,9 @@ PA_OUT = os.path.join(HERE, "libns_paged_attention.so")
 # the benchmark's bandwidth reference (not part of the sampler's ABI)
 PROBE_SRC = os.path.join(HERE, "csrc", "ns_probe.hip")
 PROBE_OUT = os.path.join(HERE, "libns_probe.so")
+# the sampler with the top-k kernel's phase stamps (bench.py --phase-stamps; never loaded by
+# the package)
+STAMPS_OUT = os.path.join(HERE, "libns_sampling_stamps.so")
 ARCH = os.environ.get("NS_OFFLOAD_ARCH", "gfx950")
 
 
@@ -31,9 +34,8 @@ def hipcc() -> str:
     return os.path.join(rocm, "bin", "hipcc")
 
 
-def _compile(src: str, out: str, verbose: bool) -> None:
-    tmp = out + ".tmp"
-    cmd = [
+def _command(src: str, out: str, defines=()) -> list:
+    return [
         hipcc(), f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC", "-shared",
         "-ffp-contract=off", "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
         "-Wno-unused-command-line-argument",
@@ -42,21 +44,30 @@ def _compile(src: str, out: str, verbose: bool) -> None:
         # another exec-mask count (measured: the wide path 5-7% faster without it)
         "-mllvm", "-amdgpu-atomic-optimizer-strategy=None",
         "-I", os.path.join(ROOT, "include"), "-I", os.path.join(HERE, "csrc"),
-        src, "-o", tmp,
+        *[f"-D{d}" for d in defines], src, "-o", out + ".tmp",
     ]
-    if verbose:
-        print(" ".join(cmd), flush=True)
-    res = subprocess.run(cmd, capture_output=True, text=True)
-    if res.returncode != 0:
-        sys.stderr.write(res.stdout + res.stderr)
-        raise RuntimeError(f"hipcc failed with exit code {res.returncode}")
-    os.replace(tmp, out)
 
 
 def build(verbose: bool = False) -> str:
-    _compile(SRC, OUT, verbose)
-    _compile(PA_SRC, PA_OUT, verbose)
-    _compile(PROBE_SRC, PROBE_OUT, verbose)
+    """Compile every library, the four hipcc processes side by side."""
+    jobs = [(SRC, OUT, ()), (PA_SRC, PA_OUT, ()), (PROBE_SRC, PROBE_OUT, ()),
+            (SRC, STAMPS_OUT, ("NS_PHASE_STAMPS",))]
+    procs = []
+    for src, out, defines in jobs:
+        cmd = _command(src, out, defines)
+        if verbose:
+            print(" ".join(cmd), flush=True)
+        procs.append((out, subprocess.Popen(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)))
+    failed = []
+    for out, proc in procs:
+        log, _ = proc.communicate()
+        if proc.returncode != 0:
+            sys.stderr.write(log)
+            failed.append(os.path.basename(out))
+        else:
+            os.replace(out + ".tmp", out)
+    if failed:
+        raise RuntimeError(f"hipcc failed for {', '.join(failed)}")
     return OUT
 
 

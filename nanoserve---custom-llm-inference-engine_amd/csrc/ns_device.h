@@ -17,6 +17,24 @@ constexpr int NWAVE = NT / 64;    // 16 wave64s
 __device__ __forceinline__ int lane_id() { return threadIdx.x & 63; }
 __device__ __forceinline__ int wave_id() { return threadIdx.x >> 6; }
 
+// Phase stamps of the top-k streaming kernel, in the library built with NS_PHASE_STAMPS
+// only (the shipped library compiles them away): the shader clock (s_memtime) at phase
+// boundaries of each workgroup, stored to ns_stamp_buf[workgroup * NS_STAMPS + slot] by
+// one lane.  No work is skipped; each stamp waits for the wave's outstanding scalar and LDS
+// operations, which lengthens the path it sits on slightly.
+constexpr int NS_STAMPS = 8;
+#ifdef NS_PHASE_STAMPS
+__device__ uint64_t* ns_stamp_buf;
+#define NS_STAMP_LANE(slot, cond)                                                           \
+  do {                                                                                       \
+    if ((cond) && ns::ns_stamp_buf != nullptr)                                               \
+      ns::ns_stamp_buf[(int64_t)blockIdx.x * ns::NS_STAMPS + (slot)] = __builtin_amdgcn_s_memtime(); \
+  } while (0)
+#else
+#define NS_STAMP_LANE(slot, cond) do { } while (0)
+#endif
+#define NS_STAMP(slot) NS_STAMP_LANE(slot, threadIdx.x == 0)
+
 // IEEE-754-2019 maximum/minimum: NaN-propagating (v_maximum3_f32 on gfx950).
 __device__ __forceinline__ float fmax_nan(float a, float b) { return __builtin_elementwise_maximum(a, b); }
 __device__ __forceinline__ float fmin_nan(float a, float b) { return __builtin_elementwise_minimum(a, b); }

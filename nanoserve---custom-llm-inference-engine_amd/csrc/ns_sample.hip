@@ -1114,12 +1114,11 @@ __device__ __attribute__((always_inline, cold)) inline void row_general(KArgs PA
                       topp_on, P.pen_rcp != nullptr});
 }
 
+// The per-row code for one row: the streaming path for greedy and small-k rows that fit in
+// registers, the general code otherwise.  P is the kernel's first argument (the general code
+// reads it through the argument segment).
 template <typename T>
-__global__ __launch_bounds__(NT) void sample_kernel(const KParams P) {
-  const int row = blockIdx.x;
-  // rows the segment kernel or the wide path resolved carry status 0 (every other row 1):
-  // those workgroups end before anything else is read
-  if (P.status != nullptr && P.status[row] == 0) return;
+__device__ __forceinline__ void sample_row(const KParams P, const int row) {
   // every per-row parameter is requested before any is used: one round trip to memory
   // ahead of the row's stream instead of a chain of dependent ones
   const float temp = P.temperature[row];
@@ -1152,6 +1151,41 @@ __global__ __launch_bounds__(NT) void sample_kernel(const KParams P) {
   row_general<T>((KArgs)__builtin_amdgcn_kernarg_segment_ptr(), row);
 }
 
+template <typename T>
+__global__ __launch_bounds__(NT) void sample_kernel(const KParams P) {
+  const int row = blockIdx.x;
+  // rows the segment kernel or the wide path resolved carry status 0 (every other row 1):
+  // those workgroups end before anything else is read
+  if (P.status != nullptr && P.status[row] == 0) return;
+  sample_row<T>(P, row);
+}
+
+// The last launch of a call with wide rows, one workgroup per sampled row: a wide row the
+// cut pass planned is ordered, cut and drawn (wide_final_row); the rows the earlier launches
+// left (status 1), and a planned row the final step hands back, take the per-row code, in
+// the same workgroup.  The wide step and the per-row code share the dynamic LDS region.
+template <typename T>
+__global__ __launch_bounds__(NT) void final_kernel(const KParams P, const WideParams W) {
+  const int row = blockIdx.x;
+  const int32_t step = W.rows[row].step;
+  if (step == WSTEP_CUT || step == WSTEP_FULL) {
+    extern __shared__ __align__(16) unsigned char smem[];
+    wide_final_row<T>(W, *reinterpret_cast<WideSmemCut*>(smem), row);
+    // the final step writes status 1 (by thread 0) for a row it hands back; the word past the
+    // wide step's LDS tells every thread, and the per-row code reuses the region only after
+    // all have read it
+    int32_t* rest = reinterpret_cast<int32_t*>(smem + sizeof(WideSmemCut));
+    if (threadIdx.x == 0) *rest = P.status[row];
+    __syncthreads();
+    const int32_t handed_back = *rest;
+    __syncthreads();
+    if (handed_back == 0) return;
+  } else if (P.status[row] == 0) {
+    return;
+  }
+  sample_row<T>(P, row);
+}
+
 // One workgroup per sampled row for calls whose rows are all top-k rows with
 // 1 <= k <= KFAST (the host's NS_KIND_SMALL_K hint): the row's loads are issued before the
 // per-row parameters return (topk_stream, ns_topk.h).  A row of another kind, or one that
@@ -1167,6 +1201,7 @@ __device__ __forceinline__ uint32_t vload_word(const void* base, int32_t i, uint
 template <typename T, int NPH>
 __global__ __launch_bounds__(NT) void topk_kernel(const KParams P) {
   const int row = blockIdx.x;
+  NS_STAMP(0);
   // Without sample indices or device-resident history slots the row and its history range
   // need no dependent load: the per-row parameters are requested first (vector loads, served
   // in issue order ahead of the row) and the row's first chunks right behind them, before the
@@ -1321,7 +1356,7 @@ __global__ __launch_bounds__(1024) void debug_scaled_kernel(KParams p, int32_t f
   c.rdiv = 1.0f / c.tdiv;
   c.scale = c.tdiv != 1.0f;
   c.lo_t = div_lo(c.tdiv, c.rdiv);
-  c.lo_pen = div_lo(pen, c.rpen);
+  c.lo_pen = c.recip ? __builtin_inff() : div_lo(pen, c.rpen);   // as wide_row_ctx
   c.pen_on = pen != 1.0f && h1 > h0;                           // sampler.py:33
   const int64_t nch = (V + EPC - 1) / EPC;
   const int64_t nfull = V / EPC;
@@ -1498,7 +1533,9 @@ int device_info(int dev, DevInfo& out) {
                          reinterpret_cast<const void*>(&ns::topk_kernel<ns::BF16, 2>),
                          reinterpret_cast<const void*>(&ns::topk_kernel<ns::F32, 2>),
                          reinterpret_cast<const void*>(&ns::split_kernel<ns::BF16>),
-                         reinterpret_cast<const void*>(&ns::split_kernel<ns::F32>)};
+                         reinterpret_cast<const void*>(&ns::split_kernel<ns::F32>),
+                         reinterpret_cast<const void*>(&ns::final_kernel<ns::BF16>),
+                         reinterpret_cast<const void*>(&ns::final_kernel<ns::F32>)};
     for (const void* fn : fns) {
       e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, d.max_lds);
       if (e != hipSuccess) return fail(NS_ERR_HIP, std::string("hipFuncSetAttribute: ") + hipGetErrorString(e));
@@ -1587,6 +1624,16 @@ int sample_params(const ns_sample_args* a, ns::KParams& p, bool& has_hist) {
 extern "C" {
 
 int ns_abi_version(void) { return NS_ABI_VERSION; }
+
+#ifdef NS_PHASE_STAMPS
+// The stamps library only (built with NS_PHASE_STAMPS, never shipped): where the top-k
+// streaming kernel stores its phase stamps, NS_STAMPS uint64 per workgroup (NULL: none).
+int ns_phase_stamps_set(void* buf) {
+  const hipError_t e = hipMemcpyToSymbol(HIP_SYMBOL(ns::ns_stamp_buf), &buf, sizeof(buf));
+  if (e != hipSuccess) return fail(NS_ERR_HIP, std::string("hipMemcpyToSymbol: ") + hipGetErrorString(e));
+  return NS_OK;
+}
+#endif
 
 int ns_hist_state_bytes(int32_t n_slots, int32_t capacity, uint64_t* bytes) {
   if (bytes == nullptr) return fail(NS_ERR_INVALID, "bytes is NULL");
@@ -2002,15 +2049,24 @@ int ns_sample(const ns_sample_args* a, hipStream_t stream) {
     }
     if (bf) hipLaunchKernelGGL((ns::wide_cut_kernel<ns::BF16>), g, bs, 0, stream, w);
     else hipLaunchKernelGGL((ns::wide_cut_kernel<ns::F32>), g, bs, 0, stream, w);
+    // 3) one workgroup per row: the wide rows' final step, and every row the launches above
+    //    left, in one launch (the wide step's LDS and the per-row code's share one region)
     const dim3 gr((unsigned)a->n_sample), br(ns::NT);
-    if (bf) hipLaunchKernelGGL((ns::wide_final_kernel<ns::BF16>), gr, br, 0, stream, w);
-    else hipLaunchKernelGGL((ns::wide_final_kernel<ns::F32>), gr, br, 0, stream, w);
+    const int32_t wlds = (int32_t)sizeof(ns::WideSmemCut) + 16;   // the wide step, and one word past it
+    const int32_t flds = lds > wlds ? lds : wlds;
+    if (flds > max_lds)
+      return fail(NS_ERR_INVALID, "LDS requirement " + std::to_string(flds) + " exceeds device limit " +
+                                      std::to_string(max_lds));
+    if (bf) hipLaunchKernelGGL((ns::final_kernel<ns::BF16>), gr, br, flds, stream, p, w);
+    else hipLaunchKernelGGL((ns::final_kernel<ns::F32>), gr, br, flds, stream, p, w);
     if (a->out_probs != nullptr) {
+      // every token's probability of the rows the wide path drew (after their final step)
       if (bf) hipLaunchKernelGGL((ns::wide_probs_kernel<ns::BF16>), g, bs, 0, stream, w);
       else hipLaunchKernelGGL((ns::wide_probs_kernel<ns::F32>), g, bs, 0, stream, w);
     }
     e = hipGetLastError();
     if (e != hipSuccess) return fail(NS_ERR_HIP, std::string("wide kernel launch: ") + hipGetErrorString(e));
+    return NS_OK;
   }
 
   // 3) one workgroup per row: every other row, and rows the segment kernel deferred.  A call

@@ -709,6 +709,7 @@ __device__ __forceinline__ void block_finalize_keys(const uint64_t* list, uint64
   const bool g8 = n <= WAVE_CAP / 2;
   block_rank_keys<NTH>(list, out, n);
   __syncthreads();
+  NS_STAMP(5);
   if (tid >= 64) return;
   // the first 128 sorted keys in registers: row maximum, k-th largest, kept count
   uint64_t a2[2];

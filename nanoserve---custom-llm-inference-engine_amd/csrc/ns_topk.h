@@ -239,10 +239,12 @@ __device__ __forceinline__ int topk_stream(const RowArgs P, const int row, const
   gmax = __builtin_fmaxf(gmax, lane_xor(gmax, 2));
   gmax = __builtin_fmaxf(gmax, lane_xor(gmax, 4));
   if ((lane & 7) == 0) fs[(NPH - 1) * 128 + wid * 8 + (lane >> 3)] = gmax;
+  NS_STAMP(1);   // wave 0: its share of the row streamed and reduced
   {
     int ticket = 0;
     if (lane == 0) ticket = __hip_atomic_fetch_add(&misc->ib[0], 1, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_WORKGROUP);
     if (__builtin_amdgcn_readfirstlane(ticket) == NWAVE - 1) {
+      NS_STAMP_LANE(2, lane == 0);   // the last wave to finish its share
       const uint32_t kp =
           NPH == 1 ? wave_kth_key<T::SZ == 2 ? 16 : 24>(fkey(fs[lane]), fkey(fs[64 + lane]), k)
                    : wave_kth_key4<T::SZ == 2 ? 16 : 24>(fkey(fs[lane]), fkey(fs[64 + lane]), fkey(fs[128 + lane]),
@@ -260,6 +262,7 @@ __device__ __forceinline__ int topk_stream(const RowArgs P, const int row, const
   const bool ws = ballot(special) != 0ull;
   if (lane == 0) is[wid] = ws ? 1 : 0;
   __syncthreads();   // group maxima, flags, the bitmap, the bound
+  NS_STAMP(3);
   int spec = 0;
 #pragma unroll
   for (int w = 0; w < NWAVE; ++w) spec |= is[w];
@@ -365,6 +368,7 @@ __device__ __forceinline__ int topk_stream(const RowArgs P, const int row, const
   };
   collect(std::false_type{});
   __syncthreads();   // the list complete
+  NS_STAMP(4);
   int n = misc->cand_n;
   if (__builtin_expect(n < k && pen_on, 0)) {
     // The penalty took the list under k keys (history tokens among the largest values): the
@@ -447,6 +451,7 @@ __device__ __forceinline__ int topk_stream(const RowArgs P, const int row, const
   zero_probs(o);
   block_finalize_keys<NT>(cand, cand + WAVE_CAP, n, k, topp < 1.0f, topp, u, row, P.out_ids, P.out_probs, V,
                           P.out_info, flags, n, PATH_WAVE_SET);
+  NS_STAMP(6);   // wave 0: drawn and written
   return 0;
 }
 

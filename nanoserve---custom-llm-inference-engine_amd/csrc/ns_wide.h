@@ -314,7 +314,7 @@ __device__ __forceinline__ WRowCtx wide_row_ctx(const WideParams& P, int row) {
   c.recip = P.pen_rcp != nullptr;
   c.rpen = c.recip ? P.pen_rcp[row] : 1.0f / c.pen;
   c.lo_t = div_lo(c.tdiv, c.rdiv);
-  c.lo_pen = div_lo(c.pen, c.rpen);
+  c.lo_pen = c.recip ? __builtin_inff() : div_lo(c.pen, c.rpen);
   c.rowp = (const unsigned char*)P.logits + c.src * P.row_stride * T::SZ;
   return c;
 }
@@ -385,9 +385,9 @@ __device__ __forceinline__ void chunk_y(const WRowCtx& c, const uint4& w, uint32
         const float x = y[e];
         if (x < 0.0f) {
           y[e] = x * c.pen;
-        } else if (c.recip) {
-          y[e] = x * c.rpen;
         } else {
+          // the division's multiply-and-correct form (a reciprocal penalty has lo_pen = +inf:
+          // its chunks always take chunk_y_exact, which multiplies)
           const float q0 = x * c.rpen;
           const float aq = __builtin_fabsf(q0);
           slow |= !(aq >= c.lo_pen && aq <= 0x1.0p+100f);
@@ -1130,12 +1130,10 @@ __device__ __forceinline__ uint64_t block_key_at(const uint64_t (&k)[E], int pos
 // descending, id ascending), the exact top-k threshold and top-p cut, the kept mass per
 // segment, the draw.
 template <typename T>
-__global__ __launch_bounds__(NT) void wide_final_kernel(const WideParams P) {
-  __shared__ WideSmemCut sm;
+__device__ __forceinline__ void wide_final_row(const WideParams& P, WideSmemCut& sm, const int row) {
   constexpr int EPC = T::EPC;
   constexpr int SEG_EL = SEG_CH * EPC;
   const int tid = threadIdx.x;
-  const int row = blockIdx.x;
   if (row >= P.n_sample) return;
   WideRow* R = P.rows + row;
   const int32_t step = R->step;
