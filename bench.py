@@ -502,8 +502,8 @@ def paged_attention_leg(dev, stream, steps=200, seqs=64, ctx=2048):
 
     def call(i):
         k, v = caches[i % 2]
-        A.paged_attention_hip(q, k, v, bt, sl, qsl, ql, d ** -0.5, bs, max_seq_len=ctx, out=out, workspace=ws, counters=cnt,
-                              stream=stream.cuda_stream)
+        A.paged_attention_hip(q, k, v, bt, sl, qsl, ql, d ** -0.5, bs, max_seq_len=ctx, max_query_len=1, out=out,
+                              workspace=ws, counters=cnt, stream=stream.cuda_stream)
 
     for i in range(20):
         call(i)
@@ -524,6 +524,73 @@ def paged_attention_leg(dev, stream, steps=200, seqs=64, ctx=2048):
             "paged_attention_decode_hbm_gbs": gbs,
             "paged_attention_decode_hbm_frac": gbs / HBM_PEAK_GBS,
             "paged_attention_decode_tokens_per_s": seqs / (us * 1e-6)}
+
+
+def paged_attention_prefill_leg(dev, stream, steps=50, chunk=512, ends=(2048, 4096, 6144, 8192)):
+    """A chunked-prefill step at Llama-3.2-3B's layout (24 query heads, 8 KV heads, head_dim 128,
+    block_size 16, bf16): one 512-token chunk (the reference's chunked_prefill_size, config.py:53)
+    ending at each of ``ends`` positions, physical blocks shuffled, two caches alternated.  Timed
+    on the query-tile MFMA kernel (the plan made once, as an engine makes it once per step for all
+    its layers) and on the per-token kernel for the same batch.  Roofline: MFMA bf16; algorithmic
+    flops 4 * head_dim per (query token, query head, visible position) (the two products; the
+    kernel's second, low-part product of P is not counted)."""
+    import torch
+
+    A = _pkg("paged_attention")
+    hq, hkv, d, bs = 24, 8, 128, 16
+    seqs = len(ends)
+    per = [e // bs for e in ends]
+    nblk = sum(per)
+    g = torch.Generator(device=dev)
+    g.manual_seed(11)
+    caches = [(torch.randn(nblk, bs, hkv, d, device=dev, generator=g, dtype=torch.bfloat16),
+               torch.randn(nblk, bs, hkv, d, device=dev, generator=g, dtype=torch.bfloat16)) for _ in range(2)]
+    perm = torch.randperm(nblk, device=dev, generator=g).to(torch.int32)
+    bt = torch.zeros((seqs, max(per)), dtype=torch.int32, device=dev)
+    at = 0
+    for s, n in enumerate(per):
+        bt[s, :n] = perm[at:at + n]
+        at += n
+    total_q = chunk * seqs
+    q = torch.randn(total_q, hq, d, device=dev, generator=g, dtype=torch.bfloat16)
+    sl = torch.tensor(list(ends), dtype=torch.int32, device=dev)
+    ql = torch.full((seqs,), chunk, dtype=torch.int32, device=dev)
+    qsl = torch.arange(0, total_q + 1, chunk, dtype=torch.int32, device=dev)
+    out = torch.empty_like(q)
+    plan = A.PagedAttentionPlan(sl, qsl, ql, hq, hkv, dev)
+    res = {}
+    for name, kw in (("tiles", dict(plan=plan)), ("per_token", dict(max_query_len=1))):
+        ws, cnt = None, None
+
+        def call(i):
+            k, v = caches[i % 2]
+            return A.paged_attention_hip(q, k, v, bt, sl, qsl, ql, d ** -0.5, bs, max_seq_len=max(ends), out=out,
+                                         workspace=ws, counters=cnt, stream=stream.cuda_stream, **kw)
+
+        for i in range(3):
+            call(i)
+        torch.cuda.synchronize()
+        n = steps if name == "tiles" else max(3, steps // 10)
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for i in range(n):
+            call(i)
+        e1.record(stream)
+        torch.cuda.synchronize()
+        res[name] = e0.elapsed_time(e1) / n * 1e3
+    visible = sum(sum(e - chunk + i + 1 for i in range(chunk)) for e in ends)
+    flops = 4.0 * d * hq * visible
+    kv_bytes = sum(ends) * hkv * d * 2 * 2
+    del caches
+    tf = flops / (res["tiles"] * 1e-6) / 1e12
+    return {"paged_attention_prefill_workload": f"{seqs} chunks of {chunk} tokens ending at {list(ends)} positions, "
+                                                f"24/8 heads, head_dim 128, bf16",
+            "paged_attention_prefill_tiles_us": res["tiles"], "paged_attention_prefill_per_token_us": res["per_token"],
+            "paged_attention_prefill_algorithmic_flops": flops, "paged_attention_prefill_tflops": tf,
+            "paged_attention_prefill_mfma_frac": tf / MFMA_BF16_PEAK_TFLOPS,
+            "paged_attention_prefill_kv_bytes": kv_bytes,
+            "paged_attention_prefill_tokens_per_s": total_q / (res["tiles"] * 1e-6)}
 
 
 def paged_attention_cpu_baseline(seqs=64, ctx=2048, reps=3):
@@ -603,7 +670,16 @@ def main(argv=None):
         lm_head_sweep(L, dev)
         return 0
     if args.paged_attention:
-        print(json.dumps(paged_attention_leg(dev, torch.cuda.current_stream(dev), steps=args.steps)), flush=True)
+        st = torch.cuda.current_stream(dev)
+        line = {}
+        for seqs, ctx in ((64, 2048), (8, 8192), (256, 1024)):
+            r = paged_attention_leg(dev, st, steps=args.steps, seqs=seqs, ctx=ctx)
+            print(f"[bench] paged attention decode {seqs}x{ctx}: {r}", file=sys.stderr, flush=True)
+            line.update({k.replace("paged_attention_decode_", f"paged_attention_decode_b{seqs}_ctx{ctx}_")
+                         if not k.startswith(f"paged_attention_decode_b{seqs}_ctx{ctx}") else k: v
+                         for k, v in r.items()})
+        line.update(paged_attention_prefill_leg(dev, st, steps=max(10, args.steps // 8)))
+        print(json.dumps(line), flush=True)
         if args.copy_mb > 0:
             copy_reference(dev, args.copy_mb)
         return 0
@@ -688,6 +764,8 @@ def main(argv=None):
     small = small_batch_leg(L, lib, dev, stream, cpu_reps=20 if args.cpu_rows > 0 else 0) \
         if args.config == WORKLOAD_CFG else {}
     attention = paged_attention_leg(dev, stream) if args.config == WORKLOAD_CFG else {}
+    if attention:
+        attention.update(paged_attention_prefill_leg(dev, stream))
     if attention and args.cpu_rows > 0:
         attention["paged_attention_cpu_baseline"] = paged_attention_cpu_baseline()
     if args.config != WORKLOAD_CFG:

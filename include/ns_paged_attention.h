@@ -32,7 +32,7 @@
 extern "C" {
 #endif
 
-#define NS_PA_ABI_VERSION 2
+#define NS_PA_ABI_VERSION 3
 
 #define NS_PA_DTYPE_F32 0
 #define NS_PA_DTYPE_BF16 1
@@ -43,6 +43,9 @@ extern "C" {
                                       max_blocks_per_seq blocks: that key is skipped */
 #define NS_PA_STATUS_SEQ_TOO_LONG 2 /* a sequence needs more KV partitions than max_seq_len sized the
                                        grid for: that query's output is undefined */
+#define NS_PA_STATUS_BAD_TILE 4     /* a prefill tile that is not 1 .. tile-width consecutive query tokens
+                                       of one sequence, or a listed decode token outside the batch:
+                                       skipped, its outputs not written */
 
 typedef struct ns_paged_attn_args {
   const void*    query;            /* (total_q, num_heads_q, head_dim), dtype */
@@ -76,6 +79,18 @@ typedef struct ns_paged_attn_args {
   int32_t        max_seq_len;      /* >= every seq_lens[s]; sizes the grid and the workspace */
   int32_t        dtype;            /* NS_PA_DTYPE_* */
   float          scale;
+  /* Query tiles for sequences with several query tokens (chunked prefill), bfloat16 and float16
+   * only: prefill_tiles holds n_prefill_tiles int32 triples (sequence, first query token, token
+   * count), each 1 .. 64 / (num_heads_q / num_kv_heads) consecutive tokens of one sequence; a tile
+   * reads each key and value row once for all its tokens and heads (MFMA).  With tiles,
+   * decode_tokens lists the n_decode_tokens other query tokens (flat indices), which the per-token
+   * kernel takes; every query token belongs to exactly one tile or the list (an unlisted token's
+   * output is not written).  prefill_tiles NULL: the per-token kernel takes decode_tokens when it is
+   * set, else every token.  Device pointers. */
+  const int32_t* decode_tokens;
+  int32_t        n_decode_tokens;
+  const int32_t* prefill_tiles;
+  int32_t        n_prefill_tiles;
 } ns_paged_attn_args;
 
 /* Version of this ABI (NS_PA_ABI_VERSION). */
@@ -89,6 +104,11 @@ const char* ns_pa_last_error(void);
  * counters buffer. Returns 0 on success, nonzero on invalid sizes. */
 int ns_paged_attention_workspace_bytes(int32_t total_q, int32_t num_heads_q, int32_t num_kv_heads,
                                        int32_t head_dim, int32_t max_seq_len, uint64_t* bytes);
+
+/* Workspace bytes and counter words a call with these arguments needs (prefill tiles included):
+ * the counters buffer holds total_q * num_kv_heads words for the per-token kernel, then
+ * n_prefill_tiles * num_kv_heads for the tiles; zero-filled once, left zeroed by every call. */
+int ns_paged_attention_call_workspace(const ns_paged_attn_args* args, uint64_t* bytes, uint64_t* counters);
 
 /* Paged attention (paged_attention_triton.py:134-170, paged_attention_torch.py:31-100): one
  * launch; one workgroup per (query token, KV head, KV partition) computes all query heads of that

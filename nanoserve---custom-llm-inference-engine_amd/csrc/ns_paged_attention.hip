@@ -65,6 +65,8 @@ struct PaParams {
                       // (a buffer of its own: any call shape leaves every counter at zero)
   int64_t sq_tok, sq_head, sk_blk, sk_tok, sk_head, sv_blk, sv_tok, sv_head, so_tok, so_head, sbt;
   int32_t num_seqs, hq, hkv, block_size, num_blocks, max_blocks_per_seq, part_tokens, max_parts;
+  int32_t total_q;
+  const int32_t* tokens;  // the query tokens the decode kernel takes (blockIdx.x indexes it), or NULL: all
   int32_t bs_shift;  // log2(block_size) when it is a power of two, else -1
   float scale_log2;  // scale * log2(e): scores in log2 units, exp2 for the softmax
 };
@@ -212,8 +214,13 @@ __global__ __launch_bounds__(kThreads) void pa_partition_kernel(PaParams p) {
   __shared__ float s_m[G], s_l[G];
   __shared__ int s_blk[kMaxPart + 2];  // physical block of each block-table entry the partition spans
 
-  const int qi = blockIdx.x, kvh = blockIdx.y, part = blockIdx.z;
+  const int qi = p.tokens != nullptr ? p.tokens[blockIdx.x] : (int)blockIdx.x;
+  const int kvh = blockIdx.y, part = blockIdx.z;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  if (qi < 0 || qi >= p.total_q) {   // a listed token outside the batch: flagged, nothing touched
+    if (threadIdx.x == 0 && part == 0 && kvh == 0 && p.status) atomicOr(p.status, NS_PA_STATUS_BAD_TILE);
+    return;
+  }
   const int slot = lane >> 3;  // position within a half step
   const int dl = lane & 7;     // dim slice
   const QueryPlace qp = place_query(p, qi);
@@ -465,7 +472,364 @@ __global__ __launch_bounds__(kThreads) void pa_partition_kernel(PaParams p) {
   }
 }
 
+// ---- prefill kernel: query tiles on MFMA -------------------------------------------------------
+//
+// Sequences with several query tokens (chunked prefill) go by query tile: one 64-thread workgroup
+// per (tile, KV head, KV partition) holds 64 query columns -- kPfCols / G tokens of one sequence
+// times the G query heads of the KV head, column c = token (c / G), head (c % G) -- and walks the
+// partition's positions 32 at a time, so each key and value row is read once per tile instead of
+// once per query token.  On v_mfma_f32_32x32x16 (bf16 or f16 operands, float32 accumulation):
+//   * S^T = K Q^T: rows the tile's 32 positions, columns the queries.  A lane holds one query
+//     column (lane % 32) of 16 positions, so the online softmax of a column (max, exp2, sum) runs
+//     in the lane plus one exchange with lane ^ 32;
+//   * O^T += V^T P^T over the positions, the probabilities taken straight from the S^T layout as
+//     the B operand: position slot i of k-step s in the lanes of half h is position
+//     16 s + 8 (i / 4) + 4 h + i % 4 of the tile, and the V^T operand is gathered from the value
+//     rows staged in LDS in that order.  P goes in as two 16-bit parts, hi = RN(p) and
+//     lo = RN(p - hi): both products with a value are exact in float32, so the sum carries p to
+//     about 2^-17 relative, the float32 arithmetic of the reference's kernel (a single 16-bit P
+//     would round each weight by up to 2^-9).
+// The scores are the float32 dot products times scale * log2(e) and exp2 replaces exp, as in the
+// decode kernel.  A tile whose positions span several partitions has them merged by the last to
+// arrive, as the decode kernel's split rows are.
+
+constexpr int kPfCols = 64;     // query columns of a tile (two 32-column blocks)
+constexpr int kPfPos = 32;      // positions per step (the MFMA's 32 rows)
+constexpr int kPfMaxPart = 1024;
+constexpr int kPfMinPart = 128;
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x16_t __attribute__((ext_vector_type(16)));
+
+template <typename T> struct Mma;
+template <> struct Mma<Bf16> {
+  typedef bf16x8_t vec;
+  static __device__ __forceinline__ f32x16_t mma(vec a, vec b, f32x16_t c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+  }
+  // float -> bfloat16 bits, round to nearest even (p and its remainder are finite)
+  static __device__ __forceinline__ uint32_t bits(float x) {
+    const uint32_t u = __float_as_uint(x);
+    return (u + 0x7FFFu + ((u >> 16) & 1u)) >> 16;
+  }
+  static __device__ __forceinline__ float widen(uint32_t h) { return __uint_as_float(h << 16); }
+};
+template <> struct Mma<F16> {
+  typedef f16x8_t vec;
+  static __device__ __forceinline__ f32x16_t mma(vec a, vec b, f32x16_t c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+  }
+  static __device__ __forceinline__ uint32_t bits(float x) {
+    return (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)x);
+  }
+  static __device__ __forceinline__ float widen(uint32_t h) {
+    return (float)__builtin_bit_cast(_Float16, (uint16_t)h);
+  }
+};
+
+struct PfParams {
+  const int32_t* tiles;   // (n_tiles, 3): sequence, first query token (flat index), token count
+  float* ws_acc;          // (n_tiles, hkv, max_parts, kPfCols, D) unnormalised partition outputs
+  float* ws_ml;           // (n_tiles, hkv, max_parts, kPfCols, 2) partition max (log2 units), sum
+  int32_t* counters;      // (n_tiles, hkv) arrivals of split tiles; zero between calls
+  int32_t part_tokens;    // positions per partition (a multiple of kPfPos)
+  int32_t max_parts;
+};
+
+template <typename T, int D, int G>
+__global__ __launch_bounds__(64) void pa_prefill_kernel(PaParams p, PfParams f) {
+  using M = Mma<T>;
+  using vec = typename M::vec;
+  constexpr int BQ = kPfCols / G;          // tokens per tile
+  constexpr int KS = D / 16;               // k-steps of S^T = K Q^T
+  constexpr int DB = D / 32;               // 32-row blocks of O^T
+  constexpr int PITCH = D * 2 + 16;        // bytes per staged value row (rows 4 apart in other banks)
+  __shared__ __align__(16) unsigned char s_v[kPfPos * PITCH];
+  __shared__ int s_blk[kPfMaxPart / 1 + 2];
+  __shared__ int s_last;
+
+  const int tile = blockIdx.x, kvh = blockIdx.y, part = blockIdx.z;
+  const int lane = threadIdx.x, h = lane >> 5, c32 = lane & 31;
+  const int seq = f.tiles[3 * tile];
+  const int t0 = f.tiles[3 * tile + 1];
+  const int nq = f.tiles[3 * tile + 2];
+  // a tile must hold 1 .. BQ consecutive query tokens of one sequence: anything else is flagged
+  // and left alone (nothing is read or written out of bounds)
+  if (seq < 0 || seq >= p.num_seqs || nq < 1 || nq > BQ || t0 < p.qsl[seq] || t0 + nq > p.qsl[seq] + p.qlens[seq] ||
+      t0 + nq > p.total_q) {
+    if (lane == 0 && part == 0 && p.status) atomicOr(p.status, NS_PA_STATUS_BAD_TILE);
+    return;
+  }
+  const int seq_len = p.seq_lens[seq];
+  const int kv_pos0 = seq_len - p.qlens[seq] + (t0 - p.qsl[seq]);   // the first token's KV position
+  int lt = kv_pos0 + nq < seq_len ? kv_pos0 + nq : seq_len;          // positions the last token sees
+  if (lt < 0) lt = 0;
+  const int n_parts = (lt + f.part_tokens - 1) / f.part_tokens;
+  if (part == 0 && n_parts > f.max_parts && lane == 0 && p.status) atomicOr(p.status, NS_PA_STATUS_SEQ_TOO_LONG);
+
+  // the lane's two columns: token i, head g, visible positions kvl
+  int tok[2], head[2], kvl[2];
+#pragma unroll
+  for (int cb = 0; cb < 2; ++cb) {
+    const int c = cb * 32 + c32;
+    tok[cb] = c / G;
+    head[cb] = c % G;
+    const bool ok = c < BQ * G && tok[cb] < nq;
+    int kl = kv_pos0 + tok[cb] + 1 < seq_len ? kv_pos0 + tok[cb] + 1 : seq_len;
+    kvl[cb] = ok ? (kl > 0 ? kl : 0) : -1;   // -1: a padding column (never written)
+  }
+  auto out_ptr = [&](int cb) -> int64_t {
+    return (int64_t)(t0 + tok[cb]) * p.so_tok + (int64_t)(kvh * G + head[cb]) * p.so_head;
+  };
+  if (part >= n_parts) {
+    if (part == 0) {   // no visible key for any token of the tile: zeros
+#pragma unroll
+      for (int cb = 0; cb < 2; ++cb)
+        if (kvl[cb] >= 0 && h == 0)
+          for (int d = 0; d < D; ++d) store_one<T>(p.out, out_ptr(cb) + d, 0.f);
+    }
+    return;
+  }
+  const int j0 = part * f.part_tokens;
+  const int j1 = lt < j0 + f.part_tokens ? lt : j0 + f.part_tokens;
+  const int32_t* bt_row = p.bt + (int64_t)seq * p.sbt;
+  // the partition's slice of the block table, validated once, into LDS
+  const int bi0 = j0 / p.block_size;
+  const int nbi = (j1 - 1) / p.block_size - bi0 + 1;
+  for (int i = lane; i < nbi; i += 64) {
+    const int bi = bi0 + i;
+    int blk = bi < p.max_blocks_per_seq ? bt_row[bi] : -1;
+    if (blk < 0 || blk >= p.num_blocks) {
+      blk = -1;
+      if (p.status) atomicOr(p.status, NS_PA_STATUS_BAD_BLOCK);
+    }
+    s_blk[i] = blk;
+  }
+
+  // Q^T operands: column c's 8 dims 16 ks + 8 h .. + 7 (zeros for padding columns)
+  vec qop[2][KS];
+#pragma unroll
+  for (int cb = 0; cb < 2; ++cb) {
+    const int64_t qoff = (int64_t)(t0 + tok[cb]) * p.sq_tok + (int64_t)(kvh * G + head[cb]) * p.sq_head;
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      u32x4 w = {0u, 0u, 0u, 0u};
+      if (kvl[cb] >= 0) w = *reinterpret_cast<const u32x4*>(reinterpret_cast<const char*>(p.q) +
+                                                           (qoff + 16 * ks + 8 * h) * 2);
+      qop[cb][ks] = __builtin_bit_cast(vec, w);
+    }
+  }
+  __syncthreads();   // the block slice
+
+  // the K / V rows of one step: row jt + c32, dims 16 ks + 8 h .. (zeros past the partition or for
+  // an invalid block); vm: bit r set when row r of the step is a valid position
+  auto load_rows = [&](int jt, u32x4 (&kr)[KS], u32x4 (&vr)[KS], uint32_t& vm) {
+    const int j = jt + c32;
+    int blk = -1, off = 0;
+    if (j < j1) {
+      int bi;
+      if (p.bs_shift >= 0) { bi = j >> p.bs_shift; off = j & (p.block_size - 1); }
+      else { bi = j / p.block_size; off = j - bi * p.block_size; }
+      blk = s_blk[bi - bi0];
+    }
+    vm = (uint32_t)__builtin_amdgcn_ballot_w64(blk >= 0);   // lanes 0..31 (32..63 repeat them)
+    const int64_t kb = (int64_t)blk * p.sk_blk + (int64_t)off * p.sk_tok + (int64_t)kvh * p.sk_head + 8 * h;
+    const int64_t vb = (int64_t)blk * p.sv_blk + (int64_t)off * p.sv_tok + (int64_t)kvh * p.sv_head + 8 * h;
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      kr[ks] = u32x4{0u, 0u, 0u, 0u};
+      vr[ks] = u32x4{0u, 0u, 0u, 0u};
+      if (blk >= 0) {
+        kr[ks] = *reinterpret_cast<const u32x4*>(reinterpret_cast<const char*>(p.k) + (kb + 16 * ks) * 2);
+        vr[ks] = *reinterpret_cast<const u32x4*>(reinterpret_cast<const char*>(p.v) + (vb + 16 * ks) * 2);
+      }
+    }
+  };
+
+  f32x16_t acc[DB][2];
+#pragma unroll
+  for (int db = 0; db < DB; ++db)
+#pragma unroll
+    for (int cb = 0; cb < 2; ++cb)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[db][cb][e] = 0.f;
+  float m[2] = {-INFINITY, -INFINITY}, l[2] = {0.f, 0.f};
+
+  u32x4 kr[KS], vr[KS];
+  uint32_t vm;
+  load_rows(j0, kr, vr, vm);
+  for (int jt = j0; jt < j1; jt += kPfPos) {
+    // this step's value rows to LDS (the previous step's gathers are done: barrier at its end)
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks)
+      *reinterpret_cast<u32x4*>(s_v + c32 * PITCH + (16 * ks + 8 * h) * 2) = vr[ks];
+    // S^T = K Q^T for both column blocks
+    f32x16_t st[2];
+#pragma unroll
+    for (int cb = 0; cb < 2; ++cb)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) st[cb][e] = 0.f;
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      const vec a = __builtin_bit_cast(vec, kr[ks]);
+#pragma unroll
+      for (int cb = 0; cb < 2; ++cb) st[cb] = M::mma(a, qop[cb][ks], st[cb]);
+    }
+    const uint32_t vmask = vm;
+    // the next step's rows, in flight across the softmax and the value products
+    if (jt + kPfPos < j1) load_rows(jt + kPfPos, kr, vr, vm);
+    // online softmax per column; P as the hi / lo B operands
+    vec phi[2][2], plo[2][2];
+#pragma unroll
+    for (int cb = 0; cb < 2; ++cb) {
+      float sv[16];
+      float mt = -INFINITY;
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const int r = 8 * (e >> 2) + 4 * h + (e & 3);   // row of the step
+        const bool ok = ((vmask >> r) & 1u) && jt + r < kvl[cb];
+        sv[e] = ok ? st[cb][e] * p.scale_log2 : -INFINITY;
+        mt = fmaxf(mt, sv[e]);
+      }
+      mt = fmaxf(mt, __shfl_xor(mt, 32));
+      const float mn = fmaxf(m[cb], mt);
+      const float alpha = mn == -INFINITY ? 1.f : exp2f(m[cb] - mn);
+      float ls = 0.f;
+      uint32_t hb[16], lb[16];
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const float pe = sv[e] == -INFINITY ? 0.f : exp2f(sv[e] - mn);
+        ls += pe;
+        hb[e] = M::bits(pe);
+        lb[e] = M::bits(pe - M::widen(hb[e]));
+      }
+      ls += __shfl_xor(ls, 32);
+      l[cb] = l[cb] * alpha + ls;
+      m[cb] = mn;
+#pragma unroll
+      for (int db = 0; db < DB; ++db)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) acc[db][cb][e] *= alpha;
+#pragma unroll
+      for (int s2 = 0; s2 < 2; ++s2) {
+        u32x4 wh, wl;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          wh[i] = hb[8 * s2 + 2 * i] | (hb[8 * s2 + 2 * i + 1] << 16);
+          wl[i] = lb[8 * s2 + 2 * i] | (lb[8 * s2 + 2 * i + 1] << 16);
+        }
+        phi[cb][s2] = __builtin_bit_cast(vec, wh);
+        plo[cb][s2] = __builtin_bit_cast(vec, wl);
+      }
+    }
+    __syncthreads();   // the value rows in LDS
+    // O^T += V^T P^T: the V^T operand of dims 32 db + c32, positions in the S^T row order
+#pragma unroll
+    for (int db = 0; db < DB; ++db) {
+#pragma unroll
+      for (int s2 = 0; s2 < 2; ++s2) {
+        const unsigned char* col = s_v + (32 * db + c32) * 2;
+        u32x4 w;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int r0 = 16 * s2 + 8 * ((2 * i) >> 2) + 4 * h + ((2 * i) & 3);
+          const uint32_t lo16 = *reinterpret_cast<const uint16_t*>(col + r0 * PITCH);
+          const uint32_t hi16 = *reinterpret_cast<const uint16_t*>(col + (r0 + 1) * PITCH);
+          w[i] = lo16 | (hi16 << 16);
+        }
+        const vec a = __builtin_bit_cast(vec, w);
+#pragma unroll
+        for (int cb = 0; cb < 2; ++cb) {
+          acc[db][cb] = M::mma(a, phi[cb][s2], acc[db][cb]);
+          acc[db][cb] = M::mma(a, plo[cb][s2], acc[db][cb]);
+        }
+      }
+    }
+    __syncthreads();   // the gathers are done before the next step's rows overwrite LDS
+  }
+
+  // O^T layout: lane l, element e -> column l % 32, dim 32 db + 8 (e / 4) + 4 h + e % 4
+  const bool direct = n_parts == 1;
+  const int64_t wbase = ((int64_t)tile * p.hkv + kvh) * f.max_parts;
+  if (direct || part < f.max_parts) {
+#pragma unroll
+    for (int cb = 0; cb < 2; ++cb) {
+      if (kvl[cb] < 0) continue;
+      const int c = cb * 32 + c32;
+#pragma unroll
+      for (int db = 0; db < DB; ++db)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+          const int d = 32 * db + 8 * (e >> 2) + 4 * h + (e & 3);
+          if (direct) {
+            store_one<T>(p.out, out_ptr(cb) + d, l[cb] > 0.f ? acc[db][cb][e] / l[cb] : 0.f);
+          } else {
+            st_dev(&f.ws_acc[((wbase + part) * kPfCols + c) * D + d], acc[db][cb][e]);
+          }
+        }
+      if (!direct && h == 0) {
+        st_dev(&f.ws_ml[((wbase + part) * kPfCols + c) * 2], m[cb]);
+        st_dev(&f.ws_ml[((wbase + part) * kPfCols + c) * 2 + 1], l[cb]);
+      }
+    }
+  }
+  if (direct || part >= f.max_parts) return;
+
+  // split tile: the last partition to arrive merges (the partials crossed through agent-scope
+  // atomic stores completed by the s_waitcnt, read back through agent-scope loads)
+  const int arrivals = n_parts < f.max_parts ? n_parts : f.max_parts;
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  int32_t* counter = f.counters + (int64_t)tile * p.hkv + kvh;
+  if (lane == 0) s_last = atomicAdd(counter, 1) == arrivals - 1;
+  __syncthreads();
+  if (!s_last) return;
+  if (lane == 0) __hip_atomic_store(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  // lane c merges column c: the partitions' weights, then every dim
+  const int c = lane;
+  const int ti = c / G, hg = c % G;
+  if (c >= BQ * G || ti >= nq) return;
+  float mx = -INFINITY;
+  for (int i = 0; i < arrivals; ++i) mx = fmaxf(mx, ld_dev(&f.ws_ml[((wbase + i) * kPfCols + c) * 2]));
+  float L = 0.f;
+  for (int i = 0; i < arrivals; ++i) {
+    const float mi = ld_dev(&f.ws_ml[((wbase + i) * kPfCols + c) * 2]);
+    if (mi == -INFINITY) continue;
+    L = fmaf(exp2f(mi - mx), ld_dev(&f.ws_ml[((wbase + i) * kPfCols + c) * 2 + 1]), L);
+  }
+  const int64_t ob = (int64_t)(t0 + ti) * p.so_tok + (int64_t)(kvh * G + hg) * p.so_head;
+  for (int d = 0; d < D; ++d) {
+    float o = 0.f;
+    for (int i = 0; i < arrivals; ++i) {
+      const float mi = ld_dev(&f.ws_ml[((wbase + i) * kPfCols + c) * 2]);
+      if (mi == -INFINITY) continue;
+      o = fmaf(exp2f(mi - mx), ld_dev(&f.ws_acc[((wbase + i) * kPfCols + c) * D + d]), o);
+    }
+    store_one<T>(p.out, ob + d, L > 0.f ? o / L : 0.f);
+  }
+}
+
 // ---- host side ---------------------------------------------------------------------------------
+
+int pf_part_tokens_for(int32_t n_tiles, int32_t hkv, int32_t max_seq_len) {
+  int part = kPfMaxPart;
+  while (part > kPfMinPart) {
+    const int64_t parts = ((int64_t)max_seq_len + part - 1) / part;
+    if ((int64_t)n_tiles * hkv * parts >= kTargetGroups) break;
+    part >>= 1;
+  }
+  return part;
+}
+
+// Bytes of the prefill tiles' partials (0 when every tile fits one partition).
+uint64_t pf_workspace_bytes(int32_t n_tiles, int32_t hkv, int32_t head_dim, int32_t max_seq_len) {
+  if (n_tiles <= 0) return 0;
+  const int part = pf_part_tokens_for(n_tiles, hkv, max_seq_len);
+  const int64_t max_parts = ((int64_t)max_seq_len + part - 1) / part;
+  if (max_parts <= 1) return 0;
+  return (uint64_t)n_tiles * hkv * max_parts * kPfCols * (head_dim + 2) * sizeof(float);
+}
 
 int part_tokens_for(int32_t total_q, int32_t hkv, int32_t max_seq_len) {
   int part = kMaxPart;
@@ -490,34 +854,50 @@ int check_sizes(int32_t total_q, int32_t hq, int32_t hkv, int32_t head_dim, int3
   return 0;
 }
 
-uint64_t workspace_bytes(int32_t total_q, int32_t hq, int32_t hkv, int32_t head_dim, int32_t max_seq_len) {
-  const int part = part_tokens_for(total_q, hkv, max_seq_len);
+// Bytes of the per-token kernel's partials: total_q query slots (the kernel indexes them by query
+// token), the partition length sized for the n_tokens workgroups along x.
+uint64_t workspace_bytes(int32_t total_q, int32_t hq, int32_t hkv, int32_t head_dim, int32_t max_seq_len,
+                         int32_t n_tokens) {
+  const int part = part_tokens_for(n_tokens, hkv, max_seq_len);
   const int64_t max_parts = ((int64_t)max_seq_len + part - 1) / part;
   if (max_parts <= 1) return 0;
   return (uint64_t)total_q * hq * max_parts * (head_dim + 2) * sizeof(float);
 }
+uint64_t workspace_bytes(int32_t total_q, int32_t hq, int32_t hkv, int32_t head_dim, int32_t max_seq_len) {
+  return workspace_bytes(total_q, hq, hkv, head_dim, max_seq_len, total_q);
+}
 
+// n_tokens decode workgroups along x (p.tokens or the first n_tokens tokens); the prefill tiles
+// when f.tiles is set (16-bit types only)
 template <typename T, int D, int G>
-void launch(const PaParams& p, int total_q, hipStream_t stream) {
-  dim3 grid(total_q, p.hkv, p.max_parts > 0 ? p.max_parts : 1);
-  hipLaunchKernelGGL((pa_partition_kernel<T, D, G>), grid, dim3(kThreads), 0, stream, p);
+void launch(const PaParams& p, const PfParams& f, int n_tokens, int n_tiles, hipStream_t stream) {
+  if (n_tokens > 0) {
+    dim3 grid(n_tokens, p.hkv, p.max_parts > 0 ? p.max_parts : 1);
+    hipLaunchKernelGGL((pa_partition_kernel<T, D, G>), grid, dim3(kThreads), 0, stream, p);
+  }
+  if constexpr (Elem<T>::bytes == 2) {
+    if (n_tiles > 0) {
+      dim3 grid(n_tiles, p.hkv, f.max_parts > 0 ? f.max_parts : 1);
+      hipLaunchKernelGGL((pa_prefill_kernel<T, D, G>), grid, dim3(64), 0, stream, p, f);
+    }
+  }
 }
 
 template <typename T, int D>
-void launch_g(const PaParams& p, int total_q, int g, hipStream_t stream) {
+void launch_g(const PaParams& p, const PfParams& f, int n_tokens, int n_tiles, int g, hipStream_t stream) {
   switch (g) {
-    case 1: launch<T, D, 1>(p, total_q, stream); break;
-    case 2: launch<T, D, 2>(p, total_q, stream); break;
-    case 3: launch<T, D, 3>(p, total_q, stream); break;
-    case 4: launch<T, D, 4>(p, total_q, stream); break;
-    default: launch<T, D, 8>(p, total_q, stream); break;
+    case 1: launch<T, D, 1>(p, f, n_tokens, n_tiles, stream); break;
+    case 2: launch<T, D, 2>(p, f, n_tokens, n_tiles, stream); break;
+    case 3: launch<T, D, 3>(p, f, n_tokens, n_tiles, stream); break;
+    case 4: launch<T, D, 4>(p, f, n_tokens, n_tiles, stream); break;
+    default: launch<T, D, 8>(p, f, n_tokens, n_tiles, stream); break;
   }
 }
 
 template <typename T>
-void launch_d(const PaParams& p, int total_q, int d, int g, hipStream_t stream) {
-  if (d == 64) launch_g<T, 64>(p, total_q, g, stream);
-  else launch_g<T, 128>(p, total_q, g, stream);
+void launch_d(const PaParams& p, const PfParams& f, int n_tokens, int n_tiles, int d, int g, hipStream_t stream) {
+  if (d == 64) launch_g<T, 64>(p, f, n_tokens, n_tiles, g, stream);
+  else launch_g<T, 128>(p, f, n_tokens, n_tiles, g, stream);
 }
 
 }  // namespace
@@ -533,6 +913,19 @@ int ns_paged_attention_workspace_bytes(int32_t total_q, int32_t num_heads_q, int
   if (!bytes) return fail("bytes is NULL");
   if (check_sizes(total_q, num_heads_q, num_kv_heads, head_dim, max_seq_len)) return 1;
   *bytes = workspace_bytes(total_q, num_heads_q, num_kv_heads, head_dim, max_seq_len);
+  return 0;
+}
+
+int ns_paged_attention_call_workspace(const ns_paged_attn_args* a, uint64_t* bytes, uint64_t* counters) {
+  if (!a || !bytes || !counters) return fail("a pointer argument is NULL");
+  if (check_sizes(a->total_q, a->num_heads_q, a->num_kv_heads, a->head_dim, a->max_seq_len)) return 1;
+  if (a->n_decode_tokens < 0 || a->n_prefill_tiles < 0) return fail("token and tile counts must be >= 0");
+  const int32_t n_tokens = a->decode_tokens ? a->n_decode_tokens : a->total_q;
+  const uint64_t dec =
+      workspace_bytes(a->total_q, a->num_heads_q, a->num_kv_heads, a->head_dim, a->max_seq_len, n_tokens);
+  const int32_t tiles = a->prefill_tiles ? a->n_prefill_tiles : 0;
+  *bytes = dec + pf_workspace_bytes(tiles, a->num_kv_heads, a->head_dim, a->max_seq_len);
+  *counters = (uint64_t)a->total_q * a->num_kv_heads + (uint64_t)tiles * a->num_kv_heads;
   return 0;
 }
 
@@ -558,14 +951,28 @@ int ns_paged_attention(const ns_paged_attn_args* a, hipStream_t stream) {
     return fail("query and cache pointers must be 16-byte aligned");
   if (a->stride_bt_seq < 0) return fail("stride_bt_seq must be >= 0");
   if (a->max_blocks_per_seq < 0) return fail("max_blocks_per_seq must be >= 0");
-  const uint64_t need = workspace_bytes(a->total_q, a->num_heads_q, a->num_kv_heads, a->head_dim, a->max_seq_len);
-  if (need > 0 && (!a->workspace || a->workspace_bytes < need))
-    return fail("workspace of %llu bytes needed (got %llu)", (unsigned long long)need,
-                (unsigned long long)a->workspace_bytes);
+  // the prefill tiles (16-bit types) and the token list of the per-token kernel
+  if (a->n_decode_tokens < 0 || a->n_prefill_tiles < 0) return fail("token and tile counts must be >= 0");
+  if (a->prefill_tiles && a->dtype == NS_PA_DTYPE_F32)
+    return fail("prefill tiles take bfloat16 or float16 (float32 queries go through the per-token kernel)");
+  if (a->prefill_tiles && !a->decode_tokens)
+    return fail("a call with prefill tiles lists its other query tokens in decode_tokens");
+  const int32_t n_tiles = a->prefill_tiles ? a->n_prefill_tiles : 0;
+  const int32_t n_tokens = a->decode_tokens ? a->n_decode_tokens : a->total_q;
+  const uint64_t need =
+      workspace_bytes(a->total_q, a->num_heads_q, a->num_kv_heads, a->head_dim, a->max_seq_len, n_tokens);
   if (need > 0 && !a->counters) return fail("a call with split rows needs the zero-filled counters buffer");
-  const int part = part_tokens_for(a->total_q, a->num_kv_heads, a->max_seq_len);
+  const int part = part_tokens_for(n_tokens, a->num_kv_heads, a->max_seq_len);
   const int64_t max_parts = ((int64_t)a->max_seq_len + part - 1) / part;
   if (max_parts > 65535) return fail("max_seq_len too large");
+  const uint64_t pf_need = pf_workspace_bytes(n_tiles, a->num_kv_heads, a->head_dim, a->max_seq_len);
+  if (need + pf_need > 0 && (!a->workspace || a->workspace_bytes < need + pf_need))
+    return fail("workspace of %llu bytes needed (got %llu)", (unsigned long long)(need + pf_need),
+                (unsigned long long)a->workspace_bytes);
+  if (pf_need > 0 && !a->counters) return fail("a call with split tiles needs the zero-filled counters buffer");
+  const int pf_part = pf_part_tokens_for(n_tiles, a->num_kv_heads, a->max_seq_len);
+  const int64_t pf_max_parts = ((int64_t)a->max_seq_len + pf_part - 1) / pf_part;
+  if (pf_max_parts > 65535) return fail("max_seq_len too large");
 
   PaParams p;
   p.q = a->query;
@@ -604,12 +1011,23 @@ int ns_paged_attention(const ns_paged_attn_args* a, hipStream_t stream) {
   p.part_tokens = part;
   p.max_parts = (int32_t)max_parts;
   p.scale_log2 = a->scale * kLog2e;
+  p.total_q = a->total_q;
+  p.tokens = a->decode_tokens;
+
+  PfParams f;
+  f.tiles = a->prefill_tiles;
+  char* ws = reinterpret_cast<char*>(a->workspace);
+  f.ws_acc = pf_need ? reinterpret_cast<float*>(ws + need) : nullptr;
+  f.ws_ml = pf_need ? f.ws_acc + (uint64_t)n_tiles * a->num_kv_heads * pf_max_parts * kPfCols * a->head_dim : nullptr;
+  f.counters = a->counters ? a->counters + (int64_t)a->total_q * a->num_kv_heads : nullptr;
+  f.part_tokens = pf_part;
+  f.max_parts = (int32_t)pf_max_parts;
 
   const int g = a->num_heads_q / a->num_kv_heads;
   switch (a->dtype) {
-    case NS_PA_DTYPE_F32: launch_d<float>(p, a->total_q, a->head_dim, g, stream); break;
-    case NS_PA_DTYPE_BF16: launch_d<Bf16>(p, a->total_q, a->head_dim, g, stream); break;
-    default: launch_d<F16>(p, a->total_q, a->head_dim, g, stream); break;
+    case NS_PA_DTYPE_F32: launch_d<float>(p, f, n_tokens, 0, a->head_dim, g, stream); break;
+    case NS_PA_DTYPE_BF16: launch_d<Bf16>(p, f, n_tokens, n_tiles, a->head_dim, g, stream); break;
+    default: launch_d<F16>(p, f, n_tokens, n_tiles, a->head_dim, g, stream); break;
   }
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) return fail("kernel launch failed: %s", hipGetErrorString(e));

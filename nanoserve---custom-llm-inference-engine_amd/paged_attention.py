@@ -8,11 +8,16 @@ with the same meaning, and returns a tensor shaped and typed like ``query``. The
 library raises.
 
 Differences from the reference's launcher, all on the host side:
-  * the per-query sequence index and KV position (paged_attention_triton.py:109-131) are found by
-    the kernel itself from ``query_start_loc``, so no index tensors are built;
-  * the grid's KV split needs the batch's longest sequence: ``max_seq_len`` (keyword) or, when
-    omitted, ``int(seq_lens.max())`` -- one device-to-host read, as the reference's
-    ``seq_lens.tolist()`` (paged_attention_triton.py:120, paged_attention_torch.py:51).
+  * decode batches (every ``query_lens`` entry 1, declared by ``max_query_len=1``): the
+    per-query sequence index and KV position (paged_attention_triton.py:109-131) are found by
+    the kernel itself from ``query_start_loc``, so no index tensors are built, and with
+    ``max_seq_len`` given the call reads nothing on the host;
+  * otherwise the batch layout (``seq_lens``, ``query_start_loc``, ``query_lens``) is read on the
+    host once, as the reference's launcher reads ``seq_lens.tolist()`` and ``query_lens.tolist()``
+    (paged_attention_triton.py:120-121, paged_attention_torch.py:51): sequences of at least
+    ``PREFILL_MIN_QUERY`` query tokens (bfloat16 and float16) are cut into query tiles of
+    ``64 // G`` tokens for the MFMA prefill kernel, which reads each key and value row once per
+    tile; the other query tokens go to the per-token kernel.
 """
 from __future__ import annotations
 
@@ -20,18 +25,23 @@ import ctypes
 import os
 from typing import Optional
 
+import numpy as np
+
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libns_paged_attention.so")
 
-ABI_VERSION = 2
+ABI_VERSION = 3
 NS_PA_DTYPE_F32 = 0
 NS_PA_DTYPE_BF16 = 1
 NS_PA_DTYPE_F16 = 2
 STATUS_BAD_BLOCK = 1
 STATUS_SEQ_TOO_LONG = 2
+STATUS_BAD_TILE = 4
+TILE_COLUMNS = 64          # query columns of a prefill tile: 64 // G tokens of G heads
+PREFILL_MIN_QUERY = 2      # sequences with at least this many query tokens go by tile
 
 EXPORTS = ("ns_pa_abi_version", "ns_pa_last_error", "ns_paged_attention_workspace_bytes",
-           "ns_paged_attention")
+           "ns_paged_attention_call_workspace", "ns_paged_attention")
 
 
 class PagedAttentionError(RuntimeError):
@@ -76,6 +86,10 @@ class NsPagedAttnArgs(ctypes.Structure):
         ("max_seq_len", ctypes.c_int32),
         ("dtype", ctypes.c_int32),
         ("scale", ctypes.c_float),
+        ("decode_tokens", ctypes.c_void_p),
+        ("n_decode_tokens", ctypes.c_int32),
+        ("prefill_tiles", ctypes.c_void_p),
+        ("n_prefill_tiles", ctypes.c_int32),
     ]
 
 
@@ -96,6 +110,10 @@ def load(path: str = LIB_PATH) -> ctypes.CDLL:
     lib.ns_pa_last_error.argtypes = []
     lib.ns_paged_attention_workspace_bytes.restype = ctypes.c_int
     lib.ns_paged_attention_workspace_bytes.argtypes = [ctypes.c_int32] * 5 + [ctypes.POINTER(ctypes.c_uint64)]
+    lib.ns_paged_attention_call_workspace.restype = ctypes.c_int
+    lib.ns_paged_attention_call_workspace.argtypes = [ctypes.POINTER(NsPagedAttnArgs),
+                                                      ctypes.POINTER(ctypes.c_uint64),
+                                                      ctypes.POINTER(ctypes.c_uint64)]
     lib.ns_paged_attention.restype = ctypes.c_int
     lib.ns_paged_attention.argtypes = [ctypes.POINTER(NsPagedAttnArgs), ctypes.c_void_p]
     if lib.ns_pa_abi_version() != ABI_VERSION:
@@ -137,6 +155,58 @@ def counters_for(device, n: int, stream=None):
     return buf
 
 
+def plan_tiles(seq_lens, query_start_loc, query_lens, num_heads_q: int, num_kv_heads: int):
+    """Host plan of a batch with prefill chunks: (tiles, decode tokens) as int32 numpy arrays.
+    Each sequence with at least PREFILL_MIN_QUERY query tokens is cut into tiles of
+    TILE_COLUMNS // G consecutive tokens, (sequence, first token, count) each; every other query
+    token is listed for the per-token kernel."""
+    import numpy as np
+
+    ql = np.asarray(query_lens, dtype=np.int64)
+    qsl = np.asarray(query_start_loc, dtype=np.int64)
+    bq = TILE_COLUMNS // (num_heads_q // num_kv_heads)
+    tiles, tokens = [], []
+    for s in range(ql.size):
+        q, start = int(ql[s]), int(qsl[s])
+        if q >= PREFILL_MIN_QUERY:
+            for t in range(0, q, bq):
+                tiles.append((s, start + t, min(bq, q - t)))
+        elif q > 0:
+            tokens.extend(range(start, start + q))
+    return (np.asarray(tiles, dtype=np.int32).reshape(-1, 3), np.asarray(tokens, dtype=np.int32))
+
+
+class PagedAttentionPlan:
+    """The host plan of one batch layout, reusable by every layer's call of a step: the device
+    lists of prefill tiles and per-token queries, and the layout's longest sequence and query.
+    The reference's launcher reads the layout on every call (paged_attention_triton.py:120-121);
+    with a plan the calls read nothing on the host."""
+
+    def __init__(self, seq_lens, query_start_loc, query_lens, num_heads_q: int, num_kv_heads: int, device):
+        import torch
+
+        h_sl = np.asarray(seq_lens.cpu() if hasattr(seq_lens, "cpu") else seq_lens, dtype=np.int64).reshape(-1)
+        h_qsl = np.asarray(query_start_loc.cpu() if hasattr(query_start_loc, "cpu") else query_start_loc,
+                           dtype=np.int64).reshape(-1)
+        h_ql = np.asarray(query_lens.cpu() if hasattr(query_lens, "cpu") else query_lens, dtype=np.int64).reshape(-1)
+        self.num_heads_q, self.num_kv_heads = int(num_heads_q), int(num_kv_heads)
+        self.total_q = int(h_ql.sum())
+        self.max_seq_len = int(h_sl.max()) if h_sl.size else 0
+        self.max_query_len = int(h_ql.max()) if h_ql.size else 0
+        self.staged = None
+        self.tokens = (0, 0)
+        self.tiles = None
+        if self.max_query_len >= PREFILL_MIN_QUERY:
+            h_tiles, h_tokens = plan_tiles(h_sl, h_qsl, h_ql, num_heads_q, num_kv_heads)
+            staged = torch.from_numpy(np.concatenate([h_tokens, h_tiles.reshape(-1)]).astype(np.int32))
+            if torch.device(device).type == "cuda":
+                staged = staged.pin_memory()
+            self.staged = staged.to(device, non_blocking=True)
+            # the per-token list starts the staged buffer (a valid address even when it is empty)
+            self.tokens = (self.staged.data_ptr(), int(h_tokens.size))
+            self.tiles = (self.staged.data_ptr() + 4 * int(h_tokens.size), int(h_tiles.shape[0]))
+
+
 def _dtype_code(dtype) -> int:
     import torch
 
@@ -154,6 +224,7 @@ def _i32(t, device):
 
 def paged_attention_hip(query, k_cache, v_cache, block_tables, seq_lens, query_start_loc, query_lens,
                         scale: float, block_size: int, *, max_seq_len: Optional[int] = None,
+                        max_query_len: Optional[int] = None, plan: Optional[PagedAttentionPlan] = None,
                         out=None, workspace=None, counters=None, status=None, stream=None):
     """Attention of every query token over its sequence's paged KV (the reference's
     ``paged_attention_triton``; same arguments, same result up to float32 rounding order).
@@ -165,7 +236,9 @@ def paged_attention_hip(query, k_cache, v_cache, block_tables, seq_lens, query_s
     than ``max_seq_len``): a caller that wants the check reads it after the call. ``workspace``
     (uint8, any contents) and ``counters`` (int32, zero-filled once; every call leaves it so) are
     allocated per call, resp. taken from this module's per-device, per-stream buffer, when not
-    given.  ``stream``: a ``torch.cuda.Stream`` or a raw HIP stream handle, default the current
+    given.  ``max_query_len``: an upper bound of ``query_lens`` (1 for a decode step, which then
+    takes the per-token kernel without reading the batch layout on the host).  ``plan``: a
+    ``PagedAttentionPlan`` of this batch layout (then nothing is read on the host).  ``stream``: a ``torch.cuda.Stream`` or a raw HIP stream handle, default the current
     stream; the call's own temporaries are made on it, so nothing orders them against another.
     """
     import torch
@@ -178,15 +251,21 @@ def paged_attention_hip(query, k_cache, v_cache, block_tables, seq_lens, query_s
         s = torch.cuda.current_stream(dev)
     elif isinstance(stream, torch.cuda.Stream):
         s = stream
+    elif int(stream) == 0:
+        # the null stream is torch's default stream (an ExternalStream of handle 0 is not it)
+        s = torch.cuda.default_stream(dev)
+    elif int(stream) == torch.cuda.current_stream(dev).cuda_stream:
+        s = torch.cuda.current_stream(dev)
     else:
         s = torch.cuda.ExternalStream(int(stream), device=dev)
     with torch.cuda.stream(s):
         return _paged_attention_on(lib, s, query, k_cache, v_cache, block_tables, seq_lens, query_start_loc,
-                                   query_lens, scale, block_size, max_seq_len, out, workspace, counters, status)
+                                   query_lens, scale, block_size, max_seq_len, max_query_len, plan, out,
+                                   workspace, counters, status)
 
 
 def _paged_attention_on(lib, s, query, k_cache, v_cache, block_tables, seq_lens, query_start_loc, query_lens,
-                        scale, block_size, max_seq_len, out, workspace, counters, status):
+                        scale, block_size, max_seq_len, max_query_len, plan, out, workspace, counters, status):
     """paged_attention_hip with ``s`` the current stream: every temporary below is made on it."""
     import torch
 
@@ -212,6 +291,19 @@ def _paged_attention_on(lib, s, query, k_cache, v_cache, block_tables, seq_lens,
     num_seqs = bt.shape[0]
     if sl.numel() != num_seqs or ql.numel() != num_seqs or qsl.numel() != num_seqs + 1:
         raise PagedAttentionError("seq_lens/query_lens need num_seqs entries and query_start_loc num_seqs + 1")
+    # prefill tiles: 16-bit types, unless the caller declares a decode step
+    tiles = tokens = None
+    if plan is not None:
+        if plan.total_q != total_q or plan.num_heads_q != hq or plan.num_kv_heads != hkv:
+            raise PagedAttentionError("the plan was made for another batch layout or head layout")
+        if max_seq_len is None:
+            max_seq_len = plan.max_seq_len
+    elif query.dtype != torch.float32 and (max_query_len is None or max_query_len >= PREFILL_MIN_QUERY):
+        plan = PagedAttentionPlan(sl, qsl, ql, hq, hkv, dev)   # one read of the batch layout
+        if max_seq_len is None:
+            max_seq_len = plan.max_seq_len
+    if plan is not None and plan.tiles is not None and query.dtype != torch.float32:
+        tokens, tiles = plan.tokens, plan.tiles
     if max_seq_len is None:
         max_seq_len = int(sl.max().item()) if num_seqs else 0
     if out is None:
@@ -220,26 +312,36 @@ def _paged_attention_on(lib, s, query, k_cache, v_cache, block_tables, seq_lens,
         raise PagedAttentionError("out must match query's shape, dtype and device")
     elif out.stride(-1) != 1:
         raise PagedAttentionError("out must have a unit head_dim stride")
-    need = workspace_bytes(total_q, hq, hkv, d, max_seq_len)
-    if need and workspace is None:
-        workspace = torch.empty(need, dtype=torch.uint8, device=dev)
-    elif need and workspace.numel() * workspace.element_size() < need:
-        raise PagedAttentionError(f"workspace of {need} bytes needed")
-    if need and counters is None:
-        counters = counters_for(dev, total_q * hkv, s)
-    elif need and (counters.dtype != torch.int32 or counters.device != dev or counters.numel() < total_q * hkv):
-        raise PagedAttentionError(f"counters must be an int32 device tensor of at least {total_q * hkv} entries")
     if status is not None and (status.dtype != torch.int32 or status.device != dev or status.numel() < 1):
         raise PagedAttentionError("status must be an int32 device tensor")
     a = NsPagedAttnArgs(
         query.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(), out.data_ptr(), bt.data_ptr(), sl.data_ptr(),
         qsl.data_ptr(), ql.data_ptr(), status.data_ptr() if status is not None else None,
-        workspace.data_ptr() if need else None, need, counters.data_ptr() if need else None,
+        None, 0, None,
         query.stride(0), query.stride(1), k_cache.stride(0), k_cache.stride(1), k_cache.stride(2),
         v_cache.stride(0), v_cache.stride(1), v_cache.stride(2), out.stride(0), out.stride(1),
         bt.stride(0) if bt.dim() == 2 else 0,
         total_q, num_seqs, hq, hkv, d, bs, nb, bt.shape[1] if bt.dim() == 2 else 0, max_seq_len,
         _dtype_code(query.dtype), float(scale))
+    if tiles is not None:
+        a.decode_tokens, a.n_decode_tokens = tokens
+        a.prefill_tiles, a.n_prefill_tiles = tiles
+    need_b, need_c = ctypes.c_uint64(0), ctypes.c_uint64(0)
+    _check(lib.ns_paged_attention_call_workspace(ctypes.byref(a), ctypes.byref(need_b), ctypes.byref(need_c)))
+    need, ncount = int(need_b.value), int(need_c.value)
+    if need and workspace is None:
+        workspace = torch.empty(need, dtype=torch.uint8, device=dev)
+    elif need and workspace.numel() * workspace.element_size() < need:
+        raise PagedAttentionError(
+            f"workspace of {need} bytes needed, {workspace.numel() * workspace.element_size()} given (total_q "
+            f"{total_q}, max_seq_len {max_seq_len}, {a.n_decode_tokens if tiles is not None else total_q} "
+            f"per-token queries, {a.n_prefill_tiles if tiles is not None else 0} prefill tiles)")
+    if need and counters is None:
+        counters = counters_for(dev, ncount, s)
+    elif need and (counters.dtype != torch.int32 or counters.device != dev or counters.numel() < ncount):
+        raise PagedAttentionError(f"counters must be an int32 device tensor of at least {ncount} entries")
+    if need:
+        a.workspace, a.workspace_bytes, a.counters = workspace.data_ptr(), need, counters.data_ptr()
     _check(lib.ns_paged_attention(ctypes.byref(a), ctypes.c_void_p(int(s.cuda_stream))))
     return out
 

@@ -41,8 +41,14 @@ def query_places(seq_lens, query_start_loc, query_lens):
 
 
 def paged_attention(query, k_cache, v_cache, block_tables, seq_lens, query_start_loc, query_lens,
-                    scale: float, block_size: int) -> np.ndarray:
-    """float64 (total_q, Hq, D) attention output (paged_attention_triton.py:19-106)."""
+                    scale: float, block_size: int, terms: bool = False):
+    """float64 (total_q, Hq, D) attention output (paged_attention_triton.py:19-106).
+
+    ``terms``: also return, per output element, the condition term ``S * dev + Vabs`` that scales a
+    float computation's rounding error: S = max over visible keys of ``scale * sum_i |q_i k_i|``
+    (a dot product's error is at most proportional to it, and it moves the output by the softmax
+    weights times ``v - o``), dev = ``sum_t w_t |v_t - o|``, Vabs = ``sum_t w_t |v_t|`` (the
+    weighted sum's own error bound, w the normalised weights)."""
     q = np.asarray(query, dtype=np.float64)
     kc = np.asarray(k_cache, dtype=np.float64)
     vc = np.asarray(v_cache, dtype=np.float64)
@@ -51,6 +57,7 @@ def paged_attention(query, k_cache, v_cache, block_tables, seq_lens, query_start
     hkv = kc.shape[2]
     groups = hq // hkv
     out = np.zeros((total_q, hq, d), dtype=np.float64)
+    cond = np.zeros((total_q, hq, d), dtype=np.float64) if terms else None
     for s, kv_len, row in query_places(seq_lens, query_start_loc, query_lens):
         if kv_len == 0:
             continue
@@ -64,4 +71,9 @@ def paged_attention(query, k_cache, v_cache, block_tables, seq_lens, query_start
             sc = (k[:, kvh, :] @ q[row, h]) * scale
             w = np.exp(sc - sc.max())
             out[row, h] = (w @ v[:, kvh, :]) / w.sum()
-    return out
+            if terms:
+                wn = w / w.sum()
+                vv = v[:, kvh, :]
+                smax = float((np.abs(k[:, kvh, :]) @ np.abs(q[row, h])).max()) * abs(scale)
+                cond[row, h] = smax * (wn @ np.abs(vv - out[row, h])) + wn @ np.abs(vv)
+    return (out, cond) if terms else out

@@ -72,7 +72,52 @@ def to_device(case, device):
 TOL = {torch.float32: (1e-5, 1e-4), torch.float16: (1e-4, 2.0 ** -9), torch.bfloat16: (1e-4, 2.0 ** -7)}
 
 
+# unit roundoff of the kernels' arithmetic per input type: float32 throughout for float32 inputs;
+# for 16-bit inputs the weights enter the MFMA value product as a high and a low 16-bit part
+# (16 significant bits at least)
+UNIT = {torch.float32: 2.0 ** -24, torch.float16: 2.0 ** -16, torch.bfloat16: 2.0 ** -16}
+OUT_BITS = {torch.float32: None, torch.float16: 11, torch.bfloat16: 8}
+# Arithmetic bound: |out - oracle| <= half an output ulp + K * UNIT * cond, cond = S * dev + Vabs
+# per element (the oracle's condition term).  Worst ratios over the GPU suite
+# (|err| - half ulp) / (UNIT * cond): float32 2.4, float16 0.0017, bfloat16 0.026; K sits a few
+# times above each.
+ARITH_K = {torch.float32: 8.0, torch.float16: 0.25, torch.bfloat16: 0.25}
+
+
+def half_ulp(x, dtype):
+    """Half a unit in the last place of |x| in the output type (0 for float32 outputs)."""
+    bits = OUT_BITS[dtype]
+    if bits is None:
+        return np.zeros_like(x)
+    _, e = np.frexp(np.abs(x))
+    h = np.ldexp(1.0, e - 1 - bits)
+    if dtype == torch.float16:
+        h = np.maximum(h, 2.0 ** -25)   # subnormal spacing
+    return h
+
+
+def arithmetic_ratio(out, ref, cond, dtype):
+    """max over elements of (|err| - half an output ulp) / (u * cond): the error in units of the
+    arithmetic's rounding scaled by the element's condition term."""
+    got = out.double().cpu().numpy()
+    err = np.abs(got - ref) - half_ulp(np.maximum(np.abs(ref), np.abs(got)), dtype)
+    return float((err / (UNIT[dtype] * np.maximum(cond, 1e-30))).max())
+
+
 def assert_close_to_oracle(out, ref, dtype):
+    """``ref``: the oracle's output, or (output, condition terms) for the arithmetic bound."""
+    if isinstance(ref, tuple):
+        ref, cond = ref
+        got = out.double().cpu().numpy()
+        err = np.abs(got - ref)
+        bound = half_ulp(np.maximum(np.abs(ref), np.abs(got)), dtype) + ARITH_K[dtype] * UNIT[dtype] * cond
+        ratio = arithmetic_ratio(out, ref, cond, dtype)
+        print(f"paged attention: arithmetic error ratio {ratio:.3g} (bound {ARITH_K[dtype]})", flush=True)
+        bad = err > bound
+        assert not bad.any(), (
+            f"{int(bad.sum())} of {bad.size} outputs outside half an ulp + {ARITH_K[dtype]} * u * cond; worst ratio "
+            f"{ratio:.3g} at {np.unravel_index(int(np.argmax(err - bound)), err.shape)}")
+        return
     atol, rtol = TOL[dtype]
     got = out.double().cpu().numpy()
     err = np.abs(got - ref)

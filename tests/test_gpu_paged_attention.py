@@ -1,7 +1,9 @@
 """GPU parity of the HIP paged-attention kernels (through the C-ABI) against the CPU oracle
-(float64 restatement of nanoserve/kernels/paged_attention_triton.py:19-131). Tolerances: float32
-output atol 1e-5 + rtol 1e-4; float16 atol 1e-4 + rtol 2^-9; bfloat16 atol 1e-4 + rtol 2^-7 (one
-rounding of the float32 result to the output type, plus float32 arithmetic)."""
+(float64 restatement of nanoserve/kernels/paged_attention_triton.py:19-131). Tolerance per output
+element: half an ulp of the output type (none for float32) + K * u * cond, cond = S * dev + Vabs the
+oracle's condition term (the largest |q|.|k| score scale times the weighted spread of the values,
+plus the weighted |v|), u = 2^-24 for float32 and 2^-16 for the 16-bit types, K = 8 resp. 0.25
+(tests/pa_cases.py)."""
 import numpy as np
 import pytest
 import torch
@@ -26,7 +28,7 @@ def run(case, device, **kw):
 
 def check(case, device, **kw):
     out = run(case, device, **kw)
-    ref = PA.paged_attention(**oracle_args(case))
+    ref = PA.paged_attention(**oracle_args(case), terms=True)
     assert_close_to_oracle(out, ref, case["query"].dtype)
     return out
 
@@ -92,9 +94,9 @@ def test_status_flags_bad_block_and_short_max_seq_len(device):
     status = torch.zeros(1, dtype=torch.int32, device=device)
     out = run(bad, device, status=status)
     assert status.item() & A.STATUS_BAD_BLOCK
-    ref = PA.paged_attention(**oracle_args(case))
+    ref, cond = PA.paged_attention(**oracle_args(case), terms=True)
     # the other sequence is untouched by the bad entry
-    assert_close_to_oracle(out[1:], ref[1:], case["query"].dtype)
+    assert_close_to_oracle(out[1:], (ref[1:], cond[1:]), case["query"].dtype)
     status.zero_()
     run(case, device, status=status)
     assert status.item() == 0
@@ -125,7 +127,7 @@ def test_split_rows_leave_the_counters_at_zero(device):
         case = make_case(seed, lens, [1] * len(lens))
         q = case["query"]
         assert A.workspace_bytes(q.shape[0], q.shape[1], case["k_cache"].shape[2], q.shape[2], max(lens)) > 0
-        ref = PA.paged_attention(**oracle_args(case))
+        ref = PA.paged_attention(**oracle_args(case), terms=True)
         outs = []
         for _ in range(2):
             out = run(case, device, workspace=ws, counters=counters)
@@ -166,3 +168,94 @@ def test_side_stream_and_output_stride(device):
     with pytest.raises(A.PagedAttentionError, match="unit head_dim stride"):
         A.paged_attention_hip(q, c["k_cache"], c["v_cache"], c["block_tables"], c["seq_lens"],
                               c["query_start_loc"], c["query_lens"], c["scale"], c["block_size"], out=bad)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("hq,hkv,d", [(24, 8, 128), (32, 8, 128), (8, 8, 64), (16, 8, 64), (64, 8, 128)])
+def test_prefill_tiles_head_layouts(device, dtype, hq, hkv, d):
+    # sequences of several query tokens go by MFMA query tile (64 // G tokens each): a chunk in the
+    # middle of a long sequence, a full prefill, chunks shorter than a tile, and decode rows beside them
+    case = make_case(50 + hq + d, [700, 300, 190, 1, 90, 45], [200, 300, 3, 1, 17, 1], hq=hq, hkv=hkv, d=d,
+                     dtype=dtype)
+    check(case, device)
+
+
+def test_prefill_chunk_512_over_4096_positions(device):
+    # the reference's chunked_prefill_size (config.py:53): a 512-token chunk at the end of a 4096-position
+    # sequence, split over KV partitions merged by the last to arrive, and a second chunk of another sequence
+    case = make_case(60, [4096, 1500], [512, 512])
+    check(case, device)
+
+
+@pytest.mark.parametrize("block_size", [1, 7, 16, 32])
+def test_prefill_tiles_block_sizes(device, block_size):
+    case = make_case(70 + block_size, [130, 77], [64, 77], block_size=block_size)
+    check(case, device)
+
+
+def test_prefill_tiles_repeat_bit_exact_and_strided_query(device):
+    case = make_case(80, [900, 64], [300, 64], qkv_view=True)
+    a = check(case, device)
+    b = run(case, device)
+    assert torch.equal(a, b)
+
+
+def test_prefill_bad_tile_is_flagged(device):
+    # a tile reaching past its sequence's query tokens is refused by the kernel (status bit), nothing
+    # out of bounds is touched, and the other tiles and tokens are exact
+    import ctypes
+
+    case = make_case(90, [100, 40], [40, 1])
+    c = to_device(case, device)
+    q = c["query"]
+    out = torch.full_like(q, 7.0)
+    tiles = torch.tensor([[0, 0, 21], [0, 21, 19], [0, 30, 21]], dtype=torch.int32, device=device)
+    tokens = torch.tensor([40], dtype=torch.int32, device=device)
+    status = torch.zeros(1, dtype=torch.int32, device=device)
+    lib = A.load()
+    bt = c["block_tables"]
+    a = A.NsPagedAttnArgs(
+        q.data_ptr(), c["k_cache"].data_ptr(), c["v_cache"].data_ptr(), out.data_ptr(), bt.data_ptr(),
+        c["seq_lens"].data_ptr(), c["query_start_loc"].data_ptr(), c["query_lens"].data_ptr(), status.data_ptr(),
+        None, 0, None, q.stride(0), q.stride(1), c["k_cache"].stride(0), c["k_cache"].stride(1),
+        c["k_cache"].stride(2), c["v_cache"].stride(0), c["v_cache"].stride(1), c["v_cache"].stride(2),
+        out.stride(0), out.stride(1), bt.stride(0), q.shape[0], 2, 24, 8, 128, 16, c["k_cache"].shape[0], bt.shape[1],
+        100, A.NS_PA_DTYPE_BF16, c["scale"])
+    a.decode_tokens, a.n_decode_tokens = tokens.data_ptr(), 1
+    a.prefill_tiles, a.n_prefill_tiles = tiles.data_ptr(), 3
+    nb, nc = ctypes.c_uint64(0), ctypes.c_uint64(0)
+    assert lib.ns_paged_attention_call_workspace(ctypes.byref(a), ctypes.byref(nb), ctypes.byref(nc)) == 0
+    ws = torch.empty(max(int(nb.value), 1), dtype=torch.uint8, device=device)
+    cnt = torch.zeros(max(int(nc.value), 1), dtype=torch.int32, device=device)
+    a.workspace, a.workspace_bytes, a.counters = ws.data_ptr(), int(nb.value), cnt.data_ptr()
+    assert lib.ns_paged_attention(ctypes.byref(a), None) == 0
+    torch.cuda.synchronize()
+    assert status.item() & A.STATUS_BAD_TILE
+    ref = PA.paged_attention(**oracle_args(case), terms=True)
+    assert_close_to_oracle(out, ref, q.dtype)   # the two valid tiles cover tokens 0..39, the list token 40
+    assert torch.count_nonzero(cnt).item() == 0
+
+
+def test_plan_reused_across_layers_and_refused_for_another_layout(device):
+    # one host plan per step serves every layer's call (two caches here): same outputs as the
+    # calls that plan for themselves, and a plan of another layout is refused
+    case = make_case(95, [1200, 333, 64, 9], [400, 333, 1, 1])
+    other = make_case(96, [1200, 333, 64, 9], [400, 333, 1, 1])
+    c, o = to_device(case, device), to_device(other, device)
+    plan = A.PagedAttentionPlan(c["seq_lens"], c["query_start_loc"], c["query_lens"], 24, 8, device)
+    assert plan.tiles is not None and plan.tokens[1] == 2
+    outs = []
+    for x in (c, o):
+        args = (x["query"], x["k_cache"], x["v_cache"], x["block_tables"], x["seq_lens"], x["query_start_loc"],
+                x["query_lens"], x["scale"], x["block_size"])
+        with_plan = A.paged_attention_hip(*args, plan=plan)
+        without = A.paged_attention_hip(*args)
+        torch.cuda.synchronize()
+        assert torch.equal(with_plan, without)
+        outs.append(with_plan)
+    for case_, out in zip((case, other), outs):
+        assert_close_to_oracle(out, PA.paged_attention(**oracle_args(case_), terms=True), torch.bfloat16)
+    bad = A.PagedAttentionPlan(c["seq_lens"], c["query_start_loc"], c["query_lens"], 32, 8, device)
+    with pytest.raises(A.PagedAttentionError, match="another batch layout"):
+        A.paged_attention_hip(c["query"], c["k_cache"], c["v_cache"], c["block_tables"], c["seq_lens"],
+                              c["query_start_loc"], c["query_lens"], c["scale"], c["block_size"], plan=bad)

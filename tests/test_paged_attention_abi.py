@@ -4,6 +4,8 @@ invalid arguments before touching a GPU."""
 import ctypes
 import os
 import re
+import subprocess
+import tempfile
 
 import pytest
 
@@ -38,11 +40,54 @@ def test_library_exports_every_header_symbol():
 def test_struct_layout_matches_header():
     txt = open(HEADER).read()
     body = txt[txt.index("typedef struct ns_paged_attn_args"):txt.index("} ns_paged_attn_args;")]
+    body = re.sub(r"/\*.*?\*/", "", body, flags=re.S)   # comments may hold semicolons
     names = []
     for decl in re.findall(r"^\s*([^/{}]+?);", body, flags=re.M):
         names += [n.strip().lstrip("*") for n in re.sub(r"^.*?\b(\w+)\s*(,|$)", r"\1\2", decl, count=1).split(",")]
     assert names == [f[0] for f in PA.NsPagedAttnArgs._fields_]
-    assert ctypes.sizeof(PA.NsPagedAttnArgs) == 232
+    # every field's offset and the size, as the C compiler lays the header's struct out
+    src = "#include <stdio.h>\n#include <stddef.h>\n#include \"ns_paged_attention.h\"\nint main(void) {\n"
+    src += '  printf("%zu\\n", sizeof(ns_paged_attn_args));\n'
+    for n in names:
+        src += f'  printf("%zu\\n", offsetof(ns_paged_attn_args, {n}));\n'
+    src += "  return 0;\n}\n"
+    with tempfile.TemporaryDirectory() as d:
+        c, exe = os.path.join(d, "layout.c"), os.path.join(d, "layout")
+        with open(c, "w") as f:
+            f.write(src)
+        rocm = os.environ.get("ROCM_PATH", "/opt/rocm")
+        subprocess.run(["gcc", "-D__HIP_PLATFORM_AMD__", "-I", os.path.dirname(HEADER), "-I",
+                        os.path.join(rocm, "include"), c, "-o", exe], check=True)
+        got = [int(v) for v in subprocess.run([exe], check=True, capture_output=True, text=True).stdout.split()]
+    assert got[0] == ctypes.sizeof(PA.NsPagedAttnArgs)
+    assert got[1:] == [getattr(PA.NsPagedAttnArgs, n).offset for n in names]
+
+
+def test_plan_tiles_covers_every_token_once():
+    """The host plan of a chunked-prefill batch: sequences with several query tokens cut into tiles
+    of 64 // G consecutive tokens of one sequence, every other token listed once, for any G."""
+    import numpy as np
+
+    rng = np.random.default_rng(3)
+    for hq, hkv in ((24, 8), (32, 8), (8, 8), (16, 8), (64, 8)):
+        qlens = np.concatenate([rng.integers(0, 3, 40), rng.integers(2, 700, 12), [0, 1, 64, 65]])
+        rng.shuffle(qlens)
+        qsl = np.zeros(qlens.size + 1, dtype=np.int64)
+        qsl[1:] = np.cumsum(qlens)
+        seq_lens = qlens + rng.integers(0, 3000, qlens.size)
+        tiles, tokens = PA.plan_tiles(seq_lens, qsl, qlens, hq, hkv)
+        bq = 64 // (hq // hkv)
+        owner = np.full(int(qsl[-1]), -1)
+        for s, t0, n in tiles.tolist():
+            assert 1 <= n <= bq and qlens[s] >= PA.PREFILL_MIN_QUERY
+            assert qsl[s] <= t0 and t0 + n <= qsl[s + 1]
+            assert (owner[t0:t0 + n] == -1).all()
+            owner[t0:t0 + n] = 1
+        for t in tokens.tolist():
+            s = int(np.searchsorted(qsl, t, side="right") - 1)
+            assert qlens[s] < PA.PREFILL_MIN_QUERY and owner[t] == -1
+            owner[t] = 0
+        assert (owner >= 0).all()
 
 
 def test_workspace_sizes():

@@ -102,3 +102,31 @@ def test_query_places_match_the_reference_launcher():
     # repeat_interleave of the sequence ids and kv_pos = seq_len - q_len + i (triton.py:109-131)
     places = PA.query_places([5, 3, 9], [0, 2, 2, 6], [2, 0, 4])
     assert [(s, kv, r) for s, kv, r in places] == [(0, 4, 0), (0, 5, 1), (2, 6, 2), (2, 7, 3), (2, 8, 4), (2, 9, 5)]
+
+
+def test_oracle_condition_terms_closed_forms():
+    # the condition term the GPU tolerance scales with: a single visible key gives dev = 0 and
+    # cond = |v|; constant keys and constant values give dev = 0, cond = |v|; and the terms leave
+    # the output unchanged
+    case = make_case(5, [9, 6], [9, 1], hq=2, hkv=1, d=64, block_size=4, dtype=torch.float32)
+    a = oracle_args(case)
+    out, cond = PA.paged_attention(**a, terms=True)
+    np.testing.assert_array_equal(out, PA.paged_attention(**a))
+    v0 = a["v_cache"][a["block_tables"][0, 0], 0, 0]
+    np.testing.assert_allclose(cond[0, 0], np.abs(v0), rtol=1e-15, atol=0)
+    case["k_cache"][:] = 0.5
+    case["v_cache"][:] = -1.5
+    a = oracle_args(case)
+    out, cond = PA.paged_attention(**a, terms=True)
+    np.testing.assert_allclose(out, -1.5, rtol=1e-15)
+    np.testing.assert_allclose(cond, 1.5, rtol=1e-15)
+    # two keys, hand-computed: q = e0, k0 = 2 e0, k1 = -e0 (scale 1), v0 = 1, v1 = 3 in dim 0
+    q = np.zeros((1, 1, 4)); q[0, 0, 0] = 1.0
+    kc = np.zeros((1, 2, 1, 4)); kc[0, 0, 0, 0] = 2.0; kc[0, 1, 0, 0] = -1.0
+    vc = np.zeros((1, 2, 1, 4)); vc[0, 0, 0, 0] = 1.0; vc[0, 1, 0, 0] = 3.0
+    out, cond = PA.paged_attention(q, kc, vc, np.zeros((1, 1), np.int64), [2], [0, 1], [1], 1.0, 2, terms=True)
+    w0, w1 = math.exp(2) / (math.exp(2) + math.exp(-1)), math.exp(-1) / (math.exp(2) + math.exp(-1))
+    o = w0 * 1 + w1 * 3
+    np.testing.assert_allclose(out[0, 0, 0], o, rtol=1e-14)
+    np.testing.assert_allclose(cond[0, 0, 0], 2.0 * (w0 * abs(1 - o) + w1 * abs(3 - o)) + w0 * 1 + w1 * 3,
+                               rtol=1e-14)
