@@ -307,19 +307,23 @@ def measured_traffic():
     return int(vals["traffic_bytes_per_launch"])
 
 
-STAMP_NAMES = ("entry", "wave0_streamed", "last_wave_streamed", "bound_barrier", "list_barrier", "order_barrier",
-               "drawn")
+# stamp slots of the top-k kernel, in the order a row passes them
+STAMP_SLOTS = (("entry", 0), ("wave0_streamed", 1), ("last_wave_streamed", 2), ("last_wave_bound", 7),
+               ("bound_barrier", 3), ("wave0_staged", 8), ("wave0_listed", 9), ("list_barrier", 4),
+               ("order_barrier", 5), ("wave0_cut", 10), ("drawn", 6))
+NS_STAMPS = 16
 
 
 def phase_stamps(L, dev, w, sets, ws, stream, reps=20, calls=20):
     """Where the top-k kernel's time goes, from its phase stamps: libns_sampling_stamps.so is
     the sampler built with NS_PHASE_STAMPS, whose top-k kernel stores the shader clock
-    (s_memtime) of each workgroup at entry, when wave 0 and when the last wave have streamed and
-    reduced their share of the row, after the bound's barrier, after the candidate list's
-    barrier, after the ordering's barrier and when the id is drawn.  ``reps`` times: ``calls``
-    back-to-back calls over the rotating input sets, then the last call's stamps (every
-    workgroup's, in steady state) are read.  Returns the median clocks of each phase over all
-    rows and repetitions, and the same in microseconds at the clock rate that makes the median
+    (s_memtime) of each workgroup at the points STAMP_SLOTS names: entry; wave 0 and the last
+    wave done streaming and reducing their share of the row; the last wave's bound; the bound's
+    barrier; wave 0's chunks staged and candidates listed; the list's barrier; the ordering's
+    barrier; wave 0's top-k cut; the id drawn.  ``reps`` times: ``calls`` back-to-back calls
+    over the rotating input sets, then the last call's stamps (every workgroup's, in steady
+    state) are read.  Returns, per point, the median clocks since entry over all rows and
+    repetitions, and the same in microseconds at the clock rate that makes the median
     workgroup's span equal the per-call time measured by events in the same run."""
     import torch
 
@@ -327,7 +331,7 @@ def phase_stamps(L, dev, w, sets, ws, stream, reps=20, calls=20):
     lib = ctypes.CDLL(so)
     lib.ns_sample.restype = ctypes.c_int
     lib.ns_phase_stamps_set.restype = ctypes.c_int
-    buf = torch.zeros(w.batch * 8, dtype=torch.int64, device=dev)
+    buf = torch.zeros(w.batch * NS_STAMPS, dtype=torch.int64, device=dev)
     if lib.ns_phase_stamps_set(ctypes.c_void_p(buf.data_ptr())) != 0:
         raise RuntimeError("ns_phase_stamps_set failed")
     cargs = [make_args(L, st, ws) for st in sets]
@@ -345,18 +349,19 @@ def phase_stamps(L, dev, w, sets, ws, stream, reps=20, calls=20):
         e1.record(stream)
         torch.cuda.synchronize()
         t_ms += e0.elapsed_time(e1)
-        rows.append(buf.view(w.batch, 8).cpu().numpy().astype(np.int64))
+        rows.append(buf.view(w.batch, NS_STAMPS).cpu().numpy().astype(np.int64))
     lib.ns_phase_stamps_set(ctypes.c_void_p(0))
-    st = np.concatenate(rows)[:, :len(STAMP_NAMES)]
-    d = np.diff(st, axis=1)
+    st = np.concatenate(rows)
+    t0 = st[:, 0]
     us_per_call = t_ms / (reps * calls) * 1e3
-    span = float(np.median(st[:, -1] - st[:, 0]))
+    span = float(np.median(st[:, 6] - t0))
     per_us = span / us_per_call
     out = {"stamped_kernel_us": us_per_call, "median_workgroup_span_clocks": span, "clocks_per_us": per_us}
-    for j in range(d.shape[1]):
-        name = f"{STAMP_NAMES[j]}->{STAMP_NAMES[j + 1]}"
-        out[name + "_clocks"] = float(np.median(d[:, j]))
-        out[name + "_us"] = float(np.median(d[:, j])) / per_us
+    prev = STAMP_SLOTS[0]
+    for name, slot in STAMP_SLOTS[1:]:
+        out[f"{name}_after_entry_us"] = float(np.median(st[:, slot] - t0)) / per_us
+        out[f"{prev[0]}->{name}_us"] = float(np.median(st[:, slot] - st[:, prev[1]])) / per_us
+        prev = (name, slot)
     return out
 
 

@@ -21,16 +21,19 @@ __device__ __forceinline__ int wave_id() { return threadIdx.x >> 6; }
 // only (the shipped library compiles them away): the shader clock (s_memtime) at phase
 // boundaries of each workgroup, stored to ns_stamp_buf[workgroup * NS_STAMPS + slot] by
 // one lane.  No work is skipped; each stamp waits for the wave's outstanding scalar and LDS
-// operations, which lengthens the path it sits on slightly.
-constexpr int NS_STAMPS = 8;
+// operations, which lengthens the path it sits on slightly.  A function that stamps declares
+// NS_STAMP_DECL first: the buffer's address is read once there, not at every stamp.
+constexpr int NS_STAMPS = 16;
 #ifdef NS_PHASE_STAMPS
 __device__ uint64_t* ns_stamp_buf;
+#define NS_STAMP_DECL uint64_t* const ns_sb_ = ns::ns_stamp_buf
 #define NS_STAMP_LANE(slot, cond)                                                           \
   do {                                                                                       \
-    if ((cond) && ns::ns_stamp_buf != nullptr)                                               \
-      ns::ns_stamp_buf[(int64_t)blockIdx.x * ns::NS_STAMPS + (slot)] = __builtin_amdgcn_s_memtime(); \
+    if ((cond) && ns_sb_ != nullptr)                                                         \
+      ns_sb_[(int64_t)blockIdx.x * ns::NS_STAMPS + (slot)] = __builtin_amdgcn_s_memtime();  \
   } while (0)
 #else
+#define NS_STAMP_DECL do { } while (0)
 #define NS_STAMP_LANE(slot, cond) do { } while (0)
 #endif
 #define NS_STAMP(slot) NS_STAMP_LANE(slot, threadIdx.x == 0)

@@ -1201,6 +1201,7 @@ __device__ __forceinline__ uint32_t vload_word(const void* base, int32_t i, uint
 template <typename T, int NPH>
 __global__ __launch_bounds__(NT) void topk_kernel(const KParams P) {
   const int row = blockIdx.x;
+  NS_STAMP_DECL;
   NS_STAMP(0);
   // Without sample indices or device-resident history slots the row and its history range
   // need no dependent load: the per-row parameters are requested first (vector loads, served

@@ -702,6 +702,7 @@ __device__ __forceinline__ void block_finalize_keys(const uint64_t* list, uint64
                                                     float p32, float u, int row, const IdSink& out_ids, float* out_probs,
                                                     int64_t V, int32_t* out_info, int32_t flags, int32_t n_cand,
                                                     int32_t path) {
+  NS_STAMP_DECL;
   const int tid = threadIdx.x;
   uint64_t* sorted = out;
   uint64_t* byid = out + WAVE_CAP;
@@ -724,6 +725,7 @@ __device__ __forceinline__ void block_finalize_keys(const uint64_t* list, uint64
     const int i = base + tid;
     nk += __popcll(ballot(i < n && desc_key_val(sorted[i < n ? i : 0]) >= thr));
   }
+  NS_STAMP(10);   // wave 0: the top-k cut
   if (nk <= 64 && g8) {
     wave_draw_sorted(a2[0], nk, n, byid, vr, M, thr, topp_on, p32, u, row, out_ids, out_probs, V, out_info, flags,
                      n_cand, path);

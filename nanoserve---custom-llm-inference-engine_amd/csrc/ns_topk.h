@@ -119,6 +119,7 @@ __device__ __forceinline__ int topk_stream(const RowArgs P, const int row, const
                                            const float u, const int32_t H, Misc* misc, uint32_t* bm,
                                            uint64_t* cand) {
   constexpr int EPC = T::EPC;
+  NS_STAMP_DECL;
   const int tid = threadIdx.x;
   const int lane = lane_id();
   const int wid = wave_id();
@@ -251,6 +252,7 @@ __device__ __forceinline__ int topk_stream(const RowArgs P, const int row, const
                                                          fkey(fs[192 + lane]), k);
       const float taux = kp <= fkey(-__builtin_inff()) ? -__builtin_inff() : fkey_inv(kp);
       const float b = lower_preimage(taux, tdiv, rdiv);
+      NS_STAMP_LANE(7, lane == 0);   // the last wave: the bound taken
       if (lane == 0) misc->fb[0] = b;
     }
   }
@@ -344,6 +346,7 @@ __device__ __forceinline__ int topk_stream(const RowArgs P, const int row, const
         nh += __popcll(m);
       }
     }
+    NS_STAMP(8);   // wave 0: its chunks staged
     if (__builtin_expect(nh > HIT_PER_WAVE, 0)) {
       // more hit chunks than slots: the count goes past WAVE_CAP and the general code
       // takes the row
@@ -365,6 +368,7 @@ __device__ __forceinline__ int topk_stream(const RowArgs P, const int row, const
       }
     }
     if (ntail > 0 && wid == 0) take_key(xt, (uint32_t)(nf * EPC + lane), lane < ntail);
+    NS_STAMP(9);   // wave 0: its candidates listed
   };
   collect(std::false_type{});
   __syncthreads();   // the list complete
