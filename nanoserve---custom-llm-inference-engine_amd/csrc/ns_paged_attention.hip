@@ -31,8 +31,7 @@ namespace {
 
 constexpr int kThreads = 256;
 constexpr int kWaves = kThreads / 64;
-constexpr int kSub = 2;                 // KV positions per lane per batch (8 lanes per position)
-constexpr int kBatch = 8 * kSub;        // KV positions per wave batch
+constexpr int kSub = 2;                 // KV positions per lane per batch
 constexpr int kMaxPart = 1024;          // largest KV partition (LDS score buffer)
 constexpr int kMinPart = 64;
 constexpr int kTargetGroups = 1024;     // workgroups a launch aims for before splitting stops
@@ -151,11 +150,18 @@ __device__ __forceinline__ float octet_sum(float x) {
   return x;
 }
 
-// Sum over the lanes that share lane & 7 (xor 8, 16, 32).
+// Sum over the 16 lanes of an aligned group (the octet sum, then xor 8).
+__device__ __forceinline__ float hex_sum(float x) {
+  x = octet_sum(x);
+  x += __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(x), 0x201F));
+  return x;
+}
+
+// Sum over the lanes that share lane % L (xor L, 2L, ... 32).
+template <int L>
 __device__ __forceinline__ float slot_sum(float x) {
-  x += __shfl_xor(x, 8);
-  x += __shfl_xor(x, 16);
-  x += __shfl_xor(x, 32);
+#pragma unroll
+  for (int s = L; s < 64; s <<= 1) x += __shfl_xor(x, s);
   return x;
 }
 
@@ -208,7 +214,13 @@ __device__ __forceinline__ QueryPlace place_query(const PaParams& p, int qi) {
 
 template <typename T, int D, int G>
 __global__ __launch_bounds__(kThreads) void pa_partition_kernel(PaParams p) {
-  constexpr int DS = D / 8;  // dims per lane
+  // L lanes per KV position, DS dims each: 8 lanes, or 16 for eight heads of 128 dims (the query
+  // slices and accumulators of eight heads would not fit the registers at 16 dims a lane)
+  constexpr int L = (G == 8 && D == 128) ? 16 : 8;
+  constexpr int DS = D / L;           // dims per lane
+  constexpr int NSLOT = 64 / L;       // positions a wave covers per row of a batch
+  constexpr int kBatch = NSLOT * kSub;  // KV positions per wave batch
+  static_assert(G <= L, "the lane with dl == g stores head g's score");
   __shared__ float s_score[G * kMaxPart];
   __shared__ float s_red[kWaves * G * D];
   __shared__ float s_m[G], s_l[G];
@@ -221,8 +233,8 @@ __global__ __launch_bounds__(kThreads) void pa_partition_kernel(PaParams p) {
     if (threadIdx.x == 0 && part == 0 && kvh == 0 && p.status) atomicOr(p.status, NS_PA_STATUS_BAD_TILE);
     return;
   }
-  const int slot = lane >> 3;  // position within a half step
-  const int dl = lane & 7;     // dim slice
+  const int slot = lane / L;  // position within a row of the batch
+  const int dl = lane % L;     // dim slice
   const QueryPlace qp = place_query(p, qi);
   const int n_parts = (qp.kv_len + p.part_tokens - 1) / p.part_tokens;
 
@@ -289,7 +301,7 @@ __global__ __launch_bounds__(kThreads) void pa_partition_kernel(PaParams p) {
 #pragma unroll
     for (int r = 0; r < kSub; ++r) {
       int off = 0;
-      blk[r] = block_of(base + r * 8 + slot, off);
+      blk[r] = block_of(base + r * NSLOT + slot, off);
       if (blk[r] >= 0)
         load_raw<T, DS>(p.k, (int64_t)blk[r] * p.sk_blk + (int64_t)off * p.sk_tok + (int64_t)kvh * p.sk_head + dl * DS,
                         raw[r]);
@@ -298,13 +310,13 @@ __global__ __launch_bounds__(kThreads) void pa_partition_kernel(PaParams p) {
     for (int r = 0; r < kSub; ++r) {
       float kx[DS];
       to_float<T, DS>(raw[r], kx);
-      const int j = base + r * 8 + slot;
+      const int j = base + r * NSLOT + slot;
 #pragma unroll
       for (int g = 0; g < G; ++g) {
         float sc = 0.f;
 #pragma unroll
         for (int i = 0; i < DS; ++i) sc = fmaf(qv[g][i], kx[i], sc);
-        sc = octet_sum(sc);
+        sc = L == 8 ? octet_sum(sc) : hex_sum(sc);
         if (dl == g && j < n) s_score[g * kMaxPart + j] = blk[r] >= 0 ? sc : -INFINITY;
       }
     }
@@ -317,7 +329,7 @@ __global__ __launch_bounds__(kThreads) void pa_partition_kernel(PaParams p) {
 #pragma unroll
     for (int r = 0; r < kSub; ++r) {
       int off = 0;
-      vblk[r] = block_of(base + r * 8 + slot, off);
+      vblk[r] = block_of(base + r * NSLOT + slot, off);
       if (vblk[r] >= 0)
         load_raw<T, DS>(p.v, (int64_t)vblk[r] * p.sv_blk + (int64_t)off * p.sv_tok + (int64_t)kvh * p.sv_head + dl * DS,
                         vraw[r]);
@@ -358,7 +370,7 @@ __global__ __launch_bounds__(kThreads) void pa_partition_kernel(PaParams p) {
       if (vblk[r] < 0) continue;
       float vx[DS];
       to_float<T, DS>(vraw[r], vx);
-      const int j = base + r * 8 + slot;
+      const int j = base + r * NSLOT + slot;
 #pragma unroll
       for (int g = 0; g < G; ++g) {
         const float w = s_score[g * kMaxPart + j];
@@ -367,11 +379,11 @@ __global__ __launch_bounds__(kThreads) void pa_partition_kernel(PaParams p) {
       }
     }
   }
-  // sum the 8 position slots of the wave, then the waves through LDS
+  // sum the position slots of the wave, then the waves through LDS
 #pragma unroll
   for (int g = 0; g < G; ++g)
 #pragma unroll
-    for (int i = 0; i < DS; ++i) acc[g][i] = slot_sum(acc[g][i]);
+    for (int i = 0; i < DS; ++i) acc[g][i] = slot_sum<L>(acc[g][i]);
   if (slot == 0) {
 #pragma unroll
     for (int g = 0; g < G; ++g)

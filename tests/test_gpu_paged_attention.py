@@ -52,7 +52,7 @@ def test_chunked_prefill_mix(device):
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16])
-@pytest.mark.parametrize("hq,hkv,d", [(8, 8, 128), (16, 8, 64), (32, 8, 128), (32, 4, 64), (24, 8, 64)])
+@pytest.mark.parametrize("hq,hkv,d", [(8, 8, 128), (16, 8, 64), (32, 8, 128), (32, 4, 64), (24, 8, 64), (64, 8, 128)])
 def test_head_layouts_and_dtypes(device, dtype, hq, hkv, d):
     case = make_case(13 + hq + d, [70, 1, 260, 33], [1, 1, 30, 33], hq=hq, hkv=hkv, d=d, block_size=16,
                      dtype=dtype)
