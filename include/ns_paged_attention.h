@@ -38,6 +38,10 @@ extern "C" {
 #define NS_PA_DTYPE_BF16 1
 #define NS_PA_DTYPE_F16 2
 
+/* query columns of a prefill tile: a tile holds 1 .. NS_PA_TILE_COLUMNS / (num_heads_q /
+   num_kv_heads) consecutive query tokens of one sequence */
+#define NS_PA_TILE_COLUMNS 128
+
 /* status bits written (OR-ed) by the kernels when args->status is not NULL */
 #define NS_PA_STATUS_BAD_BLOCK 1   /* a block table entry outside [0, num_blocks), or a position past
                                       max_blocks_per_seq blocks: that key is skipped */
@@ -81,7 +85,7 @@ typedef struct ns_paged_attn_args {
   float          scale;
   /* Query tiles for sequences with several query tokens (chunked prefill), bfloat16 and float16
    * only: prefill_tiles holds n_prefill_tiles int32 triples (sequence, first query token, token
-   * count), each 1 .. 64 / (num_heads_q / num_kv_heads) consecutive tokens of one sequence; a tile
+   * count), each 1 .. NS_PA_TILE_COLUMNS / (num_heads_q / num_kv_heads) consecutive tokens of one sequence; a tile
    * reads each key and value row once for all its tokens and heads (MFMA).  With tiles,
    * decode_tokens lists the n_decode_tokens other query tokens (flat indices), which the per-token
    * kernel takes; every query token belongs to exactly one tile or the list (an unlisted token's

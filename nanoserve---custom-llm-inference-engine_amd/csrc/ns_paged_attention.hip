@@ -486,57 +486,71 @@ __global__ __launch_bounds__(kThreads) void pa_partition_kernel(PaParams p) {
 
 // ---- prefill kernel: query tiles on MFMA -------------------------------------------------------
 //
-// Sequences with several query tokens (chunked prefill) go by query tile: one 64-thread workgroup
-// per (tile, KV head, KV partition) holds 64 query columns -- kPfCols / G tokens of one sequence
-// times the G query heads of the KV head, column c = token (c / G), head (c % G) -- and walks the
-// partition's positions 32 at a time, so each key and value row is read once per tile instead of
-// once per query token.  On v_mfma_f32_32x32x16 (bf16 or f16 operands, float32 accumulation):
-//   * S^T = K Q^T: rows the tile's 32 positions, columns the queries.  A lane holds one query
-//     column (lane % 32) of 16 positions, so the online softmax of a column (max, exp2, sum) runs
-//     in the lane plus one exchange with lane ^ 32;
-//   * O^T += V^T P^T over the positions, the probabilities taken straight from the S^T layout as
-//     the B operand: position slot i of k-step s in the lanes of half h is position
-//     16 s + 8 (i / 4) + 4 h + i % 4 of the tile, and the V^T operand is gathered from the value
-//     rows staged in LDS in that order.  P goes in as two 16-bit parts, hi = RN(p) and
-//     lo = RN(p - hi): both products with a value are exact in float32, so the sum carries p to
-//     about 2^-17 relative, the float32 arithmetic of the reference's kernel (a single 16-bit P
-//     would round each weight by up to 2^-9).
+// Sequences with several query tokens (chunked prefill) go by query tile: one workgroup of four
+// waves per (tile, KV head, KV partition) holds kPfCols = 128 query columns -- kPfCols / G tokens
+// of one sequence times the G query heads of the KV head, column c = token (c / G), head (c % G),
+// 32 columns per wave -- and walks the partition's positions 64 at a time.  Each step's key and
+// value rows are read from memory once for the whole tile (all 256 threads load them into LDS:
+// keys as rows, values transposed, dims as rows), so each row is read once per 128 columns
+// instead of once per query token.  On v_mfma_f32_32x32x16 (bf16 or f16 operands, float32
+// accumulation), per wave:
+//   * S^T = K Q^T for the step's two 32-position row blocks: rows positions, columns the wave's
+//     queries.  A lane holds one query column (lane % 32) of 16 positions per block, so the
+//     online softmax of a column (max, exp2, sum) runs in the lane plus one exchange with
+//     lane ^ 32;
+//   * O^T += V^T P^T over the step's four 16-position k-steps, the probabilities taken straight
+//     from the S^T layout as the B operand: k-slot i of the lanes of half h is position
+//     16 s + 8 (i / 4) + 4 h + i % 4 of the step, and the V^T operand is read in that order from
+//     the transposed value rows (two 8-byte reads).  P goes in as two 16-bit parts, hi = RN(p)
+//     and lo = RN(p - hi): both products with a value are exact in float32, so the sum carries p
+//     to about 2^-17 relative, the float32 arithmetic of the reference's kernel (a single 16-bit
+//     P would round each weight by up to 2^-9).
 // The scores are the float32 dot products times scale * log2(e) and exp2 replaces exp, as in the
 // decode kernel.  A tile whose positions span several partitions has them merged by the last to
 // arrive, as the decode kernel's split rows are.
 
-constexpr int kPfCols = 64;     // query columns of a tile (two 32-column blocks)
-constexpr int kPfPos = 32;      // positions per step (the MFMA's 32 rows)
+constexpr int kPfWaves = 4;
+constexpr int kPfThreads = 64 * kPfWaves;
+constexpr int kPfCols = 32 * kPfWaves;   // query columns of a tile (32 per wave)
+constexpr int kPfPos = 64;               // positions per step (two 32-row blocks)
 constexpr int kPfMaxPart = 1024;
-constexpr int kPfMinPart = 128;
+constexpr int kPfMinPart = 256;
+constexpr int kPfTargetGroups = 512;     // two four-wave workgroups per CU
+static_assert(kPfCols == NS_PA_TILE_COLUMNS, "the header's tile width");
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
 
+// The MFMA and the 16-bit type's conversions: pack2 rounds two floats to nearest even into one
+// word (low half the first; v_cvt_pk_bf16_f32 for bfloat16), lo / hi widen a word's halves back.
 template <typename T> struct Mma;
 template <> struct Mma<Bf16> {
   typedef bf16x8_t vec;
   static __device__ __forceinline__ f32x16_t mma(vec a, vec b, f32x16_t c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
   }
-  // float -> bfloat16 bits, round to nearest even (p and its remainder are finite)
-  static __device__ __forceinline__ uint32_t bits(float x) {
-    const uint32_t u = __float_as_uint(x);
-    return (u + 0x7FFFu + ((u >> 16) & 1u)) >> 16;
+  static __device__ __forceinline__ uint32_t pack2(float a, float b) {
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2){a, b}, bf16x2_t));
   }
-  static __device__ __forceinline__ float widen(uint32_t h) { return __uint_as_float(h << 16); }
+  static __device__ __forceinline__ float lo(uint32_t w) { return __uint_as_float(w << 16); }
+  static __device__ __forceinline__ float hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
 };
 template <> struct Mma<F16> {
   typedef f16x8_t vec;
   static __device__ __forceinline__ f32x16_t mma(vec a, vec b, f32x16_t c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
   }
-  static __device__ __forceinline__ uint32_t bits(float x) {
-    return (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)x);
+  static __device__ __forceinline__ uint32_t pack2(float a, float b) {
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2){a, b}, f16x2_t));
   }
-  static __device__ __forceinline__ float widen(uint32_t h) {
-    return (float)__builtin_bit_cast(_Float16, (uint16_t)h);
+  static __device__ __forceinline__ float lo(uint32_t w) { return (float)__builtin_bit_cast(_Float16, (uint16_t)w); }
+  static __device__ __forceinline__ float hi(uint32_t w) {
+    return (float)__builtin_bit_cast(_Float16, (uint16_t)(w >> 16));
   }
 };
 
@@ -550,19 +564,26 @@ struct PfParams {
 };
 
 template <typename T, int D, int G>
-__global__ __launch_bounds__(64) void pa_prefill_kernel(PaParams p, PfParams f) {
+__global__ __launch_bounds__(kPfThreads) __attribute__((amdgpu_waves_per_eu(2, 2))) void pa_prefill_kernel(PaParams p,
+                                                                                                        PfParams f) {
   using M = Mma<T>;
   using vec = typename M::vec;
-  constexpr int BQ = kPfCols / G;          // tokens per tile
-  constexpr int KS = D / 16;               // k-steps of S^T = K Q^T
-  constexpr int DB = D / 32;               // 32-row blocks of O^T
-  constexpr int PITCH = D * 2 + 16;        // bytes per staged value row (rows 4 apart in other banks)
-  __shared__ __align__(16) unsigned char s_v[kPfPos * PITCH];
-  __shared__ int s_blk[kPfMaxPart / 1 + 2];
+  constexpr int BQ = kPfCols / G;                 // tokens per tile
+  constexpr int KS = D / 16;                      // k-steps of S^T = K Q^T
+  constexpr int DB = D / 32;                      // 32-dim blocks of O^T
+  constexpr int CPP = D / 8;                      // 16-byte chunks of a key or value row
+  constexpr int LPT = kPfPos * CPP / kPfThreads;  // chunks of each kind a thread loads per step
+  constexpr int PK = D * 2 + 16;                  // bytes per staged key row
+  constexpr int PV = kPfPos * 2 + 8;              // bytes per staged value row of the transpose (one dim)
+  static_assert(LPT * kPfThreads == kPfPos * CPP, "the step's chunks split evenly over the threads");
+  __shared__ __align__(16) unsigned char s_k[kPfPos * PK];
+  __shared__ __align__(16) unsigned char s_vt[D * PV];
+  __shared__ __align__(16) uint8_t s_ok[kPfPos];
+  __shared__ int s_blk[kPfMaxPart + 2];
   __shared__ int s_last;
 
   const int tile = blockIdx.x, kvh = blockIdx.y, part = blockIdx.z;
-  const int lane = threadIdx.x, h = lane >> 5, c32 = lane & 31;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, h = lane >> 5, c32 = lane & 31;
   const int seq = f.tiles[3 * tile];
   const int t0 = f.tiles[3 * tile + 1];
   const int nq = f.tiles[3 * tile + 2];
@@ -570,7 +591,7 @@ __global__ __launch_bounds__(64) void pa_prefill_kernel(PaParams p, PfParams f) 
   // and left alone (nothing is read or written out of bounds)
   if (seq < 0 || seq >= p.num_seqs || nq < 1 || nq > BQ || t0 < p.qsl[seq] || t0 + nq > p.qsl[seq] + p.qlens[seq] ||
       t0 + nq > p.total_q) {
-    if (lane == 0 && part == 0 && p.status) atomicOr(p.status, NS_PA_STATUS_BAD_TILE);
+    if (tid == 0 && part == 0 && p.status) atomicOr(p.status, NS_PA_STATUS_BAD_TILE);
     return;
   }
   const int seq_len = p.seq_lens[seq];
@@ -578,212 +599,210 @@ __global__ __launch_bounds__(64) void pa_prefill_kernel(PaParams p, PfParams f) 
   int lt = kv_pos0 + nq < seq_len ? kv_pos0 + nq : seq_len;          // positions the last token sees
   if (lt < 0) lt = 0;
   const int n_parts = (lt + f.part_tokens - 1) / f.part_tokens;
-  if (part == 0 && n_parts > f.max_parts && lane == 0 && p.status) atomicOr(p.status, NS_PA_STATUS_SEQ_TOO_LONG);
+  if (part == 0 && n_parts > f.max_parts && tid == 0 && p.status) atomicOr(p.status, NS_PA_STATUS_SEQ_TOO_LONG);
 
-  // the lane's two columns: token i, head g, visible positions kvl
-  int tok[2], head[2], kvl[2];
-#pragma unroll
-  for (int cb = 0; cb < 2; ++cb) {
-    const int c = cb * 32 + c32;
-    tok[cb] = c / G;
-    head[cb] = c % G;
-    const bool ok = c < BQ * G && tok[cb] < nq;
-    int kl = kv_pos0 + tok[cb] + 1 < seq_len ? kv_pos0 + tok[cb] + 1 : seq_len;
-    kvl[cb] = ok ? (kl > 0 ? kl : 0) : -1;   // -1: a padding column (never written)
+  // the lane's column: token tok, head hd, visible positions kvl (-1: a padding column, never written)
+  const int c = wave * 32 + c32;
+  const int tok = c / G, hd = c % G;
+  int kvl = -1;
+  if (c < BQ * G && tok < nq) {
+    const int kl = kv_pos0 + tok + 1 < seq_len ? kv_pos0 + tok + 1 : seq_len;
+    kvl = kl > 0 ? kl : 0;
   }
-  auto out_ptr = [&](int cb) -> int64_t {
-    return (int64_t)(t0 + tok[cb]) * p.so_tok + (int64_t)(kvh * G + head[cb]) * p.so_head;
-  };
+  const int64_t obase = (int64_t)(t0 + tok) * p.so_tok + (int64_t)(kvh * G + hd) * p.so_head;
   if (part >= n_parts) {
-    if (part == 0) {   // no visible key for any token of the tile: zeros
-#pragma unroll
-      for (int cb = 0; cb < 2; ++cb)
-        if (kvl[cb] >= 0 && h == 0)
-          for (int d = 0; d < D; ++d) store_one<T>(p.out, out_ptr(cb) + d, 0.f);
-    }
+    if (part == 0 && kvl >= 0 && h == 0)   // no visible key for any token of the tile: zeros
+      for (int d = 0; d < D; ++d) store_one<T>(p.out, obase + d, 0.f);
     return;
   }
   const int j0 = part * f.part_tokens;
   const int j1 = lt < j0 + f.part_tokens ? lt : j0 + f.part_tokens;
+  const int kend = kvl < j1 ? kvl : j1;   // the column's positions below kend are visible here
   const int32_t* bt_row = p.bt + (int64_t)seq * p.sbt;
   // the partition's slice of the block table, validated once, into LDS
   const int bi0 = j0 / p.block_size;
   const int nbi = (j1 - 1) / p.block_size - bi0 + 1;
-  for (int i = lane; i < nbi; i += 64) {
+  int bad = 0;
+  for (int i = tid; i < nbi; i += kPfThreads) {
     const int bi = bi0 + i;
     int blk = bi < p.max_blocks_per_seq ? bt_row[bi] : -1;
     if (blk < 0 || blk >= p.num_blocks) {
       blk = -1;
+      bad = 1;
       if (p.status) atomicOr(p.status, NS_PA_STATUS_BAD_BLOCK);
     }
     s_blk[i] = blk;
   }
 
-  // Q^T operands: column c's 8 dims 16 ks + 8 h .. + 7 (zeros for padding columns)
-  vec qop[2][KS];
-#pragma unroll
-  for (int cb = 0; cb < 2; ++cb) {
-    const int64_t qoff = (int64_t)(t0 + tok[cb]) * p.sq_tok + (int64_t)(kvh * G + head[cb]) * p.sq_head;
+  // Q^T operand: column c, dims 16 ks + 8 h .. + 7 (zeros for a padding column)
+  vec qop[KS];
+  {
+    const int64_t qoff = (int64_t)(t0 + tok) * p.sq_tok + (int64_t)(kvh * G + hd) * p.sq_head;
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) {
       u32x4 w = {0u, 0u, 0u, 0u};
-      if (kvl[cb] >= 0) w = *reinterpret_cast<const u32x4*>(reinterpret_cast<const char*>(p.q) +
-                                                           (qoff + 16 * ks + 8 * h) * 2);
-      qop[cb][ks] = __builtin_bit_cast(vec, w);
+      if (kvl >= 0) w = *reinterpret_cast<const u32x4*>(reinterpret_cast<const char*>(p.q) + (qoff + 16 * ks + 8 * h) * 2);
+      qop[ks] = __builtin_bit_cast(vec, w);
     }
   }
-  __syncthreads();   // the block slice
+  // the slice, and whether any of its blocks is invalid (then every step masks by position)
+  const bool any_bad = __syncthreads_or(bad) != 0;
 
-  // the K / V rows of one step: row jt + c32, dims 16 ks + 8 h .. (zeros past the partition or for
-  // an invalid block); vm: bit r set when row r of the step is a valid position
-  auto load_rows = [&](int jt, u32x4 (&kr)[KS], u32x4 (&vr)[KS], uint32_t& vm) {
-    const int j = jt + c32;
-    int blk = -1, off = 0;
-    if (j < j1) {
-      int bi;
-      if (p.bs_shift >= 0) { bi = j >> p.bs_shift; off = j & (p.block_size - 1); }
-      else { bi = j / p.block_size; off = j - bi * p.block_size; }
-      blk = s_blk[bi - bi0];
-    }
-    vm = (uint32_t)__builtin_amdgcn_ballot_w64(blk >= 0);   // lanes 0..31 (32..63 repeat them)
-    const int64_t kb = (int64_t)blk * p.sk_blk + (int64_t)off * p.sk_tok + (int64_t)kvh * p.sk_head + 8 * h;
-    const int64_t vb = (int64_t)blk * p.sv_blk + (int64_t)off * p.sv_tok + (int64_t)kvh * p.sv_head + 8 * h;
+  // the step's key and value rows: chunk i = tid + kPfThreads r is position i / CPP, dims
+  // 8 (i % CPP) .. + 7; zeros past the partition or for an invalid block
+  // every chunk of the thread has dims 8 dc .. (kPfThreads is a multiple of CPP); the host
+  // keeps token strides times block_size below 2^31, so a slot's offset is a 32-bit product
+  const int dc0 = tid % CPP;
+  const char* kbase = reinterpret_cast<const char*>(p.k) + ((int64_t)kvh * p.sk_head + 8 * dc0) * 2;
+  const char* vbase = reinterpret_cast<const char*>(p.v) + ((int64_t)kvh * p.sv_head + 8 * dc0) * 2;
+  const int sk_tok = (int)p.sk_tok, sv_tok = (int)p.sv_tok;
+  auto load_step = [&](int jt, u32x4 (&kreg)[LPT], u32x4 (&vreg)[LPT], bool (&okr)[LPT]) {
 #pragma unroll
-    for (int ks = 0; ks < KS; ++ks) {
-      kr[ks] = u32x4{0u, 0u, 0u, 0u};
-      vr[ks] = u32x4{0u, 0u, 0u, 0u};
+    for (int r = 0; r < LPT; ++r) {
+      const int j = jt + (tid + kPfThreads * r) / CPP;
+      int blk = -1, off = 0;
+      if (j < j1) {
+        int bi;
+        if (p.bs_shift >= 0) { bi = j >> p.bs_shift; off = j & (p.block_size - 1); }
+        else { bi = j / p.block_size; off = j - bi * p.block_size; }
+        blk = s_blk[bi - bi0];
+      }
+      okr[r] = blk >= 0;
+      kreg[r] = u32x4{0u, 0u, 0u, 0u};
+      vreg[r] = u32x4{0u, 0u, 0u, 0u};
       if (blk >= 0) {
-        kr[ks] = *reinterpret_cast<const u32x4*>(reinterpret_cast<const char*>(p.k) + (kb + 16 * ks) * 2);
-        vr[ks] = *reinterpret_cast<const u32x4*>(reinterpret_cast<const char*>(p.v) + (vb + 16 * ks) * 2);
+        kreg[r] = *reinterpret_cast<const u32x4*>(kbase + ((int64_t)blk * p.sk_blk + off * sk_tok) * 2);
+        vreg[r] = *reinterpret_cast<const u32x4*>(vbase + ((int64_t)blk * p.sv_blk + off * sv_tok) * 2);
       }
     }
   };
+  auto store_step = [&](const u32x4 (&kreg)[LPT], const u32x4 (&vreg)[LPT], const bool (&okr)[LPT]) {
+#pragma unroll
+    for (int r = 0; r < LPT; ++r) {
+      const int i = tid + kPfThreads * r;
+      const int pos = i / CPP, dc = i % CPP;
+      *reinterpret_cast<u32x4*>(s_k + pos * PK + dc * 16) = kreg[r];
+      // the transpose: dim 8 dc + e of this position
+#pragma unroll
+      for (int e = 0; e < 8; ++e)
+        *reinterpret_cast<uint16_t*>(s_vt + (8 * dc + e) * PV + pos * 2) = (uint16_t)(vreg[r][e >> 1] >> (16 * (e & 1)));
+      if (dc == 0) s_ok[pos] = okr[r] ? 1 : 0;
+    }
+  };
 
-  f32x16_t acc[DB][2];
+  f32x16_t acc[DB];
 #pragma unroll
   for (int db = 0; db < DB; ++db)
 #pragma unroll
-    for (int cb = 0; cb < 2; ++cb)
-#pragma unroll
-      for (int e = 0; e < 16; ++e) acc[db][cb][e] = 0.f;
-  float m[2] = {-INFINITY, -INFINITY}, l[2] = {0.f, 0.f};
+    for (int e = 0; e < 16; ++e) acc[db][e] = 0.f;
+  float m = -INFINITY, l = 0.f;
 
-  u32x4 kr[KS], vr[KS];
-  uint32_t vm;
-  load_rows(j0, kr, vr, vm);
-  for (int jt = j0; jt < j1; jt += kPfPos) {
-    // this step's value rows to LDS (the previous step's gathers are done: barrier at its end)
+  // Two register sets of step rows, so each step's loads are issued two steps ahead of the step
+  // that stages them; the loop runs two steps per iteration, one per set.
+  u32x4 ka[LPT], va[LPT], kb[LPT], vb[LPT];
+  bool oka[LPT], okb[LPT];
+  auto step = [&](int jt, u32x4 (&kreg)[LPT], u32x4 (&vreg)[LPT], bool (&okr)[LPT]) {
+    __syncthreads();   // the previous step's reads of the staged rows are done
+    store_step(kreg, vreg, okr);
+    __syncthreads();   // this step's rows staged
+    // the rows of the step after next, in flight across this step's and the next step's work
+    if (jt + 2 * kPfPos < j1) load_step(jt + 2 * kPfPos, kreg, vreg, okr);
+    // the step's two 32-position row blocks in turn: S^T = K Q^T, the online softmax of the lane's
+    // column (element e: position 32 rb + 8 (e / 4) + 4 h + e % 4), P as the hi / lo B operands
+    // of the block's two k-steps, O^T += V^T P^T
 #pragma unroll
-    for (int ks = 0; ks < KS; ++ks)
-      *reinterpret_cast<u32x4*>(s_v + c32 * PITCH + (16 * ks + 8 * h) * 2) = vr[ks];
-    // S^T = K Q^T for both column blocks
-    f32x16_t st[2];
+    for (int rb = 0; rb < 2; ++rb) {
+      f32x16_t st;
 #pragma unroll
-    for (int cb = 0; cb < 2; ++cb)
+      for (int e = 0; e < 16; ++e) st[e] = 0.f;
 #pragma unroll
-      for (int e = 0; e < 16; ++e) st[cb][e] = 0.f;
+      for (int ks = 0; ks < KS; ++ks) {
+        const u32x4 w = *reinterpret_cast<const u32x4*>(s_k + (32 * rb + c32) * PK + (16 * ks + 8 * h) * 2);
+        st = M::mma(__builtin_bit_cast(vec, w), qop[ks], st);
+      }
+      uint32_t okw[4] = {0x01010101u, 0x01010101u, 0x01010101u, 0x01010101u};
+      if (any_bad) {
 #pragma unroll
-    for (int ks = 0; ks < KS; ++ks) {
-      const vec a = __builtin_bit_cast(vec, kr[ks]);
-#pragma unroll
-      for (int cb = 0; cb < 2; ++cb) st[cb] = M::mma(a, qop[cb][ks], st[cb]);
-    }
-    const uint32_t vmask = vm;
-    // the next step's rows, in flight across the softmax and the value products
-    if (jt + kPfPos < j1) load_rows(jt + kPfPos, kr, vr, vm);
-    // online softmax per column; P as the hi / lo B operands
-    vec phi[2][2], plo[2][2];
-#pragma unroll
-    for (int cb = 0; cb < 2; ++cb) {
-      float sv[16];
+        for (int q4 = 0; q4 < 4; ++q4) okw[q4] = *reinterpret_cast<const uint32_t*>(s_ok + 32 * rb + 8 * q4 + 4 * h);
+      }
       float mt = -INFINITY;
 #pragma unroll
       for (int e = 0; e < 16; ++e) {
-        const int r = 8 * (e >> 2) + 4 * h + (e & 3);   // row of the step
-        const bool ok = ((vmask >> r) & 1u) && jt + r < kvl[cb];
-        sv[e] = ok ? st[cb][e] * p.scale_log2 : -INFINITY;
-        mt = fmaxf(mt, sv[e]);
+        const int r = 32 * rb + 8 * (e >> 2) + 4 * h + (e & 3);
+        const bool ok = jt + r < kend && ((okw[e >> 2] >> (8 * (e & 3))) & 0xffu) != 0u;
+        st[e] = ok ? st[e] * p.scale_log2 : -INFINITY;
+        mt = fmaxf(mt, st[e]);
       }
       mt = fmaxf(mt, __shfl_xor(mt, 32));
-      const float mn = fmaxf(m[cb], mt);
-      const float alpha = mn == -INFINITY ? 1.f : exp2f(m[cb] - mn);
+      const float mn = fmaxf(m, mt);
+      // exp2 by v_exp_f32 (a result below 2^-126 of the column's max weight flushes to zero);
+      // -inf scores give 0, and a column with no score yet subtracts 0
+      const float msub = mn == -INFINITY ? 0.f : mn;
+      const float alpha = __builtin_amdgcn_exp2f(m - msub);
       float ls = 0.f;
-      uint32_t hb[16], lb[16];
-#pragma unroll
-      for (int e = 0; e < 16; ++e) {
-        const float pe = sv[e] == -INFINITY ? 0.f : exp2f(sv[e] - mn);
-        ls += pe;
-        hb[e] = M::bits(pe);
-        lb[e] = M::bits(pe - M::widen(hb[e]));
-      }
-      ls += __shfl_xor(ls, 32);
-      l[cb] = l[cb] * alpha + ls;
-      m[cb] = mn;
-#pragma unroll
-      for (int db = 0; db < DB; ++db)
-#pragma unroll
-        for (int e = 0; e < 16; ++e) acc[db][cb][e] *= alpha;
+      vec phi[2], plo[2];
 #pragma unroll
       for (int s2 = 0; s2 < 2; ++s2) {
         u32x4 wh, wl;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          wh[i] = hb[8 * s2 + 2 * i] | (hb[8 * s2 + 2 * i + 1] << 16);
-          wl[i] = lb[8 * s2 + 2 * i] | (lb[8 * s2 + 2 * i + 1] << 16);
+        for (int i2 = 0; i2 < 4; ++i2) {
+          const float p0 = __builtin_amdgcn_exp2f(st[8 * s2 + 2 * i2] - msub);
+          const float p1 = __builtin_amdgcn_exp2f(st[8 * s2 + 2 * i2 + 1] - msub);
+          ls += p0 + p1;
+          wh[i2] = M::pack2(p0, p1);
+          wl[i2] = M::pack2(p0 - M::lo(wh[i2]), p1 - M::hi(wh[i2]));
         }
-        phi[cb][s2] = __builtin_bit_cast(vec, wh);
-        plo[cb][s2] = __builtin_bit_cast(vec, wl);
+        phi[s2] = __builtin_bit_cast(vec, wh);
+        plo[s2] = __builtin_bit_cast(vec, wl);
+      }
+      ls += __shfl_xor(ls, 32);
+      l = l * alpha + ls;
+      m = mn;
+      if (__ballot(alpha != 1.f) != 0ull) {   // a column's maximum moved: rescale (rare after the first steps)
+#pragma unroll
+        for (int db = 0; db < DB; ++db)
+#pragma unroll
+          for (int e = 0; e < 16; ++e) acc[db][e] *= alpha;
+      }
+      // the V^T operand of dim 32 db + c32: k-slot i of half h at position 16 s + 8 (i / 4) + 4 h + i % 4
+#pragma unroll
+      for (int db = 0; db < DB; ++db) {
+        const unsigned char* vrow = s_vt + (32 * db + c32) * PV;
+#pragma unroll
+        for (int s2 = 0; s2 < 2; ++s2) {
+          const int s = 2 * rb + s2;
+          const u32x2 lo4 = *reinterpret_cast<const u32x2*>(vrow + (16 * s + 4 * h) * 2);
+          const u32x2 hi4 = *reinterpret_cast<const u32x2*>(vrow + (16 * s + 8 + 4 * h) * 2);
+          const u32x4 w = {lo4[0], lo4[1], hi4[0], hi4[1]};
+          const vec a = __builtin_bit_cast(vec, w);
+          acc[db] = M::mma(a, phi[s2], acc[db]);
+          acc[db] = M::mma(a, plo[s2], acc[db]);
+        }
       }
     }
-    __syncthreads();   // the value rows in LDS
-    // O^T += V^T P^T: the V^T operand of dims 32 db + c32, positions in the S^T row order
-#pragma unroll
-    for (int db = 0; db < DB; ++db) {
-#pragma unroll
-      for (int s2 = 0; s2 < 2; ++s2) {
-        const unsigned char* col = s_v + (32 * db + c32) * 2;
-        u32x4 w;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int r0 = 16 * s2 + 8 * ((2 * i) >> 2) + 4 * h + ((2 * i) & 3);
-          const uint32_t lo16 = *reinterpret_cast<const uint16_t*>(col + r0 * PITCH);
-          const uint32_t hi16 = *reinterpret_cast<const uint16_t*>(col + (r0 + 1) * PITCH);
-          w[i] = lo16 | (hi16 << 16);
-        }
-        const vec a = __builtin_bit_cast(vec, w);
-#pragma unroll
-        for (int cb = 0; cb < 2; ++cb) {
-          acc[db][cb] = M::mma(a, phi[cb][s2], acc[db][cb]);
-          acc[db][cb] = M::mma(a, plo[cb][s2], acc[db][cb]);
-        }
-      }
-    }
-    __syncthreads();   // the gathers are done before the next step's rows overwrite LDS
+  };
+  load_step(j0, ka, va, oka);
+  if (j0 + kPfPos < j1) load_step(j0 + kPfPos, kb, vb, okb);
+  for (int jt = j0; jt < j1; jt += 2 * kPfPos) {
+    step(jt, ka, va, oka);
+    if (jt + kPfPos < j1) step(jt + kPfPos, kb, vb, okb);
   }
 
-  // O^T layout: lane l, element e -> column l % 32, dim 32 db + 8 (e / 4) + 4 h + e % 4
+  // O^T layout: lane l, element e -> column c, dim 32 db + 8 (e / 4) + 4 h + e % 4
   const bool direct = n_parts == 1;
   const int64_t wbase = ((int64_t)tile * p.hkv + kvh) * f.max_parts;
-  if (direct || part < f.max_parts) {
+  if ((direct || part < f.max_parts) && kvl >= 0) {
 #pragma unroll
-    for (int cb = 0; cb < 2; ++cb) {
-      if (kvl[cb] < 0) continue;
-      const int c = cb * 32 + c32;
+    for (int db = 0; db < DB; ++db)
 #pragma unroll
-      for (int db = 0; db < DB; ++db)
-#pragma unroll
-        for (int e = 0; e < 16; ++e) {
-          const int d = 32 * db + 8 * (e >> 2) + 4 * h + (e & 3);
-          if (direct) {
-            store_one<T>(p.out, out_ptr(cb) + d, l[cb] > 0.f ? acc[db][cb][e] / l[cb] : 0.f);
-          } else {
-            st_dev(&f.ws_acc[((wbase + part) * kPfCols + c) * D + d], acc[db][cb][e]);
-          }
-        }
-      if (!direct && h == 0) {
-        st_dev(&f.ws_ml[((wbase + part) * kPfCols + c) * 2], m[cb]);
-        st_dev(&f.ws_ml[((wbase + part) * kPfCols + c) * 2 + 1], l[cb]);
+      for (int e = 0; e < 16; ++e) {
+        const int d = 32 * db + 8 * (e >> 2) + 4 * h + (e & 3);
+        if (direct) store_one<T>(p.out, obase + d, l > 0.f ? acc[db][e] / l : 0.f);
+        else st_dev(&f.ws_acc[((wbase + part) * kPfCols + c) * D + d], acc[db][e]);
       }
+    if (!direct && h == 0) {
+      st_dev(&f.ws_ml[((wbase + part) * kPfCols + c) * 2], m);
+      st_dev(&f.ws_ml[((wbase + part) * kPfCols + c) * 2 + 1], l);
     }
   }
   if (direct || part >= f.max_parts) return;
@@ -794,32 +813,97 @@ __global__ __launch_bounds__(64) void pa_prefill_kernel(PaParams p, PfParams f) 
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
   int32_t* counter = f.counters + (int64_t)tile * p.hkv + kvh;
-  if (lane == 0) s_last = atomicAdd(counter, 1) == arrivals - 1;
+  if (tid == 0) s_last = atomicAdd(counter, 1) == arrivals - 1;
   __syncthreads();
   if (!s_last) return;
-  if (lane == 0) __hip_atomic_store(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  // lane c merges column c: the partitions' weights, then every dim
-  const int c = lane;
-  const int ti = c / G, hg = c % G;
-  if (c >= BQ * G || ti >= nq) return;
-  float mx = -INFINITY;
-  for (int i = 0; i < arrivals; ++i) mx = fmaxf(mx, ld_dev(&f.ws_ml[((wbase + i) * kPfCols + c) * 2]));
-  float L = 0.f;
-  for (int i = 0; i < arrivals; ++i) {
-    const float mi = ld_dev(&f.ws_ml[((wbase + i) * kPfCols + c) * 2]);
-    if (mi == -INFINITY) continue;
-    L = fmaf(exp2f(mi - mx), ld_dev(&f.ws_ml[((wbase + i) * kPfCols + c) * 2 + 1]), L);
-  }
-  const int64_t ob = (int64_t)(t0 + ti) * p.so_tok + (int64_t)(kvh * G + hg) * p.so_head;
-  for (int d = 0; d < D; ++d) {
-    float o = 0.f;
-    for (int i = 0; i < arrivals; ++i) {
-      const float mi = ld_dev(&f.ws_ml[((wbase + i) * kPfCols + c) * 2]);
-      if (mi == -INFINITY) continue;
-      o = fmaf(exp2f(mi - mx), ld_dev(&f.ws_acc[((wbase + i) * kPfCols + c) * D + d]), o);
+  if (tid == 0) __hip_atomic_store(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  // The weights w_i = exp2(m_i - max) of every column's partitions and their sum L: up to
+  // kPfMergeLds partitions in LDS (the staged key rows are free now), computed once, with all
+  // the (m, l) loads of a thread in flight together; then two threads per column, half the dims
+  // each, accumulate the partials partition by partition, all of a partition's loads issued
+  // before the first is used.
+  constexpr int HD = D / 2;
+  constexpr int kPfMergeLds = (kPfPos * PK) / (kPfCols * 4) >= 32 ? 32 : 16;   // partitions in the table
+  float* s_w = reinterpret_cast<float*>(s_k);        // [i][column] weights
+  float* s_L = reinterpret_cast<float*>(s_vt);       // [column] the weights' sum of l
+  static_assert(kPfMergeLds * kPfCols * 4 <= kPfPos * PK && kPfCols * 4 <= D * PV, "merge tables fit");
+  const int mc = tid >> 1, d0 = (tid & 1) * HD;
+  const int ti = mc / G, hg = mc % G;
+  const bool live = mc < BQ * G && ti < nq;
+  if (arrivals <= kPfMergeLds) {
+    if (tid < kPfCols) {
+      float mi[kPfMergeLds], li[kPfMergeLds];
+#pragma unroll
+      for (int i = 0; i < kPfMergeLds; ++i) {
+        mi[i] = -INFINITY;
+        li[i] = 0.f;
+        if (i < arrivals) {
+          mi[i] = ld_dev(&f.ws_ml[((wbase + i) * kPfCols + tid) * 2]);
+          li[i] = ld_dev(&f.ws_ml[((wbase + i) * kPfCols + tid) * 2 + 1]);
+        }
+      }
+      float mx = -INFINITY;
+#pragma unroll
+      for (int i = 0; i < kPfMergeLds; ++i) mx = fmaxf(mx, mi[i]);
+      float L = 0.f;
+#pragma unroll
+      for (int i = 0; i < kPfMergeLds; ++i) {
+        // a partition whose keys were all skipped (m = -inf) weighs 0
+        const float w = mi[i] == -INFINITY ? 0.f : exp2f(mi[i] - mx);
+        L = fmaf(w, li[i], L);
+        if (i < arrivals) s_w[i * kPfCols + tid] = w;
+      }
+      s_L[tid] = L;
     }
-    store_one<T>(p.out, ob + d, L > 0.f ? o / L : 0.f);
+    __syncthreads();
+    if (!live) return;
+    float o[HD];
+#pragma unroll
+    for (int d = 0; d < HD; ++d) o[d] = 0.f;
+    for (int i = 0; i < arrivals; ++i) {
+      const float w = s_w[i * kPfCols + mc];
+      const float* src = &f.ws_acc[((wbase + i) * kPfCols + mc) * D + d0];
+      float a[HD];
+#pragma unroll
+      for (int d = 0; d < HD; ++d) a[d] = ld_dev(src + d);
+#pragma unroll
+      for (int d = 0; d < HD; ++d) o[d] = fmaf(w, a[d], o[d]);
+    }
+    const float L = s_L[mc];
+    const int64_t ob = (int64_t)(t0 + ti) * p.so_tok + (int64_t)(kvh * G + hg) * p.so_head + d0;
+#pragma unroll
+    for (int d = 0; d < HD; ++d) store_one<T>(p.out, ob + d, L > 0.f ? o[d] / L : 0.f);
+    return;
   }
+  // more partitions than the LDS table holds: one pass of max-rescaled sums per thread
+  if (!live) return;
+  float mm = -INFINITY, L = 0.f;
+  float o[HD];
+#pragma unroll
+  for (int d = 0; d < HD; ++d) o[d] = 0.f;
+  for (int i = 0; i < arrivals; ++i) {
+    const float mi = ld_dev(&f.ws_ml[((wbase + i) * kPfCols + mc) * 2]);
+    const float li = ld_dev(&f.ws_ml[((wbase + i) * kPfCols + mc) * 2 + 1]);
+    if (mi == -INFINITY) continue;
+    const float* src = &f.ws_acc[((wbase + i) * kPfCols + mc) * D + d0];
+    float a[HD];
+#pragma unroll
+    for (int d = 0; d < HD; ++d) a[d] = ld_dev(src + d);
+    if (mi > mm) {
+      const float r = mm == -INFINITY ? 0.f : exp2f(mm - mi);
+      L *= r;
+#pragma unroll
+      for (int d = 0; d < HD; ++d) o[d] *= r;
+      mm = mi;
+    }
+    const float w = exp2f(mi - mm);
+    L = fmaf(w, li, L);
+#pragma unroll
+    for (int d = 0; d < HD; ++d) o[d] = fmaf(w, a[d], o[d]);
+  }
+  const int64_t ob = (int64_t)(t0 + ti) * p.so_tok + (int64_t)(kvh * G + hg) * p.so_head + d0;
+#pragma unroll
+  for (int d = 0; d < HD; ++d) store_one<T>(p.out, ob + d, L > 0.f ? o[d] / L : 0.f);
 }
 
 // ---- host side ---------------------------------------------------------------------------------
@@ -828,7 +912,7 @@ int pf_part_tokens_for(int32_t n_tiles, int32_t hkv, int32_t max_seq_len) {
   int part = kPfMaxPart;
   while (part > kPfMinPart) {
     const int64_t parts = ((int64_t)max_seq_len + part - 1) / part;
-    if ((int64_t)n_tiles * hkv * parts >= kTargetGroups) break;
+    if ((int64_t)n_tiles * hkv * parts >= kPfTargetGroups) break;
     part >>= 1;
   }
   return part;
@@ -890,7 +974,7 @@ void launch(const PaParams& p, const PfParams& f, int n_tokens, int n_tiles, hip
   if constexpr (Elem<T>::bytes == 2) {
     if (n_tiles > 0) {
       dim3 grid(n_tiles, p.hkv, f.max_parts > 0 ? f.max_parts : 1);
-      hipLaunchKernelGGL((pa_prefill_kernel<T, D, G>), grid, dim3(64), 0, stream, p, f);
+      hipLaunchKernelGGL((pa_prefill_kernel<T, D, G>), grid, dim3(kPfThreads), 0, stream, p, f);
     }
   }
 }
@@ -962,6 +1046,10 @@ int ns_paged_attention(const ns_paged_attn_args* a, hipStream_t stream) {
   if (((uintptr_t)a->query | (uintptr_t)a->k_cache | (uintptr_t)a->v_cache) % 16 != 0)
     return fail("query and cache pointers must be 16-byte aligned");
   if (a->stride_bt_seq < 0) return fail("stride_bt_seq must be >= 0");
+  if (a->stride_k_token < 0 || a->stride_v_token < 0 ||
+      (int64_t)a->block_size * (a->stride_k_token > a->stride_v_token ? a->stride_k_token : a->stride_v_token) >=
+          ((int64_t)1 << 31))
+    return fail("token strides times block_size must lie in [0, 2^31)");
   if (a->max_blocks_per_seq < 0) return fail("max_blocks_per_seq must be >= 0");
   // the prefill tiles (16-bit types) and the token list of the per-token kernel
   if (a->n_decode_tokens < 0 || a->n_prefill_tiles < 0) return fail("token and tile counts must be >= 0");

@@ -37,7 +37,7 @@ NS_PA_DTYPE_F16 = 2
 STATUS_BAD_BLOCK = 1
 STATUS_SEQ_TOO_LONG = 2
 STATUS_BAD_TILE = 4
-TILE_COLUMNS = 64          # query columns of a prefill tile: 64 // G tokens of G heads
+TILE_COLUMNS = 128         # query columns of a prefill tile (NS_PA_TILE_COLUMNS): 128 // G tokens of G heads
 PREFILL_MIN_QUERY = 2      # sequences with at least this many query tokens go by tile
 
 EXPORTS = ("ns_pa_abi_version", "ns_pa_last_error", "ns_paged_attention_workspace_bytes",

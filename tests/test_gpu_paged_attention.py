@@ -173,7 +173,7 @@ def test_side_stream_and_output_stride(device):
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("hq,hkv,d", [(24, 8, 128), (32, 8, 128), (8, 8, 64), (16, 8, 64), (64, 8, 128)])
 def test_prefill_tiles_head_layouts(device, dtype, hq, hkv, d):
-    # sequences of several query tokens go by MFMA query tile (64 // G tokens each): a chunk in the
+    # sequences of several query tokens go by MFMA query tile (128 // G tokens each): a chunk in the
     # middle of a long sequence, a full prefill, chunks shorter than a tile, and decode rows beside them
     case = make_case(50 + hq + d, [700, 300, 190, 1, 90, 45], [200, 300, 3, 1, 17, 1], hq=hq, hkv=hkv, d=d,
                      dtype=dtype)
@@ -259,3 +259,11 @@ def test_plan_reused_across_layers_and_refused_for_another_layout(device):
     with pytest.raises(A.PagedAttentionError, match="another batch layout"):
         A.paged_attention_hip(c["query"], c["k_cache"], c["v_cache"], c["block_tables"], c["seq_lens"],
                               c["query_start_loc"], c["query_lens"], c["scale"], c["block_size"], plan=bad)
+
+
+@pytest.mark.parametrize("d", [128, 64])
+def test_prefill_tile_merged_from_many_partitions(device, d):
+    # one tile over 9000 positions splits into more partitions than the merge's LDS weight table
+    # holds (the one-pass rescaled merge) and a 4000-position tile into fewer (the table)
+    case = make_case(97 + d, [9000, 4000], [20, 30], d=d)
+    check(case, device)

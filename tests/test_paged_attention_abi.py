@@ -65,8 +65,12 @@ def test_struct_layout_matches_header():
 
 def test_plan_tiles_covers_every_token_once():
     """The host plan of a chunked-prefill batch: sequences with several query tokens cut into tiles
-    of 64 // G consecutive tokens of one sequence, every other token listed once, for any G."""
+    of TILE_COLUMNS // G consecutive tokens of one sequence, every other token listed once, for any G;
+    TILE_COLUMNS is the header's NS_PA_TILE_COLUMNS."""
     import numpy as np
+
+    with open(os.path.join(ROOT, "include", "ns_paged_attention.h")) as fh:
+        assert int(re.search(r"#define NS_PA_TILE_COLUMNS (\d+)", fh.read()).group(1)) == PA.TILE_COLUMNS
 
     rng = np.random.default_rng(3)
     for hq, hkv in ((24, 8), (32, 8), (8, 8), (16, 8), (64, 8)):
@@ -76,7 +80,7 @@ def test_plan_tiles_covers_every_token_once():
         qsl[1:] = np.cumsum(qlens)
         seq_lens = qlens + rng.integers(0, 3000, qlens.size)
         tiles, tokens = PA.plan_tiles(seq_lens, qsl, qlens, hq, hkv)
-        bq = 64 // (hq // hkv)
+        bq = PA.TILE_COLUMNS // (hq // hkv)
         owner = np.full(int(qsl[-1]), -1)
         for s, t0, n in tiles.tolist():
             assert 1 <= n <= bq and qlens[s] >= PA.PREFILL_MIN_QUERY
