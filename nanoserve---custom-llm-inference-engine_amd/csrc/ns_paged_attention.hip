@@ -522,6 +522,7 @@ typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef short i16x4 __attribute__((ext_vector_type(4)));
 typedef float f32x2 __attribute__((ext_vector_type(2)));
 typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
@@ -573,11 +574,10 @@ __global__ __launch_bounds__(kPfThreads) __attribute__((amdgpu_waves_per_eu(2, 2
   constexpr int DB = D / 32;                      // 32-dim blocks of O^T
   constexpr int CPP = D / 8;                      // 16-byte chunks of a key or value row
   constexpr int LPT = kPfPos * CPP / kPfThreads;  // chunks of each kind a thread loads per step
-  constexpr int PK = D * 2 + 16;                  // bytes per staged key row
-  constexpr int PV = kPfPos * 2 + 8;              // bytes per staged value row of the transpose (one dim)
+  constexpr int PK = D * 2 + 16;                  // bytes per staged key or value row
   static_assert(LPT * kPfThreads == kPfPos * CPP, "the step's chunks split evenly over the threads");
   __shared__ __align__(16) unsigned char s_k[kPfPos * PK];
-  __shared__ __align__(16) unsigned char s_vt[D * PV];
+  __shared__ __align__(16) unsigned char s_v[kPfPos * PK];
   __shared__ __align__(16) uint8_t s_ok[kPfPos];
   __shared__ int s_blk[kPfMaxPart + 2];
   __shared__ int s_last;
@@ -618,6 +618,11 @@ __global__ __launch_bounds__(kPfThreads) __attribute__((amdgpu_waves_per_eu(2, 2
   const int j0 = part * f.part_tokens;
   const int j1 = lt < j0 + f.part_tokens ? lt : j0 + f.part_tokens;
   const int kend = kvl < j1 ? kvl : j1;   // the column's positions below kend are visible here
+  // the smallest kend of the wave's columns (padding columns aside): positions below it are
+  // visible to every column of the wave
+  int kend_w = kvl >= 0 ? kend : INT32_MAX;
+#pragma unroll
+  for (int sh = 1; sh < 64; sh <<= 1) kend_w = min(kend_w, __shfl_xor(kend_w, sh));
   const int32_t* bt_row = p.bt + (int64_t)seq * p.sbt;
   // the partition's slice of the block table, validated once, into LDS
   const int bi0 = j0 / p.block_size;
@@ -682,10 +687,7 @@ __global__ __launch_bounds__(kPfThreads) __attribute__((amdgpu_waves_per_eu(2, 2
       const int i = tid + kPfThreads * r;
       const int pos = i / CPP, dc = i % CPP;
       *reinterpret_cast<u32x4*>(s_k + pos * PK + dc * 16) = kreg[r];
-      // the transpose: dim 8 dc + e of this position
-#pragma unroll
-      for (int e = 0; e < 8; ++e)
-        *reinterpret_cast<uint16_t*>(s_vt + (8 * dc + e) * PV + pos * 2) = (uint16_t)(vreg[r][e >> 1] >> (16 * (e & 1)));
+      *reinterpret_cast<u32x4*>(s_v + pos * PK + dc * 16) = vreg[r];
       if (dc == 0) s_ok[pos] = okr[r] ? 1 : 0;
     }
   };
@@ -697,6 +699,12 @@ __global__ __launch_bounds__(kPfThreads) __attribute__((amdgpu_waves_per_eu(2, 2
     for (int e = 0; e < 16; ++e) acc[db][e] = 0.f;
   float m = -INFINITY, l = 0.f;
 
+  // The transposing read (ds_read_b64_tr_b16): in each 16-lane group, lane j's four results are
+  // element j % 4 of the 4-element rows that lanes 4 m + j / 4 address, m = 0..3.  So that lane L
+  // receives positions 16 s + 4 h + m of dim 32 db + L % 32, lane L addresses position
+  // 16 s + 4 (L / 32) + (L % 16) / 4, dims 32 db + 16 ((L / 16) % 2) + 4 (L % 4) .. + 3.
+  const int tr_pos = 4 * (lane >> 5) + ((lane & 15) >> 2);
+  const int tr_dim = 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
   // Two register sets of step rows, so each step's loads are issued two steps ahead of the step
   // that stages them; the loop runs two steps per iteration, one per set.
   u32x4 ka[LPT], va[LPT], kb[LPT], vb[LPT];
@@ -720,25 +728,36 @@ __global__ __launch_bounds__(kPfThreads) __attribute__((amdgpu_waves_per_eu(2, 2
         const u32x4 w = *reinterpret_cast<const u32x4*>(s_k + (32 * rb + c32) * PK + (16 * ks + 8 * h) * 2);
         st = M::mma(__builtin_bit_cast(vec, w), qop[ks], st);
       }
-      uint32_t okw[4] = {0x01010101u, 0x01010101u, 0x01010101u, 0x01010101u};
-      if (any_bad) {
-#pragma unroll
-        for (int q4 = 0; q4 < 4; ++q4) okw[q4] = *reinterpret_cast<const uint32_t*>(s_ok + 32 * rb + 8 * q4 + 4 * h);
-      }
       float mt = -INFINITY;
+      if (jt + 32 * rb + 32 <= kend_w && !any_bad) {   // every position of the block visible to every column
 #pragma unroll
-      for (int e = 0; e < 16; ++e) {
-        const int r = 32 * rb + 8 * (e >> 2) + 4 * h + (e & 3);
-        const bool ok = jt + r < kend && ((okw[e >> 2] >> (8 * (e & 3))) & 0xffu) != 0u;
-        st[e] = ok ? st[e] * p.scale_log2 : -INFINITY;
-        mt = fmaxf(mt, st[e]);
+        for (int e = 0; e < 16; ++e) {
+          st[e] *= p.scale_log2;
+          mt = fmaxf(mt, st[e]);
+        }
+      } else {
+        uint32_t okw[4] = {0x01010101u, 0x01010101u, 0x01010101u, 0x01010101u};
+        if (any_bad) {
+#pragma unroll
+          for (int q4 = 0; q4 < 4; ++q4) okw[q4] = *reinterpret_cast<const uint32_t*>(s_ok + 32 * rb + 8 * q4 + 4 * h);
+        }
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+          const int r = 32 * rb + 8 * (e >> 2) + 4 * h + (e & 3);
+          const bool ok = jt + r < kend && ((okw[e >> 2] >> (8 * (e & 3))) & 0xffu) != 0u;
+          st[e] = ok ? st[e] * p.scale_log2 : -INFINITY;
+          mt = fmaxf(mt, st[e]);
+        }
       }
       mt = fmaxf(mt, __shfl_xor(mt, 32));
-      const float mn = fmaxf(m, mt);
-      // exp2 by v_exp_f32 (a result below 2^-126 of the column's max weight flushes to zero);
-      // -inf scores give 0, and a column with no score yet subtracts 0
+      // The column's reference m moves only when a score exceeds it by more than 8 (log2
+      // units), to the new maximum: weights stay at most 2^8 and the accumulators are rescaled
+      // rarely.  exp2 by v_exp_f32 (a weight below 2^-126 flushes to zero); -inf scores weigh
+      // 0, and a column with no score yet subtracts 0.
+      const bool move = mt > m + 8.f;
+      const float mn = move ? mt : m;
       const float msub = mn == -INFINITY ? 0.f : mn;
-      const float alpha = __builtin_amdgcn_exp2f(m - msub);
+      const float alpha = move ? __builtin_amdgcn_exp2f(m - msub) : 1.f;
       float ls = 0.f;
       vec phi[2], plo[2];
 #pragma unroll
@@ -758,21 +777,24 @@ __global__ __launch_bounds__(kPfThreads) __attribute__((amdgpu_waves_per_eu(2, 2
       ls += __shfl_xor(ls, 32);
       l = l * alpha + ls;
       m = mn;
-      if (__ballot(alpha != 1.f) != 0ull) {   // a column's maximum moved: rescale (rare after the first steps)
+      if (__ballot(move) != 0ull) {   // a column's reference moved: rescale
 #pragma unroll
         for (int db = 0; db < DB; ++db)
 #pragma unroll
           for (int e = 0; e < 16; ++e) acc[db][e] *= alpha;
       }
-      // the V^T operand of dim 32 db + c32: k-slot i of half h at position 16 s + 8 (i / 4) + 4 h + i % 4
+      // the V^T operand of dim 32 db + c32: k-slot i of half h at position 16 s + 8 (i / 4) + 4 h + i % 4,
+      // read from the value rows by two transposing reads (k-slots 0-3, then 4-7)
 #pragma unroll
       for (int db = 0; db < DB; ++db) {
-        const unsigned char* vrow = s_vt + (32 * db + c32) * PV;
 #pragma unroll
         for (int s2 = 0; s2 < 2; ++s2) {
           const int s = 2 * rb + s2;
-          const u32x2 lo4 = *reinterpret_cast<const u32x2*>(vrow + (16 * s + 4 * h) * 2);
-          const u32x2 hi4 = *reinterpret_cast<const u32x2*>(vrow + (16 * s + 8 + 4 * h) * 2);
+          const unsigned char* src = s_v + (16 * s + tr_pos) * PK + (32 * db + tr_dim) * 2;
+          const u32x2 lo4 = __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                                                          (__attribute__((address_space(3))) i16x4*)(src)));
+          const u32x2 hi4 = __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                                                          (__attribute__((address_space(3))) i16x4*)(src + 8 * PK)));
           const u32x4 w = {lo4[0], lo4[1], hi4[0], hi4[1]};
           const vec a = __builtin_bit_cast(vec, w);
           acc[db] = M::mma(a, phi[s2], acc[db]);
@@ -825,8 +847,8 @@ __global__ __launch_bounds__(kPfThreads) __attribute__((amdgpu_waves_per_eu(2, 2
   constexpr int HD = D / 2;
   constexpr int kPfMergeLds = (kPfPos * PK) / (kPfCols * 4) >= 32 ? 32 : 16;   // partitions in the table
   float* s_w = reinterpret_cast<float*>(s_k);        // [i][column] weights
-  float* s_L = reinterpret_cast<float*>(s_vt);       // [column] the weights' sum of l
-  static_assert(kPfMergeLds * kPfCols * 4 <= kPfPos * PK && kPfCols * 4 <= D * PV, "merge tables fit");
+  float* s_L = reinterpret_cast<float*>(s_v);        // [column] the weights' sum of l
+  static_assert(kPfMergeLds * kPfCols * 4 <= kPfPos * PK && kPfCols * 4 <= kPfPos * PK, "merge tables fit");
   const int mc = tid >> 1, d0 = (tid & 1) * HD;
   const int ti = mc / G, hg = mc % G;
   const bool live = mc < BQ * G && ti < nq;
