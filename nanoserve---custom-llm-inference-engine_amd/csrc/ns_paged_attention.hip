@@ -561,7 +561,7 @@ struct PfParams {
   float* ws_ml;           // (n_tiles, hkv, max_parts, kPfCols, 2) partition max (log2 units), sum
   int32_t* counters;      // (n_tiles, hkv) arrivals of split tiles; zero between calls
   int32_t part_tokens;    // positions per partition (a multiple of kPfPos)
-  int32_t max_parts;
+  int32_t max_parts;      // at least 1
 };
 
 template <typename T, int D, int G>
@@ -705,37 +705,43 @@ __global__ __launch_bounds__(kPfThreads) __attribute__((amdgpu_waves_per_eu(2, 2
   // 16 s + 4 (L / 32) + (L % 16) / 4, dims 32 db + 16 ((L / 16) % 2) + 4 (L % 4) .. + 3.
   const int tr_pos = 4 * (lane >> 5) + ((lane & 15) >> 2);
   const int tr_dim = 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
-  // Two register sets of step rows, so each step's loads are issued two steps ahead of the step
-  // that stages them; the loop runs two steps per iteration, one per set.
-  u32x4 ka[LPT], va[LPT], kb[LPT], vb[LPT];
-  bool oka[LPT], okb[LPT];
-  auto step = [&](int jt, u32x4 (&kreg)[LPT], u32x4 (&vreg)[LPT], bool (&okr)[LPT]) {
+  u32x4 kreg[LPT], vreg[LPT];
+  bool okr[LPT];
+  load_step(j0, kreg, vreg, okr);
+  for (int jt = j0; jt < j1; jt += kPfPos) {
     __syncthreads();   // the previous step's reads of the staged rows are done
     store_step(kreg, vreg, okr);
     __syncthreads();   // this step's rows staged
-    // the rows of the step after next, in flight across this step's and the next step's work
-    if (jt + 2 * kPfPos < j1) load_step(jt + 2 * kPfPos, kreg, vreg, okr);
-    // the step's two 32-position row blocks in turn: S^T = K Q^T, the online softmax of the lane's
-    // column (element e: position 32 rb + 8 (e / 4) + 4 h + e % 4), P as the hi / lo B operands
-    // of the block's two k-steps, O^T += V^T P^T
+    // the next step's rows, in flight across this step's products and softmax
+    if (jt + kPfPos < j1) load_step(jt + kPfPos, kreg, vreg, okr);
+    // S^T = K Q^T for the step's two 32-position row blocks (two independent MFMA chains)
+    f32x16_t st[2];
 #pragma unroll
-    for (int rb = 0; rb < 2; ++rb) {
-      f32x16_t st;
+    for (int rb = 0; rb < 2; ++rb)
 #pragma unroll
-      for (int e = 0; e < 16; ++e) st[e] = 0.f;
+      for (int e = 0; e < 16; ++e) st[rb][e] = 0.f;
 #pragma unroll
-      for (int ks = 0; ks < KS; ++ks) {
+    for (int ks = 0; ks < KS; ++ks) {
+#pragma unroll
+      for (int rb = 0; rb < 2; ++rb) {
         const u32x4 w = *reinterpret_cast<const u32x4*>(s_k + (32 * rb + c32) * PK + (16 * ks + 8 * h) * 2);
-        st = M::mma(__builtin_bit_cast(vec, w), qop[ks], st);
+        st[rb] = M::mma(__builtin_bit_cast(vec, w), qop[ks], st[rb]);
       }
-      float mt = -INFINITY;
-      if (jt + 32 * rb + 32 <= kend_w && !any_bad) {   // every position of the block visible to every column
+    }
+    // the online softmax of the lane's column over the step's 64 positions (element e of block
+    // rb: position 32 rb + 8 (e / 4) + 4 h + e % 4; the other half in lane ^ 32)
+    float mt = -INFINITY;
+    if (jt + kPfPos <= kend_w && !any_bad) {   // every position of the step visible to every column
+#pragma unroll
+      for (int rb = 0; rb < 2; ++rb)
 #pragma unroll
         for (int e = 0; e < 16; ++e) {
-          st[e] *= p.scale_log2;
-          mt = fmaxf(mt, st[e]);
+          st[rb][e] *= p.scale_log2;
+          mt = fmaxf(mt, st[rb][e]);
         }
-      } else {
+    } else {
+#pragma unroll
+      for (int rb = 0; rb < 2; ++rb) {
         uint32_t okw[4] = {0x01010101u, 0x01010101u, 0x01010101u, 0x01010101u};
         if (any_bad) {
 #pragma unroll
@@ -745,69 +751,59 @@ __global__ __launch_bounds__(kPfThreads) __attribute__((amdgpu_waves_per_eu(2, 2
         for (int e = 0; e < 16; ++e) {
           const int r = 32 * rb + 8 * (e >> 2) + 4 * h + (e & 3);
           const bool ok = jt + r < kend && ((okw[e >> 2] >> (8 * (e & 3))) & 0xffu) != 0u;
-          st[e] = ok ? st[e] * p.scale_log2 : -INFINITY;
-          mt = fmaxf(mt, st[e]);
-        }
-      }
-      mt = fmaxf(mt, __shfl_xor(mt, 32));
-      // The column's reference m moves only when a score exceeds it by more than 8 (log2
-      // units), to the new maximum: weights stay at most 2^8 and the accumulators are rescaled
-      // rarely.  exp2 by v_exp_f32 (a weight below 2^-126 flushes to zero); -inf scores weigh
-      // 0, and a column with no score yet subtracts 0.
-      const bool move = mt > m + 8.f;
-      const float mn = move ? mt : m;
-      const float msub = mn == -INFINITY ? 0.f : mn;
-      const float alpha = move ? __builtin_amdgcn_exp2f(m - msub) : 1.f;
-      float ls = 0.f;
-      vec phi[2], plo[2];
-#pragma unroll
-      for (int s2 = 0; s2 < 2; ++s2) {
-        u32x4 wh, wl;
-#pragma unroll
-        for (int i2 = 0; i2 < 4; ++i2) {
-          const float p0 = __builtin_amdgcn_exp2f(st[8 * s2 + 2 * i2] - msub);
-          const float p1 = __builtin_amdgcn_exp2f(st[8 * s2 + 2 * i2 + 1] - msub);
-          ls += p0 + p1;
-          wh[i2] = M::pack2(p0, p1);
-          wl[i2] = M::pack2(p0 - M::lo(wh[i2]), p1 - M::hi(wh[i2]));
-        }
-        phi[s2] = __builtin_bit_cast(vec, wh);
-        plo[s2] = __builtin_bit_cast(vec, wl);
-      }
-      ls += __shfl_xor(ls, 32);
-      l = l * alpha + ls;
-      m = mn;
-      if (__ballot(move) != 0ull) {   // a column's reference moved: rescale
-#pragma unroll
-        for (int db = 0; db < DB; ++db)
-#pragma unroll
-          for (int e = 0; e < 16; ++e) acc[db][e] *= alpha;
-      }
-      // the V^T operand of dim 32 db + c32: k-slot i of half h at position 16 s + 8 (i / 4) + 4 h + i % 4,
-      // read from the value rows by two transposing reads (k-slots 0-3, then 4-7)
-#pragma unroll
-      for (int db = 0; db < DB; ++db) {
-#pragma unroll
-        for (int s2 = 0; s2 < 2; ++s2) {
-          const int s = 2 * rb + s2;
-          const unsigned char* src = s_v + (16 * s + tr_pos) * PK + (32 * db + tr_dim) * 2;
-          const u32x2 lo4 = __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-                                                          (__attribute__((address_space(3))) i16x4*)(src)));
-          const u32x2 hi4 = __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-                                                          (__attribute__((address_space(3))) i16x4*)(src + 8 * PK)));
-          const u32x4 w = {lo4[0], lo4[1], hi4[0], hi4[1]};
-          const vec a = __builtin_bit_cast(vec, w);
-          acc[db] = M::mma(a, phi[s2], acc[db]);
-          acc[db] = M::mma(a, plo[s2], acc[db]);
+          st[rb][e] = ok ? st[rb][e] * p.scale_log2 : -INFINITY;
+          mt = fmaxf(mt, st[rb][e]);
         }
       }
     }
-  };
-  load_step(j0, ka, va, oka);
-  if (j0 + kPfPos < j1) load_step(j0 + kPfPos, kb, vb, okb);
-  for (int jt = j0; jt < j1; jt += 2 * kPfPos) {
-    step(jt, ka, va, oka);
-    if (jt + kPfPos < j1) step(jt + kPfPos, kb, vb, okb);
+    mt = fmaxf(mt, __shfl_xor(mt, 32));
+    // The column's reference m moves only when a score exceeds it by more than 8 (log2 units),
+    // to the new maximum: weights stay at most 2^8 and the accumulators are rescaled rarely.
+    // exp2 by v_exp_f32 (a weight below 2^-126 flushes to zero); -inf scores weigh 0, and a
+    // column with no score yet subtracts 0.
+    const bool move = mt > m + 8.f;
+    const float mn = move ? mt : m;
+    const float msub = mn == -INFINITY ? 0.f : mn;
+    const float alpha = move ? __builtin_amdgcn_exp2f(m - msub) : 1.f;
+    m = mn;
+    if (__ballot(move) != 0ull) {   // a column's reference moved: rescale
+      l *= alpha;
+#pragma unroll
+      for (int db = 0; db < DB; ++db)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) acc[db][e] *= alpha;
+    }
+    // per 16-position k-step s: P as the hi / lo B operands, then O^T += V^T P^T with the V^T
+    // operand of dim 32 db + c32 (k-slot i of half h at position 16 s + 8 (i / 4) + 4 h + i % 4)
+    // read from the value rows by two transposing reads (k-slots 0-3, then 4-7)
+    float ls = 0.f;
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      u32x4 wh, wl;
+#pragma unroll
+      for (int i2 = 0; i2 < 4; ++i2) {
+        const float p0 = __builtin_amdgcn_exp2f(st[s >> 1][8 * (s & 1) + 2 * i2] - msub);
+        const float p1 = __builtin_amdgcn_exp2f(st[s >> 1][8 * (s & 1) + 2 * i2 + 1] - msub);
+        ls += p0 + p1;
+        wh[i2] = M::pack2(p0, p1);
+        wl[i2] = M::pack2(p0 - M::lo(wh[i2]), p1 - M::hi(wh[i2]));
+      }
+      const vec phi = __builtin_bit_cast(vec, wh), plo = __builtin_bit_cast(vec, wl);
+#pragma unroll
+      for (int db = 0; db < DB; ++db) {
+        const unsigned char* src = s_v + (16 * s + tr_pos) * PK + (32 * db + tr_dim) * 2;
+        const u32x2 lo4 = __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                                                        (__attribute__((address_space(3))) i16x4*)(src)));
+        const u32x2 hi4 = __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                                                        (__attribute__((address_space(3))) i16x4*)(src + 8 * PK)));
+        const u32x4 w = {lo4[0], lo4[1], hi4[0], hi4[1]};
+        const vec a = __builtin_bit_cast(vec, w);
+        acc[db] = M::mma(a, phi, acc[db]);
+        acc[db] = M::mma(a, plo, acc[db]);
+      }
+    }
+    ls += __shfl_xor(ls, 32);
+    l += ls;
   }
 
   // O^T layout: lane l, element e -> column c, dim 32 db + 8 (e / 4) + 4 h + e % 4
@@ -995,7 +991,7 @@ void launch(const PaParams& p, const PfParams& f, int n_tokens, int n_tiles, hip
   }
   if constexpr (Elem<T>::bytes == 2) {
     if (n_tiles > 0) {
-      dim3 grid(n_tiles, p.hkv, f.max_parts > 0 ? f.max_parts : 1);
+      dim3 grid(n_tiles, p.hkv, f.max_parts);
       hipLaunchKernelGGL((pa_prefill_kernel<T, D, G>), grid, dim3(kPfThreads), 0, stream, p, f);
     }
   }
@@ -1143,7 +1139,7 @@ int ns_paged_attention(const ns_paged_attn_args* a, hipStream_t stream) {
   f.ws_ml = pf_need ? f.ws_acc + (uint64_t)n_tiles * a->num_kv_heads * pf_max_parts * kPfCols * a->head_dim : nullptr;
   f.counters = a->counters ? a->counters + (int64_t)a->total_q * a->num_kv_heads : nullptr;
   f.part_tokens = pf_part;
-  f.max_parts = (int32_t)pf_max_parts;
+  f.max_parts = pf_max_parts > 0 ? (int32_t)pf_max_parts : 1;
 
   const int g = a->num_heads_q / a->num_kv_heads;
   switch (a->dtype) {

@@ -163,6 +163,15 @@ def test_side_stream_and_output_stride(device):
                                 stream=side.cuda_stream)
     side.synchronize()
     assert torch.equal(raw, want)
+    # a raw handle of 0 is the null stream, torch's default stream: the call is ordered after the
+    # default stream's unsynchronized work (the caches written just before it)
+    torch.cuda.synchronize()
+    with torch.cuda.stream(torch.cuda.default_stream(device)):
+        kc, vc = c["k_cache"].clone(), c["v_cache"].clone()
+        null = A.paged_attention_hip(c["query"], kc, vc, c["block_tables"], c["seq_lens"], c["query_start_loc"],
+                                     c["query_lens"], c["scale"], c["block_size"], stream=0)
+    torch.cuda.default_stream(device).synchronize()
+    assert torch.equal(null, want)
     q = c["query"]
     bad = torch.empty((q.shape[0], q.shape[1], q.shape[2] * 2), dtype=q.dtype, device=device)[:, :, ::2]
     with pytest.raises(A.PagedAttentionError, match="unit head_dim stride"):
