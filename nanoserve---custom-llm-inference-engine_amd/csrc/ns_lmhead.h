@@ -27,6 +27,9 @@
 //   Inside a stage the k order is permuted the same way for both operands: at k-step s
 //   the lanes of half h (lane / 32) take k = 32h + 8s .. 32h + 8s + 7.  A dot product does
 //   not depend on the order of its terms; only the fp32 rounding of the running sum does.
+// Batches beyond 64 rows over the packed weight take lm_head_cols_kernel (below): the same
+// products in the same order, with each wave owning 32 vocab rows and the whole batch, the
+// weight streamed straight into registers and only the hidden tile in LDS.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -79,11 +82,20 @@ __device__ __forceinline__ void lm_lds_barrier() {
 }
 
 // Packed weight layout (ns_lm_head_pack_bf16): for each block of LM_NT vocab rows and each
-// k stage, the stage's tile [LM_NT rows][LM_KT] bf16 as 32 contiguous KB, in the order the
-// kernel reads it; rows past n are zero.  Each stage is then one contiguous 32 KB read per
-// workgroup instead of 256 pieces of 128 B at the row stride, which HBM serves at a far
-// lower rate.
+// k stage, the stage's tile [LM_NT rows][LM_KT] bf16 as 32 contiguous KB; rows past n are
+// zero.  Each stage is then one contiguous 32 KB read per workgroup instead of 256 pieces of
+// 128 B at the row stride, which HBM serves at a far lower rate.  Inside the tile the
+// 16-byte pieces are in the order one wave's MFMA B operands take them: for each block of
+// 32 rows (one wave's columns in lm_head_cols_kernel), for each k-step s, the 64 lanes'
+// pieces (lane l: row l % 32, k = 32 (l / 32) + 8 s .. + 7), so each load instruction of a
+// wave reads 1 KB contiguous.
 constexpr int LM_TILE_BYTES = LM_NT * LM_KT * 2;
+
+// Piece index, inside its packed tile, of tile row `row` (0..LM_NT-1) and the stage's k chunk c
+// (k = 8c .. 8c + 7 of the stage; c = 4 h + s for lane half h and k-step s).
+__host__ __device__ __forceinline__ int lm_packed_piece(int row, int c) {
+  return (((row >> 5) * 4 + (c & 3)) << 6) + (row & 31) + ((c >> 2) << 5);
+}
 
 __global__ void lm_head_pack_kernel(const uint16_t* __restrict__ w, int64_t ldw, int32_t n, int32_t k,
                                     uint16_t* __restrict__ packed) {
@@ -96,11 +108,14 @@ __global__ void lm_head_pack_kernel(const uint16_t* __restrict__ w, int64_t ldw,
   const int64_t b = i / per_block;
   const int64_t rem = i - b * per_block;
   const int st = (int)(rem / (LM_TILE_BYTES / 16));
-  const int q = (int)(rem % (LM_TILE_BYTES / 16));   // 16-byte piece within the tile
-  const int r = q >> 3, c = (q & 7) * 8;               // tile row, first k of the piece
+  const int p = (int)(rem % (LM_TILE_BYTES / 16));   // 16-byte piece within the tile
+  // the inverse of lm_packed_piece: row block p / 256, k-step (p / 64) % 4, lane p % 64
+  const int l = p & 63;
+  const int r = ((p >> 8) << 5) + (l & 31);            // tile row
+  const int c = ((l >> 5) << 2) + ((p >> 6) & 3);      // k chunk of the stage
   const int64_t v = b * LM_NT + r;
   lm_u32x4 x = {0u, 0u, 0u, 0u};
-  if (v < n) x = *reinterpret_cast<const lm_u32x4*>(w + v * ldw + (int64_t)st * LM_KT + c);
+  if (v < n) x = *reinterpret_cast<const lm_u32x4*>(w + v * ldw + (int64_t)st * LM_KT + c * 8);
   *reinterpret_cast<lm_u32x4*>(packed + i * 8) = x;
 }
 
@@ -135,7 +150,7 @@ __global__ __launch_bounds__(LM_THREADS, 1) void lm_head_kernel(const LmParams P
   uint32_t woff[LM_WL];
 #pragma unroll
   for (int j = 0; j < LM_WL; ++j)
-    woff[j] = PACKED ? (uint32_t)((tr + 64 * j) * (LM_KT * 2) + tp * 16) : (uint32_t)((tr + 64 * j) * P.ldw * 2 + tp * 16);
+    woff[j] = PACKED ? (uint32_t)(lm_packed_piece(tr + 64 * j, tp) * 16) : (uint32_t)((tr + 64 * j) * P.ldw * 2 + tp * 16);
   // hidden: the gathered rows (rows past m read the last row; never stored)
   const uint16_t* asrc[LM_AL];
 #pragma unroll
@@ -259,6 +274,162 @@ __global__ __launch_bounds__(LM_THREADS, 1) void lm_head_kernel(const LmParams P
               ((bad >> (i * 16 + e)) & 1u) ? (uint16_t)0x7fc0u : lm_bf16_rne(acc[i][j][e]);
       }
     }
+}
+
+typedef __attribute__((address_space(3))) void lm_lds_void;
+
+// One direct-to-LDS load: 16 bytes per lane from the buffer at voff + soff, to LDS at dst + 16 lane
+// (dst wave-uniform, a __shared__ address).
+__device__ __forceinline__ void lm_load_lds16(__amdgpu_buffer_rsrc_t r, unsigned char* dst, uint32_t voff, int soff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lm_lds_void*)dst, 16, voff, soff, 0, 0);
+}
+
+// Large batches (more than 64 rows) over the packed weight: the column-owner form.  Wave w owns vocab rows
+// n0 + 32 w .. + 31 and all MT = 32 TM batch rows of the workgroup (TM tiles of 32 x 32,
+// 16 TM accumulators per lane), so each weight piece is used by one wave only: it goes from
+// HBM straight into that wave's B operand registers and never through LDS.  A register set
+// holds one stage (four k-steps); each k-step's registers are refilled with the stage three
+// ahead as soon as its products are issued, so about three stages of weight (96 KB per CU)
+// stay in flight.  The hidden tile, shared by the eight waves, goes to LDS by direct-to-LDS
+// buffer loads two stages ahead, into a ring of three stage arrays: slot t of a stage
+// (16 bytes) holds batch row t / 8's k chunk (t % 8) ^ ((row / 2) % 8), an XOR swizzle under
+// which the 16 lanes (16 consecutive rows) of each 256-byte LDS read cycle hit all 64 banks
+// once.  The ring's three stages are three arrays and the stage loop is unrolled by three, so
+// every LDS access names its array: the compiler then sees that a stage's reads do not touch
+// the arrays its direct loads are filling and does not wait for those loads before them.
+// Per stage st: this wave's hidden loads of stage st are waited for (the counter form below:
+// the loads issued since stay in flight), a barrier makes every wave's share visible (and
+// every wave is past stage st - 1's reads, so that array can be refilled), stage st + 2's
+// hidden is issued, then stage st's products with the weight refills.  The MFMA operands and
+// their order are lm_head_kernel's, so the logits are the same bit for bit.
+template <int TM>
+__global__ __launch_bounds__(LM_THREADS, 1) void lm_head_cols_kernel(const LmParams P) {
+  constexpr int MT = 32 * TM;                   // batch rows per workgroup
+  constexpr int SB = MT * LM_KT * 2;            // LDS bytes of one hidden stage
+  constexpr int HL = SB / 16 / LM_THREADS;      // direct 16-byte loads per thread per stage
+  // loads issued after stage st's hidden loads when stage st is waited for (from stage st + 2
+  // on; the prologue's first stages have more): w(st+1), h(st+1), w(st+2)
+  constexpr int VMC = 8 + HL;
+  constexpr int WAIT = (VMC & 15) | (7 << 4) | (15 << 8) | ((VMC >> 4) << 14);   // vmcnt(VMC) only
+  static_assert(HL >= 1 && VMC < 64, "tiling");
+  __shared__ __attribute__((aligned(16))) unsigned char sh0[SB];
+  __shared__ __attribute__((aligned(16))) unsigned char sh1[SB];
+  __shared__ __attribute__((aligned(16))) unsigned char sh2[SB];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int r32 = lane & 31, h = lane >> 5;
+  const int n0 = blockIdx.x * LM_NT;
+  const int m0 = blockIdx.y * MT;
+  const int nst = P.k / LM_KT;
+
+  // weight (packed): this lane's piece of k-step s of a stage, 1 KB contiguous per wave and
+  // k-step (k-step s at + 1 KB)
+  const __amdgpu_buffer_rsrc_t wrs =
+      make_rsrc(P.weight + (int64_t)blockIdx.x * nst * (LM_TILE_BYTES / 2), (uint32_t)(nst * LM_TILE_BYTES));
+  const uint32_t woff = (uint32_t)(lm_packed_piece(32 * wave + r32, 4 * h) * 16);
+  // hidden: this thread's slots j * LM_THREADS + tid of a stage (rows past m read the last row,
+  // never stored; a gathered index outside the hidden tensor reads row 0, its logits row is NaN)
+  const __amdgpu_buffer_rsrc_t hrs = make_rsrc(P.hidden, (uint32_t)(P.n_hidden * P.ldh * 2));
+  uint32_t hoff[HL];
+#pragma unroll
+  for (int j = 0; j < HL; ++j) {
+    const int t = j * LM_THREADS + tid;
+    const int mr = t >> 3, c = (t & 7) ^ ((mr >> 1) & 7);
+    int r = m0 + mr;
+    r = r < P.m ? r : P.m - 1;
+    int64_t hr = P.rows != nullptr ? P.rows[r] : (int64_t)r;
+    hr = hr >= 0 && hr < P.n_hidden ? hr : 0;
+    hoff[j] = (uint32_t)(hr * P.ldh * 2 + c * 16);
+  }
+  // rows whose gathered index lies outside the hidden tensor (their logits rows are written as
+  // NaN): bit rr % 64 of badm[rr / 64] for row m0 + rr, the same in every lane
+  uint64_t badm[MT / 64 > 0 ? MT / 64 : 1];
+#pragma unroll
+  for (int q = 0; q < (MT + 63) / 64; ++q) {
+    const int r = m0 + 64 * q + lane;
+    bool b = false;
+    if (P.rows != nullptr && r < P.m && 64 * q + lane < MT) {
+      const int64_t hr = P.rows[r];
+      b = hr < 0 || hr >= P.n_hidden;
+    }
+    badm[q] = __ballot(b);
+  }
+
+  lm_f32x16 acc[TM];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int e = 0; e < 16; ++e) acc[i][e] = 0.0f;
+  lm_bf16x8 wr[3][4];
+
+  // Loads of stages past the last are clamped to it (their data is never used): every stage
+  // issues the same loads, so the counter wait counts the same loads every time.
+  auto slot = [&](int b) -> unsigned char* { return b == 0 ? sh0 : b == 1 ? sh1 : sh2; };
+  auto issue_h = [&](int st, int b) {
+    const int sl = st < nst ? st : nst - 1;
+    unsigned char* dst = slot(b) + wave * 64 * 16;
+#pragma unroll
+    for (int j = 0; j < HL; ++j) lm_load_lds16(hrs, dst + j * LM_THREADS * 16, hoff[j], sl * LM_KT * 2);
+  };
+  auto load_w = [&](int st, int s) -> lm_bf16x8 {
+    const int sl = st < nst ? st : nst - 1;
+    // streamed once: non-temporal
+    const ns_v4u x = __builtin_amdgcn_raw_buffer_load_b128(wrs, (int)(woff + 1024u * s), sl * LM_TILE_BYTES, 2);
+    return __builtin_bit_cast(lm_bf16x8, x);
+  };
+  auto stage = [&](int st, int d) {   // d = st % 3
+    __builtin_amdgcn_s_waitcnt(WAIT);
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+    issue_h(st + 2, (d + 2) % 3);
+    __builtin_amdgcn_sched_barrier(0);   // the hidden loads go out first, not after the products
+    const unsigned char* ab = slot(d) + r32 * (LM_KT * 2);
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      const int q = ((4 * h + s) ^ ((r32 >> 1) & 7)) << 4;
+#pragma unroll
+      for (int i = 0; i < TM; ++i) {
+        const lm_bf16x8 a = *reinterpret_cast<const lm_bf16x8*>(ab + i * 4096 + q);
+        acc[i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, wr[d][s], acc[i], 0, 0, 0);
+      }
+      wr[d][s] = load_w(st + 3, s);   // the k-step's registers, refilled three stages ahead
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  };
+
+  // issue order: h0 w0 h1 w1 w2, then at stage st: h(st + 2), and w(st + 3) one k-step at a time
+  issue_h(0, 0);
+#pragma unroll
+  for (int s = 0; s < 4; ++s) wr[0][s] = load_w(0, s);
+  issue_h(1, 1);
+#pragma unroll
+  for (int s = 0; s < 4; ++s) wr[1][s] = load_w(1, s);
+#pragma unroll
+  for (int s = 0; s < 4; ++s) wr[2][s] = load_w(2, s);
+  int st = 0;
+  for (; st + 3 <= nst; st += 3) {
+    stage(st, 0);
+    stage(st + 1, 1);
+    stage(st + 2, 2);
+  }
+  if (st < nst) stage(st, 0);
+  if (st + 1 < nst) stage(st + 1, 1);
+  // nothing may land in LDS after the workgroup ends
+  __builtin_amdgcn_s_waitcnt(0);
+
+  // accumulator layout as in lm_head_kernel: lane l, element e -> column l % 32,
+  // row 8 (e / 4) + 4 (l / 32) + e % 4 of tile i
+  const int col = n0 + 32 * wave + r32;
+  if (col < P.n) {
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const int rr = 32 * i + 8 * (e >> 2) + 4 * h + (e & 3);   // row within the workgroup's rows
+        const bool nan_row = (badm[i >> 1] >> (rr & 63)) & 1ull;
+        if (m0 + rr < P.m)
+          P.logits[(int64_t)(m0 + rr) * P.ldl + col] = nan_row ? (uint16_t)0x7fc0u : lm_bf16_rne(acc[i][e]);
+      }
+  }
 }
 
 }  // namespace ns

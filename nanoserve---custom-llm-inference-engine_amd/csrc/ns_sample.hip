@@ -1722,6 +1722,19 @@ static int lm_launch(const void* hidden, int64_t ld_hidden, int64_t n_hidden, co
   if (gy > 65535) return fail(NS_ERR_INVALID, "m too large");
   ns::LmParams P{static_cast<const uint16_t*>(hidden), ld_hidden, rows, n_hidden, static_cast<const uint16_t*>(weight),
                  packed ? 0 : ld_weight, static_cast<uint16_t*>(logits), ld_logits, m, n, k};
+  // batches beyond 64 rows: the column-owner kernel (weight straight into registers), over
+  // 256-row (or, up to 128 rows, 128-row) workgroup rows; its hidden loads take 32-bit offsets
+  if (packed && m > 64 && n_hidden * ld_hidden * 2 < (int64_t)0xffffffffu) {
+    const int tm = m <= 128 ? 4 : 8;
+    const int64_t gyc = ((int64_t)m + 32 * tm - 1) / (32 * tm);
+    if (gyc > 65535) return fail(NS_ERR_INVALID, "m too large");
+    const dim3 gridc((unsigned)((n + ns::LM_NT - 1) / ns::LM_NT), (unsigned)gyc), blockc(ns::LM_THREADS);
+    if (tm == 4) hipLaunchKernelGGL((ns::lm_head_cols_kernel<4>), gridc, blockc, 0, stream, P);
+    else hipLaunchKernelGGL((ns::lm_head_cols_kernel<8>), gridc, blockc, 0, stream, P);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return fail(NS_ERR_HIP, std::string("lm_head launch: ") + hipGetErrorString(e));
+    return NS_OK;
+  }
   const dim3 grid((unsigned)((n + ns::LM_NT - 1) / ns::LM_NT), (unsigned)gy), block(ns::LM_THREADS);
   if (packed) {
     if (wm == 1) hipLaunchKernelGGL((ns::lm_head_kernel<1, 4, true>), grid, block, 0, stream, P);
