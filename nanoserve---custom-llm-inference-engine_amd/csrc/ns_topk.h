@@ -83,19 +83,19 @@ __device__ __forceinline__ void topk_issue_early(uint4 (&v)[TK_CPT], const unsig
   }
 }
 
-// The k-th largest of the wave's 256 keys (a0..a3 in every lane), truncated to its top NB
-// bits, as wave_kth_key.
-template <int NB>
-__device__ __forceinline__ uint32_t wave_kth_key4(uint32_t a0, uint32_t a1, uint32_t a2, uint32_t a3, int k) {
-  uint32_t p = 0u;
-#pragma unroll
-  for (int b = 31; b >= 32 - NB; --b) {
-    const uint32_t c = p | (1u << b);
-    const int cnt = __popcll(ballot(a0 >= c)) + __popcll(ballot(a1 >= c)) + __popcll(ballot(a2 >= c)) +
-                    __popcll(ballot(a3 >= c));
-    p = cnt >= k ? c : p;
-  }
-  return p;
+// The bound's key: the k-th largest of the row's group maxima fs (128 per phase; maxima of
+// disjoint element groups, so k of them reach it), truncated to its top bits.  One phase:
+// 16 bits for bfloat16 (the bits its values carry), 24 for float32.  Two phases: each first-phase
+// group is merged with the second-phase group of the same index (the maximum of their union),
+// and the key of the k-th of those 128 is truncated to 16 bits, a slightly weaker bound (within
+// 2^-7 of the value) for a select of half the votes over two thirds of the bits: it is the
+// last wave's serial step after the stream.  Called by one wave.
+template <typename T, int NPH>
+__device__ __forceinline__ uint32_t topk_bound_key(const float* fs, int lane, int k) {
+  if constexpr (NPH == 1) return wave_kth_key<T::SZ == 2 ? 16 : 24>(fkey(fs[lane]), fkey(fs[64 + lane]), k);
+  else
+    return wave_kth_key<16>(fkey(__builtin_fmaxf(fs[lane], fs[128 + lane])),
+                            fkey(__builtin_fmaxf(fs[64 + lane], fs[192 + lane])), k);
 }
 
 // A chunk maximum kept as the top 16 bits of its order key, rounded up (the value it stands
@@ -246,10 +246,7 @@ __device__ __forceinline__ int topk_stream(const RowArgs P, const int row, const
     if (lane == 0) ticket = __hip_atomic_fetch_add(&misc->ib[0], 1, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_WORKGROUP);
     if (__builtin_amdgcn_readfirstlane(ticket) == NWAVE - 1) {
       NS_STAMP_LANE(2, lane == 0);   // the last wave to finish its share
-      const uint32_t kp =
-          NPH == 1 ? wave_kth_key<T::SZ == 2 ? 16 : 24>(fkey(fs[lane]), fkey(fs[64 + lane]), k)
-                   : wave_kth_key4<T::SZ == 2 ? 16 : 24>(fkey(fs[lane]), fkey(fs[64 + lane]), fkey(fs[128 + lane]),
-                                                         fkey(fs[192 + lane]), k);
+      const uint32_t kp = topk_bound_key<T, NPH>(fs, lane, k);
       const float taux = kp <= fkey(-__builtin_inff()) ? -__builtin_inff() : fkey_inv(kp);
       const float b = lower_preimage(taux, tdiv, rdiv);
       NS_STAMP_LANE(7, lane == 0);   // the last wave: the bound taken
@@ -438,10 +435,7 @@ __device__ __forceinline__ int topk_stream(const RowArgs P, const int row, const
     if (tid == 0) misc->cand_n = 0;
     __syncthreads();
     if (wid == 0) {
-      const uint32_t kp =
-          NPH == 1 ? wave_kth_key<T::SZ == 2 ? 16 : 24>(fkey(fs[lane]), fkey(fs[64 + lane]), k)
-                   : wave_kth_key4<T::SZ == 2 ? 16 : 24>(fkey(fs[lane]), fkey(fs[64 + lane]), fkey(fs[128 + lane]),
-                                                         fkey(fs[192 + lane]), k);
+      const uint32_t kp = topk_bound_key<T, NPH>(fs, lane, k);
       const float taux = kp <= fkey(-__builtin_inff()) ? -__builtin_inff() : fkey_inv(kp);
       if (lane == 0) misc->fb[0] = lower_preimage(taux, tdiv, rdiv);
     }
