@@ -61,9 +61,9 @@ __device__ __forceinline__ void uniform_row_out(const RowOut& o, float u, int32_
   }
 }
 
-// A row chunk with the cache policy of its phase: non-temporal for the last phase (read once,
-// from registers), the default policy before it (its chunks that reach the bound are read
-// again, from the L2).
+// A row chunk with the cache policy of its row: non-temporal for one-phase rows (read once,
+// staged from registers), the default policy for two-phase rows (their chunks that reach the
+// bound are read again, from the L2).
 template <int NPH>
 __device__ __forceinline__ uint4 topk_load(__amdgpu_buffer_rsrc_t r, uint32_t voff) {
   if constexpr (NPH == 1) return buf_load16_nt(r, voff);
@@ -111,7 +111,7 @@ __device__ __forceinline__ float key16_val(uint32_t k16) { return fkey_inv(k16 <
 // resolved, 1 when it is left to the general per-row code.  NPH = 2: the row streams in two
 // phases of TK_PH chunks through the same registers; the first phase's chunk maxima are
 // kept (rounded up, 16 bits each), the bound is taken over both phases' group maxima, and
-// the first phase's chunks that reach it are read again from the L2.
+// the chunks of both phases that reach it are read again from the L2.
 template <typename T, int NPH = 1>
 __device__ __forceinline__ int topk_stream(const RowArgs P, const int row, const unsigned char* rowp,
                                            uint4 (&v)[TK_CPT], const bool early, const int32_t* hp,
@@ -219,7 +219,8 @@ __device__ __forceinline__ int topk_stream(const RowArgs P, const int row, const
     }
 #pragma unroll
     for (int q = 0; q < TK_CPT; ++q) {
-      v[q] = buf_load16_nt(r2, (uint32_t)(q * NT + tid) * 16u);
+      // the default cache policy: this phase's chunks that reach the bound are read again too
+      v[q] = buf_load16(r2, (uint32_t)(q * NT + tid) * 16u, 0u);
       __builtin_amdgcn_sched_barrier(0);
     }
     gmax = __builtin_fmaxf(gmax, lane_xor(gmax, 1));
@@ -313,34 +314,52 @@ __device__ __forceinline__ int topk_stream(const RowArgs P, const int row, const
     constexpr bool RR = decltype(reread)::value;
     int nh = 0;             // this wave's hit chunks (wave-uniform)
     if constexpr (NPH == 2) {
-      // first-phase chunks whose kept maximum reaches tc: only their index is staged, with
-      // the top bit set (the expansion reads them again)
+      // Two phases: every chunk that reaches tc is staged by index (top bit set) and read again
+      // from the L2 by the expansion.  Each lane first forms its hit masks of both phases (the
+      // first phase against its kept maxima); then one append per round for the lanes that
+      // still hold hits, their lowest first (rarely more than one round), instead of a vote
+      // per chunk.
+      uint32_t h1 = 0u, h2 = 0u;
 #pragma unroll
       for (int q = 0; q < TK_CPT; ++q) {
-        const bool hit = key16_val((pk[q >> 1] >> ((q & 1) * 16)) & 0xffffu) >= tc;
+        h1 |= (key16_val((pk[q >> 1] >> ((q & 1) * 16)) & 0xffffu) >= tc ? 1u : 0u) << q;
+        h2 |= (cm[q] >= tc ? 1u : 0u) << q;   // -inf past the row, and tc > -inf
+      }
+      while (true) {
+        const bool act = (h1 | h2) != 0u;
+        const uint64_t m = ballot(act);
+        if (m == 0ull) break;
+        uint32_t ci = 0u;
+        if (act) {
+          if (h1 != 0u) {
+            ci = (uint32_t)(__builtin_ctz(h1) * NT + tid);
+            h1 &= h1 - 1u;
+          } else {
+            ci = (uint32_t)(C0 + __builtin_ctz(h2) * NT + tid);
+            h2 &= h2 - 1u;
+          }
+        }
+        const int pos = nh + lanes_below(m);
+        if (act && pos < HIT_PER_WAVE) hidx[pos] = (int32_t)(0x80000000u | ci);
+        nh += __popcll(m);
+      }
+    } else {
+#pragma unroll
+      for (int q = 0; q < TK_CPT; ++q) {
+        const bool hit = cm[q] >= tc;   // -inf past the row, and tc > -inf
         const uint64_t m = ballot(hit);
         if (m != 0ull) {
           const int pos = nh + lanes_below(m);
-          if (hit && pos < HIT_PER_WAVE) hidx[pos] = (int32_t)(0x80000000u | (uint32_t)(q * NT + tid));
+          if (hit && pos < HIT_PER_WAVE) {
+            if constexpr (RR) {
+              hidx[pos] = (int32_t)(0x80000000u | (uint32_t)(C0 + q * NT + tid));
+            } else {
+              hdat[pos] = v[q];
+              hidx[pos] = C0 + q * NT + tid;
+            }
+          }
           nh += __popcll(m);
         }
-      }
-    }
-#pragma unroll
-    for (int q = 0; q < TK_CPT; ++q) {
-      const bool hit = cm[q] >= tc;   // -inf past the row, and tc > -inf
-      const uint64_t m = ballot(hit);
-      if (m != 0ull) {
-        const int pos = nh + lanes_below(m);
-        if (hit && pos < HIT_PER_WAVE) {
-          if constexpr (RR) {
-            hidx[pos] = (int32_t)(0x80000000u | (uint32_t)(C0 + q * NT + tid));
-          } else {
-            hdat[pos] = v[q];
-            hidx[pos] = C0 + q * NT + tid;
-          }
-        }
-        nh += __popcll(m);
       }
     }
     NS_STAMP(8);   // wave 0: its chunks staged
