@@ -673,6 +673,8 @@ def main(argv=None):
     torch.cuda.set_device(dev)
     if args.lm_head_sweep:
         lm_head_sweep(L, dev)
+        if args.copy_mb > 0:
+            copy_reference(dev, args.copy_mb)
         return 0
     if args.paged_attention:
         st = torch.cuda.current_stream(dev)
