@@ -109,3 +109,31 @@ def test_lm_head_special_values(device):
     assert torch.equal(torch.isinf(ours), torch.isinf(ref))
     fin = torch.isfinite(ref)
     assert bool(((ours[fin] - ref[fin]).abs() <= ref[fin].abs() * 2.0 ** -8 + 1e-3).all())
+
+
+@pytest.mark.parametrize("m", [100, 260])
+def test_packed_large_batch_gathers_rows_and_flags_bad_indices(device, m):
+    """Packed batches beyond 64 rows (the column-owner kernel, one and two workgroup rows):
+    gathered rows, a padded hidden stride, invalid indices as NaN rows, a logits buffer wider
+    than the vocab; the same bits as the weight as stored."""
+    hidden_full, weight = make(device, 700, 1300, 192, seed=31 + m, scale=3.0)
+    hidden = torch.zeros((700, 200), dtype=torch.bfloat16, device=device)[:, :192]
+    hidden.copy_(hidden_full)
+    g = np.random.default_rng(m)
+    rows_np = g.integers(0, 700, size=m).astype(np.int64)
+    bad_pos = g.choice(m, 5, replace=False)
+    rows_np[bad_pos] = np.array([-1, 700, 701, -5, 1 << 40], dtype=np.int64)
+    rows = torch.from_numpy(rows_np).to(device)
+    pw = L.PackedLmHead(weight)
+    out_full = torch.full((m, 1400), 7.0, dtype=torch.bfloat16, device=device)
+    out = out_full[:, :1300]
+    L.lm_head_bf16(hidden, pw, rows=rows, out=out)
+    plain = L.lm_head_bf16(hidden, weight, rows=rows)
+    torch.cuda.synchronize()
+    assert bool((out_full[:, 1300:] == 7.0).all())   # nothing written past n
+    bad = torch.zeros(m, dtype=torch.bool, device=device)
+    bad[torch.from_numpy(bad_pos).to(device)] = True
+    assert bool(torch.isnan(out.float()[bad]).all())
+    good = ~bad
+    check(out[good], hidden_full, weight, rows=rows[good])
+    assert torch.equal(out[good].contiguous().view(torch.int16), plain[good].contiguous().view(torch.int16))
