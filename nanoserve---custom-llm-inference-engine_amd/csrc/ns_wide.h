@@ -128,6 +128,7 @@ struct WideSmemT {
   unsigned long long segfx[MAX_SEGS];
   unsigned long long subq[MAX_SEGS];         // the finaliser's kept mass per segment
   int32_t off[MAX_SEGS + 1];
+  int32_t nab[MAX_SEGS];                     // the finaliser's elements above the plan per segment
   unsigned long long ured[NWAVE];
   double dred[NWAVE];
   float fred[NWAVE];
@@ -563,6 +564,131 @@ __device__ __forceinline__ int64_t wide_locate(const WideParams& P, const WRowCt
   return tok;
 }
 
+// A raw logit below which no token of the row reaches the scaled value B (finite): RN(x / t)
+// >= B implies x >= t * B less a few units in the last place, so x >= lx for lx = RN(t * B)
+// lowered by 2^-21 of itself (four units in the last place at least) and by a margin for
+// subnormal quotients.  A penalty >= 1 (also as a multiply by RN(1/p) <= 1) never raises a
+// value, so the bound holds for history tokens too.  -inf (no bound) for a penalty below 1 or
+// an out-of-range product.
+__device__ __forceinline__ float wide_raw_bound(const WRowCtx& c, float B) {
+  if (!(B > -__builtin_inff()) || (c.pen_on && !(c.pen >= 1.0f))) return -__builtin_inff();
+  const float L = c.scale ? B * c.tdiv : B;
+  if (!(__builtin_fabsf(L) < 0x1.0p+120f)) return -__builtin_inff();
+  return L - __builtin_fabsf(L) * 0x1.0p-21f - (c.tdiv + 1.0f) * 0x1.0p-140f;
+}
+
+// wide_locate for a planned row, over the tokens that can be kept: every token of the range
+// whose raw logit reaches lx (a superset of the kept set, wide_raw_bound) is listed in
+// ascending id order in `list` (LIST_CAP entries of (scaled value bits << 32) | id, one block
+// scan of the per-thread counts, four 16-bit fields one per step), and only the listed tokens
+// take the scaled value's probability and the cumulative sum.  The same tokens, values and
+// probabilities as wide_locate, which takes the range when more than LIST_CAP tokens reach lx.
+template <typename T, int NTH, int WL, int NCH, int LIST_CAP, typename SM>
+__device__ __forceinline__ int64_t wide_locate_list(const WideParams& P, const WRowCtx& c, int64_t c0, double pstart,
+                                                    double rz, float M, const WKeep& keep, float lx, uint64_t* list,
+                                                    SM* sm, int32_t* fl) {
+  constexpr int EPC = T::EPC;
+  static_assert(NCH % (NTH * WL) == 0 && NCH <= SEG_CH, "whole steps inside one segment's bitmap");
+  constexpr int NSTEP = NCH / (NTH * WL);
+  static_assert(NSTEP <= 4 && NSTEP * WL <= 4 && WL * EPC <= 8, "four 16-bit counts of at most 8 per thread");
+  constexpr int PER = LIST_CAP / NTH;   // listed tokens per thread in the walk
+  const int tid = threadIdx.x;
+  const uint32_t nbytes = (uint32_t)((c.V / EPC) * 16);
+  uint4 raw[NSTEP][WL];
+#pragma unroll
+  for (int step = 0; step < NSTEP; ++step)
+#pragma unroll
+    for (int j = 0; j < WL; ++j)
+      raw[step][j] = buf_load16_at(c.rowp, nbytes,
+                                   (uint32_t)((c0 + (int64_t)step * NTH * WL + (int64_t)tid * WL + j) * 16), 0u);
+  *fl |= wide_bitmap<T, NTH>(P, c, c0 * EPC, sm);
+  // the tokens reaching lx: a mask per step, their count in the step's 16-bit field
+  uint32_t hit[NSTEP];
+  unsigned long long cnt = 0ull;
+#pragma unroll
+  for (int step = 0; step < NSTEP; ++step) {
+    hit[step] = 0u;
+    const int64_t cb = c0 + (int64_t)step * NTH * WL + (int64_t)tid * WL;
+#pragma unroll
+    for (int j = 0; j < WL; ++j) {
+      raw[step][j] = wide_chunk_fix<T>(c, cb + j, raw[step][j]);
+#pragma unroll
+      for (int e = 0; e < EPC; ++e) hit[step] |= (T::elem(raw[step][j], e) >= lx ? 1u : 0u) << (j * EPC + e);
+    }
+    cnt |= (unsigned long long)__popc(hit[step]) << (16 * step);
+  }
+  unsigned long long tot;
+  const unsigned long long off = wexcl_int<unsigned long long, NTH>(cnt, &tot, sm);
+  int base[NSTEP];
+  int n = 0;
+#pragma unroll
+  for (int step = 0; step < NSTEP; ++step) {
+    base[step] = n + (int)((off >> (16 * step)) & 0xffffu);
+    n += (int)((tot >> (16 * step)) & 0xffffu);
+  }
+  if (n > LIST_CAP) return wide_locate<T, NTH, WL, NCH>(P, c, c0, pstart, rz, M, keep, sm, fl);
+  // the listed tokens' scaled values (chunk_y on the chunks holding one), in id order
+#pragma unroll
+  for (int step = 0; step < NSTEP; ++step) {
+    const int64_t cb = c0 + (int64_t)step * NTH * WL + (int64_t)tid * WL;
+    int pos = base[step];
+#pragma unroll
+    for (int j = 0; j < WL; ++j) {
+      const uint32_t hj = (hit[step] >> (j * EPC)) & ((1u << EPC) - 1u);
+      if (hj != 0u) {
+        const int64_t ch = cb + j;
+        const uint32_t hb = c.pen_on ? T::bits(sm->bm, (int)(ch - c0)) : 0u;
+        float y[EPC];
+        chunk_y<T>(c, raw[step][j], hb, ch * EPC, y);
+#pragma unroll
+        for (int e = 0; e < EPC; ++e)
+          if ((hj >> e) & 1u) list[pos++] = ((uint64_t)__float_as_uint(y[e]) << 32) | (uint32_t)(ch * EPC + e);
+      }
+    }
+  }
+  if (tid == 0) { sm->ib[0] = 0x7fffffff; sm->ib[1] = -1; }
+  __syncthreads();
+  // the walk over the list: PER consecutive entries per thread
+  const double ud = (double)c.u;
+  float p[PER];
+  int32_t id[PER];
+  double own = 0.0;
+#pragma unroll
+  for (int i = 0; i < PER; ++i) {
+    const int li = tid * PER + i;
+    p[i] = 0.0f;
+    id[i] = 0;
+    if (li < n) {
+      const uint64_t e = list[li];
+      const float y = __uint_as_float((uint32_t)(e >> 32));
+      id[i] = (int32_t)(uint32_t)e;
+      if (keep(y, id[i])) p[i] = (float)((double)ns_expf(y - M) * rz);
+    }
+    own += (double)p[i];
+  }
+  double total;
+  double run = pstart + wexcl_f64<NTH>(own, &total, sm);
+  int32_t first = 0x7fffffff, lastnz = -1;
+#pragma unroll
+  for (int i = 0; i < PER; ++i) {
+    if (p[i] > 0.0f) {
+      run += (double)p[i];
+      lastnz = id[i];
+      if (run > ud && first == 0x7fffffff) first = id[i];
+    }
+  }
+  if (first != 0x7fffffff) atomicMin(&sm->ib[0], first);
+  if (lastnz >= 0) atomicMax(&sm->ib[1], lastnz);
+  __syncthreads();
+  int64_t tok = sm->ib[0];
+  if (tok == 0x7fffffff) {
+    *fl |= FLAG_LOCATE_FALLBACK;
+    tok = sm->ib[1] >= 0 ? sm->ib[1] : c0 * EPC;
+  }
+  __syncthreads();
+  return tok;
+}
+
 // (row, segment) of this workgroup: all segments of a row share blockIdx % 8 (one XCD).
 __device__ __forceinline__ void wide_rowseg(int S, int* row, int* seg) {
   const int b = blockIdx.x;
@@ -846,6 +972,15 @@ __device__ __forceinline__ void wide_stats_body(const WideParams& P, WideSmem& s
       fl |= lane_xor(fl, o);
     }
     if (lane_id() == 0) { sm.fb[0] = M; sm.ib[0] = nf; sm.ib[1] = fl; }
+    // for the merge below, once per segment (its lane): how many bins its top bin lies below
+    // the row's (WBINS: no finite values, or 2048 bins or more below) and the scale exp(m - M)
+    // of its masses.  Unused unless the row is planned (finite M below WMAX_PLAN).
+    if (act) {
+      const int ds = s.ymax > -__builtin_inff() ? wgrid(M) - wgrid(s.ymax) : WBINS;
+      sm.off[lane_id()] = ds < WBINS ? ds : WBINS;
+      sm.segfx[lane_id()] =
+          (unsigned long long)__double_as_longlong(ds < WBINS ? exp((double)s.ymax - (double)M) : 0.0);
+    }
   }
   __syncthreads();
   const float M = sm.fb[0];
@@ -898,10 +1033,12 @@ __device__ __forceinline__ void wide_stats_body(const WideParams& P, WideSmem& s
     if (tid == 0) { P.status[row] = 1; R->step = WSTEP_NONE; }
     return;
   }
-  // ---- the row histograms: the segments' histograms merged onto the row's grid, 8 bins per
-  // thread (bin b below the row's top bin is bin b - ds of a segment whose top bin lies ds
-  // below the row's; its mass in units of exp(m) scaled by exp(m - M)), in a fixed order
-  const int TB = wgrid(M);
+  // ---- the row histograms: the segments' histograms merged onto the row's grid (bin b below
+  // the row's top bin is bin b - ds of a segment whose top bin lies ds below the row's; its
+  // mass in units of exp(m) scaled by exp(m - M)), in a fixed order.  Thread t merges bins
+  // t + SNT * j, so each load instruction reads 512 consecutive bytes; four segments' words
+  // are in flight per step (the loads of a step are issued together).  The merged bins then
+  // pass through LDS to the planner's layout, 8 consecutive bins per thread.
   constexpr int BPT = WBINS / SNT;
   uint32_t hc[BPT];
   unsigned long long hm[BPT];
@@ -909,36 +1046,43 @@ __device__ __forceinline__ void wide_stats_body(const WideParams& P, WideSmem& s
     double acc[BPT];
 #pragma unroll
     for (int j = 0; j < BPT; ++j) { acc[j] = 0.0; hc[j] = 0u; }
-    // two segments' words in flight per step (the loads of a step are issued together)
     constexpr int SG = 4;
     for (int sg0 = 0; sg0 < P.S; sg0 += SG) {
       uint64_t w[SG][BPT];
-      double sc[SG];
 #pragma unroll
       for (int q = 0; q < SG; ++q) {
         const int sg = sg0 + q;
-        const float ms = sg < P.S ? __uint_as_float(sm.u.h.cnt[sg]) : -__builtin_inff();
         // a segment without finite values, or 2048 bins or more below the row's top: nothing
-        const int ds = ms > -__builtin_inff() ? TB - wgrid(ms) : WBINS;
-        sc[q] = ds < WBINS ? exp((double)ms - (double)M) : 0.0;
+        const int ds = sg < P.S ? sm.off[sg] : WBINS;
         const uint64_t* ex = P.shist + ((int64_t)row * P.S + sg) * WBINS;
 #pragma unroll
         for (int j = 0; j < BPT; ++j) {
-          const int jj = tid * BPT + j - ds;
+          const int jj = tid + SNT * j - ds;
           w[q][j] = (ds < WBINS && jj >= 0) ? dc_load(ex + jj) : 0ull;
         }
       }
 #pragma unroll
       for (int q = 0; q < SG; ++q) {
+        const int sg = sg0 + q;
+        const double sc = sg < P.S && sm.off[sg] < WBINS ? __longlong_as_double((long long)sm.segfx[sg]) : 0.0;
 #pragma unroll
         for (int j = 0; j < BPT; ++j) {
-          acc[j] += (double)__uint_as_float((uint32_t)w[q][j]) * sc[q];
+          acc[j] += (double)__uint_as_float((uint32_t)w[q][j]) * sc;
           hc[j] += (uint32_t)(w[q][j] >> 32);
         }
       }
     }
 #pragma unroll
-    for (int j = 0; j < BPT; ++j) hm[j] = (unsigned long long)(acc[j] * WFX);
+    for (int j = 0; j < BPT; ++j) {
+      sm.u.h.mass[tid + SNT * j] = (unsigned long long)(acc[j] * WFX);
+      sm.u.h.cnt[tid + SNT * j] = hc[j];
+    }
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < BPT; ++j) {
+      hm[j] = sm.u.h.mass[tid * BPT + j];
+      hc[j] = sm.u.h.cnt[tid * BPT + j];
+    }
   }
   wide_plan<BPT>(P, c, R, row, nf, fl, M, hc, hm, sm);
 }
@@ -1192,6 +1336,7 @@ __device__ __forceinline__ void wide_final_row(const WideParams& P, WideSmemCut&
     sm.segfx[tid] = s.mass;
     sm.off[tid] = s.ncand;
     sm.ired[tid] = s.nabove;
+    sm.nab[tid] = s.nabove;
   }
   if (tid < P.S) sm.subq[tid] = dc_load_wseg(P.segs + (int64_t)row * P.S + tid).mass;   // mass above the plan
   if (tid == 0) sm.ib[0] = 0;
@@ -1225,7 +1370,9 @@ __device__ __forceinline__ void wide_final_row(const WideParams& P, WideSmemCut&
   // the planned elements as sort keys (value descending, id ascending), EPT per thread in
   // registers at positions tid * EPT + j, ordered over a power of two of positions; EPT the
   // fewest keys per thread that hold them all (a handful of planned elements is ordered
-  // inside one wave)
+  // inside one wave).  Thread t first holds elements j * NT + t (each load instruction reads
+  // consecutive words): with more than one key per thread the sorted range is every position
+  // (n > NT * EPT / 2), and with one it is the first next_pow2(n) >= n threads.
   auto tail = [&](auto ept) {
     constexpr int EPT = decltype(ept)::value;
     const int p0 = tid * EPT;
@@ -1234,7 +1381,7 @@ __device__ __forceinline__ void wide_final_row(const WideParams& P, WideSmemCut&
       int s = 0;
   #pragma unroll
       for (int j = 0; j < EPT; ++j) {
-        const int i = p0 + j;
+        const int i = j * NT + tid;
         kk[j] = ~0ull;
         if (i < n) {
           while (s + 1 < P.S && sm.off[s + 1] <= i) ++s;
@@ -1368,7 +1515,15 @@ __device__ __forceinline__ void wide_final_row(const WideParams& P, WideSmemCut&
     // the walk over that segment: two consecutive float32 chunks per thread a step (one
     // bfloat16 chunk: the same registers)
     constexpr int WL = EPC == 4 ? 2 : 1;
-    const int64_t tok = wide_locate<T, NT, WL, SEG_CH>(P, c, (int64_t)s * SEG_CH, start, 1.0 / zkept, M, keep, &sm, &fl);
+    // Segments whose elements above the plan and planned elements together fit the sort's LDS
+    // keys (free now) list the tokens that can be kept there; a segment holding more (a long
+    // nucleus) walks every token.
+    const float lx = wide_raw_bound(c, __builtin_fmaxf(thr, vstar));
+    const int64_t tok =
+        sm.nab[s] + (sm.off[s + 1] - sm.off[s]) <= WCAND
+            ? wide_locate_list<T, NT, WL, SEG_CH, WCAND>(P, c, (int64_t)s * SEG_CH, start, 1.0 / zkept, M, keep, lx,
+                                                         sm.u.keys, &sm, &fl)
+            : wide_locate<T, NT, WL, SEG_CH>(P, c, (int64_t)s * SEG_CH, start, 1.0 / zkept, M, keep, &sm, &fl);
     if (tid == 0) {
       put_id(P.out_ids, row, tok);
       seg_write_info(P.out_info, row, PATH_WIDE, n_kept, kon0 ? thr : -__builtin_inff(), n_topk, n, fl, vstar, istar);
