@@ -142,6 +142,15 @@ struct WideSmemT {
   uint64_t kb[2];
 };
 using WideSmem = WideSmemT<1>;               // stats, histogram and probability passes
+// The cut pass's LDS: the segment's history bitmap and the block reductions only (no
+// histogram), so more of its workgroups fit a CU.
+struct WideSmemLite {
+  uint32_t bm[SEG_CH * 8 / 32];
+  double dred[NWAVE];
+  int32_t ired[NWAVE];
+  int32_t flags;
+  int32_t cnt;
+};
 using WideSmemCut = WideSmemT<WCAND>;        // the cut pass and its finaliser
 
 // Rows this path takes: sampled (temperature != 0) and not small-k (sampler.py:55).
@@ -582,7 +591,8 @@ __device__ __forceinline__ float wide_raw_bound(const WRowCtx& c, float B) {
 // ascending id order in `list` (LIST_CAP entries of (scaled value bits << 32) | id, one block
 // scan of the per-thread counts, four 16-bit fields one per step), and only the listed tokens
 // take the scaled value's probability and the cumulative sum.  The same tokens, values and
-// probabilities as wide_locate, which takes the range when more than LIST_CAP tokens reach lx.
+// probabilities as wide_locate.  Returns -2 (nothing drawn, the bitmap built) when more than
+// LIST_CAP tokens reach lx: the caller then takes wide_locate.
 template <typename T, int NTH, int WL, int NCH, int LIST_CAP, typename SM>
 __device__ __forceinline__ int64_t wide_locate_list(const WideParams& P, const WRowCtx& c, int64_t c0, double pstart,
                                                     double rz, float M, const WKeep& keep, float lx, uint64_t* list,
@@ -619,19 +629,17 @@ __device__ __forceinline__ int64_t wide_locate_list(const WideParams& P, const W
   }
   unsigned long long tot;
   const unsigned long long off = wexcl_int<unsigned long long, NTH>(cnt, &tot, sm);
-  int base[NSTEP];
   int n = 0;
 #pragma unroll
-  for (int step = 0; step < NSTEP; ++step) {
-    base[step] = n + (int)((off >> (16 * step)) & 0xffffu);
-    n += (int)((tot >> (16 * step)) & 0xffffu);
-  }
-  if (n > LIST_CAP) return wide_locate<T, NTH, WL, NCH>(P, c, c0, pstart, rz, M, keep, sm, fl);
+  for (int step = 0; step < NSTEP; ++step) n += (int)((tot >> (16 * step)) & 0xffffu);
+  if (n > LIST_CAP) return -2;   // the caller walks every token
   // the listed tokens' scaled values (chunk_y on the chunks holding one), in id order
+  int before = 0;   // tokens listed by the earlier steps
 #pragma unroll
   for (int step = 0; step < NSTEP; ++step) {
     const int64_t cb = c0 + (int64_t)step * NTH * WL + (int64_t)tid * WL;
-    int pos = base[step];
+    int pos = before + (int)((off >> (16 * step)) & 0xffffu);
+    before += (int)((tot >> (16 * step)) & 0xffffu);
 #pragma unroll
     for (int j = 0; j < WL; ++j) {
       const uint32_t hj = (hit[step] >> (j * EPC)) & ((1u << EPC) - 1u);
@@ -651,18 +659,15 @@ __device__ __forceinline__ int64_t wide_locate_list(const WideParams& P, const W
   // the walk over the list: PER consecutive entries per thread
   const double ud = (double)c.u;
   float p[PER];
-  int32_t id[PER];
   double own = 0.0;
 #pragma unroll
   for (int i = 0; i < PER; ++i) {
     const int li = tid * PER + i;
     p[i] = 0.0f;
-    id[i] = 0;
     if (li < n) {
       const uint64_t e = list[li];
       const float y = __uint_as_float((uint32_t)(e >> 32));
-      id[i] = (int32_t)(uint32_t)e;
-      if (keep(y, id[i])) p[i] = (float)((double)ns_expf(y - M) * rz);
+      if (keep(y, (int32_t)(uint32_t)e)) p[i] = (float)((double)ns_expf(y - M) * rz);
     }
     own += (double)p[i];
   }
@@ -672,9 +677,10 @@ __device__ __forceinline__ int64_t wide_locate_list(const WideParams& P, const W
 #pragma unroll
   for (int i = 0; i < PER; ++i) {
     if (p[i] > 0.0f) {
+      const int32_t id = (int32_t)(uint32_t)list[tid * PER + i];
       run += (double)p[i];
-      lastnz = id[i];
-      if (run > ud && first == 0x7fffffff) first = id[i];
+      lastnz = id;
+      if (run > ud && first == 0x7fffffff) first = id;
     }
   }
   if (first != 0x7fffffff) atomicMin(&sm->ib[0], first);
@@ -1121,7 +1127,7 @@ __global__ __launch_bounds__(SNT) __attribute__((amdgpu_waves_per_eu(4))) void s
 // its histogram's mass above them.
 template <typename T>
 __global__ __launch_bounds__(SNT) void wide_cut_kernel(const WideParams P) {
-  __shared__ WideSmem sm;
+  __shared__ WideSmemLite sm;
   constexpr int EPC = T::EPC;
   const int tid = threadIdx.x;
   const int lane = lane_id();
@@ -1334,11 +1340,11 @@ __device__ __forceinline__ void wide_final_row(const WideParams& P, WideSmemCut&
   if (tid < P.S) {
     const WideSeg s = dc_load_wseg(P.segs + (int64_t)row * P.S + tid);
     sm.segfx[tid] = s.mass;
+    sm.subq[tid] = s.mass;   // the kept mass per segment starts from the mass above the plan
     sm.off[tid] = s.ncand;
     sm.ired[tid] = s.nabove;
     sm.nab[tid] = s.nabove;
   }
-  if (tid < P.S) sm.subq[tid] = dc_load_wseg(P.segs + (int64_t)row * P.S + tid).mass;   // mass above the plan
   if (tid == 0) sm.ib[0] = 0;
   __syncthreads();
   if (tid == 0) {
@@ -1515,15 +1521,17 @@ __device__ __forceinline__ void wide_final_row(const WideParams& P, WideSmemCut&
     // the walk over that segment: two consecutive float32 chunks per thread a step (one
     // bfloat16 chunk: the same registers)
     constexpr int WL = EPC == 4 ? 2 : 1;
-    // Segments whose elements above the plan and planned elements together fit the sort's LDS
-    // keys (free now) list the tokens that can be kept there; a segment holding more (a long
-    // nucleus) walks every token.
-    const float lx = wide_raw_bound(c, __builtin_fmaxf(thr, vstar));
-    const int64_t tok =
-        sm.nab[s] + (sm.off[s + 1] - sm.off[s]) <= WCAND
-            ? wide_locate_list<T, NT, WL, SEG_CH, WCAND>(P, c, (int64_t)s * SEG_CH, start, 1.0 / zkept, M, keep, lx,
-                                                         sm.u.keys, &sm, &fl)
-            : wide_locate<T, NT, WL, SEG_CH>(P, c, (int64_t)s * SEG_CH, start, 1.0 / zkept, M, keep, &sm, &fl);
+    // Float32 segments whose elements above the plan and planned elements together fit the
+    // sort's LDS keys (free now) list the tokens that can be kept there; a segment holding more
+    // (a long nucleus) walks every token, and so do bfloat16 rows (the listed walk's registers
+    // beside the wider chunks spill there).
+    int64_t tok = -2;
+    if (EPC == 4 && sm.nab[s] + (sm.off[s + 1] - sm.off[s]) <= WCAND) {
+      const float lx = wide_raw_bound(c, __builtin_fmaxf(thr, vstar));
+      tok = wide_locate_list<T, NT, WL, SEG_CH, WCAND>(P, c, (int64_t)s * SEG_CH, start, 1.0 / zkept, M, keep, lx,
+                                                       sm.u.keys, &sm, &fl);
+    }
+    if (tok == -2) tok = wide_locate<T, NT, WL, SEG_CH>(P, c, (int64_t)s * SEG_CH, start, 1.0 / zkept, M, keep, &sm, &fl);
     if (tid == 0) {
       put_id(P.out_ids, row, tok);
       seg_write_info(P.out_info, row, PATH_WIDE, n_kept, kon0 ? thr : -__builtin_inff(), n_topk, n, fl, vstar, istar);
