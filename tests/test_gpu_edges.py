@@ -157,3 +157,38 @@ def test_misaligned_vocab_with_invalid_sample_indices(device, path):
     r = O.sample(flat[sidx[good]], t_np[good], k_np[good], np.full(3, 0.9), np.ones(3), [[], [], []], u_np[good])
     for j, row in enumerate(good):
         assert g[row] in r.allowed_ids[j], (row, g[row], r.ids[j], r.allowed_ids[j].tolist())
+
+
+@pytest.mark.parametrize("rounding", ["division", "reciprocal"])
+@pytest.mark.parametrize("path", ["shipped", "segmented"])
+def test_wide_rows_small_kept_set(device, path, rounding):
+    """Wide fp32 rows (top-k 200 to 2000, with and without top-p) whose kept set is small
+    next to the 16,384-token segment the uniform falls in: the draw lists only the tokens
+    whose raw logit can reach the kept set's smallest value (its preimage under the
+    temperature, lowered by a few units in the last place).  Temperatures from 1e-3 to 40;
+    penalties 1, 1.2 and 0.8 (below 1 no raw bound holds and every token is walked), with
+    each row's 40 largest logits in its history so that penalized tokens sit at the bound;
+    uniforms spread over [0, 1)."""
+    B, V = 24, 128256
+    rng = np.random.default_rng(97)
+    rows = (rng.standard_normal((B, V), dtype=np.float32) * 2.5).astype(np.float32)
+    t = np.array([1e-3, 0.5, 1.0, 1.3, 40.0, 0.7])[np.arange(B) % 6]
+    k = np.array([200, 1000, 2000])[np.arange(B) % 3].astype(np.int64)
+    p = np.array([1.0, 0.9, 1.0, 0.9])[np.arange(B) % 4]
+    pen = np.array([1.0, 1.2, 0.8, 1.2, 1.2])[np.arange(B) % 5]
+    hist = [np.concatenate([np.argsort(-rows[i])[:40], rng.integers(0, V, size=60)]).astype(np.int32)
+            for i in range(B)]
+    u = ((np.arange(B) + 0.5) / B).astype(np.float32)
+    w = W.Workload(name="wide-small-kept", vocab=V, rows=rows, bf16_bits=None, temperature=t, top_k=k, top_p=p,
+                   repetition_penalty=pen, histories=hist, uniforms=u, n_rows_total=B)
+    print(f"[edges] {w.name} B={B} V={V} path={path} rounding={rounding}", flush=True)
+    g = run_path(w, device, path, penalty_rounding=rounding)
+    r = O.sample_workload(w, penalty_rounding=rounding)
+    fails, stats = compare(g, r)
+    print(f"[edges] {w.name}: {stats}", flush=True)
+    assert not fails, "\n".join(fails)
+    # the rows at temperature 0.5 and above are planned and drawn by the wide path (info word 0
+    # holds the path code, 7); at 1e-3 the k-th largest lies beyond the histograms' 32 units and
+    # the general per-row code takes the row
+    planned = t >= 0.5
+    assert (g["info"][planned, 0] == 7).all(), g["info"][:, 0]
