@@ -176,6 +176,23 @@ __device__ __forceinline__ float lower_preimage(float tau, float tdiv, float rdi
   return fkey_inv(khi);
 }
 
+// lower_preimage by a whole wave (every lane active, the same arguments in every lane): when
+// the search window [khi - w, khi] fits the wave's 64 lanes, every key of it is tested at once,
+// one per lane, and the first key that maps to RN(tau / t) or above is the answer (the mapping
+// is monotone in the key); otherwise, and when the window's first key already maps there (the
+// serial search then widens the window), the serial search.
+__device__ __forceinline__ float wave_lower_preimage(float tau, float tdiv, float rdiv) {
+  if (tdiv == 1.0f || !(__builtin_fabsf(tau) <= 3.4028235e38f)) return tau;
+  const uint32_t khi = fkey(tau);
+  const uint32_t w = 16u + 4u * (uint32_t)__builtin_fminf(__builtin_ceilf(tdiv), 8.0e6f);
+  if (w > 63u || khi < w) return lower_preimage(tau, tdiv, rdiv);
+  const float ft = div_rn(tau, tdiv, rdiv);
+  const uint32_t l = (uint32_t)lane_id();
+  const uint64_t m = ballot(l <= w && div_rn(fkey_inv(khi - w + (l <= w ? l : 0u)), tdiv, rdiv) >= ft);
+  if (m & 1ull) return lower_preimage(tau, tdiv, rdiv);
+  return fkey_inv(khi - w + (uint32_t)__builtin_ctzll(m));
+}
+
 // --------------------------------------------------------------- LDS sorts
 // Ascending bitonic sort of P (power of two, 2..CAP) u64 keys in LDS.
 __device__ __forceinline__ void lds_bitonic_sort(uint64_t* s, int P) {

@@ -249,7 +249,7 @@ __device__ __forceinline__ int topk_stream(const RowArgs P, const int row, const
       NS_STAMP_LANE(2, lane == 0);   // the last wave to finish its share
       const uint32_t kp = topk_bound_key<T, NPH>(fs, lane, k);
       const float taux = kp <= fkey(-__builtin_inff()) ? -__builtin_inff() : fkey_inv(kp);
-      const float b = lower_preimage(taux, tdiv, rdiv);
+      const float b = wave_lower_preimage(taux, tdiv, rdiv);
       NS_STAMP_LANE(7, lane == 0);   // the last wave: the bound taken
       if (lane == 0) misc->fb[0] = b;
     }
