@@ -99,12 +99,11 @@ __device__ __forceinline__ uint32_t topk_bound_key(const float* fs, int lane, in
 }
 
 // A chunk maximum kept as the top 16 bits of its order key, rounded up (the value it stands
-// for is >= the maximum, so a chunk is never missed by a test against a bound), and back.
+// for is >= the maximum, so a chunk is never missed by a test against a bound).
 __device__ __forceinline__ uint32_t key16_up(float m) {
   const uint32_t kk = fkey(m);
   return kk >= 0xffff0000u ? 0xffffu : (kk + 0xffffu) >> 16;
 }
-__device__ __forceinline__ float key16_val(uint32_t k16) { return fkey_inv(k16 << 16); }
 
 // The whole row path: every thread of the workgroup calls it.  `v` holds the first TK_EARLY
 // chunks when `early` (requested by the caller at entry).  Returns 0 when the row is
@@ -319,10 +318,13 @@ __device__ __forceinline__ int topk_stream(const RowArgs P, const int row, const
       // first phase against its kept maxima); then one append per round for the lanes that
       // still hold hits, their lowest first (rarely more than one round), instead of a vote
       // per chunk.
+      // a kept maximum reaches tc when its 16-bit key reaches tc's key rounded up to 16 bits
+      // (the kept keys' low 16 bits are zero; NaN and +inf rows never get here)
+      const uint32_t tk16 = (fkey(tc) + 0xffffu) >> 16;
       uint32_t h1 = 0u, h2 = 0u;
 #pragma unroll
       for (int q = 0; q < TK_CPT; ++q) {
-        h1 |= (key16_val((pk[q >> 1] >> ((q & 1) * 16)) & 0xffffu) >= tc ? 1u : 0u) << q;
+        h1 |= (((pk[q >> 1] >> ((q & 1) * 16)) & 0xffffu) >= tk16 ? 1u : 0u) << q;
         h2 |= (cm[q] >= tc ? 1u : 0u) << q;   // -inf past the row, and tc > -inf
       }
       while (true) {
