@@ -41,6 +41,7 @@ which is the same distribution.
 """
 from __future__ import annotations
 
+import itertools
 from typing import List, Optional, Sequence
 
 import numpy as np
@@ -63,13 +64,27 @@ class PackedRows:
     def __init__(self, params: Sequence[SamplingParams], histories: Sequence, vocab: int,
                  slots: Optional[np.ndarray] = None, slot_max_hist: int = 0, penalty_rounding: str = "division"):
         B = len(params)
+        # the four numeric fields of every row in one pass (float64 holds each float field
+        # exactly and top_k exactly below 2^53; larger top_k values clamp the same way)
+        try:
+            f4 = np.fromiter(itertools.chain.from_iterable(
+                (p.temperature, p.top_k, p.top_p, p.repetition_penalty) for p in params), dtype=np.float64,
+                count=4 * B).reshape(B, 4)
+        except (TypeError, ValueError, OverflowError):
+            f4 = None
+        if f4 is not None and np.isfinite(f4[:, 1]).all():
+            t64, rp64 = f4[:, 0], f4[:, 3]
+            topk = np.clip(np.trunc(f4[:, 1]), -1, _I32_MAX).astype(np.int32)
+            topp = f4[:, 2].astype(np.float32)
+        else:
+            # the field-by-field conversions (and their errors: a top_k that is no integer)
+            t64 = np.asarray([float(p.temperature) for p in params], dtype=np.float64).reshape(B)
+            topk = np.asarray([min(max(int(p.top_k), -1), _I32_MAX) for p in params], dtype=np.int32).reshape(B)
+            topp = np.asarray([float(p.top_p) for p in params], dtype=np.float64).reshape(B).astype(np.float32)
+            rp64 = np.asarray([float(p.repetition_penalty) for p in params], dtype=np.float64).reshape(B)
         # greedy rows are encoded as temperature 0 (sampler.py:47-50); others carry the
         # effective float32 temperature, max(t, 1e-6) if t > 0 else 1 (sampler.py:41-46)
-        t64 = np.asarray([float(p.temperature) for p in params], dtype=np.float64).reshape(B)
         temp = np.where(t64 == 0.0, 0.0, np.where(t64 > 0.0, np.maximum(t64, 1e-6), 1.0)).astype(np.float32)
-        topk = np.asarray([min(max(int(p.top_k), -1), _I32_MAX) for p in params], dtype=np.int32).reshape(B)
-        topp = np.asarray([float(p.top_p) for p in params], dtype=np.float64).reshape(B).astype(np.float32)
-        rp64 = np.asarray([float(p.repetition_penalty) for p in params], dtype=np.float64).reshape(B)
         pen = rp64.astype(np.float32)
         lens = np.zeros(B, dtype=np.int64)
         hist_rows = [None] * B
