@@ -1288,6 +1288,9 @@ __device__ __forceinline__ void wide_final_row(const WideParams& P, WideSmemCut&
   WideRow* R = P.rows + row;
   const int32_t step = R->step;
   if (step != WSTEP_CUT && step != WSTEP_FULL) return;
+  // every segment's record (one lane of wave 0 each), requested ahead of the row's parameters
+  WideSeg sg{};
+  if (tid < P.S) sg = dc_load_wseg(P.segs + (int64_t)row * P.S + tid);
   const WRowCtx c = wide_row_ctx<T>(P, row);
   const float M = R->M;
   int32_t fl = R->flags & 0xffff;
@@ -1295,7 +1298,7 @@ __device__ __forceinline__ void wide_final_row(const WideParams& P, WideSmemCut&
   if (step == WSTEP_FULL) {
     // ---- every finite value kept: the segment holding u from the per-segment masses, then
     // the walk inside it (the masses read in parallel, then summed in segment order)
-    if (tid < P.S) sm.subq[tid] = dc_load_wseg(P.segs + (int64_t)row * P.S + tid).mass;
+    if (tid < P.S) sm.subq[tid] = sg.mass;
     __syncthreads();
     if (tid == 0) {
       double Z = 0.0;
@@ -1337,28 +1340,28 @@ __device__ __forceinline__ void wide_final_row(const WideParams& P, WideSmemCut&
   const bool kon = R->kon != 0;
   const bool pon = c.topp < 1.0f;
   const bool kon0 = c.k > 0 && (int64_t)c.k < c.V;
-  if (tid < P.S) {
-    const WideSeg s = dc_load_wseg(P.segs + (int64_t)row * P.S + tid);
-    sm.segfx[tid] = s.mass;
-    sm.subq[tid] = s.mass;   // the kept mass per segment starts from the mass above the plan
-    sm.off[tid] = s.ncand;
-    sm.ired[tid] = s.nabove;
-    sm.nab[tid] = s.nabove;
-  }
-  if (tid == 0) sm.ib[0] = 0;
-  __syncthreads();
-  if (tid == 0) {
-    int o = 0, over = 0, nab = 0;
-    for (int i = 0; i < P.S; ++i) {
-      const int n = sm.off[i];
-      over |= n > SEG_CAP;
-      sm.off[i] = o;
-      o += n < SEG_CAP ? n : SEG_CAP;
-      nab += sm.ired[i];
+  if (wave_id() == 0) {
+    // the segments' candidate offsets (their counts capped at SEG_CAP, a prefix over the lanes:
+    // S <= 64, one lane per segment), the overflow flag and the elements above the plan
+    const int l = lane_id();
+    const bool act = l < P.S;
+    const int cnt = act ? sg.ncand : 0;
+    const int capped = cnt < SEG_CAP ? cnt : SEG_CAP;
+    const int incl = wave_incl_scan(capped);
+    const bool over = ballot(act && cnt > SEG_CAP) != 0ull;
+    const int o = read_lane(incl, 63);
+    const int nab = wave_sum(act ? sg.nabove : 0);
+    if (act) {
+      sm.segfx[l] = sg.mass;
+      sm.subq[l] = sg.mass;   // the kept mass per segment starts from the mass above the plan
+      sm.off[l] = incl - capped;
+      sm.nab[l] = sg.nabove;
     }
-    sm.off[P.S] = o;
-    sm.ib[0] = over || o > WCAND;
-    sm.ib[3] = nab;
+    if (l == 0) {
+      sm.off[P.S] = o;
+      sm.ib[0] = over || o > WCAND;
+      sm.ib[3] = nab;
+    }
   }
   __syncthreads();
   // finite elements above the planned bins: the compaction pass's counts (top-p rows do not
