@@ -218,6 +218,38 @@ __device__ __forceinline__ unsigned long long wsum_u64(unsigned long long v, SM*
   __syncthreads();
   return r;
 }
+// A 64-bit and a 32-bit block sum in one pair of barriers.
+template <int NTH = SNT, typename SM>
+__device__ __forceinline__ void wsum_u64_i(unsigned long long& a, int32_t& b, SM* sm) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) a += lane_xor(a, o);
+  b = wave_sum(b);
+  if (lane_id() == 0) { sm->ured[wave_id()] = a; sm->ired[wave_id()] = b; }
+  __syncthreads();
+  unsigned long long ra = 0ull;
+  int32_t rb = 0;
+#pragma unroll
+  for (int w = 0; w < NTH / 64; ++w) { ra += sm->ured[w]; rb += sm->ired[w]; }
+  __syncthreads();
+  a = ra;
+  b = rb;
+}
+// A float64 and a 32-bit block sum in one pair of barriers (the float64 terms added in the
+// same order as wsum_f64).
+template <int NTH = SNT, typename SM>
+__device__ __forceinline__ void wsum_f64_i(double& a, int32_t& b, SM* sm) {
+  a = wave_sum(a);
+  b = wave_sum(b);
+  if (lane_id() == 0) { sm->dred[wave_id()] = a; sm->ired[wave_id()] = b; }
+  __syncthreads();
+  double ra = 0.0;
+  int32_t rb = 0;
+#pragma unroll
+  for (int w = 0; w < NTH / 64; ++w) { ra += sm->dred[w]; rb += sm->ired[w]; }
+  __syncthreads();
+  a = ra;
+  b = rb;
+}
 template <int NTH = SNT, typename SM>
 __device__ __forceinline__ double wsum_f64(double v, SM* sm) {
   v = wave_sum(v);
@@ -1186,8 +1218,9 @@ __global__ __launch_bounds__(SNT) void wide_cut_kernel(const WideParams P) {
     const int lim = blo - ds < WBINS ? blo - ds : WBINS;
     for (int jj = tid; jj < lim; jj += SNT) part += (double)__uint_as_float((uint32_t)dc_load(ex + jj));
   }
-  const double above = wsum_f64(part, &sm) * (ms > -__builtin_inff() ? exp((double)ms - (double)M) : 0.0);
-  const int32_t snab = wsum_i(nab, &sm);
+  int32_t snab = nab;
+  wsum_f64_i(part, snab, &sm);
+  const double above = part * (ms > -__builtin_inff() ? exp((double)ms - (double)M) : 0.0);
   if (tid == 0) {
     WideSeg s{};
     s.mass = (uint64_t)(above * WFX);
@@ -1427,8 +1460,9 @@ __device__ __forceinline__ void wide_final_row(const WideParams& P, WideSmemCut&
           if (y >= thr) { mk += wfx(M, y); ++nk_own; }
         }
       }
-      mtopk = wsum_u64<NT>(mk, &sm);
-      n_topk_c = wsum_i<NT>(nk_own, &sm);
+      wsum_u64_i<NT>(mk, nk_own, &sm);
+      mtopk = mk;
+      n_topk_c = nk_own;
     }
     const int32_t n_topk = kon ? n_above + n_topk_c : nfin;
     const uint64_t zk_fx = kon ? mass_above + mtopk : R->mass_tot;
