@@ -363,7 +363,9 @@ __device__ __forceinline__ WRowCtx wide_row_ctx(const WideParams& P, int row) {
 
 // The history bitmap of elements [e0, e0 + SEG_EL) (set semantics, sampler.py:34-38),
 // and sm->flags cleared.  Every thread must call it (two barriers).  Returns
-// FLAG_BAD_HIST_ID when an id lies outside [0, V).
+// FLAG_BAD_HIST_ID when an id lies outside [0, V).  The ids are read WHB per thread at a time
+// (each load instruction reads consecutive ids), so a history takes one memory round trip per
+// WHB * NTH ids.
 template <typename T, int NTH = SNT, typename SM>
 __device__ __forceinline__ int32_t wide_bitmap(const WideParams& P, const WRowCtx& c, int64_t e0, SM* sm) {
   constexpr int SEG_EL = SEG_CH * T::EPC;
@@ -374,12 +376,23 @@ __device__ __forceinline__ int32_t wide_bitmap(const WideParams& P, const WRowCt
   __syncthreads();
   const int32_t* hp = P.hist_ids + c.h0;
   bool bad = false;
-  for (int j = tid; c.pen_on && j < c.H; j += NTH) {
-    const int32_t id = hp[j];
-    if (id < 0 || (int64_t)id >= c.V) bad = true;
-    else if ((int64_t)id >= e0 && (int64_t)id < e0 + SEG_EL) {
-      const int32_t l = id - (int32_t)e0;
-      atomicOr(&sm->bm[l >> 5], 1u << (l & 31));
+  constexpr int WHB = 8;
+  for (int base = 0; c.pen_on && base < c.H; base += WHB * NTH) {
+    int32_t ids[WHB];
+#pragma unroll
+    for (int s = 0; s < WHB; ++s) {
+      const int j = base + s * NTH + tid;
+      ids[s] = j < c.H ? hp[j] : 0;
+    }
+#pragma unroll
+    for (int s = 0; s < WHB; ++s) {
+      const int32_t id = ids[s];
+      if (base + s * NTH + tid >= c.H) continue;
+      if (id < 0 || (int64_t)id >= c.V) bad = true;
+      else if ((int64_t)id >= e0 && (int64_t)id < e0 + SEG_EL) {
+        const int32_t l = id - (int32_t)e0;
+        atomicOr(&sm->bm[l >> 5], 1u << (l & 31));
+      }
     }
   }
   if (bad) atomicOr(&sm->flags, FLAG_BAD_HIST_ID);
