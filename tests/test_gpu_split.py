@@ -182,3 +182,19 @@ def test_consecutive_calls_share_counters(device, path):
     b = topk_workload("split-b", 3, 50257, seed=720, bf16=True)
     for w in (a, b, a, b):
         check(w, device, path)
+
+
+@pytest.mark.parametrize("bf16,V", [(False, 128256), (True, 128256), (False, 50000)])
+def test_topk_kernel_temperature_range(device, bf16, V):
+    """The top-k kernel's bound maps the k-th largest group maximum through the temperature
+    (the smallest raw value whose quotient reaches the bound's): searched by the whole wave
+    when the window of keys fits it (temperatures up to about 11.75), by the serial search
+    otherwise.  Temperatures from 1e-3 to 1e4, k from 1 to 64, with penalties, in one phase
+    (bf16 and fp32 V=50000) and two (fp32 V=128256, whose first phase's kept 16-bit maxima
+    are compared with the bound as keys)."""
+    B = 14
+    w = topk_workload(f"topk-temps-{'bf16' if bf16 else 'f32'}-{V}", B, V, seed=311 + V, bf16=bf16, hist_len=200,
+                      k_choices=(1, 7, 50, 64), pen_choices=(1.0, 1.1, 1.5))
+    w.temperature[:] = np.array([1e-3, 0.05, 0.3, 0.8, 1.0, 1.7, 3.3, 8.0, 11.5, 12.5, 40.0, 333.0, 1e4, 0.8])[:B]
+    check(w, device, "topk")
+    check(w, device, "shipped")
